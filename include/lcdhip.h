@@ -1,0 +1,236 @@
+/*
+ * lcdhip.h -- C ABI of liblcdhip.so, the MI355X (gfx950) execution backend
+ * behind LCD's `@parallel` decorator.
+ *
+ * Everything the reference does between "the decorated function is called
+ * with host CSR/CSC arrays" and "the result array is back on the host" goes
+ * through these entry points: device buffers and copies, run-time compilation
+ * and launch of the generated HIP kernels, the level loop of the wavefront
+ * executor, and the on-device DAG inspector (edges, in-degrees, level sets,
+ * structural lookup tables).
+ *
+ * Conventions
+ *   - every function returns 0 (LCDHIP_OK) or a positive LCDHIP_ERR_* code;
+ *     lcdhip_last_error() returns a thread-local message for the last failure
+ *   - the library never frees or keeps caller memory; every *_create/_alloc/
+ *     _build/_compile/_load has a matching *_destroy/_free
+ *   - pointers named d_* are device pointers; stream arguments are opaque
+ *     handles from lcdhip_stream_create (NULL = the library's default stream)
+ *   - not re-entrant: one host thread drives one context
+ *
+ * The citations name the reference code (paths under the reference checkout)
+ * that each entry point replaces.
+ */
+#ifndef LCDHIP_H
+#define LCDHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LCDHIP_OK 0
+#define LCDHIP_ERR_HIP 1          /* a HIP runtime call failed */
+#define LCDHIP_ERR_COMPILE 2      /* hiprtc rejected the generated source */
+#define LCDHIP_ERR_ARGUMENT 3     /* bad argument / handle */
+#define LCDHIP_ERR_DAG_BOUNDS 4   /* DAG endpoint outside [0, n) */
+#define LCDHIP_ERR_DAG_CYCLE 5    /* level sets do not cover every node */
+#define LCDHIP_ERR_LOOKUP_POINTER 6 /* non-monotone / out-of-range pointers */
+#define LCDHIP_ERR_LOOKUP_ORDER 7   /* unsorted segment */
+#define LCDHIP_ERR_WATCHDOG 8     /* a spin-wait executor gave up */
+#define LCDHIP_ERR_NO_DEVICE 9    /* no usable GPU */
+
+typedef struct lcdhip_module lcdhip_module;
+typedef struct lcdhip_kernel lcdhip_kernel;
+typedef struct lcdhip_graph lcdhip_graph;
+typedef struct lcdhip_dag lcdhip_dag;
+typedef void *lcdhip_stream;
+typedef void *lcdhip_event;
+
+const char *lcdhip_last_error(void);
+const char *lcdhip_version(void);
+
+/* ------------------------------------------------------------- context ---
+ * Replaces the implicit numba.cuda context (compiler/cuda_runtime.py:141-142,
+ * compiler/scheduler.py:714-736). */
+int lcdhip_init(int device);
+int lcdhip_shutdown(void);
+int lcdhip_device_count(int *count);
+
+typedef struct {
+    int32_t compute_units;        /* 256 on MI355X */
+    int32_t xcd_count;            /* 8 */
+    int32_t wavefront_size;       /* 64 */
+    int32_t max_threads_per_block;
+    int32_t lds_bytes_per_block;
+    int32_t lds_bytes_per_cu;
+    int32_t clock_khz;
+    int32_t memory_clock_khz;
+    int32_t memory_bus_bits;
+    int32_t l2_bytes;
+    int64_t global_memory_bytes;
+    char name[128];
+    char arch[64];
+} lcdhip_props;
+int lcdhip_device_props(lcdhip_props *out);
+
+/* Measured machine constants for the analytic scheduler; replaces
+ * measure_arch_constants / _measure_launch_latency / _measure_atomic_cost
+ * (compiler/scheduler.py:714-775).  handoff_s is the latency of one
+ * release->acquire hop between two workgroups through device-scope atomics,
+ * barrier_s one grid-wide barrier of a resident persistent grid. */
+typedef struct {
+    double launch_latency_s;
+    double atomic_cost_s;
+    double memory_bandwidth_bytes_per_s;
+    double lane_flops_per_s;
+    double handoff_s;
+    double barrier_s;
+    double graph_node_s;
+} lcdhip_arch;
+int lcdhip_measure_arch(lcdhip_arch *out);
+
+/* ------------------------------------------------- buffers and streams ---
+ * Replace cuda.to_device / copy_to_host / cuda.synchronize
+ * (compiler/cuda_runtime.py:391-401, 47-55, 215). */
+int lcdhip_buffer_alloc(size_t bytes, void **d_out);
+int lcdhip_buffer_free(void *d_ptr);
+int lcdhip_buffer_upload(void *d_dst, const void *host_src, size_t bytes,
+                         lcdhip_stream stream);
+int lcdhip_buffer_download(void *host_dst, const void *d_src, size_t bytes,
+                           lcdhip_stream stream);
+int lcdhip_buffer_copy(void *d_dst, const void *d_src, size_t bytes,
+                       lcdhip_stream stream);
+/* Fill with a 32-bit pattern using a kernel (safe inside graph capture). */
+int lcdhip_buffer_fill32(void *d_dst, uint32_t value, size_t count,
+                         lcdhip_stream stream);
+int lcdhip_host_alloc(size_t bytes, void **host_out);   /* pinned */
+int lcdhip_host_free(void *host_ptr);
+int lcdhip_stream_create(lcdhip_stream *out);
+int lcdhip_stream_destroy(lcdhip_stream stream);
+int lcdhip_stream_sync(lcdhip_stream stream);
+int lcdhip_event_create(lcdhip_event *out);
+int lcdhip_event_destroy(lcdhip_event event);
+int lcdhip_event_record(lcdhip_event event, lcdhip_stream stream);
+int lcdhip_event_elapsed_ms(lcdhip_event start, lcdhip_event stop, float *ms);
+
+/* -------------------------------------------------- generated modules ---
+ * Replace compile_cuda_module and the numba JIT behind it
+ * (compiler/cuda_runtime.py:70-125).  lcdhip_module_compile_code needs no
+ * GPU (hiprtc cross-compiles for gfx950); lcdhip_module_load needs one. */
+int lcdhip_module_compile_code(const char *source, const char *name,
+                               const char *const *options, int option_count,
+                               void **code_out, size_t *size_out,
+                               char **log_out);
+void lcdhip_free_host(void *ptr); /* frees code_out / log_out */
+int lcdhip_module_load(const void *code, size_t size, lcdhip_module **out);
+int lcdhip_module_destroy(lcdhip_module *module);
+int lcdhip_module_get_kernel(lcdhip_module *module, const char *name,
+                             lcdhip_kernel **out);
+/* Largest co-resident grid of `kernel` at this block size (for persistent
+ * executors: every workgroup must be able to make progress). */
+int lcdhip_kernel_max_resident_blocks(lcdhip_kernel *kernel, int block_threads,
+                                      size_t lds_bytes, int *blocks_out);
+
+/* One launch; replaces kernel[grid, block](*args) in the generated launchers
+ * (compiler/cuda_lowering.py:673-735).  args[k] points at the value of the
+ * k-th kernel parameter. */
+int lcdhip_launch(lcdhip_kernel *kernel, uint32_t grid_x, uint32_t block_x,
+                  size_t lds_bytes, lcdhip_stream stream, void **args);
+
+/* The host level loop of the wavefront launchers
+ * (compiler/cuda_lowering.py:855-1068): for every level/band l with
+ * host_ptr[l] < host_ptr[l+1], set *(int32*)args[start_arg] = host_ptr[l],
+ * *(int32*)args[end_arg] = host_ptr[l+1] and launch
+ * ceil((host_ptr[l+1]-host_ptr[l]) / tasks_per_block) blocks.  There is no
+ * host synchronisation between levels: stream order carries the dependence.
+ * Intended to be issued once under graph capture and then replayed. */
+int lcdhip_launch_levels(lcdhip_kernel *kernel, const int32_t *host_ptr,
+                         int64_t level_count, int32_t tasks_per_block,
+                         uint32_t block_x, size_t lds_bytes,
+                         lcdhip_stream stream, void **args, int start_arg,
+                         int end_arg);
+
+/* hipGraph capture of a launcher body. */
+int lcdhip_graph_begin_capture(lcdhip_stream stream);
+int lcdhip_graph_end_capture(lcdhip_stream stream, lcdhip_graph **out);
+int lcdhip_graph_launch(lcdhip_graph *graph, lcdhip_stream stream);
+int lcdhip_graph_destroy(lcdhip_graph *graph);
+
+/* ------------------------------------------------- on-device inspector ---
+ * Replaces the generated Python `extract_dag` (compiler/dag_codegen.py:
+ * 1151-1550, 1600-1618) and compiler/dag_preprocessing.py:94-255.
+ *
+ * One rule enumerates, for every task `seg` in [0, n):
+ *     for p in [d_ptr[seg] + lower_offset, d_ptr[seg+1] + upper_offset):
+ *         if break_at_owner and d_idx[p] >= seg: break
+ *         (src, dst) = owner_is_source ? (seg, d_idx[p]) : (d_idx[p], seg)
+ *         if guard(src, dst): edge src -> dst
+ * guard: 0 none, 1 dst > src, 2 src != dst.
+ */
+#define LCDHIP_GUARD_NONE 0
+#define LCDHIP_GUARD_GREATER 1
+#define LCDHIP_GUARD_NOT_EQUAL 2
+
+typedef struct {
+    const int32_t *d_ptr;
+    const int32_t *d_idx;
+    int64_t idx_size;
+    int32_t owner_is_source;
+    int32_t lower_offset;
+    int32_t upper_offset;
+    int32_t guard;
+    int32_t break_at_owner;
+} lcdhip_dag_rule;
+
+#define LCDHIP_DAG_LEVELS 1u        /* also build level sets / wavefronts */
+#define LCDHIP_DAG_FORCE_KAHN 2u    /* use the frontier algorithm even when
+                                       every edge goes low id -> high id */
+
+typedef struct {
+    int64_t n;
+    int64_t edges;           /* unique edges */
+    int64_t levels;
+    int64_t scheduled;       /* nodes covered by the level sets */
+    int64_t max_level_width;
+    int32_t topological_ids; /* 1 when every edge has src < dst */
+    int32_t level_algorithm; /* 0 none, 1 frontier (Kahn), 2 ordered sweep */
+} lcdhip_dag_info;
+
+/* Arrays owned by the dag handle (all int32, device resident). */
+#define LCDHIP_DAG_PTR 0            /* n + 1: CSR successor offsets */
+#define LCDHIP_DAG_INDEX 1          /* edges: successors, sorted, unique */
+#define LCDHIP_DAG_DEP_COUNT 2      /* n: unique in-degree */
+#define LCDHIP_DAG_EDGE_COUNT 3     /* n: rule hits per destination */
+#define LCDHIP_DAG_LEVEL_OF 4       /* n: level, -1 = unscheduled */
+#define LCDHIP_DAG_WAVEFRONTS 5     /* scheduled: nodes by (level, id) */
+#define LCDHIP_DAG_WAVEFRONT_PTR 6  /* levels + 1 */
+
+int lcdhip_dag_build(const lcdhip_dag_rule *rules, int rule_count, int64_t n,
+                     uint32_t flags, lcdhip_stream stream, lcdhip_dag **out);
+int lcdhip_dag_get_info(const lcdhip_dag *dag, lcdhip_dag_info *out);
+int lcdhip_dag_array(const lcdhip_dag *dag, int which, void **d_out,
+                     int64_t *count_out);
+int lcdhip_dag_download(const lcdhip_dag *dag, int which, int32_t *host_out,
+                        int64_t capacity);
+int lcdhip_dag_destroy(lcdhip_dag *dag);
+
+/* Diagonal-position table; replaces _materialize_lookup
+ * (compiler/structural_lookups.py:279-333).  d_positions[s] = first p in
+ * [d_ptr[s], d_ptr[s+1]) with d_idx[p] == s, else -1. */
+int lcdhip_lookup_build(const int32_t *d_ptr, const int32_t *d_idx, int64_t n,
+                        int64_t idx_size, int32_t *d_positions,
+                        lcdhip_stream stream);
+
+/* 128-bit content digest of a device array; replaces the per-call blake2b of
+ * the structure arrays (compiler/scheduler.py:678-711) for arrays that are
+ * already resident. */
+int lcdhip_digest(const void *d_data, size_t bytes, uint64_t out[2],
+                  lcdhip_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LCDHIP_H */

@@ -1,0 +1,683 @@
+// On-device DAG inspector: edge enumeration with set semantics, unique
+// in-degrees, edge multiplicities, CSR successors, level sets and the
+// flattened wavefront arrays.  Replaces the generated Python `extract_dag`
+// (compiler/dag_codegen.py:1151-1550) and compact_successors /
+// wavefronts_from_dag / preprocess_wavefront
+// (compiler/dag_preprocessing.py:115-204) of the reference.
+//
+// Bit-exactness with the reference comes from construction, not from atomics
+// order: edges become 64-bit keys (src << 32 | dst) that are radix-sorted and
+// made unique (a sorted set per source), counts are integer histograms, and
+// the wavefront array is a stable sort of node ids by level.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+#include <rocprim/rocprim.hpp>
+
+#include "lcdhip_common.h"
+
+using lcdhip::resolve_stream;
+using lcdhip::set_error;
+
+struct lcdhip_dag {
+    lcdhip_dag_info info{};
+    int32_t *arrays[7] = {nullptr, nullptr, nullptr, nullptr,
+                          nullptr, nullptr, nullptr};
+    int64_t counts[7] = {0, 0, 0, 0, 0, 0, 0};
+};
+
+namespace {
+
+constexpr int kBlock = 256;
+
+// flags[0] endpoint / pointer out of range, flags[1] an edge with src >= dst
+struct RuleDevice {
+    const int32_t *ptr;
+    const int32_t *idx;
+    int64_t idx_size;
+    int32_t owner_is_source;
+    int32_t lower_offset;
+    int32_t upper_offset;
+    int32_t guard;
+    int32_t break_at_owner;
+};
+
+__global__ void emit_keys_kernel(RuleDevice rule, int64_t n,
+                                 unsigned long long *__restrict__ keys,
+                                 int32_t *__restrict__ edge_count,
+                                 int32_t *__restrict__ flags,
+                                 unsigned long long *__restrict__ candidates)
+{
+    int64_t seg = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (seg >= n)
+        return;
+    int64_t lo = static_cast<int64_t>(rule.ptr[seg]) + rule.lower_offset;
+    int64_t hi = static_cast<int64_t>(rule.ptr[seg + 1]) + rule.upper_offset;
+    if (lo < hi && (lo < 0 || hi > rule.idx_size)) {
+        flags[0] = 1;
+        return;
+    }
+    unsigned long long hits = 0;
+    for (int64_t p = lo; p < hi; ++p) {
+        int64_t other = rule.idx[p];
+        if (rule.break_at_owner && other >= seg)
+            break;
+        int64_t src = rule.owner_is_source ? seg : other;
+        int64_t dst = rule.owner_is_source ? other : seg;
+        if (rule.guard == LCDHIP_GUARD_GREATER && !(dst > src))
+            continue;
+        if (rule.guard == LCDHIP_GUARD_NOT_EQUAL && src == dst)
+            continue;
+        if (other < 0 || other >= n) {
+            flags[0] = 1;
+            continue;
+        }
+        if (src >= dst)
+            flags[1] = 1;
+        keys[p] = (static_cast<unsigned long long>(src) << 32) |
+                  static_cast<unsigned long long>(dst);
+        atomicAdd(&edge_count[dst], 1);
+        ++hits;
+    }
+    if (hits)
+        atomicAdd(candidates, hits);
+}
+
+// From the sorted unique keys: successor array, unique in-degree and the
+// out-degree histogram (scanned into dag_ptr afterwards).
+__global__ void split_edges_kernel(const unsigned long long *__restrict__ keys,
+                                   int64_t edges,
+                                   int32_t *__restrict__ out_degree,
+                                   int32_t *__restrict__ dag_index,
+                                   int32_t *__restrict__ dep_count,
+                                   unsigned long long *__restrict__ transposed)
+{
+    int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (e >= edges)
+        return;
+    unsigned long long key = keys[e];
+    int64_t src = static_cast<int64_t>(key >> 32);
+    int32_t dst = static_cast<int32_t>(key & 0xffffffffull);
+    dag_index[e] = dst;
+    atomicAdd(&dep_count[dst], 1);
+    atomicAdd(&out_degree[src], 1);
+    if (transposed)
+        transposed[e] = (static_cast<unsigned long long>(dst) << 32) |
+                        static_cast<unsigned long long>(src);
+}
+
+__global__ void low_words_kernel(const unsigned long long *__restrict__ keys,
+                                 int64_t count, int32_t *__restrict__ out)
+{
+    int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (e < count)
+        out[e] = static_cast<int32_t>(keys[e] & 0xffffffffull);
+}
+
+__global__ void iota_kernel(int32_t *out, int64_t count)
+{
+    int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (i < count)
+        out[i] = static_cast<int32_t>(i);
+}
+
+// ---- level sets, algorithm 1: frontier expansion (Kahn) ------------------
+// counts[0..2] rotating frontier sizes, counts[3] scheduled nodes,
+// counts[4] number of levels.
+
+__global__ void kahn_seed_kernel(const int32_t *__restrict__ dep_count,
+                                 int64_t n, int32_t *__restrict__ frontier,
+                                 int32_t *__restrict__ counts)
+{
+    int64_t v = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (v < n && dep_count[v] == 0)
+        frontier[atomicAdd(&counts[0], 1)] = static_cast<int32_t>(v);
+}
+
+__global__ void kahn_expand_kernel(const int32_t *__restrict__ dag_ptr,
+                                   const int32_t *__restrict__ dag_index,
+                                   int32_t *__restrict__ remaining,
+                                   int32_t *__restrict__ level_of,
+                                   const int32_t *__restrict__ current,
+                                   int32_t *__restrict__ next,
+                                   int32_t *__restrict__ counts, int32_t level)
+{
+    const int32_t size = counts[level % 3];
+    int32_t *next_count = &counts[(level + 1) % 3];
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        counts[(level + 2) % 3] = 0;
+        if (size > 0) {
+            atomicAdd(&counts[3], size);
+            atomicMax(&counts[4], level + 1);
+        }
+    }
+    int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t q = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+         q < size; q += stride) {
+        int32_t v = current[q];
+        level_of[v] = level;
+        for (int32_t e = dag_ptr[v]; e < dag_ptr[v + 1]; ++e) {
+            int32_t w = dag_index[e];
+            if (atomicSub(&remaining[w], 1) == 1)
+                next[atomicAdd(next_count, 1)] = w;
+        }
+    }
+}
+
+// ---- level sets, algorithm 2: ordered sweep ------------------------------
+// Valid when every edge goes from a lower to a higher id.  Wavefronts take
+// 64 consecutive ids in order; level(v) = 1 + max level(pred).  Predecessors
+// inside the same 64-id chunk are read from LDS, so a dependency chain inside
+// a chunk advances at LDS latency; predecessors in earlier chunks are polled
+// in global memory.  Chunks are handed out in id order, so the lowest
+// unfinished chunk can always finish: no deadlock.  state[0] chunk counter,
+// state[1] watchdog flag, state[2] max level + 1.
+__global__ void __launch_bounds__(256)
+sweep_levels_kernel(const int32_t *__restrict__ pred_ptr,
+                    const int32_t *__restrict__ pred_index, int64_t n,
+                    int32_t *level_of, int32_t *state)
+{
+    __shared__ volatile int32_t chunk_level[4][64];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    int32_t highest = 0;
+    while (true) {
+        int32_t chunk = 0;
+        if (lane == 0)
+            chunk = atomicAdd(&state[0], 1);
+        chunk = __shfl(chunk, 0);
+        const int64_t base = static_cast<int64_t>(chunk) * 64;
+        if (base >= n)
+            break;
+        const int64_t v = base + lane;
+        bool pending = v < n;
+        chunk_level[wave][lane] = -1;
+        int32_t p = pending ? pred_ptr[v] : 0;
+        const int32_t p_end = pending ? pred_ptr[v + 1] : 0;
+        int32_t best = -1;
+        int64_t spins = 0;
+        while (__ballot(pending)) {
+            if (pending) {
+                while (p < p_end) {
+                    const int64_t u = pred_index[p];
+                    const int32_t l =
+                        u >= base ? chunk_level[wave][u - base]
+                                  : __hip_atomic_load(&level_of[u],
+                                                      __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+                    if (l < 0)
+                        break;
+                    best = l > best ? l : best;
+                    ++p;
+                }
+                if (p == p_end) {
+                    const int32_t mine = best + 1;
+                    chunk_level[wave][lane] = mine;
+                    __hip_atomic_store(&level_of[v], mine, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                    highest = mine + 1 > highest ? mine + 1 : highest;
+                    pending = false;
+                }
+            }
+            if (++spins > (1ll << 24) ||
+                ((spins & 1023) == 0 &&
+                 __hip_atomic_load(&state[1], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT))) {
+                state[1] = 1;
+                return;
+            }
+        }
+    }
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        int32_t other = __shfl_down(highest, offset);
+        highest = other > highest ? other : highest;
+    }
+    if (lane == 0 && highest > 0)
+        atomicMax(&state[2], highest);
+}
+
+__global__ void level_histogram_kernel(const int32_t *__restrict__ level_of,
+                                       int64_t n, int32_t *__restrict__ hist)
+{
+    int64_t v = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (v < n && level_of[v] >= 0)
+        atomicAdd(&hist[level_of[v]], 1);
+}
+
+inline unsigned blocks_for(int64_t count)
+{
+    return static_cast<unsigned>((count + kBlock - 1) / kBlock);
+}
+
+inline int bits_for(uint64_t max_value)
+{
+    int bits = 1;
+    while (bits < 64 && (max_value >> bits))
+        ++bits;
+    return bits;
+}
+
+struct Scratch {
+    std::vector<void *> owned;
+    ~Scratch()
+    {
+        for (void *p : owned)
+            if (p)
+                (void)hipFree(p);
+    }
+    template <class T>
+    hipError_t alloc(T **out, size_t count)
+    {
+        void *p = nullptr;
+        hipError_t status = hipMalloc(&p, std::max<size_t>(count, 1) * sizeof(T));
+        if (status == hipSuccess)
+            owned.push_back(p);
+        *out = static_cast<T *>(p);
+        return status;
+    }
+};
+
+}  // namespace
+
+extern "C" int lcdhip_dag_destroy(lcdhip_dag *dag)
+{
+    if (!dag)
+        return LCDHIP_OK;
+    for (int32_t *&array : dag->arrays)
+        if (array) {
+            (void)hipFree(array);
+            array = nullptr;
+        }
+    delete dag;
+    return LCDHIP_OK;
+}
+
+static int dag_alloc(lcdhip_dag *dag, int which, int64_t count)
+{
+    LCDHIP_CHECK(hipMalloc(&dag->arrays[which],
+                           std::max<int64_t>(count, 1) * sizeof(int32_t)));
+    dag->counts[which] = count;
+    return LCDHIP_OK;
+}
+
+static int build_levels(lcdhip_dag *dag, const unsigned long long *d_transposed,
+                        uint32_t flags, hipStream_t stream);
+
+extern "C" int lcdhip_dag_build(const lcdhip_dag_rule *rules, int rule_count,
+                                int64_t n, uint32_t flags, lcdhip_stream stream_,
+                                lcdhip_dag **out)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (!out || rule_count < 0 || (rule_count > 0 && !rules) || n < 0 ||
+        n >= (int64_t(1) << 31) - 1) {
+        set_error("bad argument to lcdhip_dag_build");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    *out = nullptr;
+    hipStream_t stream = resolve_stream(stream_);
+    int64_t key_capacity = 0;
+    for (int r = 0; r < rule_count; ++r) {
+        if (!rules[r].d_ptr || rules[r].idx_size < 0 ||
+            (rules[r].idx_size > 0 && !rules[r].d_idx)) {
+            set_error("rule %d has a NULL structure array", r);
+            return LCDHIP_ERR_ARGUMENT;
+        }
+        key_capacity += rules[r].idx_size;
+    }
+    if (key_capacity >= (int64_t(1) << 31)) {
+        set_error("more than 2^31 candidate edges are not supported");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+
+    lcdhip_dag *dag = new lcdhip_dag();
+    struct Guard {
+        lcdhip_dag *dag;
+        ~Guard() { if (dag) lcdhip_dag_destroy(dag); }
+    } guard{dag};
+    dag->info.n = n;
+    int status;
+    if ((status = dag_alloc(dag, LCDHIP_DAG_PTR, n + 1))) return status;
+    if ((status = dag_alloc(dag, LCDHIP_DAG_DEP_COUNT, n))) return status;
+    if ((status = dag_alloc(dag, LCDHIP_DAG_EDGE_COUNT, n))) return status;
+    int32_t *dag_ptr = dag->arrays[LCDHIP_DAG_PTR];
+    int32_t *dep_count = dag->arrays[LCDHIP_DAG_DEP_COUNT];
+    int32_t *edge_count = dag->arrays[LCDHIP_DAG_EDGE_COUNT];
+    LCDHIP_CHECK(hipMemsetAsync(dag_ptr, 0, (n + 1) * 4, stream));
+    LCDHIP_CHECK(hipMemsetAsync(dep_count, 0, std::max<int64_t>(n, 1) * 4, stream));
+    LCDHIP_CHECK(hipMemsetAsync(edge_count, 0, std::max<int64_t>(n, 1) * 4, stream));
+
+    Scratch scratch;
+    unsigned long long *keys = nullptr, *sorted = nullptr, *unique_keys = nullptr;
+    unsigned long long *d_candidates = nullptr;
+    int32_t *d_flags = nullptr;
+    LCDHIP_CHECK(scratch.alloc(&keys, key_capacity));
+    LCDHIP_CHECK(scratch.alloc(&sorted, key_capacity));
+    LCDHIP_CHECK(scratch.alloc(&d_candidates, 2));
+    LCDHIP_CHECK(scratch.alloc(&d_flags, 4));
+    LCDHIP_CHECK(hipMemsetAsync(keys, 0xff, std::max<int64_t>(key_capacity, 1) * 8, stream));
+    LCDHIP_CHECK(hipMemsetAsync(d_candidates, 0, 16, stream));
+    LCDHIP_CHECK(hipMemsetAsync(d_flags, 0, 16, stream));
+
+    int64_t offset = 0;
+    for (int r = 0; r < rule_count && n > 0; ++r) {
+        RuleDevice rule{rules[r].d_ptr,         rules[r].d_idx,
+                        rules[r].idx_size,      rules[r].owner_is_source,
+                        rules[r].lower_offset,  rules[r].upper_offset,
+                        rules[r].guard,         rules[r].break_at_owner};
+        hipLaunchKernelGGL(emit_keys_kernel, dim3(blocks_for(n)), dim3(kBlock),
+                           0, stream, rule, n, keys + offset, edge_count,
+                           d_flags, d_candidates);
+        offset += rules[r].idx_size;
+    }
+    LCDHIP_CHECK(hipGetLastError());
+    unsigned long long candidates = 0;
+    int32_t host_flags[4] = {0, 0, 0, 0};
+    LCDHIP_CHECK(hipMemcpyAsync(&candidates, d_candidates, 8,
+                                hipMemcpyDeviceToHost, stream));
+    LCDHIP_CHECK(hipMemcpyAsync(host_flags, d_flags, 16, hipMemcpyDeviceToHost,
+                                stream));
+    LCDHIP_CHECK(hipStreamSynchronize(stream));
+    if (host_flags[0]) {
+        set_error("a DAG edge endpoint or segment bound is out of range "
+                  "[0, %lld)", static_cast<long long>(n));
+        return LCDHIP_ERR_DAG_BOUNDS;
+    }
+    dag->info.topological_ids = host_flags[1] ? 0 : 1;
+
+    // sorted set of (src, dst) pairs
+    int64_t edges = 0;
+    if (candidates > 0) {
+        const int end_bit = std::min(64, 32 + bits_for(static_cast<uint64_t>(n)));
+        size_t temp_bytes = 0;
+        void *temp = nullptr;
+        // invalid keys are all ones: they stay last under any bit window
+        // that covers every valid key
+        LCDHIP_CHECK(rocprim::radix_sort_keys(nullptr, temp_bytes, keys, sorted,
+                                              static_cast<size_t>(key_capacity),
+                                              0, end_bit, stream));
+        LCDHIP_CHECK(scratch.alloc(reinterpret_cast<char **>(&temp), temp_bytes));
+        LCDHIP_CHECK(rocprim::radix_sort_keys(temp, temp_bytes, keys, sorted,
+                                              static_cast<size_t>(key_capacity),
+                                              0, end_bit, stream));
+        LCDHIP_CHECK(scratch.alloc(&unique_keys, candidates));
+        size_t unique_temp_bytes = 0;
+        void *unique_temp = nullptr;
+        LCDHIP_CHECK(rocprim::unique(nullptr, unique_temp_bytes, sorted,
+                                     unique_keys, d_candidates + 1,
+                                     static_cast<size_t>(candidates),
+                                     rocprim::equal_to<unsigned long long>(),
+                                     stream));
+        LCDHIP_CHECK(scratch.alloc(reinterpret_cast<char **>(&unique_temp),
+                                   unique_temp_bytes));
+        LCDHIP_CHECK(rocprim::unique(unique_temp, unique_temp_bytes, sorted,
+                                     unique_keys, d_candidates + 1,
+                                     static_cast<size_t>(candidates),
+                                     rocprim::equal_to<unsigned long long>(),
+                                     stream));
+        unsigned long long unique_count = 0;
+        LCDHIP_CHECK(hipMemcpyAsync(&unique_count, d_candidates + 1, 8,
+                                    hipMemcpyDeviceToHost, stream));
+        LCDHIP_CHECK(hipStreamSynchronize(stream));
+        edges = static_cast<int64_t>(unique_count);
+    }
+    dag->info.edges = edges;
+    if ((status = dag_alloc(dag, LCDHIP_DAG_INDEX, edges))) return status;
+
+    const bool want_levels = flags & LCDHIP_DAG_LEVELS;
+    const bool sweep = want_levels && dag->info.topological_ids &&
+                       !(flags & LCDHIP_DAG_FORCE_KAHN);
+    unsigned long long *transposed = nullptr;
+    if (sweep && edges > 0)
+        LCDHIP_CHECK(scratch.alloc(&transposed, edges));
+    if (edges > 0) {
+        int32_t *out_degree = nullptr;
+        LCDHIP_CHECK(scratch.alloc(&out_degree, n + 1));
+        LCDHIP_CHECK(hipMemsetAsync(out_degree, 0, (n + 1) * 4, stream));
+        hipLaunchKernelGGL(split_edges_kernel, dim3(blocks_for(edges)),
+                           dim3(kBlock), 0, stream, unique_keys, edges,
+                           out_degree, dag->arrays[LCDHIP_DAG_INDEX], dep_count,
+                           transposed);
+        LCDHIP_CHECK(hipGetLastError());
+        size_t scan_bytes = 0;
+        char *scan_temp = nullptr;
+        LCDHIP_CHECK(rocprim::exclusive_scan(
+            nullptr, scan_bytes, out_degree, dag_ptr, 0,
+            static_cast<size_t>(n + 1), rocprim::plus<int32_t>(), stream));
+        LCDHIP_CHECK(scratch.alloc(&scan_temp, scan_bytes));
+        LCDHIP_CHECK(rocprim::exclusive_scan(
+            scan_temp, scan_bytes, out_degree, dag_ptr, 0,
+            static_cast<size_t>(n + 1), rocprim::plus<int32_t>(), stream));
+    }
+    if (want_levels) {
+        // the forward keys are no longer needed: release them before the
+        // level pass allocates its own scratch
+        status = build_levels(dag, transposed, flags, stream);
+        if (status)
+            return status;
+    }
+    LCDHIP_CHECK(hipStreamSynchronize(stream));
+    guard.dag = nullptr;
+    *out = dag;
+    return LCDHIP_OK;
+}
+
+static int build_levels(lcdhip_dag *dag, const unsigned long long *d_transposed,
+                        uint32_t flags, hipStream_t stream)
+{
+    const int64_t n = dag->info.n, edges = dag->info.edges;
+    int status;
+    if ((status = dag_alloc(dag, LCDHIP_DAG_LEVEL_OF, n))) return status;
+    int32_t *level_of = dag->arrays[LCDHIP_DAG_LEVEL_OF];
+    LCDHIP_CHECK(hipMemsetAsync(level_of, 0xff, std::max<int64_t>(n, 1) * 4, stream));
+    const int32_t *dag_ptr = dag->arrays[LCDHIP_DAG_PTR];
+    const int32_t *dag_index = dag->arrays[LCDHIP_DAG_INDEX];
+    const int32_t *dep_count = dag->arrays[LCDHIP_DAG_DEP_COUNT];
+    Scratch scratch;
+    int64_t levels = 0, scheduled = 0;
+    const bool sweep = dag->info.topological_ids &&
+                       !(flags & LCDHIP_DAG_FORCE_KAHN);
+
+    if (n == 0) {
+        dag->info.level_algorithm = 0;
+    } else if (sweep) {
+        dag->info.level_algorithm = 2;
+        // predecessor CSR: offsets are the scan of the unique in-degree
+        int32_t *pred_ptr = nullptr, *pred_index = nullptr, *state = nullptr;
+        LCDHIP_CHECK(scratch.alloc(&pred_ptr, n + 1));
+        LCDHIP_CHECK(scratch.alloc(&pred_index, edges));
+        LCDHIP_CHECK(scratch.alloc(&state, 4));
+        LCDHIP_CHECK(hipMemsetAsync(state, 0, 16, stream));
+        {
+            size_t temp_bytes = 0;
+            char *temp = nullptr;
+            LCDHIP_CHECK(hipMemsetAsync(pred_ptr + n, 0, 4, stream));
+            LCDHIP_CHECK(rocprim::exclusive_scan(
+                nullptr, temp_bytes, dep_count, pred_ptr, 0,
+                static_cast<size_t>(n), rocprim::plus<int32_t>(), stream));
+            LCDHIP_CHECK(scratch.alloc(&temp, temp_bytes));
+            LCDHIP_CHECK(rocprim::exclusive_scan(
+                temp, temp_bytes, dep_count, pred_ptr, 0,
+                static_cast<size_t>(n), rocprim::plus<int32_t>(), stream));
+            int32_t total = static_cast<int32_t>(edges);
+            LCDHIP_CHECK(hipMemcpyAsync(pred_ptr + n, &total, 4,
+                                        hipMemcpyHostToDevice, stream));
+            LCDHIP_CHECK(hipStreamSynchronize(stream));
+        }
+        if (edges > 0) {
+            unsigned long long *sorted = nullptr;
+            LCDHIP_CHECK(scratch.alloc(&sorted, edges));
+            size_t temp_bytes = 0;
+            char *temp = nullptr;
+            LCDHIP_CHECK(rocprim::radix_sort_keys(
+                nullptr, temp_bytes, d_transposed, sorted,
+                static_cast<size_t>(edges), 0, 64, stream));
+            LCDHIP_CHECK(scratch.alloc(&temp, temp_bytes));
+            LCDHIP_CHECK(rocprim::radix_sort_keys(
+                temp, temp_bytes, d_transposed, sorted,
+                static_cast<size_t>(edges), 0, 64, stream));
+            hipLaunchKernelGGL(low_words_kernel, dim3(blocks_for(edges)),
+                               dim3(kBlock), 0, stream, sorted, edges,
+                               pred_index);
+        }
+        const int64_t chunks = (n + 63) / 64;
+        const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(
+            (chunks + 3) / 4,
+            static_cast<int64_t>(lcdhip::context().props.multiProcessorCount) * 8));
+        hipLaunchKernelGGL(sweep_levels_kernel, dim3(blocks), dim3(256), 0,
+                           stream, pred_ptr, pred_index, n, level_of, state);
+        LCDHIP_CHECK(hipGetLastError());
+        int32_t host_state[4] = {0, 0, 0, 0};
+        LCDHIP_CHECK(hipMemcpyAsync(host_state, state, 16, hipMemcpyDeviceToHost,
+                                    stream));
+        LCDHIP_CHECK(hipStreamSynchronize(stream));
+        if (host_state[1]) {
+            set_error("the ordered level sweep gave up waiting");
+            return LCDHIP_ERR_WATCHDOG;
+        }
+        levels = host_state[2];
+        scheduled = n;
+    } else {
+        dag->info.level_algorithm = 1;
+        int32_t *remaining = nullptr, *frontier_a = nullptr, *frontier_b = nullptr;
+        int32_t *frontier_c = nullptr, *counts = nullptr;
+        LCDHIP_CHECK(scratch.alloc(&remaining, n));
+        LCDHIP_CHECK(scratch.alloc(&frontier_a, n));
+        LCDHIP_CHECK(scratch.alloc(&frontier_b, n));
+        LCDHIP_CHECK(scratch.alloc(&frontier_c, n));
+        LCDHIP_CHECK(scratch.alloc(&counts, 8));
+        LCDHIP_CHECK(hipMemcpyAsync(remaining, dep_count, n * 4,
+                                    hipMemcpyDeviceToDevice, stream));
+        LCDHIP_CHECK(hipMemsetAsync(counts, 0, 32, stream));
+        hipLaunchKernelGGL(kahn_seed_kernel, dim3(blocks_for(n)), dim3(kBlock),
+                           0, stream, dep_count, n, frontier_a, counts);
+        int32_t *frontiers[3] = {frontier_a, frontier_b, frontier_c};
+        const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(
+            blocks_for(n),
+            static_cast<int64_t>(lcdhip::context().props.multiProcessorCount) * 4));
+        int32_t level = 0;
+        int32_t host_counts[8];
+        while (true) {
+            const int batch = 32;
+            for (int step = 0; step < batch; ++step, ++level)
+                hipLaunchKernelGGL(kahn_expand_kernel, dim3(blocks),
+                                   dim3(kBlock), 0, stream, dag_ptr, dag_index,
+                                   remaining, level_of, frontiers[level % 3],
+                                   frontiers[(level + 1) % 3], counts, level);
+            LCDHIP_CHECK(hipGetLastError());
+            LCDHIP_CHECK(hipMemcpyAsync(host_counts, counts, 32,
+                                        hipMemcpyDeviceToHost, stream));
+            LCDHIP_CHECK(hipStreamSynchronize(stream));
+            if (host_counts[level % 3] == 0 || level > n + batch)
+                break;
+        }
+        levels = host_counts[4];
+        scheduled = host_counts[3];
+    }
+    dag->info.levels = levels;
+    dag->info.scheduled = scheduled;
+
+    // wavefront_ptr = exclusive scan of the level histogram; wavefronts =
+    // node ids stably sorted by level (ascending id inside a level)
+    if ((status = dag_alloc(dag, LCDHIP_DAG_WAVEFRONT_PTR, levels + 1))) return status;
+    if ((status = dag_alloc(dag, LCDHIP_DAG_WAVEFRONTS, scheduled))) return status;
+    int32_t *wavefront_ptr = dag->arrays[LCDHIP_DAG_WAVEFRONT_PTR];
+    LCDHIP_CHECK(hipMemsetAsync(wavefront_ptr, 0, (levels + 1) * 4, stream));
+    if (n > 0 && levels > 0) {
+        int32_t *hist = nullptr;
+        LCDHIP_CHECK(scratch.alloc(&hist, levels + 1));
+        LCDHIP_CHECK(hipMemsetAsync(hist, 0, (levels + 1) * 4, stream));
+        hipLaunchKernelGGL(level_histogram_kernel, dim3(blocks_for(n)),
+                           dim3(kBlock), 0, stream, level_of, n, hist);
+        size_t temp_bytes = 0;
+        char *temp = nullptr;
+        LCDHIP_CHECK(rocprim::exclusive_scan(
+            nullptr, temp_bytes, hist, wavefront_ptr, 0,
+            static_cast<size_t>(levels + 1), rocprim::plus<int32_t>(), stream));
+        LCDHIP_CHECK(scratch.alloc(&temp, temp_bytes));
+        LCDHIP_CHECK(rocprim::exclusive_scan(
+            temp, temp_bytes, hist, wavefront_ptr, 0,
+            static_cast<size_t>(levels + 1), rocprim::plus<int32_t>(), stream));
+
+        int32_t *ids = nullptr, *sorted_ids = nullptr;
+        uint32_t *sorted_levels = nullptr;
+        LCDHIP_CHECK(scratch.alloc(&ids, n));
+        LCDHIP_CHECK(scratch.alloc(&sorted_ids, n));
+        LCDHIP_CHECK(scratch.alloc(&sorted_levels, n));
+        hipLaunchKernelGGL(iota_kernel, dim3(blocks_for(n)), dim3(kBlock), 0,
+                           stream, ids, n);
+        // unscheduled nodes carry level -1 = 0xffffffff and sort last
+        const int end_bit = scheduled == n ? bits_for(static_cast<uint64_t>(levels)) : 32;
+        size_t sort_bytes = 0;
+        char *sort_temp = nullptr;
+        LCDHIP_CHECK(rocprim::radix_sort_pairs(
+            nullptr, sort_bytes, reinterpret_cast<const uint32_t *>(level_of),
+            sorted_levels, ids, sorted_ids, static_cast<size_t>(n), 0, end_bit,
+            stream));
+        LCDHIP_CHECK(scratch.alloc(&sort_temp, sort_bytes));
+        LCDHIP_CHECK(rocprim::radix_sort_pairs(
+            sort_temp, sort_bytes, reinterpret_cast<const uint32_t *>(level_of),
+            sorted_levels, ids, sorted_ids, static_cast<size_t>(n), 0, end_bit,
+            stream));
+        LCDHIP_CHECK(hipMemcpyAsync(dag->arrays[LCDHIP_DAG_WAVEFRONTS],
+                                    sorted_ids, scheduled * 4,
+                                    hipMemcpyDeviceToDevice, stream));
+        std::vector<int32_t> host_ptr(levels + 1);
+        LCDHIP_CHECK(hipMemcpyAsync(host_ptr.data(), wavefront_ptr,
+                                    (levels + 1) * 4, hipMemcpyDeviceToHost,
+                                    stream));
+        LCDHIP_CHECK(hipStreamSynchronize(stream));
+        int64_t widest = 0;
+        for (int64_t l = 0; l < levels; ++l)
+            widest = std::max<int64_t>(widest, host_ptr[l + 1] - host_ptr[l]);
+        dag->info.max_level_width = widest;
+    }
+    LCDHIP_CHECK(hipStreamSynchronize(stream));
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_dag_get_info(const lcdhip_dag *dag, lcdhip_dag_info *out)
+{
+    if (!dag || !out) {
+        set_error("dag/out must not be NULL");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    *out = dag->info;
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_dag_array(const lcdhip_dag *dag, int which, void **d_out,
+                                int64_t *count_out)
+{
+    if (!dag || which < 0 || which > 6 || !d_out || !count_out) {
+        set_error("bad argument to lcdhip_dag_array");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    if (!dag->arrays[which]) {
+        set_error("DAG array %d was not built (levels not requested?)", which);
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    *d_out = dag->arrays[which];
+    *count_out = dag->counts[which];
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_dag_download(const lcdhip_dag *dag, int which,
+                                   int32_t *host_out, int64_t capacity)
+{
+    LCDHIP_REQUIRE_INIT();
+    void *d_ptr = nullptr;
+    int64_t count = 0;
+    int status = lcdhip_dag_array(dag, which, &d_ptr, &count);
+    if (status)
+        return status;
+    if (capacity < count || (count > 0 && !host_out)) {
+        set_error("host buffer too small: %lld < %lld",
+                  static_cast<long long>(capacity), static_cast<long long>(count));
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    if (count > 0)
+        LCDHIP_CHECK(hipMemcpy(host_out, d_ptr, count * 4, hipMemcpyDeviceToHost));
+    return LCDHIP_OK;
+}

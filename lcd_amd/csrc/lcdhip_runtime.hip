@@ -1,0 +1,889 @@
+// Host runtime of liblcdhip.so: context, buffers, streams, run-time
+// compilation (hiprtc), module launch, the wavefront level loop, hipGraph
+// capture, and a few utility kernels (fill, digest, diagonal lookup, machine
+// constant probes).  Replaces compiler/cuda_runtime.py and the device-facing
+// half of compiler/scheduler.py of the reference.
+#include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "lcdhip_common.h"
+
+namespace lcdhip {
+
+static thread_local std::string g_error;
+
+void set_error(const char *format, ...)
+{
+    char buffer[2048];
+    va_list args;
+    va_start(args, format);
+    vsnprintf(buffer, sizeof(buffer), format, args);
+    va_end(args);
+    g_error = buffer;
+}
+
+Context &context()
+{
+    static Context ctx;
+    return ctx;
+}
+
+bool initialised() { return context().ready; }
+
+hipStream_t resolve_stream(lcdhip_stream stream)
+{
+    return stream ? reinterpret_cast<hipStream_t>(stream) : context().stream;
+}
+
+}  // namespace lcdhip
+
+using lcdhip::context;
+using lcdhip::resolve_stream;
+using lcdhip::set_error;
+
+struct lcdhip_module {
+    hipModule_t module = nullptr;
+};
+struct lcdhip_kernel {
+    hipFunction_t function = nullptr;
+};
+struct lcdhip_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+extern "C" const char *lcdhip_last_error(void) { return lcdhip::g_error.c_str(); }
+
+extern "C" const char *lcdhip_version(void) { return "lcdhip 0.1 (gfx950)"; }
+
+extern "C" int lcdhip_device_count(int *count)
+{
+    if (!count) {
+        set_error("count is NULL");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    *count = 0;
+    hipError_t status = hipGetDeviceCount(count);
+    if (status != hipSuccess) {
+        *count = 0;
+        set_error("hipGetDeviceCount: %s", hipGetErrorString(status));
+        return LCDHIP_ERR_NO_DEVICE;
+    }
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_init(int device)
+{
+    auto &ctx = context();
+    if (ctx.ready && ctx.device == device)
+        return LCDHIP_OK;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+        set_error("no HIP device is visible; liblcdhip needs an MI355X-class GPU");
+        return LCDHIP_ERR_NO_DEVICE;
+    }
+    if (device < 0 || device >= count) {
+        set_error("device %d out of range (found %d)", device, count);
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    LCDHIP_CHECK(hipSetDevice(device));
+    LCDHIP_CHECK(hipGetDeviceProperties(&ctx.props, device));
+    if (ctx.stream == nullptr)
+        LCDHIP_CHECK(hipStreamCreateWithFlags(&ctx.stream, hipStreamNonBlocking));
+    ctx.device = device;
+    ctx.ready = true;
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_shutdown(void)
+{
+    auto &ctx = context();
+    if (!ctx.ready)
+        return LCDHIP_OK;
+    LCDHIP_CHECK(hipStreamSynchronize(ctx.stream));
+    LCDHIP_CHECK(hipStreamDestroy(ctx.stream));
+    ctx.stream = nullptr;
+    ctx.ready = false;
+    ctx.device = -1;
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_device_props(lcdhip_props *out)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (!out) {
+        set_error("out is NULL");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    const hipDeviceProp_t &p = context().props;
+    memset(out, 0, sizeof(*out));
+    out->compute_units = p.multiProcessorCount;
+    // gfx942/gfx950 parts group their CUs into XCDs of 32 (some fused off).
+    out->xcd_count = std::max(1, (p.multiProcessorCount + 37) / 38);
+    out->wavefront_size = p.warpSize;
+    out->max_threads_per_block = p.maxThreadsPerBlock;
+    out->lds_bytes_per_block = static_cast<int32_t>(p.sharedMemPerBlock);
+    out->lds_bytes_per_cu = static_cast<int32_t>(p.maxSharedMemoryPerMultiProcessor);
+    out->clock_khz = p.clockRate;
+    out->memory_clock_khz = p.memoryClockRate;
+    out->memory_bus_bits = p.memoryBusWidth;
+    out->l2_bytes = p.l2CacheSize;
+    out->global_memory_bytes = static_cast<int64_t>(p.totalGlobalMem);
+    snprintf(out->name, sizeof(out->name), "%s", p.name);
+    snprintf(out->arch, sizeof(out->arch), "%s", p.gcnArchName);
+    return LCDHIP_OK;
+}
+
+// ------------------------------------------------------------ buffers ----
+
+extern "C" int lcdhip_buffer_alloc(size_t bytes, void **d_out)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (!d_out) {
+        set_error("d_out is NULL");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    *d_out = nullptr;
+    LCDHIP_CHECK(hipMalloc(d_out, bytes ? bytes : 4));
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_buffer_free(void *d_ptr)
+{
+    if (!d_ptr)
+        return LCDHIP_OK;
+    LCDHIP_CHECK(hipFree(d_ptr));
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_buffer_upload(void *d_dst, const void *host_src,
+                                    size_t bytes, lcdhip_stream stream)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (bytes == 0)
+        return LCDHIP_OK;
+    LCDHIP_CHECK(hipMemcpyAsync(d_dst, host_src, bytes, hipMemcpyHostToDevice,
+                                resolve_stream(stream)));
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_buffer_download(void *host_dst, const void *d_src,
+                                      size_t bytes, lcdhip_stream stream)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (bytes == 0)
+        return LCDHIP_OK;
+    LCDHIP_CHECK(hipMemcpyAsync(host_dst, d_src, bytes, hipMemcpyDeviceToHost,
+                                resolve_stream(stream)));
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_buffer_copy(void *d_dst, const void *d_src, size_t bytes,
+                                  lcdhip_stream stream)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (bytes == 0)
+        return LCDHIP_OK;
+    LCDHIP_CHECK(hipMemcpyAsync(d_dst, d_src, bytes, hipMemcpyDeviceToDevice,
+                                resolve_stream(stream)));
+    return LCDHIP_OK;
+}
+
+__global__ void lcdhip_fill32_kernel(uint32_t *dst, uint32_t value, size_t count)
+{
+    size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+    size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (; i < count; i += stride)
+        dst[i] = value;
+}
+
+extern "C" int lcdhip_buffer_fill32(void *d_dst, uint32_t value, size_t count,
+                                    lcdhip_stream stream)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (count == 0)
+        return LCDHIP_OK;
+    unsigned blocks = static_cast<unsigned>(
+        std::min<size_t>((count + 255) / 256, 16384));
+    hipLaunchKernelGGL(lcdhip_fill32_kernel, dim3(blocks), dim3(256), 0,
+                       resolve_stream(stream), static_cast<uint32_t *>(d_dst),
+                       value, count);
+    LCDHIP_CHECK(hipGetLastError());
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_host_alloc(size_t bytes, void **host_out)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (!host_out) {
+        set_error("host_out is NULL");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    LCDHIP_CHECK(hipHostMalloc(host_out, bytes ? bytes : 4, hipHostMallocDefault));
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_host_free(void *host_ptr)
+{
+    if (!host_ptr)
+        return LCDHIP_OK;
+    LCDHIP_CHECK(hipHostFree(host_ptr));
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_stream_create(lcdhip_stream *out)
+{
+    LCDHIP_REQUIRE_INIT();
+    hipStream_t stream = nullptr;
+    LCDHIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+    *out = stream;
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_stream_destroy(lcdhip_stream stream)
+{
+    if (!stream)
+        return LCDHIP_OK;
+    LCDHIP_CHECK(hipStreamDestroy(reinterpret_cast<hipStream_t>(stream)));
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_stream_sync(lcdhip_stream stream)
+{
+    LCDHIP_REQUIRE_INIT();
+    LCDHIP_CHECK(hipStreamSynchronize(resolve_stream(stream)));
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_event_create(lcdhip_event *out)
+{
+    LCDHIP_REQUIRE_INIT();
+    hipEvent_t event = nullptr;
+    LCDHIP_CHECK(hipEventCreate(&event));
+    *out = event;
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_event_destroy(lcdhip_event event)
+{
+    if (!event)
+        return LCDHIP_OK;
+    LCDHIP_CHECK(hipEventDestroy(reinterpret_cast<hipEvent_t>(event)));
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_event_record(lcdhip_event event, lcdhip_stream stream)
+{
+    LCDHIP_REQUIRE_INIT();
+    LCDHIP_CHECK(hipEventRecord(reinterpret_cast<hipEvent_t>(event),
+                                resolve_stream(stream)));
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_event_elapsed_ms(lcdhip_event start, lcdhip_event stop,
+                                       float *ms)
+{
+    LCDHIP_REQUIRE_INIT();
+    LCDHIP_CHECK(hipEventSynchronize(reinterpret_cast<hipEvent_t>(stop)));
+    LCDHIP_CHECK(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start),
+                                     reinterpret_cast<hipEvent_t>(stop)));
+    return LCDHIP_OK;
+}
+
+// ------------------------------------------------------------ modules ----
+
+extern "C" void lcdhip_free_host(void *ptr) { free(ptr); }
+
+extern "C" int lcdhip_module_compile_code(const char *source, const char *name,
+                                          const char *const *options,
+                                          int option_count, void **code_out,
+                                          size_t *size_out, char **log_out)
+{
+    if (!source || !code_out || !size_out) {
+        set_error("source/code_out/size_out must not be NULL");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    *code_out = nullptr;
+    *size_out = 0;
+    if (log_out)
+        *log_out = nullptr;
+    hiprtcProgram program = nullptr;
+    hiprtcResult result = hiprtcCreateProgram(
+        &program, source, name ? name : "lcd_generated.hip", 0, nullptr, nullptr);
+    if (result != HIPRTC_SUCCESS) {
+        set_error("hiprtcCreateProgram: %s", hiprtcGetErrorString(result));
+        return LCDHIP_ERR_COMPILE;
+    }
+    std::vector<const char *> opts(options, options + option_count);
+    result = hiprtcCompileProgram(program, static_cast<int>(opts.size()),
+                                  opts.data());
+    size_t log_size = 0;
+    hiprtcGetProgramLogSize(program, &log_size);
+    std::string log(log_size, '\0');
+    if (log_size)
+        hiprtcGetProgramLog(program, log.data());
+    if (log_out) {
+        *log_out = static_cast<char *>(malloc(log.size() + 1));
+        memcpy(*log_out, log.c_str(), log.size() + 1);
+    }
+    if (result != HIPRTC_SUCCESS) {
+        set_error("hiprtc: %s\n%s", hiprtcGetErrorString(result), log.c_str());
+        hiprtcDestroyProgram(&program);
+        return LCDHIP_ERR_COMPILE;
+    }
+    size_t code_size = 0;
+    hiprtcGetCodeSize(program, &code_size);
+    void *code = malloc(code_size ? code_size : 1);
+    hiprtcGetCode(program, static_cast<char *>(code));
+    hiprtcDestroyProgram(&program);
+    *code_out = code;
+    *size_out = code_size;
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_module_load(const void *code, size_t size,
+                                  lcdhip_module **out)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (!code || !size || !out) {
+        set_error("code/out must not be NULL");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    auto *module = new lcdhip_module();
+    hipError_t status = hipModuleLoadData(&module->module, code);
+    if (status != hipSuccess) {
+        set_error("hipModuleLoadData: %s", hipGetErrorString(status));
+        delete module;
+        return LCDHIP_ERR_HIP;
+    }
+    *out = module;
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_module_destroy(lcdhip_module *module)
+{
+    if (!module)
+        return LCDHIP_OK;
+    hipError_t status = hipModuleUnload(module->module);
+    delete module;
+    if (status != hipSuccess) {
+        set_error("hipModuleUnload: %s", hipGetErrorString(status));
+        return LCDHIP_ERR_HIP;
+    }
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_module_get_kernel(lcdhip_module *module, const char *name,
+                                        lcdhip_kernel **out)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (!module || !name || !out) {
+        set_error("module/name/out must not be NULL");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    hipFunction_t function = nullptr;
+    hipError_t status = hipModuleGetFunction(&function, module->module, name);
+    if (status != hipSuccess) {
+        set_error("generated symbol '%s' was not bound: %s", name,
+                  hipGetErrorString(status));
+        return LCDHIP_ERR_HIP;
+    }
+    auto *kernel = new lcdhip_kernel();
+    kernel->function = function;
+    *out = kernel;  // owned by the module's lifetime; small, freed at unload
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_kernel_max_resident_blocks(lcdhip_kernel *kernel,
+                                                 int block_threads,
+                                                 size_t lds_bytes,
+                                                 int *blocks_out)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (!kernel || !blocks_out || block_threads <= 0) {
+        set_error("bad kernel/blocks_out/block_threads");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    int per_cu = 0;
+    LCDHIP_CHECK(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(
+        &per_cu, kernel->function, block_threads, lds_bytes));
+    *blocks_out = per_cu * context().props.multiProcessorCount;
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_launch(lcdhip_kernel *kernel, uint32_t grid_x,
+                             uint32_t block_x, size_t lds_bytes,
+                             lcdhip_stream stream, void **args)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (!kernel || block_x == 0 || block_x > 1024) {
+        set_error("bad kernel handle or block size %u", block_x);
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    if (grid_x == 0)
+        return LCDHIP_OK;
+    LCDHIP_CHECK(hipModuleLaunchKernel(kernel->function, grid_x, 1, 1, block_x,
+                                       1, 1, static_cast<unsigned>(lds_bytes),
+                                       resolve_stream(stream), args, nullptr));
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_launch_levels(lcdhip_kernel *kernel,
+                                    const int32_t *host_ptr,
+                                    int64_t level_count, int32_t tasks_per_block,
+                                    uint32_t block_x, size_t lds_bytes,
+                                    lcdhip_stream stream, void **args,
+                                    int start_arg, int end_arg)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (!kernel || !host_ptr || !args || tasks_per_block <= 0 || block_x == 0 ||
+        block_x > 1024 || start_arg < 0 || end_arg < 0) {
+        set_error("bad argument to lcdhip_launch_levels");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    hipStream_t hip_stream = resolve_stream(stream);
+    for (int64_t level = 0; level < level_count; ++level) {
+        int32_t begin = host_ptr[level], end = host_ptr[level + 1];
+        if (end <= begin)
+            continue;
+        *static_cast<int32_t *>(args[start_arg]) = begin;
+        *static_cast<int32_t *>(args[end_arg]) = end;
+        uint32_t blocks = static_cast<uint32_t>(
+            (static_cast<int64_t>(end) - begin + tasks_per_block - 1) /
+            tasks_per_block);
+        LCDHIP_CHECK(hipModuleLaunchKernel(
+            kernel->function, blocks, 1, 1, block_x, 1, 1,
+            static_cast<unsigned>(lds_bytes), hip_stream, args, nullptr));
+    }
+    return LCDHIP_OK;
+}
+
+// ------------------------------------------------------------- graphs ----
+
+extern "C" int lcdhip_graph_begin_capture(lcdhip_stream stream)
+{
+    LCDHIP_REQUIRE_INIT();
+    LCDHIP_CHECK(hipStreamBeginCapture(resolve_stream(stream),
+                                       hipStreamCaptureModeRelaxed));
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_graph_end_capture(lcdhip_stream stream, lcdhip_graph **out)
+{
+    LCDHIP_REQUIRE_INIT();
+    auto *graph = new lcdhip_graph();
+    hipError_t status = hipStreamEndCapture(resolve_stream(stream), &graph->graph);
+    if (status != hipSuccess) {
+        set_error("hipStreamEndCapture: %s", hipGetErrorString(status));
+        delete graph;
+        return LCDHIP_ERR_HIP;
+    }
+    status = hipGraphInstantiate(&graph->exec, graph->graph, nullptr, nullptr, 0);
+    if (status != hipSuccess) {
+        set_error("hipGraphInstantiate: %s", hipGetErrorString(status));
+        (void)hipGraphDestroy(graph->graph);
+        delete graph;
+        return LCDHIP_ERR_HIP;
+    }
+    *out = graph;
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_graph_launch(lcdhip_graph *graph, lcdhip_stream stream)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (!graph) {
+        set_error("graph is NULL");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    LCDHIP_CHECK(hipGraphLaunch(graph->exec, resolve_stream(stream)));
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_graph_destroy(lcdhip_graph *graph)
+{
+    if (!graph)
+        return LCDHIP_OK;
+    (void)hipGraphExecDestroy(graph->exec);
+    (void)hipGraphDestroy(graph->graph);
+    delete graph;
+    return LCDHIP_OK;
+}
+
+// ------------------------------------------------------ lookup tables ----
+
+// One lane per segment.  status[0] collects the worst error seen:
+// 1 = pointer array not monotone / out of range, 2 = unsorted segment.
+__global__ void lcdhip_lookup_kernel(const int32_t *__restrict__ ptr,
+                                     const int32_t *__restrict__ idx, int64_t n,
+                                     int64_t idx_size,
+                                     int32_t *__restrict__ positions,
+                                     int32_t *status)
+{
+    int64_t s = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (s >= n)
+        return;
+    int64_t start = ptr[s], end = ptr[s + 1];
+    int32_t found = -1;
+    if (start < 0 || end < start || end > idx_size) {
+        atomicMax(status, 1);
+        positions[s] = -1;
+        return;
+    }
+    bool sorted = true;
+    for (int64_t p = start + 1; p < end; ++p)
+        sorted = sorted && idx[p] >= idx[p - 1];
+    if (!sorted)
+        atomicMax(status, 2);
+    int64_t lo = start, hi = end;
+    while (lo < hi) {
+        int64_t mid = (lo + hi) >> 1;
+        if (idx[mid] < s)
+            lo = mid + 1;
+        else
+            hi = mid;
+    }
+    if (lo < end && idx[lo] == s)
+        found = static_cast<int32_t>(lo);
+    positions[s] = found;
+}
+
+extern "C" int lcdhip_lookup_build(const int32_t *d_ptr, const int32_t *d_idx,
+                                   int64_t n, int64_t idx_size,
+                                   int32_t *d_positions, lcdhip_stream stream)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (n < 0 || !d_ptr || (n > 0 && !d_positions)) {
+        set_error("bad argument to lcdhip_lookup_build");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    hipStream_t hip_stream = resolve_stream(stream);
+    int32_t *d_status = nullptr;
+    LCDHIP_CHECK(hipMalloc(&d_status, 4));
+    LCDHIP_CHECK(hipMemsetAsync(d_status, 0, 4, hip_stream));
+    if (n > 0) {
+        unsigned blocks = static_cast<unsigned>((n + 255) / 256);
+        hipLaunchKernelGGL(lcdhip_lookup_kernel, dim3(blocks), dim3(256), 0,
+                           hip_stream, d_ptr, d_idx, n, idx_size, d_positions,
+                           d_status);
+    }
+    int32_t status = 0;
+    hipError_t copy_status = hipMemcpyAsync(&status, d_status, 4,
+                                            hipMemcpyDeviceToHost, hip_stream);
+    if (copy_status == hipSuccess)
+        copy_status = hipStreamSynchronize(hip_stream);
+    (void)hipFree(d_status);
+    if (copy_status != hipSuccess) {
+        set_error("lookup kernel failed: %s", hipGetErrorString(copy_status));
+        return LCDHIP_ERR_HIP;
+    }
+    if (status == 1) {
+        set_error("invalid pointer segment in the structural lookup arrays");
+        return LCDHIP_ERR_LOOKUP_POINTER;
+    }
+    if (status == 2) {
+        set_error("a segment violates the segmented_monotonically_increasing "
+                  "property");
+        return LCDHIP_ERR_LOOKUP_ORDER;
+    }
+    return LCDHIP_OK;
+}
+
+// -------------------------------------------------------------- digest ----
+
+__device__ inline uint64_t lcdhip_mix64(uint64_t x)
+{
+    x ^= x >> 30;
+    x *= 0xbf58476d1ce4e5b9ull;
+    x ^= x >> 27;
+    x *= 0x94d049bb133111ebull;
+    x ^= x >> 31;
+    return x;
+}
+
+// Position-salted word hashes combined with + and ^ (both commutative, so the
+// digest does not depend on the order in which waves finish).
+__global__ void lcdhip_digest_kernel(const uint32_t *__restrict__ words,
+                                     size_t count, unsigned long long *out)
+{
+    size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+    size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    uint64_t sum = 0, mixed = 0;
+    for (; i < count; i += stride) {
+        uint64_t h = lcdhip_mix64((static_cast<uint64_t>(words[i]) << 32) ^
+                                  (i * 0x9e3779b97f4a7c15ull + 1));
+        sum += h;
+        mixed ^= lcdhip_mix64(h + 0x632be59bd9b4e019ull);
+    }
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        sum += __shfl_down(sum, offset);
+        mixed ^= __shfl_down(mixed, offset);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        atomicAdd(&out[0], static_cast<unsigned long long>(sum));
+        atomicXor(&out[1], static_cast<unsigned long long>(mixed));
+    }
+}
+
+extern "C" int lcdhip_digest(const void *d_data, size_t bytes, uint64_t out[2],
+                             lcdhip_stream stream)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (!out || (bytes & 3)) {
+        set_error("digest needs out and a multiple of 4 bytes");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    hipStream_t hip_stream = resolve_stream(stream);
+    unsigned long long *d_out = nullptr;
+    LCDHIP_CHECK(hipMalloc(&d_out, 16));
+    LCDHIP_CHECK(hipMemsetAsync(d_out, 0, 16, hip_stream));
+    size_t count = bytes / 4;
+    if (count) {
+        unsigned blocks = static_cast<unsigned>(
+            std::min<size_t>((count + 255) / 256, 8192));
+        hipLaunchKernelGGL(lcdhip_digest_kernel, dim3(blocks), dim3(256), 0,
+                           hip_stream, static_cast<const uint32_t *>(d_data),
+                           count, d_out);
+    }
+    hipError_t status = hipMemcpyAsync(out, d_out, 16, hipMemcpyDeviceToHost,
+                                       hip_stream);
+    if (status == hipSuccess)
+        status = hipStreamSynchronize(hip_stream);
+    (void)hipFree(d_out);
+    if (status != hipSuccess) {
+        set_error("digest failed: %s", hipGetErrorString(status));
+        return LCDHIP_ERR_HIP;
+    }
+    out[0] ^= static_cast<uint64_t>(bytes) * 0x9e3779b97f4a7c15ull;
+    return LCDHIP_OK;
+}
+
+// ---------------------------------------------------- machine constants ----
+
+__global__ void lcdhip_empty_kernel() {}
+
+__global__ void lcdhip_release_probe_kernel(int32_t *counters, int32_t nodes,
+                                            int32_t stride)
+{
+    if (threadIdx.x == 0) {
+        int32_t node = blockIdx.x;
+        atomicSub(&counters[(static_cast<int64_t>(node) * stride) % nodes], 1);
+    }
+}
+
+__global__ void lcdhip_copy_probe_kernel(const float4 *__restrict__ src,
+                                         float4 *__restrict__ dst, size_t count)
+{
+    size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+    size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (; i < count; i += stride)
+        dst[i] = src[i];
+}
+
+// Two workgroups bounce a flag `hops` times.  Consecutive workgroup ids land
+// on different XCDs, so the hop crosses L2s: the cost a dependent task pays in
+// the sync-free executor.  Every wait is bounded.
+__global__ void lcdhip_handoff_probe_kernel(int32_t *flag, int32_t hops,
+                                            int32_t *timed_out)
+{
+    if (threadIdx.x != 0 || blockIdx.x > 1)
+        return;
+    const int32_t me = blockIdx.x;
+    for (int32_t hop = me; hop < hops; hop += 2) {
+        int64_t spins = 0;
+        while (__hip_atomic_load(flag, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT) != hop) {
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins > (1ll << 22)) {
+                *timed_out = 1;
+                return;
+            }
+        }
+        __atomic_thread_fence(__ATOMIC_ACQUIRE);
+        __atomic_thread_fence(__ATOMIC_RELEASE);
+        __hip_atomic_store(flag, hop + 1, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// `rounds` barriers over a grid that the host sized to be fully resident.
+__global__ void lcdhip_barrier_probe_kernel(int32_t *arrive, int32_t rounds,
+                                            int32_t *timed_out)
+{
+    for (int32_t round = 0; round < rounds; ++round) {
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            __atomic_thread_fence(__ATOMIC_RELEASE);
+            __hip_atomic_fetch_add(&arrive[round], 1, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            int64_t spins = 0;
+            while (__hip_atomic_load(&arrive[round], __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT) <
+                   static_cast<int32_t>(gridDim.x)) {
+                __builtin_amdgcn_s_sleep(1);
+                if (++spins > (1ll << 22)) {
+                    *timed_out = 1;
+                    break;
+                }
+            }
+            __atomic_thread_fence(__ATOMIC_ACQUIRE);
+        }
+        __syncthreads();
+    }
+}
+
+static double median(std::vector<double> samples)
+{
+    std::sort(samples.begin(), samples.end());
+    return samples[samples.size() / 2];
+}
+
+extern "C" int lcdhip_measure_arch(lcdhip_arch *out)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (!out) {
+        set_error("out is NULL");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    auto &ctx = context();
+    hipStream_t stream = ctx.stream;
+    memset(out, 0, sizeof(*out));
+    using clock = std::chrono::steady_clock;
+
+    // launch + synchronise round trip (compiler/scheduler.py:741-754)
+    hipLaunchKernelGGL(lcdhip_empty_kernel, dim3(1), dim3(1), 0, stream);
+    LCDHIP_CHECK(hipStreamSynchronize(stream));
+    std::vector<double> samples;
+    for (int repeat = 0; repeat < 64; ++repeat) {
+        auto start = clock::now();
+        hipLaunchKernelGGL(lcdhip_empty_kernel, dim3(1), dim3(1), 0, stream);
+        LCDHIP_CHECK(hipStreamSynchronize(stream));
+        samples.push_back(
+            std::chrono::duration<double>(clock::now() - start).count());
+    }
+    out->launch_latency_s = median(samples);
+
+    hipEvent_t start_event, stop_event;
+    LCDHIP_CHECK(hipEventCreate(&start_event));
+    LCDHIP_CHECK(hipEventCreate(&stop_event));
+    float ms = 0.f;
+
+    // release cost per node (compiler/scheduler.py:757-775)
+    const int32_t nodes = 1 << 16;
+    int32_t *d_counters = nullptr;
+    LCDHIP_CHECK(hipMalloc(&d_counters, nodes * 4));
+    LCDHIP_CHECK(hipMemsetAsync(d_counters, 0, nodes * 4, stream));
+    hipLaunchKernelGGL(lcdhip_release_probe_kernel, dim3(nodes), dim3(64), 0,
+                       stream, d_counters, nodes, 7919);
+    samples.clear();
+    for (int repeat = 0; repeat < 5; ++repeat) {
+        LCDHIP_CHECK(hipEventRecord(start_event, stream));
+        hipLaunchKernelGGL(lcdhip_release_probe_kernel, dim3(nodes), dim3(64),
+                           0, stream, d_counters, nodes, 7919);
+        LCDHIP_CHECK(hipEventRecord(stop_event, stream));
+        LCDHIP_CHECK(hipEventSynchronize(stop_event));
+        LCDHIP_CHECK(hipEventElapsedTime(&ms, start_event, stop_event));
+        samples.push_back(ms * 1.0e-3 / nodes);
+    }
+    out->atomic_cost_s = median(samples);
+    LCDHIP_CHECK(hipFree(d_counters));
+
+    // streaming copy bandwidth (read + write bytes)
+    const size_t copy_bytes = size_t(1) << 30;
+    float4 *d_src = nullptr, *d_dst = nullptr;
+    LCDHIP_CHECK(hipMalloc(&d_src, copy_bytes));
+    LCDHIP_CHECK(hipMalloc(&d_dst, copy_bytes));
+    LCDHIP_CHECK(hipMemsetAsync(d_src, 1, copy_bytes, stream));
+    samples.clear();
+    for (int repeat = 0; repeat < 6; ++repeat) {
+        LCDHIP_CHECK(hipEventRecord(start_event, stream));
+        hipLaunchKernelGGL(lcdhip_copy_probe_kernel, dim3(8192), dim3(256), 0,
+                           stream, d_src, d_dst, copy_bytes / 16);
+        LCDHIP_CHECK(hipEventRecord(stop_event, stream));
+        LCDHIP_CHECK(hipEventSynchronize(stop_event));
+        LCDHIP_CHECK(hipEventElapsedTime(&ms, start_event, stop_event));
+        if (repeat)
+            samples.push_back(2.0 * copy_bytes / (ms * 1.0e-3));
+    }
+    out->memory_bandwidth_bytes_per_s = median(samples);
+    LCDHIP_CHECK(hipFree(d_src));
+    LCDHIP_CHECK(hipFree(d_dst));
+
+    out->lane_flops_per_s = ctx.props.clockRate * 1.0e3;
+
+    // cross-workgroup hand-off
+    int32_t *d_flags = nullptr;
+    const int32_t rounds = 256;
+    LCDHIP_CHECK(hipMalloc(&d_flags, (rounds + 8) * 4));
+    int32_t *d_timed_out = d_flags + rounds + 4;
+    const int32_t hops = 2000;
+    samples.clear();
+    for (int repeat = 0; repeat < 4; ++repeat) {
+        LCDHIP_CHECK(hipMemsetAsync(d_flags, 0, (rounds + 8) * 4, stream));
+        LCDHIP_CHECK(hipEventRecord(start_event, stream));
+        hipLaunchKernelGGL(lcdhip_handoff_probe_kernel, dim3(2), dim3(64), 0,
+                           stream, d_flags, hops, d_timed_out);
+        LCDHIP_CHECK(hipEventRecord(stop_event, stream));
+        LCDHIP_CHECK(hipEventSynchronize(stop_event));
+        LCDHIP_CHECK(hipEventElapsedTime(&ms, start_event, stop_event));
+        if (repeat)
+            samples.push_back(ms * 1.0e-3 / hops);
+    }
+    out->handoff_s = median(samples);
+
+    // grid barrier over one workgroup per CU
+    samples.clear();
+    const int barrier_blocks = ctx.props.multiProcessorCount;
+    for (int repeat = 0; repeat < 4; ++repeat) {
+        LCDHIP_CHECK(hipMemsetAsync(d_flags, 0, (rounds + 8) * 4, stream));
+        LCDHIP_CHECK(hipEventRecord(start_event, stream));
+        hipLaunchKernelGGL(lcdhip_barrier_probe_kernel, dim3(barrier_blocks),
+                           dim3(256), 0, stream, d_flags, rounds, d_timed_out);
+        LCDHIP_CHECK(hipEventRecord(stop_event, stream));
+        LCDHIP_CHECK(hipEventSynchronize(stop_event));
+        LCDHIP_CHECK(hipEventElapsedTime(&ms, start_event, stop_event));
+        if (repeat)
+            samples.push_back(ms * 1.0e-3 / rounds);
+    }
+    out->barrier_s = median(samples);
+    int32_t timed_out = 0;
+    LCDHIP_CHECK(hipMemcpy(&timed_out, d_timed_out, 4, hipMemcpyDeviceToHost));
+    LCDHIP_CHECK(hipFree(d_flags));
+    if (timed_out) {
+        set_error("a machine-constant probe gave up waiting");
+        return LCDHIP_ERR_WATCHDOG;
+    }
+
+    // per-node cost of a captured chain of dependent launches
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    const int chain = 256;
+    LCDHIP_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeRelaxed));
+    for (int node = 0; node < chain; ++node)
+        hipLaunchKernelGGL(lcdhip_empty_kernel, dim3(1), dim3(64), 0, stream);
+    LCDHIP_CHECK(hipStreamEndCapture(stream, &graph));
+    LCDHIP_CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+    samples.clear();
+    for (int repeat = 0; repeat < 5; ++repeat) {
+        LCDHIP_CHECK(hipEventRecord(start_event, stream));
+        LCDHIP_CHECK(hipGraphLaunch(exec, stream));
+        LCDHIP_CHECK(hipEventRecord(stop_event, stream));
+        LCDHIP_CHECK(hipEventSynchronize(stop_event));
+        LCDHIP_CHECK(hipEventElapsedTime(&ms, start_event, stop_event));
+        if (repeat)
+            samples.push_back(ms * 1.0e-3 / chain);
+    }
+    out->graph_node_s = median(samples);
+    (void)hipGraphExecDestroy(exec);
+    (void)hipGraphDestroy(graph);
+    (void)hipEventDestroy(start_event);
+    (void)hipEventDestroy(stop_event);
+    return LCDHIP_OK;
+}

@@ -1,0 +1,467 @@
+"""The ``parallel`` decorator: LCD's `@parallel` on an MI355X backend.
+
+Same contract as compiler/decorator.py:138-528 of the reference: identical
+keyword arguments (``loop``/``block_map``/``block_loop``, ``function_props``,
+``execution_mode``, ``threads_per_block``, ``thread_loop``/``thread_map``,
+``thread_unroll``/``thread_unroll_factor``, ``n_warp``,
+``dependence_protocol``, ``scheduler``, ``arch_constants``,
+``sync_free_ready_count``, ``validate_dag_endpoints``, ``band_width``), the
+wrapper is called with ordinary host values and returns what the original
+``return`` returns, and the same introspection attributes are published
+(``cuda_*`` names are kept as aliases of the ``hip_*`` ones).
+
+What happens underneath is different: dependences come from
+``lcd_amd.dependence`` (or explicit ``edge_rules=``), the inspector runs on
+the GPU, plans keep the structure arrays and the DAG resident in HBM, kernels
+are HIP C++ compiled with hiprtc, and repeated calls replay a hipGraph.
+Extra keyword arguments: ``task_lanes`` (lanes per task, power of two <= 64),
+``edge_rules`` (explicit :class:`SegmentRule` list), ``device`` (device
+layer), ``verbose`` (print generated sources like the reference does).
+"""
+
+import ast
+import functools
+import inspect
+import textwrap
+
+import numpy as np
+
+from lcd_amd import hip_runtime
+from lcd_amd.dag_codegen import (
+    COUNTER_DEPENDENCE,
+    PUSH_DEPENDENCE,
+    build_device_dag,
+    compile_dag_builder,
+    create_dag_plan,
+    direct_dependence,
+    generate_dag_source,
+)
+from lcd_amd.dag_preprocessing import (
+    attach_auxiliary_values,
+    execution_data_from_device_dag,
+)
+from lcd_amd.dependence import DependenceAnalysis, analyze_dependences
+from lcd_amd.hip_lowering import lower_to_hip
+from lcd_amd.hip_runtime import (
+    compile_hip_module,
+    evaluate_host_prelude,
+    execute_hip_call,
+    launch_hip_call,
+    prepare_hip_arguments,
+)
+from lcd_amd.scheduler import (
+    AUTO,
+    SYNC_FREE,
+    AnalyticScheduler,
+    SchedulePlan,
+    ScheduleSpace,
+    count_inner_loop_flops,
+    extract_workload_features,
+    inspection_fingerprint,
+    pointer_array_names,
+    segment_trip_counts,
+    compile_thread_trip_counter,
+    measure_thread_trip_counts,
+)
+from lcd_amd.structural_lookups import (
+    create_structural_lookup_plan,
+    materialize_structural_lookups,
+    structural_argument_names,
+)
+
+SCHEDULE_CACHE_SIZE = 8
+VARIANT_ATTRIBUTES = (
+    "hip_lowering", "compiled_hip_module", "hip_kernel", "hip_launcher",
+    "hip_source", "hip_kernel_source", "hip_launcher_ast",
+    "hip_launcher_source",
+    # names the reference publishes
+    "cuda_lowering", "compiled_cuda_module", "cuda_kernel", "cuda_launcher",
+    "cuda_module_ast", "cuda_kernel_ast", "cuda_source", "cuda_kernel_source",
+    "cuda_launcher_ast", "cuda_launcher_source",
+)
+
+
+def _variant_attributes(lowering, compiled):
+    return {
+        "hip_lowering": lowering,
+        "compiled_hip_module": compiled,
+        "hip_kernel": lowering.kernel_name,
+        "hip_launcher": compiled.launcher,
+        "hip_source": lowering.source,
+        "hip_kernel_source": lowering.kernel_source,
+        "hip_launcher_ast": lowering.launcher_ast,
+        "hip_launcher_source": lowering.launcher_source,
+        "cuda_lowering": lowering,
+        "compiled_cuda_module": compiled,
+        "cuda_kernel": lowering.kernel_name,
+        "cuda_launcher": compiled.launcher,
+        "cuda_module_ast": None,
+        "cuda_kernel_ast": None,
+        "cuda_source": lowering.source,
+        "cuda_kernel_source": lowering.kernel_source,
+        "cuda_launcher_ast": lowering.launcher_ast,
+        "cuda_launcher_source": lowering.launcher_source,
+    }
+
+
+def _function_source(function):
+    source = textwrap.dedent(inspect.getsource(function))
+    return "\n".join(line for line in source.splitlines()
+                     if not line.startswith("@"))
+
+
+def parallel(**kwargs):
+    def decorator(function):
+        loop = kwargs.get("loop", kwargs.get("block_map",
+                                             kwargs.get("block_loop")))
+        if loop is None:
+            raise ValueError(
+                "parallel requires a block-mapped iterator via `loop`, "
+                "`block_map`, or `block_loop`.")
+        function_props = kwargs.get("function_props", {})
+        verbose = kwargs.get("verbose", False)
+        source = _function_source(function)
+        if verbose:
+            print(source)
+        function_ast = ast.parse(source)
+        structural_lookups = create_structural_lookup_plan(
+            function_ast, function_props)
+        if kwargs.get("edge_rules") is not None:
+            dependence_analysis = DependenceAnalysis(
+                ordering_dependences=list(kwargs["edge_rules"]))
+        else:
+            dependence_analysis = analyze_dependences(
+                function_ast, loop, function_props)
+        if verbose:
+            for rule in dependence_analysis.ordering_dependences:
+                print(rule.describe())
+            print("Reduction dependences:")
+            for text in dependence_analysis.reduction_dependences:
+                print(text)
+
+        signature = inspect.signature(function)
+        argument_names = list(signature.parameters)
+        execution_mode = kwargs.get("execution_mode", AUTO)
+        thread_loop = kwargs.get("thread_loop", kwargs.get("thread_map"))
+        thread_unroll = kwargs.get("thread_unroll",
+                                   kwargs.get("thread_unroll_factor"))
+        space_options = dict(
+            execution_mode=execution_mode,
+            threads_per_block=kwargs.get("threads_per_block"),
+            thread_unroll=thread_unroll,
+            thread_mapped=thread_loop is not None,
+            n_warp=kwargs.get("n_warp"),
+            task_lanes=kwargs.get("task_lanes"),
+        )
+        band_width = kwargs.get("band_width", 1)
+        scheduler = kwargs.get("scheduler") or AnalyticScheduler(
+            kwargs.get("arch_constants"))
+        device_layer = kwargs.get("device")
+        lowered_variants = {}
+        compiled_variants = {}
+        dependence = None
+
+        def get_device():
+            return device_layer or hip_runtime.default_device()
+
+        def lower_variant(lowering_key):
+            if lowering_key not in lowered_variants:
+                (mode, threads_per_block, unroll, n_warp, protocol,
+                 task_lanes) = lowering_key
+                lowered_variants[lowering_key] = lower_to_hip(
+                    function_ast,
+                    loop_iterator=loop,
+                    reductions=dependence_analysis,
+                    execution_mode=mode,
+                    sync_free_ready_count=kwargs.get(
+                        "sync_free_ready_count", 0),
+                    wavefront_threads_per_block=threads_per_block,
+                    thread_loop_iterator=thread_loop,
+                    thread_unroll_factor=unroll,
+                    n_warp=n_warp if thread_loop is not None else None,
+                    dependence_protocol=protocol,
+                    direct_dependence=(
+                        None if protocol == COUNTER_DEPENDENCE else dependence),
+                    function_props=function_props,
+                    structural_lookups=structural_lookups,
+                    task_lanes=task_lanes or None,
+                    chain_tasks=band_width != 1,
+                )
+            return lowered_variants[lowering_key]
+
+        def compile_variant(lowering_key):
+            lowering = lower_variant(lowering_key)
+            if lowering_key not in compiled_variants:
+                compiled_variants[lowering_key] = compile_hip_module(
+                    lowering, function_globals=function.__globals__)
+            return lowering, compiled_variants[lowering_key]
+
+        host_lowering = lower_variant(
+            ScheduleSpace.from_options(**space_options).configurations()[0])
+        dag_argument_names = argument_names + [
+            name for name in host_lowering.lifted_loop_parameters
+            if name not in argument_names]
+        block_loop = host_lowering  # (lowering already validated the loop)
+        loop_node = next(
+            node for node in ast.walk(function_ast)
+            if isinstance(node, ast.For) and isinstance(node.target, ast.Name)
+            and node.target.id == loop)
+        range_arguments = loop_node.iter.args
+        node_lower = (ast.unparse(range_arguments[0])
+                      if len(range_arguments) > 1 else "0")
+        node_count = ast.unparse(
+            range_arguments[1] if len(range_arguments) > 1
+            else range_arguments[0])
+        dag_plan = create_dag_plan(
+            dependence_analysis.ordering_dependences, None,
+            parallel_iterator=loop, arguments=dag_argument_names,
+            function_props=function_props, node_count=node_count,
+            node_lower=node_lower)
+        validate_endpoints = kwargs.get("validate_dag_endpoints", False)
+        dependence = direct_dependence(dag_plan, thread_loop,
+                                       validate_endpoints=validate_endpoints)
+        schedule_space = ScheduleSpace.from_options(
+            **space_options,
+            direct_protocol=None if dependence is None else dependence.kind,
+            dependence_protocol=kwargs.get("dependence_protocol"))
+        lowered_variants.clear()   # protocols are known only now
+        fixed_schedule = (schedule_space.fixed_schedule()
+                          if schedule_space.is_fixed else None)
+        edge_multiplicity = any(
+            configuration[4] == PUSH_DEPENDENCE
+            for configuration in schedule_space.configurations())
+        inspector_mode = (execution_mode if fixed_schedule is not None
+                          else SYNC_FREE)
+        inspector_options = dict(
+            validate_endpoints=validate_endpoints,
+            execution_mode=inspector_mode,
+            edge_multiplicity=edge_multiplicity)
+        dag_source = generate_dag_source(dag_plan, **inspector_options)
+        if verbose:
+            print(dag_source)
+        dag_builder = compile_dag_builder(
+            dag_plan, device=device_layer, **inspector_options)
+        rule_arrays = []
+        for rule in dag_plan.edge_rules:
+            for name in (rule.pointer_array, rule.index_array):
+                if name not in rule_arrays:
+                    rule_arrays.append(name)
+        fingerprint_names = rule_arrays + [
+            name for name in pointer_array_names(function_props)
+            + structural_argument_names(structural_lookups)
+            if name not in rule_arrays]
+        flops_per_iteration = count_inner_loop_flops(
+            function_ast, loop, thread_loop)
+        thread_loop_node = None
+        if thread_loop is not None:
+            thread_loop_node = next(
+                (node for node in ast.walk(loop_node)
+                 if isinstance(node, ast.For)
+                 and isinstance(node.target, ast.Name)
+                 and node.target.id == thread_loop), None)
+        trip_counter = {"probe": None}
+        schedule_plans = {}
+
+        def bind_arguments(args, call_kwargs):
+            bound = signature.bind(*args, **call_kwargs)
+            bound.apply_defaults()
+            return bound.arguments
+
+        def dag_values_for(argument_values):
+            values = dict(argument_values)
+            values.update(evaluate_host_prelude(
+                host_lowering, values, function.__globals__,
+                skip=tuple(host_lowering.zero_initialised)))
+            return values
+
+        def run_inspector(dag_values):
+            return dag_builder(*[dag_values[name]
+                                 for name in dag_argument_names])
+
+        def build_dag(*args, **call_kwargs):
+            return run_inspector(
+                dag_values_for(bind_arguments(args, call_kwargs)))[:2]
+
+        def trip_counts(dag_values):
+            if thread_loop is None:
+                return None
+            fast = segment_trip_counts(thread_loop_node, loop, dag_values)
+            if fast is not None:
+                return fast
+            if trip_counter["probe"] is None:
+                trip_counter["probe"] = compile_thread_trip_counter(
+                    function_ast, thread_loop, function.__globals__)
+            host_values = {
+                name: (value.copy_to_host()
+                       if hasattr(value, "copy_to_host") else value)
+                for name, value in dag_values.items()}
+            return measure_thread_trip_counts(
+                trip_counter["probe"], host_values, argument_names)
+
+        def create_schedule_plan(dag_values):
+            device = get_device()
+            # structure arrays go to HBM once per plan and stay there
+            resident = {}
+            for name in fingerprint_names:
+                value = dag_values.get(name)
+                if isinstance(value, (list, tuple)):
+                    value = np.asarray(value)
+                if isinstance(value, np.ndarray):
+                    resident[name] = device.to_device(
+                        np.ascontiguousarray(value, dtype=np.int32)
+                        if np.issubdtype(value.dtype, np.integer) else value)
+            device_values = dict(dag_values)
+            device_values.update(resident)
+            lookup_values = materialize_structural_lookups(
+                structural_lookups, device_values, device)
+            dag = build_device_dag(dag_plan, device_values, device,
+                                   levels=True)
+            if fixed_schedule is not None:
+                schedule = fixed_schedule
+                features = None
+            else:
+                features = extract_workload_features(
+                    dag.n, dag.levels, dag_values,
+                    function_props=function_props,
+                    flops_per_iteration=flops_per_iteration,
+                    thread_trip_counts=trip_counts(dag_values),
+                    edges=dag.edges)
+                schedule = scheduler.schedule(features, schedule_space)
+            lowering = lower_variant(schedule.lowering_key)
+            execution_data = execution_data_from_device_dag(
+                dag, schedule.execution_mode, lowering.warp_mapped,
+                pushed=lowering.dependence_protocol == PUSH_DEPENDENCE,
+                band_width=band_width)
+            plan = SchedulePlan(
+                schedule=schedule,
+                execution_data=attach_auxiliary_values(
+                    execution_data, lookup_values),
+                features=features, dag=dag)
+            plan_state[id(plan)] = {"resident": resident, "workspace": {}}
+            return plan
+
+        plan_state = {}
+
+        def plan_for(argument_values):
+            dag_values = dag_values_for(argument_values)
+            fingerprint = inspection_fingerprint(
+                dag_values, fingerprint_names,
+                device_layer if device_layer is not None else None)
+            plan = schedule_plans.get(fingerprint)
+            if plan is None:
+                plan = create_schedule_plan(dag_values)
+                if len(schedule_plans) >= SCHEDULE_CACHE_SIZE:
+                    evicted = schedule_plans.pop(next(iter(schedule_plans)))
+                    plan_state.pop(id(evicted), None)
+                schedule_plans[fingerprint] = plan
+            return plan
+
+        def schedule_plan(*args, **call_kwargs):
+            return plan_for(bind_arguments(args, call_kwargs))
+
+        def schedule_call(*args, **call_kwargs):
+            return schedule_plan(*args, **call_kwargs).schedule
+
+        def build_execution_data(*args, **call_kwargs):
+            return schedule_plan(*args, **call_kwargs).execution_data
+
+        def publish_variant(schedule, lowering, compiled):
+            if wrapper.current_schedule == schedule:
+                return
+            wrapper.current_schedule = schedule
+            wrapper.__dict__.update(_variant_attributes(lowering, compiled))
+
+        def resolve_call(args, call_kwargs):
+            argument_values = bind_arguments(args, call_kwargs)
+            plan = plan_for(argument_values)
+            lowering, compiled = compile_variant(plan.schedule.lowering_key)
+            publish_variant(plan.schedule, lowering, compiled)
+            state = plan_state[id(plan)]
+            values = dict(argument_values)
+            values.update(state["resident"])
+            prepared = prepare_hip_arguments(
+                lowering=lowering, argument_values=values,
+                execution_data=plan.execution_data,
+                function_globals=function.__globals__,
+                hip_module=get_device(), compiled_module=compiled,
+                workspace=state["workspace"])
+            return lowering, compiled, prepared
+
+        def prepare_hip_call(*args, **call_kwargs):
+            return resolve_call(args, call_kwargs)[2]
+
+        def bind(*args, **call_kwargs):
+            """Resolve one call without running it: returns an object with
+            ``launch()`` (enqueue, no sync), ``synchronize()``, ``result()``
+            (download what the function returns) for callers that keep their
+            data in HBM between solves."""
+            lowering, compiled, prepared = resolve_call(args, call_kwargs)
+            return BoundCall(lowering, compiled, prepared,
+                             function.__globals__)
+
+        @functools.wraps(function)
+        def wrapper(*args, **call_kwargs):
+            lowering, compiled, prepared = resolve_call(args, call_kwargs)
+            return execute_hip_call(
+                compiled_module=compiled, lowering=lowering,
+                prepared_arguments=prepared,
+                function_globals=function.__globals__)
+
+        wrapper.original_function = function
+        wrapper.build_dag = build_dag
+        wrapper.build_execution_data = build_execution_data
+        wrapper.prepare_hip_arguments = prepare_hip_call
+        wrapper.prepare_cuda_arguments = prepare_hip_call
+        wrapper.bind = bind
+        wrapper.schedule_plan = schedule_plan
+        wrapper.schedule_call = schedule_call
+        wrapper.schedule_space = schedule_space
+        wrapper.scheduler = scheduler
+        wrapper.dag_plan = dag_plan
+        wrapper.dag_source = dag_source
+        wrapper.execution_mode = execution_mode
+        wrapper.dependence_analysis = dependence_analysis
+        wrapper.structural_lookups = structural_lookups
+        wrapper.reduction_statements = dependence_analysis.atomic_statements
+        wrapper.current_schedule = None
+        wrapper.lower_variant = lower_variant
+        wrapper.__dict__.update(dict.fromkeys(VARIANT_ATTRIBUTES))
+        if fixed_schedule is not None:
+            publish_variant(fixed_schedule,
+                            *compile_variant(fixed_schedule.lowering_key))
+        return wrapper
+    return decorator
+
+
+class BoundCall:
+    """One resolved call whose operands stay on the device."""
+
+    def __init__(self, lowering, compiled, prepared, function_globals):
+        self.lowering = lowering
+        self.compiled = compiled
+        self.prepared = prepared
+        self.function_globals = function_globals
+
+    @property
+    def device(self):
+        return self.prepared.device
+
+    def launch(self, use_graph=True):
+        launch_hip_call(self.compiled, self.lowering, self.prepared, use_graph)
+
+    def synchronize(self):
+        self.prepared.device.synchronize()
+        hip_runtime.check_executor_status(self.lowering, self.prepared)
+
+    def device_value(self, name):
+        return self.prepared.values[name]
+
+    def result(self):
+        self.synchronize()
+        values = dict(self.prepared.host_values)
+        for name in hip_runtime._returned_names(self.lowering.host_epilogue):
+            if name in self.prepared.values:
+                values[name] = self.prepared.copy_to_host(name)
+        values.update(self.prepared.copy_lifted_variables_to_host())
+        return hip_runtime._evaluate_host_epilogue(
+            self.lowering, values, self.function_globals)

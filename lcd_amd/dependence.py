@@ -1,0 +1,469 @@
+"""Structural loop-carried dependence analysis for `@parallel` loops.
+
+The reference derives ordering and reduction dependences with an SPF/Z3
+pipeline (compiler/legality_check.py:406-470, compiler/dag_codegen.py:89-790)
+and then projects them onto *edge rules* that the inspector enumerates.  Z3 is
+not a dependency of this backend.  This module recognises, directly on the
+Python AST, the access shapes that the reference's planner reduces the
+supported solver loops to, and produces the same edge rules:
+
+* a task writes its own element ``X[i]`` and other tasks read ``X[I[p]]`` for
+  ``p`` in their own pointer segment           -> pull rule (source ``I[p]``,
+  destination ``i``; SpTRSV-CSR, Gauss-Seidel; test_dag_codegen.py:58-70,
+  test_gauss_seidel_codegen.py:143-148)
+* a task updates ``X[I[p]] op= ...`` for ``p`` in its own segment and the owner
+  reads ``X[i]``                               -> push rule (source ``i``,
+  destination ``I[p]``; SpTRSV-CSC; test_dag_codegen.py:72-83) plus an atomic
+  reduction on the update
+* a task writes positions of its own segment ``D[p]`` and reads positions of
+  the segment of ``I[q]``                      -> pull rule over ``q`` with
+  the loop's ``break`` (ILU0-CSR; test_spilu0_codegen.py:129-144)
+
+Anything else raises :class:`DependenceAnalysisError` rather than guessing;
+callers can pass ``edge_rules=`` to the decorator explicitly in that case.
+"""
+
+import ast
+from copy import deepcopy
+from dataclasses import dataclass, field
+
+GUARD_NONE, GUARD_GREATER, GUARD_NOT_EQUAL = 0, 1, 2
+ASSOCIATIVE_UPDATE_OPERATIONS = {
+    ast.Add: "+", ast.Sub: "-", ast.Mult: "*", ast.BitAnd: "&",
+    ast.BitOr: "|", ast.BitXor: "^",
+}
+
+
+class DependenceAnalysisError(Exception):
+    """The loop's cross-iteration dependences are outside the supported set."""
+
+
+@dataclass(frozen=True)
+class SegmentRule:
+    """One inspector edge rule over a pointer-delimited segment.
+
+    ``for seg in range(node_count): for p in range(ptr[seg] + lower_offset,
+    ptr[seg + 1] + upper_offset): [if idx[p] >= seg: break]`` yields the edge
+    ``seg -> idx[p]`` (``owner_is_source``) or ``idx[p] -> seg``.
+    """
+
+    pointer_array: str
+    index_array: str
+    owner_is_source: bool
+    lower_offset: int = 0
+    upper_offset: int = 0
+    guard: int = GUARD_GREATER
+    break_at_owner: bool = False
+    block_iterator: str = "i"
+    inner_iterator: str = "j"
+    carried_by: str = ""
+
+    @property
+    def iterators(self):
+        return [self.block_iterator, self.inner_iterator]
+
+    def endpoint_source(self):
+        return f"{self.index_array}[{self.inner_iterator}]"
+
+    def describe(self):
+        source, destination = (
+            (self.block_iterator, self.endpoint_source())
+            if self.owner_is_source
+            else (self.endpoint_source(), self.block_iterator)
+        )
+        return (f"RAW on {self.carried_by}: {source} -> {destination} "
+                f"over {self.inner_iterator} in segment of "
+                f"{self.pointer_array}[{self.block_iterator}]")
+
+
+@dataclass(frozen=True)
+class ReductionSite:
+    statement_id: str
+    operator: str
+    location: tuple
+    array: str
+
+
+@dataclass
+class DependenceAnalysis:
+    ordering_dependences: list = field(default_factory=list)
+    reduction_dependences: list = field(default_factory=list)
+    reductions: dict = field(default_factory=dict)
+
+    @property
+    def atomic_statements(self):
+        return list(self.reductions.values())
+
+
+@dataclass(frozen=True)
+class _Segment:
+    """Positions ``[ptr[owner] + lower, ptr[owner + 1] + upper)``."""
+
+    pointer_array: str
+    owner: ast.expr
+    lower_offset: int
+    upper_offset: int
+    lower_is_position: bool = False
+
+
+def _const_int(node):
+    if isinstance(node, ast.Constant) and isinstance(node.value, int) and not (
+            isinstance(node.value, bool)):
+        return node.value
+    if (isinstance(node, ast.UnaryOp) and isinstance(node.op, ast.USub)
+            and isinstance(node.operand, ast.Constant)
+            and isinstance(node.operand.value, int)):
+        return -node.operand.value
+    return None
+
+
+def _split_offset(node):
+    """``expr + c`` / ``expr - c`` -> (expr, c)."""
+    if isinstance(node, ast.BinOp) and isinstance(node.op, (ast.Add, ast.Sub)):
+        right = _const_int(node.right)
+        if right is not None:
+            base, offset = _split_offset(node.left)
+            return base, offset + (right if isinstance(node.op, ast.Add)
+                                   else -right)
+        left = _const_int(node.left)
+        if left is not None and isinstance(node.op, ast.Add):
+            base, offset = _split_offset(node.right)
+            return base, offset + left
+    return node, 0
+
+
+def _same(a, b):
+    return ast.dump(a) == ast.dump(b)
+
+
+class _AliasTable:
+    """Names assigned exactly once to a pure expression inside the function."""
+
+    def __init__(self, function):
+        counts = {}
+        values = {}
+        for node in ast.walk(function):
+            targets = []
+            if isinstance(node, ast.Assign):
+                targets = node.targets
+            elif isinstance(node, (ast.AugAssign, ast.AnnAssign)):
+                targets = [node.target]
+            elif isinstance(node, ast.For):
+                targets = [node.target]
+            for target in targets:
+                for name in ast.walk(target):
+                    if isinstance(name, ast.Name) and isinstance(
+                            name.ctx, ast.Store):
+                        counts[name.id] = counts.get(name.id, 0) + 1
+                        if isinstance(node, ast.Assign) and len(
+                                node.targets) == 1 and isinstance(
+                                    node.targets[0], ast.Name):
+                            values[name.id] = node.value
+        self.values = {
+            name: value for name, value in values.items()
+            if counts.get(name) == 1 and not any(
+                isinstance(n, ast.Call) for n in ast.walk(value))
+        }
+
+    def resolve(self, node, depth=0):
+        """Substitute aliases everywhere inside ``node`` (a copy is returned)."""
+        if depth > 16:
+            return node
+        table = self
+
+        class Substitute(ast.NodeTransformer):
+            def visit_Name(self, name):
+                if isinstance(name.ctx, ast.Load) and name.id in table.values:
+                    return table.resolve(table.values[name.id], depth + 1)
+                return name
+
+        return Substitute().visit(deepcopy(node))
+
+
+def pointer_arrays(function_props):
+    return [
+        name for name, properties in (function_props or {}).items()
+        if isinstance(name, str) and "monotonically_increasing" in properties
+    ]
+
+
+def find_block_loop(function, block_iterator):
+    matches = [
+        node for node in ast.walk(function)
+        if isinstance(node, ast.For) and isinstance(node.target, ast.Name)
+        and node.target.id == block_iterator
+    ]
+    if len(matches) != 1:
+        raise DependenceAnalysisError(
+            f"Expected exactly one loop over {block_iterator!r}; "
+            f"found {len(matches)}.")
+    return matches[0]
+
+
+class _Analyzer:
+    def __init__(self, function, block_iterator, function_props):
+        self.function = function
+        self.block = block_iterator
+        self.aliases = _AliasTable(function)
+        self.pointers = set(pointer_arrays(function_props))
+        self.segments = {}     # iterator -> _Segment
+        self.breaks = {}       # iterator -> list of resolved break tests
+        self.writes = []       # (array, classification, node, is_update)
+        self.reads = []        # (array, classification)
+        self.reductions = {}
+        self.statement_counter = 0
+
+    # ---- loop ranges ----------------------------------------------------
+    def _segment_of_range(self, loop):
+        call = loop.iter
+        if not (isinstance(call, ast.Call) and isinstance(call.func, ast.Name)
+                and call.func.id == "range" and len(call.args) == 2):
+            return None
+        lower = self.aliases.resolve(call.args[0])
+        upper = self.aliases.resolve(call.args[1])
+        lower_base, lower_offset = _split_offset(lower)
+        upper_base, upper_offset = _split_offset(upper)
+        if not (isinstance(upper_base, ast.Subscript)
+                and isinstance(upper_base.value, ast.Name)
+                and upper_base.value.id in self.pointers):
+            return None
+        pointer = upper_base.value.id
+        owner_plus, one = _split_offset(upper_base.slice)
+        if one != 1:
+            return None
+        if (isinstance(lower_base, ast.Subscript)
+                and isinstance(lower_base.value, ast.Name)
+                and lower_base.value.id == pointer
+                and _same(lower_base.slice, owner_plus)):
+            return _Segment(pointer, owner_plus, lower_offset, upper_offset)
+        # lower bound is a position of the same segment plus a constant
+        if isinstance(lower_base, ast.Name) and lower_base.id in self.segments:
+            outer = self.segments[lower_base.id]
+            if (outer.pointer_array == pointer
+                    and _same(outer.owner, owner_plus) and lower_offset >= 0):
+                return _Segment(pointer, owner_plus, outer.lower_offset,
+                                upper_offset, lower_is_position=True)
+        return None
+
+    # ---- access classification -------------------------------------------
+    def _owner_kind(self, owner):
+        owner = self.aliases.resolve(owner)
+        if isinstance(owner, ast.Name) and owner.id == self.block:
+            return ("self",)
+        if (isinstance(owner, ast.Subscript) and isinstance(owner.value, ast.Name)
+                and isinstance(owner.slice, ast.Name)
+                and owner.slice.id in self.segments):
+            inner = self.segments[owner.slice.id]
+            if self._owner_kind(inner.owner) == ("self",):
+                return ("indirect", owner.value.id, owner.slice.id)
+        return ("unknown", ast.unparse(owner))
+
+    def _classify(self, index):
+        index = self.aliases.resolve(index)
+        if isinstance(index, ast.Name) and index.id == self.block:
+            return ("self",)
+        if isinstance(index, ast.Name) and index.id in self.segments:
+            kind = self._owner_kind(self.segments[index.id].owner)
+            if kind == ("self",):
+                return ("own_position", index.id)
+            if kind[0] == "indirect":
+                return ("other_position", kind[1], kind[2], index.id)
+            return ("unknown", ast.unparse(index))
+        if isinstance(index, ast.Subscript) and isinstance(index.value, ast.Name):
+            base, offset = _split_offset(index.slice)
+            if (isinstance(base, ast.Name) and base.id in self.segments
+                    and offset == 0
+                    and self._owner_kind(self.segments[base.id].owner)
+                    == ("self",)):
+                return ("indirect", index.value.id, base.id)
+        return ("unknown", ast.unparse(index))
+
+    # ---- traversal ---------------------------------------------------------
+    def _record_reads(self, node, written_arrays):
+        for sub in ast.walk(node):
+            if (isinstance(sub, ast.Subscript) and isinstance(sub.ctx, ast.Load)
+                    and isinstance(sub.value, ast.Name)
+                    and sub.value.id in written_arrays):
+                self.reads.append((sub.value.id, self._classify(sub.slice)))
+
+    def _visit(self, statements, written_arrays, loop_stack):
+        for statement in statements:
+            if isinstance(statement, ast.For):
+                segment = None
+                if isinstance(statement.target, ast.Name):
+                    segment = self._segment_of_range(statement)
+                    if segment is not None:
+                        self.segments[statement.target.id] = segment
+                self._record_reads(statement.iter, written_arrays)
+                self._visit(statement.body, written_arrays,
+                            loop_stack + [statement])
+            elif isinstance(statement, ast.If):
+                self._record_reads(statement.test, written_arrays)
+                if (loop_stack and len(statement.body) == 1
+                        and isinstance(statement.body[0], ast.Break)
+                        and not statement.orelse
+                        and isinstance(loop_stack[-1].target, ast.Name)):
+                    self.breaks.setdefault(
+                        loop_stack[-1].target.id, []
+                    ).append(self.aliases.resolve(statement.test))
+                self._visit(statement.body, written_arrays, loop_stack)
+                self._visit(statement.orelse, written_arrays, loop_stack)
+            elif isinstance(statement, ast.While):
+                self._record_reads(statement.test, written_arrays)
+                self._visit(statement.body, written_arrays, loop_stack)
+            elif isinstance(statement, ast.Assign):
+                self._record_reads(statement.value, written_arrays)
+                for target in statement.targets:
+                    if isinstance(target, ast.Subscript) and isinstance(
+                            target.value, ast.Name):
+                        self._record_reads(target.slice, written_arrays)
+                        self.writes.append((
+                            target.value.id, self._classify(target.slice),
+                            statement, False))
+            elif isinstance(statement, ast.AugAssign):
+                self._record_reads(statement.value, written_arrays)
+                target = statement.target
+                if isinstance(target, ast.Subscript) and isinstance(
+                        target.value, ast.Name):
+                    self._record_reads(target.slice, written_arrays)
+                    self.writes.append((
+                        target.value.id, self._classify(target.slice),
+                        statement, True))
+            elif isinstance(statement, ast.Expr):
+                self._record_reads(statement.value, written_arrays)
+
+    def _break_at_owner(self, iterator, index_array):
+        """True when the loop over ``iterator`` starts with
+        ``if index_array[iterator] >= block: break``."""
+        for test in self.breaks.get(iterator, []):
+            if (isinstance(test, ast.Compare) and len(test.ops) == 1
+                    and isinstance(test.ops[0], ast.GtE)
+                    and isinstance(test.left, ast.Subscript)
+                    and isinstance(test.left.value, ast.Name)
+                    and test.left.value.id == index_array
+                    and isinstance(test.left.slice, ast.Name)
+                    and test.left.slice.id == iterator
+                    and isinstance(test.comparators[0], ast.Name)
+                    and test.comparators[0].id == self.block):
+                return True
+        if self.breaks.get(iterator):
+            raise DependenceAnalysisError(
+                f"Unsupported break condition in the loop over {iterator!r}.")
+        return False
+
+    def _rule(self, owner_is_source, index_array, iterator, array):
+        segment = self.segments[iterator]
+        if segment.lower_is_position:
+            raise DependenceAnalysisError(
+                f"The dependence carried by {array!r} is enumerated by a loop "
+                f"over {iterator!r} whose lower bound is not a segment start.")
+        broken = self._break_at_owner(iterator, index_array)
+        if broken and owner_is_source:
+            raise DependenceAnalysisError(
+                "A break-guarded segment loop cannot release successors.")
+        return SegmentRule(
+            pointer_array=segment.pointer_array,
+            index_array=index_array,
+            owner_is_source=owner_is_source,
+            lower_offset=segment.lower_offset,
+            upper_offset=segment.upper_offset,
+            guard=GUARD_NONE if broken else GUARD_GREATER,
+            break_at_owner=broken,
+            block_iterator=self.block,
+            inner_iterator=iterator,
+            carried_by=array,
+        )
+
+    def run(self):
+        loop = find_block_loop(self.function, self.block)
+        local_names = set()
+        for node in ast.walk(loop):
+            if isinstance(node, ast.Name) and isinstance(node.ctx, ast.Store):
+                local_names.add(node.id)
+        written_arrays = set()
+        for node in ast.walk(loop):
+            target = None
+            if isinstance(node, ast.Assign):
+                for candidate in node.targets:
+                    if isinstance(candidate, ast.Subscript):
+                        target = candidate
+            elif isinstance(node, ast.AugAssign) and isinstance(
+                    node.target, ast.Subscript):
+                target = node.target
+            if target is not None and isinstance(target.value, ast.Name):
+                written_arrays.add(target.value.id)
+        self._visit(loop.body, written_arrays, [loop])
+
+        rules, reductions, reduction_rules = [], {}, []
+        for array, write_kind, statement, is_update in self.writes:
+            if write_kind[0] == "unknown":
+                raise DependenceAnalysisError(
+                    f"Cannot tell which task owns the write "
+                    f"{ast.unparse(statement)!r} (index {write_kind[1]}).")
+            if write_kind[0] == "other_position":
+                raise DependenceAnalysisError(
+                    f"{ast.unparse(statement)!r} writes another task's "
+                    "segment; this pattern is not supported.")
+            if write_kind[0] == "indirect":
+                operator = ASSOCIATIVE_UPDATE_OPERATIONS.get(
+                    type(statement.op)) if is_update else None
+                if operator is None:
+                    raise DependenceAnalysisError(
+                        f"{ast.unparse(statement)!r} scatters a "
+                        "non-associative write to other tasks' elements.")
+                location = (statement.lineno, statement.col_offset)
+                if location not in reductions:
+                    site = ReductionSite(
+                        statement_id=f"S{len(reductions) + 1}",
+                        operator=operator, location=location, array=array)
+                    reductions[location] = site
+                    reduction_rules.append(
+                        f"reduction on {array}[{write_kind[1]}"
+                        f"[{write_kind[2]}]] ({operator}=)")
+            for read_array, read_kind in self.reads:
+                if read_array != array:
+                    continue
+                rule = None
+                if write_kind == ("self",) and read_kind[0] == "indirect":
+                    rule = self._rule(False, read_kind[1], read_kind[2], array)
+                elif write_kind[0] == "indirect" and read_kind == ("self",):
+                    rule = self._rule(True, write_kind[1], write_kind[2], array)
+                elif (write_kind[0] == "own_position"
+                      and read_kind[0] == "other_position"):
+                    rule = self._rule(False, read_kind[1], read_kind[2], array)
+                elif write_kind[0] in ("self", "own_position") and (
+                        read_kind[0] in ("self", "own_position")):
+                    rule = None          # same task
+                elif write_kind[0] == "indirect" and read_kind[0] == "indirect":
+                    rule = None          # the update's own read-modify-write
+                elif read_kind[0] == "unknown":
+                    raise DependenceAnalysisError(
+                        f"Cannot tell which task produced the value read as "
+                        f"{array}[{read_kind[1]}].")
+                else:
+                    raise DependenceAnalysisError(
+                        f"Unsupported dependence on {array!r}: write "
+                        f"{write_kind[0]} / read {read_kind[0]}.")
+                if rule is not None and rule not in rules:
+                    rules.append(rule)
+        return DependenceAnalysis(
+            ordering_dependences=rules,
+            reduction_dependences=reduction_rules,
+            reductions=reductions,
+        )
+
+
+def analyze_dependences(function_ast, block_iterator, function_props=None):
+    """Return the :class:`DependenceAnalysis` of the block loop.
+
+    ``function_ast`` is an ``ast.Module`` holding one function, or the
+    ``ast.FunctionDef`` itself.
+    """
+    function = function_ast
+    if isinstance(function_ast, ast.Module):
+        functions = [n for n in function_ast.body
+                     if isinstance(n, ast.FunctionDef)]
+        if len(functions) != 1:
+            raise DependenceAnalysisError("Expected exactly one function.")
+        function = functions[0]
+    return _Analyzer(function, block_iterator, function_props).run()

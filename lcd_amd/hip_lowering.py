@@ -1,0 +1,1563 @@
+"""Lower one annotated Python loop to HIP C++ for gfx950 (MI355X).
+
+Counterpart of the reference's Numba-CUDA lowering
+(compiler/cuda_lowering.py): the block-mapped loop is removed, its iterator is
+bound from a task list, an optional inner loop is distributed over the lanes
+of a *task group*, cross-task updates become device-scope atomics, and the
+result is wrapped in one of the executors.  Differences that come from
+targeting CDNA4 rather than translating the CUDA code:
+
+* Kernels are HIP C++ text built from hand-written executor templates and
+  compiled at run time with hiprtc; the launcher is a small Python function
+  that drives ``liblcdhip`` (level loops are captured into a hipGraph).
+* A task is mapped to a group of ``task_lanes`` lanes, a power of two up to
+  the 64-lane wavefront.  ``n_warp == 1`` in the reference means "one warp per
+  task"; here it means one wavefront (64 lanes) unless the scheduler picks a
+  narrower group, in which case one wavefront carries ``64 / task_lanes``
+  tasks.  ``n_warp > 1`` makes ``n_warp`` wavefronts (one workgroup) cooperate.
+* Sync-free executors are persistent: wavefronts fetch tasks in topological
+  (level) order from a global counter and *poll* readiness inside a
+  wave-uniform loop, so tasks that share a wavefront cannot deadlock each
+  other and every wait is bounded by a watchdog.
+* Statements outside the distributed loop are executed by every lane of the
+  group (uniform control flow); their stores are issued by lane 0 and
+  followed by a group-scope fence.
+"""
+
+import ast
+from copy import deepcopy
+from dataclasses import dataclass, field
+import textwrap
+
+from lcd_amd.structural_lookups import (
+    match_segment_search,
+    rewrite_structural_lookups,
+    segmented_array_pairs,
+    structural_lookup_names,
+)
+
+
+class HIPLoweringError(Exception):
+    """Base error for unsupported HIP lowering."""
+
+
+class UnsupportedAtomicOperation(HIPLoweringError):
+    """A reduction has no direct device atomic."""
+
+
+COUNTER_DEPENDENCE = "counter"
+PUSH_DEPENDENCE = "push"
+PULL_DEPENDENCE = "pull"
+DEPENDENCE_PROTOCOLS = (COUNTER_DEPENDENCE, PUSH_DEPENDENCE, PULL_DEPENDENCE)
+
+HIP_EXECUTION_MODES = frozenset({"plain", "sync_free", "wavefront"})
+WAVEFRONT_SIZE = 64
+# Executor argument names: the kernel ABI the lowering and the runtime agree
+# on (same names as compiler/cuda_lowering.py:51-64).
+SYNC_FREE_ARGUMENTS = ("dep_count", "initial_dep_count", "dag_ptr", "dag_index",
+                       "task_nodes", "task_ptr", "task_counter", "task_count")
+PUSH_ARGUMENTS = ("dep_count", "initial_dep_count", "task_nodes", "task_ptr",
+                  "task_counter", "task_count")
+PULL_ARGUMENTS = ("done", "task_nodes", "task_ptr", "task_counter",
+                  "task_count")
+WAVEFRONT_ARGUMENTS = ("task_nodes", "task_ptr", "band_start", "band_end")
+STATUS_ARGUMENT = "_lcd_status"
+HOST_LAUNCH_ARGUMENTS = frozenset({"band_ptr", "wavefront_ptr"})
+INTEGER_EXECUTOR_ARRAYS = frozenset({
+    "dep_count", "initial_dep_count", "dag_ptr", "dag_index", "task_nodes",
+    "task_ptr", "task_counter", "done", STATUS_ARGUMENT,
+})
+DEFAULT_SPIN_LIMIT = 1 << 22
+
+_ATOMIC_CALLS = {"+": "lcd_atomic_add", "-": "lcd_atomic_sub",
+                 "&": "lcd_atomic_and", "|": "lcd_atomic_or",
+                 "^": "lcd_atomic_xor"}
+_AUG_TEXT = {ast.Add: "+", ast.Sub: "-", ast.Mult: "*", ast.Div: "/",
+             ast.BitAnd: "&", ast.BitOr: "|", ast.BitXor: "^",
+             ast.FloorDiv: "//", ast.Mod: "%"}
+_BIN_TEXT = {ast.Add: "+", ast.Sub: "-", ast.Mult: "*", ast.BitAnd: "&",
+             ast.BitOr: "|", ast.BitXor: "^", ast.LShift: "<<",
+             ast.RShift: ">>"}
+_CMP_TEXT = {ast.Eq: "==", ast.NotEq: "!=", ast.Lt: "<", ast.LtE: "<=",
+             ast.Gt: ">", ast.GtE: ">="}
+INT, FLOAT = "int", "float"
+
+
+@dataclass
+class HIPLoweringResult:
+    """Everything the runtime needs to compile, bind and launch one variant.
+
+    Field names follow CUDALoweringResult (compiler/cuda_lowering.py:72-98).
+    ``source`` is HIP C++; ``launcher_source`` is the Python launcher.
+    """
+
+    source: str
+    kernel_source: str
+    launcher_source: str
+    launcher_ast: ast.Module
+    kernel_name: str
+    launcher_name: str
+    reset_kernel_name: str | None
+    kernel_arguments: list
+    launcher_arguments: list
+    lifted_variables: list
+    lifted_loop_parameters: list
+    host_prelude: list
+    host_epilogue: list
+    atomic_statement_ids: set
+    execution_mode: str
+    auxiliary_arguments: list
+    thread_loop_iterator: str | None = None
+    thread_unroll_factor: int = 1
+    host_loop_iterators: tuple = ()
+    n_warp: int | None = None
+    warp_mapped: bool = False
+    dependence_protocol: str = COUNTER_DEPENDENCE
+    task_lanes: int = 1
+    threads_per_block: int = 128
+    tasks_per_block: int = 128
+    array_arguments: dict = field(default_factory=dict)   # name -> INT|FLOAT
+    scalar_arguments: dict = field(default_factory=dict)  # name -> INT|FLOAT
+    written_arrays: tuple = ()
+    zero_initialised: dict = field(default_factory=dict)  # lifted -> shape src
+    persistent: bool = False
+    function_name: str = ""
+
+    @property
+    def module_source(self):
+        return self.source
+
+
+# --------------------------------------------------------------------------
+# small AST helpers
+
+def _names_in(node):
+    return {n.id for n in ast.walk(node) if isinstance(n, ast.Name)}
+
+
+def _stored_names(statements):
+    names = []
+    for statement in statements:
+        for node in ast.walk(statement):
+            if (isinstance(node, ast.Name) and isinstance(node.ctx, ast.Store)
+                    and node.id not in names):
+                names.append(node.id)
+    return names
+
+
+def _is_range_loop(node):
+    return (isinstance(node, ast.For) and isinstance(node.target, ast.Name)
+            and isinstance(node.iter, ast.Call)
+            and isinstance(node.iter.func, ast.Name)
+            and node.iter.func.id == "range" and not node.iter.keywords
+            and 1 <= len(node.iter.args) <= 3 and not node.orelse)
+
+
+def _to_module(code):
+    if isinstance(code, ast.Module):
+        return deepcopy(code)
+    if isinstance(code, ast.FunctionDef):
+        return ast.Module(body=[deepcopy(code)], type_ignores=[])
+    if isinstance(code, str):
+        return ast.parse(textwrap.dedent(code))
+    raise HIPLoweringError("HIP lowering expects source text or an AST.")
+
+
+def _normalize_mode(execution_mode):
+    mode = execution_mode.replace("-", "_")
+    if mode not in HIP_EXECUTION_MODES:
+        raise HIPLoweringError(
+            f"Unknown HIP execution mode {execution_mode!r}; expected one of "
+            f"{sorted(HIP_EXECUTION_MODES)}.")
+    return mode
+
+
+def _normalize_reductions(reductions):
+    """Accept a DependenceAnalysis, a dict/list of reduction sites, or
+    ``(lineno, col)`` tuples."""
+    if reductions is None:
+        return {}
+    if hasattr(reductions, "reductions"):
+        reductions = reductions.reductions
+    if isinstance(reductions, dict):
+        reductions = reductions.values()
+    sites = {}
+    for position, site in enumerate(reductions):
+        if isinstance(site, tuple) and len(site) == 2:
+            sites[site] = (f"S{position + 1}", None)
+            continue
+        location = getattr(site, "location", None)
+        if location is None or getattr(site, "statement_id", None) is None:
+            raise HIPLoweringError(
+                "Reduction metadata must come from dependence analysis and "
+                "contain a source location, statement ID, and operator.")
+        sites[tuple(location)] = (site.statement_id, site.operator)
+    return sites
+
+
+# --------------------------------------------------------------------------
+# type inference
+
+class _Kinds:
+    """INT/FLOAT kinds of arrays, scalars and locals, inferred from use."""
+
+    def __init__(self, function, function_props, lookup_names, forced=None):
+        self.function = function
+        arguments = [a.arg for a in function.args.args]
+        subscripted = {
+            n.value.id for n in ast.walk(function)
+            if isinstance(n, ast.Subscript) and isinstance(n.value, ast.Name)}
+        demanded = set(lookup_names)
+        for key in (function_props or {}):
+            for name in (key if isinstance(key, tuple) else (key,)):
+                if isinstance(name, str):
+                    demanded.add(name)
+        index_contexts = []
+        for node in ast.walk(function):
+            if isinstance(node, ast.Subscript):
+                index_contexts.append(node.slice)
+            if (isinstance(node, ast.Call) and isinstance(node.func, ast.Name)
+                    and node.func.id == "range"):
+                index_contexts.extend(node.args)
+        for context in index_contexts:
+            demanded |= _names_in(context)
+        assignments = [
+            (node.targets[0].id, node.value) for node in ast.walk(function)
+            if isinstance(node, ast.Assign) and len(node.targets) == 1
+            and isinstance(node.targets[0], ast.Name)]
+        changed = True
+        while changed:
+            changed = False
+            for name, value in assignments:
+                if name in demanded:
+                    if isinstance(value, ast.Call):
+                        continue  # e.g. x = np.zeros(n): x stays a value array
+                    new = _names_in(value) - demanded
+                    if new:
+                        demanded |= new
+                        changed = True
+        self.arrays = {}
+        for name in subscripted | set(lookup_names):
+            self.arrays[name] = INT if name in demanded else FLOAT
+        for name in INTEGER_EXECUTOR_ARRAYS:
+            self.arrays[name] = INT
+        for name, kind in (forced or {}).items():
+            if name in self.arrays:
+                self.arrays[name] = kind
+        self.scalars = {
+            name: (INT if name in demanded else FLOAT)
+            for name in arguments if name not in subscripted}
+        self.locals = {}
+        self.iterators = {
+            node.target.id for node in ast.walk(function)
+            if isinstance(node, ast.For) and isinstance(node.target, ast.Name)}
+
+    def infer_locals(self, statements, extra_int=()):
+        names = _stored_names(statements)
+        for name in names:
+            self.locals.setdefault(name, INT)
+        for name in extra_int:
+            self.locals[name] = INT
+        changed = True
+        while changed:
+            changed = False
+            for statement in statements:
+                for node in ast.walk(statement):
+                    target, value = None, None
+                    if (isinstance(node, ast.Assign) and len(node.targets) == 1
+                            and isinstance(node.targets[0], ast.Name)):
+                        target, value = node.targets[0].id, node.value
+                    elif (isinstance(node, ast.AugAssign)
+                          and isinstance(node.target, ast.Name)):
+                        target = node.target.id
+                        value = ast.BinOp(left=ast.Name(id=target, ctx=ast.Load()),
+                                          op=node.op, right=node.value)
+                    if target is None or target in self.iterators:
+                        continue
+                    if self.kind(value) == FLOAT and self.locals.get(target) != FLOAT:
+                        self.locals[target] = FLOAT
+                        changed = True
+
+    def kind(self, node):
+        if isinstance(node, ast.Constant):
+            return FLOAT if isinstance(node.value, float) else INT
+        if isinstance(node, ast.Name):
+            if node.id in self.iterators:
+                return INT
+            if node.id in self.locals:
+                return self.locals[node.id]
+            return self.scalars.get(node.id, INT)
+        if isinstance(node, ast.Subscript):
+            if isinstance(node.value, ast.Name):
+                return self.arrays.get(node.value.id, FLOAT)
+            return FLOAT
+        if isinstance(node, ast.BinOp):
+            if isinstance(node.op, (ast.Div, ast.Pow)):
+                return FLOAT
+            kinds = (self.kind(node.left), self.kind(node.right))
+            return FLOAT if FLOAT in kinds else INT
+        if isinstance(node, ast.UnaryOp):
+            return INT if isinstance(node.op, ast.Not) else self.kind(node.operand)
+        if isinstance(node, (ast.Compare, ast.BoolOp)):
+            return INT
+        if isinstance(node, ast.IfExp):
+            kinds = (self.kind(node.body), self.kind(node.orelse))
+            return FLOAT if FLOAT in kinds else INT
+        if isinstance(node, ast.Call) and isinstance(node.func, ast.Name):
+            if node.func.id in ("float",):
+                return FLOAT
+            if node.func.id in ("int", "len", "_lcd_sorted_find"):
+                return INT
+            if node.func.id in ("abs", "min", "max"):
+                kinds = [self.kind(a) for a in node.args]
+                return FLOAT if FLOAT in kinds else INT
+        return FLOAT
+
+
+# --------------------------------------------------------------------------
+# Python AST -> C++ text
+
+class _Emitter:
+    def __init__(self, kinds, reductions, lowered_ids):
+        self.kinds = kinds
+        self.reductions = reductions
+        self.lowered_ids = lowered_ids
+
+    # ---- expressions
+    def expr(self, node):
+        k = self.kinds
+        if isinstance(node, ast.Constant):
+            if isinstance(node.value, bool):
+                return "1" if node.value else "0"
+            if isinstance(node.value, int):
+                return str(node.value)
+            if isinstance(node.value, float):
+                return repr(node.value)
+            raise HIPLoweringError(f"Unsupported constant {node.value!r}.")
+        if isinstance(node, ast.Name):
+            return node.id
+        if isinstance(node, ast.Subscript):
+            if not isinstance(node.value, ast.Name):
+                raise HIPLoweringError("Only 1-D array indexing is supported.")
+            return f"{node.value.id}[{self.expr(node.slice)}]"
+        if isinstance(node, ast.BinOp):
+            left, right = self.expr(node.left), self.expr(node.right)
+            if isinstance(node.op, ast.Div):
+                if k.kind(node.left) == INT:
+                    left = f"(double)({left})"
+                if k.kind(node.right) == INT:
+                    right = f"(double)({right})"
+                return f"({left} / {right})"
+            if isinstance(node.op, ast.FloorDiv):
+                if k.kind(node) == INT:
+                    return f"lcd_floordiv({left}, {right})"
+                return f"floor({left} / {right})"
+            if isinstance(node.op, ast.Mod):
+                if k.kind(node) == INT:
+                    return f"lcd_mod({left}, {right})"
+                return f"lcd_fmod({left}, {right})"
+            if isinstance(node.op, ast.Pow):
+                return f"pow((double)({left}), (double)({right}))"
+            text = _BIN_TEXT.get(type(node.op))
+            if text is None:
+                raise HIPLoweringError(
+                    f"Unsupported operator {type(node.op).__name__}.")
+            return f"({left} {text} {right})"
+        if isinstance(node, ast.UnaryOp):
+            operand = self.expr(node.operand)
+            if isinstance(node.op, ast.USub):
+                return f"(-{operand})"
+            if isinstance(node.op, ast.UAdd):
+                return operand
+            if isinstance(node.op, ast.Not):
+                return f"(!{operand})"
+            if isinstance(node.op, ast.Invert):
+                return f"(~{operand})"
+        if isinstance(node, ast.Compare):
+            parts = []
+            left = node.left
+            for op, right in zip(node.ops, node.comparators):
+                text = _CMP_TEXT.get(type(op))
+                if text is None:
+                    raise HIPLoweringError(
+                        f"Unsupported comparison {type(op).__name__}.")
+                parts.append(f"({self.expr(left)} {text} {self.expr(right)})")
+                left = right
+            return parts[0] if len(parts) == 1 else "(" + " && ".join(parts) + ")"
+        if isinstance(node, ast.BoolOp):
+            joiner = " && " if isinstance(node.op, ast.And) else " || "
+            return "(" + joiner.join(self.expr(v) for v in node.values) + ")"
+        if isinstance(node, ast.IfExp):
+            return (f"({self.expr(node.test)} ? {self.expr(node.body)} : "
+                    f"{self.expr(node.orelse)})")
+        if isinstance(node, ast.Call) and isinstance(node.func, ast.Name):
+            name = node.func.id
+            args = [self.expr(a) for a in node.args]
+            if name == "abs" and len(args) == 1:
+                return (f"fabs({args[0]})" if k.kind(node.args[0]) == FLOAT
+                        else f"lcd_iabs({args[0]})")
+            if name in ("min", "max") and len(args) == 2:
+                if FLOAT in (k.kind(node.args[0]), k.kind(node.args[1])):
+                    return f"f{name}((double)({args[0]}), (double)({args[1]}))"
+                return f"lcd_i{name}({args[0]}, {args[1]})"
+            if name == "float" and len(args) == 1:
+                return f"(double)({args[0]})"
+            if name == "int" and len(args) == 1:
+                return f"(lcd_index_t)({args[0]})"
+            if name == "_lcd_sorted_find" and len(args) == 4:
+                return f"lcd_sorted_find({', '.join(args)})"
+        raise HIPLoweringError(
+            f"Unsupported expression in a device loop: {ast.unparse(node)!r}.")
+
+    # ---- statements
+    def block(self, statements, indent, hooks=None):
+        lines = []
+        for statement in statements:
+            lines.extend(self.stmt(statement, indent, hooks))
+        return lines
+
+    def range_parts(self, loop):
+        args = loop.iter.args
+        if len(args) == 1:
+            return "0", self.expr(args[0]), "1"
+        if len(args) == 2:
+            return self.expr(args[0]), self.expr(args[1]), "1"
+        return self.expr(args[0]), self.expr(args[1]), self.expr(args[2])
+
+    def atomic(self, node):
+        location = (getattr(node, "lineno", None), getattr(node, "col_offset", None))
+        site = self.reductions.get(location)
+        if site is None:
+            return None
+        statement_id, operator = site
+        operator = operator or _AUG_TEXT.get(type(node.op))
+        call = _ATOMIC_CALLS.get(operator)
+        if call is None:
+            raise UnsupportedAtomicOperation(
+                f"Reduction {statement_id} uses {operator!r}, which has no "
+                "direct atomic lowering in this stage.")
+        if not (isinstance(node.target, ast.Subscript)
+                and isinstance(node.target.value, ast.Name)):
+            raise HIPLoweringError(
+                "Device atomics require an indexed 1-D array target.")
+        self.lowered_ids.add(statement_id)
+        return (f"{call}(&{node.target.value.id}"
+                f"[{self.expr(node.target.slice)}], {self.expr(node.value)});")
+
+    def stmt(self, node, indent, hooks=None):
+        pad = "    " * indent
+        if isinstance(node, ast.Pass):
+            return []
+        if isinstance(node, ast.Expr):
+            if isinstance(node.value, ast.Constant):
+                return []
+            raise HIPLoweringError(
+                f"Unsupported statement {ast.unparse(node)!r}.")
+        if isinstance(node, ast.Assign):
+            if len(node.targets) != 1:
+                raise HIPLoweringError("Chained assignment is not supported.")
+            target = node.targets[0]
+            if isinstance(target, (ast.Name, ast.Subscript)):
+                return [f"{pad}{self.expr(target)} = {self.expr(node.value)};"]
+            raise HIPLoweringError("Unsupported assignment target.")
+        if isinstance(node, ast.AugAssign):
+            atomic = self.atomic(node)
+            if atomic is not None:
+                return [pad + atomic]
+            expanded = ast.BinOp(left=deepcopy(node.target), op=node.op,
+                                 right=node.value)
+            for sub in ast.walk(expanded.left):
+                if hasattr(sub, "ctx"):
+                    sub.ctx = ast.Load()
+            return [f"{pad}{self.expr(node.target)} = {self.expr(expanded)};"]
+        if isinstance(node, ast.If):
+            lines = [f"{pad}if ({self.expr(node.test)}) {{"]
+            lines += self.block(node.body, indent + 1, hooks)
+            if node.orelse:
+                lines.append(f"{pad}}} else {{")
+                lines += self.block(node.orelse, indent + 1, hooks)
+            lines.append(f"{pad}}}")
+            return lines
+        if isinstance(node, ast.While):
+            lines = [f"{pad}while ({self.expr(node.test)}) {{"]
+            lines += self.block(node.body, indent + 1, hooks)
+            lines.append(f"{pad}}}")
+            return lines
+        if isinstance(node, ast.Break):
+            return [f"{pad}break;"]
+        if isinstance(node, ast.Continue):
+            return [f"{pad}continue;"]
+        if isinstance(node, ast.For):
+            if hooks is not None and hooks.is_mapped(node):
+                return hooks.mapped_loop(node, indent)
+            if not _is_range_loop(node):
+                raise HIPLoweringError(
+                    "Device loops must be `for name in range(...)`.")
+            lower, upper, step = self.range_parts(node)
+            name = node.target.id
+            if step == "1":
+                head = (f"{pad}for ({name} = {lower}; {name} < {upper}; "
+                        f"++{name}) {{")
+            else:
+                head = (f"{pad}for ({name} = {lower}; lcd_in_range({name}, "
+                        f"{upper}, {step}); {name} += {step}) {{")
+            return [head, *self.block(node.body, indent + 1, hooks), f"{pad}}}"]
+        raise HIPLoweringError(
+            f"Unsupported statement in a device loop: {ast.unparse(node)!r}.")
+
+
+# --------------------------------------------------------------------------
+# the lowerer
+
+_PRELUDE = r"""
+// ---- generated by lcd_amd.hip_lowering for gfx950 -------------------------
+// (hiprtc provides the HIP device headers implicitly)
+typedef LCD_INDEX_TYPE lcd_index_t;
+#define LCD_AGENT __HIP_MEMORY_SCOPE_AGENT
+
+__device__ __forceinline__ lcd_index_t lcd_floordiv(lcd_index_t a, lcd_index_t b) {
+    lcd_index_t q = a / b;
+    return ((a % b != 0) && ((a < 0) != (b < 0))) ? q - 1 : q;
+}
+__device__ __forceinline__ lcd_index_t lcd_mod(lcd_index_t a, lcd_index_t b) {
+    lcd_index_t r = a % b;
+    return (r != 0 && ((r < 0) != (b < 0))) ? r + b : r;
+}
+__device__ __forceinline__ double lcd_fmod(double a, double b) {
+    double r = fmod(a, b);
+    return (r != 0.0 && ((r < 0.0) != (b < 0.0))) ? r + b : r;
+}
+__device__ __forceinline__ lcd_index_t lcd_iabs(lcd_index_t a) { return a < 0 ? -a : a; }
+__device__ __forceinline__ lcd_index_t lcd_imin(lcd_index_t a, lcd_index_t b) { return a < b ? a : b; }
+__device__ __forceinline__ lcd_index_t lcd_imax(lcd_index_t a, lcd_index_t b) { return a > b ? a : b; }
+__device__ __forceinline__ bool lcd_in_range(lcd_index_t v, lcd_index_t stop, lcd_index_t step) {
+    return step > 0 ? v < stop : v > stop;
+}
+// First position p in [lo, hi) of a sorted segment with idx[p] == key, else -1.
+template <class T>
+__device__ __forceinline__ lcd_index_t lcd_sorted_find(const T* idx, lcd_index_t lo,
+                                                       lcd_index_t hi, lcd_index_t key) {
+    lcd_index_t left = lo, right = hi;
+    while (left < right) {
+        lcd_index_t middle = (left + right) >> 1;
+        if ((lcd_index_t)idx[middle] < key) left = middle + 1; else right = middle;
+    }
+    return (left < hi && (lcd_index_t)idx[left] == key) ? left : (lcd_index_t)-1;
+}
+// Device-scope relaxed atomics (fp64 add is a hardware L2 atomic on CDNA3/4).
+template <class T, class V> __device__ __forceinline__ void lcd_atomic_add(T* p, V v) {
+    __hip_atomic_fetch_add(p, (T)v, __ATOMIC_RELAXED, LCD_AGENT);
+}
+template <class T, class V> __device__ __forceinline__ void lcd_atomic_sub(T* p, V v) {
+    __hip_atomic_fetch_add(p, (T)(-(T)v), __ATOMIC_RELAXED, LCD_AGENT);
+}
+template <class T, class V> __device__ __forceinline__ void lcd_atomic_and(T* p, V v) {
+    __hip_atomic_fetch_and(p, (T)v, __ATOMIC_RELAXED, LCD_AGENT);
+}
+template <class T, class V> __device__ __forceinline__ void lcd_atomic_or(T* p, V v) {
+    __hip_atomic_fetch_or(p, (T)v, __ATOMIC_RELAXED, LCD_AGENT);
+}
+template <class T, class V> __device__ __forceinline__ void lcd_atomic_xor(T* p, V v) {
+    __hip_atomic_fetch_xor(p, (T)v, __ATOMIC_RELAXED, LCD_AGENT);
+}
+__device__ __forceinline__ int lcd_load_relaxed(const int* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, LCD_AGENT);
+}
+__device__ __forceinline__ void lcd_release_fence() { __atomic_thread_fence(__ATOMIC_RELEASE); }
+__device__ __forceinline__ void lcd_acquire_fence() { __atomic_thread_fence(__ATOMIC_ACQUIRE); }
+// Sum over the LCD_TASK_LANES lanes of one task group (xor butterfly: every
+// lane ends with the total, the compiler lowers the fixed masks to DPP).
+__device__ __forceinline__ double lcd_group_sum(double v) {
+#if LCD_TASK_LANES <= 64
+#pragma unroll
+    for (int offset = LCD_TASK_LANES / 2; offset > 0; offset >>= 1)
+        v += __shfl_xor(v, offset, LCD_TASK_LANES);
+#endif
+    return v;
+}
+"""
+
+_GROUP_SYNC_WAVE = ("__builtin_amdgcn_fence(__ATOMIC_ACQ_REL, \"wavefront\"); "
+                    "__builtin_amdgcn_wave_barrier();")
+_GROUP_SYNC_BLOCK = "__syncthreads();"
+
+
+class _MappedLoopHooks:
+    """Turns the thread-mapped loop into a lane-strided loop."""
+
+    def __init__(self, lowerer, emitter, loop):
+        self.lowerer = lowerer
+        self.emitter = emitter
+        self.loop = loop
+        self.partials = []   # (partial_name, target_node, op)
+
+    def is_mapped(self, node):
+        return node is self.loop
+
+    def mapped_loop(self, node, indent):
+        low = self.lowerer
+        pad = "    " * indent
+        emitter = self.emitter
+        lower, upper, step = emitter.range_parts(node)
+        if step != "1":
+            raise HIPLoweringError(
+                "The thread-mapped loop must have a unit step.")
+        name = node.target.id
+        lanes = "LCD_TASK_LANES"
+        unroll = low.thread_unroll_factor
+        body = deepcopy(node.body)
+        lines = [f"{pad}{low.group_sync}"]
+        for partial, _, _ in self.partials:
+            lines.append(f"{pad}{partial} = 0.0;")
+        body_lines = emitter.block(body, indent + (2 if unroll > 1 else 1), None)
+        hook_lines = low.push_hook_lines(indent + (2 if unroll > 1 else 1))
+        if unroll == 1:
+            lines.append(f"{pad}for ({name} = ({lower}) + _lane; {name} < {upper}; "
+                         f"{name} += {lanes}) {{")
+            lines += body_lines + hook_lines
+            lines.append(f"{pad}}}")
+        else:
+            base = f"_{name}_base"
+            lines.append(f"{pad}for (lcd_index_t {base} = ({lower}) + _lane; "
+                         f"{base} < {upper}; {base} += {lanes} * {unroll}) {{")
+            lines.append(f"{pad}#pragma unroll")
+            lines.append(f"{pad}    for (int _u = 0; _u < {unroll}; ++_u) {{")
+            lines.append(f"{pad}        {name} = {base} + _u * {lanes};")
+            lines.append(f"{pad}        if ({name} < {upper}) {{")
+            lines += ["    " + line for line in body_lines + hook_lines]
+            lines.append(f"{pad}        }}")
+            lines.append(f"{pad}    }}")
+            lines.append(f"{pad}}}")
+        lines.append(f"{pad}{low.group_sync}")
+        for partial, target, op in self.partials:
+            total = low.group_total(partial)
+            op_text = "+" if isinstance(op, ast.Add) else "-"
+            target_text = emitter.expr(target)
+            lines.append(f"{pad}{partial} = {total};")
+            if isinstance(target, ast.Subscript):
+                lines.append(f"{pad}if (_lane == 0) {target_text} = "
+                             f"{target_text} {op_text} {partial};")
+                lines.append(f"{pad}{low.group_sync}")
+            else:
+                lines.append(f"{pad}{target_text} = {target_text} {op_text} {partial};")
+        return lines
+
+
+class HIPLowerer:
+    def __init__(self, loop_iterator, reductions=None, kernel_name=None,
+                 execution_mode="plain", sync_free_ready_count=0,
+                 wavefront_threads_per_block=128, thread_loop_iterator=None,
+                 thread_unroll_factor=1, n_warp=None,
+                 dependence_protocol=COUNTER_DEPENDENCE, direct_dependence=None,
+                 function_props=None, structural_lookups=(), task_lanes=None,
+                 chain_tasks=False, argument_kinds=None,
+                 spin_limit=DEFAULT_SPIN_LIMIT):
+        self.loop_iterator = loop_iterator
+        self.thread_loop_iterator = thread_loop_iterator
+        self.reductions = _normalize_reductions(reductions)
+        self.kernel_name = kernel_name
+        self.execution_mode = _normalize_mode(execution_mode)
+        self.sync_free_ready_count = sync_free_ready_count
+        self.threads_per_block = wavefront_threads_per_block
+        self.thread_unroll_factor = thread_unroll_factor
+        self.n_warp = n_warp
+        self.function_props = function_props or {}
+        self.structural_lookups = tuple(structural_lookups or ())
+        self.chain_tasks = chain_tasks
+        self.argument_kinds = argument_kinds
+        self.spin_limit = spin_limit
+        if not isinstance(sync_free_ready_count, int):
+            raise HIPLoweringError(
+                "The sync-free readiness count must be an integer.")
+        if (not isinstance(wavefront_threads_per_block, int)
+                or wavefront_threads_per_block <= 0
+                or wavefront_threads_per_block > 1024):
+            raise HIPLoweringError(
+                "The thread-block size must be an integer in [1, 1024].")
+        if not isinstance(thread_unroll_factor, int) or thread_unroll_factor <= 0:
+            raise HIPLoweringError(
+                "The thread unroll factor must be a positive integer.")
+        if thread_unroll_factor != 1 and thread_loop_iterator is None:
+            raise HIPLoweringError(
+                "A thread unroll factor requires a thread-mapped loop.")
+        if n_warp is not None and (not isinstance(n_warp, int) or n_warp <= 0):
+            raise HIPLoweringError("n_warp must be a positive integer.")
+        if dependence_protocol not in DEPENDENCE_PROTOCOLS:
+            raise HIPLoweringError(
+                f"Unknown dependence protocol {dependence_protocol!r}.")
+        tpb = self.threads_per_block
+        self.block_task = (thread_loop_iterator is not None
+                           and n_warp is not None and n_warp > 1)
+        if self.block_task:
+            if tpb != n_warp * WAVEFRONT_SIZE:
+                raise HIPLoweringError(
+                    f"n_warp={n_warp} maps one task to "
+                    f"{n_warp * WAVEFRONT_SIZE} threads, but "
+                    f"threads_per_block={tpb}.")
+            self.task_lanes = tpb
+        elif thread_loop_iterator is None:
+            self.task_lanes = 1
+        else:
+            lanes = task_lanes if task_lanes is not None else min(
+                WAVEFRONT_SIZE, tpb)
+            if (lanes <= 0 or lanes & (lanes - 1) or lanes > WAVEFRONT_SIZE
+                    or tpb % lanes):
+                raise HIPLoweringError(
+                    "task_lanes must be a power of two <= 64 that divides "
+                    f"threads_per_block; got {lanes} with {tpb}.")
+            self.task_lanes = lanes
+        if self.execution_mode != "plain" and not self.block_task and (
+                tpb % WAVEFRONT_SIZE and tpb > WAVEFRONT_SIZE):
+            raise HIPLoweringError(
+                "threads_per_block must be a multiple of the 64-lane "
+                f"wavefront; got {tpb}.")
+        # "warp mapped" in the reference: one warp cooperates on one task.
+        self.warp_mapped = (
+            thread_loop_iterator is not None and not self.block_task
+            and self.execution_mode in {"sync_free", "wavefront"})
+        self.direct_dependence = direct_dependence
+        self.dependence_protocol = (
+            dependence_protocol
+            if (direct_dependence is not None
+                and direct_dependence.kind == dependence_protocol
+                and self.warp_mapped and self.execution_mode == "sync_free"
+                and sync_free_ready_count == 0)
+            else COUNTER_DEPENDENCE)
+        self.group_sync = (_GROUP_SYNC_BLOCK if self.block_task
+                           else _GROUP_SYNC_WAVE)
+        self.segmented_sorted = segmented_array_pairs(self.function_props)
+
+    # ---- helpers used by the hooks
+    def group_total(self, partial):
+        if self.block_task:
+            return f"lcd_block_sum({partial}, _lcd_reduce)"
+        if self.task_lanes == 1:
+            return partial
+        return f"lcd_group_sum({partial})"
+
+    def push_hook_lines(self, indent):
+        if self.dependence_protocol != PUSH_DEPENDENCE:
+            return []
+        pad = "    " * indent
+        dependence = self.direct_dependence
+        endpoint = self._emitter.expr(dependence.endpoint)
+        lines = [f"{pad}lcd_release_fence();"]
+        if dependence.guard is not None:
+            lines.append(f"{pad}if ({self._emitter.expr(dependence.guard)})")
+            lines.append(f"{pad}    lcd_atomic_sub(&dep_count[{endpoint}], 1);")
+        else:
+            lines.append(f"{pad}lcd_atomic_sub(&dep_count[{endpoint}], 1);")
+        return lines
+
+    # ---- main entry
+    def lower(self, code):
+        module = _to_module(code)
+        module = rewrite_structural_lookups(
+            module, self.structural_lookups, self.function_props)
+        functions = [n for n in module.body
+                     if isinstance(n, (ast.FunctionDef, ast.AsyncFunctionDef))]
+        if len(functions) != 1 or not isinstance(functions[0], ast.FunctionDef):
+            raise HIPLoweringError(
+                "HIP lowering expects exactly one synchronous function.")
+        function = functions[0]
+        function.decorator_list = []
+        top_index, target_loop, enclosing = self._target_loop(function)
+        self._target_loop_cache = target_loop
+        self.host_loops = enclosing
+        host_loop_iterators = [loop.target.id for loop in enclosing]
+        host_prelude = deepcopy(function.body[:top_index])
+        host_epilogue = deepcopy(function.body[top_index + 1:])
+        arguments = [a.arg for a in function.args.args]
+        body = deepcopy(target_loop.body)
+        body = self._lower_sorted_searches(body)
+
+        loaded = set()
+        for statement in body:
+            loaded |= {n.id for n in ast.walk(statement)
+                       if isinstance(n, ast.Name) and isinstance(n.ctx, ast.Load)}
+        loaded |= _names_in(target_loop.iter)
+        prelude_names = _stored_names(host_prelude)
+        subscripted = {
+            n.value.id for s in body for n in ast.walk(s)
+            if isinstance(n, ast.Subscript) and isinstance(n.value, ast.Name)}
+        lifted_variables = [
+            name for name in prelude_names
+            if name in loaded and name not in arguments and name in subscripted]
+        lifted_loop_parameters = [
+            name for name in prelude_names
+            if name in loaded and name not in arguments
+            and name not in subscripted]
+        zero_initialised = self._zero_initialised(host_prelude, lifted_variables)
+
+        lookup_names = structural_lookup_names(self.structural_lookups)
+        kinds = _Kinds(function, self.function_props, lookup_names,
+                       self.argument_kinds)
+        for name in lifted_variables:
+            kinds.arrays.setdefault(name, FLOAT)
+        for name in lifted_loop_parameters:
+            kinds.scalars[name] = INT
+        for name in host_loop_iterators:
+            kinds.scalars[name] = INT
+        local_names = [
+            name for name in _stored_names(body)
+            if name not in arguments and name not in lifted_variables]
+        kinds.infer_locals(body)
+        self._kinds = kinds
+        lowered_ids = set()
+        emitter = _Emitter(kinds, self.reductions, lowered_ids)
+        self._emitter = emitter
+
+        written_arrays = self._written_arrays(body)
+        user_arguments = list(arguments)
+        for name in lifted_variables + lifted_loop_parameters:
+            if name not in user_arguments:
+                user_arguments.append(name)
+        for name in host_loop_iterators:
+            if name not in user_arguments and name in loaded:
+                user_arguments.append(name)
+        for name in lookup_names:
+            if name not in user_arguments:
+                user_arguments.append(name)
+        executor_arguments = self._executor_arguments()
+        kernel_arguments = user_arguments + [
+            name for name in executor_arguments if name not in user_arguments]
+
+        task_body = self._task_body(body, emitter, local_names, target_loop)
+        missing = ({sid for sid, _ in self.reductions.values()} - lowered_ids)
+        if missing:
+            raise HIPLoweringError(
+                "Reduction statements were not found in the selected loop: "
+                + ", ".join(sorted(missing)))
+
+        function_name = function.name
+        kernel_name = self.kernel_name or function_name + "_hip_kernel"
+        launcher_name = function_name + "_hip_launch"
+        reset_name = None
+        array_arguments = {
+            name: kinds.arrays[name] for name in kernel_arguments
+            if name in kinds.arrays}
+        scalar_arguments = {
+            name: kinds.scalars.get(name, INT) for name in kernel_arguments
+            if name not in array_arguments}
+        for name in ("band_start", "band_end", "task_count"):
+            if name in scalar_arguments:
+                scalar_arguments[name] = INT
+
+        kernel_text = self._kernel_text(
+            kernel_name, kernel_arguments, array_arguments, scalar_arguments,
+            written_arrays, task_body, local_names, target_loop)
+        reset_text = ""
+        if self.execution_mode == "sync_free":
+            reset_name = function_name + "_hip_reset"
+            reset_text = self._reset_kernel_text(reset_name)
+        source = self._module_text(
+            array_arguments, scalar_arguments, reset_text, kernel_text)
+        launcher_source, launcher_arguments = self._launcher_text(
+            launcher_name, kernel_name, reset_name, kernel_arguments)
+        return HIPLoweringResult(
+            source=source,
+            kernel_source=kernel_text,
+            launcher_source=launcher_source,
+            launcher_ast=ast.parse(launcher_source),
+            kernel_name=kernel_name,
+            launcher_name=launcher_name,
+            reset_kernel_name=reset_name,
+            kernel_arguments=kernel_arguments,
+            launcher_arguments=launcher_arguments,
+            lifted_variables=lifted_variables,
+            lifted_loop_parameters=lifted_loop_parameters,
+            host_prelude=host_prelude,
+            host_epilogue=host_epilogue,
+            atomic_statement_ids=lowered_ids,
+            execution_mode=self.execution_mode,
+            auxiliary_arguments=[*lookup_names, *executor_arguments],
+            thread_loop_iterator=self.thread_loop_iterator,
+            thread_unroll_factor=self.thread_unroll_factor,
+            host_loop_iterators=tuple(host_loop_iterators),
+            n_warp=self.n_warp,
+            warp_mapped=self.warp_mapped,
+            dependence_protocol=self.dependence_protocol,
+            task_lanes=self.task_lanes,
+            threads_per_block=self.threads_per_block,
+            tasks_per_block=max(1, self.threads_per_block // self.task_lanes),
+            array_arguments=array_arguments,
+            scalar_arguments=scalar_arguments,
+            written_arrays=tuple(sorted(written_arrays)),
+            zero_initialised=zero_initialised,
+            persistent=self.execution_mode == "sync_free",
+            function_name=function_name,
+        )
+
+    # ---- structure discovery
+    def _target_loop(self, function):
+        matches = []
+
+        def search(statements, enclosing, top_index):
+            for index, statement in enumerate(statements):
+                top = index if top_index is None else top_index
+                if not isinstance(statement, ast.For):
+                    continue
+                if (isinstance(statement.target, ast.Name)
+                        and statement.target.id == self.loop_iterator):
+                    matches.append((top, statement, tuple(enclosing)))
+                    continue
+                search(statement.body, enclosing + [statement], top)
+
+        search(function.body, [], None)
+        if len(matches) != 1:
+            raise HIPLoweringError(
+                f"Expected exactly one top-level loop over "
+                f"{self.loop_iterator!r}; found {len(matches)}.")
+        top_index, loop, enclosing = matches[0]
+        if not _is_range_loop(loop):
+            raise HIPLoweringError(
+                "The block-mapped loop must iterate over range(...).")
+        for outer, inner in zip(enclosing, list(enclosing[1:]) + [loop]):
+            if not _is_range_loop(outer) or outer.body != [inner]:
+                raise HIPLoweringError(
+                    "Loops enclosing the block-mapped loop may contain only "
+                    "the next loop.")
+        return top_index, loop, enclosing
+
+    def _zero_initialised(self, host_prelude, lifted_variables):
+        """``x = np.zeros(expr)`` in the prelude: allocate and zero on the
+        device instead of building the array on the host."""
+        found = {}
+        for statement in host_prelude:
+            if not (isinstance(statement, ast.Assign)
+                    and len(statement.targets) == 1
+                    and isinstance(statement.targets[0], ast.Name)
+                    and statement.targets[0].id in lifted_variables):
+                continue
+            call = statement.value
+            if (isinstance(call, ast.Call)
+                    and isinstance(call.func, ast.Attribute)
+                    and call.func.attr == "zeros"
+                    and isinstance(call.func.value, ast.Name)
+                    and call.func.value.id in ("np", "numpy")
+                    and len(call.args) == 1 and not call.keywords):
+                found[statement.targets[0].id] = ast.unparse(call.args[0])
+        return found
+
+    def _written_arrays(self, body):
+        written = set()
+        for statement in body:
+            for node in ast.walk(statement):
+                targets = []
+                if isinstance(node, ast.Assign):
+                    targets = node.targets
+                elif isinstance(node, ast.AugAssign):
+                    targets = [node.target]
+                for target in targets:
+                    if isinstance(target, ast.Subscript) and isinstance(
+                            target.value, ast.Name):
+                        written.add(target.value.id)
+        return written
+
+    def _lower_sorted_searches(self, body):
+        """Equality searches over a sorted segment become a lower-bound
+        search (the reference does this for nested thread-mapped loops,
+        compiler/cuda_lowering.py:1640-1756)."""
+        if not self.segmented_sorted:
+            return body
+        pairs = self.segmented_sorted
+
+        class Searches(ast.NodeTransformer):
+            def visit_For(self, node):
+                node = self.generic_visit(node)
+                match = match_segment_search(node, pairs)
+                if match is None:
+                    return node
+                lower, upper = node.iter.args
+                find = ast.Assign(
+                    targets=[ast.Name(id=match.iterator, ctx=ast.Store())],
+                    value=ast.Call(
+                        func=ast.Name(id="_lcd_sorted_find", ctx=ast.Load()),
+                        args=[ast.Name(id=match.index_array, ctx=ast.Load()),
+                              deepcopy(lower), deepcopy(upper),
+                              deepcopy(match.needle)],
+                        keywords=[]))
+                found = ast.If(
+                    test=ast.Compare(
+                        left=ast.Name(id=match.iterator, ctx=ast.Load()),
+                        ops=[ast.GtE()], comparators=[ast.Constant(value=0)]),
+                    body=[deepcopy(s) for s in match.matched_body]
+                    or [ast.Pass()],
+                    orelse=[])
+                return [ast.copy_location(find, node),
+                        ast.copy_location(found, node)]
+
+        wrapper = ast.Module(body=body, type_ignores=[])
+        return ast.fix_missing_locations(Searches().visit(wrapper)).body
+
+    def _executor_arguments(self):
+        if self.execution_mode == "sync_free":
+            if self.dependence_protocol == PUSH_DEPENDENCE:
+                names = list(PUSH_ARGUMENTS)
+            elif self.dependence_protocol == PULL_DEPENDENCE:
+                names = list(PULL_ARGUMENTS)
+            else:
+                names = list(SYNC_FREE_ARGUMENTS)
+            return names + [STATUS_ARGUMENT]
+        if self.execution_mode == "wavefront":
+            return list(WAVEFRONT_ARGUMENTS)
+        return []
+
+    # ---- task body
+    def _find_mapped_loop(self, body):
+        if self.thread_loop_iterator is None:
+            return None
+        matches = [
+            node for statement in body for node in ast.walk(statement)
+            if isinstance(node, ast.For) and isinstance(node.target, ast.Name)
+            and node.target.id == self.thread_loop_iterator]
+        if len(matches) != 1:
+            raise HIPLoweringError(
+                "The selected thread iterator must identify exactly one inner "
+                f"for loop; found {len(matches)} for "
+                f"{self.thread_loop_iterator!r}.")
+        if not _is_range_loop(matches[0]):
+            raise HIPLoweringError(
+                "The thread-mapped loop must iterate over range(...).")
+        return matches[0]
+
+    def _privatize(self, loop, hooks, outer_assigned):
+        """Updates of group-invariant targets inside the mapped loop become
+        per-lane partial sums (compiler/cuda_lowering.py:2061-2121)."""
+        loop_local = {loop.target.id} | set(_stored_names(loop.body))
+        safe = True
+        counter = [0]
+
+        def invariant(target):
+            if isinstance(target, ast.Name):
+                return target.id in outer_assigned
+            if isinstance(target, ast.Subscript):
+                return not (_names_in(target) & loop_local)
+            return False
+
+        lowerer = self
+
+        class Privatizer(ast.NodeTransformer):
+            depth = 0
+
+            def visit_AugAssign(self, node):
+                location = (node.lineno, node.col_offset)
+                if location in lowerer.reductions or not invariant(node.target):
+                    return self.generic_visit(node)
+                if not isinstance(node.op, (ast.Add, ast.Sub)):
+                    nonlocal safe
+                    safe = False
+                    return node
+                name = f"_thread_partial_{counter[0]}"
+                counter[0] += 1
+                hooks.partials.append((name, deepcopy(node.target), node.op))
+                return ast.copy_location(ast.AugAssign(
+                    target=ast.Name(id=name, ctx=ast.Store()), op=ast.Add(),
+                    value=node.value), node)
+
+            def visit_Assign(self, node):
+                nonlocal safe
+                if any(invariant(t) for t in node.targets):
+                    safe = False
+                return node
+
+            def visit_For(self, node):
+                self.depth += 1
+                node = self.generic_visit(node)
+                self.depth -= 1
+                return node
+
+            visit_While = visit_For
+
+            def visit_Break(self, node):
+                nonlocal safe
+                if self.depth == 0:
+                    safe = False
+                return node
+
+            visit_Continue = visit_Break
+
+        loop.body = [Privatizer().visit(s) for s in loop.body]
+        ast.fix_missing_locations(loop)
+        return safe
+
+    def _guard_stores(self, statements, mapped_loop):
+        """Outside the mapped loop, array stores are issued by lane 0 of the
+        group and followed by a group-scope fence."""
+        lowerer = self
+
+        class Guard(ast.NodeTransformer):
+            def visit_For(self, node):
+                if node is mapped_loop:
+                    return node
+                return self.generic_visit(node)
+
+            def _guarded(self, node):
+                marker = ast.If(
+                    test=ast.Name(id="_LCD_LANE0", ctx=ast.Load()),
+                    body=[node], orelse=[])
+                marker._lcd_store_guard = True
+                return ast.copy_location(marker, node)
+
+            def visit_Assign(self, node):
+                if any(isinstance(t, ast.Subscript) for t in node.targets):
+                    return self._guarded(node)
+                return node
+
+            def visit_AugAssign(self, node):
+                if isinstance(node.target, ast.Subscript):
+                    location = (node.lineno, node.col_offset)
+                    if location in lowerer.reductions:
+                        return self._guarded(node)
+                    return self._guarded(node)
+                return node
+
+        wrapper = ast.Module(body=statements, type_ignores=[])
+        return Guard().visit(wrapper).body
+
+    def _task_body(self, body, emitter, local_names, target_loop):
+        """C++ lines of one task (indent level 0), `i` already bound."""
+        mapped = self._find_mapped_loop(body)
+        hooks = None
+        if mapped is not None:
+            hooks = _MappedLoopHooks(self, emitter, mapped)
+            outer_assigned = set(local_names) - (
+                {mapped.target.id} | set(_stored_names(mapped.body)))
+            if not self._privatize(mapped, hooks, outer_assigned):
+                raise HIPLoweringError(
+                    "The thread-mapped loop writes state that cannot be "
+                    "privatized safely.")
+            for partial, _, _ in hooks.partials:
+                self._kinds.locals[partial] = FLOAT
+            if self.task_lanes > 1:
+                body = self._guard_stores(body, mapped)
+            if (self.dependence_protocol != COUNTER_DEPENDENCE
+                    and mapped not in body):
+                # hooks describe task-level edges; a nested work-sharing loop
+                # would change their multiplicity
+                self.dependence_protocol = COUNTER_DEPENDENCE
+        self._partials = hooks.partials if hooks else []
+        lines = []
+        for statement in body:
+            lines.extend(self._emit_guarded(statement, emitter, 0, hooks))
+        return lines
+
+    def _emit_guarded(self, node, emitter, indent, hooks):
+        pad = "    " * indent
+        if isinstance(node, ast.If) and getattr(node, "_lcd_store_guard", False):
+            inner = emitter.block(node.body, indent + 1, None)
+            return [f"{pad}if (_lane == 0) {{", *inner, f"{pad}}}",
+                    f"{pad}{self.group_sync}"]
+        if isinstance(node, ast.If):
+            lines = [f"{pad}if ({emitter.expr(node.test)}) {{"]
+            for child in node.body:
+                lines += self._emit_guarded(child, emitter, indent + 1, hooks)
+            if node.orelse:
+                lines.append(f"{pad}}} else {{")
+                for child in node.orelse:
+                    lines += self._emit_guarded(child, emitter, indent + 1, hooks)
+            lines.append(f"{pad}}}")
+            return lines
+        if isinstance(node, ast.For) and not (hooks and hooks.is_mapped(node)):
+            if not _is_range_loop(node):
+                raise HIPLoweringError(
+                    "Device loops must be `for name in range(...)`.")
+            lower, upper, step = emitter.range_parts(node)
+            name = node.target.id
+            if step == "1":
+                head = f"{pad}for ({name} = {lower}; {name} < {upper}; ++{name}) {{"
+            else:
+                head = (f"{pad}for ({name} = {lower}; lcd_in_range({name}, "
+                        f"{upper}, {step}); {name} += {step}) {{")
+            lines = [head]
+            for child in node.body:
+                lines += self._emit_guarded(child, emitter, indent + 1, hooks)
+            lines.append(f"{pad}}}")
+            return lines
+        if isinstance(node, ast.While):
+            lines = [f"{pad}while ({emitter.expr(node.test)}) {{"]
+            for child in node.body:
+                lines += self._emit_guarded(child, emitter, indent + 1, hooks)
+            lines.append(f"{pad}}}")
+            return lines
+        return emitter.stmt(node, indent, hooks)
+
+    # ---- text assembly
+    def _c_type(self, name, kind, is_array):
+        return f"LCD_T_{name}"
+
+    def _module_text(self, array_arguments, scalar_arguments, reset_text,
+                     kernel_text):
+        defines = [
+            "#ifndef LCD_INDEX_TYPE", "#define LCD_INDEX_TYPE int", "#endif",
+            f"#define LCD_TPB {self.threads_per_block}",
+            f"#define LCD_TASK_LANES {self.task_lanes}",
+            f"#define LCD_GROUPS_PER_BLOCK (LCD_TPB / LCD_TASK_LANES)",
+            "#ifndef LCD_SPIN_LIMIT",
+            f"#define LCD_SPIN_LIMIT {self.spin_limit}", "#endif",
+            f"#define LCD_READY_COUNT {self.sync_free_ready_count}",
+        ]
+        for name, kind in array_arguments.items():
+            default = "int" if kind == INT else "double"
+            defines += [f"#ifndef LCD_T_{name}",
+                        f"#define LCD_T_{name} {default}", "#endif"]
+        for name, kind in scalar_arguments.items():
+            default = "long long" if kind == INT else "double"
+            if name in ("band_start", "band_end", "task_count"):
+                default = "int"
+            defines += [f"#ifndef LCD_T_{name}",
+                        f"#define LCD_T_{name} {default}", "#endif"]
+        block_sum = ""
+        if self.block_task:
+            block_sum = textwrap.dedent("""
+            // Sum over the whole workgroup: butterfly inside each wavefront,
+            // then one LDS slot per wavefront.
+            __device__ __forceinline__ double lcd_block_sum(double v, double* slots) {
+                for (int offset = 32; offset > 0; offset >>= 1)
+                    v += __shfl_xor(v, offset, 64);
+                __syncthreads();
+                if ((threadIdx.x & 63) == 0) slots[threadIdx.x >> 6] = v;
+                __syncthreads();
+                double total = 0.0;
+                for (int w = 0; w < LCD_TPB / 64; ++w) total += slots[w];
+                return total;
+            }
+            """)
+        return ("\n".join(defines) + "\n" + _PRELUDE + block_sum + reset_text
+                + kernel_text)
+
+    def _signature(self, kernel_arguments, array_arguments, scalar_arguments,
+                   written_arrays):
+        parts = []
+        mutable_executor = {"dep_count", "task_counter", "done", STATUS_ARGUMENT}
+        for name in kernel_arguments:
+            if name in array_arguments:
+                const = (name not in written_arrays
+                         and name not in mutable_executor)
+                qualifier = "const " if const else ""
+                restrict = " __restrict__" if const else ""
+                parts.append(f"{qualifier}LCD_T_{name}*{restrict} {name}")
+            else:
+                parts.append(f"LCD_T_{name} {name}")
+        return ",\n        ".join(parts)
+
+    def _declarations(self, local_names, indent):
+        pad = "    " * indent
+        lines = []
+        declared = set()
+        for name in list(local_names) + [p for p, _, _ in self._partials]:
+            if name in declared or name == self.loop_iterator:
+                continue
+            declared.add(name)
+            kind = self._kinds.locals.get(name, INT)
+            if name in self._kinds.iterators:
+                kind = INT
+            ctype = "lcd_index_t" if kind == INT else "double"
+            init = "0" if kind == INT else "0.0"
+            lines.append(f"{pad}{ctype} {name} = {init};")
+        return lines
+
+    def _node_guard(self, target_loop):
+        emitter = self._emitter
+        lower, upper, step = emitter.range_parts(target_loop)
+        tests = [f"{self.loop_iterator} < {upper}"]
+        if lower != "0":
+            tests.append(f"{self.loop_iterator} >= {lower}")
+        return " && ".join(tests)
+
+    def _kernel_text(self, kernel_name, kernel_arguments, array_arguments,
+                     scalar_arguments, written_arrays, task_body, local_names,
+                     target_loop):
+        it = self.loop_iterator
+        signature = self._signature(kernel_arguments, array_arguments,
+                                    scalar_arguments, written_arrays)
+        lines = [
+            "", f'extern "C" __global__ void __launch_bounds__(LCD_TPB)',
+            f"{kernel_name}(", f"        {signature})", "{",
+        ]
+        if self.block_task:
+            lines.append("    __shared__ double _lcd_reduce[LCD_TPB / 64];")
+            lines.append("    __shared__ int _lcd_task_slot;")
+        lines.append("    const int _lane = threadIdx.x % LCD_TASK_LANES;")
+        lines.append("    (void)_lane;")
+        lines.append(f"    lcd_index_t {it} = 0;")
+        lines += self._declarations(local_names, 1)
+        guard = self._node_guard(target_loop)
+
+        def task(indent):
+            pad = "    " * indent
+            out = [f"{pad}if ({guard}) {{"]
+            out += [pad + "    " + line for line in task_body]
+            out.append(f"{pad}}}")
+            return out
+
+        def node_loop(indent, body_fn):
+            pad = "    " * indent
+            if self.chain_tasks:
+                return ([f"{pad}for (int _pos = task_ptr[_task]; "
+                         f"_pos < task_ptr[_task + 1]; ++_pos) {{",
+                         f"{pad}    {it} = task_nodes[_pos];",
+                         *body_fn(indent + 1), f"{pad}}}"])
+            return [f"{pad}{it} = task_nodes[_task];", *body_fn(indent)]
+
+        if self.execution_mode == "plain":
+            lower, _, _ = self._emitter.range_parts(target_loop)
+            lines.append("    const long long _group = "
+                         "((long long)blockIdx.x * LCD_TPB + threadIdx.x) "
+                         "/ LCD_TASK_LANES;")
+            lines.append(f"    {it} = (lcd_index_t)(({lower}) + _group);")
+            lines += task(1)
+        elif self.execution_mode == "wavefront":
+            lines.append("    const long long _task = (long long)band_start + "
+                         "((long long)blockIdx.x * LCD_TPB + threadIdx.x) "
+                         "/ LCD_TASK_LANES;")
+            lines.append("    if (_task >= band_end) return;")
+            lines += node_loop(1, task)
+        else:
+            lines += self._sync_free_text(task, node_loop)
+        lines.append("}")
+        return "\n".join(lines) + "\n"
+
+    def _sync_free_text(self, task, node_loop):
+        """Persistent poll-loop executor.
+
+        Wavefronts fetch ``64 / task_lanes`` consecutive tasks from the
+        level-ordered queue, then loop until every one of them has run: a
+        group whose dependences are satisfied executes its task inside the
+        loop, the others keep polling.  Because nothing blocks inside the
+        loop, tasks that share a wavefront can depend on each other.  The
+        lowest unfinished task in queue order is always held by a resident
+        wavefront and has all its producers finished or running, which is the
+        forward-progress argument; a watchdog bounds every wait anyway.
+        """
+        it = self.loop_iterator
+        protocol = self.dependence_protocol
+        if self.chain_tasks:
+            raise HIPLoweringError(
+                "Chain tasks are not supported by the sync-free executor.")
+        lines = ["    const int _task_count = (int)task_count;"]
+        if self.block_task:
+            lines += [
+                "    while (true) {",
+                "        if (threadIdx.x == 0)",
+                "            _lcd_task_slot = atomicAdd(&task_counter[0], 1);",
+                "        __syncthreads();",
+                "        const int _task = _lcd_task_slot;",
+                "        __syncthreads();",
+                "        if (_task >= _task_count) return;",
+                f"        {it} = (lcd_index_t)task_nodes[_task];",
+                "        if (threadIdx.x == 0) {",
+                "            long long _spins = 0;",
+                "            int _ok = 1;",
+                f"            while (lcd_load_relaxed(&dep_count[{it}]) != LCD_READY_COUNT) {{",
+                "                __builtin_amdgcn_s_sleep(1);",
+                "                if (++_spins > LCD_SPIN_LIMIT || ((_spins & 255) == 0 && "
+                f"lcd_load_relaxed(&{STATUS_ARGUMENT}[0]) != 0)) {{",
+                f"                    {STATUS_ARGUMENT}[0] = 1;",
+                "                    _ok = 0;",
+                "                    break;",
+                "                }",
+                "            }",
+                "            _lcd_task_slot = _ok;",
+                "        }",
+                "        __syncthreads();",
+                "        if (!_lcd_task_slot) return;",
+                "        __syncthreads();",
+                "        lcd_acquire_fence();",
+            ]
+            lines += task(2)
+            lines += [
+                "        lcd_release_fence();",
+                "        __syncthreads();",
+                f"        for (int _e = dag_ptr[{it}] + _lane; "
+                f"_e < dag_ptr[{it} + 1]; _e += LCD_TASK_LANES)",
+                "            lcd_atomic_sub(&dep_count[dag_index[_e]], 1);",
+                "    }",
+            ]
+            return lines
+        lines += [
+            "    const int _tasks_per_wave = 64 / LCD_TASK_LANES;",
+            "    while (true) {",
+            "        int _base = 0;",
+            "        if ((threadIdx.x & 63) == 0)",
+            "            _base = atomicAdd(&task_counter[0], _tasks_per_wave);",
+            "        _base = __shfl(_base, 0, 64);",
+            "        if (_base >= _task_count) return;",
+            "        const int _task = _base + (int)(threadIdx.x & 63) / LCD_TASK_LANES;",
+            "        bool _pending = _task < _task_count;",
+            f"        {it} = _pending ? (lcd_index_t)task_nodes[_task] : 0;",
+            "        long long _spins = 0;",
+            "        while (__ballot(_pending)) {",
+            "            if (_pending) {",
+        ]
+        if protocol == PULL_DEPENDENCE:
+            lines += self._pull_ready_lines(4)
+        else:
+            lines.append(f"                const bool _ready = "
+                         f"lcd_load_relaxed(&dep_count[{it}]) == LCD_READY_COUNT;")
+        lines.append("                if (_ready) {")
+        lines.append("                    lcd_acquire_fence();")
+        lines += task(5)
+        if protocol == COUNTER_DEPENDENCE:
+            lines += [
+                f"                    {self.group_sync}",
+                "                    lcd_release_fence();",
+                f"                    for (int _e = dag_ptr[{it}] + _lane; "
+                f"_e < dag_ptr[{it} + 1]; _e += LCD_TASK_LANES)",
+                "                        lcd_atomic_sub(&dep_count[dag_index[_e]], 1);",
+            ]
+        elif protocol == PULL_DEPENDENCE:
+            lines += [
+                f"                    {self.group_sync}",
+                "                    lcd_release_fence();",
+                f"                    if (_lane == 0) __hip_atomic_store(&done[{it}], 1, "
+                "__ATOMIC_RELAXED, LCD_AGENT);",
+            ]
+        lines += [
+            "                    _pending = false;",
+            "                } else {",
+            "                    __builtin_amdgcn_s_sleep(1);",
+            "                    if (++_spins > LCD_SPIN_LIMIT || ((_spins & 255) == 0 && "
+            f"lcd_load_relaxed(&{STATUS_ARGUMENT}[0]) != 0)) {{",
+            f"                        {STATUS_ARGUMENT}[0] = 1;",
+            "                        _pending = false;",
+            "                        _task_aborted = true;",
+            "                    }",
+            "                }",
+            "            }",
+            "        }",
+            "        if (__ballot(_task_aborted)) return;",
+            "    }",
+        ]
+        lines.insert(1, "    bool _task_aborted = false;")
+        return lines
+
+    def _pull_ready_lines(self, indent):
+        """Readiness for the pull protocol: every producer this task reads
+        from (the endpoint of the direct dependence over the mapped loop's
+        range) has published ``done``."""
+        pad = "    " * indent
+        dependence = self.direct_dependence
+        emitter = self._emitter
+        loop = dependence.thread_loop
+        lower, upper, _ = emitter.range_parts(loop)
+        name = loop.target.id
+        endpoint = emitter.expr(dependence.endpoint)
+        guard = (emitter.expr(dependence.guard)
+                 if dependence.guard is not None else "true")
+        total = ("lcd_group_sum((double)_missing) != 0.0"
+                 if self.task_lanes > 1 else "_missing != 0")
+        return [
+            f"{pad}int _missing = 0;",
+            f"{pad}for ({name} = ({lower}) + _lane; {name} < {upper}; "
+            f"{name} += LCD_TASK_LANES)",
+            f"{pad}    if (({guard}) && lcd_load_relaxed(&done[{endpoint}]) == 0) "
+            "{ _missing = 1; break; }",
+            f"{pad}bool _ready = !({total});",
+        ]
+
+    def _reset_kernel_text(self, reset_name):
+        """Restores the mutable executor state before every sweep (the
+        reference's reset kernel, compiler/cuda_lowering.py:737-853)."""
+        if self.dependence_protocol == PULL_DEPENDENCE:
+            body = ("    if (t < count) done[t] = 0;\n"
+                    "    if (t == 0) { task_counter[0] = 0; }\n")
+            signature = ("int* done, int* task_counter, long long count")
+        else:
+            body = ("    if (t < count) dep_count[t] = initial_dep_count[t];\n"
+                    "    if (t == 0) { task_counter[0] = 0; }\n")
+            signature = ("int* dep_count, const int* __restrict__ "
+                         "initial_dep_count, int* task_counter, long long count")
+        return (f'\nextern "C" __global__ void {reset_name}({signature})\n{{\n'
+                "    const long long t = (long long)blockIdx.x * blockDim.x + "
+                f"threadIdx.x;\n{body}}}\n")
+
+    def _launcher_text(self, launcher_name, kernel_name, reset_name,
+                       kernel_arguments):
+        """The Python launcher: what the host does on every call."""
+        launcher_arguments = []
+        for name in kernel_arguments:
+            if name in ("band_start", "band_end"):
+                if "band_ptr" not in launcher_arguments:
+                    launcher_arguments.append("band_ptr")
+                continue
+            if name == "task_count":
+                continue
+            launcher_arguments.append(name)
+        args = []
+        for name in kernel_arguments:
+            if name in ("band_start", "band_end"):
+                args.append("0")
+            elif name == "task_count":
+                args.append("_count")
+            else:
+                args.append(name)
+        call_args = "(" + ", ".join(args) + ("," if len(args) == 1 else "") + ")"
+        body = []
+        if self.execution_mode == "plain":
+            emitter = self._emitter
+            loop = self._target_loop_cache
+            body.append(f"_tasks = len(range({', '.join(ast.unparse(a) for a in loop.iter.args)}))")
+            body.append(f"_blocks = (_tasks * {self.task_lanes} + "
+                        f"{self.threads_per_block} - 1) // {self.threads_per_block}")
+            body.append(f"_hip.launch({kernel_name!r}, _blocks, "
+                        f"{self.threads_per_block}, {call_args})")
+        elif self.execution_mode == "wavefront":
+            start = kernel_arguments.index("band_start")
+            end = kernel_arguments.index("band_end")
+            body.append(
+                f"_hip.launch_levels({kernel_name!r}, band_ptr, "
+                f"{max(1, self.threads_per_block // self.task_lanes)}, "
+                f"{self.threads_per_block}, {call_args}, {start}, {end})")
+        else:
+            count_array = ("done" if self.dependence_protocol == PULL_DEPENDENCE
+                           else "dep_count")
+            if self.dependence_protocol == PULL_DEPENDENCE:
+                reset_args = "(done, task_counter, _hip.length(done))"
+            else:
+                reset_args = ("(dep_count, initial_dep_count, task_counter, "
+                              "_hip.length(dep_count))")
+            body.append(f"_count = _hip.length({count_array})")
+            body.append(f"_hip.launch({reset_name!r}, (_count + 255) // 256 or 1, "
+                        f"256, {reset_args})")
+            tasks_per_block = max(1, self.threads_per_block // self.task_lanes)
+            body.append(f"_blocks = min((_count + {tasks_per_block} - 1) // "
+                        f"{tasks_per_block}, _hip.resident_blocks({kernel_name!r}, "
+                        f"{self.threads_per_block}))")
+            body.append(f"_hip.launch({kernel_name!r}, max(_blocks, 1), "
+                        f"{self.threads_per_block}, {call_args})")
+        for loop in reversed(self.host_loops):
+            header = (f"for {loop.target.id} in "
+                      f"{ast.unparse(loop.iter)}:")
+            body = [header] + ["    " + line for line in body]
+        text = (f"def {launcher_name}(_hip, " + ", ".join(launcher_arguments)
+                + "):\n" + "\n".join("    " + line for line in body) + "\n")
+        return text, launcher_arguments
+
+
+def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
+                 execution_mode="plain", sync_free_ready_count=0,
+                 wavefront_threads_per_block=128, thread_loop_iterator=None,
+                 thread_unroll_factor=1, n_warp=None,
+                 dependence_protocol=COUNTER_DEPENDENCE, direct_dependence=None,
+                 function_props=None, structural_lookups=(), task_lanes=None,
+                 chain_tasks=False, argument_kinds=None,
+                 spin_limit=DEFAULT_SPIN_LIMIT):
+    """HIP counterpart of ``lower_to_numba_cuda``
+    (compiler/cuda_lowering.py:2854-2884); same parameters plus
+    ``task_lanes`` (lanes cooperating on one task, a power of two <= 64),
+    ``chain_tasks`` (tasks are node sequences, ``band_width > 1``) and
+    ``spin_limit`` (watchdog of the sync-free poll loop)."""
+    lowerer = HIPLowerer(
+        loop_iterator=loop_iterator, reductions=reductions,
+        kernel_name=kernel_name, execution_mode=execution_mode,
+        sync_free_ready_count=sync_free_ready_count,
+        wavefront_threads_per_block=wavefront_threads_per_block,
+        thread_loop_iterator=thread_loop_iterator,
+        thread_unroll_factor=thread_unroll_factor, n_warp=n_warp,
+        dependence_protocol=dependence_protocol,
+        direct_dependence=direct_dependence, function_props=function_props,
+        structural_lookups=structural_lookups, task_lanes=task_lanes,
+        chain_tasks=chain_tasks, argument_kinds=argument_kinds,
+        spin_limit=spin_limit)
+    return lowerer.lower(code)

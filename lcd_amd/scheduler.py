@@ -1,0 +1,631 @@
+"""Schedule space, workload features and the analytic scheduler for MI355X.
+
+Counterpart of compiler/scheduler.py of the reference (space :172-303, cost
+model :306-419, features :422-452, trip-count probe :455-571, fingerprint
+:678-711, machine constants :714-775), re-fitted to CDNA4:
+
+* a wavefront is 64 lanes (``WAVE_SIZE``); ``n_warp`` counts cooperating
+  wavefronts;
+* a thread-mapped task may use a *slice* of a wavefront: ``task_lanes`` is an
+  extra schedule dimension (4..64 lanes), searched when the user fixes neither
+  ``n_warp`` nor ``task_lanes``;
+* the level loop of the wavefront executor is replayed from a hipGraph, so its
+  per-level cost is the measured graph-node cost, not a host launch;
+* the sync-free estimate includes the dependency critical path
+  ``levels * handoff``, the measured cross-workgroup release/acquire latency;
+* machine constants are measured by ``lcdhip_measure_arch`` on the device.
+"""
+
+import ast
+import hashlib
+import itertools
+from collections import deque
+from copy import deepcopy
+from dataclasses import dataclass
+
+import numpy as np
+
+from lcd_amd.dag_codegen import (
+    COUNTER_DEPENDENCE,
+    PULL_DEPENDENCE,
+    PUSH_DEPENDENCE,
+)
+
+WAVEFRONT = "wavefront"
+SYNC_FREE = "sync_free"
+AUTO = "auto"
+EXECUTION_MODES = (WAVEFRONT, SYNC_FREE)
+BLOCK_SIZES = (64, 128, 256, 512)
+UNROLL_FACTORS = (1, 2, 4, 8)
+DEFAULT_THREADS_PER_BLOCK = 128
+N_WARP_CANDIDATES = (1,)
+WAVE_SIZE = 64
+TASK_LANE_CANDIDATES = (4, 8, 16, 32, 64)
+PULL_POLLING_FACTOR = 2.0
+ARITHMETIC_OPERATORS = (ast.Add, ast.Sub, ast.Mult, ast.Div, ast.FloorDiv,
+                        ast.Mod, ast.Pow)
+
+
+class SchedulerError(Exception):
+    pass
+
+
+@dataclass(frozen=True)
+class ArchConstants:
+    launch_latency_s: float
+    atomic_cost_s: float
+    memory_bandwidth_bytes_per_s: float
+    lane_flops_per_s: float
+    handoff_s: float = 0.0        # release -> acquire between workgroups
+    barrier_s: float = 0.0        # one grid barrier of a resident grid
+    graph_node_s: float = 0.0     # one dependent kernel node of a hipGraph
+
+
+# Used when no device is available to measure (MI355X data-sheet scale).
+FALLBACK_ARCH_CONSTANTS = ArchConstants(
+    launch_latency_s=8.0e-6,
+    atomic_cost_s=2.0e-9,
+    memory_bandwidth_bytes_per_s=8.0e12,
+    lane_flops_per_s=2.4e9,
+    handoff_s=1.5e-6,
+    barrier_s=4.0e-6,
+    graph_node_s=2.5e-6,
+)
+
+
+@dataclass(frozen=True)
+class WorkloadFeatures:
+    rows: int
+    edges: int
+    levels: int
+    nonzeros: int
+    flops: float
+    memory_bytes: int
+    thread_work_items: int = 0
+    thread_loop_invocations: int = 0
+
+    @property
+    def average_in_degree(self):
+        return 0.0 if self.rows == 0 else self.edges / self.rows
+
+    @property
+    def average_thread_trip_count(self):
+        if self.thread_loop_invocations == 0:
+            return 0.0
+        return self.thread_work_items / self.thread_loop_invocations
+
+
+@dataclass(frozen=True)
+class CostEstimate:
+    launch_s: float
+    sync_s: float
+    memory_s: float
+    compute_s: float
+
+    @property
+    def total_s(self):
+        return self.launch_s + self.sync_s + self.memory_s + self.compute_s
+
+
+@dataclass(frozen=True)
+class Schedule:
+    execution_mode: str
+    threads_per_block: int
+    thread_unroll: int
+    n_warp: int = 1
+    dependence_protocol: str = COUNTER_DEPENDENCE
+    task_lanes: int = 0           # 0: the default group (a whole wavefront)
+    cost: CostEstimate | None = None
+
+    @property
+    def lowering_key(self):
+        return (self.execution_mode, self.threads_per_block,
+                self.thread_unroll, self.n_warp, self.dependence_protocol,
+                self.task_lanes)
+
+
+@dataclass(frozen=True)
+class SchedulePlan:
+    schedule: Schedule
+    execution_data: object
+    features: WorkloadFeatures | None = None
+    dag: object = None
+
+
+def normalize_execution_mode(execution_mode):
+    if execution_mode is None or execution_mode == AUTO:
+        return None
+    if execution_mode.replace("-", "_") == SYNC_FREE:
+        return SYNC_FREE
+    return WAVEFRONT
+
+
+def task_threads(threads_per_block, n_warp, task_lanes=0):
+    """Lanes that cooperate on one task."""
+    if task_lanes:
+        return task_lanes
+    if threads_per_block % WAVE_SIZE:
+        return threads_per_block
+    return min(threads_per_block, WAVE_SIZE * n_warp)
+
+
+def _wave_task(threads_per_block, n_warp):
+    return n_warp == 1 and threads_per_block % WAVE_SIZE == 0
+
+
+@dataclass(frozen=True)
+class ScheduleSpace:
+    execution_modes: tuple
+    block_sizes: tuple
+    unroll_factors: tuple
+    n_warps: tuple = N_WARP_CANDIDATES
+    thread_mapped: bool = False
+    dependence_protocols: tuple = (COUNTER_DEPENDENCE,)
+    task_lanes: tuple = (0,)
+
+    @classmethod
+    def from_options(cls, execution_mode=None, threads_per_block=None,
+                     thread_unroll=None, thread_mapped=False, n_warp=None,
+                     direct_protocol=None, dependence_protocol=None,
+                     task_lanes=None):
+        mode = normalize_execution_mode(execution_mode)
+        if n_warp is not None and (not isinstance(n_warp, int) or n_warp <= 0):
+            raise SchedulerError("n_warp must be a positive integer.")
+        block_task = n_warp is not None and n_warp > 1
+        if (block_task and threads_per_block is not None
+                and threads_per_block != n_warp * WAVE_SIZE):
+            raise SchedulerError(
+                f"n_warp={n_warp} maps one task to {n_warp * WAVE_SIZE} "
+                f"threads, but threads_per_block={threads_per_block}.")
+        if (n_warp == 1 and thread_mapped and threads_per_block is not None
+                and threads_per_block % WAVE_SIZE):
+            raise SchedulerError(
+                "n_warp=1 requires threads_per_block to be a multiple of "
+                f"{WAVE_SIZE}, but threads_per_block={threads_per_block}.")
+        if task_lanes is not None:
+            if (not isinstance(task_lanes, int) or task_lanes <= 0
+                    or task_lanes & (task_lanes - 1) or task_lanes > WAVE_SIZE):
+                raise SchedulerError(
+                    "task_lanes must be a power of two between 1 and "
+                    f"{WAVE_SIZE}.")
+            if block_task:
+                raise SchedulerError(
+                    "task_lanes cannot be combined with n_warp > 1.")
+        if threads_per_block is not None:
+            block_sizes = (threads_per_block,)
+        elif block_task:
+            block_sizes = (n_warp * WAVE_SIZE,)
+        elif thread_mapped:
+            block_sizes = BLOCK_SIZES
+        else:
+            block_sizes = (DEFAULT_THREADS_PER_BLOCK,)
+        if thread_unroll is not None:
+            unroll_factors = (thread_unroll,)
+        elif thread_mapped:
+            unroll_factors = UNROLL_FACTORS
+        else:
+            unroll_factors = (1,)
+        if not thread_mapped or block_task:
+            lanes = (0,)
+        elif task_lanes is not None:
+            lanes = (task_lanes,)
+        elif n_warp == 1:
+            lanes = (0,)                 # one whole wavefront per task
+        else:
+            lanes = TASK_LANE_CANDIDATES
+        execution_modes = EXECUTION_MODES if mode is None else (mode,)
+        n_warps = N_WARP_CANDIDATES if n_warp is None else (n_warp,)
+        available = (COUNTER_DEPENDENCE,) + (
+            (direct_protocol,)
+            if thread_mapped and direct_protocol is not None else ())
+        searched = (len(execution_modes) * len(block_sizes)
+                    * len(unroll_factors) * len(n_warps) * len(lanes)) > 1
+        if dependence_protocol is not None:
+            if dependence_protocol not in available:
+                raise SchedulerError(
+                    f"Dependence protocol {dependence_protocol!r} is not "
+                    "supported by this loop; available protocols: "
+                    + ", ".join(available) + ".")
+            protocols = (dependence_protocol,)
+        elif PUSH_DEPENDENCE in available:
+            protocols = (PUSH_DEPENDENCE,)
+        elif PULL_DEPENDENCE in available and searched:
+            protocols = (COUNTER_DEPENDENCE, PULL_DEPENDENCE)
+        else:
+            protocols = (COUNTER_DEPENDENCE,)
+        return cls(execution_modes=execution_modes, block_sizes=block_sizes,
+                   unroll_factors=unroll_factors, n_warps=n_warps,
+                   thread_mapped=thread_mapped,
+                   dependence_protocols=protocols, task_lanes=lanes)
+
+    def configurations(self):
+        result = []
+        for mode, block, unroll, n_warp, lanes in itertools.product(
+                self.execution_modes, self.block_sizes, self.unroll_factors,
+                self.n_warps, self.task_lanes):
+            if lanes and block % lanes:
+                continue
+            protocols = (
+                self.dependence_protocols
+                if (mode == SYNC_FREE and self.thread_mapped
+                    and _wave_task(block, n_warp))
+                else (COUNTER_DEPENDENCE,))
+            result.extend((mode, block, unroll, n_warp, protocol, lanes)
+                          for protocol in protocols)
+        return result
+
+    @property
+    def is_fixed(self):
+        return len(self.configurations()) == 1
+
+    def fixed_schedule(self):
+        if not self.is_fixed:
+            raise SchedulerError(
+                "The schedule space has more than one configuration.")
+        return Schedule(*self.configurations()[0])
+
+
+class AnalyticScheduler:
+    def __init__(self, arch_constants=None):
+        self._arch_constants = arch_constants
+
+    @property
+    def arch_constants(self):
+        if self._arch_constants is None:
+            self._arch_constants = measure_arch_constants()
+        return self._arch_constants
+
+    def estimate(self, features, execution_mode, threads_per_block,
+                 thread_unroll, n_warp, thread_mapped,
+                 dependence_protocol=COUNTER_DEPENDENCE, task_lanes=0):
+        arch = self.arch_constants
+        average_in_degree = features.average_in_degree
+        if execution_mode == WAVEFRONT:
+            per_level = arch.graph_node_s or arch.launch_latency_s
+            launch_s = features.levels * per_level
+            sync_s = 0.0
+        elif execution_mode == SYNC_FREE:
+            launch_s = arch.launch_latency_s
+            if dependence_protocol == PUSH_DEPENDENCE:
+                sync_s = arch.atomic_cost_s * features.rows / n_warp
+            elif dependence_protocol == PULL_DEPENDENCE:
+                sync_s = arch.atomic_cost_s * average_in_degree * (
+                    1.0 + PULL_POLLING_FACTOR * features.levels)
+            else:
+                sync_s = arch.atomic_cost_s * (
+                    average_in_degree + features.rows / n_warp)
+            sync_s += features.levels * arch.handoff_s
+        else:
+            raise SchedulerError(f"Unknown execution mode {execution_mode!r}.")
+        lanes = (task_threads(threads_per_block, n_warp, task_lanes)
+                 * thread_unroll if thread_mapped else 1)
+        parallelism = (features.average_thread_trip_count
+                       if thread_mapped and features.thread_loop_invocations
+                       else average_in_degree)
+        active_lanes = min(lanes, max(parallelism, 1.0))
+        return CostEstimate(
+            launch_s=launch_s, sync_s=sync_s,
+            memory_s=features.memory_bytes / arch.memory_bandwidth_bytes_per_s,
+            compute_s=features.flops / (active_lanes * arch.lane_flops_per_s))
+
+    def candidates(self, features, space):
+        return [
+            Schedule(mode, block, unroll, n_warp, protocol, lanes,
+                     cost=self.estimate(features, mode, block, unroll, n_warp,
+                                        space.thread_mapped, protocol, lanes))
+            for mode, block, unroll, n_warp, protocol, lanes
+            in space.configurations()]
+
+    def schedule(self, features, space):
+        return min(self.candidates(features, space), key=_schedule_rank)
+
+
+def _schedule_rank(schedule):
+    return (
+        schedule.cost.total_s,
+        task_threads(schedule.threads_per_block, schedule.n_warp,
+                     schedule.task_lanes) * schedule.thread_unroll,
+        abs(schedule.threads_per_block.bit_length()
+            - DEFAULT_THREADS_PER_BLOCK.bit_length()),
+        schedule.threads_per_block,
+        schedule.n_warp,
+        EXECUTION_MODES.index(schedule.execution_mode),
+        schedule.dependence_protocol,
+    )
+
+
+def extract_workload_features(dag_successors, wavefront_list, argument_values,
+                              function_props=None, flops_per_iteration=1,
+                              thread_trip_counts=None, edges=None):
+    """Features from host lists (reference interface) or, when
+    ``dag_successors`` is an int, from counts the device inspector reports
+    (``dag_successors`` = rows, ``wavefront_list`` = levels, ``edges``)."""
+    if isinstance(dag_successors, (int, np.integer)):
+        rows, levels = int(dag_successors), int(wavefront_list)
+        edges = int(edges or 0)
+    else:
+        rows = len(dag_successors)
+        edges = sum(len(successors) for successors in dag_successors)
+        levels = len(wavefront_list)
+    nonzeros = _nonzeros_from_pointer_arrays(argument_values, function_props)
+    if nonzeros is None:
+        nonzeros = rows + edges
+    if thread_trip_counts is None:
+        work_items = invocations = 0
+    elif isinstance(thread_trip_counts, dict):
+        work_items = int(thread_trip_counts["work_items"])
+        invocations = int(thread_trip_counts["invocations"])
+    else:
+        counts = tuple(max(int(c), 0) for c in thread_trip_counts)
+        work_items, invocations = sum(counts), len(counts)
+    base = nonzeros if thread_trip_counts is None else work_items
+    return WorkloadFeatures(
+        rows=rows, edges=edges, levels=levels, nonzeros=nonzeros,
+        flops=float(flops_per_iteration * base),
+        memory_bytes=_array_bytes(argument_values),
+        thread_work_items=work_items, thread_loop_invocations=invocations)
+
+
+# ---- trip counts of the thread-mapped loop -------------------------------
+
+def compile_thread_trip_counter(function_ast, thread_loop_iterator,
+                                function_globals=None):
+    """Host probe: the user function with the mapped loop replaced by the
+    length of its range (side effects of the loop body removed).  Kept for
+    interface parity; the decorator prefers :func:`segment_trip_counts`."""
+    if thread_loop_iterator is None:
+        return None
+    module = deepcopy(function_ast)
+    functions = [n for n in module.body if isinstance(n, ast.FunctionDef)]
+    if len(functions) != 1:
+        raise SchedulerError(
+            "Thread-loop trip counting requires exactly one function.")
+    function = functions[0]
+    matches = []
+
+    class Counter(ast.NodeTransformer):
+        def visit_For(self, node):
+            if not (isinstance(node.target, ast.Name)
+                    and node.target.id == thread_loop_iterator):
+                return self.generic_visit(node)
+            matches.append(node)
+            if node.orelse:
+                raise SchedulerError(
+                    "Thread-mapped loops with for/else cannot be trip-counted.")
+            if not (isinstance(node.iter, ast.Call)
+                    and isinstance(node.iter.func, ast.Name)
+                    and node.iter.func.id == "range"
+                    and not node.iter.keywords
+                    and 1 <= len(node.iter.args) <= 3):
+                raise SchedulerError(
+                    "Thread-loop trip counting requires a range-based loop.")
+            return ast.parse(
+                f"_lcd_trip_counts.append(len({ast.unparse(node.iter)}))"
+            ).body[0]
+
+        def visit_Return(self, node):
+            return ast.Return(
+                value=ast.Name(id="_lcd_trip_counts", ctx=ast.Load()))
+
+    function.body = [Counter().visit(s) for s in function.body]
+    flat = []
+    for statement in function.body:
+        flat.extend(statement if isinstance(statement, list) else [statement])
+    function.body = flat
+    if not matches:
+        raise SchedulerError(
+            f"Could not find thread-mapped loop {thread_loop_iterator!r}.")
+    if len(matches) > 1:
+        raise SchedulerError(
+            "Thread-loop trip counting requires a unique loop iterator; "
+            f"found {len(matches)} loops named {thread_loop_iterator!r}.")
+    function.name = "_lcd_thread_trip_counter"
+    function.decorator_list = []
+    function.body.insert(0, ast.parse("_lcd_trip_counts = []").body[0])
+    function.body.append(
+        ast.Return(value=ast.Name(id="_lcd_trip_counts", ctx=ast.Load())))
+    module.body = [function]
+    namespace = dict(function_globals or {})
+    exec(compile(ast.fix_missing_locations(module),
+                 "<lcd-thread-trip-counter>", "exec"), namespace)
+    return namespace[function.name]
+
+
+def measure_thread_trip_counts(counter, argument_values, argument_names):
+    """Run a trip-count probe on copies of the mutable arguments."""
+    if counter is None:
+        return None
+    arguments = []
+    for name in argument_names:
+        value = argument_values[name]
+        if isinstance(value, np.ndarray):
+            value = value.copy()
+        elif isinstance(value, (list, dict, set)):
+            value = deepcopy(value)
+        arguments.append(value)
+    return tuple(counter(*arguments))
+
+
+def segment_trip_counts(thread_loop, block_iterator, argument_values):
+    """Trip totals of ``for j in range(P[i] + a, P[i + 1] + b)`` directly
+    from the pointer array (no interpretation of the user loop).  Returns
+    ``None`` when the loop is not of that shape."""
+    from lcd_amd.dependence import _split_offset
+
+    if thread_loop is None or not (
+            isinstance(thread_loop.iter, ast.Call)
+            and len(thread_loop.iter.args) == 2):
+        return None
+    lower, lower_offset = _split_offset(thread_loop.iter.args[0])
+    upper, upper_offset = _split_offset(thread_loop.iter.args[1])
+    if not (isinstance(lower, ast.Subscript) and isinstance(upper, ast.Subscript)
+            and isinstance(lower.value, ast.Name)
+            and isinstance(upper.value, ast.Name)
+            and lower.value.id == upper.value.id
+            and isinstance(lower.slice, ast.Name)
+            and lower.slice.id == block_iterator):
+        return None
+    base, one = _split_offset(upper.slice)
+    if not (isinstance(base, ast.Name) and base.id == block_iterator
+            and one == 1):
+        return None
+    pointers = argument_values.get(lower.value.id)
+    if pointers is None:
+        return None
+    if hasattr(pointers, "copy_to_host"):
+        pointers = pointers.copy_to_host()
+    pointers = np.asarray(pointers, dtype=np.int64)
+    trips = np.maximum(
+        pointers[1:] + upper_offset - pointers[:-1] - lower_offset, 0)
+    return {"work_items": int(trips.sum()), "invocations": int(trips.size)}
+
+
+def pointer_array_names(function_props):
+    return [name for name, properties in (function_props or {}).items()
+            if isinstance(name, str)
+            and "monotonically_increasing" in properties]
+
+
+def _nonzeros_from_pointer_arrays(argument_values, function_props):
+    counts = []
+    for name in pointer_array_names(function_props):
+        value = argument_values.get(name)
+        if value is None:
+            continue
+        if hasattr(value, "copy_to_host"):
+            meta = value.shape
+            if len(meta) == 1 and meta[0] >= 2:
+                ends = value.copy_to_host()
+                counts.append(int(ends[-1]) - int(ends[0]))
+            continue
+        pointers = np.asarray(value)
+        if pointers.ndim == 1 and pointers.size >= 2:
+            counts.append(int(pointers[-1]) - int(pointers[0]))
+    return max(counts) if counts else None
+
+
+def _array_bytes(argument_values):
+    arrays = {}
+    for value in argument_values.values():
+        if isinstance(value, np.ndarray) or hasattr(value, "nbytes"):
+            arrays[id(value)] = value
+    return int(sum(array.nbytes for array in arrays.values()))
+
+
+def count_inner_loop_flops(function_ast, block_iterator,
+                           thread_loop_iterator=None):
+    block_loop = _find_loop(function_ast, block_iterator)
+    if block_loop is None:
+        return 1
+    inner = None
+    if thread_loop_iterator is not None:
+        inner = _find_loop(block_loop, thread_loop_iterator)
+    if inner is None:
+        inner = _deepest_loop(block_loop)
+    counter = _ArithmeticCounter()
+    for statement in inner.body:
+        counter.visit(statement)
+    return max(counter.count, 1)
+
+
+def _find_loop(tree, iterator):
+    for node in ast.walk(tree):
+        if (isinstance(node, ast.For) and isinstance(node.target, ast.Name)
+                and node.target.id == iterator):
+            return node
+    return None
+
+
+def _deepest_loop(loop):
+    best_depth, best = 0, loop
+    pending = deque([(loop, 0)])
+    while pending:
+        node, depth = pending.popleft()
+        for child in ast.iter_child_nodes(node):
+            child_depth = depth + isinstance(child, ast.For)
+            if isinstance(child, ast.For) and child_depth > best_depth:
+                best_depth, best = child_depth, child
+            pending.append((child, child_depth))
+    return best
+
+
+class _ArithmeticCounter(ast.NodeVisitor):
+    def __init__(self):
+        self.count = 0
+
+    def visit_BinOp(self, node):
+        if isinstance(node.op, ARITHMETIC_OPERATORS):
+            self.count += 1
+        self.generic_visit(node)
+
+    def visit_AugAssign(self, node):
+        if isinstance(node.op, ARITHMETIC_OPERATORS):
+            self.count += 1
+        self.visit(node.value)
+
+    def visit_Subscript(self, node):
+        self.visit(node.value)
+
+    def visit_For(self, node):
+        for statement in node.body:
+            self.visit(statement)
+
+
+# ---- plan cache keys -------------------------------------------------------
+
+def inspection_fingerprint(values, content_names, device=None):
+    """Cache key of one sparsity structure: content digests of the structure
+    arrays plus dtype/shape of every array.  Host arrays are hashed with
+    blake2b-128 like the reference; arrays already in HBM are digested on the
+    device (``lcdhip_digest``)."""
+    content = tuple((name, _value_digest(values.get(name), device))
+                    for name in sorted(set(content_names)))
+    shapes = []
+    for name, value in sorted(values.items()):
+        if isinstance(value, np.ndarray):
+            shapes.append((name, value.dtype.str, value.shape))
+        elif hasattr(value, "__cuda_array_interface__"):
+            interface = value.__cuda_array_interface__
+            shapes.append((name, interface["typestr"],
+                           tuple(interface["shape"])))
+    return content, tuple(shapes)
+
+
+def _value_digest(value, device=None):
+    if hasattr(value, "__cuda_array_interface__"):
+        if device is None:
+            from lcd_amd import hip_runtime
+            device = hip_runtime.default_device()
+        interface = value.__cuda_array_interface__
+        return (interface["typestr"], tuple(interface["shape"]),
+                device.digest(value))
+    if isinstance(value, np.ndarray):
+        if value.dtype.hasobject:
+            return object()
+        contiguous = np.ascontiguousarray(value)
+        return (contiguous.dtype.str, contiguous.shape,
+                hashlib.blake2b(contiguous.reshape(-1).view(np.uint8),
+                                digest_size=16).digest())
+    if isinstance(value, (list, tuple)):
+        try:
+            return _value_digest(np.asarray(value), device)
+        except (TypeError, ValueError):
+            return object()
+    if value is None or np.isscalar(value):
+        return type(value).__name__, value
+    return object()
+
+
+def measure_arch_constants(device=None):
+    """Machine constants measured on the GPU (``lcdhip_measure_arch``);
+    data-sheet fallbacks when no device is present."""
+    try:
+        from lcd_amd import hip_runtime
+        if device is None:
+            if not hip_runtime.device_available():
+                return FALLBACK_ARCH_CONSTANTS
+            device = hip_runtime.default_device()
+        measured = device.measure_arch()
+    except Exception:
+        return FALLBACK_ARCH_CONSTANTS
+    return ArchConstants(**measured)

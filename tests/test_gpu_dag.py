@@ -1,0 +1,176 @@
+"""On-device inspector vs the CPU oracle: bit-exact edges, counts, levels."""
+
+import json
+import os
+
+import numpy as np
+import pytest
+
+from lcd_amd import workloads
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden",
+                      "reference_vectors.json")
+
+
+def _check_dag(device, oracle, rule, n, force_kahn=False):
+    expected = oracle.dag_build([rule], n)
+    dag = device.dag_build([rule], n, levels=True, force_kahn=force_kahn)
+    assert dag.n == n
+    assert dag.edges == expected.edges
+    np.testing.assert_array_equal(dag.host("dag_ptr"), expected.dag_ptr)
+    np.testing.assert_array_equal(dag.host("dag_index"), expected.dag_index)
+    np.testing.assert_array_equal(dag.host("dep_count"), expected.dep_count)
+    np.testing.assert_array_equal(dag.host("edge_count"), expected.edge_count)
+    assert dag.levels == expected.levels
+    assert dag.scheduled == expected.scheduled == n
+    np.testing.assert_array_equal(dag.host("level_of"), expected.level_of)
+    np.testing.assert_array_equal(dag.host("wavefronts"), expected.wavefronts)
+    np.testing.assert_array_equal(dag.host("wavefront_ptr"),
+                                  expected.wavefront_ptr)
+    return dag, expected
+
+
+def _rule_for(oracle, work):
+    if work.kind == "sptrsv_csc":
+        return oracle.rule_sptrsv_csc(work.indptr, work.indices)
+    if work.kind == "sptrsv_csr":
+        return oracle.rule_sptrsv_csr(work.indptr, work.indices)
+    return oracle.rule_ilu0_csr(work.indptr, work.indices)
+
+
+SMALL = [
+    ("c1", {}),
+    ("c2", dict(nx=24, ny=20, nz=18)),
+    ("c3", dict(n=30000)),
+    ("c4", dict(nx=96, ny=80)),
+    ("c5", dict(n=50000)),
+]
+
+
+@pytest.mark.parametrize("name,overrides", SMALL)
+@pytest.mark.parametrize("force_kahn", [False, True])
+def test_dag_matches_oracle(device, oracle, name, overrides, force_kahn):
+    if force_kahn and name == "c5":
+        overrides = dict(n=3000)   # one launch per level: keep the chain short
+    work = workloads.configuration(name, **overrides)
+    print("dag", name, overrides, "kahn" if force_kahn else "sweep", flush=True)
+    dag, _ = _check_dag(device, oracle, _rule_for(oracle, work), work.n,
+                        force_kahn)
+    assert dag.level_algorithm == (1 if force_kahn else 2)
+    if "levels" in work.meta and not overrides.get("n"):
+        grid = work.meta.get("grid")
+        if grid is not None and name in ("c1", "c2"):
+            assert dag.levels == sum(grid) - len(grid) + 1
+
+
+def test_golden_vectors(device, oracle):
+    with open(GOLDEN) as handle:
+        golden = json.load(handle)
+    for case in golden["dag_cases"]:
+        maker = getattr(oracle, "rule_" + case["rule"])
+        rule = maker(case["ptr"], case["idx"])
+        dag = device.dag_build([rule], case["n"], levels=True)
+        assert dag.successors() == case["dag"], case["name"]
+        assert dag.host("dep_count").tolist() == case["dep_count"], case["name"]
+        if "dag_ptr" in case:
+            assert dag.host("dag_ptr").tolist() == case["dag_ptr"]
+            assert dag.host("dag_index").tolist() == case["dag_index"]
+        if "wavefronts" in case:
+            assert dag.wavefront_list() == case["wavefronts"], case["name"]
+
+
+def test_random_unsorted_duplicates(device, oracle):
+    """Unsorted segments with repeated entries: set semantics + multiplicity."""
+    rng = np.random.default_rng(7)
+    n = 5000
+    counts = rng.integers(0, 12, n)
+    ptr = np.zeros(n + 1, dtype=np.int32)
+    np.cumsum(counts, out=ptr[1:])
+    idx = rng.integers(0, n, int(ptr[-1])).astype(np.int32)
+    for owner_is_source in (True, False):
+        rule = oracle.make_rule(ptr, idx, owner_is_source,
+                                guard=oracle.GUARD_GREATER)
+        _check_dag(device, oracle, rule, n)
+        _check_dag(device, oracle, rule, n, force_kahn=True)
+
+
+def test_non_topological_ids_use_frontier_levels(device, oracle):
+    """Edges from high to low ids force the frontier algorithm."""
+    rng = np.random.default_rng(11)
+    n = 4000
+    perm = rng.permutation(n)
+    work_ptr, work_idx, _ = workloads.banded_lower_csc(n, 3)
+    # relabel node v as perm[v]: segments stay, endpoints are permuted
+    inverse = np.argsort(perm)
+    order = inverse  # new id k holds old column inverse[k]
+    counts = (work_ptr[1:] - work_ptr[:-1])[order]
+    ptr = np.zeros(n + 1, dtype=np.int32)
+    np.cumsum(counts, out=ptr[1:])
+    idx = np.concatenate([
+        perm[work_idx[work_ptr[c]:work_ptr[c + 1]]] for c in order
+    ]).astype(np.int32)
+    rule = oracle.make_rule(ptr, idx, True, lower_offset=1,
+                            guard=oracle.GUARD_NOT_EQUAL)
+    dag, _ = _check_dag(device, oracle, rule, n)
+    assert not dag.topological_ids and dag.level_algorithm == 1
+
+
+def test_cycle_is_reported(device, oracle):
+    from lcd_amd.dag_preprocessing import (DAGPreprocessingError,
+                                           execution_data_from_device_dag)
+    ptr = np.array([0, 1, 2], dtype=np.int32)
+    idx = np.array([1, 0], dtype=np.int32)
+    rule = oracle.make_rule(ptr, idx, True, guard=oracle.GUARD_NONE)
+    dag = device.dag_build([rule], 2, levels=True)
+    assert dag.scheduled == 0 and dag.levels == 0
+    with pytest.raises(DAGPreprocessingError, match="may contain a cycle"):
+        execution_data_from_device_dag(dag, "wavefront", True)
+
+
+def test_out_of_range_endpoint(device, oracle):
+    from lcd_amd import hip_runtime
+    ptr = np.array([0, 1, 2], dtype=np.int32)
+    idx = np.array([1, 7], dtype=np.int32)
+    rule = oracle.make_rule(ptr, idx, True, guard=oracle.GUARD_NONE)
+    with pytest.raises(hip_runtime.HIPRuntimeError) as info:
+        device.dag_build([rule], 2)
+    assert info.value.code == hip_runtime.ERR_DAG_BOUNDS
+
+
+def test_empty_and_edgeless(device, oracle):
+    ptr = np.zeros(1, dtype=np.int32)
+    idx = np.zeros(0, dtype=np.int32)
+    dag = device.dag_build(
+        [oracle.make_rule(ptr, idx, True, guard=oracle.GUARD_NONE)], 0)
+    assert dag.n == 0 and dag.edges == 0 and dag.levels == 0
+    n = 1000
+    ptr = np.arange(n + 1, dtype=np.int32)
+    idx = np.arange(n, dtype=np.int32)   # diagonal only
+    dag = device.dag_build([oracle.rule_sptrsv_csc(ptr, idx)], n)
+    assert dag.edges == 0 and dag.levels == 1
+    np.testing.assert_array_equal(dag.host("wavefronts"), np.arange(n))
+
+
+def test_lookup_table(device, oracle):
+    from lcd_amd import hip_runtime
+    work = workloads.configuration("c4", nx=64, ny=48)
+    status, expected = oracle.lookup_positions(work.indptr, work.indices)
+    assert status == 0
+    table = device.lookup_build(work.indptr, work.indices).copy_to_host()
+    np.testing.assert_array_equal(table, expected)
+    table = device.lookup_build([0, 2, 3, 5], [0, 2, 0, 1, 2]).copy_to_host()
+    assert table.tolist() == [0, -1, 4]
+    with pytest.raises(hip_runtime.HIPRuntimeError) as info:
+        device.lookup_build([0, 2], [1, 0])
+    assert info.value.code == hip_runtime.ERR_LOOKUP_ORDER
+
+
+def test_digest_is_content_sensitive(device):
+    a = device.to_device(np.arange(10000, dtype=np.int32))
+    b = device.to_device(np.arange(10000, dtype=np.int32))
+    c_host = np.arange(10000, dtype=np.int32)
+    c_host[1234] += 1
+    c = device.to_device(c_host)
+    assert device.digest(a) == device.digest(b)
+    assert device.digest(a) != device.digest(c)

@@ -1,0 +1,297 @@
+"""Parity of the generated HIP executors with the CPU oracle.
+
+Tolerances.  Where the floating-point evaluation order is the sequential
+loop's (one lane per task, ILU0's per-entry updates) the results must be
+bit-identical (device code is compiled with -ffp-contract=off).  Where the
+order differs -- atomic accumulation in CSC SpTRSV, lane-strided partial sums
+with a butterfly reduction in CSR SpTRSV -- the bound is a normwise relative
+error of 1e-12 (max|x - ref| / max|ref|), the north-star tolerance.
+"""
+
+import numpy as np
+import pytest
+
+from lcd_amd import workloads
+from lcd_amd.demo import gauss_seidel, spilu0, sptrsv
+
+pytestmark = pytest.mark.gpu
+TOLERANCE = 1e-12
+
+
+def relative_error(result, expected):
+    scale = float(np.max(np.abs(expected))) or 1.0
+    return float(np.max(np.abs(result - expected))) / scale
+
+
+def solve_and_check(solver, work, expected, exact=False):
+    result = solver(work.indptr, work.indices, work.data, work.rhs, work.n)
+    assert result.shape == expected.shape
+    if exact:
+        np.testing.assert_array_equal(result, expected)
+    else:
+        assert relative_error(result, expected) <= TOLERANCE
+    return result
+
+
+CSC_VARIANTS = [
+    dict(execution_mode="wavefront", threads_per_block=128, task_lanes=4),
+    dict(execution_mode="wavefront", threads_per_block=128, n_warp=1),
+    dict(execution_mode="wavefront", threads_per_block=256, task_lanes=8,
+         thread_unroll=2),
+    dict(execution_mode="sync_free", threads_per_block=128, task_lanes=4),
+    dict(execution_mode="sync_free", threads_per_block=256, task_lanes=8),
+    dict(execution_mode="sync_free", threads_per_block=128, n_warp=1),
+    dict(execution_mode="sync_free", threads_per_block=128, task_lanes=4,
+         dependence_protocol="counter"),
+    dict(execution_mode="wavefront", threads_per_block=128, n_warp=2),
+    dict(execution_mode="sync_free", threads_per_block=128, n_warp=2),
+    dict(),   # scheduler decides
+]
+
+
+@pytest.mark.parametrize("options", CSC_VARIANTS, ids=lambda o: "-".join(
+    f"{k}={v}" for k, v in o.items()) or "auto")
+def test_sptrsv_csc_variants(oracle, options):
+    print("csc", options, flush=True)
+    solver = sptrsv.compile_sptrsv_csc(**options)
+    for name, overrides in (("c1", {}), ("c2", dict(nx=20, ny=18, nz=16)),
+                            ("c5", dict(n=6000))):
+        work = workloads.configuration(name, **overrides)
+        expected = oracle.sptrsv_csc(work.indptr, work.indices, work.data,
+                                     work.rhs, work.n)
+        solve_and_check(solver, work, expected)
+    schedule = solver.current_schedule
+    if "execution_mode" in options:
+        assert schedule.execution_mode == options["execution_mode"]
+    if options.get("execution_mode") == "sync_free" and (
+            "dependence_protocol" not in options
+            and options.get("n_warp", 1) == 1):
+        assert schedule.dependence_protocol == "push"
+
+
+CSR_VARIANTS = [
+    dict(execution_mode="wavefront", threads_per_block=128, task_lanes=8),
+    dict(execution_mode="wavefront", threads_per_block=128, n_warp=1,
+         thread_unroll=4),
+    dict(execution_mode="sync_free", threads_per_block=128, task_lanes=8,
+         dependence_protocol="pull"),
+    dict(execution_mode="sync_free", threads_per_block=128, n_warp=1,
+         dependence_protocol="pull"),
+    dict(execution_mode="sync_free", threads_per_block=128, task_lanes=16,
+         dependence_protocol="counter"),
+    dict(execution_mode="wavefront", threads_per_block=256, n_warp=4),
+    dict(),
+]
+
+
+@pytest.mark.parametrize("options", CSR_VARIANTS, ids=lambda o: "-".join(
+    f"{k}={v}" for k, v in o.items()) or "auto")
+def test_sptrsv_csr_variants(oracle, options):
+    print("csr", options, flush=True)
+    solver = sptrsv.compile_sptrsv_csr(**options)
+    work = workloads.configuration("c3", n=20000)
+    expected = oracle.sptrsv_csr(work.indptr, work.indices, work.data,
+                                 work.rhs, work.n)
+    solve_and_check(solver, work, expected)
+    if options.get("dependence_protocol"):
+        assert (solver.current_schedule.dependence_protocol
+                == options["dependence_protocol"])
+
+
+def test_sptrsv_csr_lane_per_task_is_bit_exact(oracle):
+    """No thread map: each task runs the sequential row loop on one lane."""
+    work = workloads.configuration("c3", n=20000)
+    expected = oracle.sptrsv_csr(work.indptr, work.indices, work.data,
+                                 work.rhs, work.n)
+    solve_and_check(sptrsv.simple_sptrsv_csr, work, expected, exact=True)
+    from lcd_amd import parallel
+    sync_free = parallel(loop="i", function_props=sptrsv.FUNCTION_PROPS_CSR,
+                         execution_mode="sync_free")(sptrsv.sptrsv_csr_loop)
+    solve_and_check(sync_free, work, expected, exact=True)
+
+
+def test_sptrsv_matches_scipy_and_manufactured_solution(oracle):
+    """The reference's own e2e oracle (test_sptrsv_e2e.py:58-69) and its
+    demo's manufactured solution (demo/sptrsv.py:51-52)."""
+    from scipy.sparse import csc_matrix
+    from scipy.sparse.linalg import spsolve_triangular
+    work = workloads.configuration("c2", nx=16, ny=16, nz=16)
+    matrix = csc_matrix((work.data, work.indices, work.indptr),
+                        shape=(work.n, work.n))
+    expected = np.linspace(1.0, 2.0, work.n)
+    rhs = np.asarray(matrix @ expected).ravel()
+    result = sptrsv.simple_sptrsv_csc(work.indptr, work.indices, work.data,
+                                      rhs, work.n)
+    np.testing.assert_allclose(result, expected, rtol=1e-10, atol=1e-12)
+    reference = spsolve_triangular(matrix.tocsr(), rhs, lower=True)
+    np.testing.assert_allclose(result, reference, rtol=1e-10, atol=1e-12)
+
+
+ILU_VARIANTS = [
+    dict(execution_mode="wavefront", threads_per_block=128, thread_unroll=1),
+    dict(execution_mode="wavefront", threads_per_block=128, task_lanes=4),
+    dict(execution_mode="wavefront", threads_per_block=128, task_lanes=8,
+         thread_unroll=2),
+    dict(execution_mode="sync_free", threads_per_block=128, task_lanes=8),
+    dict(execution_mode="sync_free", threads_per_block=128, n_warp=1),
+    dict(execution_mode="wavefront", threads_per_block=128, n_warp=2),
+    dict(execution_mode=None, threads_per_block=None),
+]
+
+
+@pytest.mark.parametrize("options", ILU_VARIANTS, ids=lambda o: "-".join(
+    f"{k}={v}" for k, v in o.items()))
+def test_ilu0_csr_variants(oracle, options):
+    print("ilu0", options, flush=True)
+    factor = spilu0.compile_ilu0_csr(**options)
+    work = workloads.configuration("c4", nx=72, ny=56)
+    expected = oracle.ilu0_csr(work.data, work.indices, work.indptr)
+    original = work.data.copy()
+    result = factor(work.data.copy(), work.indices, work.indptr)
+    np.testing.assert_array_equal(work.data, original)
+    # every entry is updated once per pivot, by one lane, in ascending pivot
+    # order: the evaluation order is the sequential loop's
+    np.testing.assert_array_equal(result, expected)
+    assert len(factor.structural_lookups) == 1
+    assert factor.structural_lookups[0].name in factor.hip_kernel_source
+    assert "for (diag_ptr" not in factor.hip_kernel_source
+
+
+def test_ilu0_dense_pattern_is_lu(oracle):
+    """On a dense pattern ILU0 is LU without pivoting."""
+    rng = np.random.default_rng(5)
+    n = 24
+    dense = rng.uniform(-1, 1, (n, n)) + n * np.eye(n)
+    indptr = np.arange(0, n * n + 1, n, dtype=np.int32)
+    indices = np.tile(np.arange(n, dtype=np.int32), n)
+    factor = spilu0.compile_ilu0_csr(execution_mode="sync_free",
+                                     threads_per_block=128, task_lanes=8)
+    result = factor(dense.ravel().copy(), indices, indptr).reshape(n, n)
+    lower = np.tril(result, -1) + np.eye(n)
+    upper = np.triu(result)
+    np.testing.assert_allclose(lower @ upper, dense, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("variant", ["simple", "full"])
+def test_gauss_seidel_two_sweeps(oracle, variant):
+    from scipy.sparse import csr_matrix
+    work = workloads.configuration("c4", nx=40, ny=32)
+    matrix = csr_matrix((work.data, work.indices, work.indptr),
+                        shape=(work.n, work.n))
+    rng = np.random.default_rng(9)
+    rhs, start = rng.random(work.n), rng.random(work.n)
+    if variant == "simple":
+        from scipy.sparse import tril
+        strict = tril(matrix, -1, format="csr")
+        strict.sort_indices()
+        diagonal = matrix.diagonal()
+        ap = strict.indptr.astype(np.int32)
+        ai = strict.indices.astype(np.int32)
+        expected = oracle.gauss_seidel_csr(ap, ai, strict.data, diagonal, rhs,
+                                           start, work.n, 2)
+        result = gauss_seidel.simple_gauss_seidel_csr(
+            ap, ai, strict.data, diagonal, rhs, start.copy(), work.n, 2)
+        np.testing.assert_array_equal(result, expected)
+    else:
+        lower = csr_matrix(np.tril(matrix.toarray()))
+        lower.sort_indices()
+        ap = lower.indptr.astype(np.int32)
+        ai = lower.indices.astype(np.int32)
+        expected = start.copy()
+        for _ in range(2):
+            for i in range(work.n):
+                sigma, diag = 0.0, 1.0
+                for j in range(ap[i], ap[i + 1]):
+                    if ai[j] == i:
+                        diag = lower.data[j]
+                    else:
+                        sigma += lower.data[j] * expected[ai[j]]
+                expected[i] = (rhs[i] - sigma) / diag
+        result = gauss_seidel.full_gauss_seidel_csr(
+            ap, ai, lower.data, rhs, start.copy(), work.n, 2)
+        np.testing.assert_array_equal(result, expected)
+
+
+def test_edge_cases(oracle):
+    solver = sptrsv.compile_sptrsv_csc(execution_mode="sync_free",
+                                       threads_per_block=128, task_lanes=4)
+    # a single unknown
+    x = solver(np.array([0, 1], dtype=np.int32), np.array([0], dtype=np.int32),
+               np.array([2.0]), np.array([3.0]), 1)
+    assert x.tolist() == [1.5]
+    # diagonal matrix: no edges, one level
+    n = 1000
+    diag = np.linspace(1.0, 2.0, n)
+    rhs = np.arange(n, dtype=np.float64)
+    x = solver(np.arange(n + 1, dtype=np.int32), np.arange(n, dtype=np.int32),
+               diag, rhs, n)
+    np.testing.assert_array_equal(x, rhs / diag)
+    # the same wrapper on a second structure (plan cache) and back
+    first = workloads.configuration("c1")
+    second = workloads.configuration("c2", nx=10, ny=9, nz=8)
+    for work in (first, second, first):
+        expected = oracle.sptrsv_csc(work.indptr, work.indices, work.data,
+                                     work.rhs, work.n)
+        solve_and_check(solver, work, expected)
+    # same structure, new values: the captured graph is replayed
+    for seed in range(3):
+        rhs = np.random.default_rng(seed).random(first.n)
+        expected = oracle.sptrsv_csc(first.indptr, first.indices, first.data,
+                                     rhs, first.n)
+        result = solver(first.indptr, first.indices, first.data, rhs, first.n)
+        assert relative_error(result, expected) <= TOLERANCE
+
+
+def test_device_resident_operands(device, oracle):
+    work = workloads.configuration("c2", nx=20, ny=20, nz=20)
+    expected = oracle.sptrsv_csc(work.indptr, work.indices, work.data,
+                                 work.rhs, work.n)
+    solver = sptrsv.compile_sptrsv_csc(execution_mode="wavefront",
+                                       threads_per_block=128, task_lanes=4)
+    operands = [device.to_device(a) for a in
+                (work.indptr, work.indices, work.data, work.rhs)]
+    call = solver.bind(*operands, work.n)
+    for _ in range(3):
+        call.launch()
+    result = call.result()
+    assert relative_error(result, expected) <= TOLERANCE
+
+
+FULL_SIZE = [("c2", "sptrsv_csc"), ("c4", "ilu0"), ("c3", "sptrsv_csr"),
+             ("c5", "sptrsv_csc")]
+
+
+@pytest.mark.parametrize("name,kind", FULL_SIZE)
+def test_full_size_configurations(oracle, name, kind):
+    """BASELINE.json's sizes: oracle parity and a size-independent property
+    (residual of the solve / L*U == A on the pattern)."""
+    print("full size", name, flush=True)
+    work = workloads.configuration(name)
+    if kind == "ilu0":
+        factor = spilu0.compile_ilu0_csr(execution_mode="wavefront",
+                                         threads_per_block=128, task_lanes=4,
+                                         thread_unroll=1)
+        result = factor(work.data.copy(), work.indices, work.indptr)
+        expected = oracle.ilu0_csr(work.data, work.indices, work.indptr)
+        np.testing.assert_array_equal(result, expected)
+        return
+    if kind == "sptrsv_csc":
+        mode = work.execution_mode
+        solver = sptrsv.compile_sptrsv_csc(execution_mode=mode,
+                                           threads_per_block=256, task_lanes=4
+                                           if name == "c2" else 8)
+        expected = oracle.sptrsv_csc(work.indptr, work.indices, work.data,
+                                     work.rhs, work.n)
+        from scipy.sparse import csc_matrix as sparse
+    else:
+        solver = sptrsv.compile_sptrsv_csr(execution_mode="sync_free",
+                                           threads_per_block=256, task_lanes=16)
+        expected = oracle.sptrsv_csr(work.indptr, work.indices, work.data,
+                                     work.rhs, work.n)
+        from scipy.sparse import csr_matrix as sparse
+    result = solve_and_check(solver, work, expected)
+    matrix = sparse((work.data, work.indices, work.indptr),
+                    shape=(work.n, work.n))
+    residual = np.asarray(matrix @ result).ravel() - work.rhs
+    scale = float(np.max(np.abs(work.rhs)))
+    assert float(np.max(np.abs(residual))) <= 1e-10 * max(scale, 1.0) * 10
