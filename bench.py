@@ -1,0 +1,265 @@
+#!/usr/bin/env python3
+"""Benchmark of the `@parallel` solve path on one MI355X.
+
+A step is one solve (SpTRSV) or one factorisation (ILU0) of a synthetic
+configuration whose operands are already resident in HBM: the lifted output
+is cleared on the device, the executor state is reset, and the generated
+kernels run (all replayed from one hipGraph).  Host/device copies, the DAG
+inspection and hiprtc compilation happen before the timed region and are
+reported separately.
+
+Default workload: configuration 2 of BASELINE.json (SpTRSV-CSC on the lower
+factor of the 3-D 7-point Laplacian, 128^3).  Prints ONE JSON line.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "SpTRSV/SpILU0 solve ms, GFLOP/s, HBM GB/s (% roofline) on 1 MI355X"
+
+
+def build_solver(work, args):
+    from lcd_amd.demo import spilu0, sptrsv
+    options = {}
+    mode = args.mode or work.execution_mode
+    options["execution_mode"] = mode
+    if args.tpb:
+        options["threads_per_block"] = args.tpb
+    if args.lanes:
+        options["task_lanes"] = args.lanes
+    if args.unroll:
+        options["thread_unroll"] = args.unroll
+    if args.protocol:
+        options["dependence_protocol"] = args.protocol
+    if args.level_loop:
+        options["level_loop"] = args.level_loop
+    if work.kind == "sptrsv_csc":
+        return sptrsv.compile_sptrsv_csc(**options)
+    if work.kind == "sptrsv_csr":
+        return sptrsv.compile_sptrsv_csr(**options)
+    options.setdefault("thread_unroll", 1)
+    return spilu0.compile_ilu0_csr(**options)
+
+
+def cpu_baseline(work, seconds):
+    """The C restatement of the reference loop (oracle) on one host core."""
+    from oracle import lcd_oracle
+    lcd_oracle.lib()
+    runs, elapsed = 0, 0.0
+    start = time.perf_counter()
+    while True:
+        if work.kind == "sptrsv_csc":
+            lcd_oracle.sptrsv_csc(work.indptr, work.indices, work.data,
+                                  work.rhs, work.n)
+        elif work.kind == "sptrsv_csr":
+            lcd_oracle.sptrsv_csr(work.indptr, work.indices, work.data,
+                                  work.rhs, work.n)
+        else:
+            lcd_oracle.ilu0_csr(work.data, work.indices, work.indptr)
+        runs += 1
+        elapsed = time.perf_counter() - start
+        if elapsed >= seconds or runs >= 1000:
+            break
+    per_solve = elapsed / runs
+    return {
+        "value": round(work.algorithmic_bytes / per_solve / 1e9, 3),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "solve_ms": round(per_solve * 1e3, 3),
+        "sample": f"{runs} full solves of {work.name} by the single-threaded "
+                  "C restatement (gcc -O2, no FMA) of the reference loop",
+        "host_cores_available": os.cpu_count(),
+    }
+
+
+def python_loop_baseline(work, rows):
+    """The undecorated Python loop on the leading ``rows`` tasks."""
+    from oracle import lcd_oracle
+    rows = min(rows, work.n)
+    ptr = work.indptr[:rows + 1].tolist()
+    if work.kind != "sptrsv_csc":
+        return None
+    idx, val, rhs = work.indices.tolist(), work.data.tolist(), work.rhs.tolist()
+    x = [0.0] * work.n
+    start = time.perf_counter()
+    for i in range(rows):
+        x[i] = (rhs[i] - x[i]) / val[ptr[i]]
+        for j in range(ptr[i] + 1, ptr[i + 1]):
+            x[idx[j]] += val[j] * x[i]
+    elapsed = time.perf_counter() - start
+    del lcd_oracle
+    return {"rows": rows, "seconds": round(elapsed, 4),
+            "projected_full_solve_ms": round(elapsed / rows * work.n * 1e3, 1),
+            "note": "CPython list-based restatement of the README loop, "
+                    "one core; numba is not installed on this image"}
+
+
+def main():
+    parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--config", default="c2",
+                        choices=["c1", "c2", "c3", "c4", "c5"])
+    parser.add_argument("--mode", default=None)
+    parser.add_argument("--tpb", type=int, default=None)
+    parser.add_argument("--lanes", type=int, default=None)
+    parser.add_argument("--unroll", type=int, default=None)
+    parser.add_argument("--protocol", default=None)
+    parser.add_argument("--level-loop", dest="level_loop", default=None)
+    parser.add_argument("--cpu-seconds", type=float, default=5.0)
+    parser.add_argument("--no-cpu", action="store_true")
+    parser.add_argument("--no-check", action="store_true")
+    parser.add_argument("--arch", action="store_true",
+                        help="also report measured machine constants")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this path (one sparse triangular "
+              "DAG) runs on a single MI355X; --gpus must be 1.",
+              file=sys.stderr)
+        return 2
+
+    from lcd_amd import hip_runtime, workloads
+    device = hip_runtime.default_device()
+    t0 = time.perf_counter()
+    work = workloads.configuration(args.config)
+    generate_s = time.perf_counter() - t0
+
+    solver = build_solver(work, args)
+    t0 = time.perf_counter()
+    if work.kind == "ilu0_csr":
+        pristine = device.to_device(work.data)
+        operands = [device.to_device(work.data),
+                    device.to_device(work.indices),
+                    device.to_device(work.indptr)]
+        scalars = []
+    else:
+        operands = [device.to_device(a) for a in
+                    (work.indptr, work.indices, work.data, work.rhs)]
+        scalars = [work.n]
+    upload_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    call = solver.bind(*operands, *scalars)
+    device.synchronize()
+    inspect_s = time.perf_counter() - t0
+    schedule = solver.current_schedule
+    plan = solver.schedule_plan(*operands, *scalars)
+
+    def step():
+        if work.kind == "ilu0_csr":
+            device.copy(operands[0], pristine)   # factorisation is in place
+        call.launch()
+
+    t0 = time.perf_counter()
+    step()
+    call.synchronize()
+    first_call_s = time.perf_counter() - t0
+    for _ in range(args.warmup):
+        step()
+    call.synchronize()
+    start, stop = device.event(), device.event()
+    device.record(start)
+    for _ in range(args.steps):
+        step()
+    device.record(stop)
+    elapsed_ms = device.elapsed_ms(start, stop)
+    call.synchronize()
+    ms_per_step = elapsed_ms / args.steps
+
+    launches_per_step = plan.dag.levels if schedule.execution_mode == "wavefront" \
+        and not getattr(solver.hip_lowering, "single_launch", False) else 1
+    gbps = work.algorithmic_bytes / (ms_per_step * 1e-3) / 1e9
+    result = {
+        "metric": METRIC,
+        "value": round(gbps, 3),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64",
+        "data": "synthetic",
+        "config": {
+            "workload": work.name, "kind": work.kind, "n": work.n,
+            "nnz": work.nnz, "levels": plan.dag.levels,
+            "dag_edges": plan.dag.edges, "seed": work.seed,
+            "execution_mode": schedule.execution_mode,
+            "threads_per_block": schedule.threads_per_block,
+            "task_lanes": solver.hip_lowering.task_lanes,
+            "thread_unroll": schedule.thread_unroll,
+            "dependence_protocol": solver.hip_lowering.dependence_protocol,
+        },
+        "solve_ms": round(ms_per_step, 5),
+        "roofline_pct": round(100.0 * gbps / HBM_PEAK_GBPS, 3),
+        "algorithmic_bytes": work.algorithmic_bytes,
+        "setup": {
+            "generate_s": round(generate_s, 3), "upload_s": round(upload_s, 3),
+            "inspect_compile_bind_s": round(inspect_s, 3),
+            "first_call_s": round(first_call_s, 4),
+        },
+    }
+    if work.true_flops is not None:
+        result["gflops"] = round(work.true_flops / (ms_per_step * 1e-3) / 1e9, 3)
+    result["gflops_reference_formula"] = round(
+        work.reference_style_flops / (ms_per_step * 1e-3) / 1e9, 3)
+
+    kernel_ms = ms_per_step / launches_per_step
+    bytes_per_launch = work.algorithmic_bytes / launches_per_step
+    achieved = bytes_per_launch / (kernel_ms * 1e-3) / 1e9
+    result["roofline"] = {
+        "bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBPS,
+        "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 6),
+        "traffic": None,
+        "kernel": solver.hip_lowering.kernel_name,
+        "launches_per_step": launches_per_step,
+        "avg_launch_ms": round(kernel_ms, 6),
+        "dependency_levels": plan.dag.levels,
+    }
+
+    if not args.no_check:
+        from oracle import lcd_oracle
+        if work.kind == "sptrsv_csc":
+            expected = lcd_oracle.sptrsv_csc(work.indptr, work.indices,
+                                             work.data, work.rhs, work.n)
+            got = call.result()
+        elif work.kind == "sptrsv_csr":
+            expected = lcd_oracle.sptrsv_csr(work.indptr, work.indices,
+                                             work.data, work.rhs, work.n)
+            got = call.result()
+        else:
+            expected = lcd_oracle.ilu0_csr(work.data, work.indices,
+                                           work.indptr)
+            call.synchronize()
+            got = operands[0].copy_to_host()
+        error = float(np.max(np.abs(got - expected))) / float(
+            np.max(np.abs(expected)))
+        result["max_rel_error_vs_oracle"] = error
+        if error > 1e-12:
+            print(f"parity check failed: {error}", file=sys.stderr)
+            return 1
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(work, args.cpu_seconds)
+        python_loop = python_loop_baseline(work, 200_000)
+        if python_loop is not None:
+            result["cpu_python_loop"] = python_loop
+    if args.arch:
+        result["arch_constants"] = device.measure_arch()
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
