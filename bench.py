@@ -40,8 +40,10 @@ def build_solver(work, args):
         options["thread_unroll"] = args.unroll
     if args.protocol:
         options["dependence_protocol"] = args.protocol
-    if args.level_loop:
-        options["level_loop"] = args.level_loop
+    if args.waves_per_cu:
+        options["resident_waves_per_cu"] = args.waves_per_cu
+    if args.spin_sleep is not None:
+        options["spin_sleep"] = args.spin_sleep
     if work.kind == "sptrsv_csc":
         return sptrsv.compile_sptrsv_csc(**options)
     if work.kind == "sptrsv_csr":
@@ -116,7 +118,10 @@ def main():
     parser.add_argument("--lanes", type=int, default=None)
     parser.add_argument("--unroll", type=int, default=None)
     parser.add_argument("--protocol", default=None)
-    parser.add_argument("--level-loop", dest="level_loop", default=None)
+    parser.add_argument("--waves-per-cu", dest="waves_per_cu", type=int,
+                        default=None)
+    parser.add_argument("--spin-sleep", dest="spin_sleep", type=int,
+                        default=None)
     parser.add_argument("--cpu-seconds", type=float, default=5.0)
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-check", action="store_true")

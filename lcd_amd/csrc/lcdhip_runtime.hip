@@ -706,8 +706,8 @@ __global__ void lcdhip_handoff_probe_kernel(int32_t *flag, int32_t hops,
                 return;
             }
         }
-        __atomic_thread_fence(__ATOMIC_ACQUIRE);
-        __atomic_thread_fence(__ATOMIC_RELEASE);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         __hip_atomic_store(flag, hop + 1, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -720,7 +720,7 @@ __global__ void lcdhip_barrier_probe_kernel(int32_t *arrive, int32_t rounds,
     for (int32_t round = 0; round < rounds; ++round) {
         __syncthreads();
         if (threadIdx.x == 0) {
-            __atomic_thread_fence(__ATOMIC_RELEASE);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
             __hip_atomic_fetch_add(&arrive[round], 1, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
             int64_t spins = 0;
@@ -733,7 +733,7 @@ __global__ void lcdhip_barrier_probe_kernel(int32_t *arrive, int32_t rounds,
                     break;
                 }
             }
-            __atomic_thread_fence(__ATOMIC_ACQUIRE);
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         }
         __syncthreads();
     }

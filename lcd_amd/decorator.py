@@ -186,6 +186,8 @@ def parallel(**kwargs):
                     structural_lookups=structural_lookups,
                     task_lanes=task_lanes or None,
                     chain_tasks=band_width != 1,
+                    resident_waves_per_cu=kwargs.get("resident_waves_per_cu"),
+                    spin_sleep=kwargs.get("spin_sleep", 1),
                 )
             return lowered_variants[lowering_key]
 

@@ -563,8 +563,8 @@ template <class T, class V> __device__ __forceinline__ void lcd_atomic_xor(T* p,
 __device__ __forceinline__ int lcd_load_relaxed(const int* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, LCD_AGENT);
 }
-__device__ __forceinline__ void lcd_release_fence() { __atomic_thread_fence(__ATOMIC_RELEASE); }
-__device__ __forceinline__ void lcd_acquire_fence() { __atomic_thread_fence(__ATOMIC_ACQUIRE); }
+__device__ __forceinline__ void lcd_release_fence() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
+__device__ __forceinline__ void lcd_acquire_fence() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
 // Sum over the LCD_TASK_LANES lanes of one task group (xor butterfly: every
 // lane ends with the total, the compiler lowers the fixed masks to DPP).
 __device__ __forceinline__ double lcd_group_sum(double v) {
@@ -651,7 +651,10 @@ class HIPLowerer:
                  dependence_protocol=COUNTER_DEPENDENCE, direct_dependence=None,
                  function_props=None, structural_lookups=(), task_lanes=None,
                  chain_tasks=False, argument_kinds=None,
-                 spin_limit=DEFAULT_SPIN_LIMIT):
+                 spin_limit=DEFAULT_SPIN_LIMIT, resident_waves_per_cu=None,
+                 spin_sleep=1):
+        self.resident_waves_per_cu = resident_waves_per_cu
+        self.spin_sleep = spin_sleep
         self.loop_iterator = loop_iterator
         self.thread_loop_iterator = thread_loop_iterator
         self.reductions = _normalize_reductions(reductions)
@@ -1196,6 +1199,8 @@ class HIPLowerer:
             "#ifndef LCD_SPIN_LIMIT",
             f"#define LCD_SPIN_LIMIT {self.spin_limit}", "#endif",
             f"#define LCD_READY_COUNT {self.sync_free_ready_count}",
+            "#ifndef LCD_SPIN_SLEEP",
+            f"#define LCD_SPIN_SLEEP {self.spin_sleep}", "#endif",
         ]
         for name, kind in array_arguments.items():
             default = "int" if kind == INT else "double"
@@ -1350,7 +1355,7 @@ class HIPLowerer:
                 "            long long _spins = 0;",
                 "            int _ok = 1;",
                 f"            while (lcd_load_relaxed(&dep_count[{it}]) != LCD_READY_COUNT) {{",
-                "                __builtin_amdgcn_s_sleep(1);",
+                "                __builtin_amdgcn_s_sleep(LCD_SPIN_SLEEP);",
                 "                if (++_spins > LCD_SPIN_LIMIT || ((_spins & 255) == 0 && "
                 f"lcd_load_relaxed(&{STATUS_ARGUMENT}[0]) != 0)) {{",
                 f"                    {STATUS_ARGUMENT}[0] = 1;",
@@ -1416,7 +1421,7 @@ class HIPLowerer:
         lines += [
             "                    _pending = false;",
             "                } else {",
-            "                    __builtin_amdgcn_s_sleep(1);",
+            "                    __builtin_amdgcn_s_sleep(LCD_SPIN_SLEEP);",
             "                    if (++_spins > LCD_SPIN_LIMIT || ((_spins & 255) == 0 && "
             f"lcd_load_relaxed(&{STATUS_ARGUMENT}[0]) != 0)) {{",
             f"                        {STATUS_ARGUMENT}[0] = 1;",
@@ -1523,7 +1528,7 @@ class HIPLowerer:
             tasks_per_block = max(1, self.threads_per_block // self.task_lanes)
             body.append(f"_blocks = min((_count + {tasks_per_block} - 1) // "
                         f"{tasks_per_block}, _hip.resident_blocks({kernel_name!r}, "
-                        f"{self.threads_per_block}))")
+                        f"{self.threads_per_block}, {self.resident_waves_per_cu!r}))")
             body.append(f"_hip.launch({kernel_name!r}, max(_blocks, 1), "
                         f"{self.threads_per_block}, {call_args})")
         for loop in reversed(self.host_loops):
@@ -1542,7 +1547,8 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
                  dependence_protocol=COUNTER_DEPENDENCE, direct_dependence=None,
                  function_props=None, structural_lookups=(), task_lanes=None,
                  chain_tasks=False, argument_kinds=None,
-                 spin_limit=DEFAULT_SPIN_LIMIT):
+                 spin_limit=DEFAULT_SPIN_LIMIT, resident_waves_per_cu=None,
+                 spin_sleep=1):
     """HIP counterpart of ``lower_to_numba_cuda``
     (compiler/cuda_lowering.py:2854-2884); same parameters plus
     ``task_lanes`` (lanes cooperating on one task, a power of two <= 64),
@@ -1559,5 +1565,6 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
         direct_dependence=direct_dependence, function_props=function_props,
         structural_lookups=structural_lookups, task_lanes=task_lanes,
         chain_tasks=chain_tasks, argument_kinds=argument_kinds,
-        spin_limit=spin_limit)
+        spin_limit=spin_limit, resident_waves_per_cu=resident_waves_per_cu,
+        spin_sleep=spin_sleep)
     return lowerer.lower(code)

@@ -689,8 +689,16 @@ class LaunchContext:
             return int(device_array_meta(array)[0][0])
         return len(array)
 
-    def resident_blocks(self, name, block):
-        return self.device.resident_blocks(self.module.kernel(name), block)
+    def resident_blocks(self, name, block, waves_per_cu=None):
+        """Size of a persistent grid: every workgroup must be resident.
+        ``waves_per_cu`` caps it below what occupancy allows."""
+        blocks = self.device.resident_blocks(self.module.kernel(name), block)
+        if waves_per_cu:
+            waves_per_block = max(1, (block + 63) // 64)
+            cap = (self.device.props.compute_units * int(waves_per_cu)
+                   + waves_per_block - 1) // waves_per_block
+            blocks = min(blocks, max(cap, 1))
+        return blocks
 
     def launch(self, name, grid, block, args):
         self.device.launch(self.module.kernel(name), grid, block, args)
@@ -1011,7 +1019,7 @@ def launch_hip_call(compiled_module, lowering, prepared_arguments,
     prepared = prepared_arguments
     device = prepared.device
     module = prepared.module
-    if module is None:
+    if module is None and hasattr(device, "load_module"):
         module = _load_for_values(compiled_module, lowering, prepared.values,
                                   device)
         prepared.module = module

@@ -1,0 +1,560 @@
+"""Host-side logic that needs no GPU: preprocessing, scheduling, lookup
+plans, dependence analysis, lowering structure, and the C-ABI surface."""
+
+import ast
+import ctypes
+import json
+import os
+import re
+
+import numpy as np
+import pytest
+
+from lcd_amd import dag_preprocessing as P
+from lcd_amd import hip_runtime, scheduler as S
+from lcd_amd.dag_codegen import (DAGCodegenError, create_dag_plan,
+                                 direct_dependence, generate_dag_source)
+from lcd_amd.dependence import (DependenceAnalysisError, SegmentRule,
+                                analyze_dependences)
+from lcd_amd.hip_lowering import (HIPLoweringError, UnsupportedAtomicOperation,
+                                  lower_to_hip)
+from lcd_amd.structural_lookups import (create_structural_lookup_plan,
+                                        rewrite_structural_lookups)
+from oracle import lcd_oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GOLDEN = json.load(open(os.path.join(ROOT, "tests", "golden",
+                                     "reference_vectors.json")))
+
+CSC_PROPS = {"Ap": ["monotonically_increasing"], "Ai": [],
+             ("Ap", "Ai"): ["triangularity"]}
+ILU_PROPS = {"A_indptr": ["monotonically_increasing"], "A_indices": [],
+             ("A_indptr", "A_indices"): [
+                 ("segmented_monotonically_increasing", "n")]}
+
+
+def demo_source(module, name):
+    path = os.path.join(ROOT, "lcd_amd", "demo", module + ".py")
+    tree = ast.parse(open(path).read())
+    function = next(n for n in tree.body
+                    if isinstance(n, ast.FunctionDef) and n.name == name)
+    function.decorator_list = []
+    return ast.Module(body=[function], type_ignores=[])
+
+
+# ---------------------------------------------------------------- C ABI
+
+def test_library_exports_every_declared_symbol():
+    header = open(os.path.join(ROOT, "include", "lcdhip.h")).read()
+    declared = set(re.findall(r"\b(lcdhip_[a-z0-9_]+)\s*\(", header))
+    assert len(declared) >= 40
+    library = ctypes.CDLL(hip_runtime.LIBRARY_PATH)
+    for name in sorted(declared):
+        assert hasattr(library, name), name
+    assert declared == set(hip_runtime.EXPORTED_SYMBOLS)
+    library.lcdhip_version.restype = ctypes.c_char_p
+    assert b"gfx950" in library.lcdhip_version()
+
+
+def test_compute_entry_points_fail_loudly_without_init():
+    library = hip_runtime.load_library()
+    if hip_runtime.device_available():
+        pytest.skip("a GPU is present")
+    pointer = ctypes.c_void_p()
+    assert library.lcdhip_init(0) == hip_runtime.ERR_NO_DEVICE
+    assert library.lcdhip_buffer_alloc(ctypes.c_size_t(16),
+                                       ctypes.byref(pointer)) != 0
+    assert b"lcdhip_init" in library.lcdhip_last_error()
+    with pytest.raises(hip_runtime.HIPRuntimeError):
+        hip_runtime.HIPDevice(0)
+
+
+def test_hiprtc_reports_compile_errors():
+    with pytest.raises(hip_runtime.HIPModuleCompilationError, match="error"):
+        hip_runtime.compile_code('extern "C" __global__ void k() { oops; }')
+
+
+# ------------------------------------------------------- preprocessing
+
+def test_preprocess_known_answers():
+    case = GOLDEN["dag_cases"][1]
+    data = P.preprocess_dag_output(case["dag"], case["dep_count"], "sync_free")
+    assert data.dep_count.tolist() == case["dep_count"]
+    assert data.dag_ptr.tolist() == case["dag_ptr"]
+    assert data.dag_index.tolist() == case["dag_index"]
+    assert data.dag_ptr.dtype == np.int32
+    case = GOLDEN["dag_cases"][2]
+    assert P.wavefronts_from_dag(case["dag"], case["dep_count"]) == (
+        case["wavefronts"])
+    data = P.preprocess_dag_output(case["dag"], case["wavefronts"],
+                                   "wavefront")
+    assert data.wavefronts.tolist() == case["wavefronts_flat"]
+    assert data.wavefront_ptr.tolist() == case["wavefront_ptr"]
+    with pytest.raises(P.DAGPreprocessingError, match="may contain a cycle"):
+        P.preprocess_dag_output(GOLDEN["cyclic_dag"]["successors"], [],
+                                "wavefront")
+    with pytest.raises(P.DAGPreprocessingError, match="out of bounds"):
+        P.compact_successors([[5]])
+    with pytest.raises(P.DAGPreprocessingError, match="negative"):
+        P.preprocess_sync_free([[1], []], [0, -1])
+    with pytest.raises(P.DAGPreprocessingError, match="more than one"):
+        P.preprocess_wavefront([[1], []], [[0], [0, 1]])
+    with pytest.raises(P.DAGPreprocessingError, match="Unknown execution"):
+        P.preprocess_dag_output([[]], [0], "eager")
+
+
+def test_warp_tasks_and_band_chains_match_oracle():
+    from lcd_amd import workloads
+    work = workloads.configuration("c2", nx=5, ny=4, nz=4)
+    dag = O.dag_build([O.rule_sptrsv_csc(work.indptr, work.indices)], work.n)
+    successors, levels = dag.successors(), dag.wavefront_list()
+    assert P.wavefronts_from_dag(successors, dag.dep_count.tolist()) == levels
+    data = P.preprocess_warp_tasks(successors, levels)
+    assert data.task_nodes.tolist() == dag.wavefronts.tolist()
+    assert data.task_ptr.tolist() == list(range(work.n + 1))
+    assert data.band_ptr.tolist() == dag.wavefront_ptr.tolist()
+    assert data.dep_count.tolist() == dag.dep_count.tolist()
+    pushed = P.preprocess_warp_tasks(successors, levels,
+                                     edge_count=dag.edge_count)
+    assert pushed.dep_count.tolist() == dag.edge_count.tolist()
+    for band_width in (2, 3):
+        data = P.preprocess_warp_tasks(successors, levels, band_width)
+        nodes, ptr, bands = dag.band_chains(band_width)
+        assert data.task_nodes.tolist() == nodes.tolist()
+        assert data.task_ptr.tolist() == ptr.tolist()
+        assert data.band_ptr.tolist() == bands.tolist()
+    with pytest.raises(P.DAGPreprocessingError, match="positive integer"):
+        P.preprocess_warp_tasks(successors, levels, 0)
+    merged = P.attach_auxiliary_values(data, {"table": np.arange(3)})
+    assert "table" in merged.auxiliary_values
+    with pytest.raises(P.DAGPreprocessingError, match="Duplicate"):
+        P.attach_auxiliary_values(merged, {"table": np.arange(3)})
+
+
+# ------------------------------------------------------------ scheduler
+
+def test_trip_counter_follows_outer_breaks():
+    source = """
+def update(data, indices, indptr):
+    n = len(indptr) - 1
+    for i in range(n):
+        row_end = indptr[i + 1]
+        for k_ptr in range(indptr[i], row_end):
+            if indices[k_ptr] >= i:
+                break
+            data[k_ptr] /= data[indptr[indices[k_ptr]]]
+            for j_ptr in range(k_ptr + 1, row_end):
+                data[j_ptr] -= data[k_ptr]
+    return data
+"""
+    case = GOLDEN["trip_count_case"]
+    counter = S.compile_thread_trip_counter(ast.parse(source), "j_ptr")
+    data = np.asarray(case["data"])
+    original = data.copy()
+    counts = S.measure_thread_trip_counts(
+        counter,
+        {"data": data, "indices": np.asarray(case["indices"]),
+         "indptr": np.asarray(case["indptr"])},
+        ("data", "indices", "indptr"))
+    assert counts == tuple(case["counts"])
+    np.testing.assert_array_equal(data, original)
+    with pytest.raises(S.SchedulerError, match="Could not find"):
+        S.compile_thread_trip_counter(ast.parse(source), "missing")
+
+
+def test_workload_features_and_unroll_choice():
+    features = S.extract_workload_features(
+        dag_successors=[[], [], []], wavefront_list=[[0, 1, 2]],
+        argument_values={}, flops_per_iteration=2,
+        thread_trip_counts=(1, 2, 1))
+    assert features.thread_work_items == 4
+    assert features.thread_loop_invocations == 3
+    assert features.average_thread_trip_count == pytest.approx(4 / 3)
+    assert features.flops == 8.0
+    assert S.UNROLL_FACTORS == (1, 2, 4, 8)
+    zero_latency = S.ArchConstants(0.0, 0.0, 1.0e30, 1.0)
+    engine = S.AnalyticScheduler(zero_latency)
+    space = S.ScheduleSpace.from_options(
+        execution_mode=S.WAVEFRONT, threads_per_block=128, thread_mapped=True,
+        n_warp=1)
+
+    def work(items):
+        return S.WorkloadFeatures(rows=10, edges=0, levels=1, nonzeros=items,
+                                  flops=float(items), memory_bytes=0,
+                                  thread_work_items=items,
+                                  thread_loop_invocations=10)
+
+    # the reference's vector is stated for 32-lane warps: 16 vs 48 iterations
+    # per task give unroll 1 vs 2.  A task group here is a 64-lane wavefront,
+    # so the same rule flips at twice the trip count.
+    assert engine.schedule(work(160), space).thread_unroll == 1
+    assert engine.schedule(work(480), space).thread_unroll == 1
+    assert engine.schedule(work(960), space).thread_unroll == 2
+    reference_group = S.ScheduleSpace.from_options(
+        execution_mode=S.WAVEFRONT, threads_per_block=128, thread_mapped=True,
+        task_lanes=32)
+    assert engine.schedule(work(160), reference_group).thread_unroll == 1
+    assert engine.schedule(work(480), reference_group).thread_unroll == 2
+
+
+def test_schedule_space_rules():
+    space = S.ScheduleSpace.from_options(thread_mapped=True,
+                                         direct_protocol="push")
+    configurations = space.configurations()
+    assert {c[0] for c in configurations} == {"wavefront", "sync_free"}
+    assert all(c[4] == "push" for c in configurations if c[0] == "sync_free")
+    assert all(c[4] == "counter" for c in configurations if c[0] == "wavefront")
+    assert {c[5] for c in configurations} == set(S.TASK_LANE_CANDIDATES)
+    fixed = S.ScheduleSpace.from_options(
+        execution_mode="wavefront", threads_per_block=128)
+    assert fixed.is_fixed
+    assert fixed.fixed_schedule().lowering_key == (
+        "wavefront", 128, 1, 1, "counter", 0)
+    pulled = S.ScheduleSpace.from_options(thread_mapped=True,
+                                          direct_protocol="pull")
+    assert set(pulled.dependence_protocols) == {"counter", "pull"}
+    with pytest.raises(S.SchedulerError, match="n_warp=2"):
+        S.ScheduleSpace.from_options(n_warp=2, threads_per_block=64,
+                                     thread_mapped=True)
+    with pytest.raises(S.SchedulerError, match="multiple of 64"):
+        S.ScheduleSpace.from_options(n_warp=1, threads_per_block=96,
+                                     thread_mapped=True)
+    with pytest.raises(S.SchedulerError, match="not supported"):
+        S.ScheduleSpace.from_options(thread_mapped=True,
+                                     dependence_protocol="push")
+    with pytest.raises(S.SchedulerError, match="positive integer"):
+        S.ScheduleSpace.from_options(n_warp=0)
+
+
+def test_cost_model_terms():
+    arch = S.ArchConstants(1e-5, 2e-9, 1e12, 1.5e9, handoff_s=5e-7,
+                           graph_node_s=2e-6)
+    engine = S.AnalyticScheduler(arch)
+    features = S.WorkloadFeatures(rows=1000, edges=3000, levels=10,
+                                  nonzeros=4000, flops=8000.0,
+                                  memory_bytes=10**6)
+    wave = engine.estimate(features, "wavefront", 128, 1, 1, False)
+    assert wave.launch_s == pytest.approx(10 * 2e-6) and wave.sync_s == 0.0
+    assert wave.memory_s == pytest.approx(1e-6)
+    assert wave.compute_s == pytest.approx(8000 / 1.5e9)
+    push = engine.estimate(features, "sync_free", 128, 1, 1, True, "push")
+    assert push.sync_s == pytest.approx(2e-9 * 1000 + 10 * 5e-7)
+    pull = engine.estimate(features, "sync_free", 128, 1, 1, True, "pull")
+    assert pull.sync_s == pytest.approx(2e-9 * 3.0 * 21.0 + 10 * 5e-7)
+    counter = engine.estimate(features, "sync_free", 128, 1, 2, True)
+    assert counter.sync_s == pytest.approx(2e-9 * (3.0 + 500) + 10 * 5e-7)
+    with pytest.raises(S.SchedulerError):
+        engine.estimate(features, "eager", 128, 1, 1, False)
+
+
+def test_fingerprint_and_flops():
+    a = np.arange(10, dtype=np.int32)
+    values = {"Ap": a, "Ai": a.copy(), "Ax": np.ones(3), "n": 9}
+    first = S.inspection_fingerprint(values, ["Ap", "Ai"])
+    values["Ax"] = np.zeros(3)
+    assert S.inspection_fingerprint(values, ["Ap", "Ai"]) == first
+    values["Ai"] = a[::-1].copy()
+    assert S.inspection_fingerprint(values, ["Ap", "Ai"]) != first
+    module = demo_source("sptrsv", "sptrsv_csc_loop")
+    assert S.count_inner_loop_flops(module, "i", "j") == 2
+    loop = next(n for n in ast.walk(module) if isinstance(n, ast.For)
+                and n.target.id == "j")
+    trips = S.segment_trip_counts(loop, "i", {"Ap": np.array([0, 3, 4, 9])})
+    assert trips == {"work_items": 2 + 0 + 4, "invocations": 3}
+
+
+# ---------------------------------------------------- structural lookups
+
+def test_lookup_plan_and_rewrite():
+    module = demo_source("spilu0", "ilu0_csr")
+    plan = create_structural_lookup_plan(module, ILU_PROPS)
+    assert len(plan) == 1
+    assert (plan[0].pointer_array, plan[0].index_array) == (
+        "A_indptr", "A_indices")
+    assert plan[0].name == "_lcd_lookup_position_0"
+    rewritten = ast.unparse(rewrite_structural_lookups(module, plan, ILU_PROPS))
+    assert "for diag_ptr in range" not in rewritten
+    assert "diag_ptr = _lcd_lookup_position_0[k]" in rewritten
+    assert "if diag_ptr >= 0:" in rewritten
+    assert "for kj_ptr in range" in rewritten          # not a self lookup
+    assert create_structural_lookup_plan(module, {}) == ()
+
+
+# ------------------------------------------------- dependence analysis
+
+def test_edge_rules_of_the_supported_loops():
+    csc = analyze_dependences(demo_source("sptrsv", "sptrsv_csc_loop"), "i",
+                              CSC_PROPS)
+    assert csc.ordering_dependences == [SegmentRule(
+        "Ap", "Ai", True, 1, 0, 1, False, "i", "j", "x")]
+    assert len(csc.reductions) == 1
+    assert csc.atomic_statements[0].operator == "+"
+    csr = analyze_dependences(demo_source("sptrsv", "sptrsv_csr_loop"), "i",
+                              CSC_PROPS)
+    assert csr.ordering_dependences == [SegmentRule(
+        "Ap", "Ai", False, 0, -1, 1, False, "i", "j", "x")]
+    assert not csr.reductions
+    ilu = analyze_dependences(demo_source("spilu0", "ilu0_csr"), "i",
+                              ILU_PROPS)
+    assert ilu.ordering_dependences == [SegmentRule(
+        "A_indptr", "A_indices", False, 0, 0, 0, True, "i", "k_ptr",
+        "A_data")]
+    for name in ("simple_gauss_seidel_csr", "full_gauss_seidel_csr"):
+        gs = analyze_dependences(demo_source("gauss_seidel", name), "i",
+                                 CSC_PROPS)
+        assert gs.ordering_dependences == [SegmentRule(
+            "Ap", "Ai", False, 0, 0, 1, False, "i", "j", "x")]
+
+
+def test_generated_inspector_text_matches_the_reference_shape():
+    ilu = analyze_dependences(demo_source("spilu0", "ilu0_csr"), "i",
+                              ILU_PROPS)
+    plan = create_dag_plan(ilu.ordering_dependences, None, "i",
+                           ["A_data", "A_indices", "A_indptr", "n"])
+    source = generate_dag_source(plan)
+    # the strings compiler/transform_tests/test_spilu0_codegen.py:129-144 checks
+    assert "for i in range(0, n):" in source
+    assert "for k_ptr in range(A_indptr[i], A_indptr[i + 1]):" in source
+    assert "if A_indices[k_ptr] >= i:" in source
+    assert "_dag_source_0 = A_indices[k_ptr]" in source
+    assert "_dag_destination_0 = i" in source
+    assert "j_ptr" not in source and "diag_ptr" not in source
+    compile(source, "<dag>", "exec")
+    csc = analyze_dependences(demo_source("sptrsv", "sptrsv_csc_loop"), "i",
+                              CSC_PROPS)
+    plan = create_dag_plan(csc.ordering_dependences, None, "i",
+                           ["Ap", "Ai", "Ax", "b", "n"])
+    source = generate_dag_source(plan, execution_mode="wavefront")
+    assert "dep_count[_dag_destination] += 1" in source
+    assert "0 <= _dag_source" not in source
+    assert "_dag_source_0 != _dag_destination_0" not in source
+    assert "if count == 0" in source
+    assert "remaining_dep_count[successor] -= 1" in source
+    # the generated text is runnable and agrees with the oracle
+    namespace = {}
+    exec(compile(source, "<dag>", "exec"), namespace)
+    case = GOLDEN["dag_cases"][2]
+    dag, levels = namespace["extract_dag"](case["ptr"], case["idx"], None,
+                                           None, 4)
+    assert dag == case["dag"] and levels == case["wavefronts"]
+    direct = direct_dependence(plan, "j")
+    assert direct.kind == "push" and ast.unparse(direct.endpoint) == "Ai[j]"
+    assert ast.unparse(direct.guard) == "Ai[j] > i"
+    assert direct_dependence(plan, None) is None
+
+
+def test_unsupported_dependences_are_rejected():
+    source = """
+def f(Ap, Ai, x, y, n):
+    for i in range(n):
+        for j in range(Ap[i], Ap[i + 1]):
+            x[Ai[j]] = y[i]
+"""
+    with pytest.raises(DependenceAnalysisError, match="non-associative"):
+        analyze_dependences(ast.parse(source),
+                            "i", {"Ap": ["monotonically_increasing"]})
+    with pytest.raises(DAGCodegenError, match="SegmentRule"):
+        create_dag_plan([object()], None, "i", [])
+
+
+# ------------------------------------------------------------ lowering
+
+def lower(module, **options):
+    function_props = options.pop("function_props", CSC_PROPS)
+    analysis = analyze_dependences(module, "i", function_props)
+    plan = create_dag_plan(analysis.ordering_dependences, None, "i", [])
+    thread = options.get("thread_loop_iterator")
+    options.setdefault("direct_dependence", direct_dependence(plan, thread))
+    return lower_to_hip(module, "i", reductions=analysis,
+                        function_props=function_props, **options)
+
+
+def test_csc_argument_lists_and_protocols():
+    module = demo_source("sptrsv", "sptrsv_csc_loop")
+    result = lower(module, execution_mode="sync_free",
+                   thread_loop_iterator="j", n_warp=1,
+                   dependence_protocol="push")
+    assert result.kernel_arguments == [
+        "Ap", "Ai", "Ax", "b", "n", "x", "dep_count", "initial_dep_count",
+        "task_nodes", "task_ptr", "task_counter", "task_count", "_lcd_status"]
+    assert result.dependence_protocol == "push" and result.warp_mapped
+    assert result.lifted_variables == ["x"]
+    assert result.zero_initialised == {"x": "n"}
+    assert result.task_lanes == 64 and result.tasks_per_block == 2
+    assert "lcd_atomic_add(&x[Ai[j]], (Ax[j] * x[i]));" in result.kernel_source
+    assert "lcd_atomic_sub(&dep_count[Ai[j]], 1);" in result.kernel_source
+    assert "if ((Ai[j] > i))" in result.kernel_source
+    assert "lcd_load_relaxed(&dep_count[i]) == LCD_READY_COUNT" in (
+        result.kernel_source)
+    assert "dag_ptr" not in result.kernel_source
+    assert result.atomic_statement_ids == {"S1"}
+    counter = lower(module, execution_mode="sync_free",
+                    thread_loop_iterator="j", n_warp=1)
+    assert counter.dependence_protocol == "counter"
+    assert "dag_index[_e]" in counter.kernel_source
+    wave = lower(module, execution_mode="wavefront",
+                 thread_loop_iterator="j", task_lanes=4,
+                 wavefront_threads_per_block=256, thread_unroll_factor=2)
+    assert wave.kernel_arguments[-4:] == [
+        "task_nodes", "task_ptr", "band_start", "band_end"]
+    assert wave.launcher_arguments[-1] == "band_ptr"
+    assert wave.tasks_per_block == 64
+    assert "launch_levels" in wave.launcher_source
+    assert "_j_base += LCD_TASK_LANES * 2" in wave.kernel_source
+    plain = lower(module, execution_mode="plain")
+    assert plain.auxiliary_arguments == []
+    for result in (counter, wave, plain):
+        hip_runtime.compile_code(result.source)
+
+
+def test_csr_reduction_is_privatised_and_pull_polls_done():
+    module = demo_source("sptrsv", "sptrsv_csr_loop")
+    result = lower(module, execution_mode="sync_free",
+                   thread_loop_iterator="j", n_warp=1,
+                   dependence_protocol="pull")
+    assert result.dependence_protocol == "pull"
+    assert "done" in result.kernel_arguments
+    assert "dep_count" not in result.kernel_arguments
+    assert "_thread_partial_0 = lcd_group_sum(_thread_partial_0);" in (
+        result.kernel_source)
+    assert "lcd_load_relaxed(&done[Ai[j]]) == 0" in result.kernel_source
+    assert "__hip_atomic_store(&done[i], 1" in result.kernel_source
+    hip_runtime.compile_code(result.source)
+    lane = lower(module, execution_mode="wavefront")
+    assert lane.task_lanes == 1 and "_thread_partial" not in lane.kernel_source
+
+
+def test_ilu0_nested_mapping_lookup_and_binary_search():
+    module = demo_source("spilu0", "ilu0_csr")
+    plan = create_structural_lookup_plan(module, ILU_PROPS)
+    for mode in ("wavefront", "sync_free"):
+        result = lower(module, function_props=ILU_PROPS, execution_mode=mode,
+                       thread_loop_iterator="j_ptr", task_lanes=8,
+                       structural_lookups=plan)
+        kernel = result.kernel_source
+        assert result.lifted_loop_parameters == ["n"]
+        assert "_lcd_lookup_position_0" in result.kernel_arguments
+        assert "_lcd_lookup_position_0" in result.launcher_source
+        assert "diag_ptr = _lcd_lookup_position_0[k];" in kernel
+        assert "lcd_sorted_find(A_indices, A_indptr[k]" in kernel
+        assert "for (diag_ptr" not in kernel and "for (kj_ptr" not in kernel
+        assert "if (_lane == 0) {" in kernel
+        assert result.dependence_protocol == "counter"
+        hip_runtime.compile_code(result.source)
+
+
+def test_lowering_errors():
+    module = demo_source("sptrsv", "sptrsv_csc_loop")
+    with pytest.raises(HIPLoweringError, match="Unknown HIP execution mode"):
+        lower(module, execution_mode="eager")
+    with pytest.raises(HIPLoweringError, match="requires a thread-mapped"):
+        lower(module, thread_unroll_factor=2)
+    with pytest.raises(HIPLoweringError, match="exactly one inner"):
+        lower(module, execution_mode="wavefront", thread_loop_iterator="q")
+    with pytest.raises(HIPLoweringError, match="n_warp=2"):
+        lower(module, execution_mode="wavefront", thread_loop_iterator="j",
+              n_warp=2, wavefront_threads_per_block=64)
+    source = """
+def f(Ap, Ai, x, n):
+    for i in range(n):
+        for j in range(Ap[i], Ap[i + 1]):
+            x[Ai[j]] *= 2.0
+"""
+    analysis = analyze_dependences(ast.parse(source), "i", CSC_PROPS)
+    with pytest.raises(UnsupportedAtomicOperation):
+        lower_to_hip(ast.parse(source), "i", reductions=analysis)
+
+
+# ----------------------------------------------------------- decorator
+
+def test_decorator_contract_without_a_gpu():
+    from lcd_amd import parallel
+    from lcd_amd.demo import spilu0, sptrsv
+    with pytest.raises(ValueError, match="block-mapped iterator"):
+        parallel(function_props={})(sptrsv.sptrsv_csc_loop)
+    solver = sptrsv.simple_sptrsv_csc
+    assert solver.original_function.__name__ == "simple_sptrsv_csc"
+    assert solver.current_schedule.execution_mode == "wavefront"
+    assert solver.current_schedule.threads_per_block == 128
+    assert "simple_sptrsv_csc_hip_kernel" in solver.hip_source
+    assert solver.cuda_kernel_source == solver.hip_kernel_source
+    assert len(solver.reduction_statements) == 1
+    assert "Ai[j] > i" in solver.dag_source
+    assert solver.schedule_space.is_fixed
+    auto = sptrsv.compile_sptrsv_csc()
+    assert auto.current_schedule is None and not auto.schedule_space.is_fixed
+    # task_lanes is an extra schedule dimension here: fixing it (or n_warp)
+    # makes the space a single configuration, as in the reference's demo
+    factor = spilu0.compile_ilu0_csr(thread_unroll=1, n_warp=1)
+    assert factor.schedule_space.is_fixed
+    assert len(factor.structural_lookups) == 1
+    assert factor.structural_lookups[0].name in factor.hip_launcher_source
+    assert not spilu0.compile_ilu0_csr(thread_unroll=1).schedule_space.is_fixed
+    if not hip_runtime.device_available():
+        with pytest.raises(hip_runtime.HIPRuntimeError):
+            solver(np.array([0, 1], dtype=np.int32),
+                   np.array([0], dtype=np.int32), np.array([1.0]),
+                   np.array([1.0]), 1)
+
+
+def test_runtime_layer_accepts_an_injected_device():
+    """A fake device layer (the reference's cuda_module= injection point)."""
+    launches = []
+
+    class FakeArray:
+        def __init__(self, data):
+            self.data = np.array(data)
+            self.shape, self.dtype = self.data.shape, self.data.dtype
+            self.nbytes = self.data.nbytes
+
+        @property
+        def __cuda_array_interface__(self):
+            return {"shape": self.shape, "typestr": self.dtype.str,
+                    "data": (self.data.ctypes.data, False), "version": 3}
+
+        def __len__(self):
+            return len(self.data)
+
+        def copy_to_host(self):
+            return self.data.copy()
+
+    class FakeDevice:
+        def empty(self, shape, dtype):
+            return FakeArray(np.zeros(shape, dtype))
+
+        def to_device(self, value, into=None):
+            return FakeArray(value)
+
+        def fill_zero(self, array):
+            array.data[...] = 0
+
+        def synchronize(self):
+            launches.append("sync")
+
+    module = demo_source("sptrsv", "sptrsv_csc_loop")
+    lowering = lower(module, execution_mode="wavefront",
+                     thread_loop_iterator="j", task_lanes=4)
+    compiled = hip_runtime.compile_hip_module(lowering, {"np": np},
+                                              hip_module=FakeDevice())
+    compiled.launcher = lambda hip, *args: launches.append(
+        [type(a).__name__ for a in args])
+    data = P.preprocess_warp_tasks([[1], []], [[0], [1]])
+    prepared = hip_runtime.prepare_hip_arguments(
+        lowering,
+        {"Ap": np.array([0, 2, 3], dtype=np.int32),
+         "Ai": np.array([0, 1, 1], dtype=np.int32),
+         "Ax": np.ones(3), "b": np.ones(2), "n": 2},
+        data, {"np": np}, hip_module=FakeDevice())
+    assert prepared.launcher_argument_names[-1] == "band_ptr"
+    assert isinstance(prepared.values["band_ptr"], np.ndarray)
+    assert prepared.values["x"].shape == (2,)
+    result = hip_runtime.execute_hip_call(compiled, lowering, prepared,
+                                          {"np": np})
+    assert result.tolist() == [0.0, 0.0] and launches[-1] == "sync"
+    with pytest.raises(hip_runtime.HIPRuntimePreparationError,
+                       match="level-ordered"):
+        hip_runtime.prepare_hip_arguments(
+            lower(module, execution_mode="sync_free"),
+            {"Ap": None, "Ai": None, "Ax": None, "b": None, "n": 2},
+            P.preprocess_sync_free([[1], []], [0, 1]), {"np": np},
+            hip_module=FakeDevice())

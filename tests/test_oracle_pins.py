@@ -1,0 +1,272 @@
+"""Pins for the CPU oracle (no GPU).
+
+The oracle is only trusted after it reproduces (a) every known-answer vector
+the reference's own tests hold for this path, (b) closed forms and library
+routines that a plausible mistake would violate, and (c) a literal set-based
+restatement of the generated inspector on random small inputs.
+"""
+
+import json
+import os
+
+import numpy as np
+import pytest
+
+from lcd_amd import workloads
+from oracle import lcd_oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden",
+                      "reference_vectors.json")
+
+
+@pytest.fixture(scope="module")
+def golden():
+    with open(GOLDEN) as handle:
+        return json.load(handle)
+
+
+def test_reference_dag_vectors(golden):
+    for case in golden["dag_cases"]:
+        rule = getattr(O, "rule_" + case["rule"])(case["ptr"], case["idx"])
+        dag = O.dag_build([rule], case["n"])
+        assert dag.successors() == case["dag"], case["name"]
+        assert dag.dep_count.tolist() == case["dep_count"], case["name"]
+        if "dag_ptr" in case:
+            assert dag.dag_ptr.tolist() == case["dag_ptr"]
+            assert dag.dag_index.tolist() == case["dag_index"]
+        if "wavefronts" in case:
+            assert dag.wavefront_list() == case["wavefronts"], case["name"]
+        if "wavefront_ptr" in case:
+            assert dag.wavefronts.tolist() == case["wavefronts_flat"]
+            assert dag.wavefront_ptr.tolist() == case["wavefront_ptr"]
+
+
+def test_reference_cycle_vector(golden):
+    dag = O.dag_from_successors(golden["cyclic_dag"]["successors"])
+    assert dag.scheduled < dag.n      # the reference raises "may contain a cycle"
+
+
+def test_reference_lookup_vectors(golden):
+    for case in golden["lookup_cases"]:
+        status, positions = O.lookup_positions(case["ptr"], case["idx"])
+        if "error" in case:
+            assert status == 2
+        else:
+            assert status == 0 and positions.tolist() == case["positions"]
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_inspector_matches_literal_restatement(seed):
+    """Random, unsorted segments with duplicates; all rule shapes."""
+    rng = np.random.default_rng(seed)
+    n = int(rng.integers(1, 60))
+    counts = rng.integers(0, 7, n)
+    ptr = np.zeros(n + 1, dtype=np.int32)
+    np.cumsum(counts, out=ptr[1:])
+    idx = rng.integers(0, n, int(ptr[-1])).astype(np.int32)
+    sorted_idx = idx.copy()
+    for s in range(n):
+        sorted_idx[ptr[s]:ptr[s + 1]].sort()
+    rules = [
+        O.make_rule(ptr, idx, True, guard=O.GUARD_GREATER),
+        O.make_rule(ptr, idx, False, guard=O.GUARD_GREATER),
+        O.make_rule(ptr, idx, True, guard=O.GUARD_NOT_EQUAL),
+        O.make_rule(ptr, sorted_idx, False, guard=O.GUARD_NONE,
+                    break_at_owner=True),
+    ]
+    for rule in rules:
+        acyclic = rule["guard"] == O.GUARD_GREATER or rule["break_at_owner"]
+        dag = O.dag_build([rule], n)
+        successors, dep_count, edge_count = O.literal_extract_dag(
+            rule, n, "sync_free", edge_multiplicity=True)
+        assert dag.successors() == successors
+        assert dag.dep_count.tolist() == dep_count
+        assert dag.edge_count.tolist() == edge_count
+        levels = O.literal_wavefronts_from_dag(successors, dep_count)
+        assert dag.wavefront_list() == levels
+        if acyclic:
+            assert dag.scheduled == n
+            # Kahn levels are longest-path levels
+            level_of = dag.level_of
+            for v, nbrs in enumerate(successors):
+                for w in nbrs:
+                    assert level_of[w] > level_of[v]
+            for w in range(n):
+                preds = [v for v in range(n) if w in successors[v]]
+                expected = 1 + max((level_of[v] for v in preds), default=-1)
+                assert level_of[w] == expected
+
+
+def test_offsets_select_the_segment_part():
+    """lower/upper offsets: CSC skips the leading diagonal, CSR the trailing."""
+    csc = O.dag_build([O.rule_sptrsv_csc([0, 2, 3], [0, 1, 1])], 2)
+    assert csc.successors() == [[1], []]
+    csr = O.dag_build([O.rule_sptrsv_csr([0, 1, 3], [0, 0, 1])], 2)
+    assert csr.successors() == [[1], []]
+    # without the offsets the diagonal is examined too (and rejected by the
+    # strict guard), so the result is the same; a wrong sign would add (1,0)
+    wrong = O.dag_build([O.make_rule([0, 1, 3], [0, 0, 1], True)], 2)
+    assert wrong.successors() == [[], []]
+
+
+@pytest.mark.parametrize("shape", [(7, 5), (4, 5, 3), (9,)])
+def test_stencil_closed_forms(shape):
+    """Level of a grid node is the sum of its coordinates; in-degree counts
+    its lower neighbours; successors are id + stride."""
+    ptr, idx, _ = workloads.stencil_lower_csc(shape, 2.0 * len(shape))
+    n = int(np.prod(shape))
+    dag = O.dag_build([O.rule_sptrsv_csc(ptr, idx)], n)
+    ids = np.arange(n)
+    coords, stride = [], 1
+    for d in shape:
+        coords.append((ids // stride) % d)
+        stride *= d
+    np.testing.assert_array_equal(dag.level_of, sum(coords))
+    np.testing.assert_array_equal(dag.dep_count,
+                                  sum((c > 0).astype(int) for c in coords))
+    assert dag.levels == sum(shape) - len(shape) + 1
+    assert dag.edges == sum(
+        (shape[d] - 1) * n // shape[d] for d in range(len(shape)))
+    # inside a level node ids ascend
+    for k in range(dag.levels):
+        level = dag.wavefronts[dag.wavefront_ptr[k]:dag.wavefront_ptr[k + 1]]
+        assert np.all(np.diff(level) > 0)
+
+
+def test_configuration_sizes_match_the_published_table():
+    c1 = workloads.configuration("c1")
+    assert (c1.n, c1.nnz, c1.algorithmic_bytes) == (4096, 12160, 227844)
+    c5 = workloads.configuration("c5", n=4096)
+    assert c5.nnz == 4096 * 9 - 36
+    c4 = workloads.configuration("c4", nx=32, ny=16)
+    assert c4.nnz == 32 * 16 + 2 * 31 * 16 + 2 * 32 * 15 + 4 * 31 * 15
+    c3 = workloads.configuration("c3", n=5000)
+    for row in (1, 17, 4999):
+        cols = c3.indices[c3.indptr[row]:c3.indptr[row + 1]]
+        assert cols[-1] == row and np.all(np.diff(cols) > 0)
+        values = c3.data[c3.indptr[row]:c3.indptr[row + 1]]
+        assert values[-1] == pytest.approx(1 + np.abs(values[:-1]).sum())
+
+
+def test_banded_and_ilu_closed_forms():
+    ptr, idx, _ = workloads.banded_lower_csc(300, 8)
+    dag = O.dag_build([O.rule_sptrsv_csc(ptr, idx)], 300)
+    np.testing.assert_array_equal(dag.dep_count,
+                                  np.minimum(np.arange(300), 8))
+    np.testing.assert_array_equal(dag.level_of, np.arange(300))
+    nx, ny = 9, 7
+    ptr, idx, _ = workloads.stencil9_csr(nx, ny)
+    dag = O.dag_build([O.rule_ilu0_csr(ptr, idx)], nx * ny)
+    ids = np.arange(nx * ny)
+    x, y = ids % nx, ids // nx
+    np.testing.assert_array_equal(dag.level_of, x + 2 * y)
+    assert dag.levels == nx + 2 * ny - 2
+
+
+def test_sptrsv_against_scipy_and_dense():
+    from scipy.sparse import csc_matrix, csr_matrix
+    from scipy.sparse.linalg import spsolve_triangular
+    work = workloads.configuration("c2", nx=6, ny=5, nz=4)
+    matrix = csc_matrix((work.data, work.indices, work.indptr),
+                        shape=(work.n, work.n))
+    x = O.sptrsv_csc(work.indptr, work.indices, work.data, work.rhs, work.n)
+    np.testing.assert_allclose(
+        x, spsolve_triangular(matrix.tocsr(), work.rhs, lower=True),
+        rtol=1e-13, atol=1e-14)
+    np.testing.assert_allclose(x, np.linalg.solve(matrix.toarray(), work.rhs),
+                               rtol=1e-12, atol=1e-13)
+    np.testing.assert_array_equal(
+        x, O.literal_sptrsv_csc(work.indptr, work.indices, work.data,
+                                work.rhs, work.n))
+    work = workloads.configuration("c3", n=300)
+    matrix = csr_matrix((work.data, work.indices, work.indptr),
+                        shape=(work.n, work.n))
+    x = O.sptrsv_csr(work.indptr, work.indices, work.data, work.rhs, work.n)
+    np.testing.assert_allclose(x, np.linalg.solve(matrix.toarray(), work.rhs),
+                               rtol=1e-11, atol=1e-12)
+    np.testing.assert_array_equal(
+        x, O.literal_sptrsv_csr(work.indptr, work.indices, work.data,
+                                work.rhs, work.n))
+    # special cases: diagonal matrix, unit bidiagonal recurrence
+    n = 50
+    d = np.linspace(1, 2, n)
+    b = np.arange(n, dtype=float)
+    np.testing.assert_array_equal(
+        O.sptrsv_csc(np.arange(n + 1), np.arange(n), d, b, n), b / d)
+    ptr, idx, val = workloads.banded_lower_csc(n, 1, seed=3)
+    x = O.sptrsv_csc(ptr, idx, val, b, n)
+    expected = np.zeros(n)
+    for i in range(n):
+        expected[i] = b[i] - (val[ptr[i - 1] + 1] * expected[i - 1] if i else 0)
+    np.testing.assert_allclose(x, expected, rtol=1e-14)
+
+
+def test_ilu0_against_dense_lu_and_pattern_identity():
+    rng = np.random.default_rng(2)
+    n = 20
+    dense = rng.uniform(-1, 1, (n, n)) + n * np.eye(n)
+    indptr = np.arange(0, n * n + 1, n, dtype=np.int32)
+    indices = np.tile(np.arange(n, dtype=np.int32), n)
+    factors = O.ilu0_csr(dense.ravel(), indices, indptr).reshape(n, n)
+    doolittle = dense.copy()
+    for k in range(n):
+        doolittle[k + 1:, k] /= doolittle[k, k]
+        doolittle[k + 1:, k + 1:] -= np.outer(doolittle[k + 1:, k],
+                                              doolittle[k, k + 1:])
+    np.testing.assert_allclose(factors, doolittle, rtol=1e-12, atol=1e-13)
+    # sparse pattern: (L U)[i, j] == A[i, j] on the pattern
+    work = workloads.configuration("c4", nx=11, ny=9)
+    from scipy.sparse import csr_matrix
+    result = O.ilu0_csr(work.data, work.indices, work.indptr)
+    np.testing.assert_array_equal(
+        result, O.literal_ilu0_csr(work.data.copy(), work.indices.tolist(),
+                                   work.indptr.tolist()))
+    a = csr_matrix((work.data, work.indices, work.indptr),
+                   shape=(work.n, work.n)).toarray()
+    f = csr_matrix((result, work.indices, work.indptr),
+                   shape=(work.n, work.n)).toarray()
+    product = (np.tril(f, -1) + np.eye(work.n)) @ np.triu(f)
+    mask = a != 0
+    np.testing.assert_allclose(product[mask], a[mask], rtol=1e-12, atol=1e-12)
+    # tridiagonal: Thomas recurrence
+    n = 12
+    main, off = np.full(n, 4.0), np.full(n - 1, -1.0)
+    tri = csr_matrix(np.diag(main) + np.diag(off, 1) + np.diag(off, -1))
+    tri.sort_indices()
+    out = O.ilu0_csr(tri.data, tri.indices, tri.indptr)
+    pivots = [4.0]
+    for _ in range(n - 1):
+        pivots.append(4.0 - 1.0 / pivots[-1])
+    diag = csr_matrix((out, tri.indices, tri.indptr), shape=(n, n)).diagonal()
+    np.testing.assert_allclose(diag, pivots, rtol=1e-14)
+
+
+def test_band_chains_against_literal():
+    rng = np.random.default_rng(4)
+    for band_width in (1, 2, 3, 5):
+        work = workloads.configuration("c2", nx=5, ny=4, nz=3)
+        dag = O.dag_build([O.rule_sptrsv_csc(work.indptr, work.indices)],
+                          work.n)
+        nodes, ptr, bands = dag.band_chains(band_width)
+        expected = O.literal_band_chains(
+            dag.wavefronts.tolist(), dag.wavefront_ptr.tolist(),
+            dag.dag_ptr.tolist(), dag.dag_index.tolist(), band_width)
+        assert nodes.tolist() == expected[0]
+        assert ptr.tolist() == expected[1]
+        assert bands.tolist() == expected[2]
+    del rng
+
+
+def test_gauss_seidel_is_repeated_forward_substitution():
+    work = workloads.configuration("c4", nx=6, ny=5)
+    from scipy.sparse import csr_matrix, tril
+    matrix = csr_matrix((work.data, work.indices, work.indptr),
+                        shape=(work.n, work.n))
+    strict = tril(matrix, -1, format="csr")
+    strict.sort_indices()
+    diagonal = matrix.diagonal()
+    b = np.linspace(0, 1, work.n)
+    x = O.gauss_seidel_csr(strict.indptr, strict.indices, strict.data,
+                           diagonal, b, np.zeros(work.n), work.n, 1)
+    lower = (strict + csr_matrix(np.diag(diagonal))).toarray()
+    np.testing.assert_allclose(x, np.linalg.solve(lower, b), rtol=1e-12)
