@@ -318,10 +318,13 @@ class _Kinds:
 # Python AST -> C++ text
 
 class _Emitter:
-    def __init__(self, kinds, reductions, lowered_ids):
+    def __init__(self, kinds, reductions, lowered_ids, coherent_arrays=()):
         self.kinds = kinds
         self.reductions = reductions
         self.lowered_ids = lowered_ids
+        # arrays other tasks write while this kernel runs: every access goes
+        # through device-scope (cache-bypassing / write-through) accessors
+        self.coherent_arrays = set(coherent_arrays)
 
     # ---- expressions
     def expr(self, node):
@@ -339,7 +342,10 @@ class _Emitter:
         if isinstance(node, ast.Subscript):
             if not isinstance(node.value, ast.Name):
                 raise HIPLoweringError("Only 1-D array indexing is supported.")
-            return f"{node.value.id}[{self.expr(node.slice)}]"
+            element = f"{node.value.id}[{self.expr(node.slice)}]"
+            if node.value.id in self.coherent_arrays:
+                return f"lcd_ld(&{element})"
+            return element
         if isinstance(node, ast.BinOp):
             left, right = self.expr(node.left), self.expr(node.right)
             if isinstance(node.op, ast.Div):
@@ -409,6 +415,19 @@ class _Emitter:
         raise HIPLoweringError(
             f"Unsupported expression in a device loop: {ast.unparse(node)!r}.")
 
+    def element(self, target):
+        """``X[e]`` as an lvalue (no accessor)."""
+        if not (isinstance(target, ast.Subscript)
+                and isinstance(target.value, ast.Name)):
+            raise HIPLoweringError("Only 1-D array indexing is supported.")
+        return f"{target.value.id}[{self.expr(target.slice)}]"
+
+    def store(self, target, value_text):
+        element = self.element(target)
+        if target.value.id in self.coherent_arrays:
+            return f"lcd_st(&{element}, {value_text});"
+        return f"{element} = {value_text};"
+
     # ---- statements
     def block(self, statements, indent, hooks=None):
         lines = []
@@ -441,8 +460,7 @@ class _Emitter:
             raise HIPLoweringError(
                 "Device atomics require an indexed 1-D array target.")
         self.lowered_ids.add(statement_id)
-        return (f"{call}(&{node.target.value.id}"
-                f"[{self.expr(node.target.slice)}], {self.expr(node.value)});")
+        return f"{call}(&{self.element(node.target)}, {self.expr(node.value)});"
 
     def stmt(self, node, indent, hooks=None):
         pad = "    " * indent
@@ -457,8 +475,10 @@ class _Emitter:
             if len(node.targets) != 1:
                 raise HIPLoweringError("Chained assignment is not supported.")
             target = node.targets[0]
-            if isinstance(target, (ast.Name, ast.Subscript)):
-                return [f"{pad}{self.expr(target)} = {self.expr(node.value)};"]
+            if isinstance(target, ast.Subscript):
+                return [pad + self.store(target, self.expr(node.value))]
+            if isinstance(target, ast.Name):
+                return [f"{pad}{target.id} = {self.expr(node.value)};"]
             raise HIPLoweringError("Unsupported assignment target.")
         if isinstance(node, ast.AugAssign):
             atomic = self.atomic(node)
@@ -469,7 +489,9 @@ class _Emitter:
             for sub in ast.walk(expanded.left):
                 if hasattr(sub, "ctx"):
                     sub.ctx = ast.Load()
-            return [f"{pad}{self.expr(node.target)} = {self.expr(expanded)};"]
+            if isinstance(node.target, ast.Subscript):
+                return [pad + self.store(node.target, self.expr(expanded))]
+            return [f"{pad}{node.target.id} = {self.expr(expanded)};"]
         if isinstance(node, ast.If):
             lines = [f"{pad}if ({self.expr(node.test)}) {{"]
             lines += self.block(node.body, indent + 1, hooks)
@@ -563,8 +585,46 @@ template <class T, class V> __device__ __forceinline__ void lcd_atomic_xor(T* p,
 __device__ __forceinline__ int lcd_load_relaxed(const int* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, LCD_AGENT);
 }
-__device__ __forceinline__ void lcd_release_fence() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
-__device__ __forceinline__ void lcd_acquire_fence() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+// Coherent accessors for arrays that other tasks write while the kernel runs
+// (sync-free executors).  Device-scope relaxed atomics: loads always observe
+// the device coherence point, stores are written through to it, so no L2
+// write-back or invalidation is ever needed around a dependence hand-off.
+template <class T> __device__ __forceinline__ T lcd_ld(const T* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, LCD_AGENT);
+}
+template <class T, class V> __device__ __forceinline__ void lcd_st(T* p, V v) {
+    __hip_atomic_store(p, (T)v, __ATOMIC_RELAXED, LCD_AGENT);
+}
+// Release: every store/atomic this wavefront issued has completed at the
+// coherence point before anything after the fence is issued.
+__device__ __forceinline__ void lcd_release_fence() {
+#ifdef LCD_FULL_FENCES
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+#else
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#endif
+}
+// Between a task's atomic updates of other tasks' elements and the counter
+// decrement that releases them.  The updates are device-scope atomics, which
+// are performed at the device coherence point (never left dirty in an L2), so
+// it is enough to wait until they have completed: no L2 write-back is needed.
+__device__ __forceinline__ void lcd_push_fence() {
+#ifdef LCD_FULL_FENCES
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+#else
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#endif
+}
+// Acquire: the ready test is a completed device-scope load and the GPU issues
+// nothing speculatively past the branch on it; with coherent accessors for
+// the data, only the compiler has to be kept from hoisting loads.
+__device__ __forceinline__ void lcd_acquire_fence() {
+#ifdef LCD_FULL_FENCES
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+#else
+    asm volatile("" ::: "memory");
+#endif
+}
 // Sum over the LCD_TASK_LANES lanes of one task group (xor butterfly: every
 // lane ends with the total, the compiler lowers the fixed masks to DPP).
 __device__ __forceinline__ double lcd_group_sum(double v) {
@@ -606,7 +666,17 @@ class _MappedLoopHooks:
         lanes = "LCD_TASK_LANES"
         unroll = low.thread_unroll_factor
         body = deepcopy(node.body)
-        lines = [f"{pad}{low.group_sync}"]
+        # lanes only need a group fence after the loop when it stored to
+        # memory that later uniform code may read (atomics and register
+        # partial sums do not)
+        stores = any(
+            isinstance(sub, (ast.Assign, ast.AugAssign))
+            and any(isinstance(t, ast.Subscript) for t in (
+                sub.targets if isinstance(sub, ast.Assign) else [sub.target]))
+            and (getattr(sub, "lineno", None), getattr(sub, "col_offset", None))
+            not in low.reductions
+            for statement in node.body for sub in ast.walk(statement))
+        lines = []
         for partial, _, _ in self.partials:
             lines.append(f"{pad}{partial} = 0.0;")
         body_lines = emitter.block(body, indent + (2 if unroll > 1 else 1), None)
@@ -628,15 +698,16 @@ class _MappedLoopHooks:
             lines.append(f"{pad}        }}")
             lines.append(f"{pad}    }}")
             lines.append(f"{pad}}}")
-        lines.append(f"{pad}{low.group_sync}")
+        if stores:
+            lines.append(f"{pad}{low.group_sync}")
         for partial, target, op in self.partials:
             total = low.group_total(partial)
             op_text = "+" if isinstance(op, ast.Add) else "-"
             target_text = emitter.expr(target)
             lines.append(f"{pad}{partial} = {total};")
             if isinstance(target, ast.Subscript):
-                lines.append(f"{pad}if (_lane == 0) {target_text} = "
-                             f"{target_text} {op_text} {partial};")
+                lines.append(f"{pad}if (_lane == 0) " + emitter.store(
+                    target, f"{target_text} {op_text} {partial}"))
                 lines.append(f"{pad}{low.group_sync}")
             else:
                 lines.append(f"{pad}{target_text} = {target_text} {op_text} {partial};")
@@ -652,7 +723,8 @@ class HIPLowerer:
                  function_props=None, structural_lookups=(), task_lanes=None,
                  chain_tasks=False, argument_kinds=None,
                  spin_limit=DEFAULT_SPIN_LIMIT, resident_waves_per_cu=None,
-                 spin_sleep=1):
+                 spin_sleep=1, promote_own_elements=True):
+        self.promote_own_elements = promote_own_elements
         self.resident_waves_per_cu = resident_waves_per_cu
         self.spin_sleep = spin_sleep
         self.loop_iterator = loop_iterator
@@ -744,7 +816,7 @@ class HIPLowerer:
         pad = "    " * indent
         dependence = self.direct_dependence
         endpoint = self._emitter.expr(dependence.endpoint)
-        lines = [f"{pad}lcd_release_fence();"]
+        lines = [f"{pad}lcd_push_fence();"]
         if dependence.guard is not None:
             lines.append(f"{pad}if ({self._emitter.expr(dependence.guard)})")
             lines.append(f"{pad}    lcd_atomic_sub(&dep_count[{endpoint}], 1);")
@@ -807,10 +879,13 @@ class HIPLowerer:
         kinds.infer_locals(body)
         self._kinds = kinds
         lowered_ids = set()
-        emitter = _Emitter(kinds, self.reductions, lowered_ids)
+        written_arrays = self._written_arrays(body)
+        emitter = _Emitter(
+            kinds, self.reductions, lowered_ids,
+            coherent_arrays=(written_arrays
+                             if self.execution_mode == "sync_free" else ()))
         self._emitter = emitter
 
-        written_arrays = self._written_arrays(body)
         user_arguments = list(arguments)
         for name in lifted_variables + lifted_loop_parameters:
             if name not in user_arguments:
@@ -821,11 +896,20 @@ class HIPLowerer:
         for name in lookup_names:
             if name not in user_arguments:
                 user_arguments.append(name)
+        if (self.thread_loop_iterator is not None
+                and self.dependence_protocol != COUNTER_DEPENDENCE):
+            nested = self._find_mapped_loop(body)
+            if nested not in body:
+                # hooks describe task-level edges; a nested work-sharing loop
+                # would change their multiplicity
+                self.dependence_protocol = COUNTER_DEPENDENCE
         executor_arguments = self._executor_arguments()
         kernel_arguments = user_arguments + [
             name for name in executor_arguments if name not in user_arguments]
 
-        task_body = self._task_body(body, emitter, local_names, target_loop)
+        self._lifted_parameters = list(lifted_loop_parameters)
+        task_body = self._task_body(body, emitter, local_names, target_loop,
+                                    arguments)
         missing = ({sid for sid, _ in self.reductions.values()} - lowered_ids)
         if missing:
             raise HIPLoweringError(
@@ -1118,10 +1202,154 @@ class HIPLowerer:
         wrapper = ast.Module(body=statements, type_ignores=[])
         return Guard().visit(wrapper).body
 
-    def _task_body(self, body, emitter, local_names, target_loop):
+    def _promote_own_elements(self, body, mapped, hooks, arguments):
+        """Keep ``X[E]`` in a register for the whole task when ``E`` depends
+        only on the block iterator and loop-invariant inputs and the task
+        stores it at its top level (``x[i]`` of the triangular solves).
+
+        Every lane of the group computes the value (uniform code, identical
+        loads), the distributed loop reads the register instead of memory,
+        and lane 0 stores it once at the end of the task, before successors
+        are released.  This removes the store -> fence -> reload round trips
+        from the task's dependency chain.  Other elements of ``X`` may only be
+        touched inside the distributed loop (reads, atomic updates, or stores
+        at loop-variant positions): a task's own element is never one of
+        those, because the DAG has no self edges.
+        """
+        written = self._written_arrays(body)
+        invariant_names = {self.loop_iterator} | {
+            name for name in arguments if name not in written}
+        invariant_names |= set(self._lifted_parameters)
+        top_level = [s for s in body if s is not mapped]
+
+        def own(node):
+            return (isinstance(node, ast.Subscript)
+                    and isinstance(node.value, ast.Name)
+                    and node.value.id in written
+                    and _names_in(node.slice) <= invariant_names
+                    and not (_names_in(node.slice) & written))
+
+        candidates = {}
+        for statement in top_level:
+            target = None
+            if isinstance(statement, ast.Assign) and len(statement.targets) == 1:
+                target = statement.targets[0]
+            elif isinstance(statement, ast.AugAssign):
+                target = statement.target
+            if target is not None and own(target):
+                if (isinstance(statement, ast.AugAssign)
+                        and (statement.lineno, statement.col_offset)
+                        in self.reductions):
+                    continue
+                candidates.setdefault(ast.dump(target.value) + "|"
+                                      + ast.unparse(target.slice), target)
+        for _, target, _ in (hooks.partials if hooks else []):
+            if own(target):
+                candidates.setdefault(ast.dump(target.value) + "|"
+                                      + ast.unparse(target.slice), target)
+        promoted = {}
+        for key, target in candidates.items():
+            array = target.value.id
+            index_text = ast.unparse(target.slice)
+            safe = True
+            for statement in top_level:
+                for node in ast.walk(statement):
+                    if (isinstance(node, ast.Subscript)
+                            and isinstance(node.value, ast.Name)
+                            and node.value.id == array
+                            and ast.unparse(node.slice) != index_text):
+                        safe = False
+            if any(other != key and other.split("|")[0] == key.split("|")[0]
+                   for other in candidates):
+                safe = False
+            if safe:
+                promoted[key] = (array, index_text,
+                                 f"_lcd_own_{len(promoted)}", target)
+        if not promoted:
+            return body, [], []
+
+        by_text = {(array, index_text): name
+                   for array, index_text, name, _ in promoted.values()}
+        first_access = {}   # name -> "read" | "write"
+
+        class Replace(ast.NodeTransformer):
+            def visit_Subscript(self, node):
+                if isinstance(node.value, ast.Name):
+                    name = by_text.get((node.value.id, ast.unparse(node.slice)))
+                    if name is not None:
+                        return ast.copy_location(
+                            ast.Name(id=name, ctx=node.ctx), node)
+                return self.generic_visit(node)
+
+        def note(statement):
+            reads, writes = set(), set()
+            for node in ast.walk(statement):
+                if isinstance(node, ast.Subscript) and isinstance(
+                        node.value, ast.Name):
+                    name = by_text.get((node.value.id, ast.unparse(node.slice)))
+                    if name is None:
+                        continue
+                    if isinstance(node.ctx, ast.Store) and not isinstance(
+                            statement, ast.AugAssign):
+                        writes.add(name)
+                    else:
+                        reads.add(name)
+            if isinstance(statement, ast.Assign):
+                value_reads = set()
+                for node in ast.walk(statement.value):
+                    if isinstance(node, ast.Subscript) and isinstance(
+                            node.value, ast.Name):
+                        name = by_text.get(
+                            (node.value.id, ast.unparse(node.slice)))
+                        if name is not None:
+                            value_reads.add(name)
+                reads = value_reads | (reads - writes)
+            for name in reads:
+                first_access.setdefault(name, "read")
+            for name in writes:
+                first_access.setdefault(name, "write")
+
+        for statement in body:
+            note(statement)
+        for _, target, _ in (hooks.partials if hooks else []):
+            name = by_text.get((target.value.id, ast.unparse(target.slice))
+                               ) if isinstance(target, ast.Subscript) else None
+            if name is not None:
+                first_access.setdefault(name, "read")
+        replacer = Replace()
+        new_body = []
+        for statement in body:
+            if statement is mapped:
+                mapped.body = [replacer.visit(s) for s in mapped.body]
+                new_body.append(mapped)
+            else:
+                new_body.append(replacer.visit(statement))
+        if hooks:
+            hooks.partials = [
+                (partial, replacer.visit(deepcopy(target)), op)
+                for partial, target, op in hooks.partials]
+        if self.direct_dependence is not None:
+            pass   # endpoints never name an own element
+        prologue, epilogue = [], []
+        emitter = self._emitter
+        for array, index_text, name, target in promoted.values():
+            self._kinds.locals[name] = self._kinds.arrays.get(array, FLOAT)
+            self._own_registers.append(name)
+            load_node = ast.Subscript(
+                value=ast.Name(id=array, ctx=ast.Load()),
+                slice=deepcopy(target.slice), ctx=ast.Load())
+            if first_access.get(name, "read") == "read":
+                prologue.append(f"{name} = {emitter.expr(load_node)};")
+            epilogue.append("if (_lane == 0) " + emitter.store(load_node, name))
+        ast.fix_missing_locations(ast.Module(body=new_body, type_ignores=[]))
+        return new_body, prologue, epilogue
+
+    def _task_body(self, body, emitter, local_names, target_loop, arguments):
         """C++ lines of one task (indent level 0), `i` already bound."""
         mapped = self._find_mapped_loop(body)
         hooks = None
+        self._own_registers = []
+        self._pending_sync = False
         if mapped is not None:
             hooks = _MappedLoopHooks(self, emitter, mapped)
             outer_assigned = set(local_names) - (
@@ -1132,23 +1360,24 @@ class HIPLowerer:
                     "privatized safely.")
             for partial, _, _ in hooks.partials:
                 self._kinds.locals[partial] = FLOAT
-            if self.task_lanes > 1:
-                body = self._guard_stores(body, mapped)
-            if (self.dependence_protocol != COUNTER_DEPENDENCE
-                    and mapped not in body):
-                # hooks describe task-level edges; a nested work-sharing loop
-                # would change their multiplicity
-                self.dependence_protocol = COUNTER_DEPENDENCE
+        prologue, epilogue = [], []
+        if self.promote_own_elements:
+            body, prologue, epilogue = self._promote_own_elements(
+                body, mapped, hooks, arguments)
+        if mapped is not None and self.task_lanes > 1:
+            body = self._guard_stores(body, mapped)
         self._partials = hooks.partials if hooks else []
-        lines = []
+        lines = list(prologue)
         for statement in body:
             lines.extend(self._emit_guarded(statement, emitter, 0, hooks))
+        lines.extend(epilogue)
         return lines
 
     def _emit_guarded(self, node, emitter, indent, hooks):
         pad = "    " * indent
         if isinstance(node, ast.If) and getattr(node, "_lcd_store_guard", False):
             inner = emitter.block(node.body, indent + 1, None)
+            self._pending_sync = False
             return [f"{pad}if (_lane == 0) {{", *inner, f"{pad}}}",
                     f"{pad}{self.group_sync}"]
         if isinstance(node, ast.If):
@@ -1250,7 +1479,8 @@ class HIPLowerer:
         pad = "    " * indent
         lines = []
         declared = set()
-        for name in list(local_names) + [p for p, _, _ in self._partials]:
+        for name in (list(local_names) + [p for p, _, _ in self._partials]
+                     + list(self._own_registers)):
             if name in declared or name == self.loop_iterator:
                 continue
             declared.add(name)
@@ -1382,11 +1612,18 @@ class HIPLowerer:
             return lines
         lines += [
             "    const int _tasks_per_wave = 64 / LCD_TASK_LANES;",
+            "    int _round = 0; (void)_round;",
             "    while (true) {",
+            "#ifndef LCD_DYNAMIC_FETCH",
+            "        const int _base = (_round * (int)(gridDim.x * (LCD_TPB / 64)) + "
+            "(int)(blockIdx.x * (LCD_TPB / 64) + (threadIdx.x >> 6))) * _tasks_per_wave;",
+            "        ++_round;",
+            "#else",
             "        int _base = 0;",
             "        if ((threadIdx.x & 63) == 0)",
             "            _base = atomicAdd(&task_counter[0], _tasks_per_wave);",
             "        _base = __shfl(_base, 0, 64);",
+            "#endif",
             "        if (_base >= _task_count) return;",
             "        const int _task = _base + (int)(threadIdx.x & 63) / LCD_TASK_LANES;",
             "        bool _pending = _task < _task_count;",
@@ -1548,7 +1785,7 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
                  function_props=None, structural_lookups=(), task_lanes=None,
                  chain_tasks=False, argument_kinds=None,
                  spin_limit=DEFAULT_SPIN_LIMIT, resident_waves_per_cu=None,
-                 spin_sleep=1):
+                 spin_sleep=1, promote_own_elements=True):
     """HIP counterpart of ``lower_to_numba_cuda``
     (compiler/cuda_lowering.py:2854-2884); same parameters plus
     ``task_lanes`` (lanes cooperating on one task, a power of two <= 64),
@@ -1566,5 +1803,5 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
         structural_lookups=structural_lookups, task_lanes=task_lanes,
         chain_tasks=chain_tasks, argument_kinds=argument_kinds,
         spin_limit=spin_limit, resident_waves_per_cu=resident_waves_per_cu,
-        spin_sleep=spin_sleep)
+        spin_sleep=spin_sleep, promote_own_elements=promote_own_elements)
     return lowerer.lower(code)

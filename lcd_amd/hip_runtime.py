@@ -162,7 +162,8 @@ def _check(status):
 def compile_code(source, name="lcd_generated.hip", options=()):
     """hiprtc-compile HIP source for gfx950; works without a GPU."""
     lib = load_library()
-    opts = [o.encode() for o in (*DEVICE_COMPILE_OPTIONS, *options)]
+    extra = tuple(os.environ.get("LCD_HIP_EXTRA_OPTIONS", "").split())
+    opts = [o.encode() for o in (*DEVICE_COMPILE_OPTIONS, *options, *extra)]
     array = (ctypes.c_char_p * len(opts))(*opts)
     code, size, log = ctypes.c_void_p(), ctypes.c_size_t(), ctypes.c_char_p()
     status = lib.lcdhip_module_compile_code(

@@ -381,7 +381,21 @@ def test_csc_argument_lists_and_protocols():
     assert result.lifted_variables == ["x"]
     assert result.zero_initialised == {"x": "n"}
     assert result.task_lanes == 64 and result.tasks_per_block == 2
-    assert "lcd_atomic_add(&x[Ai[j]], (Ax[j] * x[i]));" in result.kernel_source
+    # the task's own element lives in a register: computed by every lane,
+    # read by the distributed loop, stored once by lane 0
+    assert "_lcd_own_0 = ((b[i] - _lcd_own_0) / Ax[Ap[i]]);" in (
+        result.kernel_source)
+    assert "lcd_atomic_add(&x[Ai[j]], (Ax[j] * _lcd_own_0));" in (
+        result.kernel_source)
+    # sync-free kernels reach arrays that other tasks write through
+    # device-scope accessors
+    assert "_lcd_own_0 = lcd_ld(&x[i]);" in result.kernel_source
+    assert "if (_lane == 0) lcd_st(&x[i], _lcd_own_0);" in result.kernel_source
+    unpromoted = lower(module, execution_mode="sync_free",
+                       thread_loop_iterator="j", n_warp=1,
+                       dependence_protocol="push", promote_own_elements=False)
+    assert "lcd_atomic_add(&x[Ai[j]], (Ax[j] * lcd_ld(&x[i])));" in (
+        unpromoted.kernel_source)
     assert "lcd_atomic_sub(&dep_count[Ai[j]], 1);" in result.kernel_source
     assert "if ((Ai[j] > i))" in result.kernel_source
     assert "lcd_load_relaxed(&dep_count[i]) == LCD_READY_COUNT" in (
