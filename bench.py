@@ -27,11 +27,40 @@ HBM_PEAK_GBPS = 8000.0
 METRIC = "SpTRSV/SpILU0 solve ms, GFLOP/s, HBM GB/s (% roofline) on 1 MI355X"
 
 
+# Executor settings per configuration (the fastest measured on MI355X; every
+# one can be overridden on the command line).
+TUNED = {
+    "c1": dict(execution_mode="sync_free", threads_per_block=64, task_lanes=4,
+               thread_unroll=1, resident_waves_per_cu=1),
+    "c2": dict(execution_mode="sync_free", threads_per_block=256, task_lanes=4,
+               thread_unroll=1, resident_waves_per_cu=2),
+    "c3": dict(execution_mode="sync_free", threads_per_block=256,
+               task_lanes=16, thread_unroll=1, resident_waves_per_cu=4,
+               dependence_protocol="counter"),
+    "c4": dict(execution_mode="wavefront", threads_per_block=64, task_lanes=8,
+               thread_unroll=1),
+    "c5": dict(execution_mode="sync_free", threads_per_block=256, task_lanes=8,
+               thread_unroll=1, resident_waves_per_cu=2),
+}
+
+
+# HBM bytes per launch of the dominant kernel from rocprofv3 --pmc FETCH_SIZE /
+# WRITE_SIZE (scaled by the copy-probe kernel); source: the summaries under
+# profiles/.  Keyed by (config, mode, protocol, task_lanes); anything not
+# profiled reports null.
+MEASURED_TRAFFIC = {
+    ("c2", "sync_free", "push", 4): 1_937_433_319,
+}
+
+
 def build_solver(work, args):
     from lcd_amd.demo import spilu0, sptrsv
-    options = {}
-    mode = args.mode or work.execution_mode
-    options["execution_mode"] = mode
+    options = dict(TUNED[args.config])
+    if args.mode:
+        options["execution_mode"] = args.mode
+        if args.mode != TUNED[args.config]["execution_mode"]:
+            options.pop("resident_waves_per_cu", None)
+            options.pop("dependence_protocol", None)
     if args.tpb:
         options["threads_per_block"] = args.tpb
     if args.lanes:
@@ -48,7 +77,6 @@ def build_solver(work, args):
         return sptrsv.compile_sptrsv_csc(**options)
     if work.kind == "sptrsv_csr":
         return sptrsv.compile_sptrsv_csr(**options)
-    options.setdefault("thread_unroll", 1)
     return spilu0.compile_ilu0_csr(**options)
 
 
@@ -181,8 +209,8 @@ def main():
     call.synchronize()
     ms_per_step = elapsed_ms / args.steps
 
-    launches_per_step = plan.dag.levels if schedule.execution_mode == "wavefront" \
-        and not getattr(solver.hip_lowering, "single_launch", False) else 1
+    launches_per_step = (plan.dag.levels
+                         if schedule.execution_mode == "wavefront" else 1)
     gbps = work.algorithmic_bytes / (ms_per_step * 1e-3) / 1e9
     result = {
         "metric": METRIC,
@@ -227,7 +255,10 @@ def main():
     result["roofline"] = {
         "bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBPS,
         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 6),
-        "traffic": None,
+        "traffic": MEASURED_TRAFFIC.get(
+            (args.config, schedule.execution_mode,
+             solver.hip_lowering.dependence_protocol,
+             solver.hip_lowering.task_lanes)),
         "kernel": solver.hip_lowering.kernel_name,
         "launches_per_step": launches_per_step,
         "avg_launch_ms": round(kernel_ms, 6),
