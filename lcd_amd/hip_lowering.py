@@ -684,6 +684,7 @@ class _MappedLoopHooks:
         if unroll == 1:
             lines.append(f"{pad}for ({name} = ({lower}) + _lane; {name} < {upper}; "
                          f"{name} += {lanes}) {{")
+            lines += [f"{pad}    {line}" for line in low._first_iteration_reload]
             lines += body_lines + hook_lines
             lines.append(f"{pad}}}")
         else:
@@ -723,8 +724,10 @@ class HIPLowerer:
                  function_props=None, structural_lookups=(), task_lanes=None,
                  chain_tasks=False, argument_kinds=None,
                  spin_limit=DEFAULT_SPIN_LIMIT, resident_waves_per_cu=None,
-                 spin_sleep=1, promote_own_elements=True):
+                 spin_sleep=1, promote_own_elements=True,
+                 prefetch_node_loads=True):
         self.promote_own_elements = promote_own_elements
+        self.prefetch_node_loads = prefetch_node_loads
         self.resident_waves_per_cu = resident_waves_per_cu
         self.spin_sleep = spin_sleep
         self.loop_iterator = loop_iterator
@@ -815,10 +818,13 @@ class HIPLowerer:
             return []
         pad = "    " * indent
         dependence = self.direct_dependence
-        endpoint = self._emitter.expr(dependence.endpoint)
+        endpoint_node = self._hook_endpoint or dependence.endpoint
+        guard_node = (self._hook_guard if self._hook_endpoint is not None
+                      else dependence.guard)
+        endpoint = self._emitter.expr(endpoint_node)
         lines = [f"{pad}lcd_push_fence();"]
-        if dependence.guard is not None:
-            lines.append(f"{pad}if ({self._emitter.expr(dependence.guard)})")
+        if guard_node is not None:
+            lines.append(f"{pad}if ({self._emitter.expr(guard_node)})")
             lines.append(f"{pad}    lcd_atomic_sub(&dep_count[{endpoint}], 1);")
         else:
             lines.append(f"{pad}lcd_atomic_sub(&dep_count[{endpoint}], 1);")
@@ -880,6 +886,7 @@ class HIPLowerer:
         self._kinds = kinds
         lowered_ids = set()
         written_arrays = self._written_arrays(body)
+        self._all_written = set(written_arrays)
         emitter = _Emitter(
             kinds, self.reductions, lowered_ids,
             coherent_arrays=(written_arrays
@@ -1344,6 +1351,119 @@ class HIPLowerer:
         ast.fix_missing_locations(ast.Module(body=new_body, type_ignores=[]))
         return new_body, prologue, epilogue
 
+    def _hoist_node_loads(self, body, mapped, arguments):
+        """Issue a task's read-only loads before it waits for its producers.
+
+        Loads ``R[e]`` of arrays the kernel never writes whose index depends
+        only on the block iterator and loop-invariant inputs (``Ap[i]``,
+        ``b[i]``, ``Ax[Ap[i]]``) are moved into registers right after the
+        task is fetched (the reference prefetches node loads before its spin,
+        compiler/cuda_lowering.py:1991-2029).  For a top-level distributed
+        loop the loads of each lane's *first* iteration (``Ai[j]``,
+        ``Ax[j]``) are issued there as well, so that after the wait only the
+        data other tasks produce is still to be fetched.
+        """
+        kinds = self._kinds
+        written = self._all_written      # as written by the original loop
+        readonly = {name for name in kinds.arrays if name not in written}
+        invariant = {self.loop_iterator} | {
+            name for name in arguments if name not in kinds.arrays}
+        invariant |= set(self._lifted_parameters)
+        temps = {}          # unparse text -> (temp name, load node)
+        order = []
+        lowerer = self
+
+        def hoistable(node, extra=()):
+            if not (isinstance(node, ast.Subscript)
+                    and isinstance(node.value, ast.Name)
+                    and node.value.id in readonly
+                    and isinstance(node.ctx, ast.Load)):
+                return False
+            allowed = invariant | set(extra) | {
+                name for name, _ in temps.values()
+                if name.startswith("_nl_") or extra}
+            for sub in ast.walk(node.slice):
+                if isinstance(sub, ast.Name) and sub.id not in allowed and (
+                        sub.id not in readonly):
+                    return False
+                if isinstance(sub, ast.Call):
+                    return False
+            return True
+
+        class Hoist(ast.NodeTransformer):
+            def __init__(self, prefix, extra=()):
+                self.prefix = prefix
+                self.extra = extra
+
+            def visit_Subscript(self, node):
+                node = self.generic_visit(node)   # innermost first
+                if not hoistable(node, self.extra):
+                    return node
+                text = ast.unparse(node)
+                if text not in temps:
+                    name = f"{self.prefix}{len(temps)}"
+                    temps[text] = (name, deepcopy(node))
+                    order.append(text)
+                    kinds.locals[name] = kinds.arrays.get(node.value.id, FLOAT)
+                return ast.copy_location(
+                    ast.Name(id=temps[text][0], ctx=ast.Load()), node)
+
+        def visit_unconditional(statement, transformer):
+            if isinstance(statement, ast.Assign):
+                statement.value = transformer.visit(statement.value)
+                for target in statement.targets:
+                    if isinstance(target, ast.Subscript):
+                        target.slice = transformer.visit(target.slice)
+            elif isinstance(statement, ast.AugAssign):
+                statement.value = transformer.visit(statement.value)
+                if isinstance(statement.target, ast.Subscript):
+                    statement.target.slice = transformer.visit(
+                        statement.target.slice)
+            return statement
+
+        node_hoist = Hoist("_nl_")
+        for statement in body:
+            if statement is mapped:
+                mapped.iter.args = [node_hoist.visit(a) for a in mapped.iter.args]
+                for inner in mapped.body:
+                    visit_unconditional(inner, node_hoist)
+            else:
+                visit_unconditional(statement, node_hoist)
+        node_count = len(order)
+        first_iteration = []
+        if (mapped is not None and mapped in body
+                and self.thread_unroll_factor == 1 and len(mapped.iter.args) == 2):
+            lane_hoist = Hoist("_pf_", extra=(mapped.target.id,))
+            for inner in mapped.body:
+                visit_unconditional(inner, lane_hoist)
+            first_iteration = order[node_count:]
+            if self.direct_dependence is not None and first_iteration:
+                dependence = self.direct_dependence
+                self._hook_endpoint = lane_hoist.visit(deepcopy(dependence.endpoint))
+                self._hook_guard = (lane_hoist.visit(deepcopy(dependence.guard))
+                                    if dependence.guard is not None else None)
+                # the hook may not create new prefetches
+                first_iteration = order[node_count:]
+        elif self.direct_dependence is not None:
+            pass
+        emitter = self._emitter
+        prefetch = [f"{temps[text][0]} = {emitter.expr(temps[text][1])};"
+                    for text in order[:node_count]]
+        self._own_registers.extend(temps[text][0] for text in order)
+        reload_lines = []
+        if first_iteration:
+            lower, upper, _ = emitter.range_parts(mapped)
+            it = mapped.target.id
+            loads = " ".join(
+                f"{temps[text][0]} = {emitter.expr(temps[text][1])};"
+                for text in first_iteration)
+            prefetch.append(f"{it} = ({lower}) + _lane;")
+            prefetch.append(f"if ({it} < {upper}) {{ {loads} }}")
+            reload_lines = [f"if ({it} != ({lower}) + _lane) {{ {loads} }}"]
+        self._first_iteration_reload = reload_lines
+        ast.fix_missing_locations(ast.Module(body=body, type_ignores=[]))
+        return body, prefetch
+
     def _task_body(self, body, emitter, local_names, target_loop, arguments):
         """C++ lines of one task (indent level 0), `i` already bound."""
         mapped = self._find_mapped_loop(body)
@@ -1364,6 +1484,12 @@ class HIPLowerer:
         if self.promote_own_elements:
             body, prologue, epilogue = self._promote_own_elements(
                 body, mapped, hooks, arguments)
+        self._hook_endpoint = self._hook_guard = None
+        self._first_iteration_reload = []
+        self._prefetch_lines = []
+        if self.prefetch_node_loads:
+            body, self._prefetch_lines = self._hoist_node_loads(
+                body, mapped, arguments)
         if mapped is not None and self.task_lanes > 1:
             body = self._guard_stores(body, mapped)
         self._partials = hooks.partials if hooks else []
@@ -1519,9 +1645,14 @@ class HIPLowerer:
         lines += self._declarations(local_names, 1)
         guard = self._node_guard(target_loop)
 
+        prefetch = list(self._prefetch_lines)
+        self._prefetch_guard = guard
+
         def task(indent):
             pad = "    " * indent
             out = [f"{pad}if ({guard}) {{"]
+            if self.execution_mode != "sync_free":
+                out += [pad + "    " + line for line in prefetch]
             out += [pad + "    " + line for line in task_body]
             out.append(f"{pad}}}")
             return out
@@ -1581,6 +1712,9 @@ class HIPLowerer:
                 "        __syncthreads();",
                 "        if (_task >= _task_count) return;",
                 f"        {it} = (lcd_index_t)task_nodes[_task];",
+                f"        if ({self._prefetch_guard}) {{",
+                *[f"            {line}" for line in self._prefetch_lines],
+                "        }",
                 "        if (threadIdx.x == 0) {",
                 "            long long _spins = 0;",
                 "            int _ok = 1;",
@@ -1628,6 +1762,13 @@ class HIPLowerer:
             "        const int _task = _base + (int)(threadIdx.x & 63) / LCD_TASK_LANES;",
             "        bool _pending = _task < _task_count;",
             f"        {it} = _pending ? (lcd_index_t)task_nodes[_task] : 0;",
+            f"        if (_pending && ({self._prefetch_guard})) {{",
+            *[f"            {line}" for line in self._prefetch_lines],
+            "        }",
+            *(["        int _release_begin = 0, _release_end = 0;",
+               f"        if (_pending) {{ _release_begin = dag_ptr[{it}]; "
+               f"_release_end = dag_ptr[{it} + 1]; }}"]
+              if protocol == COUNTER_DEPENDENCE else []),
             "        long long _spins = 0;",
             "        while (__ballot(_pending)) {",
             "            if (_pending) {",
@@ -1644,8 +1785,8 @@ class HIPLowerer:
             lines += [
                 f"                    {self.group_sync}",
                 "                    lcd_release_fence();",
-                f"                    for (int _e = dag_ptr[{it}] + _lane; "
-                f"_e < dag_ptr[{it} + 1]; _e += LCD_TASK_LANES)",
+                "                    for (int _e = _release_begin + _lane; "
+                "_e < _release_end; _e += LCD_TASK_LANES)",
                 "                        lcd_atomic_sub(&dep_count[dag_index[_e]], 1);",
             ]
         elif protocol == PULL_DEPENDENCE:
@@ -1785,7 +1926,8 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
                  function_props=None, structural_lookups=(), task_lanes=None,
                  chain_tasks=False, argument_kinds=None,
                  spin_limit=DEFAULT_SPIN_LIMIT, resident_waves_per_cu=None,
-                 spin_sleep=1, promote_own_elements=True):
+                 spin_sleep=1, promote_own_elements=True,
+                 prefetch_node_loads=True):
     """HIP counterpart of ``lower_to_numba_cuda``
     (compiler/cuda_lowering.py:2854-2884); same parameters plus
     ``task_lanes`` (lanes cooperating on one task, a power of two <= 64),
@@ -1803,5 +1945,6 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
         structural_lookups=structural_lookups, task_lanes=task_lanes,
         chain_tasks=chain_tasks, argument_kinds=argument_kinds,
         spin_limit=spin_limit, resident_waves_per_cu=resident_waves_per_cu,
-        spin_sleep=spin_sleep, promote_own_elements=promote_own_elements)
+        spin_sleep=spin_sleep, promote_own_elements=promote_own_elements,
+        prefetch_node_loads=prefetch_node_loads)
     return lowerer.lower(code)

@@ -626,12 +626,26 @@ class CompiledHIPModule:
     def code_for(self, options=()):
         key = tuple(options)
         if key not in self.code_objects:
+            source = self.lowering.source
+            # developer aids: LCD_HIP_DUMP_DIR writes every generated module,
+            # LCD_HIP_OVERRIDE_DIR/<kernel>.hip replaces one with edited text
+            dump = os.environ.get("LCD_HIP_DUMP_DIR")
+            if dump:
+                os.makedirs(dump, exist_ok=True)
+                with open(os.path.join(
+                        dump, self.lowering.kernel_name + ".hip"), "w") as out:
+                    out.write(source)
+            override = os.environ.get("LCD_HIP_OVERRIDE_DIR")
+            if override:
+                path = os.path.join(override, self.lowering.kernel_name + ".hip")
+                if os.path.exists(path):
+                    with open(path) as handle:
+                        source = handle.read()
             digest = hashlib.blake2b(
-                (self.lowering.source + "\0".join(key)).encode(),
+                (source + "\0".join(key)).encode(),
                 digest_size=8).hexdigest()
             code, _ = compile_code(
-                self.lowering.source,
-                f"{self.lowering.function_name}_{digest}.hip", key)
+                source, f"{self.lowering.function_name}_{digest}.hip", key)
             self.code_objects[key] = code
         return self.code_objects[key]
 

@@ -383,9 +383,16 @@ def test_csc_argument_lists_and_protocols():
     assert result.task_lanes == 64 and result.tasks_per_block == 2
     # the task's own element lives in a register: computed by every lane,
     # read by the distributed loop, stored once by lane 0
-    assert "_lcd_own_0 = ((b[i] - _lcd_own_0) / Ax[Ap[i]]);" in (
+    # read-only node loads are issued before the task waits
+    for line in ("_nl_0 = b[i];", "_nl_1 = Ap[i];", "_nl_2 = Ax[_nl_1];",
+                 "_nl_3 = Ap[(i + 1)];",
+                 "if (j < _nl_3) { _pf_4 = Ax[j]; _pf_5 = Ai[j]; }"):
+        assert line in result.kernel_source
+    assert result.kernel_source.index("_nl_0 = b[i];") < (
+        result.kernel_source.index("lcd_load_relaxed(&dep_count[i])"))
+    assert "_lcd_own_0 = ((_nl_0 - _lcd_own_0) / _nl_2);" in (
         result.kernel_source)
-    assert "lcd_atomic_add(&x[Ai[j]], (Ax[j] * _lcd_own_0));" in (
+    assert "lcd_atomic_add(&x[_pf_5], (_pf_4 * _lcd_own_0));" in (
         result.kernel_source)
     # sync-free kernels reach arrays that other tasks write through
     # device-scope accessors
@@ -393,11 +400,12 @@ def test_csc_argument_lists_and_protocols():
     assert "if (_lane == 0) lcd_st(&x[i], _lcd_own_0);" in result.kernel_source
     unpromoted = lower(module, execution_mode="sync_free",
                        thread_loop_iterator="j", n_warp=1,
-                       dependence_protocol="push", promote_own_elements=False)
+                       dependence_protocol="push", promote_own_elements=False,
+                       prefetch_node_loads=False)
     assert "lcd_atomic_add(&x[Ai[j]], (Ax[j] * lcd_ld(&x[i])));" in (
         unpromoted.kernel_source)
-    assert "lcd_atomic_sub(&dep_count[Ai[j]], 1);" in result.kernel_source
-    assert "if ((Ai[j] > i))" in result.kernel_source
+    assert "lcd_atomic_sub(&dep_count[_pf_5], 1);" in result.kernel_source
+    assert "if ((_pf_5 > i))" in result.kernel_source
     assert "lcd_load_relaxed(&dep_count[i]) == LCD_READY_COUNT" in (
         result.kernel_source)
     assert "dag_ptr" not in result.kernel_source
