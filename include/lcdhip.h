@@ -188,6 +188,8 @@ typedef struct {
 #define LCDHIP_DAG_LEVELS 1u        /* also build level sets / wavefronts */
 #define LCDHIP_DAG_FORCE_KAHN 2u    /* use the frontier algorithm even when
                                        every edge goes low id -> high id */
+#define LCDHIP_DAG_INCOMING 4u      /* also list, per destination, the
+                                       positions p that produce its edges */
 
 typedef struct {
     int64_t n;
@@ -207,6 +209,14 @@ typedef struct {
 #define LCDHIP_DAG_LEVEL_OF 4       /* n: level, -1 = unscheduled */
 #define LCDHIP_DAG_WAVEFRONTS 5     /* scheduled: nodes by (level, id) */
 #define LCDHIP_DAG_WAVEFRONT_PTR 6  /* levels + 1 */
+/* With LCDHIP_DAG_INCOMING: for destination v the positions
+ * in_pos[in_ptr[v] .. in_ptr[v+1]) of the rule's index array whose entries
+ * produce an edge into v, ordered by (source, position), duplicates kept
+ * (in_ptr is the scan of EDGE_COUNT).  Positions of rule r are offset by the
+ * sum of idx_size of the rules before it.  The mailbox protocol delivers one
+ * message per position. */
+#define LCDHIP_DAG_IN_PTR 7         /* n + 1 */
+#define LCDHIP_DAG_IN_POS 8         /* candidate edges */
 
 int lcdhip_dag_build(const lcdhip_dag_rule *rules, int rule_count, int64_t n,
                      uint32_t flags, lcdhip_stream stream, lcdhip_dag **out);

@@ -24,9 +24,9 @@ using lcdhip::set_error;
 
 struct lcdhip_dag {
     lcdhip_dag_info info{};
-    int32_t *arrays[7] = {nullptr, nullptr, nullptr, nullptr,
-                          nullptr, nullptr, nullptr};
-    int64_t counts[7] = {0, 0, 0, 0, 0, 0, 0};
+    int32_t *arrays[9] = {nullptr, nullptr, nullptr, nullptr, nullptr,
+                          nullptr, nullptr, nullptr, nullptr};
+    int64_t counts[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
 };
 
 namespace {
@@ -107,6 +107,20 @@ __global__ void split_edges_kernel(const unsigned long long *__restrict__ keys,
     if (transposed)
         transposed[e] = (static_cast<unsigned long long>(dst) << 32) |
                         static_cast<unsigned long long>(src);
+}
+
+// (dst << 32 | src) keys with their position for every valid candidate.
+__global__ void incoming_keys_kernel(const unsigned long long *__restrict__ keys,
+                                     int64_t capacity,
+                                     unsigned long long *__restrict__ out_keys,
+                                     int32_t *__restrict__ out_positions)
+{
+    int64_t p = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (p >= capacity)
+        return;
+    unsigned long long key = keys[p];
+    out_positions[p] = static_cast<int32_t>(p);
+    out_keys[p] = key == ~0ull ? key : ((key << 32) | (key >> 32));
 }
 
 __global__ void low_words_kernel(const unsigned long long *__restrict__ keys,
@@ -386,6 +400,58 @@ extern "C" int lcdhip_dag_build(const lcdhip_dag_rule *rules, int rule_count,
     }
     dag->info.topological_ids = host_flags[1] ? 0 : 1;
 
+    if (flags & LCDHIP_DAG_INCOMING) {
+        // in_ptr = scan of the multiplicities; in_pos = positions stably
+        // sorted by (dst, src): ties keep ascending position
+        if ((status = dag_alloc(dag, LCDHIP_DAG_IN_PTR, n + 1))) return status;
+        if ((status = dag_alloc(dag, LCDHIP_DAG_IN_POS,
+                                static_cast<int64_t>(candidates))))
+            return status;
+        int32_t *in_ptr = dag->arrays[LCDHIP_DAG_IN_PTR];
+        LCDHIP_CHECK(hipMemsetAsync(in_ptr, 0, (n + 1) * 4, stream));
+        if (n > 0) {
+            size_t scan_bytes = 0;
+            char *scan_temp = nullptr;
+            LCDHIP_CHECK(rocprim::exclusive_scan(
+                nullptr, scan_bytes, edge_count, in_ptr, 0,
+                static_cast<size_t>(n), rocprim::plus<int32_t>(), stream));
+            LCDHIP_CHECK(scratch.alloc(&scan_temp, scan_bytes));
+            LCDHIP_CHECK(rocprim::exclusive_scan(
+                scan_temp, scan_bytes, edge_count, in_ptr, 0,
+                static_cast<size_t>(n), rocprim::plus<int32_t>(), stream));
+            int32_t total = static_cast<int32_t>(candidates);
+            LCDHIP_CHECK(hipMemcpyAsync(in_ptr + n, &total, 4,
+                                        hipMemcpyHostToDevice, stream));
+            LCDHIP_CHECK(hipStreamSynchronize(stream));
+        }
+        if (candidates > 0) {
+            unsigned long long *in_keys = nullptr, *in_sorted = nullptr;
+            int32_t *positions = nullptr, *sorted_positions = nullptr;
+            LCDHIP_CHECK(scratch.alloc(&in_keys, key_capacity));
+            LCDHIP_CHECK(scratch.alloc(&in_sorted, key_capacity));
+            LCDHIP_CHECK(scratch.alloc(&positions, key_capacity));
+            LCDHIP_CHECK(scratch.alloc(&sorted_positions, key_capacity));
+            hipLaunchKernelGGL(incoming_keys_kernel,
+                               dim3(blocks_for(key_capacity)), dim3(kBlock), 0,
+                               stream, keys, key_capacity, in_keys, positions);
+            size_t sort_bytes = 0;
+            char *sort_temp = nullptr;
+            LCDHIP_CHECK(rocprim::radix_sort_pairs(
+                nullptr, sort_bytes, in_keys, in_sorted, positions,
+                sorted_positions, static_cast<size_t>(key_capacity), 0, 64,
+                stream));
+            LCDHIP_CHECK(scratch.alloc(&sort_temp, sort_bytes));
+            LCDHIP_CHECK(rocprim::radix_sort_pairs(
+                sort_temp, sort_bytes, in_keys, in_sorted, positions,
+                sorted_positions, static_cast<size_t>(key_capacity), 0, 64,
+                stream));
+            LCDHIP_CHECK(hipMemcpyAsync(dag->arrays[LCDHIP_DAG_IN_POS],
+                                        sorted_positions, candidates * 4,
+                                        hipMemcpyDeviceToDevice, stream));
+            LCDHIP_CHECK(hipStreamSynchronize(stream));
+        }
+    }
+
     // sorted set of (src, dst) pairs
     int64_t edges = 0;
     if (candidates > 0) {
@@ -650,7 +716,7 @@ extern "C" int lcdhip_dag_get_info(const lcdhip_dag *dag, lcdhip_dag_info *out)
 extern "C" int lcdhip_dag_array(const lcdhip_dag *dag, int which, void **d_out,
                                 int64_t *count_out)
 {
-    if (!dag || which < 0 || which > 6 || !d_out || !count_out) {
+    if (!dag || which < 0 || which > 8 || !d_out || !count_out) {
         set_error("bad argument to lcdhip_dag_array");
         return LCDHIP_ERR_ARGUMENT;
     }

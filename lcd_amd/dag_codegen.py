@@ -26,7 +26,9 @@ EXECUTION_MODES = frozenset({"sync_free", "wavefront"})
 COUNTER_DEPENDENCE = "counter"
 PUSH_DEPENDENCE = "push"
 PULL_DEPENDENCE = "pull"
-DEPENDENCE_PROTOCOLS = (COUNTER_DEPENDENCE, PUSH_DEPENDENCE, PULL_DEPENDENCE)
+MAILBOX_DEPENDENCE = "mailbox"   # push edges delivered as per-entry messages
+DEPENDENCE_PROTOCOLS = (COUNTER_DEPENDENCE, PUSH_DEPENDENCE, PULL_DEPENDENCE,
+                        MAILBOX_DEPENDENCE)
 
 
 class DAGCodegenError(Exception):
@@ -214,7 +216,7 @@ def node_count_value(plan, argument_values):
 
 
 def build_device_dag(plan, argument_values, device=None, levels=True,
-                     force_kahn=False):
+                     force_kahn=False, incoming=False):
     """Run the on-device inspector for concrete inputs -> ``DeviceDag``."""
     from lcd_amd import hip_runtime
 
@@ -223,7 +225,7 @@ def build_device_dag(plan, argument_values, device=None, levels=True,
         return device.dag_build(
             device_rules(plan, argument_values),
             node_count_value(plan, argument_values), levels=levels,
-            force_kahn=force_kahn)
+            force_kahn=force_kahn, incoming=incoming)
     except hip_runtime.HIPRuntimeError as error:
         if error.code == hip_runtime.ERR_DAG_BOUNDS:
             from lcd_amd.dag_preprocessing import DAGPreprocessingError
@@ -284,6 +286,7 @@ def direct_dependence(plan, thread_iterator, validate_endpoints=False):
 
 __all__ = [
     "COUNTER_DEPENDENCE", "PUSH_DEPENDENCE", "PULL_DEPENDENCE",
+    "MAILBOX_DEPENDENCE",
     "DEPENDENCE_PROTOCOLS", "DAGCodegenError", "DAGPlan", "DirectDependence",
     "EdgeRule", "GUARD_GREATER", "GUARD_NONE", "GUARD_NOT_EQUAL",
     "build_device_dag", "compile_dag_builder", "create_dag_plan",

@@ -252,7 +252,7 @@ def band_chains(nodes, level_ptr, dag_ptr, dag_index, band_width):
 
 
 def execution_data_from_device_dag(dag, execution_mode, warp_mapped,
-                                   pushed=False, band_width=1):
+                                   pushed=False, band_width=1, mailbox=False):
     """Executor arrays straight from the on-device inspector (no host copy
     except the level offsets the launcher iterates over)."""
     if band_width != 1:
@@ -264,6 +264,15 @@ def execution_data_from_device_dag(dag, execution_mode, warp_mapped,
             "Wavefront scheduling did not cover every DAG node; the DAG may "
             f"contain a cycle. Scheduled {dag.scheduled} of {dag.n} nodes.")
     counts = dag.array("edge_count" if pushed else "dep_count")
+    if mailbox:
+        # per destination: the positions whose entries send it a message
+        auxiliary = {"_lcd_in_ptr": dag.array("in_ptr"),
+                     "_lcd_in_pos": dag.array("in_pos")}
+        return WarpTaskExecutionData(
+            task_nodes=dag.array("wavefronts"), task_ptr=None,
+            band_ptr=dag.host("wavefront_ptr"), dep_count=counts,
+            initial_dep_count=counts, dag_ptr=dag.array("dag_ptr"),
+            dag_index=dag.array("dag_index"), auxiliary_values=auxiliary)
     if warp_mapped or execution_mode.replace("-", "_") == "sync_free":
         return WarpTaskExecutionData(
             task_nodes=dag.array("wavefronts"), task_ptr=None,

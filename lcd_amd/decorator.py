@@ -29,6 +29,7 @@ import numpy as np
 from lcd_amd import hip_runtime
 from lcd_amd.dag_codegen import (
     COUNTER_DEPENDENCE,
+    MAILBOX_DEPENDENCE,
     PUSH_DEPENDENCE,
     build_device_dag,
     compile_dag_builder,
@@ -230,7 +231,10 @@ def parallel(**kwargs):
         fixed_schedule = (schedule_space.fixed_schedule()
                           if schedule_space.is_fixed else None)
         edge_multiplicity = any(
-            configuration[4] == PUSH_DEPENDENCE
+            configuration[4] in (PUSH_DEPENDENCE, MAILBOX_DEPENDENCE)
+            for configuration in schedule_space.configurations())
+        incoming_positions = any(
+            configuration[4] == MAILBOX_DEPENDENCE
             for configuration in schedule_space.configurations())
         inspector_mode = (execution_mode if fixed_schedule is not None
                           else SYNC_FREE)
@@ -317,7 +321,7 @@ def parallel(**kwargs):
             lookup_values = materialize_structural_lookups(
                 structural_lookups, device_values, device)
             dag = build_device_dag(dag_plan, device_values, device,
-                                   levels=True)
+                                   levels=True, incoming=incoming_positions)
             if fixed_schedule is not None:
                 schedule = fixed_schedule
                 features = None
@@ -333,7 +337,8 @@ def parallel(**kwargs):
             execution_data = execution_data_from_device_dag(
                 dag, schedule.execution_mode, lowering.warp_mapped,
                 pushed=lowering.dependence_protocol == PUSH_DEPENDENCE,
-                band_width=band_width)
+                band_width=band_width,
+                mailbox=lowering.dependence_protocol == MAILBOX_DEPENDENCE)
             plan = SchedulePlan(
                 schedule=schedule,
                 execution_data=attach_auxiliary_values(

@@ -48,7 +48,9 @@ class UnsupportedAtomicOperation(HIPLoweringError):
 COUNTER_DEPENDENCE = "counter"
 PUSH_DEPENDENCE = "push"
 PULL_DEPENDENCE = "pull"
-DEPENDENCE_PROTOCOLS = (COUNTER_DEPENDENCE, PUSH_DEPENDENCE, PULL_DEPENDENCE)
+MAILBOX_DEPENDENCE = "mailbox"
+DEPENDENCE_PROTOCOLS = (COUNTER_DEPENDENCE, PUSH_DEPENDENCE, PULL_DEPENDENCE,
+                        MAILBOX_DEPENDENCE)
 
 HIP_EXECUTION_MODES = frozenset({"plain", "sync_free", "wavefront"})
 WAVEFRONT_SIZE = 64
@@ -60,12 +62,15 @@ PUSH_ARGUMENTS = ("dep_count", "initial_dep_count", "task_nodes", "task_ptr",
                   "task_counter", "task_count")
 PULL_ARGUMENTS = ("done", "task_nodes", "task_ptr", "task_counter",
                   "task_count")
+MAILBOX_ARGUMENTS = ("_lcd_mailbox", "_lcd_in_ptr", "_lcd_in_pos",
+                     "task_nodes", "task_ptr", "task_counter", "task_count")
 WAVEFRONT_ARGUMENTS = ("task_nodes", "task_ptr", "band_start", "band_end")
 STATUS_ARGUMENT = "_lcd_status"
 HOST_LAUNCH_ARGUMENTS = frozenset({"band_ptr", "wavefront_ptr"})
 INTEGER_EXECUTOR_ARRAYS = frozenset({
     "dep_count", "initial_dep_count", "dag_ptr", "dag_index", "task_nodes",
-    "task_ptr", "task_counter", "done", STATUS_ARGUMENT,
+    "task_ptr", "task_counter", "done", STATUS_ARGUMENT, "_lcd_in_ptr",
+    "_lcd_in_pos",
 })
 DEFAULT_SPIN_LIMIT = 1 << 22
 
@@ -122,6 +127,7 @@ class HIPLoweringResult:
     zero_initialised: dict = field(default_factory=dict)  # lifted -> shape src
     persistent: bool = False
     function_name: str = ""
+    mailbox_index_array: str | None = None
 
     @property
     def module_source(self):
@@ -241,6 +247,7 @@ class _Kinds:
             self.arrays[name] = INT if name in demanded else FLOAT
         for name in INTEGER_EXECUTOR_ARRAYS:
             self.arrays[name] = INT
+        self.arrays["_lcd_mailbox"] = FLOAT
         for name, kind in (forced or {}).items():
             if name in self.arrays:
                 self.arrays[name] = kind
@@ -325,6 +332,8 @@ class _Emitter:
         # arrays other tasks write while this kernel runs: every access goes
         # through device-scope (cache-bypassing / write-through) accessors
         self.coherent_arrays = set(coherent_arrays)
+        self.mailbox = None
+        self.lowerer = None
 
     # ---- expressions
     def expr(self, node):
@@ -460,7 +469,21 @@ class _Emitter:
             raise HIPLoweringError(
                 "Device atomics require an indexed 1-D array target.")
         self.lowered_ids.add(statement_id)
-        return f"{call}(&{self.element(node.target)}, {self.expr(node.value)});"
+        atomic = f"{call}(&{self.element(node.target)}, {self.expr(node.value)});"
+        box = self.mailbox
+        if box is not None and node.target.value.id == box["array"]:
+            # one message per position instead of an atomic update; the
+            # consumer adds the messages in source order
+            value = self.expr(node.value)
+            if operator == "-":
+                value = f"(-({value}))"
+            slot = self.expr(box["slot"])
+            store = f"lcd_st(&_lcd_mailbox[{slot}], {value});"
+            guard = self.lowerer.mailbox_guard_text()
+            if guard is None:
+                return store
+            return f"if ({guard}) {store} else {atomic}"
+        return atomic
 
     def stmt(self, node, indent, hooks=None):
         pad = "    " * indent
@@ -594,6 +617,13 @@ template <class T> __device__ __forceinline__ T lcd_ld(const T* p) {
 }
 template <class T, class V> __device__ __forceinline__ void lcd_st(T* p, V v) {
     __hip_atomic_store(p, (T)v, __ATOMIC_RELAXED, LCD_AGENT);
+}
+// Mailbox protocol: a slot holds this quiet-NaN bit pattern until its message
+// (a finite product) has been stored; both 32-bit halves are equal so a
+// 32-bit fill resets the buffer.
+#define LCD_EMPTY_WORD 0x7FF84C43u
+__device__ __forceinline__ bool lcd_is_empty(double v) {
+    return __double_as_longlong(v) == (long long)0x7FF84C437FF84C43ull;
 }
 // Release: every store/atomic this wavefront issued has completed at the
 // coherence point before anything after the fence is issued.
@@ -794,16 +824,75 @@ class HIPLowerer:
             thread_loop_iterator is not None and not self.block_task
             and self.execution_mode in {"sync_free", "wavefront"})
         self.direct_dependence = direct_dependence
+        required_kind = (PUSH_DEPENDENCE
+                         if dependence_protocol == MAILBOX_DEPENDENCE
+                         else dependence_protocol)
         self.dependence_protocol = (
             dependence_protocol
             if (direct_dependence is not None
-                and direct_dependence.kind == dependence_protocol
+                and direct_dependence.kind == required_kind
                 and self.warp_mapped and self.execution_mode == "sync_free"
                 and sync_free_ready_count == 0)
             else COUNTER_DEPENDENCE)
+        self._mailbox = None
         self.group_sync = (_GROUP_SYNC_BLOCK if self.block_task
                            else _GROUP_SYNC_WAVE)
         self.segmented_sorted = segmented_array_pairs(self.function_props)
+
+    # ---- mailbox protocol
+    def _mailbox_plan(self, body):
+        """The mailbox protocol applies when the loop's only cross-task
+        writes are ``X[endpoint] +=/-= value`` inside the top level of the
+        distributed loop, the endpoint is the push dependence's, and the task
+        reads and rewrites its own ``X[i]`` at the top level."""
+        dependence = self.direct_dependence
+        endpoint = dependence.endpoint
+        if not (isinstance(endpoint, ast.Subscript)
+                and isinstance(endpoint.value, ast.Name)):
+            return None
+        mapped = self._find_mapped_loop(body)
+        if mapped is None or mapped not in body:
+            return None
+        sites = [node for statement in body for node in ast.walk(statement)
+                 if isinstance(node, ast.AugAssign)
+                 and (node.lineno, node.col_offset) in self.reductions]
+        if not sites or len(sites) != len(self.reductions):
+            return None
+        arrays = set()
+        for site in sites:
+            if site not in mapped.body:
+                return None
+            if not isinstance(site.op, (ast.Add, ast.Sub)):
+                return None
+            if not (isinstance(site.target, ast.Subscript)
+                    and isinstance(site.target.value, ast.Name)
+                    and ast.unparse(site.target.slice) == ast.unparse(endpoint)):
+                return None
+            arrays.add(site.target.value.id)
+        if len(arrays) != 1:
+            return None
+        array = arrays.pop()
+        own_text = f"{array}[{self.loop_iterator}]"
+        rewritten = False
+        for statement in body:
+            if statement is mapped:
+                continue
+            if (isinstance(statement, ast.Assign) and len(statement.targets) == 1
+                    and ast.unparse(statement.targets[0]) == own_text
+                    and any(ast.unparse(n) == own_text
+                            for n in ast.walk(statement.value)
+                            if isinstance(n, ast.Subscript))):
+                rewritten = True
+        if not rewritten:
+            return None
+        return {"array": array, "slot": deepcopy(endpoint.slice),
+                "index_array": endpoint.value.id, "own_text": own_text}
+
+    def mailbox_guard_text(self):
+        dependence = self.direct_dependence
+        guard = (self._hook_guard if self._hook_endpoint is not None
+                 else dependence.guard)
+        return None if guard is None else self._emitter.expr(guard)
 
     # ---- helpers used by the hooks
     def group_total(self, partial):
@@ -887,10 +976,18 @@ class HIPLowerer:
         lowered_ids = set()
         written_arrays = self._written_arrays(body)
         self._all_written = set(written_arrays)
-        emitter = _Emitter(
-            kinds, self.reductions, lowered_ids,
-            coherent_arrays=(written_arrays
-                             if self.execution_mode == "sync_free" else ()))
+        if self.dependence_protocol == MAILBOX_DEPENDENCE:
+            self._mailbox = self._mailbox_plan(body)
+            if self._mailbox is None:
+                self.dependence_protocol = PUSH_DEPENDENCE
+        coherent = set(written_arrays) if self.execution_mode == "sync_free" else set()
+        if self._mailbox is not None:
+            # only a task itself touches its element of the reduced array
+            coherent.discard(self._mailbox["array"])
+        emitter = _Emitter(kinds, self.reductions, lowered_ids,
+                           coherent_arrays=coherent)
+        emitter.mailbox = self._mailbox
+        emitter.lowerer = self
         self._emitter = emitter
 
         user_arguments = list(arguments)
@@ -980,6 +1077,8 @@ class HIPLowerer:
             zero_initialised=zero_initialised,
             persistent=self.execution_mode == "sync_free",
             function_name=function_name,
+            mailbox_index_array=(self._mailbox["index_array"]
+                                 if self._mailbox else None),
         )
 
     # ---- structure discovery
@@ -1090,6 +1189,8 @@ class HIPLowerer:
                 names = list(PUSH_ARGUMENTS)
             elif self.dependence_protocol == PULL_DEPENDENCE:
                 names = list(PULL_ARGUMENTS)
+            elif self.dependence_protocol == MAILBOX_DEPENDENCE:
+                names = list(MAILBOX_ARGUMENTS)
             else:
                 names = list(SYNC_FREE_ARGUMENTS)
             return names + [STATUS_ARGUMENT]
@@ -1340,6 +1441,8 @@ class HIPLowerer:
         prologue, epilogue = [], []
         emitter = self._emitter
         for array, index_text, name, target in promoted.values():
+            self._own_map[f"{array}[{index_text}]"] = (
+                name, first_access.get(name, "read"))
             self._kinds.locals[name] = self._kinds.arrays.get(array, FLOAT)
             self._own_registers.append(name)
             load_node = ast.Subscript(
@@ -1469,6 +1572,7 @@ class HIPLowerer:
         mapped = self._find_mapped_loop(body)
         hooks = None
         self._own_registers = []
+        self._own_map = {}
         self._pending_sync = False
         if mapped is not None:
             hooks = _MappedLoopHooks(self, emitter, mapped)
@@ -1490,6 +1594,17 @@ class HIPLowerer:
         if self.prefetch_node_loads:
             body, self._prefetch_lines = self._hoist_node_loads(
                 body, mapped, arguments)
+        if self._mailbox is not None:
+            own = self._own_map.get(self._mailbox["own_text"])
+            if own is None or own[1] != "read":
+                raise HIPLoweringError(
+                    "The mailbox protocol needs the task's own element of "
+                    f"{self._mailbox['array']!r} in a register.")
+            self._mailbox["register"] = own[0]
+            # nobody else writes the own element: its initial value is loaded
+            # with the other node loads, before the wait
+            self._prefetch_lines = list(self._prefetch_lines) + list(prologue)
+            prologue = []
         if mapped is not None and self.task_lanes > 1:
             body = self._guard_stores(body, mapped)
         self._partials = hooks.partials if hooks else []
@@ -1589,7 +1704,8 @@ class HIPLowerer:
     def _signature(self, kernel_arguments, array_arguments, scalar_arguments,
                    written_arrays):
         parts = []
-        mutable_executor = {"dep_count", "task_counter", "done", STATUS_ARGUMENT}
+        mutable_executor = {"dep_count", "task_counter", "done",
+                            STATUS_ARGUMENT, "_lcd_mailbox"}
         for name in kernel_arguments:
             if name in array_arguments:
                 const = (name not in written_arrays
@@ -1769,12 +1885,20 @@ class HIPLowerer:
                f"        if (_pending) {{ _release_begin = dag_ptr[{it}]; "
                f"_release_end = dag_ptr[{it} + 1]; }}"]
               if protocol == COUNTER_DEPENDENCE else []),
+            *(["        int _mb_next = 0, _mb_end = 0, _mb_slot = -1;",
+               f"        if (_pending) {{ _mb_next = _lcd_in_ptr[{it}]; "
+               f"_mb_end = _lcd_in_ptr[{it} + 1]; "
+               "if (_mb_next + _lane < _mb_end) "
+               "_mb_slot = _lcd_in_pos[_mb_next + _lane]; }"]
+              if protocol == MAILBOX_DEPENDENCE else []),
             "        long long _spins = 0;",
             "        while (__ballot(_pending)) {",
             "            if (_pending) {",
         ]
         if protocol == PULL_DEPENDENCE:
             lines += self._pull_ready_lines(4)
+        elif protocol == MAILBOX_DEPENDENCE:
+            lines += self._mailbox_ready_lines(4)
         else:
             lines.append(f"                const bool _ready = "
                          f"lcd_load_relaxed(&dep_count[{it}]) == LCD_READY_COUNT;")
@@ -1815,6 +1939,36 @@ class HIPLowerer:
         lines.insert(1, "    bool _task_aborted = false;")
         return lines
 
+    def _mailbox_ready_lines(self, indent):
+        """Readiness for the mailbox protocol: every incoming message has
+        arrived.  Lane ``l`` of the group polls message ``next + l``; arrived
+        messages are added to the task's own element in (source, position)
+        order -- the order of the sequential loop -- by broadcasting them
+        lane by lane, so the sum is deterministic."""
+        pad = "    " * indent
+        own = self._mailbox["register"]
+        return [
+            f"{pad}bool _ready = _mb_next == _mb_end;",
+            f"{pad}if (!_ready) {{",
+            f"{pad}    const double _mb_value = _mb_slot >= 0 ? "
+            "lcd_ld(&_lcd_mailbox[_mb_slot]) : 0.0;",
+            f"{pad}    const int _mb_have = (_mb_end - _mb_next) < LCD_TASK_LANES ? "
+            "(_mb_end - _mb_next) : LCD_TASK_LANES;",
+            f"{pad}    int _mb_k = 0;",
+            f"{pad}    for (; _mb_k < _mb_have; ++_mb_k) {{",
+            f"{pad}        const double _mb_in = __shfl(_mb_value, _mb_k, LCD_TASK_LANES);",
+            f"{pad}        if (lcd_is_empty(_mb_in)) break;",
+            f"{pad}        {own} = {own} + _mb_in;",
+            f"{pad}    }}",
+            f"{pad}    if (_mb_k > 0) {{",
+            f"{pad}        _mb_next += _mb_k;",
+            f"{pad}        _mb_slot = (_mb_next + _lane < _mb_end) ? "
+            "_lcd_in_pos[_mb_next + _lane] : -1;",
+            f"{pad}    }}",
+            f"{pad}    _ready = _mb_next == _mb_end;",
+            f"{pad}}}",
+        ]
+
     def _pull_ready_lines(self, indent):
         """Readiness for the pull protocol: every producer this task reads
         from (the endpoint of the direct dependence over the mapped loop's
@@ -1842,7 +1996,13 @@ class HIPLowerer:
     def _reset_kernel_text(self, reset_name):
         """Restores the mutable executor state before every sweep (the
         reference's reset kernel, compiler/cuda_lowering.py:737-853)."""
-        if self.dependence_protocol == PULL_DEPENDENCE:
+        if self.dependence_protocol == MAILBOX_DEPENDENCE:
+            body = ("    if (t < count) { _lcd_mailbox[2 * t] = LCD_EMPTY_WORD; "
+                    "_lcd_mailbox[2 * t + 1] = LCD_EMPTY_WORD; }\n"
+                    "    if (t == 0) { task_counter[0] = 0; }\n")
+            signature = ("unsigned int* _lcd_mailbox, int* task_counter, "
+                         "long long count")
+        elif self.dependence_protocol == PULL_DEPENDENCE:
             body = ("    if (t < count) done[t] = 0;\n"
                     "    if (t == 0) { task_counter[0] = 0; }\n")
             signature = ("int* done, int* task_counter, long long count")
@@ -1893,15 +2053,21 @@ class HIPLowerer:
                 f"{max(1, self.threads_per_block // self.task_lanes)}, "
                 f"{self.threads_per_block}, {call_args}, {start}, {end})")
         else:
-            count_array = ("done" if self.dependence_protocol == PULL_DEPENDENCE
-                           else "dep_count")
+            count_array = {PULL_DEPENDENCE: "done",
+                           MAILBOX_DEPENDENCE: "task_nodes"}.get(
+                               self.dependence_protocol, "dep_count")
+            reset_count = "_count"
             if self.dependence_protocol == PULL_DEPENDENCE:
                 reset_args = "(done, task_counter, _hip.length(done))"
+            elif self.dependence_protocol == MAILBOX_DEPENDENCE:
+                reset_args = ("(_lcd_mailbox, task_counter, "
+                              "_hip.length(_lcd_mailbox))")
+                reset_count = "_hip.length(_lcd_mailbox)"
             else:
                 reset_args = ("(dep_count, initial_dep_count, task_counter, "
                               "_hip.length(dep_count))")
             body.append(f"_count = _hip.length({count_array})")
-            body.append(f"_hip.launch({reset_name!r}, (_count + 255) // 256 or 1, "
+            body.append(f"_hip.launch({reset_name!r}, ({reset_count} + 255) // 256 or 1, "
                         f"256, {reset_args})")
             tasks_per_block = max(1, self.threads_per_block // self.task_lanes)
             body.append(f"_blocks = min((_count + {tasks_per_block} - 1) // "

@@ -35,7 +35,8 @@ STATUS_ARGUMENT = "_lcd_status"
 
 DAG_PTR, DAG_INDEX, DAG_DEP_COUNT, DAG_EDGE_COUNT = 0, 1, 2, 3
 DAG_LEVEL_OF, DAG_WAVEFRONTS, DAG_WAVEFRONT_PTR = 4, 5, 6
-DAG_FLAG_LEVELS, DAG_FLAG_FORCE_KAHN = 1, 2
+DAG_IN_PTR, DAG_IN_POS = 7, 8
+DAG_FLAG_LEVELS, DAG_FLAG_FORCE_KAHN, DAG_FLAG_INCOMING = 1, 2, 4
 
 DEVICE_COMPILE_OPTIONS = (
     "--offload-arch=gfx950", "-O3", "-munsafe-fp-atomics",
@@ -306,7 +307,8 @@ class DeviceDag:
     ARRAYS = {"dag_ptr": DAG_PTR, "dag_index": DAG_INDEX,
               "dep_count": DAG_DEP_COUNT, "edge_count": DAG_EDGE_COUNT,
               "level_of": DAG_LEVEL_OF, "wavefronts": DAG_WAVEFRONTS,
-              "wavefront_ptr": DAG_WAVEFRONT_PTR}
+              "wavefront_ptr": DAG_WAVEFRONT_PTR, "in_ptr": DAG_IN_PTR,
+              "in_pos": DAG_IN_POS}
 
     def __init__(self, device, handle):
         self.device = device
@@ -534,7 +536,8 @@ class HIPDevice:
         keep.append(array)
         return array.pointer, array.size
 
-    def dag_build(self, rules, n, levels=True, force_kahn=False):
+    def dag_build(self, rules, n, levels=True, force_kahn=False,
+                  incoming=False):
         """Run the on-device inspector. ``rules`` are dicts/objects with
         ptr, idx, owner_is_source, lower_offset, upper_offset, guard,
         break_at_owner (ptr/idx host or device arrays)."""
@@ -551,7 +554,8 @@ class HIPDevice:
             slot.guard = int(get("guard"))
             slot.break_at_owner = int(bool(get("break_at_owner")))
         flags = (DAG_FLAG_LEVELS if levels else 0) | (
-            DAG_FLAG_FORCE_KAHN if force_kahn else 0)
+            DAG_FLAG_FORCE_KAHN if force_kahn else 0) | (
+            DAG_FLAG_INCOMING if incoming else 0)
         handle = ctypes.c_void_p()
         _check(self.lib.lcdhip_dag_build(
             array, len(rules), ctypes.c_int64(int(n)), ctypes.c_uint32(flags),
@@ -896,6 +900,13 @@ def prepare_hip_arguments(lowering, argument_values, execution_data,
                 cached = device.empty((n_tasks,), np.int32)
                 workspace[("state", "done")] = cached
             host_values["done"] = cached
+        if "_lcd_mailbox" in lowering.launcher_arguments:
+            slots = len(host_values[lowering.mailbox_index_array])
+            cached = workspace.get(("state", "_lcd_mailbox"))
+            if cached is None or len(cached) != slots:
+                cached = device.empty((slots,), np.float64)
+                workspace[("state", "_lcd_mailbox")] = cached
+            host_values["_lcd_mailbox"] = cached
         for name in ("task_counter", STATUS_ARGUMENT):
             cached = workspace.get(("state", name))
             if cached is None:
@@ -1013,7 +1024,7 @@ def _load_for_values(compiled, lowering, prepared, device):
                                  else _CTYPES[text])
         argument_ctypes = {lowering.kernel_name: ctypes_of}
         if lowering.reset_kernel_name:
-            if lowering.dependence_protocol == "pull":
+            if lowering.dependence_protocol in ("pull", "mailbox"):
                 reset = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
             else:
                 reset = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,

@@ -27,6 +27,7 @@ import numpy as np
 
 from lcd_amd.dag_codegen import (
     COUNTER_DEPENDENCE,
+    MAILBOX_DEPENDENCE,
     PULL_DEPENDENCE,
     PUSH_DEPENDENCE,
 )
@@ -218,6 +219,8 @@ class ScheduleSpace:
         available = (COUNTER_DEPENDENCE,) + (
             (direct_protocol,)
             if thread_mapped and direct_protocol is not None else ())
+        if PUSH_DEPENDENCE in available:
+            available += (MAILBOX_DEPENDENCE,)
         searched = (len(execution_modes) * len(block_sizes)
                     * len(unroll_factors) * len(n_warps) * len(lanes)) > 1
         if dependence_protocol is not None:
@@ -286,7 +289,7 @@ class AnalyticScheduler:
             sync_s = 0.0
         elif execution_mode == SYNC_FREE:
             launch_s = arch.launch_latency_s
-            if dependence_protocol == PUSH_DEPENDENCE:
+            if dependence_protocol in (PUSH_DEPENDENCE, MAILBOX_DEPENDENCE):
                 sync_s = arch.atomic_cost_s * features.rows / n_warp
             elif dependence_protocol == PULL_DEPENDENCE:
                 sync_s = arch.atomic_cost_s * average_in_degree * (

@@ -80,6 +80,37 @@ def test_golden_vectors(device, oracle):
             assert dag.wavefront_list() == case["wavefronts"], case["name"]
 
 
+def test_incoming_positions(device, oracle):
+    """Per destination, the positions whose entries produce its edges, by
+    (source, position), duplicates kept."""
+    rng = np.random.default_rng(3)
+    n = 3000
+    counts = rng.integers(0, 9, n)
+    ptr = np.zeros(n + 1, dtype=np.int32)
+    np.cumsum(counts, out=ptr[1:])
+    idx = rng.integers(0, n, int(ptr[-1])).astype(np.int32)
+    rule = oracle.make_rule(ptr, idx, True, lower_offset=1,
+                            guard=oracle.GUARD_GREATER)
+    dag = device.dag_build([rule], n, levels=True, incoming=True)
+    expected = [[] for _ in range(n)]
+    for seg in range(n):
+        for p in range(ptr[seg] + 1, ptr[seg + 1]):
+            if idx[p] > seg:
+                expected[idx[p]].append((seg, p))
+    in_ptr, in_pos = dag.host("in_ptr"), dag.host("in_pos")
+    np.testing.assert_array_equal(np.diff(in_ptr), dag.host("edge_count"))
+    for v in range(n):
+        want = [p for _, p in sorted(expected[v])]
+        assert in_pos[in_ptr[v]:in_ptr[v + 1]].tolist() == want
+    work = workloads.configuration("c2", nx=12, ny=10, nz=9)
+    dag = device.dag_build([oracle.rule_sptrsv_csc(work.indptr, work.indices)],
+                           work.n, incoming=True)
+    in_ptr, in_pos = dag.host("in_ptr"), dag.host("in_pos")
+    assert in_ptr[-1] == dag.edges == len(in_pos)
+    np.testing.assert_array_equal(work.indices[in_pos],
+                                  np.repeat(np.arange(work.n), np.diff(in_ptr)))
+
+
 def test_random_unsorted_duplicates(device, oracle):
     """Unsorted segments with repeated entries: set semantics + multiplicity."""
     rng = np.random.default_rng(7)

@@ -45,6 +45,12 @@ CSC_VARIANTS = [
          dependence_protocol="counter"),
     dict(execution_mode="wavefront", threads_per_block=128, n_warp=2),
     dict(execution_mode="sync_free", threads_per_block=128, n_warp=2),
+    dict(execution_mode="sync_free", threads_per_block=256, task_lanes=4,
+         dependence_protocol="mailbox"),
+    dict(execution_mode="sync_free", threads_per_block=128, task_lanes=2,
+         dependence_protocol="mailbox", thread_unroll=2),
+    dict(execution_mode="sync_free", threads_per_block=128, n_warp=1,
+         dependence_protocol="mailbox"),
     dict(),   # scheduler decides
 ]
 
@@ -54,12 +60,18 @@ CSC_VARIANTS = [
 def test_sptrsv_csc_variants(oracle, options):
     print("csc", options, flush=True)
     solver = sptrsv.compile_sptrsv_csc(**options)
+    # the mailbox protocol adds the incoming products in the order of the
+    # sequential loop: bit-identical results, not just 1e-12
+    exact = options.get("dependence_protocol") == "mailbox"
     for name, overrides in (("c1", {}), ("c2", dict(nx=20, ny=18, nz=16)),
                             ("c5", dict(n=6000))):
         work = workloads.configuration(name, **overrides)
         expected = oracle.sptrsv_csc(work.indptr, work.indices, work.data,
                                      work.rhs, work.n)
-        solve_and_check(solver, work, expected)
+        solve_and_check(solver, work, expected, exact=exact)
+    if exact:
+        assert solver.current_schedule.dependence_protocol == "mailbox"
+        assert "_lcd_mailbox" in solver.hip_kernel_source
     schedule = solver.current_schedule
     if "execution_mode" in options:
         assert schedule.execution_mode == options["execution_mode"]
