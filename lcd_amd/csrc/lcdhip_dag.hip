@@ -24,9 +24,8 @@ using lcdhip::set_error;
 
 struct lcdhip_dag {
     lcdhip_dag_info info{};
-    int32_t *arrays[9] = {nullptr, nullptr, nullptr, nullptr, nullptr,
-                          nullptr, nullptr, nullptr, nullptr};
-    int64_t counts[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+    int32_t *arrays[LCDHIP_DAG_ARRAYS] = {};
+    int64_t counts[LCDHIP_DAG_ARRAYS] = {};
 };
 
 namespace {
@@ -121,6 +120,15 @@ __global__ void incoming_keys_kernel(const unsigned long long *__restrict__ keys
     unsigned long long key = keys[p];
     out_positions[p] = static_cast<int32_t>(p);
     out_keys[p] = key == ~0ull ? key : ((key << 32) | (key >> 32));
+}
+
+// out_slot[in_pos[k]] = k: the inverse of the incoming listing.
+__global__ void out_slot_kernel(const int32_t *__restrict__ in_pos,
+                                int64_t count, int32_t *__restrict__ out_slot)
+{
+    int64_t k = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (k < count)
+        out_slot[in_pos[k]] = static_cast<int32_t>(k);
 }
 
 __global__ void low_words_kernel(const unsigned long long *__restrict__ keys,
@@ -407,6 +415,11 @@ extern "C" int lcdhip_dag_build(const lcdhip_dag_rule *rules, int rule_count,
         if ((status = dag_alloc(dag, LCDHIP_DAG_IN_POS,
                                 static_cast<int64_t>(candidates))))
             return status;
+        if ((status = dag_alloc(dag, LCDHIP_DAG_OUT_SLOT, key_capacity)))
+            return status;
+        if (key_capacity > 0)
+            LCDHIP_CHECK(hipMemsetAsync(dag->arrays[LCDHIP_DAG_OUT_SLOT], 0xff,
+                                        key_capacity * 4, stream));
         int32_t *in_ptr = dag->arrays[LCDHIP_DAG_IN_PTR];
         LCDHIP_CHECK(hipMemsetAsync(in_ptr, 0, (n + 1) * 4, stream));
         if (n > 0) {
@@ -448,6 +461,13 @@ extern "C" int lcdhip_dag_build(const lcdhip_dag_rule *rules, int rule_count,
             LCDHIP_CHECK(hipMemcpyAsync(dag->arrays[LCDHIP_DAG_IN_POS],
                                         sorted_positions, candidates * 4,
                                         hipMemcpyDeviceToDevice, stream));
+            hipLaunchKernelGGL(out_slot_kernel,
+                               dim3(blocks_for(static_cast<int64_t>(candidates))),
+                               dim3(kBlock), 0, stream,
+                               dag->arrays[LCDHIP_DAG_IN_POS],
+                               static_cast<int64_t>(candidates),
+                               dag->arrays[LCDHIP_DAG_OUT_SLOT]);
+            LCDHIP_CHECK(hipGetLastError());
             LCDHIP_CHECK(hipStreamSynchronize(stream));
         }
     }
@@ -716,7 +736,7 @@ extern "C" int lcdhip_dag_get_info(const lcdhip_dag *dag, lcdhip_dag_info *out)
 extern "C" int lcdhip_dag_array(const lcdhip_dag *dag, int which, void **d_out,
                                 int64_t *count_out)
 {
-    if (!dag || which < 0 || which > 8 || !d_out || !count_out) {
+    if (!dag || which < 0 || which >= LCDHIP_DAG_ARRAYS || !d_out || !count_out) {
         set_error("bad argument to lcdhip_dag_array");
         return LCDHIP_ERR_ARGUMENT;
     }

@@ -265,9 +265,11 @@ def execution_data_from_device_dag(dag, execution_mode, warp_mapped,
             f"contain a cycle. Scheduled {dag.scheduled} of {dag.n} nodes.")
     counts = dag.array("edge_count" if pushed else "dep_count")
     if mailbox:
-        # per destination: the positions whose entries send it a message
+        # destination v reads message slots in_ptr[v] .. in_ptr[v+1); the
+        # entry at position p writes slot out_slot[p]
         auxiliary = {"_lcd_in_ptr": dag.array("in_ptr"),
-                     "_lcd_in_pos": dag.array("in_pos")}
+                     "_lcd_in_pos": dag.array("in_pos"),
+                     "_lcd_out_slot": dag.array("out_slot")}
         return WarpTaskExecutionData(
             task_nodes=dag.array("wavefronts"), task_ptr=None,
             band_ptr=dag.host("wavefront_ptr"), dep_count=counts,

@@ -62,7 +62,7 @@ PUSH_ARGUMENTS = ("dep_count", "initial_dep_count", "task_nodes", "task_ptr",
                   "task_counter", "task_count")
 PULL_ARGUMENTS = ("done", "task_nodes", "task_ptr", "task_counter",
                   "task_count")
-MAILBOX_ARGUMENTS = ("_lcd_mailbox", "_lcd_in_ptr", "_lcd_in_pos",
+MAILBOX_ARGUMENTS = ("_lcd_mailbox", "_lcd_in_ptr", "_lcd_out_slot",
                      "task_nodes", "task_ptr", "task_counter", "task_count")
 WAVEFRONT_ARGUMENTS = ("task_nodes", "task_ptr", "band_start", "band_end")
 STATUS_ARGUMENT = "_lcd_status"
@@ -70,7 +70,7 @@ HOST_LAUNCH_ARGUMENTS = frozenset({"band_ptr", "wavefront_ptr"})
 INTEGER_EXECUTOR_ARRAYS = frozenset({
     "dep_count", "initial_dep_count", "dag_ptr", "dag_index", "task_nodes",
     "task_ptr", "task_counter", "done", STATUS_ARGUMENT, "_lcd_in_ptr",
-    "_lcd_in_pos",
+    "_lcd_out_slot",
 })
 DEFAULT_SPIN_LIMIT = 1 << 22
 
@@ -885,8 +885,14 @@ class HIPLowerer:
                 rewritten = True
         if not rewritten:
             return None
-        return {"array": array, "slot": deepcopy(endpoint.slice),
+        return {"array": array, "position": deepcopy(endpoint.slice),
                 "index_array": endpoint.value.id, "own_text": own_text}
+
+    def _mailbox_slot_load(self):
+        """``_lcd_out_slot[position]``: the message slot a position writes."""
+        return ast.fix_missing_locations(ast.Subscript(
+            value=ast.Name(id="_lcd_out_slot", ctx=ast.Load()),
+            slice=deepcopy(self._mailbox["position"]), ctx=ast.Load()))
 
     def mailbox_guard_text(self):
         dependence = self.direct_dependence
@@ -1539,6 +1545,11 @@ class HIPLowerer:
             lane_hoist = Hoist("_pf_", extra=(mapped.target.id,))
             for inner in mapped.body:
                 visit_unconditional(inner, lane_hoist)
+            if self._mailbox is not None:
+                # the message slot of this lane's position loads with the
+                # first iteration's operands, ahead of the wait
+                self._mailbox["slot"] = lane_hoist.visit(
+                    self._mailbox_slot_load())
             first_iteration = order[node_count:]
             if self.direct_dependence is not None and first_iteration:
                 dependence = self.direct_dependence
@@ -1591,6 +1602,8 @@ class HIPLowerer:
         self._hook_endpoint = self._hook_guard = None
         self._first_iteration_reload = []
         self._prefetch_lines = []
+        if self._mailbox is not None:
+            self._mailbox["slot"] = self._mailbox_slot_load()
         if self.prefetch_node_loads:
             body, self._prefetch_lines = self._hoist_node_loads(
                 body, mapped, arguments)
@@ -1885,11 +1898,9 @@ class HIPLowerer:
                f"        if (_pending) {{ _release_begin = dag_ptr[{it}]; "
                f"_release_end = dag_ptr[{it} + 1]; }}"]
               if protocol == COUNTER_DEPENDENCE else []),
-            *(["        int _mb_next = 0, _mb_end = 0, _mb_slot = -1;",
+            *(["        int _mb_next = 0, _mb_end = 0;",
                f"        if (_pending) {{ _mb_next = _lcd_in_ptr[{it}]; "
-               f"_mb_end = _lcd_in_ptr[{it} + 1]; "
-               "if (_mb_next + _lane < _mb_end) "
-               "_mb_slot = _lcd_in_pos[_mb_next + _lane]; }"]
+               f"_mb_end = _lcd_in_ptr[{it} + 1]; }}"]
               if protocol == MAILBOX_DEPENDENCE else []),
             "        long long _spins = 0;",
             "        while (__ballot(_pending)) {",
@@ -1941,7 +1952,8 @@ class HIPLowerer:
 
     def _mailbox_ready_lines(self, indent):
         """Readiness for the mailbox protocol: every incoming message has
-        arrived.  Lane ``l`` of the group polls message ``next + l``; arrived
+        arrived.  A task's message slots are contiguous, in (source, position)
+        order; lane ``l`` of the group polls slot ``next + l``; arrived
         messages are added to the task's own element in (source, position)
         order -- the order of the sequential loop -- by broadcasting them
         lane by lane, so the sum is deterministic."""
@@ -1950,21 +1962,17 @@ class HIPLowerer:
         return [
             f"{pad}bool _ready = _mb_next == _mb_end;",
             f"{pad}if (!_ready) {{",
-            f"{pad}    const double _mb_value = _mb_slot >= 0 ? "
-            "lcd_ld(&_lcd_mailbox[_mb_slot]) : 0.0;",
             f"{pad}    const int _mb_have = (_mb_end - _mb_next) < LCD_TASK_LANES ? "
             "(_mb_end - _mb_next) : LCD_TASK_LANES;",
+            f"{pad}    const double _mb_value = _lane < _mb_have ? "
+            "lcd_ld(&_lcd_mailbox[_mb_next + _lane]) : 0.0;",
             f"{pad}    int _mb_k = 0;",
             f"{pad}    for (; _mb_k < _mb_have; ++_mb_k) {{",
             f"{pad}        const double _mb_in = __shfl(_mb_value, _mb_k, LCD_TASK_LANES);",
             f"{pad}        if (lcd_is_empty(_mb_in)) break;",
             f"{pad}        {own} = {own} + _mb_in;",
             f"{pad}    }}",
-            f"{pad}    if (_mb_k > 0) {{",
-            f"{pad}        _mb_next += _mb_k;",
-            f"{pad}        _mb_slot = (_mb_next + _lane < _mb_end) ? "
-            "_lcd_in_pos[_mb_next + _lane] : -1;",
-            f"{pad}    }}",
+            f"{pad}    _mb_next += _mb_k;",
             f"{pad}    _ready = _mb_next == _mb_end;",
             f"{pad}}}",
         ]

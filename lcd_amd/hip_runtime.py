@@ -35,7 +35,7 @@ STATUS_ARGUMENT = "_lcd_status"
 
 DAG_PTR, DAG_INDEX, DAG_DEP_COUNT, DAG_EDGE_COUNT = 0, 1, 2, 3
 DAG_LEVEL_OF, DAG_WAVEFRONTS, DAG_WAVEFRONT_PTR = 4, 5, 6
-DAG_IN_PTR, DAG_IN_POS = 7, 8
+DAG_IN_PTR, DAG_IN_POS, DAG_OUT_SLOT = 7, 8, 9
 DAG_FLAG_LEVELS, DAG_FLAG_FORCE_KAHN, DAG_FLAG_INCOMING = 1, 2, 4
 
 DEVICE_COMPILE_OPTIONS = (
@@ -308,7 +308,7 @@ class DeviceDag:
               "dep_count": DAG_DEP_COUNT, "edge_count": DAG_EDGE_COUNT,
               "level_of": DAG_LEVEL_OF, "wavefronts": DAG_WAVEFRONTS,
               "wavefront_ptr": DAG_WAVEFRONT_PTR, "in_ptr": DAG_IN_PTR,
-              "in_pos": DAG_IN_POS}
+              "in_pos": DAG_IN_POS, "out_slot": DAG_OUT_SLOT}
 
     def __init__(self, device, handle):
         self.device = device
@@ -901,7 +901,8 @@ def prepare_hip_arguments(lowering, argument_values, execution_data,
                 workspace[("state", "done")] = cached
             host_values["done"] = cached
         if "_lcd_mailbox" in lowering.launcher_arguments:
-            slots = len(host_values[lowering.mailbox_index_array])
+            # one slot per message: out_slot holds the slots 0 .. count-1
+            slots = max(len(host_values["_lcd_in_pos"]), 1)
             cached = workspace.get(("state", "_lcd_mailbox"))
             if cached is None or len(cached) != slots:
                 cached = device.empty((slots,), np.float64)

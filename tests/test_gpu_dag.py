@@ -102,6 +102,12 @@ def test_incoming_positions(device, oracle):
     for v in range(n):
         want = [p for _, p in sorted(expected[v])]
         assert in_pos[in_ptr[v]:in_ptr[v + 1]].tolist() == want
+    # out_slot inverts the listing; positions without an edge hold -1
+    out_slot = dag.host("out_slot")
+    assert len(out_slot) == len(idx)
+    np.testing.assert_array_equal(out_slot[in_pos], np.arange(len(in_pos)))
+    assert int((out_slot >= 0).sum()) == len(in_pos)
+    assert set(out_slot[out_slot < 0].tolist()) <= {-1}
     work = workloads.configuration("c2", nx=12, ny=10, nz=9)
     dag = device.dag_build([oracle.rule_sptrsv_csc(work.indptr, work.indices)],
                            work.n, incoming=True)
