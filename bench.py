@@ -31,16 +31,19 @@ METRIC = "SpTRSV/SpILU0 solve ms, GFLOP/s, HBM GB/s (% roofline) on 1 MI355X"
 # one can be overridden on the command line).
 TUNED = {
     "c1": dict(execution_mode="sync_free", threads_per_block=64, task_lanes=4,
-               thread_unroll=1, resident_waves_per_cu=1),
+               thread_unroll=1, resident_waves_per_cu=1,
+               dependence_protocol="mailbox"),
     "c2": dict(execution_mode="sync_free", threads_per_block=256, task_lanes=4,
-               thread_unroll=1, resident_waves_per_cu=2),
+               thread_unroll=1, resident_waves_per_cu=4,
+               dependence_protocol="mailbox"),
     "c3": dict(execution_mode="sync_free", threads_per_block=256,
-               task_lanes=16, thread_unroll=1, resident_waves_per_cu=4,
+               task_lanes=64, thread_unroll=1, resident_waves_per_cu=16,
                dependence_protocol="counter"),
     "c4": dict(execution_mode="wavefront", threads_per_block=64, task_lanes=8,
                thread_unroll=1),
     "c5": dict(execution_mode="sync_free", threads_per_block=256, task_lanes=8,
-               thread_unroll=1, resident_waves_per_cu=2),
+               thread_unroll=1, resident_waves_per_cu=2,
+               dependence_protocol="mailbox"),
 }
 
 

@@ -231,7 +231,10 @@ class ScheduleSpace:
                     + ", ".join(available) + ".")
             protocols = (dependence_protocol,)
         elif PUSH_DEPENDENCE in available:
-            protocols = (PUSH_DEPENDENCE,)
+            # message slots beat atomics + counters wherever a push applies
+            # (one hop per edge, deterministic sums); the lowering falls back
+            # to the push protocol for loop shapes the mailbox cannot express
+            protocols = (MAILBOX_DEPENDENCE,)
         elif PULL_DEPENDENCE in available and searched:
             protocols = (COUNTER_DEPENDENCE, PULL_DEPENDENCE)
         else:

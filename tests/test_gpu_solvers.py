@@ -39,8 +39,10 @@ CSC_VARIANTS = [
     dict(execution_mode="wavefront", threads_per_block=256, task_lanes=8,
          thread_unroll=2),
     dict(execution_mode="sync_free", threads_per_block=128, task_lanes=4),
-    dict(execution_mode="sync_free", threads_per_block=256, task_lanes=8),
-    dict(execution_mode="sync_free", threads_per_block=128, n_warp=1),
+    dict(execution_mode="sync_free", threads_per_block=256, task_lanes=8,
+         dependence_protocol="push"),
+    dict(execution_mode="sync_free", threads_per_block=128, n_warp=1,
+         dependence_protocol="push"),
     dict(execution_mode="sync_free", threads_per_block=128, task_lanes=4,
          dependence_protocol="counter"),
     dict(execution_mode="wavefront", threads_per_block=128, n_warp=2),
@@ -62,7 +64,10 @@ def test_sptrsv_csc_variants(oracle, options):
     solver = sptrsv.compile_sptrsv_csc(**options)
     # the mailbox protocol adds the incoming products in the order of the
     # sequential loop: bit-identical results, not just 1e-12
-    exact = options.get("dependence_protocol") == "mailbox"
+    defaulted = (options.get("execution_mode") == "sync_free"
+                 and "dependence_protocol" not in options
+                 and options.get("n_warp", 1) == 1)
+    exact = options.get("dependence_protocol") == "mailbox" or defaulted
     for name, overrides in (("c1", {}), ("c2", dict(nx=20, ny=18, nz=16)),
                             ("c5", dict(n=6000))):
         work = workloads.configuration(name, **overrides)
@@ -75,10 +80,9 @@ def test_sptrsv_csc_variants(oracle, options):
     schedule = solver.current_schedule
     if "execution_mode" in options:
         assert schedule.execution_mode == options["execution_mode"]
-    if options.get("execution_mode") == "sync_free" and (
-            "dependence_protocol" not in options
-            and options.get("n_warp", 1) == 1):
+    if options.get("dependence_protocol") == "push":
         assert schedule.dependence_protocol == "push"
+        assert "_lcd_mailbox" not in solver.hip_kernel_source
 
 
 CSR_VARIANTS = [

@@ -202,7 +202,12 @@ def test_schedule_space_rules():
                                          direct_protocol="push")
     configurations = space.configurations()
     assert {c[0] for c in configurations} == {"wavefront", "sync_free"}
-    assert all(c[4] == "push" for c in configurations if c[0] == "sync_free")
+    # a pushable loop defaults to message slots; push stays selectable
+    assert all(c[4] == "mailbox" for c in configurations if c[0] == "sync_free")
+    explicit = S.ScheduleSpace.from_options(
+        thread_mapped=True, direct_protocol="push", dependence_protocol="push")
+    assert {c[4] for c in explicit.configurations()
+            if c[0] == "sync_free"} == {"push"}
     assert all(c[4] == "counter" for c in configurations if c[0] == "wavefront")
     assert {c[5] for c in configurations} == set(S.TASK_LANE_CANDIDATES)
     fixed = S.ScheduleSpace.from_options(
