@@ -62,6 +62,9 @@ PUSH_ARGUMENTS = ("dep_count", "initial_dep_count", "task_nodes", "task_ptr",
                   "task_counter", "task_count")
 PULL_ARGUMENTS = ("done", "task_nodes", "task_ptr", "task_counter",
                   "task_count")
+VALUE_PULL_ARGUMENTS = ("task_nodes", "task_ptr", "task_counter", "task_count")
+VALUE_WAIT_BEGIN = "//@lcd-wait-begin"
+VALUE_WAIT_END = "//@lcd-wait-end"
 MAILBOX_ARGUMENTS = ("_lcd_mailbox", "_lcd_in_ptr", "_lcd_out_slot",
                      "task_nodes", "task_ptr", "task_counter", "task_count")
 WAVEFRONT_ARGUMENTS = ("task_nodes", "task_ptr", "band_start", "band_end")
@@ -128,6 +131,11 @@ class HIPLoweringResult:
     persistent: bool = False
     function_name: str = ""
     mailbox_index_array: str | None = None
+    # pull protocol without flags: consumers poll the producers' elements of
+    # this array, which the reset kernel fills with the empty marker
+    value_flag_array: str | None = None
+    # lifted zero-initialised arrays the executor needs no host-side clear for
+    executor_initialised: tuple = ()
 
     @property
     def module_source(self):
@@ -680,6 +688,7 @@ class _MappedLoopHooks:
         self.emitter = emitter
         self.loop = loop
         self.partials = []   # (partial_name, target_node, op)
+        self.value_pull = None
 
     def is_mapped(self, node):
         return node is self.loop
@@ -709,6 +718,8 @@ class _MappedLoopHooks:
         lines = []
         for partial, _, _ in self.partials:
             lines.append(f"{pad}{partial} = 0.0;")
+        if self.value_pull is not None:
+            return self._value_pull_loop(node, body, indent, lines, stores)
         body_lines = emitter.block(body, indent + (2 if unroll > 1 else 1), None)
         hook_lines = low.push_hook_lines(indent + (2 if unroll > 1 else 1))
         if unroll == 1:
@@ -729,6 +740,64 @@ class _MappedLoopHooks:
             lines.append(f"{pad}        }}")
             lines.append(f"{pad}    }}")
             lines.append(f"{pad}}}")
+        lines += self._after_loop(pad, stores)
+        return lines
+
+    def _value_pull_loop(self, node, body, indent, lines, stores):
+        """The distributed loop of a value-flagged pull: resumable.  Each lane
+        walks its positions as far as the producers' values are final (not
+        the empty marker) and keeps its position across polls; the lines
+        between the two markers are re-entered by the executor's poll loop."""
+        low, emitter = self.lowerer, self.emitter
+        pad = "    " * indent
+        plan = self.value_pull
+        lower, upper, _ = emitter.range_parts(node)
+        name = node.target.id
+        array = plan["array"]
+        endpoint = (low._hook_endpoint if low._hook_endpoint is not None
+                    else low.direct_dependence.endpoint)
+        guard = (low._hook_guard if low._hook_endpoint is not None
+                 else low.direct_dependence.guard)
+        endpoint_texts = {plan["endpoint_text"], ast.unparse(endpoint)}
+
+        class Substitute(ast.NodeTransformer):
+            count = 0
+
+            def visit_Subscript(self, sub):
+                if (isinstance(sub.value, ast.Name) and sub.value.id == array
+                        and ast.unparse(sub.slice) in endpoint_texts):
+                    Substitute.count += 1
+                    return ast.copy_location(
+                        ast.Name(id="_lcd_vf", ctx=ast.Load()), sub)
+                return self.generic_visit(sub)
+
+        body = [Substitute().visit(statement) for statement in body]
+        if Substitute.count == 0:
+            raise HIPLoweringError(
+                "Value-flagged pull found no read of the producers' values.")
+        low._kinds.locals["_lcd_vf"] = FLOAT
+        body_lines = emitter.block(body, indent + 1, None)
+        lines.append(f"{pad}{name} = ({lower}) + _lane;")
+        lines.append(VALUE_WAIT_BEGIN)
+        lines.append(f"{pad}for (; {name} < {upper}; {name} += LCD_TASK_LANES) {{")
+        lines += [f"{pad}    {line}" for line in low._first_iteration_reload]
+        lines.append(f"{pad}    double _lcd_vf = lcd_ld(&{array}[{emitter.expr(endpoint)}]);")
+        if guard is None:
+            lines.append(f"{pad}    if (lcd_is_empty(_lcd_vf)) break;")
+        else:
+            # a read the DAG does not order sees the initial zero
+            lines.append(f"{pad}    if (lcd_is_empty(_lcd_vf)) {{ "
+                         f"if ({emitter.expr(guard)}) break; _lcd_vf = 0.0; }}")
+        lines += body_lines
+        lines.append(f"{pad}}}")
+        lines.append(VALUE_WAIT_END)
+        plan["remaining"] = f"{name} < {upper}"
+        lines += self._after_loop(pad, stores)
+        return lines
+
+    def _after_loop(self, pad, stores):
+        low, emitter = self.lowerer, self.emitter
+        lines = []
         if stores:
             lines.append(f"{pad}{low.group_sync}")
         for partial, target, op in self.partials:
@@ -755,7 +824,10 @@ class HIPLowerer:
                  chain_tasks=False, argument_kinds=None,
                  spin_limit=DEFAULT_SPIN_LIMIT, resident_waves_per_cu=None,
                  spin_sleep=1, promote_own_elements=True,
-                 prefetch_node_loads=True):
+                 prefetch_node_loads=True, value_flags=True):
+        self.value_flags = value_flags
+        self._value_pull = None
+        self._own_zero_arrays = set()
         self.promote_own_elements = promote_own_elements
         self.prefetch_node_loads = prefetch_node_loads
         self.resident_waves_per_cu = resident_waves_per_cu
@@ -888,6 +960,72 @@ class HIPLowerer:
         return {"array": array, "position": deepcopy(endpoint.slice),
                 "index_array": endpoint.value.id, "own_text": own_text}
 
+    def _fully_rewritten_arrays(self, body, target_loop, zero_initialised):
+        """Lifted ``X = np.zeros(count)`` arrays whose element ``X[i]`` every
+        task assigns unconditionally at its top level, with ``i`` running over
+        ``range(count)``: after the loop no element keeps its initial zero."""
+        arguments = target_loop.iter.args
+        if len(arguments) != 1:
+            return set()
+        count = ast.unparse(arguments[0])
+        found = set()
+        for name, shape in zero_initialised.items():
+            if shape != count:
+                continue
+            own_text = f"{name}[{self.loop_iterator}]"
+            if any(isinstance(statement, ast.Assign)
+                   and len(statement.targets) == 1
+                   and ast.unparse(statement.targets[0]) == own_text
+                   for statement in body):
+                found.add(name)
+        return found
+
+    def _value_pull_plan(self, body):
+        """The pull protocol can drop its ``done`` flags when the values
+        themselves tell whether they are final: the consumers read
+        ``X[endpoint]`` only inside the distributed loop, ``X`` is a lifted
+        zero-initialised array every task writes exactly once (its own
+        element, kept in a register until the end of the task), and nothing
+        else is written.  ``X`` then starts as the empty marker and a consumer
+        advances through its loop as far as final values are there."""
+        dependence = self.direct_dependence
+        if (dependence is None or self.block_task or self.chain_tasks
+                or self.thread_unroll_factor != 1
+                or not self.promote_own_elements
+                or not self.prefetch_node_loads):
+            return None
+        mapped = self._find_mapped_loop(body)
+        if mapped is None or mapped not in body or len(mapped.iter.args) != 2:
+            return None
+        endpoint_text = ast.unparse(dependence.endpoint)
+        arrays = {
+            node.value.id for statement in mapped.body
+            for node in ast.walk(statement)
+            if isinstance(node, ast.Subscript)
+            and isinstance(node.value, ast.Name)
+            and isinstance(node.ctx, ast.Load)
+            and node.value.id in self._all_written
+            and ast.unparse(node.slice) == endpoint_text}
+        if len(arrays) != 1 or self._all_written != arrays:
+            return None
+        array = next(iter(arrays))
+        if array not in self._fully_rewritten:
+            return None
+        # inside the distributed loop X is read at the endpoint only; its
+        # other accesses are the task's own element (a privatised reduction)
+        for statement in mapped.body:
+            for node in ast.walk(statement):
+                if not (isinstance(node, ast.Subscript)
+                        and isinstance(node.value, ast.Name)
+                        and node.value.id == array):
+                    continue
+                index = ast.unparse(node.slice)
+                if index == self.loop_iterator:
+                    continue
+                if not isinstance(node.ctx, ast.Load) or index != endpoint_text:
+                    return None
+        return {"array": array, "endpoint_text": endpoint_text}
+
     def _mailbox_slot_load(self):
         """``_lcd_out_slot[position]``: the message slot a position writes."""
         return ast.fix_missing_locations(ast.Subscript(
@@ -986,6 +1124,14 @@ class HIPLowerer:
             self._mailbox = self._mailbox_plan(body)
             if self._mailbox is None:
                 self.dependence_protocol = PUSH_DEPENDENCE
+        self._fully_rewritten = self._fully_rewritten_arrays(
+            body, target_loop, zero_initialised)
+        if (self.dependence_protocol == PULL_DEPENDENCE and self.value_flags
+                and self.execution_mode == "sync_free"):
+            self._value_pull = self._value_pull_plan(body)
+        if self._mailbox is not None and (
+                self._mailbox["array"] in self._fully_rewritten):
+            self._own_zero_arrays.add(self._mailbox["array"])
         coherent = set(written_arrays) if self.execution_mode == "sync_free" else set()
         if self._mailbox is not None:
             # only a task itself touches its element of the reduced array
@@ -1085,6 +1231,11 @@ class HIPLowerer:
             function_name=function_name,
             mailbox_index_array=(self._mailbox["index_array"]
                                  if self._mailbox else None),
+            value_flag_array=(self._value_pull["array"]
+                              if self._value_pull else None),
+            executor_initialised=tuple(sorted(
+                self._own_zero_arrays
+                | ({self._value_pull["array"]} if self._value_pull else set()))),
         )
 
     # ---- structure discovery
@@ -1193,6 +1344,9 @@ class HIPLowerer:
         if self.execution_mode == "sync_free":
             if self.dependence_protocol == PUSH_DEPENDENCE:
                 names = list(PUSH_ARGUMENTS)
+            elif (self.dependence_protocol == PULL_DEPENDENCE
+                  and self._value_pull is not None):
+                names = list(VALUE_PULL_ARGUMENTS)
             elif self.dependence_protocol == PULL_DEPENDENCE:
                 names = list(PULL_ARGUMENTS)
             elif self.dependence_protocol == MAILBOX_DEPENDENCE:
@@ -1455,7 +1609,14 @@ class HIPLowerer:
                 value=ast.Name(id=array, ctx=ast.Load()),
                 slice=deepcopy(target.slice), ctx=ast.Load())
             if first_access.get(name, "read") == "read":
-                prologue.append(f"{name} = {emitter.expr(load_node)};")
+                if (array in self._own_zero_arrays or (
+                        self._value_pull is not None
+                        and self._value_pull["array"] == array)):
+                    # still its initial zero: no other task writes it, and
+                    # the executor does not clear the array
+                    prologue.append(f"{name} = 0.0;")
+                else:
+                    prologue.append(f"{name} = {emitter.expr(load_node)};")
             epilogue.append("if (_lane == 0) " + emitter.store(load_node, name))
         ast.fix_missing_locations(ast.Module(body=new_body, type_ignores=[]))
         return new_body, prologue, epilogue
@@ -1607,6 +1768,14 @@ class HIPLowerer:
         if self.prefetch_node_loads:
             body, self._prefetch_lines = self._hoist_node_loads(
                 body, mapped, arguments)
+        if self._value_pull is not None:
+            own = self._own_map.get(
+                f"{self._value_pull['array']}[{self.loop_iterator}]")
+            if own is None or mapped is None:
+                raise HIPLoweringError(
+                    "Value-flagged pull needs the task's own element of "
+                    f"{self._value_pull['array']!r} in a register.")
+            hooks.value_pull = self._value_pull
         if self._mailbox is not None:
             own = self._own_map.get(self._mailbox["own_text"])
             if own is None or own[1] != "read":
@@ -1777,14 +1946,21 @@ class HIPLowerer:
         prefetch = list(self._prefetch_lines)
         self._prefetch_guard = guard
 
-        def task(indent):
+        def task(indent, body_lines=None):
             pad = "    " * indent
             out = [f"{pad}if ({guard}) {{"]
             if self.execution_mode != "sync_free":
                 out += [pad + "    " + line for line in prefetch]
-            out += [pad + "    " + line for line in task_body]
+            out += [pad + "    " + line for line in (
+                task_body if body_lines is None else body_lines)]
             out.append(f"{pad}}}")
             return out
+
+        if self._value_pull is not None:
+            begin = task_body.index(VALUE_WAIT_BEGIN)
+            end = task_body.index(VALUE_WAIT_END)
+            self._value_segments = (task_body[:begin], task_body[begin + 1:end],
+                                    task_body[end + 1:])
 
         def node_loop(indent, body_fn):
             pad = "    " * indent
@@ -1902,11 +2078,25 @@ class HIPLowerer:
                f"        if (_pending) {{ _mb_next = _lcd_in_ptr[{it}]; "
                f"_mb_end = _lcd_in_ptr[{it} + 1]; }}"]
               if protocol == MAILBOX_DEPENDENCE else []),
+        ]
+        value = self._value_pull
+        if value is not None:
+            before, waiting, after = self._value_segments
+            # everything ahead of the distributed loop reads nothing another
+            # task writes: it runs before the first poll
+            lines += ["        if (_pending) {", *task(3, before), "        }"]
+        lines += [
             "        long long _spins = 0;",
             "        while (__ballot(_pending)) {",
             "            if (_pending) {",
         ]
-        if protocol == PULL_DEPENDENCE:
+        if value is not None:
+            missing = f"({value['remaining']})"
+            total = (f"lcd_group_sum((double){missing}) != 0.0"
+                     if self.task_lanes > 1 else missing)
+            lines.append("                bool _ready = true;")
+            lines += task(4, waiting + [f"_ready = !({total});"])
+        elif protocol == PULL_DEPENDENCE:
             lines += self._pull_ready_lines(4)
         elif protocol == MAILBOX_DEPENDENCE:
             lines += self._mailbox_ready_lines(4)
@@ -1914,8 +2104,13 @@ class HIPLowerer:
             lines.append(f"                const bool _ready = "
                          f"lcd_load_relaxed(&dep_count[{it}]) == LCD_READY_COUNT;")
         lines.append("                if (_ready) {")
-        lines.append("                    lcd_acquire_fence();")
-        lines += task(5)
+        if value is not None:
+            # the last act of the task is the store of its own element:
+            # the value is the flag
+            lines += task(5, after)
+        else:
+            lines.append("                    lcd_acquire_fence();")
+            lines += task(5)
         if protocol == COUNTER_DEPENDENCE:
             lines += [
                 f"                    {self.group_sync}",
@@ -1924,7 +2119,7 @@ class HIPLowerer:
                 "_e < _release_end; _e += LCD_TASK_LANES)",
                 "                        lcd_atomic_sub(&dep_count[dag_index[_e]], 1);",
             ]
-        elif protocol == PULL_DEPENDENCE:
+        elif protocol == PULL_DEPENDENCE and value is None:
             lines += [
                 f"                    {self.group_sync}",
                 "                    lcd_release_fence();",
@@ -2010,6 +2205,13 @@ class HIPLowerer:
                     "    if (t == 0) { task_counter[0] = 0; }\n")
             signature = ("unsigned int* _lcd_mailbox, int* task_counter, "
                          "long long count")
+        elif (self.dependence_protocol == PULL_DEPENDENCE
+              and self._value_pull is not None):
+            body = ("    if (t < count) { _lcd_values[2 * t] = LCD_EMPTY_WORD; "
+                    "_lcd_values[2 * t + 1] = LCD_EMPTY_WORD; }\n"
+                    "    if (t == 0) { task_counter[0] = 0; }\n")
+            signature = ("unsigned int* _lcd_values, int* task_counter, "
+                         "long long count")
         elif self.dependence_protocol == PULL_DEPENDENCE:
             body = ("    if (t < count) done[t] = 0;\n"
                     "    if (t == 0) { task_counter[0] = 0; }\n")
@@ -2065,7 +2267,14 @@ class HIPLowerer:
                            MAILBOX_DEPENDENCE: "task_nodes"}.get(
                                self.dependence_protocol, "dep_count")
             reset_count = "_count"
-            if self.dependence_protocol == PULL_DEPENDENCE:
+            if (self.dependence_protocol == PULL_DEPENDENCE
+                    and self._value_pull is not None):
+                count_array = "task_nodes"
+                values = self._value_pull["array"]
+                reset_args = (f"({values}, task_counter, "
+                              f"_hip.length({values}))")
+                reset_count = f"_hip.length({values})"
+            elif self.dependence_protocol == PULL_DEPENDENCE:
                 reset_args = "(done, task_counter, _hip.length(done))"
             elif self.dependence_protocol == MAILBOX_DEPENDENCE:
                 reset_args = ("(_lcd_mailbox, task_counter, "
@@ -2101,7 +2310,7 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
                  chain_tasks=False, argument_kinds=None,
                  spin_limit=DEFAULT_SPIN_LIMIT, resident_waves_per_cu=None,
                  spin_sleep=1, promote_own_elements=True,
-                 prefetch_node_loads=True):
+                 prefetch_node_loads=True, value_flags=True):
     """HIP counterpart of ``lower_to_numba_cuda``
     (compiler/cuda_lowering.py:2854-2884); same parameters plus
     ``task_lanes`` (lanes cooperating on one task, a power of two <= 64),
@@ -2120,5 +2329,5 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
         chain_tasks=chain_tasks, argument_kinds=argument_kinds,
         spin_limit=spin_limit, resident_waves_per_cu=resident_waves_per_cu,
         spin_sleep=spin_sleep, promote_own_elements=promote_own_elements,
-        prefetch_node_loads=prefetch_node_loads)
+        prefetch_node_loads=prefetch_node_loads, value_flags=value_flags)
     return lowerer.lower(code)

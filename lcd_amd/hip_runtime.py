@@ -946,7 +946,10 @@ def prepare_hip_arguments(lowering, argument_values, execution_data,
         launcher_argument_names=tuple(lowering.launcher_arguments),
         values=prepared, host_values=host_values,
         lifted_variables=tuple(lowering.lifted_variables), device=device,
-        module=module, zero_on_launch=tuple(zero_arrays),
+        module=module,
+        zero_on_launch=tuple(
+            name for name in zero_arrays
+            if name not in getattr(lowering, "executor_initialised", ())),
         graph=workspace.get(graph_key), workspace=workspace,
         graph_key=graph_key)
 

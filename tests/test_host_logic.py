@@ -438,8 +438,9 @@ def test_csr_reduction_is_privatised_and_pull_polls_done():
     module = demo_source("sptrsv", "sptrsv_csr_loop")
     result = lower(module, execution_mode="sync_free",
                    thread_loop_iterator="j", n_warp=1,
-                   dependence_protocol="pull")
+                   dependence_protocol="pull", value_flags=False)
     assert result.dependence_protocol == "pull"
+    assert result.value_flag_array is None
     assert "done" in result.kernel_arguments
     assert "dep_count" not in result.kernel_arguments
     assert "_thread_partial_0 = lcd_group_sum(_thread_partial_0);" in (
@@ -449,6 +450,53 @@ def test_csr_reduction_is_privatised_and_pull_polls_done():
     hip_runtime.compile_code(result.source)
     lane = lower(module, execution_mode="wavefront")
     assert lane.task_lanes == 1 and "_thread_partial" not in lane.kernel_source
+
+
+def test_csr_pull_polls_the_values_themselves():
+    """x is a lifted zero array every task writes once: the pull protocol
+    needs no done flags, the reset kernel fills x with the empty marker and
+    the distributed loop resumes where a value was not final yet."""
+    module = demo_source("sptrsv", "sptrsv_csr_loop")
+    result = lower(module, execution_mode="sync_free",
+                   thread_loop_iterator="j", task_lanes=4,
+                   dependence_protocol="pull")
+    kernel = result.kernel_source
+    assert result.value_flag_array == "x"
+    assert result.executor_initialised == ("x",)
+    assert "done" not in result.kernel_arguments
+    assert "done" not in kernel
+    assert "double _lcd_vf = lcd_ld(&x[" in kernel
+    assert "if (lcd_is_empty(_lcd_vf))" in kernel
+    assert "for (; j < " in kernel          # resumes, does not restart
+    assert "lcd_release_fence" not in kernel.split("while (true)")[1]
+    assert "_lcd_values[2 * t] = LCD_EMPTY_WORD" in result.source
+    assert "(x, task_counter, _hip.length(x))" in result.launcher_source
+    hip_runtime.compile_code(result.source)
+    # not applicable: unrolled distributed loop, or a whole workgroup per task
+    for options in (dict(task_lanes=4, thread_unroll_factor=2),
+                    dict(n_warp=2, wavefront_threads_per_block=128)):
+        flagged = lower(module, execution_mode="sync_free",
+                        thread_loop_iterator="j", dependence_protocol="pull",
+                        **options)
+        assert flagged.value_flag_array is None
+        assert flagged.executor_initialised == ()
+        if "n_warp" not in options:
+            assert "done" in flagged.kernel_arguments
+
+
+def test_mailbox_needs_no_clear_of_the_solution():
+    module = demo_source("sptrsv", "sptrsv_csc_loop")
+    result = lower(module, execution_mode="sync_free",
+                   thread_loop_iterator="j", task_lanes=4,
+                   dependence_protocol="mailbox")
+    assert result.dependence_protocol == "mailbox"
+    assert result.executor_initialised == ("x",)
+    assert "_lcd_own_0 = 0.0;" in result.kernel_source
+    assert "_lcd_own_0 = x[i];" not in result.kernel_source
+    pushed = lower(module, execution_mode="sync_free",
+                   thread_loop_iterator="j", task_lanes=4,
+                   dependence_protocol="push")
+    assert pushed.executor_initialised == ()
 
 
 def test_ilu0_nested_mapping_lookup_and_binary_search():
