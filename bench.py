@@ -37,8 +37,8 @@ TUNED = {
                thread_unroll=1, resident_waves_per_cu=4,
                dependence_protocol="mailbox"),
     "c3": dict(execution_mode="sync_free", threads_per_block=256,
-               task_lanes=64, thread_unroll=1, resident_waves_per_cu=16,
-               dependence_protocol="counter"),
+               task_lanes=32, thread_unroll=1, resident_waves_per_cu=32,
+               dependence_protocol="pull"),
     "c4": dict(execution_mode="wavefront", threads_per_block=64, task_lanes=8,
                thread_unroll=1),
     "c5": dict(execution_mode="sync_free", threads_per_block=256, task_lanes=8,

@@ -214,14 +214,16 @@ typedef struct {
  * produce an edge into v, ordered by (source, position), duplicates kept
  * (in_ptr is the scan of EDGE_COUNT).  Positions of rule r are offset by the
  * sum of idx_size of the rules before it.  out_slot is the inverse listing:
- * out_slot[in_pos[k]] = k, and -1 for positions that produce no edge.  The
+ * out_slot[in_pos[k]] = k, and -1 for positions that produce no edge; in_src[k]
+ * is the source node of the edge in_pos[k] produces.  The
  * mailbox protocol delivers one message per position: the producer of
  * position p writes message slot out_slot[p], the consumer v reads slots
  * in_ptr[v] .. in_ptr[v+1) in order. */
 #define LCDHIP_DAG_IN_PTR 7         /* n + 1 */
 #define LCDHIP_DAG_IN_POS 8         /* candidate edges */
 #define LCDHIP_DAG_OUT_SLOT 9       /* sum of idx_size over the rules */
-#define LCDHIP_DAG_ARRAYS 10
+#define LCDHIP_DAG_IN_SRC 10        /* candidate edges: source of in_pos[k] */
+#define LCDHIP_DAG_ARRAYS 11
 
 int lcdhip_dag_build(const lcdhip_dag_rule *rules, int rule_count, int64_t n,
                      uint32_t flags, lcdhip_stream stream, lcdhip_dag **out);

@@ -417,6 +417,9 @@ extern "C" int lcdhip_dag_build(const lcdhip_dag_rule *rules, int rule_count,
             return status;
         if ((status = dag_alloc(dag, LCDHIP_DAG_OUT_SLOT, key_capacity)))
             return status;
+        if ((status = dag_alloc(dag, LCDHIP_DAG_IN_SRC,
+                                static_cast<int64_t>(candidates))))
+            return status;
         if (key_capacity > 0)
             LCDHIP_CHECK(hipMemsetAsync(dag->arrays[LCDHIP_DAG_OUT_SLOT], 0xff,
                                         key_capacity * 4, stream));
@@ -461,6 +464,12 @@ extern "C" int lcdhip_dag_build(const lcdhip_dag_rule *rules, int rule_count,
             LCDHIP_CHECK(hipMemcpyAsync(dag->arrays[LCDHIP_DAG_IN_POS],
                                         sorted_positions, candidates * 4,
                                         hipMemcpyDeviceToDevice, stream));
+            // sorted keys are (dst << 32 | src): the low words are the sources
+            hipLaunchKernelGGL(low_words_kernel,
+                               dim3(blocks_for(static_cast<int64_t>(candidates))),
+                               dim3(kBlock), 0, stream, in_sorted,
+                               static_cast<int64_t>(candidates),
+                               dag->arrays[LCDHIP_DAG_IN_SRC]);
             hipLaunchKernelGGL(out_slot_kernel,
                                dim3(blocks_for(static_cast<int64_t>(candidates))),
                                dim3(kBlock), 0, stream,

@@ -266,9 +266,11 @@ def execution_data_from_device_dag(dag, execution_mode, warp_mapped,
     counts = dag.array("edge_count" if pushed else "dep_count")
     if mailbox:
         # destination v reads message slots in_ptr[v] .. in_ptr[v+1); the
-        # entry at position p writes slot out_slot[p]
+        # entry at position p writes slot out_slot[p]; slot k carries the
+        # product of position in_pos[k], made by task in_src[k]
         auxiliary = {"_lcd_in_ptr": dag.array("in_ptr"),
                      "_lcd_in_pos": dag.array("in_pos"),
+                     "_lcd_in_src": dag.array("in_src"),
                      "_lcd_out_slot": dag.array("out_slot")}
         return WarpTaskExecutionData(
             task_nodes=dag.array("wavefronts"), task_ptr=None,

@@ -189,6 +189,8 @@ def parallel(**kwargs):
                     chain_tasks=band_width != 1,
                     resident_waves_per_cu=kwargs.get("resident_waves_per_cu"),
                     spin_sleep=kwargs.get("spin_sleep", 1),
+                    value_flags=kwargs.get("value_flags", True),
+                    gather_messages=kwargs.get("gather_messages", False),
                 )
             return lowered_variants[lowering_key]
 

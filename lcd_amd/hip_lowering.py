@@ -62,6 +62,8 @@ PUSH_ARGUMENTS = ("dep_count", "initial_dep_count", "task_nodes", "task_ptr",
                   "task_counter", "task_count")
 PULL_ARGUMENTS = ("done", "task_nodes", "task_ptr", "task_counter",
                   "task_count")
+GATHER_ARGUMENTS = ("_lcd_in_ptr", "_lcd_in_pos", "_lcd_in_src",
+                    "task_nodes", "task_ptr", "task_counter", "task_count")
 VALUE_PULL_ARGUMENTS = ("task_nodes", "task_ptr", "task_counter", "task_count")
 VALUE_WAIT_BEGIN = "//@lcd-wait-begin"
 VALUE_WAIT_END = "//@lcd-wait-end"
@@ -73,7 +75,7 @@ HOST_LAUNCH_ARGUMENTS = frozenset({"band_ptr", "wavefront_ptr"})
 INTEGER_EXECUTOR_ARRAYS = frozenset({
     "dep_count", "initial_dep_count", "dag_ptr", "dag_index", "task_nodes",
     "task_ptr", "task_counter", "done", STATUS_ARGUMENT, "_lcd_in_ptr",
-    "_lcd_out_slot",
+    "_lcd_out_slot", "_lcd_in_pos", "_lcd_in_src",
 })
 DEFAULT_SPIN_LIMIT = 1 << 22
 
@@ -633,6 +635,9 @@ template <class T, class V> __device__ __forceinline__ void lcd_st(T* p, V v) {
 __device__ __forceinline__ bool lcd_is_empty(double v) {
     return __double_as_longlong(v) == (long long)0x7FF84C437FF84C43ull;
 }
+__device__ __forceinline__ double lcd_empty() {
+    return __longlong_as_double((long long)0x7FF84C437FF84C43ull);
+}
 // Release: every store/atomic this wavefront issued has completed at the
 // coherence point before anything after the fence is issued.
 __device__ __forceinline__ void lcd_release_fence() {
@@ -824,7 +829,9 @@ class HIPLowerer:
                  chain_tasks=False, argument_kinds=None,
                  spin_limit=DEFAULT_SPIN_LIMIT, resident_waves_per_cu=None,
                  spin_sleep=1, promote_own_elements=True,
-                 prefetch_node_loads=True, value_flags=True):
+                 prefetch_node_loads=True, value_flags=True,
+                 gather_messages=False):
+        self.gather_messages = gather_messages
         self.value_flags = value_flags
         self._value_pull = None
         self._own_zero_arrays = set()
@@ -958,7 +965,8 @@ class HIPLowerer:
         if not rewritten:
             return None
         return {"array": array, "position": deepcopy(endpoint.slice),
-                "index_array": endpoint.value.id, "own_text": own_text}
+                "index_array": endpoint.value.id, "own_text": own_text,
+                "sites": sites, "mapped": mapped, "gather": None}
 
     def _fully_rewritten_arrays(self, body, target_loop, zero_initialised):
         """Lifted ``X = np.zeros(count)`` arrays whose element ``X[i]`` every
@@ -1025,6 +1033,90 @@ class HIPLowerer:
                 if not isinstance(node.ctx, ast.Load) or index != endpoint_text:
                     return None
         return {"array": array, "endpoint_text": endpoint_text}
+
+    def _gather_plan(self, box, arguments, lifted_loop_parameters):
+        """Gathered form of the mailbox protocol: no message slots at all.
+
+        When the distributed loop holds nothing but the one reduction
+        ``X[endpoint] op= value`` and ``value`` is a function of read-only
+        data at the position, the producer's block iterator and the
+        producer's final own element ``X[i]``, the consumer can form the
+        product itself: it walks its incoming positions (``_lcd_in_pos``,
+        ``_lcd_in_src``), polls ``X[source]`` -- ``X`` starts as the empty
+        marker and is written once per task, so the value is the flag -- and
+        adds the products in (source, position) order.  The producer's loop
+        disappears; a task ends with the single store of its own element.
+        Off by default: it saves the slot memory and the message writes, but
+        the coefficient gather ``Ax[_lcd_in_pos[s]]`` is scattered, and on
+        the 128^3 7-point grid it runs at 0.81 ms against 0.77 ms with
+        slots."""
+        mapped, sites = box["mapped"], box["sites"]
+        array = box["array"]
+        if (len(sites) != 1 or mapped.body != [sites[0]]
+                or self._all_written != {array} or self.block_task
+                or not self.promote_own_elements):
+            return None
+        site = sites[0]
+        kinds = self._kinds
+        readonly = {name for name in kinds.arrays
+                    if name not in self._all_written}
+        scalars = {name for name in arguments if name not in kinds.arrays}
+        scalars |= set(lifted_loop_parameters)
+        position, owner = mapped.target.id, self.loop_iterator
+        for node in ast.walk(site.value):
+            if isinstance(node, ast.Call):
+                return None
+            if isinstance(node, ast.Subscript):
+                if not isinstance(node.value, ast.Name):
+                    return None
+                if node.value.id == array:
+                    if ast.unparse(node.slice) != owner:
+                        return None
+                elif node.value.id not in readonly:
+                    return None
+            elif isinstance(node, ast.Name):
+                if node.id not in ({position, owner, array} | readonly
+                                   | scalars):
+                    return None
+
+        class Substitute(ast.NodeTransformer):
+            def visit_Subscript(self, node):
+                if (isinstance(node.value, ast.Name)
+                        and node.value.id == array):
+                    return ast.Name(id="_g_value", ctx=ast.Load())
+                return self.generic_visit(node)
+
+            def visit_Name(self, node):
+                if node.id == position:
+                    return ast.Name(id="_g_pos", ctx=node.ctx)
+                if node.id == owner:
+                    return ast.Name(id="_g_src", ctx=node.ctx)
+                return node
+
+        value = ast.fix_missing_locations(
+            Substitute().visit(deepcopy(site.value)))
+        # operands that do not wait for the producer load ahead of the poll
+        operands = []
+
+        class Operands(ast.NodeTransformer):
+            def visit_Subscript(self, node):
+                node = self.generic_visit(node)
+                if (isinstance(node.value, ast.Name)
+                        and node.value.id in readonly):
+                    name = f"_g_operand_{len(operands)}"
+                    operands.append((name, deepcopy(node),
+                                     kinds.arrays.get(node.value.id, FLOAT)))
+                    return ast.Name(id=name, ctx=ast.Load())
+                return node
+
+        value = ast.fix_missing_locations(Operands().visit(value))
+        for name, _, kind in operands:
+            kinds.locals[name] = kind
+        kinds.locals["_g_value"] = FLOAT
+        kinds.locals["_g_pos"] = INT
+        kinds.locals["_g_src"] = INT
+        return {"value": value, "operands": operands,
+                "negate": isinstance(site.op, ast.Sub)}
 
     def _mailbox_slot_load(self):
         """``_lcd_out_slot[position]``: the message slot a position writes."""
@@ -1132,8 +1224,11 @@ class HIPLowerer:
         if self._mailbox is not None and (
                 self._mailbox["array"] in self._fully_rewritten):
             self._own_zero_arrays.add(self._mailbox["array"])
+            if self.gather_messages and self.value_flags:
+                self._mailbox["gather"] = self._gather_plan(
+                    self._mailbox, arguments, lifted_loop_parameters)
         coherent = set(written_arrays) if self.execution_mode == "sync_free" else set()
-        if self._mailbox is not None:
+        if self._mailbox is not None and self._mailbox["gather"] is None:
             # only a task itself touches its element of the reduced array
             coherent.discard(self._mailbox["array"])
         emitter = _Emitter(kinds, self.reductions, lowered_ids,
@@ -1231,8 +1326,10 @@ class HIPLowerer:
             function_name=function_name,
             mailbox_index_array=(self._mailbox["index_array"]
                                  if self._mailbox else None),
-            value_flag_array=(self._value_pull["array"]
-                              if self._value_pull else None),
+            value_flag_array=(
+                self._value_pull["array"] if self._value_pull
+                else self._mailbox["array"]
+                if self._mailbox and self._mailbox["gather"] else None),
             executor_initialised=tuple(sorted(
                 self._own_zero_arrays
                 | ({self._value_pull["array"]} if self._value_pull else set()))),
@@ -1349,6 +1446,9 @@ class HIPLowerer:
                 names = list(VALUE_PULL_ARGUMENTS)
             elif self.dependence_protocol == PULL_DEPENDENCE:
                 names = list(PULL_ARGUMENTS)
+            elif (self.dependence_protocol == MAILBOX_DEPENDENCE
+                  and self._mailbox["gather"] is not None):
+                names = list(GATHER_ARGUMENTS)
             elif self.dependence_protocol == MAILBOX_DEPENDENCE:
                 names = list(MAILBOX_ARGUMENTS)
             else:
@@ -1741,7 +1841,17 @@ class HIPLowerer:
 
     def _task_body(self, body, emitter, local_names, target_loop, arguments):
         """C++ lines of one task (indent level 0), `i` already bound."""
-        mapped = self._find_mapped_loop(body)
+        gather = self._mailbox["gather"] if self._mailbox is not None else None
+        if gather is not None:
+            # the consumers form the products themselves: the producer's
+            # distributed loop is gone
+            site = self._mailbox["sites"][0]
+            body = [s for s in body if s is not self._mailbox["mapped"]]
+            emitter.lowered_ids.add(
+                self.reductions[(site.lineno, site.col_offset)][0])
+            mapped = None
+        else:
+            mapped = self._find_mapped_loop(body)
         hooks = None
         self._own_registers = []
         self._own_map = {}
@@ -2078,6 +2188,9 @@ class HIPLowerer:
                f"        if (_pending) {{ _mb_next = _lcd_in_ptr[{it}]; "
                f"_mb_end = _lcd_in_ptr[{it} + 1]; }}"]
               if protocol == MAILBOX_DEPENDENCE else []),
+            *(self._gather_fetch_lines(2, declare=True)
+              if protocol == MAILBOX_DEPENDENCE
+              and self._mailbox["gather"] is not None else []),
         ]
         value = self._value_pull
         if value is not None:
@@ -2098,6 +2211,8 @@ class HIPLowerer:
             lines += task(4, waiting + [f"_ready = !({total});"])
         elif protocol == PULL_DEPENDENCE:
             lines += self._pull_ready_lines(4)
+        elif protocol == MAILBOX_DEPENDENCE and self._mailbox["gather"] is not None:
+            lines += self._gather_ready_lines(4)
         elif protocol == MAILBOX_DEPENDENCE:
             lines += self._mailbox_ready_lines(4)
         else:
@@ -2144,6 +2259,63 @@ class HIPLowerer:
         ]
         lines.insert(1, "    bool _task_aborted = false;")
         return lines
+
+    def _gather_fetch_lines(self, indent, declare=False):
+        """Position, source and read-only operands of the incoming edge this
+        lane handles next (slot ``_mb_next + _lane``)."""
+        pad = "    " * indent
+        gather = self._mailbox["gather"]
+        emitter = self._emitter
+        lines = []
+        if declare:
+            lines.append(f"{pad}lcd_index_t _g_pos = 0, _g_src = 0;")
+            for name, _, kind in gather["operands"]:
+                ctype = "lcd_index_t" if kind == INT else "double"
+                lines.append(f"{pad}{ctype} {name} = 0;")
+        loads = " ".join(f"{name} = {emitter.expr(node)};"
+                         for name, node, _ in gather["operands"])
+        head = "if (_pending && _mb_next + _lane < _mb_end)" if declare else (
+            "if (_mb_next + _lane < _mb_end)")
+        lines.append(
+            f"{pad}{head} {{ _g_pos = _lcd_in_pos[_mb_next + _lane]; "
+            f"_g_src = _lcd_in_src[_mb_next + _lane]; {loads} }}")
+        return lines
+
+    def _gather_ready_lines(self, indent):
+        """Readiness for the gathered mailbox: lane ``l`` polls the final
+        value of the producer of incoming edge ``next + l`` and forms the
+        product; products are added in (source, position) order by
+        broadcasting them lane by lane, as far as they are there."""
+        pad = "    " * indent
+        own = self._mailbox["register"]
+        gather = self._mailbox["gather"]
+        array = self._mailbox["array"]
+        value = self._emitter.expr(gather["value"])
+        if gather["negate"]:
+            value = f"(-({value}))"
+        return [
+            f"{pad}bool _ready = _mb_next == _mb_end;",
+            f"{pad}if (!_ready) {{",
+            f"{pad}    const int _mb_have = (_mb_end - _mb_next) < LCD_TASK_LANES ? "
+            "(_mb_end - _mb_next) : LCD_TASK_LANES;",
+            f"{pad}    double _mb_value = lcd_empty();",
+            f"{pad}    if (_lane < _mb_have) {{",
+            f"{pad}        const double _g_value = lcd_ld(&{array}[_g_src]);",
+            f"{pad}        if (!lcd_is_empty(_g_value)) _mb_value = {value};",
+            f"{pad}    }}",
+            f"{pad}    int _mb_k = 0;",
+            f"{pad}    for (; _mb_k < _mb_have; ++_mb_k) {{",
+            f"{pad}        const double _mb_in = __shfl(_mb_value, _mb_k, LCD_TASK_LANES);",
+            f"{pad}        if (lcd_is_empty(_mb_in)) break;",
+            f"{pad}        {own} = {own} + _mb_in;",
+            f"{pad}    }}",
+            f"{pad}    if (_mb_k > 0) {{",
+            f"{pad}        _mb_next += _mb_k;",
+            *self._gather_fetch_lines(indent + 2),
+            f"{pad}    }}",
+            f"{pad}    _ready = _mb_next == _mb_end;",
+            f"{pad}}}",
+        ]
 
     def _mailbox_ready_lines(self, indent):
         """Readiness for the mailbox protocol: every incoming message has
@@ -2199,7 +2371,15 @@ class HIPLowerer:
     def _reset_kernel_text(self, reset_name):
         """Restores the mutable executor state before every sweep (the
         reference's reset kernel, compiler/cuda_lowering.py:737-853)."""
-        if self.dependence_protocol == MAILBOX_DEPENDENCE:
+        values_reset = (
+            "    if (t < count) { _lcd_values[2 * t] = LCD_EMPTY_WORD; "
+            "_lcd_values[2 * t + 1] = LCD_EMPTY_WORD; }\n"
+            "    if (t == 0) { task_counter[0] = 0; }\n",
+            "unsigned int* _lcd_values, int* task_counter, long long count")
+        if (self.dependence_protocol == MAILBOX_DEPENDENCE
+                and self._mailbox["gather"] is not None):
+            body, signature = values_reset
+        elif self.dependence_protocol == MAILBOX_DEPENDENCE:
             body = ("    if (t < count) { _lcd_mailbox[2 * t] = LCD_EMPTY_WORD; "
                     "_lcd_mailbox[2 * t + 1] = LCD_EMPTY_WORD; }\n"
                     "    if (t == 0) { task_counter[0] = 0; }\n")
@@ -2267,10 +2447,12 @@ class HIPLowerer:
                            MAILBOX_DEPENDENCE: "task_nodes"}.get(
                                self.dependence_protocol, "dep_count")
             reset_count = "_count"
-            if (self.dependence_protocol == PULL_DEPENDENCE
-                    and self._value_pull is not None):
+            if ((self.dependence_protocol == PULL_DEPENDENCE
+                 and self._value_pull is not None)
+                    or (self.dependence_protocol == MAILBOX_DEPENDENCE
+                        and self._mailbox["gather"] is not None)):
                 count_array = "task_nodes"
-                values = self._value_pull["array"]
+                values = (self._value_pull or self._mailbox)["array"]
                 reset_args = (f"({values}, task_counter, "
                               f"_hip.length({values}))")
                 reset_count = f"_hip.length({values})"
@@ -2310,7 +2492,8 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
                  chain_tasks=False, argument_kinds=None,
                  spin_limit=DEFAULT_SPIN_LIMIT, resident_waves_per_cu=None,
                  spin_sleep=1, promote_own_elements=True,
-                 prefetch_node_loads=True, value_flags=True):
+                 prefetch_node_loads=True, value_flags=True,
+                 gather_messages=False):
     """HIP counterpart of ``lower_to_numba_cuda``
     (compiler/cuda_lowering.py:2854-2884); same parameters plus
     ``task_lanes`` (lanes cooperating on one task, a power of two <= 64),
@@ -2329,5 +2512,6 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
         chain_tasks=chain_tasks, argument_kinds=argument_kinds,
         spin_limit=spin_limit, resident_waves_per_cu=resident_waves_per_cu,
         spin_sleep=spin_sleep, promote_own_elements=promote_own_elements,
-        prefetch_node_loads=prefetch_node_loads, value_flags=value_flags)
+        prefetch_node_loads=prefetch_node_loads, value_flags=value_flags,
+        gather_messages=gather_messages)
     return lowerer.lower(code)

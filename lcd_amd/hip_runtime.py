@@ -35,7 +35,7 @@ STATUS_ARGUMENT = "_lcd_status"
 
 DAG_PTR, DAG_INDEX, DAG_DEP_COUNT, DAG_EDGE_COUNT = 0, 1, 2, 3
 DAG_LEVEL_OF, DAG_WAVEFRONTS, DAG_WAVEFRONT_PTR = 4, 5, 6
-DAG_IN_PTR, DAG_IN_POS, DAG_OUT_SLOT = 7, 8, 9
+DAG_IN_PTR, DAG_IN_POS, DAG_OUT_SLOT, DAG_IN_SRC = 7, 8, 9, 10
 DAG_FLAG_LEVELS, DAG_FLAG_FORCE_KAHN, DAG_FLAG_INCOMING = 1, 2, 4
 
 DEVICE_COMPILE_OPTIONS = (
@@ -308,7 +308,8 @@ class DeviceDag:
               "dep_count": DAG_DEP_COUNT, "edge_count": DAG_EDGE_COUNT,
               "level_of": DAG_LEVEL_OF, "wavefronts": DAG_WAVEFRONTS,
               "wavefront_ptr": DAG_WAVEFRONT_PTR, "in_ptr": DAG_IN_PTR,
-              "in_pos": DAG_IN_POS, "out_slot": DAG_OUT_SLOT}
+              "in_pos": DAG_IN_POS, "out_slot": DAG_OUT_SLOT,
+              "in_src": DAG_IN_SRC}
 
     def __init__(self, device, handle):
         self.device = device

@@ -102,6 +102,9 @@ def test_incoming_positions(device, oracle):
     for v in range(n):
         want = [p for _, p in sorted(expected[v])]
         assert in_pos[in_ptr[v]:in_ptr[v + 1]].tolist() == want
+    in_src = dag.host("in_src")
+    want_src = [seg for v in range(n) for seg, _ in sorted(expected[v])]
+    assert in_src.tolist() == want_src
     # out_slot inverts the listing; positions without an edge hold -1
     out_slot = dag.host("out_slot")
     assert len(out_slot) == len(idx)

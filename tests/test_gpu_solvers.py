@@ -51,6 +51,11 @@ CSC_VARIANTS = [
          dependence_protocol="mailbox"),
     dict(execution_mode="sync_free", threads_per_block=128, task_lanes=2,
          dependence_protocol="mailbox", thread_unroll=2),
+    dict(execution_mode="sync_free", threads_per_block=256, task_lanes=4,
+         dependence_protocol="mailbox", gather_messages=True),
+    dict(execution_mode="sync_free", threads_per_block=128, task_lanes=8,
+         dependence_protocol="mailbox", gather_messages=True,
+         thread_unroll=2),
     dict(execution_mode="sync_free", threads_per_block=128, n_warp=1,
          dependence_protocol="mailbox"),
     dict(),   # scheduler decides
@@ -76,7 +81,10 @@ def test_sptrsv_csc_variants(oracle, options):
         solve_and_check(solver, work, expected, exact=exact)
     if exact:
         assert solver.current_schedule.dependence_protocol == "mailbox"
-        assert "_lcd_mailbox" in solver.hip_kernel_source
+        slots = "_lcd_mailbox" in solver.hip_kernel_source
+        # no message slots in the gathered form
+        assert slots == (not options.get("gather_messages", False))
+        assert ("_lcd_in_src" in solver.hip_kernel_source) != slots
     schedule = solver.current_schedule
     if "execution_mode" in options:
         assert schedule.execution_mode == options["execution_mode"]

@@ -484,6 +484,25 @@ def test_csr_pull_polls_the_values_themselves():
             assert "done" in flagged.kernel_arguments
 
 
+def test_gathered_mailbox_drops_the_producer_loop():
+    module = demo_source("sptrsv", "sptrsv_csc_loop")
+    result = lower(module, execution_mode="sync_free",
+                   thread_loop_iterator="j", task_lanes=4,
+                   dependence_protocol="mailbox", gather_messages=True)
+    kernel = result.kernel_source
+    assert result.dependence_protocol == "mailbox"
+    assert result.value_flag_array == "x"
+    assert "_lcd_mailbox" not in result.kernel_arguments
+    assert {"_lcd_in_ptr", "_lcd_in_pos", "_lcd_in_src"} <= set(
+        result.kernel_arguments)
+    assert "_g_operand_0 = Ax[_g_pos];" in kernel
+    assert "const double _g_value = lcd_ld(&x[_g_src]);" in kernel
+    assert "_mb_value = (_g_operand_0 * _g_value);" in kernel
+    assert "lcd_atomic_add" not in kernel.split("while (true)")[1]
+    assert "if (_lane == 0) lcd_st(&x[i], _lcd_own_0);" in kernel
+    hip_runtime.compile_code(result.source)
+
+
 def test_mailbox_needs_no_clear_of_the_solution():
     module = demo_source("sptrsv", "sptrsv_csc_loop")
     result = lower(module, execution_mode="sync_free",
