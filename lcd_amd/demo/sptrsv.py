@@ -73,3 +73,54 @@ def simple_sptrsv_csc(Ap, Ai, Ax, b, n):
         for j in range(Ap[i] + 1, Ap[i + 1]):
             x[Ai[j]] += Ax[j] * x[i]
     return x
+
+
+def run_demo(matrix_path, max_size=None, storage="both", verbose=True,
+             **options):
+    """Solve ``L x = b`` for the lower triangle of a Matrix Market input with
+    the generated CSR and/or CSC solver (compiler/demo/sptrsv.py:44-78);
+    returns ``{storage: (x, max_abs_error)}`` against the manufactured
+    solution ``linspace(1, 2, n)``."""
+    from lcd_amd.demo.matrix import (DEFAULT_MAX_N, load_matrix_market,
+                                     lower_triangle, manufactured_rhs)
+    source = load_matrix_market(
+        matrix_path, DEFAULT_MAX_N if max_size is None else max_size)
+    compilers = {"csr": compile_sptrsv_csr, "csc": compile_sptrsv_csc}
+    selected = compilers if storage == "both" else {storage: compilers[storage]}
+    results = {}
+    for name, compile_solver in selected.items():
+        indptr, indices, data = lower_triangle(source, name)
+        rhs, expected = manufactured_rhs(indptr, indices, data, name)
+        solver = compile_solver(**options)
+        result = solver(indptr, indices, data, rhs, len(rhs))
+        error = float(np.max(np.abs(result - expected)))
+        results[name] = (result, error)
+        if verbose:
+            print(f"SpTRSV {name.upper()}: n={len(rhs)}, nnz={len(data)}, "
+                  f"max_abs_error={error:.3e}")
+    return results
+
+
+def main(argv=None):
+    import argparse
+    parser = argparse.ArgumentParser(
+        description="Run generated CSR/CSC SpTRSV on a Matrix Market input.")
+    parser.add_argument("matrix",
+                        help="path to a square real Matrix Market file")
+    parser.add_argument("--max-n", type=int, default=None,
+                        help="leading principal sample size; 0 = full matrix")
+    parser.add_argument("--storage", choices=("csr", "csc", "both"),
+                        default="both")
+    parser.add_argument("--execution-mode", default=None,
+                        choices=("wavefront", "sync_free"))
+    args = parser.parse_args(argv)
+    if args.max_n is not None and args.max_n < 0:
+        parser.error("--max-n must be nonnegative")
+    options = {}
+    if args.execution_mode:
+        options["execution_mode"] = args.execution_mode
+    run_demo(args.matrix, args.max_n, args.storage, **options)
+
+
+if __name__ == "__main__":
+    main()
