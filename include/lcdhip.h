@@ -223,10 +223,24 @@ typedef struct {
 #define LCDHIP_DAG_IN_POS 8         /* candidate edges */
 #define LCDHIP_DAG_OUT_SLOT 9       /* sum of idx_size over the rules */
 #define LCDHIP_DAG_IN_SRC 10        /* candidate edges: source of in_pos[k] */
-#define LCDHIP_DAG_ARRAYS 11
+/* After lcdhip_dag_band_chains: */
+#define LCDHIP_DAG_TASK_NODES 11    /* n: chain members, chain after chain */
+#define LCDHIP_DAG_TASK_PTR 12      /* tasks + 1: chain offsets */
+#define LCDHIP_DAG_BAND_PTR 13      /* bands + 1: first chain of every band */
+#define LCDHIP_DAG_ARRAYS 14
 
 int lcdhip_dag_build(const lcdhip_dag_rule *rules, int rule_count, int64_t n,
                      uint32_t flags, lcdhip_stream stream, lcdhip_dag **out);
+/* Chain tasks for band_width > 1 (replaces _band_chains,
+ * compiler/dag_preprocessing.py:258-298): the level sets are cut into bands of
+ * band_width consecutive levels; inside a band every connected component of
+ * the DAG becomes one task whose members run in (level, id) order.  Chains are
+ * listed band by band, inside a band by their first member.  Needs a dag built
+ * with LCDHIP_DAG_LEVELS whose level sets cover every node.  May be called
+ * again with another width; the previous chain arrays are released. */
+int lcdhip_dag_band_chains(lcdhip_dag *dag, int64_t band_width,
+                           lcdhip_stream stream, int64_t *tasks_out,
+                           int64_t *bands_out);
 int lcdhip_dag_get_info(const lcdhip_dag *dag, lcdhip_dag_info *out);
 int lcdhip_dag_array(const lcdhip_dag *dag, int which, void **d_out,
                      int64_t *count_out);

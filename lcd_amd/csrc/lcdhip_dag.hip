@@ -131,6 +131,108 @@ __global__ void out_slot_kernel(const int32_t *__restrict__ in_pos,
         out_slot[in_pos[k]] = static_cast<int32_t>(k);
 }
 
+
+// ---- band chains: connected components inside bands of consecutive levels
+
+__global__ void position_of_kernel(const int32_t *__restrict__ wavefronts,
+                                   int64_t n, int32_t *__restrict__ position_of,
+                                   int32_t *__restrict__ parent)
+{
+    int64_t p = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (p >= n)
+        return;
+    position_of[wavefronts[p]] = static_cast<int32_t>(p);
+    parent[p] = static_cast<int32_t>(p);
+}
+
+__device__ __forceinline__ int32_t chain_root(const int32_t *parent, int32_t p)
+{
+    // parents only ever decrease, so a stale read still leads to the root
+    int32_t q = __hip_atomic_load(&parent[p], __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+    while (q != p) {
+        p = q;
+        q = __hip_atomic_load(&parent[p], __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return p;
+}
+
+// One pass over the edges whose endpoints share a band: the larger root is
+// hung under the smaller one.  A hook can lose against a concurrent smaller
+// one; the pass is repeated until no edge joins two roots.
+__global__ void chain_hook_kernel(const int32_t *__restrict__ dag_ptr,
+                                  const int32_t *__restrict__ dag_index,
+                                  const int32_t *__restrict__ level_of,
+                                  const int32_t *__restrict__ position_of,
+                                  int64_t n, int32_t band_width,
+                                  int32_t *parent, int32_t *changed)
+{
+    int64_t u = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (u >= n)
+        return;
+    const int32_t band = level_of[u] / band_width;
+    const int32_t pu = position_of[u];
+    for (int32_t e = dag_ptr[u]; e < dag_ptr[u + 1]; ++e) {
+        const int32_t v = dag_index[e];
+        if (level_of[v] / band_width != band)
+            continue;
+        int32_t a = chain_root(parent, pu);
+        int32_t b = chain_root(parent, position_of[v]);
+        if (a == b)
+            continue;
+        const int32_t high = a > b ? a : b, low = a > b ? b : a;
+        atomicMin(&parent[high], low);
+        *changed = 1;
+    }
+}
+
+__global__ void chain_compress_kernel(int32_t *parent, int64_t n)
+{
+    int64_t p = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (p < n)
+        parent[p] = chain_root(parent, static_cast<int32_t>(p));
+}
+
+__global__ void chain_keys_kernel(const int32_t *__restrict__ parent, int64_t n,
+                                  unsigned long long *__restrict__ keys)
+{
+    int64_t p = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (p < n)
+        keys[p] = (static_cast<unsigned long long>(parent[p]) << 32) |
+                  static_cast<unsigned long long>(p);
+}
+
+// sorted keys (root position, member position) -> members, chain starts
+__global__ void chain_members_kernel(const unsigned long long *__restrict__ keys,
+                                     const int32_t *__restrict__ wavefronts,
+                                     int64_t n, int32_t *__restrict__ task_nodes,
+                                     int32_t *__restrict__ starts)
+{
+    int64_t k = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (k >= n)
+        return;
+    task_nodes[k] = wavefronts[keys[k] & 0xffffffffull];
+    starts[k] = (k == 0 || (keys[k] >> 32) != (keys[k - 1] >> 32)) ? 1 : 0;
+}
+
+__global__ void chain_offsets_kernel(const unsigned long long *__restrict__ keys,
+                                     const int32_t *__restrict__ starts,
+                                     const int32_t *__restrict__ task_of,
+                                     const int32_t *__restrict__ wavefronts,
+                                     const int32_t *__restrict__ level_of,
+                                     int64_t n, int32_t band_width,
+                                     int32_t *__restrict__ task_ptr,
+                                     int32_t *__restrict__ band_tasks)
+{
+    int64_t k = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (k >= n || !starts[k])
+        return;
+    task_ptr[task_of[k]] = static_cast<int32_t>(k);
+    const int32_t first = wavefronts[keys[k] >> 32];
+    atomicAdd(&band_tasks[level_of[first] / band_width], 1);
+}
+
 __global__ void low_words_kernel(const unsigned long long *__restrict__ keys,
                                  int64_t count, int32_t *__restrict__ out)
 {
@@ -729,6 +831,139 @@ static int build_levels(lcdhip_dag *dag, const unsigned long long *d_transposed,
         dag->info.max_level_width = widest;
     }
     LCDHIP_CHECK(hipStreamSynchronize(stream));
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_dag_band_chains(lcdhip_dag *dag, int64_t band_width,
+                                      lcdhip_stream stream_handle,
+                                      int64_t *tasks_out, int64_t *bands_out)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (!dag || band_width <= 0 || band_width > 0x7fffffff) {
+        set_error("The band width must be a positive integer.");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    if (!dag->arrays[LCDHIP_DAG_WAVEFRONTS] ||
+        dag->info.scheduled != dag->info.n) {
+        set_error("band chains need level sets that cover every node");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    hipStream_t stream = resolve_stream(stream_handle);
+    const int64_t n = dag->info.n;
+    const int64_t bands = (dag->info.levels + band_width - 1) / band_width;
+    for (int which : {LCDHIP_DAG_TASK_NODES, LCDHIP_DAG_TASK_PTR,
+                      LCDHIP_DAG_BAND_PTR})
+        if (dag->arrays[which]) {
+            (void)hipFree(dag->arrays[which]);
+            dag->arrays[which] = nullptr;
+            dag->counts[which] = 0;
+        }
+    int status;
+    if ((status = dag_alloc(dag, LCDHIP_DAG_TASK_NODES, n))) return status;
+    if ((status = dag_alloc(dag, LCDHIP_DAG_BAND_PTR, bands + 1))) return status;
+    int32_t *band_ptr = dag->arrays[LCDHIP_DAG_BAND_PTR];
+    LCDHIP_CHECK(hipMemsetAsync(band_ptr, 0, (bands + 1) * 4, stream));
+    int64_t tasks = 0;
+    if (n > 0) {
+        const int32_t *wavefronts = dag->arrays[LCDHIP_DAG_WAVEFRONTS];
+        const int32_t *level_of = dag->arrays[LCDHIP_DAG_LEVEL_OF];
+        Scratch scratch;
+        int32_t *position_of = nullptr, *parent = nullptr, *changed = nullptr;
+        int32_t *starts = nullptr, *task_of = nullptr, *band_tasks = nullptr;
+        unsigned long long *keys = nullptr, *sorted = nullptr;
+        LCDHIP_CHECK(scratch.alloc(&position_of, n));
+        LCDHIP_CHECK(scratch.alloc(&parent, n));
+        LCDHIP_CHECK(scratch.alloc(&changed, 1));
+        LCDHIP_CHECK(scratch.alloc(&starts, n));
+        LCDHIP_CHECK(scratch.alloc(&task_of, n));
+        LCDHIP_CHECK(scratch.alloc(&band_tasks, bands + 1));
+        LCDHIP_CHECK(scratch.alloc(&keys, n));
+        LCDHIP_CHECK(scratch.alloc(&sorted, n));
+        hipLaunchKernelGGL(position_of_kernel, dim3(blocks_for(n)), dim3(kBlock),
+                           0, stream, wavefronts, n, position_of, parent);
+        // every pass at least halves nothing in the worst case, so bound the
+        // passes by the node count; practical inputs need a handful
+        for (int64_t pass = 0; pass <= n; ++pass) {
+            int32_t flag = 0;
+            LCDHIP_CHECK(hipMemsetAsync(changed, 0, 4, stream));
+            hipLaunchKernelGGL(chain_hook_kernel, dim3(blocks_for(n)),
+                               dim3(kBlock), 0, stream,
+                               dag->arrays[LCDHIP_DAG_PTR],
+                               dag->arrays[LCDHIP_DAG_INDEX], level_of,
+                               position_of, n, static_cast<int32_t>(band_width),
+                               parent, changed);
+            hipLaunchKernelGGL(chain_compress_kernel, dim3(blocks_for(n)),
+                               dim3(kBlock), 0, stream, parent, n);
+            LCDHIP_CHECK(hipMemcpyAsync(&flag, changed, 4,
+                                        hipMemcpyDeviceToHost, stream));
+            LCDHIP_CHECK(hipStreamSynchronize(stream));
+            if (!flag)
+                break;
+        }
+        hipLaunchKernelGGL(chain_keys_kernel, dim3(blocks_for(n)), dim3(kBlock),
+                           0, stream, parent, n, keys);
+        const int end_bit = std::min(64, 32 + bits_for(static_cast<uint64_t>(n)));
+        size_t sort_bytes = 0;
+        char *sort_temp = nullptr;
+        LCDHIP_CHECK(rocprim::radix_sort_keys(nullptr, sort_bytes, keys, sorted,
+                                              static_cast<size_t>(n), 0, end_bit,
+                                              stream));
+        LCDHIP_CHECK(scratch.alloc(&sort_temp, sort_bytes));
+        LCDHIP_CHECK(rocprim::radix_sort_keys(sort_temp, sort_bytes, keys, sorted,
+                                              static_cast<size_t>(n), 0, end_bit,
+                                              stream));
+        hipLaunchKernelGGL(chain_members_kernel, dim3(blocks_for(n)),
+                           dim3(kBlock), 0, stream, sorted, wavefronts, n,
+                           dag->arrays[LCDHIP_DAG_TASK_NODES], starts);
+        size_t scan_bytes = 0;
+        char *scan_temp = nullptr;
+        LCDHIP_CHECK(rocprim::exclusive_scan(nullptr, scan_bytes, starts, task_of,
+                                             0, static_cast<size_t>(n),
+                                             rocprim::plus<int32_t>(), stream));
+        LCDHIP_CHECK(scratch.alloc(&scan_temp, scan_bytes));
+        LCDHIP_CHECK(rocprim::exclusive_scan(scan_temp, scan_bytes, starts,
+                                             task_of, 0, static_cast<size_t>(n),
+                                             rocprim::plus<int32_t>(), stream));
+        int32_t last_task = 0, last_start = 0;
+        LCDHIP_CHECK(hipMemcpyAsync(&last_task, task_of + (n - 1), 4,
+                                    hipMemcpyDeviceToHost, stream));
+        LCDHIP_CHECK(hipMemcpyAsync(&last_start, starts + (n - 1), 4,
+                                    hipMemcpyDeviceToHost, stream));
+        LCDHIP_CHECK(hipStreamSynchronize(stream));
+        tasks = static_cast<int64_t>(last_task) + last_start;
+        if ((status = dag_alloc(dag, LCDHIP_DAG_TASK_PTR, tasks + 1)))
+            return status;
+        int32_t *task_ptr = dag->arrays[LCDHIP_DAG_TASK_PTR];
+        LCDHIP_CHECK(hipMemsetAsync(band_tasks, 0, (bands + 1) * 4, stream));
+        hipLaunchKernelGGL(chain_offsets_kernel, dim3(blocks_for(n)),
+                           dim3(kBlock), 0, stream, sorted, starts, task_of,
+                           wavefronts, level_of, n,
+                           static_cast<int32_t>(band_width), task_ptr,
+                           band_tasks);
+        const int32_t total = static_cast<int32_t>(n);
+        LCDHIP_CHECK(hipMemcpyAsync(task_ptr + tasks, &total, 4,
+                                    hipMemcpyHostToDevice, stream));
+        size_t band_bytes = 0;
+        char *band_temp = nullptr;
+        LCDHIP_CHECK(rocprim::exclusive_scan(
+            nullptr, band_bytes, band_tasks, band_ptr, 0,
+            static_cast<size_t>(bands + 1), rocprim::plus<int32_t>(), stream));
+        LCDHIP_CHECK(scratch.alloc(&band_temp, band_bytes));
+        LCDHIP_CHECK(rocprim::exclusive_scan(
+            band_temp, band_bytes, band_tasks, band_ptr, 0,
+            static_cast<size_t>(bands + 1), rocprim::plus<int32_t>(), stream));
+        LCDHIP_CHECK(hipGetLastError());
+        LCDHIP_CHECK(hipStreamSynchronize(stream));
+    } else {
+        if ((status = dag_alloc(dag, LCDHIP_DAG_TASK_PTR, 1))) return status;
+        LCDHIP_CHECK(hipMemsetAsync(dag->arrays[LCDHIP_DAG_TASK_PTR], 0, 4,
+                                    stream));
+        LCDHIP_CHECK(hipStreamSynchronize(stream));
+    }
+    if (tasks_out)
+        *tasks_out = tasks;
+    if (bands_out)
+        *bands_out = bands;
     return LCDHIP_OK;
 }
 

@@ -255,15 +255,27 @@ def execution_data_from_device_dag(dag, execution_mode, warp_mapped,
                                    pushed=False, band_width=1, mailbox=False):
     """Executor arrays straight from the on-device inspector (no host copy
     except the level offsets the launcher iterates over)."""
-    if band_width != 1:
+    if not isinstance(band_width, int) or band_width <= 0:
         raise DAGPreprocessingError(
-            "band_width > 1 (chain tasks) is not available on the device "
-            "inspector yet.")
+            "The band width must be a positive integer.")
     if dag.scheduled != dag.n:
         raise DAGPreprocessingError(
             "Wavefront scheduling did not cover every DAG node; the DAG may "
             f"contain a cycle. Scheduled {dag.scheduled} of {dag.n} nodes.")
     counts = dag.array("edge_count" if pushed else "dep_count")
+    if band_width != 1:
+        # chain tasks: connected components inside bands of levels, built on
+        # the device; only the band offsets come to the host (the launcher
+        # iterates over them)
+        if execution_mode.replace("-", "_") != "wavefront":
+            raise DAGPreprocessingError(
+                "band_width > 1 (chain tasks) needs the wavefront executor.")
+        dag.band_chains(band_width)
+        return WarpTaskExecutionData(
+            task_nodes=dag.array("task_nodes"), task_ptr=dag.array("task_ptr"),
+            band_ptr=dag.host("band_ptr"), dep_count=counts,
+            initial_dep_count=counts, dag_ptr=dag.array("dag_ptr"),
+            dag_index=dag.array("dag_index"))
     if mailbox:
         # destination v reads message slots in_ptr[v] .. in_ptr[v+1); the
         # entry at position p writes slot out_slot[p]; slot k carries the

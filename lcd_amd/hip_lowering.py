@@ -1227,7 +1227,12 @@ class HIPLowerer:
             if self.gather_messages and self.value_flags:
                 self._mailbox["gather"] = self._gather_plan(
                     self._mailbox, arguments, lifted_loop_parameters)
-        coherent = set(written_arrays) if self.execution_mode == "sync_free" else set()
+        # arrays other tasks of the same launch write go through coherent
+        # accessors: always in the persistent executor, and in a level launch
+        # when a chain task reads what its earlier members wrote
+        coherent = (set(written_arrays)
+                    if self.execution_mode == "sync_free" or self.chain_tasks
+                    else set())
         if self._mailbox is not None and self._mailbox["gather"] is None:
             # only a task itself touches its element of the reduced array
             coherent.discard(self._mailbox["array"])
@@ -2075,10 +2080,15 @@ class HIPLowerer:
         def node_loop(indent, body_fn):
             pad = "    " * indent
             if self.chain_tasks:
+                # a member's updates are complete and visible before the next
+                # member of the chain starts
                 return ([f"{pad}for (int _pos = task_ptr[_task]; "
                          f"_pos < task_ptr[_task + 1]; ++_pos) {{",
                          f"{pad}    {it} = task_nodes[_pos];",
-                         *body_fn(indent + 1), f"{pad}}}"])
+                         *body_fn(indent + 1),
+                         f"{pad}    lcd_release_fence();",
+                         f"{pad}    {self.group_sync}",
+                         f"{pad}}}"])
             return [f"{pad}{it} = task_nodes[_task];", *body_fn(indent)]
 
         if self.execution_mode == "plain":
@@ -2115,7 +2125,7 @@ class HIPLowerer:
         protocol = self.dependence_protocol
         if self.chain_tasks:
             raise HIPLoweringError(
-                "Chain tasks are not supported by the sync-free executor.")
+                "band_width > 1 (chain tasks) needs the wavefront executor.")
         lines = ["    const int _task_count = (int)task_count;"]
         if self.block_task:
             lines += [

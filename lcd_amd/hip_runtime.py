@@ -36,6 +36,7 @@ STATUS_ARGUMENT = "_lcd_status"
 DAG_PTR, DAG_INDEX, DAG_DEP_COUNT, DAG_EDGE_COUNT = 0, 1, 2, 3
 DAG_LEVEL_OF, DAG_WAVEFRONTS, DAG_WAVEFRONT_PTR = 4, 5, 6
 DAG_IN_PTR, DAG_IN_POS, DAG_OUT_SLOT, DAG_IN_SRC = 7, 8, 9, 10
+DAG_TASK_NODES, DAG_TASK_PTR, DAG_BAND_PTR = 11, 12, 13
 DAG_FLAG_LEVELS, DAG_FLAG_FORCE_KAHN, DAG_FLAG_INCOMING = 1, 2, 4
 
 DEVICE_COMPILE_OPTIONS = (
@@ -121,7 +122,8 @@ EXPORTED_SYMBOLS = (
     "lcdhip_launch_levels", "lcdhip_graph_begin_capture",
     "lcdhip_graph_end_capture", "lcdhip_graph_launch", "lcdhip_graph_destroy",
     "lcdhip_dag_build", "lcdhip_dag_get_info", "lcdhip_dag_array",
-    "lcdhip_dag_download", "lcdhip_dag_destroy", "lcdhip_lookup_build",
+    "lcdhip_dag_download", "lcdhip_dag_destroy", "lcdhip_dag_band_chains",
+    "lcdhip_lookup_build",
     "lcdhip_digest",
 )
 
@@ -309,7 +311,9 @@ class DeviceDag:
               "level_of": DAG_LEVEL_OF, "wavefronts": DAG_WAVEFRONTS,
               "wavefront_ptr": DAG_WAVEFRONT_PTR, "in_ptr": DAG_IN_PTR,
               "in_pos": DAG_IN_POS, "out_slot": DAG_OUT_SLOT,
-              "in_src": DAG_IN_SRC}
+              "in_src": DAG_IN_SRC, "task_nodes": DAG_TASK_NODES,
+              "task_ptr": DAG_TASK_PTR, "band_ptr": DAG_BAND_PTR}
+    CHAIN_ARRAYS = ("task_nodes", "task_ptr", "band_ptr")
 
     def __init__(self, device, handle):
         self.device = device
@@ -345,6 +349,23 @@ class DeviceDag:
                 out.ctypes.data_as(ctypes.c_void_p), ctypes.c_int64(out.size)))
             self._host[name] = out
         return self._host[name]
+
+    def band_chains(self, band_width):
+        """Build the chain tasks of bands of ``band_width`` levels on the
+        device; afterwards ``task_nodes``, ``task_ptr`` and ``band_ptr`` are
+        arrays of this DAG.  Returns ``(tasks, bands)``."""
+        if not isinstance(band_width, int) or band_width <= 0:
+            raise HIPRuntimeError("The band width must be a positive integer.",
+                                  ERR_ARGUMENT)
+        for name in self.CHAIN_ARRAYS:
+            self._views.pop(name, None)
+            self._host.pop(name, None)
+        tasks, bands = ctypes.c_int64(), ctypes.c_int64()
+        _check(load_library().lcdhip_dag_band_chains(
+            self.handle, ctypes.c_int64(band_width), self.device.stream,
+            ctypes.byref(tasks), ctypes.byref(bands)))
+        self.chain_band_width = band_width
+        return int(tasks.value), int(bands.value)
 
     def successors(self):
         ptr, index = self.host("dag_ptr"), self.host("dag_index")

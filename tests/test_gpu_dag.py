@@ -64,6 +64,52 @@ def test_dag_matches_oracle(device, oracle, name, overrides, force_kahn):
             assert dag.levels == sum(grid) - len(grid) + 1
 
 
+@pytest.mark.parametrize("name,overrides", SMALL)
+def test_band_chains_match_oracle(device, oracle, name, overrides):
+    """Chain tasks (band_width > 1): connected components inside bands of
+    levels, listed by first member, members in (level, id) order."""
+    if name == "c5":
+        overrides = dict(n=4000)
+    work = workloads.configuration(name, **overrides)
+    rule = _rule_for(oracle, work)
+    dag = device.dag_build([rule], work.n, levels=True)
+    expected = oracle.dag_build([rule], work.n)
+    for width in (1, 2, 3, 7, 64, 10 ** 6):
+        print("chains", name, overrides, width, flush=True)
+        tasks, bands = dag.band_chains(width)
+        nodes, ptr, band_ptr = expected.band_chains(width)
+        assert tasks == len(ptr) - 1 and bands == len(band_ptr) - 1
+        np.testing.assert_array_equal(dag.host("task_nodes"), nodes)
+        np.testing.assert_array_equal(dag.host("task_ptr"), ptr)
+        np.testing.assert_array_equal(dag.host("band_ptr"), band_ptr)
+    # width 1: every node is its own chain, bands are the levels
+    dag.band_chains(1)
+    np.testing.assert_array_equal(dag.host("task_nodes"), dag.host("wavefronts"))
+    np.testing.assert_array_equal(dag.host("task_ptr"), np.arange(work.n + 1))
+    np.testing.assert_array_equal(dag.host("band_ptr"), dag.host("wavefront_ptr"))
+    with pytest.raises(Exception, match="positive integer"):
+        dag.band_chains(0)
+
+
+def test_band_chains_of_a_random_dag(device, oracle):
+    rng = np.random.default_rng(11)
+    n = 5000
+    counts = rng.integers(0, 4, n)
+    ptr = np.zeros(n + 1, dtype=np.int32)
+    np.cumsum(counts, out=ptr[1:])
+    idx = np.minimum(np.repeat(np.arange(n), counts)
+                     + rng.integers(1, 40, int(ptr[-1])), n - 1).astype(np.int32)
+    rule = oracle.make_rule(ptr, idx, True, guard=oracle.GUARD_GREATER)
+    dag = device.dag_build([rule], n, levels=True)
+    expected = oracle.dag_build([rule], n)
+    for width in (2, 5, 33):
+        dag.band_chains(width)
+        nodes, task_ptr, band_ptr = expected.band_chains(width)
+        np.testing.assert_array_equal(dag.host("task_nodes"), nodes)
+        np.testing.assert_array_equal(dag.host("task_ptr"), task_ptr)
+        np.testing.assert_array_equal(dag.host("band_ptr"), band_ptr)
+
+
 def test_golden_vectors(device, oracle):
     with open(GOLDEN) as handle:
         golden = json.load(handle)

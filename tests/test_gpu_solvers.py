@@ -151,6 +151,46 @@ def test_sptrsv_matches_scipy_and_manufactured_solution(oracle):
     np.testing.assert_allclose(result, reference, rtol=1e-10, atol=1e-12)
 
 
+@pytest.mark.parametrize("band_width", [2, 5, 64])
+def test_band_chains_run_in_the_wavefront_executor(oracle, band_width):
+    """band_width > 1: one task per connected component of a band of levels,
+    members in sequence; fewer launches, same results."""
+    print("band chains", band_width, flush=True)
+    csc = sptrsv.compile_sptrsv_csc(execution_mode="wavefront",
+                                    threads_per_block=128, task_lanes=4,
+                                    band_width=band_width)
+    csr = sptrsv.compile_sptrsv_csr(execution_mode="wavefront",
+                                    threads_per_block=128, task_lanes=8,
+                                    band_width=band_width)
+    lane = sptrsv.compile_sptrsv_csc(execution_mode="wavefront",
+                                     threads_per_block=64, thread_map=None,
+                                     band_width=band_width)
+    for name, overrides in (("c1", {}), ("c2", dict(nx=20, ny=18, nz=16)),
+                            ("c5", dict(n=3000))):
+        work = workloads.configuration(name, **overrides)
+        expected = oracle.sptrsv_csc(work.indptr, work.indices, work.data,
+                                     work.rhs, work.n)
+        solve_and_check(csc, work, expected)
+        solve_and_check(lane, work, expected)
+    assert "task_ptr[_task + 1]" in csc.hip_kernel_source
+    work = workloads.configuration("c3", n=20000)
+    expected = oracle.sptrsv_csr(work.indptr, work.indices, work.data,
+                                 work.rhs, work.n)
+    solve_and_check(csr, work, expected)
+    factor = spilu0.compile_ilu0_csr(execution_mode="wavefront",
+                                     threads_per_block=128, task_lanes=8,
+                                     thread_unroll=1, band_width=band_width)
+    work = workloads.configuration("c4", nx=40, ny=36)
+    expected = oracle.ilu0_csr(work.data, work.indices, work.indptr)
+    np.testing.assert_array_equal(
+        factor(work.data.copy(), work.indices, work.indptr), expected)
+    with pytest.raises(Exception, match="wavefront executor"):
+        sptrsv.compile_sptrsv_csc(
+            execution_mode="sync_free", threads_per_block=128, task_lanes=4,
+            band_width=band_width)(work.indptr, work.indices, work.data,
+                                   np.ones(work.n), work.n)
+
+
 ILU_VARIANTS = [
     dict(execution_mode="wavefront", threads_per_block=128, thread_unroll=1),
     dict(execution_mode="wavefront", threads_per_block=128, task_lanes=4),
