@@ -248,6 +248,24 @@ def main():
             "first_call_s": round(first_call_s, 4),
         },
     }
+    # the on-device inspector alone (edges, counts, level sets and, for the
+    # mailbox protocol, the incoming listing), operands resident
+    from lcd_amd.dag_codegen import build_device_dag
+    names = solver.dag_plan.arguments
+    values = dict(zip(names, list(operands) + scalars))
+    if work.kind == "ilu0_csr":
+        values["n"] = work.n
+    mailbox = solver.hip_lowering.dependence_protocol == "mailbox"
+    inspector = []
+    for _ in range(3):
+        device.synchronize()
+        t0 = time.perf_counter()
+        dag = build_device_dag(solver.dag_plan, values, device, levels=True,
+                               incoming=mailbox)
+        device.synchronize()
+        inspector.append(time.perf_counter() - t0)
+        dag.destroy()
+    result["setup"]["inspector_ms"] = round(min(inspector) * 1e3, 3)
     if work.true_flops is not None:
         result["gflops"] = round(work.true_flops / (ms_per_step * 1e-3) / 1e9, 3)
     result["gflops_reference_formula"] = round(

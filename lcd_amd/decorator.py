@@ -191,6 +191,7 @@ def parallel(**kwargs):
                     spin_sleep=kwargs.get("spin_sleep", 1),
                     value_flags=kwargs.get("value_flags", True),
                     gather_messages=kwargs.get("gather_messages", False),
+                    segment_cache=kwargs.get("segment_cache", True),
                 )
             return lowered_variants[lowering_key]
 

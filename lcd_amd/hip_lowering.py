@@ -344,6 +344,7 @@ class _Emitter:
         self.coherent_arrays = set(coherent_arrays)
         self.mailbox = None
         self.lowerer = None
+        self.segment = None     # own-segment staging plan (HIPLowerer)
 
     # ---- expressions
     def expr(self, node):
@@ -362,6 +363,12 @@ class _Emitter:
             if not isinstance(node.value, ast.Name):
                 raise HIPLoweringError("Only 1-D array indexing is supported.")
             element = f"{node.value.id}[{self.expr(node.slice)}]"
+            segment = self.segment
+            if segment is not None and node.value.id == segment["array"]:
+                name = ("lcd_seg_ldc" if node.value.id in self.coherent_arrays
+                        else "lcd_seg_ld")
+                return (f"{name}({node.value.id}, _lcd_seg, _lcd_seg_base, "
+                        f"_lcd_seg_limit, {self.expr(node.slice)})")
             if node.value.id in self.coherent_arrays:
                 return f"lcd_ld(&{element})"
             return element
@@ -443,6 +450,12 @@ class _Emitter:
 
     def store(self, target, value_text):
         element = self.element(target)
+        segment = self.segment
+        if segment is not None and target.value.id == segment["array"]:
+            name = ("lcd_seg_stc" if target.value.id in self.coherent_arrays
+                    else "lcd_seg_st")
+            return (f"{name}({target.value.id}, _lcd_seg, _lcd_seg_base, "
+                    f"_lcd_seg_limit, {self.expr(target.slice)}, {value_text});")
         if target.value.id in self.coherent_arrays:
             return f"lcd_st(&{element}, {value_text});"
         return f"{element} = {value_text};"
@@ -592,12 +605,38 @@ __device__ __forceinline__ bool lcd_in_range(lcd_index_t v, lcd_index_t stop, lc
 template <class T>
 __device__ __forceinline__ lcd_index_t lcd_sorted_find(const T* idx, lcd_index_t lo,
                                                        lcd_index_t hi, lcd_index_t key) {
+    if (hi - lo <= 16 && hi > lo) {
+        // short segment: sixteen independent loads (one memory round trip)
+        // instead of a chain of dependent probes
+        lcd_index_t found = (lcd_index_t)-1;
+#pragma unroll
+        for (int t = 15; t >= 0; --t) {
+            const lcd_index_t p = lo + t < hi ? lo + t : hi - 1;
+            if ((lcd_index_t)idx[p] == key) found = p;
+        }
+        return found;
+    }
     lcd_index_t left = lo, right = hi;
     while (left < right) {
         lcd_index_t middle = (left + right) >> 1;
         if ((lcd_index_t)idx[middle] < key) left = middle + 1; else right = middle;
     }
     return (left < hi && (lcd_index_t)idx[left] == key) ? left : (lcd_index_t)-1;
+}
+// A task's own segment of an array it updates in place, staged in LDS: an
+// access inside [base, base + limit) goes to the staged copy, any other
+// position to memory (limit == 0 switches the staging off).
+template <class T>
+__device__ __forceinline__ T lcd_seg_ld(const T* x, const T* seg, lcd_index_t base,
+                                        lcd_index_t limit, lcd_index_t p) {
+    const unsigned off = (unsigned)(p - base);
+    return off < (unsigned)limit ? seg[off] : x[p];
+}
+template <class T, class V>
+__device__ __forceinline__ void lcd_seg_st(T* x, T* seg, lcd_index_t base,
+                                           lcd_index_t limit, lcd_index_t p, V v) {
+    const unsigned off = (unsigned)(p - base);
+    if (off < (unsigned)limit) seg[off] = (T)v; else x[p] = (T)v;
 }
 // Device-scope relaxed atomics (fp64 add is a hardware L2 atomic on CDNA3/4).
 template <class T, class V> __device__ __forceinline__ void lcd_atomic_add(T* p, V v) {
@@ -627,6 +666,18 @@ template <class T> __device__ __forceinline__ T lcd_ld(const T* p) {
 }
 template <class T, class V> __device__ __forceinline__ void lcd_st(T* p, V v) {
     __hip_atomic_store(p, (T)v, __ATOMIC_RELAXED, LCD_AGENT);
+}
+template <class T>
+__device__ __forceinline__ T lcd_seg_ldc(const T* x, const T* seg, lcd_index_t base,
+                                         lcd_index_t limit, lcd_index_t p) {
+    const unsigned off = (unsigned)(p - base);
+    return off < (unsigned)limit ? seg[off] : lcd_ld(&x[p]);
+}
+template <class T, class V>
+__device__ __forceinline__ void lcd_seg_stc(T* x, T* seg, lcd_index_t base,
+                                            lcd_index_t limit, lcd_index_t p, V v) {
+    const unsigned off = (unsigned)(p - base);
+    if (off < (unsigned)limit) seg[off] = (T)v; else lcd_st(&x[p], v);
 }
 // Mailbox protocol: a slot holds this quiet-NaN bit pattern until its message
 // (a finite product) has been stored; both 32-bit halves are equal so a
@@ -830,7 +881,9 @@ class HIPLowerer:
                  spin_limit=DEFAULT_SPIN_LIMIT, resident_waves_per_cu=None,
                  spin_sleep=1, promote_own_elements=True,
                  prefetch_node_loads=True, value_flags=True,
-                 gather_messages=False):
+                 gather_messages=False, segment_cache=True):
+        self.segment_cache = segment_cache
+        self._segment = None
         self.gather_messages = gather_messages
         self.value_flags = value_flags
         self._value_pull = None
@@ -1236,8 +1289,11 @@ class HIPLowerer:
         if self._mailbox is not None and self._mailbox["gather"] is None:
             # only a task itself touches its element of the reduced array
             coherent.discard(self._mailbox["array"])
+        if self.segment_cache and not self.block_task:
+            self._segment = self._segment_plan(body, arguments)
         emitter = _Emitter(kinds, self.reductions, lowered_ids,
                            coherent_arrays=coherent)
+        emitter.segment = self._segment
         emitter.mailbox = self._mailbox
         emitter.lowerer = self
         self._emitter = emitter
@@ -1540,6 +1596,194 @@ class HIPLowerer:
         loop.body = [Privatizer().visit(s) for s in loop.body]
         ast.fix_missing_locations(loop)
         return safe
+
+    def _segment_plan(self, body, arguments):
+        """In-place updates of the task's own segment ``X[P[i] .. P[i+1])``
+        (ILU0 rewrites row ``i`` once per pivot) are staged in LDS: the
+        segment is read once, updated there, and written back at the end of
+        the task, instead of a store -> load round trip through memory per
+        update.  Applies when ``X`` is written at positions walked by loops
+        over ``range(P[i] + a, P[i + 1] - b)`` and is no reduction target;
+        accesses are dispatched at run time (inside the staged range or not),
+        so reads of other tasks' segments keep going to memory."""
+        kinds = self._kinds
+        written = self._all_written
+        reduced = set()
+        for statement in body:
+            for node in ast.walk(statement):
+                if (isinstance(node, ast.AugAssign)
+                        and (node.lineno, node.col_offset) in self.reductions
+                        and isinstance(node.target, ast.Subscript)
+                        and isinstance(node.target.value, ast.Name)):
+                    reduced.add(node.target.value.id)
+        aliases = {}
+        for statement in body:
+            if (isinstance(statement, ast.Assign) and len(statement.targets) == 1
+                    and isinstance(statement.targets[0], ast.Name)):
+                name = statement.targets[0].id
+                aliases[name] = None if name in aliases else statement.value
+        it = self.loop_iterator
+
+        def pointer_of(node, offset):
+            """``P`` if the node is ``P[i + offset]`` (+/- a constant that
+            keeps it inside the segment), through one alias."""
+            if isinstance(node, ast.Name) and aliases.get(node.id) is not None:
+                node = aliases[node.id]
+            if isinstance(node, ast.BinOp) and isinstance(
+                    node.right, ast.Constant) and isinstance(
+                        node.right.value, int):
+                inward = ast.Add if offset == 0 else ast.Sub
+                if isinstance(node.op, inward) and node.right.value >= 0:
+                    return pointer_of(node.left, offset)
+                return None
+            if not (isinstance(node, ast.Subscript)
+                    and isinstance(node.value, ast.Name)
+                    and node.value.id not in written
+                    and kinds.arrays.get(node.value.id) == INT):
+                return None
+            want = it if offset == 0 else f"{it} + 1"
+            return node.value.id if ast.unparse(node.slice) == want else None
+
+        owned = {}      # loop variable -> pointer array
+
+        def scan(statements, inherited):
+            for statement in statements:
+                for node in ([statement] if isinstance(statement, ast.For)
+                             else []):
+                    pointer = None
+                    if _is_range_loop(node) and len(node.iter.args) == 2:
+                        low, high = node.iter.args
+                        upper = pointer_of(high, 1)
+                        lower = pointer_of(low, 0)
+                        if upper is not None and lower == upper:
+                            pointer = upper
+                        elif (upper is not None and inherited == upper
+                              and isinstance(low, (ast.Name, ast.BinOp))
+                              and _names_in(low) & set(owned)):
+                            # range(own position + c, P[i + 1]): still inside
+                            pointer = upper
+                    if pointer is not None and isinstance(node.target, ast.Name):
+                        owned[node.target.id] = pointer
+                    scan(node.body, pointer or inherited)
+                for field in ("body", "orelse"):
+                    if isinstance(statement, (ast.If, ast.While)):
+                        scan(getattr(statement, field, []), inherited)
+
+        scan(body, None)
+        candidates = {}
+        for statement in body:
+            for node in ast.walk(statement):
+                targets = []
+                if isinstance(node, ast.Assign):
+                    targets = node.targets
+                elif isinstance(node, ast.AugAssign):
+                    targets = [node.target]
+                for target in targets:
+                    if (isinstance(target, ast.Subscript)
+                            and isinstance(target.value, ast.Name)
+                            and isinstance(target.slice, ast.Name)
+                            and target.slice.id in owned
+                            and target.value.id not in reduced
+                            and kinds.arrays.get(target.value.id) == FLOAT):
+                        candidates.setdefault(
+                            target.value.id, set()).add(owned[target.slice.id])
+        if len(candidates) != 1:
+            return None
+        (array, pointers), = candidates.items()
+        if len(pointers) != 1:
+            return None
+        groups = max(1, self.threads_per_block // self.task_lanes)
+        capacity = min(32, 4096 // groups)
+        if capacity < 8:
+            return None
+        return {"array": array, "pointer": next(iter(pointers)),
+                "capacity": capacity}
+
+    def _segment_lines(self):
+        """(prologue, epilogue) of a task that stages its own segment."""
+        plan = self._segment
+        array, pointer = plan["array"], plan["pointer"]
+        it = self.loop_iterator
+        coherent = array in self._emitter.coherent_arrays
+        load = (f"lcd_ld(&{array}[_lcd_seg_base + _q])" if coherent
+                else f"{array}[_lcd_seg_base + _q]")
+        store = (f"lcd_st(&{array}[_lcd_seg_base + _q], _lcd_seg[_q]);"
+                 if coherent else f"{array}[_lcd_seg_base + _q] = _lcd_seg[_q];")
+        prologue = [
+            f"_lcd_seg_base = {pointer}[{it}];",
+            f"_lcd_seg_limit = {pointer}[{it} + 1] - _lcd_seg_base;",
+            "if (_lcd_seg_limit > LCD_SEG_CAP) _lcd_seg_limit = 0;",
+            "for (int _q = _lane; _q < _lcd_seg_limit; _q += LCD_TASK_LANES) "
+            f"_lcd_seg[_q] = {load};",
+            self.group_sync,
+        ]
+        epilogue = [
+            self.group_sync,
+            "for (int _q = _lane; _q < _lcd_seg_limit; _q += LCD_TASK_LANES) "
+            + store,
+        ]
+        return prologue, epilogue
+
+    def _forward_stores(self, statements, mapped_loop):
+        """``X[e] = value`` directly followed by ``name = X[e]``: every lane
+        keeps ``value`` in a register instead of reading the element back
+        through memory (a store -> fence -> load round trip on the task's
+        critical path; ILU0's ``A_data[k_ptr] /= diag; l_ik = A_data[k_ptr]``).
+        """
+        lowerer = self
+        counter = [0]
+
+        def rewrite(block):
+            out = []
+            index = 0
+            while index < len(block):
+                first = block[index]
+                second = block[index + 1] if index + 1 < len(block) else None
+                if (isinstance(first, ast.Assign) and len(first.targets) == 1
+                        and isinstance(first.targets[0], ast.Subscript)
+                        and isinstance(first.targets[0].value, ast.Name)
+                        and isinstance(second, ast.Assign)
+                        and len(second.targets) == 1
+                        and isinstance(second.targets[0], ast.Name)
+                        and isinstance(second.value, ast.Subscript)
+                        and ast.unparse(second.value)
+                        == ast.unparse(first.targets[0])
+                        and second.targets[0].id
+                        not in _names_in(first.targets[0].slice)):
+                    name = f"_lcd_fw_{counter[0]}"
+                    counter[0] += 1
+                    array = first.targets[0].value.id
+                    lowerer._kinds.locals[name] = lowerer._kinds.arrays.get(
+                        array, FLOAT)
+                    lowerer._own_registers.append(name)
+                    keep = ast.Assign(
+                        targets=[ast.Name(id=name, ctx=ast.Store())],
+                        value=first.value)
+                    store = ast.Assign(
+                        targets=first.targets,
+                        value=ast.Name(id=name, ctx=ast.Load()))
+                    reuse = ast.Assign(
+                        targets=second.targets,
+                        value=ast.Name(id=name, ctx=ast.Load()))
+                    for new, old in ((keep, first), (store, first),
+                                     (reuse, second)):
+                        ast.copy_location(new, old)
+                    out += [keep, store, reuse]
+                    index += 2
+                    continue
+                if first is not mapped_loop:
+                    for field in ("body", "orelse"):
+                        inner = getattr(first, field, None)
+                        if isinstance(inner, list) and inner and isinstance(
+                                inner[0], ast.stmt):
+                            setattr(first, field, rewrite(inner))
+                out.append(first)
+                index += 1
+            return out
+
+        result = rewrite(list(statements))
+        ast.fix_missing_locations(ast.Module(body=result, type_ignores=[]))
+        return result
 
     def _guard_stores(self, statements, mapped_loop):
         """Outside the mapped loop, array stores are issued by lane 0 of the
@@ -1902,10 +2146,18 @@ class HIPLowerer:
             # with the other node loads, before the wait
             self._prefetch_lines = list(self._prefetch_lines) + list(prologue)
             prologue = []
+        if not self.block_task:
+            # (a workgroup-wide task has no lock step between the wavefronts
+            # that would read the old value and the one that stores the new)
+            body = self._forward_stores(body, mapped)
         if mapped is not None and self.task_lanes > 1:
             body = self._guard_stores(body, mapped)
         self._partials = hooks.partials if hooks else []
         lines = list(prologue)
+        if self._segment is not None:
+            stage, write_back = self._segment_lines()
+            lines += stage
+            epilogue = list(write_back) + list(epilogue)
         for statement in body:
             lines.extend(self._emit_guarded(statement, emitter, 0, hooks))
         lines.extend(epilogue)
@@ -1969,6 +2221,8 @@ class HIPLowerer:
             "#ifndef LCD_SPIN_SLEEP",
             f"#define LCD_SPIN_SLEEP {self.spin_sleep}", "#endif",
         ]
+        if self._segment is not None:
+            defines.append(f"#define LCD_SEG_CAP {self._segment['capacity']}")
         for name, kind in array_arguments.items():
             default = "int" if kind == INT else "double"
             defines += [f"#ifndef LCD_T_{name}",
@@ -2054,6 +2308,15 @@ class HIPLowerer:
             lines.append("    __shared__ int _lcd_task_slot;")
         lines.append("    const int _lane = threadIdx.x % LCD_TASK_LANES;")
         lines.append("    (void)_lane;")
+        if self._segment is not None:
+            array = self._segment["array"]
+            lines += [
+                f"    __shared__ LCD_T_{array} _lcd_seg_store["
+                "LCD_GROUPS_PER_BLOCK * LCD_SEG_CAP];",
+                f"    LCD_T_{array}* const _lcd_seg = &_lcd_seg_store["
+                "(threadIdx.x / LCD_TASK_LANES) * LCD_SEG_CAP];",
+                "    lcd_index_t _lcd_seg_base = 0, _lcd_seg_limit = 0;",
+            ]
         lines.append(f"    lcd_index_t {it} = 0;")
         lines += self._declarations(local_names, 1)
         guard = self._node_guard(target_loop)
@@ -2503,7 +2766,7 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
                  spin_limit=DEFAULT_SPIN_LIMIT, resident_waves_per_cu=None,
                  spin_sleep=1, promote_own_elements=True,
                  prefetch_node_loads=True, value_flags=True,
-                 gather_messages=False):
+                 gather_messages=False, segment_cache=True):
     """HIP counterpart of ``lower_to_numba_cuda``
     (compiler/cuda_lowering.py:2854-2884); same parameters plus
     ``task_lanes`` (lanes cooperating on one task, a power of two <= 64),
@@ -2523,5 +2786,5 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
         spin_limit=spin_limit, resident_waves_per_cu=resident_waves_per_cu,
         spin_sleep=spin_sleep, promote_own_elements=promote_own_elements,
         prefetch_node_loads=prefetch_node_loads, value_flags=value_flags,
-        gather_messages=gather_messages)
+        gather_messages=gather_messages, segment_cache=segment_cache)
     return lowerer.lower(code)

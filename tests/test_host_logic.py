@@ -534,6 +534,20 @@ def test_ilu0_nested_mapping_lookup_and_binary_search():
         assert "for (diag_ptr" not in kernel and "for (kj_ptr" not in kernel
         assert "if (_lane == 0) {" in kernel
         assert result.dependence_protocol == "counter"
+        # the scaled pivot entry stays in a register: no read-back
+        assert "_lcd_fw_0 = (" in kernel and "l_ik = _lcd_fw_0;" in kernel
+        # row i is staged in LDS for the whole task: read once, updated
+        # there, written back at the end
+        accessor = "lcd_seg_stc" if mode == "sync_free" else "lcd_seg_st"
+        assert (f"{accessor}(A_data, _lcd_seg, _lcd_seg_base, _lcd_seg_limit, "
+                "k_ptr, _lcd_fw_0);") in kernel
+        assert "_lcd_seg_base = A_indptr[i];" in kernel
+        assert "__shared__ LCD_T_A_data _lcd_seg_store[" in kernel
+        assert "#define LCD_SEG_CAP 32" in result.source
+        plain = lower(module, function_props=ILU_PROPS, execution_mode=mode,
+                      thread_loop_iterator="j_ptr", task_lanes=8,
+                      structural_lookups=plan, segment_cache=False)
+        assert "_lcd_seg" not in plain.kernel_source
         hip_runtime.compile_code(result.source)
 
 
