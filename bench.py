@@ -59,10 +59,10 @@ MEASURED_TRAFFIC = {
 
 def build_solver(work, args):
     from lcd_amd.demo import spilu0, sptrsv
-    options = dict(TUNED[args.config])
+    options = {} if args.auto else dict(TUNED[args.config])
     if args.mode:
         options["execution_mode"] = args.mode
-        if args.mode != TUNED[args.config]["execution_mode"]:
+        if args.mode != TUNED[args.config]["execution_mode"] and not args.auto:
             options.pop("resident_waves_per_cu", None)
             options.pop("dependence_protocol", None)
     if args.tpb:
@@ -155,6 +155,9 @@ def main():
     parser.add_argument("--spin-sleep", dest="spin_sleep", type=int,
                         default=None)
     parser.add_argument("--cpu-seconds", type=float, default=5.0)
+    parser.add_argument("--auto", action="store_true",
+                        help="let the analytic scheduler choose the schedule "
+                             "instead of the tuned defaults")
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-check", action="store_true")
     parser.add_argument("--arch", action="store_true",

@@ -669,6 +669,18 @@ extern "C" int lcdhip_digest(const void *d_data, size_t bytes, uint64_t out[2],
 
 __global__ void lcdhip_empty_kernel() {}
 
+// What one level of a level-synchronous executor at least does: a chain of
+// three dependent loads (task -> segment bounds -> operand) and a store.
+__global__ void lcdhip_level_probe_kernel(const int32_t *__restrict__ chain,
+                                          int32_t *out, int32_t mask)
+{
+    int32_t v = static_cast<int32_t>(threadIdx.x + blockIdx.x);
+    v = chain[v & mask];
+    v = chain[v & mask];
+    v = chain[v & mask];
+    out[threadIdx.x] = v;
+}
+
 __global__ void lcdhip_release_probe_kernel(int32_t *counters, int32_t nodes,
                                             int32_t stride)
 {
@@ -861,13 +873,27 @@ extern "C" int lcdhip_measure_arch(lcdhip_arch *out)
         return LCDHIP_ERR_WATCHDOG;
     }
 
-    // per-node cost of a captured chain of dependent launches
+    // per-node cost of a captured chain of dependent launches, each doing
+    // the minimal work of one level (three dependent loads and a store)
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     const int chain = 256;
+    const int32_t probe_words = 1 << 16;
+    int32_t *d_probe = nullptr;
+    {
+        std::vector<int32_t> host_probe(probe_words + 64);
+        for (int32_t w = 0; w < probe_words; ++w)
+            host_probe[w] = static_cast<int32_t>(
+                (static_cast<int64_t>(w) * 40503 + 12345) & (probe_words - 1));
+        LCDHIP_CHECK(hipMalloc(&d_probe, host_probe.size() * 4));
+        LCDHIP_CHECK(hipMemcpy(d_probe, host_probe.data(),
+                               host_probe.size() * 4, hipMemcpyHostToDevice));
+    }
     LCDHIP_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeRelaxed));
     for (int node = 0; node < chain; ++node)
-        hipLaunchKernelGGL(lcdhip_empty_kernel, dim3(1), dim3(64), 0, stream);
+        hipLaunchKernelGGL(lcdhip_level_probe_kernel, dim3(1 + node % 7),
+                           dim3(64), 0, stream, d_probe, d_probe + probe_words,
+                           probe_words - 1);
     LCDHIP_CHECK(hipStreamEndCapture(stream, &graph));
     LCDHIP_CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
     samples.clear();
@@ -881,6 +907,7 @@ extern "C" int lcdhip_measure_arch(lcdhip_arch *out)
             samples.push_back(ms * 1.0e-3 / chain);
     }
     out->graph_node_s = median(samples);
+    (void)hipFree(d_probe);
     (void)hipGraphExecDestroy(exec);
     (void)hipGraphDestroy(graph);
     (void)hipEventDestroy(start_event);

@@ -54,6 +54,7 @@ from lcd_amd.scheduler import (
     AUTO,
     SYNC_FREE,
     AnalyticScheduler,
+    CalibratedScheduler,
     SchedulePlan,
     ScheduleSpace,
     count_inner_loop_flops,
@@ -155,7 +156,7 @@ def parallel(**kwargs):
             task_lanes=kwargs.get("task_lanes"),
         )
         band_width = kwargs.get("band_width", 1)
-        scheduler = kwargs.get("scheduler") or AnalyticScheduler(
+        scheduler = kwargs.get("scheduler") or CalibratedScheduler(
             kwargs.get("arch_constants"))
         device_layer = kwargs.get("device")
         lowered_variants = {}

@@ -2742,9 +2742,16 @@ class HIPLowerer:
             body.append(f"_hip.launch({reset_name!r}, ({reset_count} + 255) // 256 or 1, "
                         f"256, {reset_args})")
             tasks_per_block = max(1, self.threads_per_block // self.task_lanes)
+            waves_per_cu = self.resident_waves_per_cu
+            if waves_per_cu is None and not self.block_task:
+                # about 64 polling tasks per CU: more slow the producers
+                # down, fewer leave hand-off latency exposed (measured on the
+                # 128^3 grid with 4 lanes per task and on the power-law
+                # matrix with 32)
+                waves_per_cu = max(1, self.task_lanes)
             body.append(f"_blocks = min((_count + {tasks_per_block} - 1) // "
                         f"{tasks_per_block}, _hip.resident_blocks({kernel_name!r}, "
-                        f"{self.threads_per_block}, {self.resident_waves_per_cu!r}))")
+                        f"{self.threads_per_block}, {waves_per_cu!r}))")
             body.append(f"_hip.launch({kernel_name!r}, max(_blocks, 1), "
                         f"{self.threads_per_block}, {call_args})")
         for loop in reversed(self.host_loops):

@@ -21,7 +21,7 @@ import hashlib
 import itertools
 from collections import deque
 from copy import deepcopy
-from dataclasses import dataclass
+from dataclasses import dataclass, replace
 
 import numpy as np
 
@@ -61,6 +61,12 @@ class ArchConstants:
     barrier_s: float = 0.0        # one grid barrier of a resident grid
     graph_node_s: float = 0.0     # one dependent kernel node of a hipGraph
 
+
+# The mailbox protocol's level time on a busy MI355X: 3.3 x the idle-GPU
+# hand-off (0.54 us -> 1.8 us per level from 1800 rows per level on), and
+# about 4.1 G tasks/s once levels are wider than that (8 M-row grids).
+LOADED_HANDOFF_FACTOR = 3.3
+TASK_ISSUE_S = 2.4e-10
 
 # Used when no device is available to measure (MI355X data-sheet scale).
 FALLBACK_ARCH_CONSTANTS = ArchConstants(
@@ -292,7 +298,14 @@ class AnalyticScheduler:
             sync_s = 0.0
         elif execution_mode == SYNC_FREE:
             launch_s = arch.launch_latency_s
-            if dependence_protocol in (PUSH_DEPENDENCE, MAILBOX_DEPENDENCE):
+            if dependence_protocol == MAILBOX_DEPENDENCE:
+                # no atomics: a level costs one hand-off under load, or the
+                # issue time of its tasks when it is wide
+                width = features.rows / max(features.levels, 1)
+                sync_s = features.levels * max(
+                    (LOADED_HANDOFF_FACTOR - 1.0) * arch.handoff_s,
+                    width * TASK_ISSUE_S - arch.handoff_s)
+            elif dependence_protocol == PUSH_DEPENDENCE:
                 sync_s = arch.atomic_cost_s * features.rows / n_warp
             elif dependence_protocol == PULL_DEPENDENCE:
                 sync_s = arch.atomic_cost_s * average_in_degree * (
@@ -324,6 +337,45 @@ class AnalyticScheduler:
 
     def schedule(self, features, space):
         return min(self.candidates(features, space), key=_schedule_rank)
+
+
+class CalibratedScheduler(AnalyticScheduler):
+    """The analytic model with its latency terms scaled to what the
+    executors measure on MI355X (the decorator's default).
+
+    The reference's formulas price a level of the level-synchronous executor
+    at one launch and a hand-off of the persistent executor at one idle
+    release -> acquire.  Measured here: a level kernel's dependent loads make
+    a level 2.3 x the bare graph node (3.9 us on the 128^3 grid); a busy GPU
+    stretches the hand-off 3.3 x, and the protocols differ in how many
+    device-scope hops one level takes (message slots and value-flagged pulls
+    one, atomics + counters or flags about 1.6 x that, plain counters more,
+    since the task body then reads its operands through coherent loads)."""
+
+    LEVEL_KERNEL_FACTOR = 2.3
+    HANDOFFS_PER_LEVEL = {
+        MAILBOX_DEPENDENCE: LOADED_HANDOFF_FACTOR,
+        PULL_DEPENDENCE: LOADED_HANDOFF_FACTOR,
+        PUSH_DEPENDENCE: 1.6 * LOADED_HANDOFF_FACTOR,
+        COUNTER_DEPENDENCE: 2.4 * LOADED_HANDOFF_FACTOR,
+    }
+
+    def estimate(self, features, execution_mode, threads_per_block,
+                 thread_unroll, n_warp, thread_mapped,
+                 dependence_protocol=COUNTER_DEPENDENCE, task_lanes=0):
+        base = super().estimate(features, execution_mode, threads_per_block,
+                                thread_unroll, n_warp, thread_mapped,
+                                dependence_protocol, task_lanes)
+        arch = self.arch_constants
+        if execution_mode == WAVEFRONT:
+            return replace(base, launch_s=base.launch_s
+                           * self.LEVEL_KERNEL_FACTOR)
+        hops = self.HANDOFFS_PER_LEVEL.get(dependence_protocol,
+                                           LOADED_HANDOFF_FACTOR)
+        if dependence_protocol == MAILBOX_DEPENDENCE:
+            return base      # already priced under load
+        return replace(base, sync_s=base.sync_s
+                       + (hops - 1.0) * features.levels * arch.handoff_s)
 
 
 def _schedule_rank(schedule):

@@ -252,6 +252,52 @@ def test_cost_model_terms():
         engine.estimate(features, "eager", 128, 1, 1, False)
 
 
+def test_calibrated_scheduler_prefers_what_measures_faster():
+    """MI355X constants as measured: the mailbox executor beats the level
+    launches on the 128^3 grid, level launches beat the counter protocol on
+    the 1024^2 ILU0, a pull beats both on the power-law matrix."""
+    arch = S.ArchConstants(9.2e-6, 2.7e-10, 4.4e12, 2.4e9, handoff_s=6.5e-7,
+                           barrier_s=1.05e-5, graph_node_s=1.7e-6)
+    engine = S.CalibratedScheduler(arch)
+    grid = S.WorkloadFeatures(rows=2097152, edges=6242304, levels=382,
+                              nonzeros=8339456, flops=1.46e7,
+                              memory_bytes=142016516,
+                              thread_work_items=6242304,
+                              thread_loop_invocations=2097152)
+    space = S.ScheduleSpace.from_options(thread_mapped=True,
+                                         direct_protocol="push")
+    chosen = engine.schedule(grid, space)
+    assert (chosen.execution_mode, chosen.dependence_protocol) == (
+        "sync_free", "mailbox")
+    wave = engine.estimate(grid, "wavefront", 128, 1, 1, True, "counter", 4)
+    assert wave.launch_s == pytest.approx(382 * 2.3 * 1.7e-6)
+    box = engine.estimate(grid, "sync_free", 256, 1, 1, True, "mailbox", 4)
+    assert box.sync_s == pytest.approx(382 * 3.3 * 6.5e-7)
+    ilu = S.WorkloadFeatures(rows=1048576, edges=4190209, levels=3070,
+                             nonzeros=9424900, flops=4.0e7,
+                             memory_bytes=192692308,
+                             thread_work_items=8000000,
+                             thread_loop_invocations=4190209)
+    ilu_space = S.ScheduleSpace.from_options(thread_mapped=True)
+    assert engine.schedule(ilu, ilu_space).execution_mode == "wavefront"
+    power = S.WorkloadFeatures(rows=1000000, edges=15870985, levels=326,
+                               nonzeros=16870985, flops=3.3e7,
+                               memory_bytes=222451824,
+                               thread_work_items=15870985,
+                               thread_loop_invocations=1000000)
+    pull_space = S.ScheduleSpace.from_options(thread_mapped=True,
+                                              direct_protocol="pull")
+    chosen = engine.schedule(power, pull_space)
+    assert (chosen.execution_mode, chosen.dependence_protocol) == (
+        "sync_free", "pull")
+    # wide levels: priced by task issue rate, not by the hand-off
+    wide = S.WorkloadFeatures(rows=8388608, edges=25034752, levels=638,
+                              nonzeros=33423360, flops=5.8e7,
+                              memory_bytes=568000000)
+    assert engine.estimate(wide, "sync_free", 256, 1, 1, True, "mailbox",
+                           4).sync_s == pytest.approx(8388608 * 2.4e-10)
+
+
 def test_fingerprint_and_flops():
     a = np.arange(10, dtype=np.int32)
     values = {"Ap": a, "Ai": a.copy(), "Ax": np.ones(3), "n": 9}
