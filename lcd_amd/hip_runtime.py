@@ -1132,7 +1132,12 @@ def execute_hip_call(compiled_module, lowering, prepared_arguments,
     for name in _returned_names(lowering.host_epilogue):
         if name in prepared_arguments.values:
             result_values[name] = prepared_arguments.copy_to_host(name)
-    result_values.update(prepared_arguments.copy_lifted_variables_to_host())
+    # lifted arrays the epilogue may use; a returned one is already there
+    for name in prepared_arguments.lifted_variables:
+        if name not in result_values or (
+                name in prepared_arguments.values
+                and result_values[name] is prepared_arguments.values[name]):
+            result_values[name] = prepared_arguments.copy_to_host(name)
     return _evaluate_host_epilogue(lowering, result_values,
                                    function_globals or {})
 

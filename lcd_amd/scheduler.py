@@ -25,6 +25,11 @@ from dataclasses import dataclass, replace
 
 import numpy as np
 
+try:
+    import xxhash as _xxhash
+except ImportError:        # pragma: no cover - depends on the image
+    _xxhash = None
+
 from lcd_amd.dag_codegen import (
     COUNTER_DEPENDENCE,
     MAILBOX_DEPENDENCE,
@@ -633,9 +638,9 @@ class _ArithmeticCounter(ast.NodeVisitor):
 
 def inspection_fingerprint(values, content_names, device=None):
     """Cache key of one sparsity structure: content digests of the structure
-    arrays plus dtype/shape of every array.  Host arrays are hashed with
-    blake2b-128 like the reference; arrays already in HBM are digested on the
-    device (``lcdhip_digest``)."""
+    arrays plus dtype/shape of every array.  Host arrays are hashed on the
+    host (128 bits, like the reference's blake2b-128); arrays already in HBM
+    are digested on the device (``lcdhip_digest``)."""
     content = tuple((name, _value_digest(values.get(name), device))
                     for name in sorted(set(content_names)))
     shapes = []
@@ -647,6 +652,17 @@ def inspection_fingerprint(values, content_names, device=None):
             shapes.append((name, interface["typestr"],
                            tuple(interface["shape"])))
     return content, tuple(shapes)
+
+
+def _host_digest(data):
+    """128-bit content digest of a host byte buffer.  The key only has to
+    tell structures apart, so the fast non-cryptographic XXH3 is used when
+    the module is there (about 10 GB/s against blake2b's 1.5: the 42 MB of a
+    128^3 grid's structure arrays take 4 ms instead of 28 on every call);
+    blake2b-128, the reference's choice, otherwise."""
+    if _xxhash is not None:
+        return _xxhash.xxh3_128_digest(data)
+    return hashlib.blake2b(data, digest_size=16).digest()
 
 
 def _value_digest(value, device=None):
@@ -662,8 +678,7 @@ def _value_digest(value, device=None):
             return object()
         contiguous = np.ascontiguousarray(value)
         return (contiguous.dtype.str, contiguous.shape,
-                hashlib.blake2b(contiguous.reshape(-1).view(np.uint8),
-                                digest_size=16).digest())
+                _host_digest(contiguous.reshape(-1).view(np.uint8)))
     if isinstance(value, (list, tuple)):
         try:
             return _value_digest(np.asarray(value), device)
