@@ -53,7 +53,8 @@ TUNED = {
 # profiled reports null.
 MEASURED_TRAFFIC = {
     ("c2", "sync_free", "push", 4): 1_937_433_319,
-    ("c2", "sync_free", "mailbox", 4): 2_212_181_052,
+    ("c2", "sync_free", "mailbox", 4): 1_977_536_922,
+    ("c3", "sync_free", "pull", 32): 1_526_372_660,
 }
 
 
