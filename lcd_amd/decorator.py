@@ -190,6 +190,8 @@ def parallel(**kwargs):
                     chain_tasks=band_width != 1,
                     resident_waves_per_cu=kwargs.get("resident_waves_per_cu"),
                     spin_sleep=kwargs.get("spin_sleep", 1),
+                    **({"spin_limit": kwargs["spin_limit"]}
+                       if "spin_limit" in kwargs else {}),
                     value_flags=kwargs.get("value_flags", True),
                     gather_messages=kwargs.get("gather_messages", False),
                     segment_cache=kwargs.get("segment_cache", True),

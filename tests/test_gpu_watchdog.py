@@ -1,0 +1,102 @@
+"""Failure handling of the persistent executor on the GPU: a wait that can
+never be satisfied ends through the kernel's own bounded spin (every
+wavefront exits normally), the host raises ExecutorWatchdogError, and the
+same plan runs correctly afterwards.
+
+The condition is forced from the host: in the task queue handed to the
+executor the entry of node 0 is overwritten with a second copy of the last
+node (a sink: nothing depends on it), so whatever node 0 would have produced
+(a counter decrement, a message, a done flag, a final value) never comes.
+All array sizes stay as they are."""
+
+import ast
+import inspect
+from dataclasses import replace
+
+import numpy as np
+import pytest
+
+from lcd_amd import dag_preprocessing as P
+from lcd_amd import hip_runtime, workloads
+from lcd_amd.dag_codegen import create_dag_plan, direct_dependence
+from lcd_amd.demo import sptrsv
+from lcd_amd.dependence import analyze_dependences
+from lcd_amd.hip_lowering import lower_to_hip
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    ("sptrsv_csc_loop", sptrsv.FUNCTION_PROPS_CSC, "counter", {}),
+    ("sptrsv_csc_loop", sptrsv.FUNCTION_PROPS_CSC, "push", {}),
+    ("sptrsv_csc_loop", sptrsv.FUNCTION_PROPS_CSC, "mailbox", {}),
+    ("sptrsv_csc_loop", sptrsv.FUNCTION_PROPS_CSC, "mailbox",
+     dict(gather_messages=True)),
+    ("sptrsv_csr_loop", sptrsv.FUNCTION_PROPS_CSR, "pull", {}),
+    ("sptrsv_csr_loop", sptrsv.FUNCTION_PROPS_CSR, "pull",
+     dict(value_flags=False)),
+]
+
+
+@pytest.mark.parametrize(
+    "name,props,protocol,extra", CASES,
+    ids=["counter", "push", "mailbox", "mailbox-gathered", "pull-values",
+         "pull-flags"])
+def test_unsatisfiable_wait_trips_the_watchdog(oracle, name, props, protocol,
+                                               extra):
+    print("watchdog", name, protocol, extra, flush=True)
+    function = getattr(sptrsv, name)
+    module = ast.parse(inspect.getsource(function))
+    analysis = analyze_dependences(module, "i", props)
+    plan = create_dag_plan(analysis.ordering_dependences, None, "i",
+                           ["Ap", "Ai", "Ax", "b", "n"])
+    lowering = lower_to_hip(
+        module, "i", reductions=analysis, function_props=props,
+        execution_mode="sync_free", thread_loop_iterator="j", task_lanes=4,
+        wavefront_threads_per_block=64, dependence_protocol=protocol,
+        direct_dependence=(None if protocol == "counter"
+                           else direct_dependence(plan, "j")),
+        spin_limit=3000, **extra)
+    assert lowering.dependence_protocol == protocol
+    compiled = hip_runtime.compile_hip_module(lowering, {"np": np})
+
+    csc = name == "sptrsv_csc_loop"
+    work = workloads.configuration("c1")
+    if csc:
+        indptr, indices, data = work.indptr, work.indices, work.data
+        expected = oracle.sptrsv_csc(indptr, indices, data, work.rhs, work.n)
+        rule = oracle.rule_sptrsv_csc(indptr, indices)
+    else:
+        import scipy.sparse as sp
+        matrix = sp.csc_matrix((work.data, work.indices, work.indptr),
+                               shape=(work.n, work.n)).tocsr()
+        matrix.sort_indices()
+        indptr = matrix.indptr.astype(np.int32)
+        indices = matrix.indices.astype(np.int32)
+        data = matrix.data
+        expected = oracle.sptrsv_csr(indptr, indices, data, work.rhs, work.n)
+        rule = oracle.rule_sptrsv_csr(indptr, indices)
+    device = hip_runtime.default_device()
+    dag = device.dag_build([rule], work.n, levels=True,
+                           incoming=protocol == "mailbox")
+    good = P.execution_data_from_device_dag(
+        dag, "sync_free", True, pushed=protocol == "push",
+        mailbox=protocol == "mailbox")
+    # node 0 (level 0) never runs; the last node of the last level runs twice
+    nodes = dag.host("wavefronts").copy()
+    assert nodes[0] == 0 and dag.host("dag_ptr")[nodes[-1] + 1] == (
+        dag.host("dag_ptr")[nodes[-1]])
+    nodes[0] = nodes[-1]
+    bad = replace(good, task_nodes=device.to_device(nodes))
+    arguments = {"Ap": indptr, "Ai": indices, "Ax": data, "b": work.rhs,
+                 "n": work.n}
+    prepared = hip_runtime.prepare_hip_arguments(lowering, arguments, bad,
+                                                 {"np": np})
+    with pytest.raises(hip_runtime.ExecutorWatchdogError):
+        hip_runtime.execute_hip_call(compiled, lowering, prepared, {"np": np})
+    # the status word is re-armed: the intact queue solves the system
+    prepared = hip_runtime.prepare_hip_arguments(lowering, arguments, good,
+                                                 {"np": np})
+    result = hip_runtime.execute_hip_call(compiled, lowering, prepared,
+                                          {"np": np})
+    scale = float(np.max(np.abs(expected)))
+    assert float(np.max(np.abs(result - expected))) / scale <= 1e-12
