@@ -78,6 +78,10 @@ def build_solver(work, args):
         options["resident_waves_per_cu"] = args.waves_per_cu
     if args.spin_sleep is not None:
         options["spin_sleep"] = args.spin_sleep
+    if args.tile_rows is not None:
+        options["tile_rows"] = args.tile_rows or None
+    if args.gather:
+        options["gather_messages"] = True
     if work.kind == "sptrsv_csc":
         return sptrsv.compile_sptrsv_csc(**options)
     if work.kind == "sptrsv_csr":
@@ -156,6 +160,10 @@ def main():
     parser.add_argument("--spin-sleep", dest="spin_sleep", type=int,
                         default=None)
     parser.add_argument("--cpu-seconds", type=float, default=5.0)
+    parser.add_argument("--tile-rows", dest="tile_rows", type=int, default=None,
+                        help="tiled persistent executor: rows per tile")
+    parser.add_argument("--gather", action="store_true",
+                        help="gathered form of the mailbox protocol")
     parser.add_argument("--auto", action="store_true",
                         help="let the analytic scheduler choose the schedule "
                              "instead of the tuned defaults")

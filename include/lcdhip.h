@@ -227,7 +227,9 @@ typedef struct {
 #define LCDHIP_DAG_TASK_NODES 11    /* n: chain members, chain after chain */
 #define LCDHIP_DAG_TASK_PTR 12      /* tasks + 1: chain offsets */
 #define LCDHIP_DAG_BAND_PTR 13      /* bands + 1: first chain of every band */
-#define LCDHIP_DAG_ARRAYS 14
+/* After lcdhip_dag_tile_order: */
+#define LCDHIP_DAG_TILE_NODES 14    /* n: nodes by (id / tile_rows, level, id) */
+#define LCDHIP_DAG_ARRAYS 15
 
 int lcdhip_dag_build(const lcdhip_dag_rule *rules, int rule_count, int64_t n,
                      uint32_t flags, lcdhip_stream stream, lcdhip_dag **out);
@@ -241,6 +243,13 @@ int lcdhip_dag_build(const lcdhip_dag_rule *rules, int rule_count, int64_t n,
 int lcdhip_dag_band_chains(lcdhip_dag *dag, int64_t band_width,
                            lcdhip_stream stream, int64_t *tasks_out,
                            int64_t *bands_out);
+/* Task order of the tiled persistent executor (no counterpart in the
+ * reference: its executors have one global queue): nodes grouped into tiles of
+ * tile_rows consecutive ids, inside a tile in (level, id) order.  With ids in
+ * topological order (info.topological_ids) a tile depends on lower tiles only.
+ * Needs LCDHIP_DAG_LEVELS and level sets that cover every node. */
+int lcdhip_dag_tile_order(lcdhip_dag *dag, int64_t tile_rows,
+                          lcdhip_stream stream);
 int lcdhip_dag_get_info(const lcdhip_dag *dag, lcdhip_dag_info *out);
 int lcdhip_dag_array(const lcdhip_dag *dag, int which, void **d_out,
                      int64_t *count_out);

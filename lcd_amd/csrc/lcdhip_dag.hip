@@ -233,6 +233,15 @@ __global__ void chain_offsets_kernel(const unsigned long long *__restrict__ keys
     atomicAdd(&band_tasks[level_of[first] / band_width], 1);
 }
 
+__global__ void tile_keys_kernel(const int32_t *__restrict__ wavefronts,
+                                 int64_t n, int32_t tile_rows,
+                                 uint32_t *__restrict__ keys)
+{
+    int64_t p = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (p < n)
+        keys[p] = static_cast<uint32_t>(wavefronts[p] / tile_rows);
+}
+
 __global__ void low_words_kernel(const unsigned long long *__restrict__ keys,
                                  int64_t count, int32_t *__restrict__ out)
 {
@@ -964,6 +973,54 @@ extern "C" int lcdhip_dag_band_chains(lcdhip_dag *dag, int64_t band_width,
         *tasks_out = tasks;
     if (bands_out)
         *bands_out = bands;
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_dag_tile_order(lcdhip_dag *dag, int64_t tile_rows,
+                                     lcdhip_stream stream_handle)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (!dag || tile_rows <= 0 || tile_rows > 0x7fffffff) {
+        set_error("The tile size must be a positive integer.");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    if (!dag->arrays[LCDHIP_DAG_WAVEFRONTS] ||
+        dag->info.scheduled != dag->info.n) {
+        set_error("tiles need level sets that cover every node");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    hipStream_t stream = resolve_stream(stream_handle);
+    const int64_t n = dag->info.n;
+    if (dag->arrays[LCDHIP_DAG_TILE_NODES]) {
+        (void)hipFree(dag->arrays[LCDHIP_DAG_TILE_NODES]);
+        dag->arrays[LCDHIP_DAG_TILE_NODES] = nullptr;
+    }
+    int status;
+    if ((status = dag_alloc(dag, LCDHIP_DAG_TILE_NODES, n))) return status;
+    if (n == 0)
+        return LCDHIP_OK;
+    Scratch scratch;
+    uint32_t *keys = nullptr, *sorted_keys = nullptr;
+    LCDHIP_CHECK(scratch.alloc(&keys, n));
+    LCDHIP_CHECK(scratch.alloc(&sorted_keys, n));
+    hipLaunchKernelGGL(tile_keys_kernel, dim3(blocks_for(n)), dim3(kBlock), 0,
+                       stream, dag->arrays[LCDHIP_DAG_WAVEFRONTS], n,
+                       static_cast<int32_t>(tile_rows), keys);
+    // stable: inside a tile the (level, id) order of the level sets stays
+    const int end_bit = bits_for(static_cast<uint64_t>((n + tile_rows - 1) / tile_rows));
+    size_t sort_bytes = 0;
+    char *sort_temp = nullptr;
+    LCDHIP_CHECK(rocprim::radix_sort_pairs(
+        nullptr, sort_bytes, keys, sorted_keys,
+        dag->arrays[LCDHIP_DAG_WAVEFRONTS], dag->arrays[LCDHIP_DAG_TILE_NODES],
+        static_cast<size_t>(n), 0, end_bit, stream));
+    LCDHIP_CHECK(scratch.alloc(&sort_temp, sort_bytes));
+    LCDHIP_CHECK(rocprim::radix_sort_pairs(
+        sort_temp, sort_bytes, keys, sorted_keys,
+        dag->arrays[LCDHIP_DAG_WAVEFRONTS], dag->arrays[LCDHIP_DAG_TILE_NODES],
+        static_cast<size_t>(n), 0, end_bit, stream));
+    LCDHIP_CHECK(hipGetLastError());
+    LCDHIP_CHECK(hipStreamSynchronize(stream));
     return LCDHIP_OK;
 }
 

@@ -252,7 +252,8 @@ def band_chains(nodes, level_ptr, dag_ptr, dag_index, band_width):
 
 
 def execution_data_from_device_dag(dag, execution_mode, warp_mapped,
-                                   pushed=False, band_width=1, mailbox=False):
+                                   pushed=False, band_width=1, mailbox=False,
+                                   tile_rows=None):
     """Executor arrays straight from the on-device inspector (no host copy
     except the level offsets the launcher iterates over)."""
     if not isinstance(band_width, int) or band_width <= 0:
@@ -276,6 +277,14 @@ def execution_data_from_device_dag(dag, execution_mode, warp_mapped,
             band_ptr=dag.host("band_ptr"), dep_count=counts,
             initial_dep_count=counts, dag_ptr=dag.array("dag_ptr"),
             dag_index=dag.array("dag_index"))
+    task_nodes = dag.array("wavefronts")
+    if tile_rows:
+        # tiled executor: tasks grouped by id // tile_rows, level order inside
+        if not dag.topological_ids:
+            raise DAGPreprocessingError(
+                "The tiled executor needs every edge to go from a lower to a "
+                "higher node id.")
+        task_nodes = dag.tile_order(int(tile_rows))
     if mailbox:
         # destination v reads message slots in_ptr[v] .. in_ptr[v+1); the
         # entry at position p writes slot out_slot[p]; slot k carries the
@@ -285,13 +294,13 @@ def execution_data_from_device_dag(dag, execution_mode, warp_mapped,
                      "_lcd_in_src": dag.array("in_src"),
                      "_lcd_out_slot": dag.array("out_slot")}
         return WarpTaskExecutionData(
-            task_nodes=dag.array("wavefronts"), task_ptr=None,
+            task_nodes=task_nodes, task_ptr=None,
             band_ptr=dag.host("wavefront_ptr"), dep_count=counts,
             initial_dep_count=counts, dag_ptr=dag.array("dag_ptr"),
             dag_index=dag.array("dag_index"), auxiliary_values=auxiliary)
     if warp_mapped or execution_mode.replace("-", "_") == "sync_free":
         return WarpTaskExecutionData(
-            task_nodes=dag.array("wavefronts"), task_ptr=None,
+            task_nodes=task_nodes, task_ptr=None,
             band_ptr=dag.host("wavefront_ptr"), dep_count=counts,
             initial_dep_count=counts, dag_ptr=dag.array("dag_ptr"),
             dag_index=dag.array("dag_index"))

@@ -195,6 +195,8 @@ def parallel(**kwargs):
                     value_flags=kwargs.get("value_flags", True),
                     gather_messages=kwargs.get("gather_messages", False),
                     segment_cache=kwargs.get("segment_cache", True),
+                    tile_rows=(kwargs.get("tile_rows")
+                               if mode == SYNC_FREE else None),
                 )
             return lowered_variants[lowering_key]
 
@@ -344,7 +346,8 @@ def parallel(**kwargs):
                 dag, schedule.execution_mode, lowering.warp_mapped,
                 pushed=lowering.dependence_protocol == PUSH_DEPENDENCE,
                 band_width=band_width,
-                mailbox=lowering.dependence_protocol == MAILBOX_DEPENDENCE)
+                mailbox=lowering.dependence_protocol == MAILBOX_DEPENDENCE,
+                tile_rows=lowering.tile_rows)
             plan = SchedulePlan(
                 schedule=schedule,
                 execution_data=attach_auxiliary_values(

@@ -138,6 +138,12 @@ class HIPLoweringResult:
     value_flag_array: str | None = None
     # lifted zero-initialised arrays the executor needs no host-side clear for
     executor_initialised: tuple = ()
+    # kernel that gathers position-indexed operands into consumer order at
+    # the start of every launch (gathered mailbox), and its argument names
+    stage_kernel_name: str | None = None
+    stage_kernel_arguments: tuple = ()
+    # tiled persistent executor: block-iterator values per tile, or None
+    tile_rows: int | None = None
 
     @property
     def module_source(self):
@@ -345,6 +351,7 @@ class _Emitter:
         self.mailbox = None
         self.lowerer = None
         self.segment = None     # own-segment staging plan (HIPLowerer)
+        self.tile = None        # tiled executor plan (HIPLowerer)
 
     # ---- expressions
     def expr(self, node):
@@ -369,6 +376,8 @@ class _Emitter:
                         else "lcd_seg_ld")
                 return (f"{name}({node.value.id}, _lcd_seg, _lcd_seg_base, "
                         f"_lcd_seg_limit, {self.expr(node.slice)})")
+            if self.tile is not None and node.value.id == self.tile["array"]:
+                return self.tile_load(self.expr(node.slice))
             if node.value.id in self.coherent_arrays:
                 return f"lcd_ld(&{element})"
             return element
@@ -448,8 +457,17 @@ class _Emitter:
             raise HIPLoweringError("Only 1-D array indexing is supported.")
         return f"{target.value.id}[{self.expr(target.slice)}]"
 
+    def tile_load(self, index_text):
+        """Read of the value-flagged array: LDS inside the running tile."""
+        array = self.tile["array"]
+        return (f"lcd_tile_ld({array}, _lcd_tile, _lcd_tile_row0, "
+                f"_lcd_tile_rows, {index_text})")
+
     def store(self, target, value_text):
         element = self.element(target)
+        if self.tile is not None and target.value.id == self.tile["array"]:
+            return (f"lcd_tile_st({target.value.id}, _lcd_tile, _lcd_tile_row0, "
+                    f"_lcd_tile_rows, {self.expr(target.slice)}, {value_text});")
         segment = self.segment
         if segment is not None and target.value.id == segment["array"]:
             name = ("lcd_seg_stc" if target.value.id in self.coherent_arrays
@@ -689,6 +707,39 @@ __device__ __forceinline__ bool lcd_is_empty(double v) {
 __device__ __forceinline__ double lcd_empty() {
     return __longlong_as_double((long long)0x7FF84C437FF84C43ull);
 }
+// Tiled executor: the elements [row0, row0 + rows) of the value-flagged array
+// live in LDS while their tile runs.  A read inside the tile polls LDS (the
+// producer is a wavefront of this workgroup), any other read the device
+// coherence point; a task's final store goes to both.
+template <class T>
+__device__ __forceinline__ T lcd_tile_ld(const T* x, const T* tile, lcd_index_t row0,
+                                         lcd_index_t rows, lcd_index_t p) {
+    const unsigned off = (unsigned)(p - row0);
+    if (off < (unsigned)rows)
+        return __hip_atomic_load(&tile[off], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_WORKGROUP);
+    return lcd_ld(&x[p]);
+}
+template <class T, class V>
+__device__ __forceinline__ void lcd_tile_st(T* x, T* tile, lcd_index_t row0,
+                                            lcd_index_t rows, lcd_index_t p, V v) {
+    const unsigned off = (unsigned)(p - row0);
+    if (off < (unsigned)rows)
+        __hip_atomic_store(&tile[off], (T)v, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_WORKGROUP);
+    lcd_st(&x[p], v);
+}
+// True when no lane of the task group raises the flag (one ballot instead of
+// a butterfly of shuffles; lanes of other groups that are masked off read 0).
+__device__ __forceinline__ bool lcd_group_none(bool flag) {
+    const unsigned long long raised = __ballot(flag);
+#if LCD_TASK_LANES >= 64
+    return raised == 0ull;
+#else
+    const int shift = (int)((threadIdx.x & 63) / LCD_TASK_LANES) * LCD_TASK_LANES;
+    return ((raised >> shift) & ((1ull << LCD_TASK_LANES) - 1ull)) == 0ull;
+#endif
+}
 // Release: every store/atomic this wavefront issued has completed at the
 // coherence point before anything after the fence is issued.
 __device__ __forceinline__ void lcd_release_fence() {
@@ -837,7 +888,10 @@ class _MappedLoopHooks:
         lines.append(VALUE_WAIT_BEGIN)
         lines.append(f"{pad}for (; {name} < {upper}; {name} += LCD_TASK_LANES) {{")
         lines += [f"{pad}    {line}" for line in low._first_iteration_reload]
-        lines.append(f"{pad}    double _lcd_vf = lcd_ld(&{array}[{emitter.expr(endpoint)}]);")
+        load = (emitter.tile_load(emitter.expr(endpoint))
+                if emitter.tile is not None and emitter.tile["array"] == array
+                else f"lcd_ld(&{array}[{emitter.expr(endpoint)}])")
+        lines.append(f"{pad}    double _lcd_vf = {load};")
         if guard is None:
             lines.append(f"{pad}    if (lcd_is_empty(_lcd_vf)) break;")
         else:
@@ -881,7 +935,11 @@ class HIPLowerer:
                  spin_limit=DEFAULT_SPIN_LIMIT, resident_waves_per_cu=None,
                  spin_sleep=1, promote_own_elements=True,
                  prefetch_node_loads=True, value_flags=True,
-                 gather_messages=False, segment_cache=True):
+                 gather_messages=False, segment_cache=True, tile_rows=None,
+                 stage_operands=True):
+        self.stage_operands = stage_operands
+        self.tile_rows = tile_rows
+        self._tile = None
         self.segment_cache = segment_cache
         self._segment = None
         self.gather_messages = gather_messages
@@ -1168,7 +1226,22 @@ class HIPLowerer:
         kinds.locals["_g_value"] = FLOAT
         kinds.locals["_g_pos"] = INT
         kinds.locals["_g_src"] = INT
-        return {"value": value, "operands": operands,
+        # operands indexed by the position only are gathered into consumer
+        # order by a staging kernel at the start of every launch, so the
+        # executor reads them contiguously (an `Ax[in_pos[s]]` gather is a
+        # second dependent, scattered load in front of every task)
+        staged = {}
+        if self.stage_operands:
+            for name, node, kind in operands:
+                names = _names_in(node.slice)
+                if "_g_pos" in names and "_g_src" not in names:
+                    staged[name] = f"_lcd_staged_{len(staged)}"
+                    kinds.arrays[staged[name]] = kind
+        needs_position = any(
+            "_g_pos" in _names_in(node.slice) for name, node, _ in operands
+            if name not in staged) or "_g_pos" in _names_in(value)
+        return {"value": value, "operands": operands, "staged": staged,
+                "needs_position": needs_position,
                 "negate": isinstance(site.op, ast.Sub)}
 
     def _mailbox_slot_load(self):
@@ -1291,9 +1364,12 @@ class HIPLowerer:
             coherent.discard(self._mailbox["array"])
         if self.segment_cache and not self.block_task:
             self._segment = self._segment_plan(body, arguments)
+        if self.tile_rows:
+            self._tile = self._tile_plan(target_loop)
         emitter = _Emitter(kinds, self.reductions, lowered_ids,
                            coherent_arrays=coherent)
         emitter.segment = self._segment
+        emitter.tile = self._tile
         emitter.mailbox = self._mailbox
         emitter.lowerer = self
         self._emitter = emitter
@@ -1349,6 +1425,13 @@ class HIPLowerer:
         if self.execution_mode == "sync_free":
             reset_name = function_name + "_hip_reset"
             reset_text = self._reset_kernel_text(reset_name)
+        stage_name, stage_arguments = None, ()
+        if (self._mailbox is not None and self._mailbox["gather"] is not None
+                and self._mailbox["gather"]["staged"]):
+            stage_name = function_name + "_hip_stage"
+            stage_text, stage_arguments = self._stage_kernel_text(stage_name)
+            reset_text += stage_text
+        self._stage = (stage_name, stage_arguments)
         source = self._module_text(
             array_arguments, scalar_arguments, reset_text, kernel_text)
         launcher_source, launcher_arguments = self._launcher_text(
@@ -1361,6 +1444,8 @@ class HIPLowerer:
             kernel_name=kernel_name,
             launcher_name=launcher_name,
             reset_kernel_name=reset_name,
+            stage_kernel_name=stage_name,
+            stage_kernel_arguments=tuple(stage_arguments),
             kernel_arguments=kernel_arguments,
             launcher_arguments=launcher_arguments,
             lifted_variables=lifted_variables,
@@ -1387,6 +1472,7 @@ class HIPLowerer:
             function_name=function_name,
             mailbox_index_array=(self._mailbox["index_array"]
                                  if self._mailbox else None),
+            tile_rows=self._tile["rows"] if self._tile else None,
             value_flag_array=(
                 self._value_pull["array"] if self._value_pull
                 else self._mailbox["array"]
@@ -1509,7 +1595,10 @@ class HIPLowerer:
                 names = list(PULL_ARGUMENTS)
             elif (self.dependence_protocol == MAILBOX_DEPENDENCE
                   and self._mailbox["gather"] is not None):
-                names = list(GATHER_ARGUMENTS)
+                gather = self._mailbox["gather"]
+                names = [name for name in GATHER_ARGUMENTS
+                         if name != "_lcd_in_pos" or gather["needs_position"]]
+                names[2:2] = list(gather["staged"].values())
             elif self.dependence_protocol == MAILBOX_DEPENDENCE:
                 names = list(MAILBOX_ARGUMENTS)
             else:
@@ -1596,6 +1685,32 @@ class HIPLowerer:
         loop.body = [Privatizer().visit(s) for s in loop.body]
         ast.fix_missing_locations(loop)
         return safe
+
+    def _tile_plan(self, target_loop):
+        """Tiled persistent executor: one workgroup runs the tasks of
+        ``tile_rows`` consecutive block-iterator values (a tile) and keeps
+        their elements of the value-flagged array in LDS, so that hand-offs
+        between tasks of a tile are LDS round trips between wavefronts of one
+        workgroup; only edges that cross tiles pay the device-scope hop.
+        Needs a protocol in which the value is the flag (value-flagged pull
+        or the gathered mailbox), node ids 0 .. n-1 in topological order (a
+        tile then depends on lower tiles only, whatever the tile size) and
+        wavefront-sized tasks; other combinations keep the flat queue
+        (``tile_rows`` of the result is then None)."""
+        rows = self.tile_rows
+        if not isinstance(rows, int) or rows <= 0 or rows * 8 > 65536:
+            raise HIPLoweringError(
+                "tile_rows must be a positive integer of at most 8192 "
+                "(64 KB of LDS).")
+        array = None
+        if self._value_pull is not None:
+            array = self._value_pull["array"]
+        elif self._mailbox is not None and self._mailbox["gather"] is not None:
+            array = self._mailbox["array"]
+        if (array is None or self.execution_mode != "sync_free"
+                or self.block_task or len(target_loop.iter.args) != 1):
+            return None      # the flat queue serves every other combination
+        return {"array": array, "rows": rows}
 
     def _segment_plan(self, body, arguments):
         """In-place updates of the task's own segment ``X[P[i] .. P[i+1])``
@@ -2223,6 +2338,8 @@ class HIPLowerer:
         ]
         if self._segment is not None:
             defines.append(f"#define LCD_SEG_CAP {self._segment['capacity']}")
+        if self._tile is not None:
+            defines.append(f"#define LCD_TILE_ROWS {self._tile['rows']}")
         for name, kind in array_arguments.items():
             default = "int" if kind == INT else "double"
             defines += [f"#ifndef LCD_T_{name}",
@@ -2308,6 +2425,12 @@ class HIPLowerer:
             lines.append("    __shared__ int _lcd_task_slot;")
         lines.append("    const int _lane = threadIdx.x % LCD_TASK_LANES;")
         lines.append("    (void)_lane;")
+        if self._tile is not None:
+            lines += [
+                f"    __shared__ LCD_T_{self._tile['array']} "
+                "_lcd_tile[LCD_TILE_ROWS];",
+                "    lcd_index_t _lcd_tile_row0 = 0, _lcd_tile_rows = 0;",
+            ]
         if self._segment is not None:
             array = self._segment["array"]
             lines += [
@@ -2432,23 +2555,50 @@ class HIPLowerer:
                 "    }",
             ]
             return lines
+        tiled = self._tile is not None
+        if tiled:
+            # one workgroup per tile of consecutive block-iterator values,
+            # its wavefronts share the tile's tasks in (level, id) order;
+            # tiles are taken in increasing order, so the lowest unfinished
+            # tile is always running and depends on finished tiles only
+            fetch = [
+                "    for (int _tile = blockIdx.x; (long long)_tile * LCD_TILE_ROWS "
+                "< _task_count; _tile += gridDim.x) {",
+                "    _lcd_tile_row0 = _tile * LCD_TILE_ROWS;",
+                "    _lcd_tile_rows = _task_count - _lcd_tile_row0 < LCD_TILE_ROWS "
+                "? _task_count - _lcd_tile_row0 : LCD_TILE_ROWS;",
+                "    for (int _s = threadIdx.x; _s < _lcd_tile_rows; _s += LCD_TPB) "
+                "_lcd_tile[_s] = lcd_empty();",
+                "    __syncthreads();",
+                "    for (int _round = 0; ; ++_round) {",
+                "        const int _local = (_round * (LCD_TPB / 64) + "
+                "(int)(threadIdx.x >> 6)) * _tasks_per_wave;",
+                "        if (_local >= _lcd_tile_rows) break;",
+                "        const int _task = _lcd_tile_row0 + _local + "
+                "(int)(threadIdx.x & 63) / LCD_TASK_LANES;",
+                "        bool _pending = _task < _lcd_tile_row0 + _lcd_tile_rows;",
+            ]
+        else:
+            fetch = [
+                "    int _round = 0; (void)_round;",
+                "    while (true) {",
+                "#ifndef LCD_DYNAMIC_FETCH",
+                "        const int _base = (_round * (int)(gridDim.x * (LCD_TPB / 64)) + "
+                "(int)(blockIdx.x * (LCD_TPB / 64) + (threadIdx.x >> 6))) * _tasks_per_wave;",
+                "        ++_round;",
+                "#else",
+                "        int _base = 0;",
+                "        if ((threadIdx.x & 63) == 0)",
+                "            _base = atomicAdd(&task_counter[0], _tasks_per_wave);",
+                "        _base = __shfl(_base, 0, 64);",
+                "#endif",
+                "        if (_base >= _task_count) return;",
+                "        const int _task = _base + (int)(threadIdx.x & 63) / LCD_TASK_LANES;",
+                "        bool _pending = _task < _task_count;",
+            ]
         lines += [
             "    const int _tasks_per_wave = 64 / LCD_TASK_LANES;",
-            "    int _round = 0; (void)_round;",
-            "    while (true) {",
-            "#ifndef LCD_DYNAMIC_FETCH",
-            "        const int _base = (_round * (int)(gridDim.x * (LCD_TPB / 64)) + "
-            "(int)(blockIdx.x * (LCD_TPB / 64) + (threadIdx.x >> 6))) * _tasks_per_wave;",
-            "        ++_round;",
-            "#else",
-            "        int _base = 0;",
-            "        if ((threadIdx.x & 63) == 0)",
-            "            _base = atomicAdd(&task_counter[0], _tasks_per_wave);",
-            "        _base = __shfl(_base, 0, 64);",
-            "#endif",
-            "        if (_base >= _task_count) return;",
-            "        const int _task = _base + (int)(threadIdx.x & 63) / LCD_TASK_LANES;",
-            "        bool _pending = _task < _task_count;",
+            *fetch,
             f"        {it} = _pending ? (lcd_index_t)task_nodes[_task] : 0;",
             f"        if (_pending && ({self._prefetch_guard})) {{",
             *[f"            {line}" for line in self._prefetch_lines],
@@ -2478,10 +2628,10 @@ class HIPLowerer:
         ]
         if value is not None:
             missing = f"({value['remaining']})"
-            total = (f"lcd_group_sum((double){missing}) != 0.0"
-                     if self.task_lanes > 1 else missing)
+            none_left = (f"lcd_group_none({missing})"
+                         if 1 < self.task_lanes <= 64 else f"!{missing}")
             lines.append("                bool _ready = true;")
-            lines += task(4, waiting + [f"_ready = !({total});"])
+            lines += task(4, waiting + [f"_ready = {none_left};"])
         elif protocol == PULL_DEPENDENCE:
             lines += self._pull_ready_lines(4)
         elif protocol == MAILBOX_DEPENDENCE and self._mailbox["gather"] is not None:
@@ -2527,8 +2677,12 @@ class HIPLowerer:
             "                }",
             "            }",
             "        }",
-            "        if (__ballot(_task_aborted)) return;",
-            "    }",
+            *(["        if (__ballot(_task_aborted)) break;",
+               "    }",
+               "    if (__syncthreads_or((int)_task_aborted)) return;",
+               "    }"] if tiled else
+              ["        if (__ballot(_task_aborted)) return;",
+               "    }"]),
         ]
         lines.insert(1, "    bool _task_aborted = false;")
         return lines
@@ -2542,23 +2696,30 @@ class HIPLowerer:
         lines = []
         if declare:
             lines.append(f"{pad}lcd_index_t _g_pos = 0, _g_src = 0;")
+            lines.append(f"{pad}double _mb_value = lcd_empty();")
             for name, _, kind in gather["operands"]:
                 ctype = "lcd_index_t" if kind == INT else "double"
                 lines.append(f"{pad}{ctype} {name} = 0;")
-        loads = " ".join(f"{name} = {emitter.expr(node)};"
-                         for name, node, _ in gather["operands"])
+        staged = gather["staged"]
+        loads = " ".join(
+            f"{name} = {staged[name]}[_mb_next + _lane];" if name in staged
+            else f"{name} = {emitter.expr(node)};"
+            for name, node, _ in gather["operands"])
         head = "if (_pending && _mb_next + _lane < _mb_end)" if declare else (
             "if (_mb_next + _lane < _mb_end)")
+        position = ("_g_pos = _lcd_in_pos[_mb_next + _lane]; "
+                    if gather["needs_position"] else "")
         lines.append(
-            f"{pad}{head} {{ _g_pos = _lcd_in_pos[_mb_next + _lane]; "
+            f"{pad}{head} {{ {position}"
             f"_g_src = _lcd_in_src[_mb_next + _lane]; {loads} }}")
         return lines
 
     def _gather_ready_lines(self, indent):
         """Readiness for the gathered mailbox: lane ``l`` polls the final
-        value of the producer of incoming edge ``next + l`` and forms the
-        product; products are added in (source, position) order by
-        broadcasting them lane by lane, as far as they are there."""
+        value of the producer of incoming edge ``next + l`` until it is there
+        and keeps the product; once the lanes of a chunk all hold theirs, the
+        products are added in (source, position) order -- the order of the
+        sequential loop -- by broadcasting them lane by lane."""
         pad = "    " * indent
         own = self._mailbox["register"]
         gather = self._mailbox["gather"]
@@ -2566,27 +2727,33 @@ class HIPLowerer:
         value = self._emitter.expr(gather["value"])
         if gather["negate"]:
             value = f"(-({value}))"
+        load = (self._emitter.tile_load("_g_src") if self._tile is not None
+                else f"lcd_ld(&{array}[_g_src])")
+        missing = "(_lane < _mb_have && lcd_is_empty(_mb_value))"
+        complete = (f"lcd_group_none({missing})" if self.task_lanes > 1
+                    else f"!{missing}")
+        unroll = ([f"{pad}#pragma unroll"] if self.task_lanes <= 8 else [])
+        bound = "LCD_TASK_LANES" if self.task_lanes <= 8 else "_mb_have"
         return [
             f"{pad}bool _ready = _mb_next == _mb_end;",
             f"{pad}if (!_ready) {{",
             f"{pad}    const int _mb_have = (_mb_end - _mb_next) < LCD_TASK_LANES ? "
             "(_mb_end - _mb_next) : LCD_TASK_LANES;",
-            f"{pad}    double _mb_value = lcd_empty();",
-            f"{pad}    if (_lane < _mb_have) {{",
-            f"{pad}        const double _g_value = lcd_ld(&{array}[_g_src]);",
+            f"{pad}    if (_lane < _mb_have && lcd_is_empty(_mb_value)) {{",
+            f"{pad}        const double _g_value = {load};",
             f"{pad}        if (!lcd_is_empty(_g_value)) _mb_value = {value};",
             f"{pad}    }}",
-            f"{pad}    int _mb_k = 0;",
-            f"{pad}    for (; _mb_k < _mb_have; ++_mb_k) {{",
-            f"{pad}        const double _mb_in = __shfl(_mb_value, _mb_k, LCD_TASK_LANES);",
-            f"{pad}        if (lcd_is_empty(_mb_in)) break;",
-            f"{pad}        {own} = {own} + _mb_in;",
-            f"{pad}    }}",
-            f"{pad}    if (_mb_k > 0) {{",
-            f"{pad}        _mb_next += _mb_k;",
+            f"{pad}    if ({complete}) {{",
+            *unroll,
+            f"{pad}        for (int _mb_k = 0; _mb_k < {bound}; ++_mb_k) {{",
+            f"{pad}            const double _mb_in = __shfl(_mb_value, _mb_k, LCD_TASK_LANES);",
+            f"{pad}            if (_mb_k < _mb_have) {own} = {own} + _mb_in;",
+            f"{pad}        }}",
+            f"{pad}        _mb_next += _mb_have;",
+            f"{pad}        _mb_value = lcd_empty();",
             *self._gather_fetch_lines(indent + 2),
+            f"{pad}        _ready = _mb_next == _mb_end;",
             f"{pad}    }}",
-            f"{pad}    _ready = _mb_next == _mb_end;",
             f"{pad}}}",
         ]
 
@@ -2640,6 +2807,42 @@ class HIPLowerer:
             "{ _missing = 1; break; }",
             f"{pad}bool _ready = !({total});",
         ]
+
+    def _stage_kernel_text(self, stage_name):
+        """``_lcd_staged_k[s] = R[f(in_pos[s])]`` for every message ``s``."""
+        gather = self._mailbox["gather"]
+        emitter = self._emitter
+        sources = []
+        body = []
+        for name, node, _ in gather["operands"]:
+            if name not in gather["staged"]:
+                continue
+            for sub in ast.walk(node):
+                if (isinstance(sub, ast.Name) and sub.id in self._kinds.arrays
+                        and sub.id not in sources):
+                    sources.append(sub.id)
+            body.append(f"        {gather['staged'][name]}[t] = "
+                        f"{emitter.expr(node)};")
+        staged = list(gather["staged"].values())
+        scalars = sorted({
+            sub.id for name, node, _ in gather["operands"]
+            if name in gather["staged"] for sub in ast.walk(node)
+            if isinstance(sub, ast.Name) and sub.id in self._kinds.scalars
+            and sub.id not in ("_g_pos",)})
+        parameters = (
+            [f"const LCD_T_{name}* __restrict__ {name}" for name in sources]
+            + [f"LCD_T_{name} {name}" for name in scalars]
+            + ["const int* __restrict__ _lcd_in_pos"]
+            + [f"LCD_T_{name}* {name}" for name in staged]
+            + ["long long count"])
+        text = (f'\nextern "C" __global__ void {stage_name}('
+                + ", ".join(parameters) + ")\n{\n"
+                "    const long long t = (long long)blockIdx.x * blockDim.x + "
+                "threadIdx.x;\n"
+                "    if (t < count) {\n"
+                "        const lcd_index_t _g_pos = _lcd_in_pos[t];\n"
+                + "\n".join(body) + "\n    }\n}\n")
+        return text, sources + scalars + ["_lcd_in_pos"] + staged
 
     def _reset_kernel_text(self, reset_name):
         """Restores the mutable executor state before every sweep (the
@@ -2741,6 +2944,15 @@ class HIPLowerer:
             body.append(f"_count = _hip.length({count_array})")
             body.append(f"_hip.launch({reset_name!r}, ({reset_count} + 255) // 256 or 1, "
                         f"256, {reset_args})")
+            stage_name, stage_arguments = self._stage
+            if stage_name is not None:
+                for name in stage_arguments:
+                    if name not in launcher_arguments:
+                        launcher_arguments.append(name)
+                stage_args = ", ".join(stage_arguments)
+                body.append(
+                    f"_hip.launch({stage_name!r}, (_hip.length(_lcd_in_pos) + 255) "
+                    f"// 256 or 1, 256, ({stage_args}, _hip.length(_lcd_in_pos)))")
             tasks_per_block = max(1, self.threads_per_block // self.task_lanes)
             waves_per_cu = self.resident_waves_per_cu
             if waves_per_cu is None and not self.block_task:
@@ -2749,6 +2961,11 @@ class HIPLowerer:
                 # 128^3 grid with 4 lanes per task and on the power-law
                 # matrix with 32)
                 waves_per_cu = max(1, self.task_lanes)
+            if self._tile is not None:
+                # one workgroup per tile; residency is bounded by the LDS the
+                # tile takes, not by a polling budget
+                tasks_per_block = self._tile["rows"]
+                waves_per_cu = self.resident_waves_per_cu
             body.append(f"_blocks = min((_count + {tasks_per_block} - 1) // "
                         f"{tasks_per_block}, _hip.resident_blocks({kernel_name!r}, "
                         f"{self.threads_per_block}, {waves_per_cu!r}))")
@@ -2773,7 +2990,8 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
                  spin_limit=DEFAULT_SPIN_LIMIT, resident_waves_per_cu=None,
                  spin_sleep=1, promote_own_elements=True,
                  prefetch_node_loads=True, value_flags=True,
-                 gather_messages=False, segment_cache=True):
+                 gather_messages=False, segment_cache=True, tile_rows=None,
+                 stage_operands=True):
     """HIP counterpart of ``lower_to_numba_cuda``
     (compiler/cuda_lowering.py:2854-2884); same parameters plus
     ``task_lanes`` (lanes cooperating on one task, a power of two <= 64),
@@ -2793,5 +3011,6 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
         spin_limit=spin_limit, resident_waves_per_cu=resident_waves_per_cu,
         spin_sleep=spin_sleep, promote_own_elements=promote_own_elements,
         prefetch_node_loads=prefetch_node_loads, value_flags=value_flags,
-        gather_messages=gather_messages, segment_cache=segment_cache)
+        gather_messages=gather_messages, segment_cache=segment_cache,
+        tile_rows=tile_rows, stage_operands=stage_operands)
     return lowerer.lower(code)

@@ -36,7 +36,7 @@ STATUS_ARGUMENT = "_lcd_status"
 DAG_PTR, DAG_INDEX, DAG_DEP_COUNT, DAG_EDGE_COUNT = 0, 1, 2, 3
 DAG_LEVEL_OF, DAG_WAVEFRONTS, DAG_WAVEFRONT_PTR = 4, 5, 6
 DAG_IN_PTR, DAG_IN_POS, DAG_OUT_SLOT, DAG_IN_SRC = 7, 8, 9, 10
-DAG_TASK_NODES, DAG_TASK_PTR, DAG_BAND_PTR = 11, 12, 13
+DAG_TASK_NODES, DAG_TASK_PTR, DAG_BAND_PTR, DAG_TILE_NODES = 11, 12, 13, 14
 DAG_FLAG_LEVELS, DAG_FLAG_FORCE_KAHN, DAG_FLAG_INCOMING = 1, 2, 4
 
 DEVICE_COMPILE_OPTIONS = (
@@ -123,7 +123,7 @@ EXPORTED_SYMBOLS = (
     "lcdhip_graph_end_capture", "lcdhip_graph_launch", "lcdhip_graph_destroy",
     "lcdhip_dag_build", "lcdhip_dag_get_info", "lcdhip_dag_array",
     "lcdhip_dag_download", "lcdhip_dag_destroy", "lcdhip_dag_band_chains",
-    "lcdhip_lookup_build",
+    "lcdhip_dag_tile_order", "lcdhip_lookup_build",
     "lcdhip_digest",
 )
 
@@ -312,7 +312,8 @@ class DeviceDag:
               "wavefront_ptr": DAG_WAVEFRONT_PTR, "in_ptr": DAG_IN_PTR,
               "in_pos": DAG_IN_POS, "out_slot": DAG_OUT_SLOT,
               "in_src": DAG_IN_SRC, "task_nodes": DAG_TASK_NODES,
-              "task_ptr": DAG_TASK_PTR, "band_ptr": DAG_BAND_PTR}
+              "task_ptr": DAG_TASK_PTR, "band_ptr": DAG_BAND_PTR,
+              "tile_nodes": DAG_TILE_NODES}
     CHAIN_ARRAYS = ("task_nodes", "task_ptr", "band_ptr")
 
     def __init__(self, device, handle):
@@ -366,6 +367,19 @@ class DeviceDag:
             ctypes.byref(tasks), ctypes.byref(bands)))
         self.chain_band_width = band_width
         return int(tasks.value), int(bands.value)
+
+    def tile_order(self, tile_rows):
+        """Order the nodes by (id // tile_rows, level, id) on the device;
+        afterwards ``tile_nodes`` is an array of this DAG."""
+        if not isinstance(tile_rows, int) or tile_rows <= 0:
+            raise HIPRuntimeError("The tile size must be a positive integer.",
+                                  ERR_ARGUMENT)
+        self._views.pop("tile_nodes", None)
+        self._host.pop("tile_nodes", None)
+        _check(load_library().lcdhip_dag_tile_order(
+            self.handle, ctypes.c_int64(tile_rows), self.device.stream))
+        self.tile_rows = tile_rows
+        return self.array("tile_nodes")
 
     def successors(self):
         ptr, index = self.host("dag_ptr"), self.host("dag_index")
@@ -930,6 +944,19 @@ def prepare_hip_arguments(lowering, argument_values, execution_data,
                 cached = device.empty((slots,), np.float64)
                 workspace[("state", "_lcd_mailbox")] = cached
             host_values["_lcd_mailbox"] = cached
+        for name in lowering.launcher_arguments:
+            if not name.startswith("_lcd_staged_"):
+                continue
+            # position-indexed operands gathered into consumer order
+            dtype = (np.int32 if lowering.array_arguments.get(name) == "int"
+                     else np.float64)
+            slots = max(len(host_values["_lcd_in_pos"]), 1)
+            cached = workspace.get(("state", name))
+            if cached is None or len(cached) != slots or (
+                    cached.dtype != dtype):
+                cached = device.empty((slots,), dtype)
+                workspace[("state", name)] = cached
+            host_values[name] = cached
         for name in ("task_counter", STATUS_ARGUMENT):
             cached = workspace.get(("state", name))
             if cached is None:
@@ -1056,6 +1083,17 @@ def _load_for_values(compiled, lowering, prepared, device):
                 reset = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                          ctypes.c_int64]
             argument_ctypes[lowering.reset_kernel_name] = reset
+        if getattr(lowering, "stage_kernel_name", None):
+            stage = []
+            for name in lowering.stage_kernel_arguments:
+                if name in scalar_types:
+                    text = scalar_types[name]
+                    stage.append(ctypes.c_void_p if text == "const void*"
+                                 else _CTYPES[text])
+                else:
+                    stage.append(ctypes.c_void_p)
+            argument_ctypes[lowering.stage_kernel_name] = stage + [
+                ctypes.c_int64]
         compiled.loaded[cache_key] = device.load_module(code, argument_ctypes)
     return compiled.loaded[cache_key]
 

@@ -93,6 +93,41 @@ def test_sptrsv_csc_variants(oracle, options):
         assert "_lcd_mailbox" not in solver.hip_kernel_source
 
 
+@pytest.mark.parametrize("tile_rows,lanes,tpb", [(64, 4, 64), (500, 8, 128),
+                                                 (4096, 4, 256), (8192, 16, 512)])
+def test_tiled_executor(oracle, tile_rows, lanes, tpb):
+    """Workgroup-resident tiles: hand-offs inside a tile go through LDS,
+    across tiles through memory; CSR pull and the gathered CSC mailbox."""
+    print("tiles", tile_rows, lanes, tpb, flush=True)
+    csr = sptrsv.compile_sptrsv_csr(
+        execution_mode="sync_free", threads_per_block=tpb, task_lanes=lanes,
+        thread_unroll=1, dependence_protocol="pull", tile_rows=tile_rows)
+    csc = sptrsv.compile_sptrsv_csc(
+        execution_mode="sync_free", threads_per_block=tpb, task_lanes=lanes,
+        thread_unroll=1, dependence_protocol="mailbox", gather_messages=True,
+        tile_rows=tile_rows)
+    assert csr.hip_lowering.tile_rows == tile_rows
+    assert csc.hip_lowering.tile_rows == tile_rows
+    assert "lcd_tile_ld(x, _lcd_tile" in csr.hip_kernel_source
+    assert "lcd_tile_st(x, _lcd_tile" in csc.hip_kernel_source
+    for name, overrides in (("c1", {}), ("c2", dict(nx=20, ny=18, nz=16)),
+                            ("c5", dict(n=6000))):
+        work = workloads.configuration(name, **overrides)
+        expected = oracle.sptrsv_csc(work.indptr, work.indices, work.data,
+                                     work.rhs, work.n)
+        # the gathered mailbox adds in the order of the sequential loop
+        solve_and_check(csc, work, expected, exact=True)
+    work = workloads.configuration("c3", n=20000)
+    expected = oracle.sptrsv_csr(work.indptr, work.indices, work.data,
+                                 work.rhs, work.n)
+    solve_and_check(csr, work, expected)
+    # a loop the tiles do not apply to keeps the flat queue
+    pushed = sptrsv.compile_sptrsv_csc(
+        execution_mode="sync_free", threads_per_block=128, task_lanes=4,
+        thread_unroll=1, dependence_protocol="push", tile_rows=tile_rows)
+    assert pushed.hip_lowering.tile_rows is None
+
+
 CSR_VARIANTS = [
     dict(execution_mode="wavefront", threads_per_block=128, task_lanes=8),
     dict(execution_mode="wavefront", threads_per_block=128, n_warp=1,

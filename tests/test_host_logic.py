@@ -539,11 +539,24 @@ def test_gathered_mailbox_drops_the_producer_loop():
     assert result.dependence_protocol == "mailbox"
     assert result.value_flag_array == "x"
     assert "_lcd_mailbox" not in result.kernel_arguments
-    assert {"_lcd_in_ptr", "_lcd_in_pos", "_lcd_in_src"} <= set(
+    # the coefficient is gathered into consumer order by a staging kernel
+    assert {"_lcd_in_ptr", "_lcd_in_src", "_lcd_staged_0"} <= set(
         result.kernel_arguments)
-    assert "_g_operand_0 = Ax[_g_pos];" in kernel
+    assert "_lcd_in_pos" not in result.kernel_arguments
+    assert result.stage_kernel_name == "sptrsv_csc_loop_hip_stage"
+    assert result.stage_kernel_arguments == ("Ax", "_lcd_in_pos",
+                                             "_lcd_staged_0")
+    assert "_lcd_staged_0[t] = Ax[_g_pos];" in result.source
+    assert "_g_operand_0 = _lcd_staged_0[_mb_next + _lane];" in kernel
     assert "const double _g_value = lcd_ld(&x[_g_src]);" in kernel
     assert "_mb_value = (_g_operand_0 * _g_value);" in kernel
+    unstaged = lower(module, execution_mode="sync_free",
+                     thread_loop_iterator="j", task_lanes=4,
+                     dependence_protocol="mailbox", gather_messages=True,
+                     stage_operands=False)
+    assert unstaged.stage_kernel_name is None
+    assert "_g_operand_0 = Ax[_g_pos];" in unstaged.kernel_source
+    assert "_lcd_in_pos" in unstaged.kernel_arguments
     assert "lcd_atomic_add" not in kernel.split("while (true)")[1]
     assert "if (_lane == 0) lcd_st(&x[i], _lcd_own_0);" in kernel
     hip_runtime.compile_code(result.source)
