@@ -30,20 +30,20 @@ METRIC = "SpTRSV/SpILU0 solve ms, GFLOP/s, HBM GB/s (% roofline) on 1 MI355X"
 # Executor settings per configuration (the fastest measured on MI355X; every
 # one can be overridden on the command line).
 TUNED = {
-    "c1": dict(execution_mode="sync_free", threads_per_block=64, task_lanes=4,
-               thread_unroll=1, resident_waves_per_cu=1,
-               dependence_protocol="mailbox"),
+    "c1": dict(execution_mode="sync_free", threads_per_block=256, task_lanes=4,
+               thread_unroll=1, dependence_protocol="mailbox",
+               tile_rows=1024),
     "c2": dict(execution_mode="sync_free", threads_per_block=256, task_lanes=4,
-               thread_unroll=1, resident_waves_per_cu=4,
-               dependence_protocol="mailbox"),
+               thread_unroll=1, dependence_protocol="mailbox",
+               tile_rows=4096),
     "c3": dict(execution_mode="sync_free", threads_per_block=256,
                task_lanes=32, thread_unroll=1, resident_waves_per_cu=32,
-               dependence_protocol="pull"),
+               dependence_protocol="pull", tile_rows=None),
     "c4": dict(execution_mode="wavefront", threads_per_block=64, task_lanes=8,
                thread_unroll=1),
     "c5": dict(execution_mode="sync_free", threads_per_block=256, task_lanes=8,
-               thread_unroll=1, resident_waves_per_cu=2,
-               dependence_protocol="mailbox"),
+               thread_unroll=1, dependence_protocol="mailbox",
+               tile_rows=4096),
 }
 
 
@@ -53,7 +53,7 @@ TUNED = {
 # profiled reports null.
 MEASURED_TRAFFIC = {
     ("c2", "sync_free", "push", 4): 1_937_433_319,
-    ("c2", "sync_free", "mailbox", 4): 1_977_536_922,
+    ("c2", "sync_free", "mailbox-slots", 4): 1_977_536_922,
     ("c3", "sync_free", "pull", 32): 1_526_372_660,
 }
 
@@ -80,8 +80,10 @@ def build_solver(work, args):
         options["spin_sleep"] = args.spin_sleep
     if args.tile_rows is not None:
         options["tile_rows"] = args.tile_rows or None
-    if args.gather:
-        options["gather_messages"] = True
+    if args.slots:
+        options["gather_messages"] = False
+        options["tile_rows"] = None
+        options.setdefault("resident_waves_per_cu", options.get("task_lanes"))
     if work.kind == "sptrsv_csc":
         return sptrsv.compile_sptrsv_csc(**options)
     if work.kind == "sptrsv_csr":
@@ -162,8 +164,9 @@ def main():
     parser.add_argument("--cpu-seconds", type=float, default=5.0)
     parser.add_argument("--tile-rows", dest="tile_rows", type=int, default=None,
                         help="tiled persistent executor: rows per tile")
-    parser.add_argument("--gather", action="store_true",
-                        help="gathered form of the mailbox protocol")
+    parser.add_argument("--slots", action="store_true",
+                        help="message slots instead of the gathered form of "
+                             "the mailbox protocol (implies no tiles)")
     parser.add_argument("--auto", action="store_true",
                         help="let the analytic scheduler choose the schedule "
                              "instead of the tuned defaults")

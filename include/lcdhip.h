@@ -250,6 +250,12 @@ int lcdhip_dag_band_chains(lcdhip_dag *dag, int64_t band_width,
  * Needs LCDHIP_DAG_LEVELS and level sets that cover every node. */
 int lcdhip_dag_tile_order(lcdhip_dag *dag, int64_t tile_rows,
                           lcdhip_stream stream);
+/* Number of (unique) edges whose two endpoints lie in the same tile of
+ * tile_rows consecutive ids: the share of hand-offs a tiled executor keeps
+ * inside a workgroup.  (Decision input of this backend's scheduler; no
+ * counterpart in the reference.) */
+int lcdhip_dag_tile_locality(const lcdhip_dag *dag, int64_t tile_rows,
+                             lcdhip_stream stream, int64_t *local_edges_out);
 int lcdhip_dag_get_info(const lcdhip_dag *dag, lcdhip_dag_info *out);
 int lcdhip_dag_array(const lcdhip_dag *dag, int which, void **d_out,
                      int64_t *count_out);

@@ -233,6 +233,25 @@ __global__ void chain_offsets_kernel(const unsigned long long *__restrict__ keys
     atomicAdd(&band_tasks[level_of[first] / band_width], 1);
 }
 
+// edges whose endpoints fall into the same tile of tile_rows consecutive ids
+__global__ void tile_local_edges_kernel(const int32_t *__restrict__ dag_ptr,
+                                        const int32_t *__restrict__ dag_index,
+                                        int64_t n, int32_t tile_rows,
+                                        unsigned long long *local_edges)
+{
+    int64_t u = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    unsigned long long mine = 0;
+    if (u < n) {
+        const int32_t tile = static_cast<int32_t>(u / tile_rows);
+        for (int32_t e = dag_ptr[u]; e < dag_ptr[u + 1]; ++e)
+            mine += dag_index[e] / tile_rows == tile ? 1u : 0u;
+    }
+    for (int offset = 32; offset > 0; offset >>= 1)
+        mine += __shfl_xor(mine, offset, 64);
+    if ((threadIdx.x & 63) == 0 && mine)
+        atomicAdd(local_edges, mine);
+}
+
 __global__ void tile_keys_kernel(const int32_t *__restrict__ wavefronts,
                                  int64_t n, int32_t tile_rows,
                                  uint32_t *__restrict__ keys)
@@ -973,6 +992,36 @@ extern "C" int lcdhip_dag_band_chains(lcdhip_dag *dag, int64_t band_width,
         *tasks_out = tasks;
     if (bands_out)
         *bands_out = bands;
+    return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_dag_tile_locality(const lcdhip_dag *dag, int64_t tile_rows,
+                                        lcdhip_stream stream_handle,
+                                        int64_t *local_edges_out)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (!dag || !local_edges_out || tile_rows <= 0 || tile_rows > 0x7fffffff) {
+        set_error("bad argument to lcdhip_dag_tile_locality");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    hipStream_t stream = resolve_stream(stream_handle);
+    const int64_t n = dag->info.n;
+    *local_edges_out = 0;
+    if (n == 0 || dag->info.edges == 0)
+        return LCDHIP_OK;
+    Scratch scratch;
+    unsigned long long *d_count = nullptr, host_count = 0;
+    LCDHIP_CHECK(scratch.alloc(&d_count, 1));
+    LCDHIP_CHECK(hipMemsetAsync(d_count, 0, 8, stream));
+    hipLaunchKernelGGL(tile_local_edges_kernel, dim3(blocks_for(n)),
+                       dim3(kBlock), 0, stream, dag->arrays[LCDHIP_DAG_PTR],
+                       dag->arrays[LCDHIP_DAG_INDEX], n,
+                       static_cast<int32_t>(tile_rows), d_count);
+    LCDHIP_CHECK(hipGetLastError());
+    LCDHIP_CHECK(hipMemcpyAsync(&host_count, d_count, 8, hipMemcpyDeviceToHost,
+                                stream));
+    LCDHIP_CHECK(hipStreamSynchronize(stream));
+    *local_edges_out = static_cast<int64_t>(host_count);
     return LCDHIP_OK;
 }
 

@@ -21,6 +21,7 @@ layer), ``verbose`` (print generated sources like the reference does).
 
 import ast
 import functools
+from dataclasses import replace
 import inspect
 import textwrap
 
@@ -56,6 +57,8 @@ from lcd_amd.scheduler import (
     AnalyticScheduler,
     CalibratedScheduler,
     SchedulePlan,
+    TILE_THREADS_PER_BLOCK,
+    automatic_tile_rows,
     ScheduleSpace,
     count_inner_loop_flops,
     extract_workload_features,
@@ -166,11 +169,18 @@ def parallel(**kwargs):
         def get_device():
             return device_layer or hip_runtime.default_device()
 
-        def lower_variant(lowering_key):
-            if lowering_key not in lowered_variants:
+        tile_option = kwargs.get("tile_rows", "auto")
+        if not (tile_option in (None, "auto") or (
+                isinstance(tile_option, int) and tile_option >= 0)):
+            raise ValueError(
+                "tile_rows must be None, 'auto' or a positive integer.")
+
+        def lower_variant(lowering_key, tile_rows=None):
+            variant_key = (lowering_key, tile_rows)
+            if variant_key not in lowered_variants:
                 (mode, threads_per_block, unroll, n_warp, protocol,
                  task_lanes) = lowering_key
-                lowered_variants[lowering_key] = lower_to_hip(
+                lowered_variants[variant_key] = lower_to_hip(
                     function_ast,
                     loop_iterator=loop,
                     reductions=dependence_analysis,
@@ -193,19 +203,39 @@ def parallel(**kwargs):
                     **({"spin_limit": kwargs["spin_limit"]}
                        if "spin_limit" in kwargs else {}),
                     value_flags=kwargs.get("value_flags", True),
-                    gather_messages=kwargs.get("gather_messages", False),
+                    gather_messages=kwargs.get("gather_messages", True),
                     segment_cache=kwargs.get("segment_cache", True),
-                    tile_rows=(kwargs.get("tile_rows")
-                               if mode == SYNC_FREE else None),
+                    tile_rows=tile_rows if mode == SYNC_FREE else None,
                 )
-            return lowered_variants[lowering_key]
+            return lowered_variants[variant_key]
 
-        def compile_variant(lowering_key):
-            lowering = lower_variant(lowering_key)
-            if lowering_key not in compiled_variants:
-                compiled_variants[lowering_key] = compile_hip_module(
+        def compile_variant(lowering_key, tile_rows=None):
+            lowering = lower_variant(lowering_key, tile_rows)
+            variant_key = (lowering_key, tile_rows)
+            if variant_key not in compiled_variants:
+                compiled_variants[variant_key] = compile_hip_module(
                     lowering, function_globals=function.__globals__)
-            return lowering, compiled_variants[lowering_key]
+            return lowering, compiled_variants[variant_key]
+
+        def tiles_for(dag, schedule):
+            """(schedule, tile_rows): the tiled persistent executor when it
+            is asked for, or pays for this DAG, and the loop allows it."""
+            if (schedule.execution_mode != SYNC_FREE or band_width != 1
+                    or not tile_option):
+                return schedule, None
+            rows = (tile_option if isinstance(tile_option, int)
+                    else automatic_tile_rows(dag))
+            if not rows:
+                return schedule, None
+            if (tile_option == "auto" and thread_loop is not None
+                    and kwargs.get("threads_per_block") is None
+                    and not TILE_THREADS_PER_BLOCK % max(
+                        schedule.task_lanes, 1)):
+                schedule = replace(
+                    schedule, threads_per_block=TILE_THREADS_PER_BLOCK)
+            if lower_variant(schedule.lowering_key, rows).tile_rows is None:
+                return schedule, None
+            return schedule, rows
 
         host_lowering = lower_variant(
             ScheduleSpace.from_options(**space_options).configurations()[0])
@@ -341,7 +371,8 @@ def parallel(**kwargs):
                     thread_trip_counts=trip_counts(dag_values),
                     edges=dag.edges)
                 schedule = scheduler.schedule(features, schedule_space)
-            lowering = lower_variant(schedule.lowering_key)
+            schedule, tile_rows = tiles_for(dag, schedule)
+            lowering = lower_variant(schedule.lowering_key, tile_rows)
             execution_data = execution_data_from_device_dag(
                 dag, schedule.execution_mode, lowering.warp_mapped,
                 pushed=lowering.dependence_protocol == PUSH_DEPENDENCE,
@@ -352,7 +383,7 @@ def parallel(**kwargs):
                 schedule=schedule,
                 execution_data=attach_auxiliary_values(
                     execution_data, lookup_values),
-                features=features, dag=dag)
+                features=features, dag=dag, tile_rows=tile_rows)
             plan_state[id(plan)] = {"resident": resident, "workspace": {}}
             return plan
 
@@ -382,7 +413,8 @@ def parallel(**kwargs):
             return schedule_plan(*args, **call_kwargs).execution_data
 
         def publish_variant(schedule, lowering, compiled):
-            if wrapper.current_schedule == schedule:
+            if (wrapper.current_schedule == schedule
+                    and wrapper.__dict__.get("hip_lowering") is lowering):
                 return
             wrapper.current_schedule = schedule
             wrapper.__dict__.update(_variant_attributes(lowering, compiled))
@@ -390,7 +422,8 @@ def parallel(**kwargs):
         def resolve_call(args, call_kwargs):
             argument_values = bind_arguments(args, call_kwargs)
             plan = plan_for(argument_values)
-            lowering, compiled = compile_variant(plan.schedule.lowering_key)
+            lowering, compiled = compile_variant(plan.schedule.lowering_key,
+                                                 plan.tile_rows)
             publish_variant(plan.schedule, lowering, compiled)
             state = plan_state[id(plan)]
             values = dict(argument_values)
@@ -443,8 +476,15 @@ def parallel(**kwargs):
         wrapper.lower_variant = lower_variant
         wrapper.__dict__.update(dict.fromkeys(VARIANT_ATTRIBUTES))
         if fixed_schedule is not None:
+            # an explicit tile size is known now; the automatic choice only
+            # once a structure has been inspected
+            rows = (tile_option if isinstance(tile_option, int)
+                    and tile_option and band_width == 1 else None)
+            if rows and lower_variant(fixed_schedule.lowering_key,
+                                      rows).tile_rows is None:
+                rows = None
             publish_variant(fixed_schedule,
-                            *compile_variant(fixed_schedule.lowering_key))
+                            *compile_variant(fixed_schedule.lowering_key, rows))
         return wrapper
     return decorator
 

@@ -935,7 +935,7 @@ class HIPLowerer:
                  spin_limit=DEFAULT_SPIN_LIMIT, resident_waves_per_cu=None,
                  spin_sleep=1, promote_own_elements=True,
                  prefetch_node_loads=True, value_flags=True,
-                 gather_messages=False, segment_cache=True, tile_rows=None,
+                 gather_messages=True, segment_cache=True, tile_rows=None,
                  stage_operands=True):
         self.stage_operands = stage_operands
         self.tile_rows = tile_rows
@@ -1157,10 +1157,10 @@ class HIPLowerer:
         marker and is written once per task, so the value is the flag -- and
         adds the products in (source, position) order.  The producer's loop
         disappears; a task ends with the single store of its own element.
-        Off by default: it saves the slot memory and the message writes, but
-        the coefficient gather ``Ax[_lcd_in_pos[s]]`` is scattered, and on
-        the 128^3 7-point grid it runs at 0.81 ms against 0.77 ms with
-        slots."""
+        Position-indexed operands (``Ax[j]``) are gathered into consumer
+        order by a staging kernel at the start of every launch.  On the 128^3
+        7-point grid: 0.71 ms against 0.75 ms with message slots, and the
+        form the tiled executor needs (0.60 ms)."""
         mapped, sites = box["mapped"], box["sites"]
         array = box["array"]
         if (len(sites) != 1 or mapped.body != [sites[0]]
@@ -2331,7 +2331,10 @@ class HIPLowerer:
             f"#define LCD_TASK_LANES {self.task_lanes}",
             f"#define LCD_GROUPS_PER_BLOCK (LCD_TPB / LCD_TASK_LANES)",
             "#ifndef LCD_SPIN_LIMIT",
-            f"#define LCD_SPIN_LIMIT {self.spin_limit}", "#endif",
+            # a poll of LDS takes a tenth of a poll of memory: keep the
+            # watchdog's time scale when the default limit is in use
+            f"#define LCD_SPIN_LIMIT {self.spin_limit * (16 if self._tile is not None and self.spin_limit == DEFAULT_SPIN_LIMIT else 1)}",
+            "#endif",
             f"#define LCD_READY_COUNT {self.sync_free_ready_count}",
             "#ifndef LCD_SPIN_SLEEP",
             f"#define LCD_SPIN_SLEEP {self.spin_sleep}", "#endif",
@@ -2990,7 +2993,7 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
                  spin_limit=DEFAULT_SPIN_LIMIT, resident_waves_per_cu=None,
                  spin_sleep=1, promote_own_elements=True,
                  prefetch_node_loads=True, value_flags=True,
-                 gather_messages=False, segment_cache=True, tile_rows=None,
+                 gather_messages=True, segment_cache=True, tile_rows=None,
                  stage_operands=True):
     """HIP counterpart of ``lower_to_numba_cuda``
     (compiler/cuda_lowering.py:2854-2884); same parameters plus

@@ -123,7 +123,8 @@ EXPORTED_SYMBOLS = (
     "lcdhip_graph_end_capture", "lcdhip_graph_launch", "lcdhip_graph_destroy",
     "lcdhip_dag_build", "lcdhip_dag_get_info", "lcdhip_dag_array",
     "lcdhip_dag_download", "lcdhip_dag_destroy", "lcdhip_dag_band_chains",
-    "lcdhip_dag_tile_order", "lcdhip_lookup_build",
+    "lcdhip_dag_tile_order", "lcdhip_dag_tile_locality",
+    "lcdhip_lookup_build",
     "lcdhip_digest",
 )
 
@@ -367,6 +368,17 @@ class DeviceDag:
             ctypes.byref(tasks), ctypes.byref(bands)))
         self.chain_band_width = band_width
         return int(tasks.value), int(bands.value)
+
+    def tile_locality(self, tile_rows):
+        """Share of the edges whose endpoints share a tile of ``tile_rows``
+        consecutive ids."""
+        if self.edges == 0:
+            return 1.0
+        local = ctypes.c_int64()
+        _check(load_library().lcdhip_dag_tile_locality(
+            self.handle, ctypes.c_int64(int(tile_rows)), self.device.stream,
+            ctypes.byref(local)))
+        return local.value / self.edges
 
     def tile_order(self, tile_rows):
         """Order the nodes by (id // tile_rows, level, id) on the device;

@@ -52,10 +52,12 @@ CSC_VARIANTS = [
     dict(execution_mode="sync_free", threads_per_block=128, task_lanes=2,
          dependence_protocol="mailbox", thread_unroll=2),
     dict(execution_mode="sync_free", threads_per_block=256, task_lanes=4,
-         dependence_protocol="mailbox", gather_messages=True),
+         dependence_protocol="mailbox", gather_messages=False),
     dict(execution_mode="sync_free", threads_per_block=128, task_lanes=8,
-         dependence_protocol="mailbox", gather_messages=True,
+         dependence_protocol="mailbox", gather_messages=False,
          thread_unroll=2),
+    dict(execution_mode="sync_free", threads_per_block=128, task_lanes=4,
+         dependence_protocol="mailbox", tile_rows=None),
     dict(execution_mode="sync_free", threads_per_block=128, n_warp=1,
          dependence_protocol="mailbox"),
     dict(),   # scheduler decides
@@ -82,8 +84,8 @@ def test_sptrsv_csc_variants(oracle, options):
     if exact:
         assert solver.current_schedule.dependence_protocol == "mailbox"
         slots = "_lcd_mailbox" in solver.hip_kernel_source
-        # no message slots in the gathered form
-        assert slots == (not options.get("gather_messages", False))
+        # message slots only when the (default) gathered form is off
+        assert slots == (options.get("gather_messages") is False)
         assert ("_lcd_in_src" in solver.hip_kernel_source) != slots
     schedule = solver.current_schedule
     if "execution_mode" in options:

@@ -28,19 +28,23 @@ pytestmark = pytest.mark.gpu
 CASES = [
     ("sptrsv_csc_loop", sptrsv.FUNCTION_PROPS_CSC, "counter", {}),
     ("sptrsv_csc_loop", sptrsv.FUNCTION_PROPS_CSC, "push", {}),
+    ("sptrsv_csc_loop", sptrsv.FUNCTION_PROPS_CSC, "mailbox",
+     dict(gather_messages=False)),
     ("sptrsv_csc_loop", sptrsv.FUNCTION_PROPS_CSC, "mailbox", {}),
     ("sptrsv_csc_loop", sptrsv.FUNCTION_PROPS_CSC, "mailbox",
-     dict(gather_messages=True)),
+     dict(tile_rows=512)),
     ("sptrsv_csr_loop", sptrsv.FUNCTION_PROPS_CSR, "pull", {}),
     ("sptrsv_csr_loop", sptrsv.FUNCTION_PROPS_CSR, "pull",
      dict(value_flags=False)),
+    ("sptrsv_csr_loop", sptrsv.FUNCTION_PROPS_CSR, "pull",
+     dict(tile_rows=512)),
 ]
 
 
 @pytest.mark.parametrize(
     "name,props,protocol,extra", CASES,
-    ids=["counter", "push", "mailbox", "mailbox-gathered", "pull-values",
-         "pull-flags"])
+    ids=["counter", "push", "mailbox-slots", "mailbox-gathered",
+         "mailbox-tiled", "pull-values", "pull-flags", "pull-tiled"])
 def test_unsatisfiable_wait_trips_the_watchdog(oracle, name, props, protocol,
                                                extra):
     print("watchdog", name, protocol, extra, flush=True)
@@ -80,11 +84,13 @@ def test_unsatisfiable_wait_trips_the_watchdog(oracle, name, props, protocol,
                            incoming=protocol == "mailbox")
     good = P.execution_data_from_device_dag(
         dag, "sync_free", True, pushed=protocol == "push",
-        mailbox=protocol == "mailbox")
+        mailbox=protocol == "mailbox", tile_rows=lowering.tile_rows)
+    assert lowering.tile_rows == extra.get("tile_rows")
     # node 0 (level 0) never runs; the last node of the last level runs twice
-    nodes = dag.host("wavefronts").copy()
+    order = "tile_nodes" if lowering.tile_rows else "wavefronts"
+    nodes = dag.host(order).copy()
     assert nodes[0] == 0 and dag.host("dag_ptr")[nodes[-1] + 1] == (
-        dag.host("dag_ptr")[nodes[-1]])
+        dag.host("dag_ptr")[nodes[-1]])       # (a sink: no successors)
     nodes[0] = nodes[-1]
     bad = replace(good, task_nodes=device.to_device(nodes))
     arguments = {"Ap": indptr, "Ai": indices, "Ax": data, "b": work.rhs,
