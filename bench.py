@@ -33,7 +33,7 @@ TUNED = {
     "c1": dict(execution_mode="sync_free", threads_per_block=256, task_lanes=4,
                thread_unroll=1, dependence_protocol="mailbox",
                tile_rows=1024),
-    "c2": dict(execution_mode="sync_free", threads_per_block=256, task_lanes=4,
+    "c2": dict(execution_mode="sync_free", threads_per_block=384, task_lanes=4,
                thread_unroll=1, dependence_protocol="mailbox",
                tile_rows=4096),
     "c3": dict(execution_mode="sync_free", threads_per_block=256,
@@ -53,7 +53,7 @@ TUNED = {
 # profiled reports null.
 MEASURED_TRAFFIC = {
     ("c2", "sync_free", "push", 4): 1_937_433_319,
-    ("c2", "sync_free", "mailbox-slots", 4): 1_977_536_922,
+    ("c2", "sync_free", "mailbox", 4): 473_026_150,
     ("c3", "sync_free", "pull", 32): 1_526_372_660,
 }
 
@@ -287,6 +287,24 @@ def main():
         work.reference_style_flops / (ms_per_step * 1e-3) / 1e9, 3)
 
     kernel_ms = ms_per_step / launches_per_step
+    if schedule.execution_mode == "sync_free":
+        # the persistent executor is one launch per step: time that launch
+        # alone with HIP events on the library stream (eager launches, so the
+        # events sit directly around the kernel; the step above also holds
+        # the reset and operand-staging kernels)
+        device.kernel_timing = {"name": solver.hip_lowering.kernel_name}
+        try:
+            for _ in range(min(args.steps, 20)):
+                if work.kind == "ilu0_csr":
+                    device.copy(operands[0], pristine)
+                call.launch(use_graph=False)
+            call.synchronize()
+            pairs = device.kernel_timing.get("events", [])
+            if pairs:
+                kernel_ms = sum(device.elapsed_ms(a, b)
+                                for a, b in pairs) / len(pairs)
+        finally:
+            device.kernel_timing = None
     bytes_per_launch = work.algorithmic_bytes / launches_per_step
     achieved = bytes_per_launch / (kernel_ms * 1e-3) / 1e9
     result["roofline"] = {

@@ -768,7 +768,17 @@ class LaunchContext:
         return blocks
 
     def launch(self, name, grid, block, args):
-        self.device.launch(self.module.kernel(name), grid, block, args)
+        kernel = self.module.kernel(name)
+        timing = getattr(self.device, "kernel_timing", None)
+        if timing is None or timing.get("name") != name:
+            self.device.launch(kernel, grid, block, args)
+            return
+        # measurement hook (eager launches only): events around this kernel
+        start, stop = self.device.event(), self.device.event()
+        self.device.record(start)
+        self.device.launch(kernel, grid, block, args)
+        self.device.record(stop)
+        timing.setdefault("events", []).append((start, stop))
 
     def launch_levels(self, name, host_ptr, tasks_per_block, block, args,
                       start_index, end_index):
