@@ -729,6 +729,16 @@ __device__ __forceinline__ void lcd_tile_st(T* x, T* tile, lcd_index_t row0,
                            __HIP_MEMORY_SCOPE_WORKGROUP);
     lcd_st(&x[p], v);
 }
+// Lane k of every group of four adjacent lanes, to all four (one DPP move per
+// 32-bit half instead of a cross-lane permute through LDS).
+template <int K>
+__device__ __forceinline__ double lcd_quad_broadcast(double v) {
+    const int ctrl = K | (K << 2) | (K << 4) | (K << 6);   // quad_perm [K,K,K,K]
+    const long long bits = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_mov_dpp((int)bits, ctrl, 0xf, 0xf, false);
+    const int hi = __builtin_amdgcn_mov_dpp((int)(bits >> 32), ctrl, 0xf, 0xf, false);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
 // True when no lane of the task group raises the flag (one ballot instead of
 // a butterfly of shuffles; lanes of other groups that are masked off read 0).
 __device__ __forceinline__ bool lcd_group_none(bool flag) {
@@ -2343,6 +2353,11 @@ class HIPLowerer:
             defines.append(f"#define LCD_SEG_CAP {self._segment['capacity']}")
         if self._tile is not None:
             defines.append(f"#define LCD_TILE_ROWS {self._tile['rows']}")
+            # a poll of memory stalls the whole wavefront for a memory round
+            # trip; sources outside the running tile are polled on every
+            # (mask + 1)-th pass only, LDS on every pass
+            defines += ["#ifndef LCD_EXTERNAL_POLL_MASK",
+                        "#define LCD_EXTERNAL_POLL_MASK 0", "#endif"]
         for name, kind in array_arguments.items():
             default = "int" if kind == INT else "double"
             defines += [f"#ifndef LCD_T_{name}",
@@ -2737,21 +2752,33 @@ class HIPLowerer:
                     else f"!{missing}")
         unroll = ([f"{pad}#pragma unroll"] if self.task_lanes <= 8 else [])
         bound = "LCD_TASK_LANES" if self.task_lanes <= 8 else "_mb_have"
+        if self.task_lanes == 4:
+            # four lanes per task: the ordered sum is four quad broadcasts
+            ordered = [
+                f"{pad}        {{ const double _mb_in = lcd_quad_broadcast<{k}>(_mb_value); "
+                f"if ({k} < _mb_have) {own} = {own} + _mb_in; }}"
+                for k in range(4)]
+        else:
+            ordered = [
+                *unroll,
+                f"{pad}        for (int _mb_k = 0; _mb_k < {bound}; ++_mb_k) {{",
+                f"{pad}            const double _mb_in = __shfl(_mb_value, _mb_k, LCD_TASK_LANES);",
+                f"{pad}            if (_mb_k < _mb_have) {own} = {own} + _mb_in;",
+                f"{pad}        }}"]
         return [
             f"{pad}bool _ready = _mb_next == _mb_end;",
             f"{pad}if (!_ready) {{",
             f"{pad}    const int _mb_have = (_mb_end - _mb_next) < LCD_TASK_LANES ? "
             "(_mb_end - _mb_next) : LCD_TASK_LANES;",
-            f"{pad}    if (_lane < _mb_have && lcd_is_empty(_mb_value)) {{",
+            f"{pad}    if (_lane < _mb_have && lcd_is_empty(_mb_value)"
+            + (" && ((unsigned)(_g_src - _lcd_tile_row0) < (unsigned)_lcd_tile_rows"
+               " || (_spins & LCD_EXTERNAL_POLL_MASK) == 0)"
+               if self._tile is not None else "") + ") {",
             f"{pad}        const double _g_value = {load};",
             f"{pad}        if (!lcd_is_empty(_g_value)) _mb_value = {value};",
             f"{pad}    }}",
             f"{pad}    if ({complete}) {{",
-            *unroll,
-            f"{pad}        for (int _mb_k = 0; _mb_k < {bound}; ++_mb_k) {{",
-            f"{pad}            const double _mb_in = __shfl(_mb_value, _mb_k, LCD_TASK_LANES);",
-            f"{pad}            if (_mb_k < _mb_have) {own} = {own} + _mb_in;",
-            f"{pad}        }}",
+            *ordered,
             f"{pad}        _mb_next += _mb_have;",
             f"{pad}        _mb_value = lcd_empty();",
             *self._gather_fetch_lines(indent + 2),
