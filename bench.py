@@ -32,10 +32,10 @@ METRIC = "SpTRSV/SpILU0 solve ms, GFLOP/s, HBM GB/s (% roofline) on 1 MI355X"
 TUNED = {
     "c1": dict(execution_mode="sync_free", threads_per_block=256, task_lanes=4,
                thread_unroll=1, dependence_protocol="mailbox",
-               tile_rows=1024),
+               tile_rows=1024, spin_sleep=0),
     "c2": dict(execution_mode="sync_free", threads_per_block=384, task_lanes=4,
                thread_unroll=1, dependence_protocol="mailbox",
-               tile_rows=4096),
+               tile_rows=4096, spin_sleep=0),
     "c3": dict(execution_mode="sync_free", threads_per_block=256,
                task_lanes=32, thread_unroll=1, resident_waves_per_cu=32,
                dependence_protocol="pull", tile_rows=None),

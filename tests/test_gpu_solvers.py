@@ -396,3 +396,33 @@ def test_full_size_configurations(oracle, name, kind):
     residual = np.asarray(matrix @ result).ravel() - work.rhs
     scale = float(np.max(np.abs(work.rhs)))
     assert float(np.max(np.abs(residual))) <= 1e-10 * max(scale, 1.0) * 10
+
+
+def test_full_size_headline_defaults(oracle):
+    """Configuration 2 as bench.py runs it (tiled gathered mailbox) and as the
+    decorator chooses by itself: bit-identical to the sequential loop."""
+    work = workloads.configuration("c2")
+    expected = oracle.sptrsv_csc(work.indptr, work.indices, work.data,
+                                 work.rhs, work.n)
+    tuned = sptrsv.compile_sptrsv_csc(
+        execution_mode="sync_free", threads_per_block=384, task_lanes=4,
+        thread_unroll=1, dependence_protocol="mailbox", tile_rows=4096)
+    solve_and_check(tuned, work, expected, exact=True)
+    assert tuned.hip_lowering.tile_rows == 4096
+    automatic = sptrsv.compile_sptrsv_csc()
+    solve_and_check(automatic, work, expected, exact=True)
+    plan = automatic.schedule_plan(work.indptr, work.indices, work.data,
+                                   work.rhs, work.n)
+    assert plan.schedule.execution_mode == "sync_free"
+    assert plan.schedule.dependence_protocol == "mailbox"
+    assert plan.tile_rows == 4096 and automatic.hip_lowering.tile_rows == 4096
+    assert 0.6 < plan.dag.tile_locality(4096) < 0.7
+    # the power-law matrix keeps no edge inside a tile: flat queue
+    work = workloads.configuration("c3", n=100000)
+    solver = sptrsv.compile_sptrsv_csr()
+    expected = oracle.sptrsv_csr(work.indptr, work.indices, work.data,
+                                 work.rhs, work.n)
+    solve_and_check(solver, work, expected)
+    plan = solver.schedule_plan(work.indptr, work.indices, work.data,
+                                work.rhs, work.n)
+    assert plan.tile_rows is None and plan.dag.tile_locality(4096) < 0.2
