@@ -36,8 +36,8 @@ TUNED = {
     "c2": dict(execution_mode="sync_free", threads_per_block=384, task_lanes=4,
                thread_unroll=1, dependence_protocol="mailbox",
                tile_rows=4096, spin_sleep=0),
-    "c3": dict(execution_mode="sync_free", threads_per_block=256,
-               task_lanes=32, thread_unroll=1, resident_waves_per_cu=32,
+    "c3": dict(execution_mode="sync_free", threads_per_block=128,
+               task_lanes=64, thread_unroll=1,
                dependence_protocol="pull", tile_rows=None),
     "c4": dict(execution_mode="wavefront", threads_per_block=64, task_lanes=8,
                thread_unroll=1),
@@ -54,7 +54,7 @@ TUNED = {
 MEASURED_TRAFFIC = {
     ("c2", "sync_free", "push", 4): 1_937_433_319,
     ("c2", "sync_free", "mailbox", 4): 473_026_150,
-    ("c3", "sync_free", "pull", 32): 1_526_372_660,
+    ("c3", "sync_free", "pull", 64): 1_529_588_218,
 }
 
 

@@ -19,6 +19,7 @@ model :306-419, features :422-452, trip-count probe :455-571, fingerprint
 import ast
 import hashlib
 import itertools
+import math
 from collections import deque
 from copy import deepcopy
 from dataclasses import dataclass, replace
@@ -95,6 +96,10 @@ class WorkloadFeatures:
     memory_bytes: int
     thread_work_items: int = 0
     thread_loop_invocations: int = 0
+    # sum of squared trip counts of the mapped loop (0 = not known): with it
+    # the trip count seen from a work item, sum t^2 / sum t, tells skewed
+    # segment lengths from uniform ones
+    thread_work_squares: int = 0
 
     @property
     def average_in_degree(self):
@@ -105,6 +110,13 @@ class WorkloadFeatures:
         if self.thread_loop_invocations == 0:
             return 0.0
         return self.thread_work_items / self.thread_loop_invocations
+
+    @property
+    def weighted_thread_trip_count(self):
+        """Trip count of the segment an average work item belongs to."""
+        if self.thread_work_items == 0 or self.thread_work_squares == 0:
+            return self.average_thread_trip_count
+        return self.thread_work_squares / self.thread_work_items
 
 
 @dataclass(frozen=True)
@@ -350,7 +362,7 @@ class AnalyticScheduler:
             raise SchedulerError(f"Unknown execution mode {execution_mode!r}.")
         lanes = (task_threads(threads_per_block, n_warp, task_lanes)
                  * thread_unroll if thread_mapped else 1)
-        parallelism = (features.average_thread_trip_count
+        parallelism = (self.lane_parallelism(features)
                        if thread_mapped and features.thread_loop_invocations
                        else average_in_degree)
         active_lanes = min(lanes, max(parallelism, 1.0))
@@ -358,6 +370,10 @@ class AnalyticScheduler:
             launch_s=launch_s, sync_s=sync_s,
             memory_s=features.memory_bytes / arch.memory_bandwidth_bytes_per_s,
             compute_s=features.flops / (active_lanes * arch.lane_flops_per_s))
+
+    def lane_parallelism(self, features):
+        """Lanes a task of the mapped loop can keep busy."""
+        return features.average_thread_trip_count
 
     def candidates(self, features, space):
         return [
@@ -391,6 +407,14 @@ class CalibratedScheduler(AnalyticScheduler):
         PUSH_DEPENDENCE: 1.6 * LOADED_HANDOFF_FACTOR,
         COUNTER_DEPENDENCE: 2.4 * LOADED_HANDOFF_FACTOR,
     }
+
+    def lane_parallelism(self, features):
+        """Geometric mean of the plain and the work-weighted trip count: with
+        uniform segments both agree; with power-law rows (n = 10^6, mean 17,
+        work-weighted 134) the long rows carry the critical path, and 32 to 64
+        lanes measured 20 % faster than the 16 the plain mean selects."""
+        return math.sqrt(features.average_thread_trip_count
+                         * features.weighted_thread_trip_count)
 
     def estimate(self, features, execution_mode, threads_per_block,
                  thread_unroll, n_warp, thread_mapped,
@@ -440,20 +464,24 @@ def extract_workload_features(dag_successors, wavefront_list, argument_values,
     nonzeros = _nonzeros_from_pointer_arrays(argument_values, function_props)
     if nonzeros is None:
         nonzeros = rows + edges
+    squares = 0
     if thread_trip_counts is None:
         work_items = invocations = 0
     elif isinstance(thread_trip_counts, dict):
         work_items = int(thread_trip_counts["work_items"])
         invocations = int(thread_trip_counts["invocations"])
+        squares = int(thread_trip_counts.get("work_squares", 0))
     else:
         counts = tuple(max(int(c), 0) for c in thread_trip_counts)
         work_items, invocations = sum(counts), len(counts)
+        squares = sum(c * c for c in counts)
     base = nonzeros if thread_trip_counts is None else work_items
     return WorkloadFeatures(
         rows=rows, edges=edges, levels=levels, nonzeros=nonzeros,
         flops=float(flops_per_iteration * base),
         memory_bytes=_array_bytes(argument_values),
-        thread_work_items=work_items, thread_loop_invocations=invocations)
+        thread_work_items=work_items, thread_loop_invocations=invocations,
+        thread_work_squares=squares)
 
 
 # ---- trip counts of the thread-mapped loop -------------------------------
@@ -567,7 +595,8 @@ def segment_trip_counts(thread_loop, block_iterator, argument_values):
     pointers = np.asarray(pointers, dtype=np.int64)
     trips = np.maximum(
         pointers[1:] + upper_offset - pointers[:-1] - lower_offset, 0)
-    return {"work_items": int(trips.sum()), "invocations": int(trips.size)}
+    return {"work_items": int(trips.sum()), "invocations": int(trips.size),
+            "work_squares": int((trips * trips).sum())}
 
 
 def pointer_array_names(function_props):

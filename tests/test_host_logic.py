@@ -311,7 +311,15 @@ def test_fingerprint_and_flops():
     loop = next(n for n in ast.walk(module) if isinstance(n, ast.For)
                 and n.target.id == "j")
     trips = S.segment_trip_counts(loop, "i", {"Ap": np.array([0, 3, 4, 9])})
-    assert trips == {"work_items": 2 + 0 + 4, "invocations": 3}
+    assert trips == {"work_items": 2 + 0 + 4, "invocations": 3,
+                     "work_squares": 4 + 0 + 16}
+    skewed = S.extract_workload_features(3, 2, {}, thread_trip_counts=trips,
+                                         edges=2)
+    assert skewed.average_thread_trip_count == 2.0
+    assert skewed.weighted_thread_trip_count == pytest.approx(20 / 6)
+    assert S.AnalyticScheduler(S.FALLBACK_ARCH_CONSTANTS).lane_parallelism(skewed) == 2.0
+    assert S.CalibratedScheduler(S.FALLBACK_ARCH_CONSTANTS).lane_parallelism(
+        skewed) == pytest.approx((2.0 * 20 / 6) ** 0.5)
 
 
 # ---------------------------------------------------- structural lookups
