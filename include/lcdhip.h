@@ -169,7 +169,18 @@ int lcdhip_graph_destroy(lcdhip_graph *graph);
  *         (src, dst) = owner_is_source ? (seg, d_idx[p]) : (d_idx[p], seg)
  *         if guard(src, dst): edge src -> dst
  * guard: 0 none, 1 dst > src, 2 src != dst.
+ *
+ * A rule with relation LCDHIP_RULE_LATER has no structure arrays (d_ptr and
+ * d_idx NULL, idx_size ignored) and enumerates
+ *     for j in [seg + lower_offset, n): edge seg -> j      (lower_offset >= 1)
+ * which is what the reference's planner emits for a relational loop such as
+ * `for j in range(k + 1, n)` (CSC ILU0, compiler/demo/spilu0.py:50-82;
+ * compiler/transform_tests/test_spilu0_codegen.py:146-150).  It yields
+ * (n - lower_offset)(n - lower_offset + 1) / 2 edges, so it is meant for
+ * small n; LCDHIP_DAG_INCOMING cannot be combined with it.
  */
+#define LCDHIP_RULE_SEGMENT 0
+#define LCDHIP_RULE_LATER 1
 #define LCDHIP_GUARD_NONE 0
 #define LCDHIP_GUARD_GREATER 1
 #define LCDHIP_GUARD_NOT_EQUAL 2
@@ -183,6 +194,7 @@ typedef struct {
     int32_t upper_offset;
     int32_t guard;
     int32_t break_at_owner;
+    int32_t relation;        /* LCDHIP_RULE_SEGMENT or LCDHIP_RULE_LATER */
 } lcdhip_dag_rule;
 
 #define LCDHIP_DAG_LEVELS 1u        /* also build level sets / wavefronts */

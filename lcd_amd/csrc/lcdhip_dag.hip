@@ -85,6 +85,34 @@ __global__ void emit_keys_kernel(RuleDevice rule, int64_t n,
         atomicAdd(candidates, hits);
 }
 
+// Relational rule: every task seg releases all tasks j >= seg + first.  One
+// thread per (seg, j) pair; the key slot of the pair is its rank in (seg, j)
+// order.
+__device__ __host__ inline int64_t later_prefix(int64_t seg, int64_t span)
+{
+    // pairs emitted by tasks below seg; task t emits max(span - t, 0) pairs
+    int64_t full = seg < span ? seg : span;
+    return full * span - full * (full - 1) / 2;
+}
+
+__global__ void emit_later_keys_kernel(int64_t n, int32_t first,
+                                       unsigned long long *__restrict__ keys,
+                                       int32_t *__restrict__ edge_count,
+                                       unsigned long long *__restrict__ candidates)
+{
+    int64_t seg = blockIdx.y;
+    int64_t j = seg + first + blockIdx.x * static_cast<int64_t>(blockDim.x) +
+                threadIdx.x;
+    if (j >= n)
+        return;
+    int64_t slot = later_prefix(seg, n - first) + (j - seg - first);
+    keys[slot] = (static_cast<unsigned long long>(seg) << 32) |
+                 static_cast<unsigned long long>(j);
+    atomicAdd(&edge_count[j], 1);
+    if (j == seg + first)
+        atomicAdd(candidates, static_cast<unsigned long long>(n - j));
+}
+
 // From the sorted unique keys: successor array, unique in-degree and the
 // out-degree histogram (scanned into dag_ptr afterwards).
 __global__ void split_edges_kernel(const unsigned long long *__restrict__ keys,
@@ -470,13 +498,29 @@ extern "C" int lcdhip_dag_build(const lcdhip_dag_rule *rules, int rule_count,
     *out = nullptr;
     hipStream_t stream = resolve_stream(stream_);
     int64_t key_capacity = 0;
+    std::vector<int64_t> rule_keys(rule_count, 0);
     for (int r = 0; r < rule_count; ++r) {
-        if (!rules[r].d_ptr || rules[r].idx_size < 0 ||
-            (rules[r].idx_size > 0 && !rules[r].d_idx)) {
+        if (rules[r].relation == LCDHIP_RULE_LATER) {
+            if (rules[r].lower_offset < 1 || n > 65535 ||
+                (flags & LCDHIP_DAG_INCOMING)) {
+                set_error("rule %d: a relational rule needs lower_offset >= 1,"
+                          " at most 65535 tasks and no incoming listing", r);
+                return LCDHIP_ERR_ARGUMENT;
+            }
+            int64_t span = std::max<int64_t>(n - rules[r].lower_offset, 0);
+            rule_keys[r] = span * (span + 1) / 2;
+        } else if (rules[r].relation != LCDHIP_RULE_SEGMENT) {
+            set_error("rule %d has an unknown relation %d", r,
+                      rules[r].relation);
+            return LCDHIP_ERR_ARGUMENT;
+        } else if (!rules[r].d_ptr || rules[r].idx_size < 0 ||
+                   (rules[r].idx_size > 0 && !rules[r].d_idx)) {
             set_error("rule %d has a NULL structure array", r);
             return LCDHIP_ERR_ARGUMENT;
+        } else {
+            rule_keys[r] = rules[r].idx_size;
         }
-        key_capacity += rules[r].idx_size;
+        key_capacity += rule_keys[r];
     }
     if (key_capacity >= (int64_t(1) << 31)) {
         set_error("more than 2^31 candidate edges are not supported");
@@ -514,6 +558,17 @@ extern "C" int lcdhip_dag_build(const lcdhip_dag_rule *rules, int rule_count,
 
     int64_t offset = 0;
     for (int r = 0; r < rule_count && n > 0; ++r) {
+        if (rules[r].relation == LCDHIP_RULE_LATER) {
+            if (rule_keys[r] > 0)
+                hipLaunchKernelGGL(
+                    emit_later_keys_kernel,
+                    dim3(blocks_for(n - rules[r].lower_offset),
+                         static_cast<unsigned>(n - rules[r].lower_offset)),
+                    dim3(kBlock), 0, stream, n, rules[r].lower_offset,
+                    keys + offset, edge_count, d_candidates);
+            offset += rule_keys[r];
+            continue;
+        }
         RuleDevice rule{rules[r].d_ptr,         rules[r].d_idx,
                         rules[r].idx_size,      rules[r].owner_is_source,
                         rules[r].lower_offset,  rules[r].upper_offset,
@@ -521,7 +576,7 @@ extern "C" int lcdhip_dag_build(const lcdhip_dag_rule *rules, int rule_count,
         hipLaunchKernelGGL(emit_keys_kernel, dim3(blocks_for(n)), dim3(kBlock),
                            0, stream, rule, n, keys + offset, edge_count,
                            d_flags, d_candidates);
-        offset += rules[r].idx_size;
+        offset += rule_keys[r];
     }
     LCDHIP_CHECK(hipGetLastError());
     unsigned long long candidates = 0;

@@ -19,6 +19,7 @@ from lcd_amd.dependence import (
     GUARD_GREATER,
     GUARD_NONE,
     GUARD_NOT_EQUAL,
+    LaterRule,
     SegmentRule,
 )
 
@@ -80,9 +81,9 @@ def create_dag_plan(ordering_dependences, node_data=None,
         if getattr(dependence, "kind", None) == "reduction":
             raise DAGCodegenError(
                 "Reduction dependences cannot be lowered to DAG edges.")
-        if not isinstance(dependence, SegmentRule):
+        if not isinstance(dependence, (SegmentRule, LaterRule)):
             raise DAGCodegenError(
-                "Edge rules must be SegmentRule objects; got "
+                "Edge rules must be SegmentRule or LaterRule objects; got "
                 f"{type(dependence).__name__}.")
         if dependence not in rules:
             rules.append(dependence)
@@ -125,10 +126,20 @@ def generate_dag_source(plan, function_name="extract_dag",
     if edge_multiplicity:
         lines.append(f"    _dag_edge_count = [0 for _dag_node in range({n})]")
     for index, rule in enumerate(plan.edge_rules):
-        lower, upper = _range_source(rule)
         it, inner = rule.block_iterator, rule.inner_iterator
         source, destination = f"_dag_source_{index}", f"_dag_destination_{index}"
         lines.append(f"    for {it} in range({plan.node_lower}, {n}):")
+        if isinstance(rule, LaterRule):
+            lines.append(f"        for {inner} in range({it} + "
+                         f"{rule.lower_offset}, {n}):")
+            lines.append(f"            {source} = {it}")
+            lines.append(f"            {destination} = {inner}")
+            lines.append(f"            _dag_successors[{source}]"
+                         f".add({destination})")
+            if edge_multiplicity:
+                lines.append(f"            _dag_edge_count[{destination}] += 1")
+            continue
+        lower, upper = _range_source(rule)
         lines.append(f"        for {inner} in range({lower}, {upper}):")
         if rule.break_at_owner:
             lines.append(f"            if {rule.endpoint_source()} >= {it}:")
@@ -186,6 +197,10 @@ def device_rules(plan, argument_values):
     """Bind the plan's rules to concrete structure arrays."""
     bound = []
     for rule in plan.edge_rules:
+        if isinstance(rule, LaterRule):
+            bound.append(dict(relation=rule.relation,
+                              lower_offset=rule.lower_offset))
+            continue
         try:
             pointers = argument_values[rule.pointer_array]
             indices = argument_values[rule.index_array]
@@ -262,6 +277,8 @@ def direct_dependence(plan, thread_iterator, validate_endpoints=False):
     if thread_iterator is None or len(plan.edge_rules) != 1:
         return None
     rule = plan.edge_rules[0]
+    if not isinstance(rule, SegmentRule):
+        return None
     if rule.iterators != [plan.parallel_iterator, thread_iterator]:
         return None
     if rule.break_at_owner:
@@ -288,7 +305,7 @@ __all__ = [
     "COUNTER_DEPENDENCE", "PUSH_DEPENDENCE", "PULL_DEPENDENCE",
     "MAILBOX_DEPENDENCE",
     "DEPENDENCE_PROTOCOLS", "DAGCodegenError", "DAGPlan", "DirectDependence",
-    "EdgeRule", "GUARD_GREATER", "GUARD_NONE", "GUARD_NOT_EQUAL",
+    "EdgeRule", "GUARD_GREATER", "GUARD_NONE", "GUARD_NOT_EQUAL", "LaterRule",
     "build_device_dag", "compile_dag_builder", "create_dag_plan",
     "direct_dependence", "generate_dag_source",
 ]

@@ -287,7 +287,10 @@ def parallel(**kwargs):
             dag_plan, device=device_layer, **inspector_options)
         rule_arrays = []
         for rule in dag_plan.edge_rules:
-            for name in (rule.pointer_array, rule.index_array):
+            for name in (getattr(rule, "pointer_array", None),
+                         getattr(rule, "index_array", None)):
+                if name is None:
+                    continue
                 if name not in rule_arrays:
                     rule_arrays.append(name)
         fingerprint_names = rule_arrays + [

@@ -18,6 +18,11 @@ supported solver loops to, and produces the same edge rules:
 * a task writes positions of its own segment ``D[p]`` and reads positions of
   the segment of ``I[q]``                      -> pull rule over ``q`` with
   the loop's ``break`` (ILU0-CSR; test_spilu0_codegen.py:129-144)
+* a task reads or writes positions of the segments of every later task,
+  ``for j in range(i + 1, n)``                 -> the relational rule
+  ``i -> j`` for all later ``j``, plus the push rule over the own segment
+  whose entries name the rows it updates there (ILU0-CSC;
+  test_spilu0_codegen.py:146-150)
 
 Anything else raises :class:`DependenceAnalysisError` rather than guessing;
 callers can pass ``edge_rules=`` to the decorator explicitly in that case.
@@ -74,6 +79,28 @@ class SegmentRule:
         return (f"RAW on {self.carried_by}: {source} -> {destination} "
                 f"over {self.inner_iterator} in segment of "
                 f"{self.pointer_array}[{self.block_iterator}]")
+
+
+@dataclass(frozen=True)
+class LaterRule:
+    """``for seg in range(node_count): for j in range(seg + lower_offset,
+    node_count)`` yields the edge ``seg -> j``: the task touches segments of
+    every later task, so all of them wait for it."""
+
+    lower_offset: int = 1
+    block_iterator: str = "i"
+    inner_iterator: str = "j"
+    carried_by: str = ""
+    relation = 1
+
+    @property
+    def iterators(self):
+        return [self.block_iterator, self.inner_iterator]
+
+    def describe(self):
+        return (f"RAW on {self.carried_by}: {self.block_iterator} -> "
+                f"{self.inner_iterator} for every {self.inner_iterator} >= "
+                f"{self.block_iterator} + {self.lower_offset}")
 
 
 @dataclass(frozen=True)
@@ -207,6 +234,9 @@ class _Analyzer:
         self.aliases = _AliasTable(function)
         self.pointers = set(pointer_arrays(function_props))
         self.segments = {}     # iterator -> _Segment
+        self.later = {}        # iterator over range(block + c, count) -> c
+        self.needles = {}      # segment iterator -> value its search matches
+        self.node_count = None
         self.breaks = {}       # iterator -> list of resolved break tests
         self.writes = []       # (array, classification, node, is_update)
         self.reads = []        # (array, classification)
@@ -250,6 +280,8 @@ class _Analyzer:
         owner = self.aliases.resolve(owner)
         if isinstance(owner, ast.Name) and owner.id == self.block:
             return ("self",)
+        if isinstance(owner, ast.Name) and owner.id in self.later:
+            return ("later", owner.id)
         if (isinstance(owner, ast.Subscript) and isinstance(owner.value, ast.Name)
                 and isinstance(owner.slice, ast.Name)
                 and owner.slice.id in self.segments):
@@ -268,6 +300,8 @@ class _Analyzer:
                 return ("own_position", index.id)
             if kind[0] == "indirect":
                 return ("other_position", kind[1], kind[2], index.id)
+            if kind[0] == "later":
+                return ("later_position", kind[1], index.id)
             return ("unknown", ast.unparse(index))
         if isinstance(index, ast.Subscript) and isinstance(index.value, ast.Name):
             base, offset = _split_offset(index.slice)
@@ -277,6 +311,38 @@ class _Analyzer:
                     == ("self",)):
                 return ("indirect", index.value.id, base.id)
         return ("unknown", ast.unparse(index))
+
+    def _later_offset(self, loop):
+        """``c`` when ``loop`` is ``for j in range(block + c, node_count)``
+        with ``c >= 1``, else None."""
+        call = loop.iter
+        if not (isinstance(call, ast.Call) and isinstance(call.func, ast.Name)
+                and call.func.id == "range" and len(call.args) == 2
+                and self.node_count is not None):
+            return None
+        base, offset = _split_offset(self.aliases.resolve(call.args[0]))
+        if not (isinstance(base, ast.Name) and base.id == self.block
+                and offset >= 1):
+            return None
+        if not _same(self.aliases.resolve(call.args[1]), self.node_count):
+            return None
+        return offset
+
+    def _search_needle(self, loop):
+        """The value ``v`` of ``for p in <segment>: if I[p] == v: ...``."""
+        if not (len(loop.body) == 1 and isinstance(loop.body[0], ast.If)
+                and isinstance(loop.body[0].test, ast.Compare)
+                and len(loop.body[0].test.ops) == 1
+                and isinstance(loop.body[0].test.ops[0], ast.Eq)):
+            return None
+        test = loop.body[0].test
+        for entry, other in ((test.left, test.comparators[0]),
+                             (test.comparators[0], test.left)):
+            if (isinstance(entry, ast.Subscript)
+                    and isinstance(entry.slice, ast.Name)
+                    and entry.slice.id == loop.target.id):
+                return self.aliases.resolve(other)
+        return None
 
     # ---- traversal ---------------------------------------------------------
     def _record_reads(self, node, written_arrays):
@@ -294,6 +360,13 @@ class _Analyzer:
                     segment = self._segment_of_range(statement)
                     if segment is not None:
                         self.segments[statement.target.id] = segment
+                        needle = self._search_needle(statement)
+                        if needle is not None:
+                            self.needles[statement.target.id] = needle
+                    else:
+                        offset = self._later_offset(statement)
+                        if offset is not None:
+                            self.later[statement.target.id] = offset
                 self._record_reads(statement.iter, written_arrays)
                 self._visit(statement.body, written_arrays,
                             loop_stack + [statement])
@@ -374,8 +447,33 @@ class _Analyzer:
             carried_by=array,
         )
 
+    def _later_rule(self, iterator, array):
+        return LaterRule(lower_offset=self.later[iterator],
+                         block_iterator=self.block, inner_iterator=iterator,
+                         carried_by=array)
+
+    def _row_rule(self, write_kind, read_kind, array):
+        """Two tasks meet in a later task's segment: the writer at the entry
+        its search finds for ``I[q]`` (``q`` in its own segment), the reader
+        at the entry found for its own id.  They coincide when ``I[q]`` is
+        the reader: the push rule over ``q``."""
+        written = self.needles.get(write_kind[2])
+        read = self.needles.get(read_kind[2])
+        if written is None or read is None:
+            return None
+        if not (isinstance(read, ast.Name) and read.id == self.block):
+            return None
+        kind = self._classify(written) if isinstance(
+            written, ast.Subscript) else ("unknown",)
+        if kind[0] != "indirect":
+            return None
+        return self._rule(True, kind[1], kind[2], array)
+
     def run(self):
         loop = find_block_loop(self.function, self.block)
+        if (isinstance(loop.iter, ast.Call) and loop.iter.args
+                and not loop.iter.keywords):
+            self.node_count = self.aliases.resolve(loop.iter.args[-1])
         local_names = set()
         for node in ast.walk(loop):
             if isinstance(node, ast.Name) and isinstance(node.ctx, ast.Store):
@@ -431,6 +529,18 @@ class _Analyzer:
                 elif (write_kind[0] == "own_position"
                       and read_kind[0] == "other_position"):
                     rule = self._rule(False, read_kind[1], read_kind[2], array)
+                elif "later_position" in (write_kind[0], read_kind[0]):
+                    if write_kind[0] == read_kind[0]:
+                        rule = self._row_rule(write_kind, read_kind, array)
+                    elif {write_kind[0], read_kind[0]} <= {
+                            "later_position", "self", "own_position"}:
+                        later = (write_kind if write_kind[0] == "later_position"
+                                 else read_kind)
+                        rule = self._later_rule(later[1], array)
+                    else:
+                        raise DependenceAnalysisError(
+                            f"Unsupported dependence on {array!r}: write "
+                            f"{write_kind[0]} / read {read_kind[0]}.")
                 elif write_kind[0] in ("self", "own_position") and (
                         read_kind[0] in ("self", "own_position")):
                     rule = None          # same task
@@ -446,6 +556,7 @@ class _Analyzer:
                         f"{write_kind[0]} / read {read_kind[0]}.")
                 if rule is not None and rule not in rules:
                     rules.append(rule)
+        rules.sort(key=lambda rule: isinstance(rule, LaterRule))
         return DependenceAnalysis(
             ordering_dependences=rules,
             reduction_dependences=reduction_rules,

@@ -31,6 +31,7 @@ import textwrap
 
 from lcd_amd.structural_lookups import (
     match_segment_search,
+    structure_aliases,
     rewrite_structural_lookups,
     segmented_array_pairs,
     structural_lookup_names,
@@ -1565,11 +1566,12 @@ class HIPLowerer:
         if not self.segmented_sorted:
             return body
         pairs = self.segmented_sorted
+        aliases = structure_aliases(ast.Module(body=body, type_ignores=[]))
 
         class Searches(ast.NodeTransformer):
             def visit_For(self, node):
                 node = self.generic_visit(node)
-                match = match_segment_search(node, pairs)
+                match = match_segment_search(node, pairs, aliases)
                 if match is None:
                     return node
                 lower, upper = node.iter.args

@@ -89,12 +89,16 @@ class _Arch(ctypes.Structure):
         "lane_flops_per_s", "handoff_s", "barrier_s", "graph_node_s")]
 
 
+RULE_SEGMENT, RULE_LATER = 0, 1
+
+
 class _DagRule(ctypes.Structure):
     _fields_ = [
         ("d_ptr", ctypes.c_void_p), ("d_idx", ctypes.c_void_p),
         ("idx_size", ctypes.c_int64), ("owner_is_source", ctypes.c_int32),
         ("lower_offset", ctypes.c_int32), ("upper_offset", ctypes.c_int32),
         ("guard", ctypes.c_int32), ("break_at_owner", ctypes.c_int32),
+        ("relation", ctypes.c_int32),
     ]
 
 
@@ -588,12 +592,18 @@ class HIPDevice:
                   incoming=False):
         """Run the on-device inspector. ``rules`` are dicts/objects with
         ptr, idx, owner_is_source, lower_offset, upper_offset, guard,
-        break_at_owner (ptr/idx host or device arrays)."""
+        break_at_owner (ptr/idx host or device arrays), or, for the
+        relational rule ``seg -> every j >= seg + lower_offset``, with
+        ``relation=RULE_LATER`` and ``lower_offset`` only."""
         keep = []
         array = (_DagRule * max(len(rules), 1))()
         for slot, rule in zip(array, rules):
             get = rule.get if isinstance(rule, dict) else (
-                lambda key, r=rule: getattr(r, key))
+                lambda key, r=rule: getattr(r, key, None))
+            if int(get("relation") or 0) == RULE_LATER:
+                slot.relation = RULE_LATER
+                slot.lower_offset = int(get("lower_offset"))
+                continue
             slot.d_ptr, _ = self._resident_int32(get("ptr"), keep)
             slot.d_idx, slot.idx_size = self._resident_int32(get("idx"), keep)
             slot.owner_is_source = int(bool(get("owner_is_source")))

@@ -72,7 +72,49 @@ def _subscript_of(node, array):
             and node.value.id == array)
 
 
-def match_segment_search(node, array_pairs):
+def structure_aliases(function_ast):
+    """Names assigned exactly once to an expression over arrays that the
+    function never stores to (``col_start = A_indptr[k]``): a search whose
+    bounds are such names is the same search as one over the expressions
+    (the reference normalises these aliases away before matching,
+    compiler/ast_normalization.py:7-30)."""
+    stored_arrays, counts, values = set(), {}, {}
+    for node in ast.walk(function_ast):
+        if isinstance(node, ast.Subscript) and isinstance(
+                node.ctx, ast.Store) and isinstance(node.value, ast.Name):
+            stored_arrays.add(node.value.id)
+        if isinstance(node, ast.arg):
+            counts[node.arg] = counts.get(node.arg, 0) + 2
+        if isinstance(node, ast.Name) and isinstance(node.ctx, ast.Store):
+            counts[node.id] = counts.get(node.id, 0) + 1
+        if (isinstance(node, ast.Assign) and len(node.targets) == 1
+                and isinstance(node.targets[0], ast.Name)):
+            values[node.targets[0].id] = node.value
+    aliases = {}
+    for name, value in values.items():
+        if counts.get(name) != 1:
+            continue
+        parts = list(ast.walk(value))
+        if any(isinstance(part, (ast.Call, ast.Attribute)) for part in parts):
+            continue
+        if any(isinstance(part, ast.Subscript)
+               and not (isinstance(part.value, ast.Name)
+                        and part.value.id not in stored_arrays)
+               for part in parts):
+            continue
+        if not any(isinstance(part, ast.Subscript) for part in parts):
+            continue
+        aliases[name] = value
+    return aliases
+
+
+def _resolve(node, aliases):
+    if isinstance(node, ast.Name) and aliases and node.id in aliases:
+        return aliases[node.id]
+    return node
+
+
+def match_segment_search(node, array_pairs, aliases=None):
     """Recognise the canonical equality search over one segment."""
     if not (isinstance(node, ast.For) and not node.orelse
             and isinstance(node.target, ast.Name)
@@ -90,7 +132,7 @@ def match_segment_search(node, array_pairs):
             or not isinstance(branch.test.ops[0], ast.Eq)):
         return None
     iterator = node.target.id
-    lower, upper = node.iter.args
+    lower, upper = (_resolve(bound, aliases) for bound in node.iter.args)
     left, right = branch.test.left, branch.test.comparators[0]
     for pointer_array, index_array in array_pairs:
         if not (_subscript_of(lower, pointer_array)
@@ -134,8 +176,9 @@ def create_structural_lookup_plan(function_ast, function_props=None):
         return ()
     used = {n.id for n in ast.walk(function_ast) if isinstance(n, ast.Name)}
     planned = []
+    aliases = structure_aliases(function_ast)
     for node in ast.walk(function_ast):
-        match = match_segment_search(node, array_pairs)
+        match = match_segment_search(node, array_pairs, aliases)
         if match is None or not _self_lookup(match):
             continue
         pair = (match.pointer_array, match.index_array)
@@ -172,11 +215,12 @@ def rewrite_structural_lookups(function_ast, plan, function_props=None):
         return deepcopy(function_ast)
     array_pairs = segmented_array_pairs(function_props)
     by_pair = {(l.pointer_array, l.index_array): l for l in plan}
+    aliases = structure_aliases(function_ast)
 
     class Rewriter(ast.NodeTransformer):
         def visit_For(self, node):
             node = self.generic_visit(node)
-            match = match_segment_search(node, array_pairs)
+            match = match_segment_search(node, array_pairs, aliases)
             if match is None or not _self_lookup(match):
                 return node
             lookup = by_pair.get((match.pointer_array, match.index_array))
@@ -253,6 +297,6 @@ __all__ = [
     "StructuralLookup", "StructuralLookupError",
     "create_structural_lookup_plan", "materialize_structural_lookups",
     "rewrite_structural_lookups", "structural_argument_names",
-    "structural_lookup_names", "match_segment_search",
+    "structural_lookup_names", "match_segment_search", "structure_aliases",
     "segmented_array_pairs",
 ]

@@ -14,6 +14,7 @@
  *   oracle_sptrsv_csr        compiler/demo/sptrsv.py:26-33
  *   oracle_gauss_seidel_csr  compiler/demo/gauss_seidel.py:18-26
  *   oracle_ilu0_csr          compiler/demo/spilu0.py:21-47
+ *   oracle_ilu0_csc          compiler/demo/spilu0.py:50-82
  *   oracle_dag_*             generated inspector, compiler/dag_codegen.py:1151-1550
  *                            (set successors, unique in-degree, edge
  *                            multiplicity), compact_successors
@@ -103,6 +104,46 @@ void oracle_ilu0_csr(double *A_data, const int32_t *A_indices,
     }
 }
 
+/* Right-looking ILU0 on CSC storage: column k scales its sub-diagonal and
+ * updates every later column j that holds an entry in row k. */
+void oracle_ilu0_csc(double *A_data, const int32_t *A_indices,
+                     const int32_t *A_indptr, int64_t n)
+{
+    for (int64_t k = 0; k < n; ++k) {
+        int64_t col_start = A_indptr[k], col_end = A_indptr[k + 1];
+        double diag_val = 0.0;
+        for (int64_t d = col_start; d < col_end; ++d)
+            if (A_indices[d] == k) {
+                diag_val = A_data[d];
+                break;
+            }
+        for (int64_t i_ptr = col_start; i_ptr < col_end; ++i_ptr) {
+            int64_t i = A_indices[i_ptr];
+            if (i <= k)
+                continue;
+            if (diag_val != 0.0) {
+                A_data[i_ptr] = A_data[i_ptr] / diag_val;
+                double l_ik = A_data[i_ptr];
+                for (int64_t j = k + 1; j < n; ++j) {
+                    int64_t j_start = A_indptr[j], j_end = A_indptr[j + 1];
+                    double u_kj = 0.0;
+                    for (int64_t kj = j_start; kj < j_end; ++kj)
+                        if (A_indices[kj] == k) {
+                            u_kj = A_data[kj];
+                            break;
+                        }
+                    if (u_kj != 0.0)
+                        for (int64_t ij = j_start; ij < j_end; ++ij)
+                            if (A_indices[ij] == i) {
+                                A_data[ij] = A_data[ij] - l_ik * u_kj;
+                                break;
+                            }
+                }
+            }
+        }
+    }
+}
+
 /* True flop count of ILU0-CSR: one division per eliminated entry plus a
  * multiply-subtract per matched (j, k) pair. */
 int64_t oracle_ilu0_csr_flops(const int32_t *A_indices, const int32_t *A_indptr,
@@ -142,6 +183,10 @@ int64_t oracle_ilu0_csr_flops(const int32_t *A_indices, const int32_t *A_indptr,
  *           if guard(src, dst): successors[src].add(dst); edge_count[dst] += 1
  *
  * guard: 0 = none, 1 = dst > src, 2 = src != dst.
+ *
+ * relation 1 (no arrays): `for j in range(seg + lower_offset, n)` yields
+ * seg -> j, the planner's output for a relational loop
+ * (compiler/transform_tests/test_spilu0_codegen.py:146-150).
  */
 typedef struct {
     const int32_t *ptr;
@@ -151,6 +196,7 @@ typedef struct {
     int32_t upper_offset;
     int32_t guard;
     int32_t break_at_owner;
+    int32_t relation;
 } oracle_rule;
 
 typedef struct {
@@ -178,6 +224,12 @@ typedef void (*edge_fn)(void *state, int64_t src, int64_t dst);
 
 static int enumerate_rule(const oracle_rule *r, int64_t n, edge_fn fn, void *st)
 {
+    if (r->relation == 1) {
+        for (int64_t seg = 0; seg < n; ++seg)
+            for (int64_t j = seg + r->lower_offset; j < n; ++j)
+                fn(st, seg, j);
+        return 0;
+    }
     for (int64_t seg = 0; seg < n; ++seg) {
         int64_t lo = (int64_t)r->ptr[seg] + r->lower_offset;
         int64_t hi = (int64_t)r->ptr[seg + 1] + r->upper_offset;

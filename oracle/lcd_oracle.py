@@ -32,6 +32,7 @@ class _Rule(ctypes.Structure):
         ("upper_offset", ctypes.c_int32),
         ("guard", ctypes.c_int32),
         ("break_at_owner", ctypes.c_int32),
+        ("relation", ctypes.c_int32),
     ]
 
 
@@ -129,6 +130,14 @@ def ilu0_csr(A_data, A_indices, A_indptr):
     return data
 
 
+def ilu0_csc(A_data, A_indices, A_indptr):
+    data = _f64(A_data).copy()
+    idx, ptr = _i32(A_indices), _i32(A_indptr)
+    lib().oracle_ilu0_csc(_p(data), _p(idx), _p(ptr),
+                          ctypes.c_int64(len(ptr) - 1))
+    return data
+
+
 def ilu0_csr_flops(A_indices, A_indptr):
     idx, ptr = _i32(A_indices), _i32(A_indptr)
     return int(lib().oracle_ilu0_csr_flops(_p(idx), _p(ptr),
@@ -220,11 +229,27 @@ def rule_ilu0_csr(A_indptr, A_indices):
                      break_at_owner=True)
 
 
+def rule_later(lower_offset=1):
+    """``for j in range(seg + lower_offset, n)``: seg -> j."""
+    return dict(relation=1, lower_offset=int(lower_offset))
+
+
+def rules_ilu0_csc(A_indptr, A_indices):
+    """The two rules of CSC ILU0
+    (compiler/transform_tests/test_spilu0_codegen.py:146-150)."""
+    return [make_rule(A_indptr, A_indices, True, guard=GUARD_GREATER),
+            rule_later(1)]
+
+
 def dag_build(rules, n):
     rules = list(rules)
     array = (_Rule * len(rules))()
     keep = []
     for slot, rule in zip(array, rules):
+        if rule.get("relation"):
+            slot.relation = int(rule["relation"])
+            slot.lower_offset = rule["lower_offset"]
+            continue
         keep.append((rule["ptr"], rule["idx"]))
         slot.ptr = rule["ptr"].ctypes.data
         slot.idx = rule["idx"].ctypes.data
@@ -261,26 +286,33 @@ def lookup_positions(ptr, idx):
 
 def literal_extract_dag(rule, n, execution_mode="sync_free",
                         edge_multiplicity=False):
-    """The generated ``extract_dag`` for one segment rule, statement by
-    statement (compiler/dag_codegen.py:1164-1196, 1484-1505)."""
-    ptr, idx = rule["ptr"].tolist(), rule["idx"].tolist()
+    """The generated ``extract_dag`` for one rule, or a list of rules,
+    statement by statement (compiler/dag_codegen.py:1164-1196, 1484-1505)."""
     successors = [set() for _ in range(n)]
     edge_count = [0 for _ in range(n)]
-    for seg in range(0, n):
-        for p in range(ptr[seg] + rule["lower_offset"],
-                       ptr[seg + 1] + rule["upper_offset"]):
-            if rule["break_at_owner"] and idx[p] >= seg:
-                break
-            if rule["owner_is_source"]:
-                source, destination = seg, idx[p]
-            else:
-                source, destination = idx[p], seg
-            if rule["guard"] == GUARD_GREATER and not destination > source:
-                continue
-            if rule["guard"] == GUARD_NOT_EQUAL and source == destination:
-                continue
-            successors[source].add(destination)
-            edge_count[destination] += 1
+    for rule in (rule if isinstance(rule, (list, tuple)) else [rule]):
+        if rule.get("relation"):
+            for seg in range(0, n):
+                for later in range(seg + rule["lower_offset"], n):
+                    successors[seg].add(later)
+                    edge_count[later] += 1
+            continue
+        ptr, idx = rule["ptr"].tolist(), rule["idx"].tolist()
+        for seg in range(0, n):
+            for p in range(ptr[seg] + rule["lower_offset"],
+                           ptr[seg + 1] + rule["upper_offset"]):
+                if rule["break_at_owner"] and idx[p] >= seg:
+                    break
+                if rule["owner_is_source"]:
+                    source, destination = seg, idx[p]
+                else:
+                    source, destination = idx[p], seg
+                if rule["guard"] == GUARD_GREATER and not destination > source:
+                    continue
+                if rule["guard"] == GUARD_NOT_EQUAL and source == destination:
+                    continue
+                successors[source].add(destination)
+                edge_count[destination] += 1
     dep_count = [0 for _ in range(n)]
     for neighbours in successors:
         for destination in neighbours:

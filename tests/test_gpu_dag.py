@@ -6,7 +6,7 @@ import os
 import numpy as np
 import pytest
 
-from lcd_amd import workloads
+from lcd_amd import hip_runtime, workloads
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden",
@@ -114,9 +114,12 @@ def test_golden_vectors(device, oracle):
     with open(GOLDEN) as handle:
         golden = json.load(handle)
     for case in golden["dag_cases"]:
-        maker = getattr(oracle, "rule_" + case["rule"])
-        rule = maker(case["ptr"], case["idx"])
-        dag = device.dag_build([rule], case["n"], levels=True)
+        if case["rule"] == "ilu0_csc":
+            rules = oracle.rules_ilu0_csc(case["ptr"], case["idx"])
+        else:
+            rules = [getattr(oracle, "rule_" + case["rule"])(case["ptr"],
+                                                             case["idx"])]
+        dag = device.dag_build(rules, case["n"], levels=True)
         assert dag.successors() == case["dag"], case["name"]
         assert dag.host("dep_count").tolist() == case["dep_count"], case["name"]
         if "dag_ptr" in case:
@@ -124,6 +127,34 @@ def test_golden_vectors(device, oracle):
             assert dag.host("dag_index").tolist() == case["dag_index"]
         if "wavefronts" in case:
             assert dag.wavefront_list() == case["wavefronts"], case["name"]
+
+
+@pytest.mark.parametrize("n,offset", [(1, 1), (2, 1), (67, 1), (300, 1),
+                                      (300, 7), (5, 9)])
+def test_relational_rule(device, oracle, n, offset):
+    """``seg -> every j >= seg + offset`` beside a segment rule (the two
+    rules of CSC ILU0), against the oracle's enumeration."""
+    print("relational rule", n, offset, flush=True)
+    work = workloads.configuration("c3", n=n, seed=n + offset)
+    rules = [oracle.make_rule(work.indptr, work.indices, False,
+                              upper_offset=-1),
+             oracle.rule_later(offset)]
+    expected = oracle.dag_build(rules, n)
+    for force_kahn in (False, True):
+        dag = device.dag_build(rules, n, levels=True, force_kahn=force_kahn)
+        for name in ("dag_ptr", "dag_index", "dep_count", "edge_count",
+                     "level_of", "wavefronts", "wavefront_ptr"):
+            np.testing.assert_array_equal(dag.host(name),
+                                          getattr(expected, name), name)
+        assert dag.topological_ids
+    if offset == 1:
+        assert dag.levels == n and dag.edges == n * (n - 1) // 2
+    with pytest.raises(hip_runtime.HIPRuntimeError):
+        device.dag_build(rules, n, incoming=True)
+    with pytest.raises(hip_runtime.HIPRuntimeError):
+        device.dag_build([dict(relation=1, lower_offset=0)], n)
+    with pytest.raises(hip_runtime.HIPRuntimeError):
+        device.dag_build([oracle.rule_later(1)], 70000)
 
 
 def test_incoming_positions(device, oracle):

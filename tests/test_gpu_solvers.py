@@ -258,6 +258,43 @@ def test_ilu0_csr_variants(oracle, options):
     assert "for (diag_ptr" not in factor.hip_kernel_source
 
 
+@pytest.mark.parametrize("mode", ["wavefront", "sync_free", None])
+def test_ilu0_csc_matches_the_sequential_loop(oracle, mode):
+    """compiler/e2e_tests/test_spilu0_e2e.py:107-121: the column form, every
+    column after all earlier ones, one thread per column; the operation
+    order is the sequential loop's, so the factor is bit-identical."""
+    from scipy.sparse import csc_matrix, csr_matrix
+    print("ilu0 csc", mode, flush=True)
+    rng = np.random.default_rng(21)
+    n = 150
+    pattern = (rng.random((n, n)) < 5.0 / n) | np.eye(n, dtype=bool)
+    a = np.where(pattern, rng.uniform(-1, 1, (n, n)), 0.0) + 8 * np.eye(n)
+    a[40, 40] = 0.0                      # a pivot that stays zero is skipped
+    a[:40, 40] = a[40, :40] = 0.0
+    matrix = csc_matrix(a)
+    matrix.sort_indices()
+    indptr = matrix.indptr.astype(np.int32)
+    indices = matrix.indices.astype(np.int32)
+    factor = spilu0.compile_ilu0_csc(execution_mode=mode)
+    expected = oracle.ilu0_csc(matrix.data, indices, indptr)
+    original = matrix.data.copy()
+    result = factor(matrix.data.copy(), indices, indptr)
+    np.testing.assert_array_equal(matrix.data, original)
+    np.testing.assert_array_equal(result, expected)
+    dag, _ = factor.build_dag(matrix.data, indices, indptr)
+    assert dag == [list(range(k + 1, n)) for k in range(n)]
+    # the row form of the same matrix gives the same incomplete factor
+    by_row = csr_matrix(matrix)
+    by_row.sort_indices()
+    row_factor = spilu0.compile_ilu0_csr(execution_mode="wavefront")(
+        by_row.data.copy(), by_row.indices.astype(np.int32),
+        by_row.indptr.astype(np.int32))
+    np.testing.assert_allclose(
+        csc_matrix((result, indices, indptr), shape=a.shape).toarray(),
+        csr_matrix((row_factor, by_row.indices, by_row.indptr),
+                   shape=a.shape).toarray(), rtol=1e-12, atol=1e-14)
+
+
 def test_ilu0_dense_pattern_is_lu(oracle):
     """On a dense pattern ILU0 is LU without pivoting."""
     rng = np.random.default_rng(5)

@@ -337,6 +337,18 @@ def test_lookup_plan_and_rewrite():
     assert "if diag_ptr >= 0:" in rewritten
     assert "for kj_ptr in range" in rewritten          # not a self lookup
     assert create_structural_lookup_plan(module, {}) == ()
+    # the column form bounds its search by aliases of the pointer array
+    # (compiler/transform_tests/test_structural_lookups.py:40-63)
+    module = demo_source("spilu0", "ilu0_csc")
+    plan = create_structural_lookup_plan(module, ILU_PROPS)
+    assert len(plan) == 1
+    assert (plan[0].pointer_array, plan[0].index_array) == (
+        "A_indptr", "A_indices")
+    rewritten = ast.unparse(rewrite_structural_lookups(module, plan, ILU_PROPS))
+    assert "_lcd_lookup_position_0[" in rewritten
+    assert "diag_val = A_data[" in rewritten
+    assert "for dptr in range" not in rewritten
+    assert "for kj_ptr in range" in rewritten and "for ij_ptr in range" in rewritten
 
 
 # ------------------------------------------------- dependence analysis
@@ -363,6 +375,40 @@ def test_edge_rules_of_the_supported_loops():
                                  CSC_PROPS)
         assert gs.ordering_dependences == [SegmentRule(
             "Ap", "Ai", False, 0, 0, 1, False, "i", "j", "x")]
+
+
+def test_column_ilu0_gets_the_push_rule_and_the_relational_rule():
+    """compiler/transform_tests/test_spilu0_codegen.py:146-167."""
+    from lcd_amd.dependence import LaterRule
+    analysis = analyze_dependences(demo_source("spilu0", "ilu0_csc"), "k",
+                                   ILU_PROPS)
+    assert analysis.ordering_dependences == [
+        SegmentRule("A_indptr", "A_indices", True, 0, 0, 1, False, "k",
+                    "i_ptr", "A_data"),
+        LaterRule(1, "k", "j", "A_data")]
+    assert not analysis.reductions
+    plan = create_dag_plan(analysis.ordering_dependences, None, "k",
+                           ["A_data", "A_indices", "A_indptr", "n"])
+    source = generate_dag_source(plan)
+    assert len(plan.edge_rules) == 2
+    assert "_dag_destination_0 = A_indices[i_ptr]" in source
+    assert "for j in range(k + 1, n):" in source
+    assert "_dag_destination_1 = j" in source
+    for absent in ("ij_ptr", "for dptr", "kj_ptr", "k1", "k2"):
+        assert absent not in source
+    assert direct_dependence(plan, "j") is None
+    namespace = {}
+    exec(compile(source, "<dag>", "exec"), namespace)
+    case = next(c for c in GOLDEN["dag_cases"]
+                if c["name"] == "ilu0_csc_dense_3x3")
+    dag, dep_count = namespace["extract_dag"]([1.0] * 9, case["idx"],
+                                              case["ptr"], 3)
+    assert dag == case["dag"] and dep_count == case["dep_count"]
+    # a later-range loop that stops short of the task count is not that rule
+    module = ast.parse(ast.unparse(demo_source("spilu0", "ilu0_csc")).replace(
+        "range(k + 1, n)", "range(k + 1, n - 1)"))
+    with pytest.raises(DependenceAnalysisError):
+        analyze_dependences(module, "k", ILU_PROPS)
 
 
 def test_generated_inspector_text_matches_the_reference_shape():
@@ -616,6 +662,24 @@ def test_ilu0_nested_mapping_lookup_and_binary_search():
                       structural_lookups=plan, segment_cache=False)
         assert "_lcd_seg" not in plain.kernel_source
         hip_runtime.compile_code(result.source)
+
+
+def test_column_ilu0_lowers_to_one_thread_per_column():
+    """compiler/transform_tests/test_spilu0_codegen.py:176-213 (csc)."""
+    from lcd_amd.demo import spilu0
+    for mode in ("wavefront", "sync_free"):
+        compiled = spilu0.compile_ilu0_csc(execution_mode=mode)
+        assert len(compiled.structural_lookups) == 1
+        name = compiled.structural_lookups[0].name
+        kernel = compiled.hip_kernel_source
+        assert name in kernel and name in compiled.hip_launcher_source
+        assert "for (dptr" not in kernel
+        assert "#define LCD_TASK_LANES 1" in compiled.hip_source
+        assert kernel.count("lcd_sorted_find(A_indices, j_start, j_end") == 2
+        assert "for (j = (k + 1); j < n; ++j)" in kernel
+        assert compiled.current_schedule.dependence_protocol == "counter"
+        assert "(&A_data" not in kernel.replace("lcd_ld(&A_data", "").replace(
+            "lcd_st(&A_data", "")        # no atomic update of the factor
 
 
 def test_lowering_errors():

@@ -27,8 +27,12 @@ def golden():
 
 def test_reference_dag_vectors(golden):
     for case in golden["dag_cases"]:
-        rule = getattr(O, "rule_" + case["rule"])(case["ptr"], case["idx"])
-        dag = O.dag_build([rule], case["n"])
+        if case["rule"] == "ilu0_csc":       # two rules, one relational
+            rules = O.rules_ilu0_csc(case["ptr"], case["idx"])
+        else:
+            rules = [getattr(O, "rule_" + case["rule"])(case["ptr"],
+                                                        case["idx"])]
+        dag = O.dag_build(rules, case["n"])
         assert dag.successors() == case["dag"], case["name"]
         assert dag.dep_count.tolist() == case["dep_count"], case["name"]
         if "dag_ptr" in case:
@@ -239,6 +243,51 @@ def test_ilu0_against_dense_lu_and_pattern_identity():
         pivots.append(4.0 - 1.0 / pivots[-1])
     diag = csr_matrix((out, tri.indices, tri.indptr), shape=(n, n)).diagonal()
     np.testing.assert_allclose(diag, pivots, rtol=1e-14)
+
+
+def test_ilu0_csc_against_dense_lu_row_form_and_inspector():
+    from scipy.sparse import csc_matrix, csr_matrix
+    # dense pattern: ILU0 is LU without pivoting, whatever the storage
+    rng = np.random.default_rng(12)
+    n = 17
+    dense = rng.uniform(-1, 1, (n, n)) + n * np.eye(n)
+    indptr = np.arange(0, n * n + 1, n, dtype=np.int32)
+    indices = np.tile(np.arange(n, dtype=np.int32), n)
+    factors = O.ilu0_csc(dense.T.ravel(), indices, indptr).reshape(n, n).T
+    doolittle = dense.copy()
+    for k in range(n):
+        doolittle[k + 1:, k] /= doolittle[k, k]
+        doolittle[k + 1:, k + 1:] -= np.outer(doolittle[k + 1:, k],
+                                              doolittle[k, k + 1:])
+    np.testing.assert_allclose(factors, doolittle, rtol=1e-12, atol=1e-13)
+    # sparse, unsymmetric pattern: the column form and the row form compute
+    # the same incomplete factor (different operation order, so a tolerance)
+    pattern = (rng.random((40, 40)) < 0.15) | np.eye(40, dtype=bool)
+    a = np.where(pattern, rng.uniform(-1, 1, (40, 40)), 0.0) + 8 * np.eye(40)
+    by_column, by_row = csc_matrix(a), csr_matrix(a)
+    by_column.sort_indices(), by_row.sort_indices()
+    column_factor = csc_matrix(
+        (O.ilu0_csc(by_column.data, by_column.indices, by_column.indptr),
+         by_column.indices, by_column.indptr), shape=a.shape).toarray()
+    row_factor = csr_matrix(
+        (O.ilu0_csr(by_row.data, by_row.indices, by_row.indptr),
+         by_row.indices, by_row.indptr), shape=a.shape).toarray()
+    np.testing.assert_allclose(column_factor, row_factor, rtol=1e-12,
+                               atol=1e-14)
+    assert np.array_equal(column_factor != 0, a != 0)
+    # zero pivot: the column is left unscaled and pushes no update
+    singular = np.array([[0.0, 1.0], [2.0, 3.0]])
+    ptr, idx = np.array([0, 2, 4], np.int32), np.array([0, 1, 0, 1], np.int32)
+    np.testing.assert_array_equal(
+        O.ilu0_csc(singular.T.ravel(), idx, ptr), singular.T.ravel())
+    # inspector: both rules against the literal set-based enumeration
+    rules = O.rules_ilu0_csc(by_column.indptr, by_column.indices)
+    dag = O.dag_build(rules, 40)
+    successors, dep_count = O.literal_extract_dag(rules, 40)
+    assert dag.successors() == successors
+    assert dag.successors() == [list(range(k + 1, 40)) for k in range(40)]
+    assert dag.dep_count.tolist() == dep_count == list(range(40))
+    assert dag.levels == 40
 
 
 def test_band_chains_against_literal():
