@@ -146,3 +146,40 @@ def test_ilu0_demo_on_a_matrix_market_file(tmp_path):
                                         verbose=False)
         assert factor.shape == (M.load_matrix_market(path, 0).nnz,)
         assert error <= 1e-12
+
+
+def test_matrix_list_orders_by_declared_entry_count(tmp_path):
+    from lcd_amd.demo import matrix_bench
+    sizes = {"big.mtx": (60, 0.2), "small.mtx": (30, 0.05), "mid.mtx": (50, 0.1)}
+    for seed, (name, (n, density)) in enumerate(sizes.items()):
+        scipy.io.mmwrite(str(tmp_path / name), random_sparse(n, density, seed),
+                         comment="generated")
+    (tmp_path / "list.txt").write_text("big.mtx\nsmall.mtx\n\nmid.mtx\n")
+    ordered = matrix_bench.matrix_list(tmp_path / "list.txt", str(tmp_path))
+    assert [p.split("/")[-1] for p in ordered] == [
+        "small.mtx", "mid.mtx", "big.mtx"]
+
+
+@pytest.mark.gpu
+def test_matrix_list_benchmark(tmp_path):
+    """The list driver: every kernel on every listed matrix, results checked
+    against the manufactured solution / the exact-ILU0 pattern identity."""
+    import io
+    from lcd_amd.demo import matrix_bench
+    for seed, n in enumerate((400, 150)):
+        scipy.io.mmwrite(str(tmp_path / f"m{n}.mtx"),
+                         random_sparse(n, 0.02, 30 + seed, symmetric=True),
+                         symmetry="symmetric")
+    (tmp_path / "list.txt").write_text("m400.mtx\nm150.mtx\n")
+    out = io.StringIO()
+    rows = matrix_bench.run(tmp_path / "list.txt", str(tmp_path), warmup=1,
+                            repeats=3, out=out)
+    assert [row["matrix"] for row in rows] == ["m150.mtx"] * 3 + ["m400.mtx"] * 3
+    assert [row["kernel"] for row in rows[:3]] == list(matrix_bench.KERNELS)
+    for row in rows:
+        assert row["max_abs_error"] <= 1e-11, row
+        assert row["median_ms"] > 0 and row["levels"] >= 1
+        assert row["p20_ms"] <= row["median_ms"] <= row["p80_ms"]
+    lines = out.getvalue().strip().splitlines()
+    assert lines[0].split(",") == list(matrix_bench.COLUMNS)
+    assert len(lines) == 7
