@@ -241,7 +241,11 @@ typedef struct {
 #define LCDHIP_DAG_BAND_PTR 13      /* bands + 1: first chain of every band */
 /* After lcdhip_dag_tile_order: */
 #define LCDHIP_DAG_TILE_NODES 14    /* n: nodes by (id / tile_rows, level, id) */
-#define LCDHIP_DAG_ARRAYS 15
+/* After lcdhip_dag_task_records (q = position in the task order): */
+#define LCDHIP_DAG_REC_IN 15        /* 2 n: in_ptr[v], in_ptr[v + 1] of task q */
+#define LCDHIP_DAG_REC_SRC 16       /* n * lanes: in_src of its first edges */
+#define LCDHIP_DAG_REC_POS 17       /* n * lanes: in_pos of its first edges */
+#define LCDHIP_DAG_ARRAYS 18
 
 int lcdhip_dag_build(const lcdhip_dag_rule *rules, int rule_count, int64_t n,
                      uint32_t flags, lcdhip_stream stream, lcdhip_dag **out);
@@ -268,6 +272,19 @@ int lcdhip_dag_tile_order(lcdhip_dag *dag, int64_t tile_rows,
  * counterpart in the reference.) */
 int lcdhip_dag_tile_locality(const lcdhip_dag *dag, int64_t tile_rows,
                              lcdhip_stream stream, int64_t *local_edges_out);
+/* Fixed-size records of the incoming listing in the order the persistent
+ * executor visits the tasks (TILE_NODES when lcdhip_dag_tile_order ran, else
+ * WAVEFRONTS): for the task at position q, REC_IN holds its range of the
+ * incoming listing and REC_SRC / REC_POS[q * lanes + l] the source and the
+ * position of its l-th incoming edge (0 beyond its in-degree).  A wavefront
+ * then fetches everything its tasks need to start polling with loads whose
+ * addresses depend on q alone.  *overflow_tasks_out (may be NULL) receives
+ * the number of tasks with more than `lanes` incoming edges, whose further
+ * edges stay in the incoming listing only.  Needs LCDHIP_DAG_INCOMING and
+ * LCDHIP_DAG_LEVELS; lanes in [1, 64].  (Layout of this backend's executor;
+ * no counterpart in the reference.) */
+int lcdhip_dag_task_records(lcdhip_dag *dag, int lanes, lcdhip_stream stream,
+                            int64_t *overflow_tasks_out);
 int lcdhip_dag_get_info(const lcdhip_dag *dag, lcdhip_dag_info *out);
 int lcdhip_dag_array(const lcdhip_dag *dag, int which, void **d_out,
                      int64_t *count_out);

@@ -1128,6 +1128,98 @@ extern "C" int lcdhip_dag_tile_order(lcdhip_dag *dag, int64_t tile_rows,
     return LCDHIP_OK;
 }
 
+namespace {
+
+__global__ void task_records_kernel(const int32_t *__restrict__ order,
+                                    const int32_t *__restrict__ in_ptr,
+                                    const int32_t *__restrict__ in_src,
+                                    const int32_t *__restrict__ in_pos,
+                                    int64_t n, int lanes,
+                                    int32_t *__restrict__ rec_in,
+                                    int32_t *__restrict__ rec_src,
+                                    int32_t *__restrict__ rec_pos,
+                                    unsigned long long *__restrict__ overflow)
+{
+    int64_t slot = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (slot >= n * lanes)
+        return;
+    const int64_t q = slot / lanes;
+    const int lane = static_cast<int>(slot - q * lanes);
+    const int32_t node = order[q];
+    const int32_t begin = in_ptr[node], end = in_ptr[node + 1];
+    if (lane == 0) {
+        rec_in[2 * q] = begin;
+        rec_in[2 * q + 1] = end;
+        if (end - begin > lanes)
+            atomicAdd(overflow, 1ull);
+    }
+    const bool has = begin + lane < end;
+    rec_src[slot] = has ? in_src[begin + lane] : 0;
+    rec_pos[slot] = has ? in_pos[begin + lane] : 0;
+}
+
+}
+
+extern "C" int lcdhip_dag_task_records(lcdhip_dag *dag, int lanes,
+                                       lcdhip_stream stream_handle,
+                                       int64_t *overflow_tasks_out)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (!dag || lanes < 1 || lanes > 64) {
+        set_error("task records need a dag and 1 to 64 lanes per task");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    const int32_t *order = dag->arrays[LCDHIP_DAG_TILE_NODES]
+                               ? dag->arrays[LCDHIP_DAG_TILE_NODES]
+                               : dag->arrays[LCDHIP_DAG_WAVEFRONTS];
+    if (!order || dag->info.scheduled != dag->info.n ||
+        !dag->arrays[LCDHIP_DAG_IN_PTR]) {
+        set_error("task records need level sets that cover every node and "
+                  "the incoming listing");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    hipStream_t stream = resolve_stream(stream_handle);
+    const int64_t n = dag->info.n;
+    if (n * lanes >= (int64_t(1) << 31)) {
+        set_error("task records of %lld tasks x %d lanes exceed 2^31 entries",
+                  static_cast<long long>(n), lanes);
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    for (int which : {LCDHIP_DAG_REC_IN, LCDHIP_DAG_REC_SRC, LCDHIP_DAG_REC_POS})
+        if (dag->arrays[which]) {
+            (void)hipFree(dag->arrays[which]);
+            dag->arrays[which] = nullptr;
+        }
+    int status;
+    if ((status = dag_alloc(dag, LCDHIP_DAG_REC_IN, 2 * n))) return status;
+    if ((status = dag_alloc(dag, LCDHIP_DAG_REC_SRC, n * lanes))) return status;
+    if ((status = dag_alloc(dag, LCDHIP_DAG_REC_POS, n * lanes))) return status;
+    if (overflow_tasks_out)
+        *overflow_tasks_out = 0;
+    if (n == 0)
+        return LCDHIP_OK;
+    Scratch scratch;
+    unsigned long long *d_overflow = nullptr;
+    LCDHIP_CHECK(scratch.alloc(&d_overflow, 1));
+    LCDHIP_CHECK(hipMemsetAsync(d_overflow, 0, 8, stream));
+    hipLaunchKernelGGL(task_records_kernel, dim3(blocks_for(n * lanes)),
+                       dim3(kBlock), 0, stream, order,
+                       dag->arrays[LCDHIP_DAG_IN_PTR],
+                       dag->arrays[LCDHIP_DAG_IN_SRC],
+                       dag->arrays[LCDHIP_DAG_IN_POS], n, lanes,
+                       dag->arrays[LCDHIP_DAG_REC_IN],
+                       dag->arrays[LCDHIP_DAG_REC_SRC],
+                       dag->arrays[LCDHIP_DAG_REC_POS], d_overflow);
+    LCDHIP_CHECK(hipGetLastError());
+    unsigned long long overflow = 0;
+    LCDHIP_CHECK(hipMemcpyAsync(&overflow, d_overflow, 8, hipMemcpyDeviceToHost,
+                                stream));
+    LCDHIP_CHECK(hipStreamSynchronize(stream));
+    if (overflow_tasks_out)
+        *overflow_tasks_out = static_cast<int64_t>(overflow);
+    return LCDHIP_OK;
+}
+
 extern "C" int lcdhip_dag_get_info(const lcdhip_dag *dag, lcdhip_dag_info *out)
 {
     if (!dag || !out) {

@@ -253,7 +253,7 @@ def band_chains(nodes, level_ptr, dag_ptr, dag_index, band_width):
 
 def execution_data_from_device_dag(dag, execution_mode, warp_mapped,
                                    pushed=False, band_width=1, mailbox=False,
-                                   tile_rows=None):
+                                   tile_rows=None, record_lanes=None):
     """Executor arrays straight from the on-device inspector (no host copy
     except the level offsets the launcher iterates over)."""
     if not isinstance(band_width, int) or band_width <= 0:
@@ -293,6 +293,12 @@ def execution_data_from_device_dag(dag, execution_mode, warp_mapped,
                      "_lcd_in_pos": dag.array("in_pos"),
                      "_lcd_in_src": dag.array("in_src"),
                      "_lcd_out_slot": dag.array("out_slot")}
+        if record_lanes:
+            # the first `record_lanes` incoming edges of every task, in the
+            # order the executor visits the tasks
+            records = dag.task_records(int(record_lanes))
+            auxiliary.update(zip(
+                ("_lcd_rec_in", "_lcd_rec_src", "_lcd_rec_pos"), records))
         return WarpTaskExecutionData(
             task_nodes=task_nodes, task_ptr=None,
             band_ptr=dag.host("wavefront_ptr"), dep_count=counts,

@@ -175,8 +175,8 @@ def parallel(**kwargs):
             raise ValueError(
                 "tile_rows must be None, 'auto' or a positive integer.")
 
-        def lower_variant(lowering_key, tile_rows=None):
-            variant_key = (lowering_key, tile_rows)
+        def lower_variant(lowering_key, tile_rows=None, single_chunk=False):
+            variant_key = (lowering_key, tile_rows, single_chunk)
             if variant_key not in lowered_variants:
                 (mode, threads_per_block, unroll, n_warp, protocol,
                  task_lanes) = lowering_key
@@ -206,12 +206,14 @@ def parallel(**kwargs):
                     gather_messages=kwargs.get("gather_messages", True),
                     segment_cache=kwargs.get("segment_cache", True),
                     tile_rows=tile_rows if mode == SYNC_FREE else None,
+                    task_records=kwargs.get("task_records", True),
+                    single_chunk=single_chunk,
                 )
             return lowered_variants[variant_key]
 
-        def compile_variant(lowering_key, tile_rows=None):
-            lowering = lower_variant(lowering_key, tile_rows)
-            variant_key = (lowering_key, tile_rows)
+        def compile_variant(lowering_key, tile_rows=None, single_chunk=False):
+            lowering = lower_variant(lowering_key, tile_rows, single_chunk)
+            variant_key = (lowering_key, tile_rows, single_chunk)
             if variant_key not in compiled_variants:
                 compiled_variants[variant_key] = compile_hip_module(
                     lowering, function_globals=function.__globals__)
@@ -381,12 +383,17 @@ def parallel(**kwargs):
                 pushed=lowering.dependence_protocol == PUSH_DEPENDENCE,
                 band_width=band_width,
                 mailbox=lowering.dependence_protocol == MAILBOX_DEPENDENCE,
-                tile_rows=lowering.tile_rows)
+                tile_rows=lowering.tile_rows,
+                record_lanes=lowering.task_record_lanes)
             plan = SchedulePlan(
                 schedule=schedule,
                 execution_data=attach_auxiliary_values(
                     execution_data, lookup_values),
-                features=features, dag=dag, tile_rows=tile_rows)
+                features=features, dag=dag, tile_rows=tile_rows,
+                # every task's incoming edges fit its record: the executor
+                # variant without the code for further chunks
+                single_chunk=bool(lowering.task_record_lanes)
+                and getattr(dag, "record_overflow", 1) == 0)
             plan_state[id(plan)] = {"resident": resident, "workspace": {}}
             return plan
 
@@ -426,7 +433,8 @@ def parallel(**kwargs):
             argument_values = bind_arguments(args, call_kwargs)
             plan = plan_for(argument_values)
             lowering, compiled = compile_variant(plan.schedule.lowering_key,
-                                                 plan.tile_rows)
+                                                 plan.tile_rows,
+                                                 plan.single_chunk)
             publish_variant(plan.schedule, lowering, compiled)
             state = plan_state[id(plan)]
             values = dict(argument_values)

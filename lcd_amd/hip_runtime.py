@@ -37,6 +37,7 @@ DAG_PTR, DAG_INDEX, DAG_DEP_COUNT, DAG_EDGE_COUNT = 0, 1, 2, 3
 DAG_LEVEL_OF, DAG_WAVEFRONTS, DAG_WAVEFRONT_PTR = 4, 5, 6
 DAG_IN_PTR, DAG_IN_POS, DAG_OUT_SLOT, DAG_IN_SRC = 7, 8, 9, 10
 DAG_TASK_NODES, DAG_TASK_PTR, DAG_BAND_PTR, DAG_TILE_NODES = 11, 12, 13, 14
+DAG_REC_IN, DAG_REC_SRC, DAG_REC_POS = 15, 16, 17
 DAG_FLAG_LEVELS, DAG_FLAG_FORCE_KAHN, DAG_FLAG_INCOMING = 1, 2, 4
 
 DEVICE_COMPILE_OPTIONS = (
@@ -128,6 +129,7 @@ EXPORTED_SYMBOLS = (
     "lcdhip_dag_build", "lcdhip_dag_get_info", "lcdhip_dag_array",
     "lcdhip_dag_download", "lcdhip_dag_destroy", "lcdhip_dag_band_chains",
     "lcdhip_dag_tile_order", "lcdhip_dag_tile_locality",
+    "lcdhip_dag_task_records",
     "lcdhip_lookup_build",
     "lcdhip_digest",
 )
@@ -318,7 +320,8 @@ class DeviceDag:
               "in_pos": DAG_IN_POS, "out_slot": DAG_OUT_SLOT,
               "in_src": DAG_IN_SRC, "task_nodes": DAG_TASK_NODES,
               "task_ptr": DAG_TASK_PTR, "band_ptr": DAG_BAND_PTR,
-              "tile_nodes": DAG_TILE_NODES}
+              "tile_nodes": DAG_TILE_NODES, "rec_in": DAG_REC_IN,
+              "rec_src": DAG_REC_SRC, "rec_pos": DAG_REC_POS}
     CHAIN_ARRAYS = ("task_nodes", "task_ptr", "band_ptr")
 
     def __init__(self, device, handle):
@@ -396,6 +399,27 @@ class DeviceDag:
             self.handle, ctypes.c_int64(tile_rows), self.device.stream))
         self.tile_rows = tile_rows
         return self.array("tile_nodes")
+
+    def task_records(self, lanes):
+        """Fixed-size records of the incoming listing in task order
+        (``tile_nodes`` when tiles were ordered, else ``wavefronts``):
+        afterwards ``rec_in`` (2 per task), ``rec_src`` and ``rec_pos``
+        (``lanes`` per task) are arrays of this DAG."""
+        if not isinstance(lanes, int) or not 1 <= lanes <= 64:
+            raise HIPRuntimeError(
+                "Task records need 1 to 64 lanes per task.", ERR_ARGUMENT)
+        for name in ("rec_in", "rec_src", "rec_pos"):
+            self._views.pop(name, None)
+            self._host.pop(name, None)
+        overflow = ctypes.c_int64()
+        _check(load_library().lcdhip_dag_task_records(
+            self.handle, ctypes.c_int(lanes), self.device.stream,
+            ctypes.byref(overflow)))
+        self.record_lanes = lanes
+        # tasks whose incoming edges do not all fit their record
+        self.record_overflow = int(overflow.value)
+        return tuple(self.array(name)
+                     for name in ("rec_in", "rec_src", "rec_pos"))
 
     def successors(self):
         ptr, index = self.host("dag_ptr"), self.host("dag_index")

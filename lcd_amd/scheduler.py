@@ -155,6 +155,7 @@ class SchedulePlan:
     features: WorkloadFeatures | None = None
     dag: object = None
     tile_rows: int | None = None     # tiled persistent executor, or None
+    single_chunk: bool = False       # no task has more in-edges than lanes
 
 
 # Tiled executor, automatic choice: tiles of 4096 consecutive block-iterator

@@ -157,6 +157,39 @@ def test_relational_rule(device, oracle, n, offset):
         device.dag_build([oracle.rule_later(1)], 70000)
 
 
+@pytest.mark.parametrize("lanes,tile_rows", [(4, 512), (2, 100), (8, None)])
+def test_task_records(device, oracle, lanes, tile_rows):
+    """Fixed-size records of the incoming listing in executor order."""
+    print("task records", lanes, tile_rows, flush=True)
+    work = workloads.configuration("c2", nx=12, ny=10, nz=9)
+    rule = oracle.rule_sptrsv_csc(work.indptr, work.indices)
+    dag = device.dag_build([rule], work.n, levels=True, incoming=True)
+    if tile_rows:
+        dag.tile_order(tile_rows)
+    rec_in, rec_src, rec_pos = (a.copy_to_host()
+                                for a in dag.task_records(lanes))
+    order = dag.host("tile_nodes" if tile_rows else "wavefronts")
+    in_ptr, in_src, in_pos = (dag.host(name)
+                              for name in ("in_ptr", "in_src", "in_pos"))
+    np.testing.assert_array_equal(rec_in.reshape(-1, 2)[:, 0], in_ptr[order])
+    np.testing.assert_array_equal(rec_in.reshape(-1, 2)[:, 1],
+                                  in_ptr[order + 1])
+    expected_src = np.zeros((work.n, lanes), dtype=np.int32)
+    expected_pos = np.zeros((work.n, lanes), dtype=np.int32)
+    for q, node in enumerate(order):
+        count = min(in_ptr[node + 1] - in_ptr[node], lanes)
+        expected_src[q, :count] = in_src[in_ptr[node]:in_ptr[node] + count]
+        expected_pos[q, :count] = in_pos[in_ptr[node]:in_ptr[node] + count]
+    np.testing.assert_array_equal(rec_src.reshape(-1, lanes), expected_src)
+    np.testing.assert_array_equal(rec_pos.reshape(-1, lanes), expected_pos)
+    assert dag.record_overflow == int(np.sum(np.diff(in_ptr) > lanes))
+    with pytest.raises(hip_runtime.HIPRuntimeError):
+        dag.task_records(0)
+    plain = device.dag_build([rule], work.n, levels=True)
+    with pytest.raises(hip_runtime.HIPRuntimeError):
+        plain.task_records(lanes)          # no incoming listing
+
+
 def test_incoming_positions(device, oracle):
     """Per destination, the positions whose entries produce its edges, by
     (source, position), duplicates kept."""

@@ -96,7 +96,8 @@ def test_sptrsv_csc_variants(oracle, options):
 
 
 @pytest.mark.parametrize("tile_rows,lanes,tpb", [(64, 4, 64), (500, 8, 128),
-                                                 (4096, 4, 256), (8192, 16, 512)])
+                                                 (4096, 4, 256), (8192, 16, 512),
+                                                 (256, 2, 128)])
 def test_tiled_executor(oracle, tile_rows, lanes, tpb):
     """Workgroup-resident tiles: hand-offs inside a tile go through LDS,
     across tiles through memory; CSR pull and the gathered CSC mailbox."""
@@ -112,6 +113,10 @@ def test_tiled_executor(oracle, tile_rows, lanes, tpb):
     assert csc.hip_lowering.tile_rows == tile_rows
     assert "lcd_tile_ld(x, _lcd_tile" in csr.hip_kernel_source
     assert "lcd_tile_st(x, _lcd_tile" in csc.hip_kernel_source
+    # the first `lanes` incoming edges of a task come from its record
+    assert csc.hip_lowering.task_record_lanes == lanes
+    assert "_lcd_rec_src[" in csc.hip_kernel_source
+    assert csc.hip_lowering.stage_kernel_name is None
     for name, overrides in (("c1", {}), ("c2", dict(nx=20, ny=18, nz=16)),
                             ("c5", dict(n=6000))):
         work = workloads.configuration(name, **overrides)
@@ -119,6 +124,14 @@ def test_tiled_executor(oracle, tile_rows, lanes, tpb):
                                      work.rhs, work.n)
         # the gathered mailbox adds in the order of the sequential loop
         solve_and_check(csc, work, expected, exact=True)
+        # in-degrees: 2 (c1), 3 (c2), 8 (c5); the executor variant without
+        # the code for a second chunk runs exactly when they fit the record
+        in_degree = {"c1": 2, "c2": 3, "c5": 8}[name]
+        plan = csc.schedule_plan(work.indptr, work.indices, work.data,
+                                 work.rhs, work.n)
+        assert plan.single_chunk == (in_degree <= lanes)
+        assert ("_lcd_in_src[_mb_next + _lane]" in csc.hip_kernel_source) == (
+            in_degree > lanes)
     work = workloads.configuration("c3", n=20000)
     expected = oracle.sptrsv_csr(work.indptr, work.indices, work.data,
                                  work.rhs, work.n)

@@ -84,7 +84,8 @@ def test_unsatisfiable_wait_trips_the_watchdog(oracle, name, props, protocol,
                            incoming=protocol == "mailbox")
     good = P.execution_data_from_device_dag(
         dag, "sync_free", True, pushed=protocol == "push",
-        mailbox=protocol == "mailbox", tile_rows=lowering.tile_rows)
+        mailbox=protocol == "mailbox", tile_rows=lowering.tile_rows,
+        record_lanes=lowering.task_record_lanes)
     assert lowering.tile_rows == extra.get("tile_rows")
     # node 0 (level 0) never runs; the last node of the last level runs twice
     order = "tile_nodes" if lowering.tile_rows else "wavefronts"
