@@ -53,7 +53,7 @@ TUNED = {
 # profiled reports null.
 MEASURED_TRAFFIC = {
     ("c2", "sync_free", "push", 4): 1_937_433_319,
-    ("c2", "sync_free", "mailbox", 4): 473_026_150,
+    ("c2", "sync_free", "mailbox", 4): 531_082_379,
     ("c3", "sync_free", "pull", 64): 1_529_588_218,
 }
 

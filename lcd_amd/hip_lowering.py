@@ -2781,7 +2781,7 @@ class HIPLowerer:
             lines.append(f"{pad}unsigned _g_off = 0; bool _g_in = false;")
         if records:
             # one guarded block, so the loads leave back to back
-            slot = "(long long)_task * LCD_TASK_LANES + _lane"
+            slot = "_task * LCD_TASK_LANES + _lane"   # < 2^31 entries
             lines.append(
                 f"{pad}if (_pending) {{ {self.loop_iterator} = "
                 "(lcd_index_t)task_nodes[_task]; "
@@ -2790,6 +2790,14 @@ class HIPLowerer:
                 f"_g_pos = _lcd_rec_pos[{slot}]; "
                 f"_g_src = _lcd_rec_src[{slot}]; {decode}}}")
             lines.append(f"{pad}{head} {{ {loads} }}")
+            if self.single_chunk:
+                lines += [
+                    f"{pad}const int _mb_have = (_mb_end - _mb_next) < "
+                    "LCD_TASK_LANES ? (_mb_end - _mb_next) : LCD_TASK_LANES;",
+                    f"{pad}bool _need = _pending && _lane < _mb_have;",
+                    # more incoming edges than lanes: never ready (watchdog)
+                    f"{pad}const bool _fits = (_mb_end - _mb_next) <= "
+                    "LCD_TASK_LANES;"]
             return lines
         position = ("_g_pos = _lcd_in_pos[_mb_next + _lane]; "
                     if gather["needs_position"] else "")
@@ -2838,6 +2846,29 @@ class HIPLowerer:
                 f"{pad}            const double _mb_in = __shfl(_mb_value, _mb_k, LCD_TASK_LANES);",
                 f"{pad}            if (_mb_k < _mb_have) {own} = {own} + _mb_in;",
                 f"{pad}        }}"]
+        if tiled and self.single_chunk and gather.get("records"):
+            # one chunk per task: what each lane still waits for is a flag
+            # set when the task is fetched and cleared by its poll
+            return [
+                f"{pad}bool _ready = false;",
+                f"{pad}if (_need) {{",
+                f"{pad}    if (_g_in) {{ const double _g_raw = "
+                "__hip_atomic_load(&_lcd_tile[_g_off], __ATOMIC_RELAXED, "
+                "__HIP_MEMORY_SCOPE_WORKGROUP); "
+                "if (!lcd_is_empty(_g_raw)) { _mb_value = _g_raw; "
+                "_need = false; } }",
+                f"{pad}    else if ((_spins & LCD_EXTERNAL_POLL_MASK) == 0) "
+                f"{{ const double _g_raw = lcd_ld(&{array}[_g_src]); "
+                "if (!lcd_is_empty(_g_raw)) { _mb_value = _g_raw; "
+                "_need = false; } }",
+                f"{pad}}}",
+                f"{pad}if (_fits && lcd_group_none(_need)) {{",
+                f"{pad}    if (_lane < _mb_have) {{ const double _g_value = "
+                f"_mb_value; _mb_value = {value}; }}",
+                *[line[4:] for line in ordered],
+                f"{pad}    _ready = true;",
+                f"{pad}}}",
+            ]
         return [
             f"{pad}bool _ready = _mb_next == _mb_end;",
             f"{pad}if (!_ready) {{",

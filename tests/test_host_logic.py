@@ -616,6 +616,47 @@ def test_gathered_mailbox_drops_the_producer_loop():
     hip_runtime.compile_code(result.source)
 
 
+def test_tiled_mailbox_reads_task_records():
+    module = demo_source("sptrsv", "sptrsv_csc_loop")
+    options = dict(execution_mode="sync_free", thread_loop_iterator="j",
+                   task_lanes=4, wavefront_threads_per_block=128,
+                   dependence_protocol="mailbox", tile_rows=1024)
+    result = lower(module, **options)
+    kernel = result.kernel_source
+    assert result.tile_rows == 1024 and result.task_record_lanes == 4
+    # records addressed by the queue position; no per-launch staging
+    assert result.stage_kernel_name is None
+    assert "_lcd_staged_0" not in result.kernel_arguments
+    position = result.kernel_arguments.index("_lcd_in_src")
+    assert result.kernel_arguments[position + 1:position + 4] == [
+        "_lcd_rec_in", "_lcd_rec_src", "_lcd_rec_pos"]
+    assert "_mb_next = _lcd_rec_in[2 * _task];" in kernel
+    assert "_g_src = _lcd_rec_src[_task * LCD_TASK_LANES + _lane];" in kernel
+    assert "_g_operand_0 = Ax[_g_pos];" in kernel
+    assert "_lcd_in_ptr[i]" not in kernel
+    # the source is decoded when fetched; LDS and memory polls are separate
+    assert "_g_in = _g_off < (unsigned)_lcd_tile_rows;" in kernel
+    assert "if (_g_in) { const double _g_raw = __hip_atomic_load(&_lcd_tile[_g_off]" in kernel
+    assert "const double _g_raw = lcd_ld(&x[_g_src]);" in kernel
+    # further chunks come from the incoming listing ...
+    assert "_g_src = _lcd_in_src[_mb_next + _lane];" in kernel
+    # ... unless the inspector found that every task fits its record
+    single = lower(module, single_chunk=True, **options)
+    assert "_lcd_in_src[_mb_next + _lane]" not in single.kernel_source
+    assert "bool _need = _pending && _lane < _mb_have;" in single.kernel_source
+    assert "if (_fits && lcd_group_none(_need)) {" in single.kernel_source
+    assert single.kernel_arguments == result.kernel_arguments
+    # the watchdog looks up once in 1024 polls
+    assert "(++_spins & 1023u) == 0u" in kernel
+    for lowered in (result, single):
+        hip_runtime.compile_code(lowered.source)
+    plain = lower(module, task_records=False, **options)
+    assert plain.task_record_lanes is None
+    assert plain.stage_kernel_name == "sptrsv_csc_loop_hip_stage"
+    assert "_lcd_rec_in" not in plain.kernel_arguments
+    hip_runtime.compile_code(plain.source)
+
+
 def test_mailbox_needs_no_clear_of_the_solution():
     module = demo_source("sptrsv", "sptrsv_csc_loop")
     result = lower(module, execution_mode="sync_free",
