@@ -273,8 +273,9 @@ int lcdhip_dag_tile_order(lcdhip_dag *dag, int64_t tile_rows,
 int lcdhip_dag_tile_locality(const lcdhip_dag *dag, int64_t tile_rows,
                              lcdhip_stream stream, int64_t *local_edges_out);
 /* Fixed-size records of the incoming listing in the order the persistent
- * executor visits the tasks (TILE_NODES when lcdhip_dag_tile_order ran, else
- * WAVEFRONTS): for the task at position q, REC_IN holds its range of the
+ * executor visits the tasks (tiled != 0: TILE_NODES, which
+ * lcdhip_dag_tile_order must have built; else WAVEFRONTS): for the task at
+ * position q, REC_IN holds its range of the
  * incoming listing and REC_SRC / REC_POS[q * lanes + l] the source and the
  * position of its l-th incoming edge (0 beyond its in-degree).  A wavefront
  * then fetches everything its tasks need to start polling with loads whose
@@ -283,8 +284,8 @@ int lcdhip_dag_tile_locality(const lcdhip_dag *dag, int64_t tile_rows,
  * edges stay in the incoming listing only.  Needs LCDHIP_DAG_INCOMING and
  * LCDHIP_DAG_LEVELS; lanes in [1, 64].  (Layout of this backend's executor;
  * no counterpart in the reference.) */
-int lcdhip_dag_task_records(lcdhip_dag *dag, int lanes, lcdhip_stream stream,
-                            int64_t *overflow_tasks_out);
+int lcdhip_dag_task_records(lcdhip_dag *dag, int lanes, int tiled,
+                            lcdhip_stream stream, int64_t *overflow_tasks_out);
 int lcdhip_dag_get_info(const lcdhip_dag *dag, lcdhip_dag_info *out);
 int lcdhip_dag_array(const lcdhip_dag *dag, int which, void **d_out,
                      int64_t *count_out);

@@ -1160,7 +1160,7 @@ __global__ void task_records_kernel(const int32_t *__restrict__ order,
 
 }
 
-extern "C" int lcdhip_dag_task_records(lcdhip_dag *dag, int lanes,
+extern "C" int lcdhip_dag_task_records(lcdhip_dag *dag, int lanes, int tiled,
                                        lcdhip_stream stream_handle,
                                        int64_t *overflow_tasks_out)
 {
@@ -1169,13 +1169,12 @@ extern "C" int lcdhip_dag_task_records(lcdhip_dag *dag, int lanes,
         set_error("task records need a dag and 1 to 64 lanes per task");
         return LCDHIP_ERR_ARGUMENT;
     }
-    const int32_t *order = dag->arrays[LCDHIP_DAG_TILE_NODES]
-                               ? dag->arrays[LCDHIP_DAG_TILE_NODES]
-                               : dag->arrays[LCDHIP_DAG_WAVEFRONTS];
+    const int32_t *order = dag->arrays[tiled ? LCDHIP_DAG_TILE_NODES
+                                             : LCDHIP_DAG_WAVEFRONTS];
     if (!order || dag->info.scheduled != dag->info.n ||
         !dag->arrays[LCDHIP_DAG_IN_PTR]) {
-        set_error("task records need level sets that cover every node and "
-                  "the incoming listing");
+        set_error("task records need level sets that cover every node, the "
+                  "incoming listing and, when tiled, the tile order");
         return LCDHIP_ERR_ARGUMENT;
     }
     hipStream_t stream = resolve_stream(stream_handle);

@@ -296,7 +296,8 @@ def execution_data_from_device_dag(dag, execution_mode, warp_mapped,
         if record_lanes:
             # the first `record_lanes` incoming edges of every task, in the
             # order the executor visits the tasks
-            records = dag.task_records(int(record_lanes))
+            records = dag.task_records(int(record_lanes),
+                                       tiled=bool(tile_rows))
             auxiliary.update(zip(
                 ("_lcd_rec_in", "_lcd_rec_src", "_lcd_rec_pos"), records))
         return WarpTaskExecutionData(

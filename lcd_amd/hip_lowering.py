@@ -1383,16 +1383,14 @@ class HIPLowerer:
             self._segment = self._segment_plan(body, arguments)
         if self.tile_rows:
             self._tile = self._tile_plan(target_loop)
-        if (self._tile is not None and self.task_records
-                and self._mailbox is not None
+        if (self.task_records and self._mailbox is not None
                 and self._mailbox["gather"] is not None):
-            # tiled executor: the first incoming edges of every task sit in
-            # fixed-size records in task order, so everything a wavefront
-            # needs to start polling is fetched with loads whose addresses
-            # depend on the task's queue position alone; operands are read
-            # through the recorded positions (no per-launch staging kernel).
-            # 128^3 grid: 0.44 ms -> 0.33 ms for the executor, 0.04 ms of
-            # staging gone.
+            # the first incoming edges of every task sit in fixed-size
+            # records in task order, so everything a wavefront needs to start
+            # polling is fetched with loads whose addresses depend on the
+            # task's queue position alone; operands are read through the
+            # recorded positions (no per-launch staging kernel).  128^3 grid:
+            # 0.475 -> 0.395 ms tiled, 0.685 -> 0.567 ms with the flat queue.
             gather = self._mailbox["gather"]
             for name in gather["staged"].values():
                 kinds.arrays.pop(name, None)
@@ -2846,21 +2844,24 @@ class HIPLowerer:
                 f"{pad}            const double _mb_in = __shfl(_mb_value, _mb_k, LCD_TASK_LANES);",
                 f"{pad}            if (_mb_k < _mb_have) {own} = {own} + _mb_in;",
                 f"{pad}        }}"]
-        if tiled and self.single_chunk and gather.get("records"):
+        if self.single_chunk and gather.get("records"):
             # one chunk per task: what each lane still waits for is a flag
             # set when the task is fetched and cleared by its poll
+            memory_poll = (
+                f"{{ const double _g_raw = lcd_ld(&{array}[_g_src]); "
+                "if (!lcd_is_empty(_g_raw)) { _mb_value = _g_raw; "
+                "_need = false; } }")
             return [
                 f"{pad}bool _ready = false;",
                 f"{pad}if (_need) {{",
-                f"{pad}    if (_g_in) {{ const double _g_raw = "
-                "__hip_atomic_load(&_lcd_tile[_g_off], __ATOMIC_RELAXED, "
-                "__HIP_MEMORY_SCOPE_WORKGROUP); "
-                "if (!lcd_is_empty(_g_raw)) { _mb_value = _g_raw; "
-                "_need = false; } }",
-                f"{pad}    else if ((_spins & LCD_EXTERNAL_POLL_MASK) == 0) "
-                f"{{ const double _g_raw = lcd_ld(&{array}[_g_src]); "
-                "if (!lcd_is_empty(_g_raw)) { _mb_value = _g_raw; "
-                "_need = false; } }",
+                *([f"{pad}    if (_g_in) {{ const double _g_raw = "
+                   "__hip_atomic_load(&_lcd_tile[_g_off], __ATOMIC_RELAXED, "
+                   "__HIP_MEMORY_SCOPE_WORKGROUP); "
+                   "if (!lcd_is_empty(_g_raw)) { _mb_value = _g_raw; "
+                   "_need = false; } }",
+                   f"{pad}    else if ((_spins & LCD_EXTERNAL_POLL_MASK) == 0) "
+                   + memory_poll] if tiled else
+                  [f"{pad}    {memory_poll}"]),
                 f"{pad}}}",
                 f"{pad}if (_fits && lcd_group_none(_need)) {{",
                 f"{pad}    if (_lane < _mb_have) {{ const double _g_value = "

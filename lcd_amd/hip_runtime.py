@@ -400,9 +400,9 @@ class DeviceDag:
         self.tile_rows = tile_rows
         return self.array("tile_nodes")
 
-    def task_records(self, lanes):
+    def task_records(self, lanes, tiled=False):
         """Fixed-size records of the incoming listing in task order
-        (``tile_nodes`` when tiles were ordered, else ``wavefronts``):
+        (``tile_nodes`` when ``tiled``, else ``wavefronts``):
         afterwards ``rec_in`` (2 per task), ``rec_src`` and ``rec_pos``
         (``lanes`` per task) are arrays of this DAG."""
         if not isinstance(lanes, int) or not 1 <= lanes <= 64:
@@ -413,8 +413,8 @@ class DeviceDag:
             self._host.pop(name, None)
         overflow = ctypes.c_int64()
         _check(load_library().lcdhip_dag_task_records(
-            self.handle, ctypes.c_int(lanes), self.device.stream,
-            ctypes.byref(overflow)))
+            self.handle, ctypes.c_int(lanes), ctypes.c_int(int(bool(tiled))),
+            self.device.stream, ctypes.byref(overflow)))
         self.record_lanes = lanes
         # tasks whose incoming edges do not all fit their record
         self.record_overflow = int(overflow.value)

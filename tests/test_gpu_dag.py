@@ -166,8 +166,12 @@ def test_task_records(device, oracle, lanes, tile_rows):
     dag = device.dag_build([rule], work.n, levels=True, incoming=True)
     if tile_rows:
         dag.tile_order(tile_rows)
-    rec_in, rec_src, rec_pos = (a.copy_to_host()
-                                for a in dag.task_records(lanes))
+    if not tile_rows:
+        with pytest.raises(hip_runtime.HIPRuntimeError):
+            dag.task_records(lanes, tiled=True)     # no tile order yet
+    rec_in, rec_src, rec_pos = (
+        a.copy_to_host()
+        for a in dag.task_records(lanes, tiled=bool(tile_rows)))
     order = dag.host("tile_nodes" if tile_rows else "wavefronts")
     in_ptr, in_src, in_pos = (dag.host(name)
                               for name in ("in_ptr", "in_src", "in_pos"))

@@ -60,6 +60,11 @@ CSC_VARIANTS = [
          dependence_protocol="mailbox", tile_rows=None),
     dict(execution_mode="sync_free", threads_per_block=128, n_warp=1,
          dependence_protocol="mailbox"),
+    # gathered operands staged per launch instead of read through records
+    dict(execution_mode="sync_free", threads_per_block=128, task_lanes=4,
+         dependence_protocol="mailbox", tile_rows=None, task_records=False),
+    dict(execution_mode="sync_free", threads_per_block=128, task_lanes=4,
+         dependence_protocol="mailbox", tile_rows=256, task_records=False),
     dict(),   # scheduler decides
 ]
 

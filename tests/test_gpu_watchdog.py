@@ -32,6 +32,8 @@ CASES = [
      dict(gather_messages=False)),
     ("sptrsv_csc_loop", sptrsv.FUNCTION_PROPS_CSC, "mailbox", {}),
     ("sptrsv_csc_loop", sptrsv.FUNCTION_PROPS_CSC, "mailbox",
+     dict(task_records=False)),
+    ("sptrsv_csc_loop", sptrsv.FUNCTION_PROPS_CSC, "mailbox",
      dict(tile_rows=512)),
     ("sptrsv_csr_loop", sptrsv.FUNCTION_PROPS_CSR, "pull", {}),
     ("sptrsv_csr_loop", sptrsv.FUNCTION_PROPS_CSR, "pull",
@@ -44,7 +46,7 @@ CASES = [
 @pytest.mark.parametrize(
     "name,props,protocol,extra", CASES,
     ids=["counter", "push", "mailbox-slots", "mailbox-gathered",
-         "mailbox-tiled", "pull-values", "pull-flags", "pull-tiled"])
+         "mailbox-staged", "mailbox-tiled", "pull-values", "pull-flags", "pull-tiled"])
 def test_unsatisfiable_wait_trips_the_watchdog(oracle, name, props, protocol,
                                                extra):
     print("watchdog", name, protocol, extra, flush=True)

@@ -586,14 +586,26 @@ def test_csr_pull_polls_the_values_themselves():
 
 def test_gathered_mailbox_drops_the_producer_loop():
     module = demo_source("sptrsv", "sptrsv_csc_loop")
+    records = lower(module, execution_mode="sync_free",
+                    thread_loop_iterator="j", task_lanes=4,
+                    dependence_protocol="mailbox", gather_messages=True)
+    # default: incoming edges in task records, operands through positions
+    assert records.task_record_lanes == 4 and records.tile_rows is None
+    assert records.stage_kernel_name is None
+    assert "_g_src = _lcd_rec_src[_task * LCD_TASK_LANES + _lane];" in (
+        records.kernel_source)
+    assert "const double _g_value = lcd_ld(&x[_g_src]);" in records.kernel_source
+    hip_runtime.compile_code(records.source)
     result = lower(module, execution_mode="sync_free",
                    thread_loop_iterator="j", task_lanes=4,
-                   dependence_protocol="mailbox", gather_messages=True)
+                   dependence_protocol="mailbox", gather_messages=True,
+                   task_records=False)
     kernel = result.kernel_source
     assert result.dependence_protocol == "mailbox"
     assert result.value_flag_array == "x"
     assert "_lcd_mailbox" not in result.kernel_arguments
-    # the coefficient is gathered into consumer order by a staging kernel
+    # without records the coefficient is gathered into consumer order by a
+    # staging kernel
     assert {"_lcd_in_ptr", "_lcd_in_src", "_lcd_staged_0"} <= set(
         result.kernel_arguments)
     assert "_lcd_in_pos" not in result.kernel_arguments
@@ -607,7 +619,7 @@ def test_gathered_mailbox_drops_the_producer_loop():
     unstaged = lower(module, execution_mode="sync_free",
                      thread_loop_iterator="j", task_lanes=4,
                      dependence_protocol="mailbox", gather_messages=True,
-                     stage_operands=False)
+                     stage_operands=False, task_records=False)
     assert unstaged.stage_kernel_name is None
     assert "_g_operand_0 = Ax[_g_pos];" in unstaged.kernel_source
     assert "_lcd_in_pos" in unstaged.kernel_arguments
