@@ -148,6 +148,77 @@ def test_tiled_executor(oracle, tile_rows, lanes, tpb):
     assert pushed.hip_lowering.tile_rows is None
 
 
+def random_lower_factor(n, seed):
+    """Lower-triangular factor with a skewed row-length mix: empty rows,
+    short rows and a few rows with up to 300 entries (more incoming edges
+    than any lane count), unit-scale values, dominant diagonal."""
+    import scipy.sparse as sp
+    rng = np.random.default_rng(seed)
+    rows, cols = [], []
+    for i in range(1, n):
+        kind = rng.random()
+        count = (0 if kind < 0.1 else int(rng.integers(1, 6)) if kind < 0.9
+                 else int(rng.integers(20, 300)))
+        count = min(count, i)
+        # mostly nearby columns, some far ones
+        near = max(0, i - 40)
+        picks = np.unique(np.concatenate([
+            rng.integers(near, i, size=count),
+            rng.integers(0, i, size=max(count // 4, 0))]))
+        rows += [i] * len(picks)
+        cols += picks.tolist()
+    values = rng.uniform(-1.0, 1.0, len(rows))
+    lower = sp.csr_matrix((values, (rows, cols)), shape=(n, n))
+    diagonal = 1.0 + np.asarray(abs(lower).sum(axis=1)).ravel()
+    return lower, diagonal, rng.standard_normal(n)
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_random_factors_through_every_persistent_executor(oracle, seed):
+    """Random structure (not a stencil): empty rows, in-degrees beyond the
+    record size, edges near and far -- CSC and CSR, flat and tiled."""
+    import scipy.sparse as sp
+    n = 3000 + 517 * seed
+    print("random factor", seed, n, flush=True)
+    lower, diagonal, rhs = random_lower_factor(n, seed)
+    # CSC with the diagonal first, CSR with the diagonal last
+    csc = sp.csc_matrix(lower + sp.diags(diagonal))
+    csc.sort_indices()
+    csr = sp.csr_matrix(lower + sp.diags(diagonal))
+    csr.sort_indices()
+    by_column = tuple(a.astype(np.int32) for a in (csc.indptr, csc.indices))
+    by_row = tuple(a.astype(np.int32) for a in (csr.indptr, csr.indices))
+    expected_csc = oracle.sptrsv_csc(*by_column, csc.data, rhs, n)
+    expected_csr = oracle.sptrsv_csr(*by_row, csr.data, rhs, n)
+    assert relative_error(expected_csc, expected_csr) <= 1e-10
+    for options in (dict(task_lanes=4, tile_rows=None),
+                    dict(task_lanes=8, tile_rows=256),
+                    dict(task_lanes=64, tile_rows=None),
+                    dict(task_lanes=4, tile_rows=None, task_records=False),
+                    dict(task_lanes=16, tile_rows=None, gather_messages=False)):
+        print("  csc", options, flush=True)
+        solver = sptrsv.compile_sptrsv_csc(
+            execution_mode="sync_free", threads_per_block=128,
+            thread_unroll=1, dependence_protocol="mailbox", **options)
+        result = solver(*by_column, csc.data, rhs, n)
+        # incoming products are added in the sequential order: bit-identical
+        np.testing.assert_array_equal(result, expected_csc)
+        if options.get("task_records", True) and options.get(
+                "gather_messages", True):
+            plan = solver.schedule_plan(*by_column, csc.data, rhs, n)
+            assert plan.dag.record_overflow > 0 or options["task_lanes"] == 64
+            assert plan.single_chunk == (plan.dag.record_overflow == 0)
+    for options in (dict(task_lanes=8, tile_rows=None),
+                    dict(task_lanes=32, tile_rows=512),
+                    dict(task_lanes=16, tile_rows=None, value_flags=False)):
+        print("  csr", options, flush=True)
+        solver = sptrsv.compile_sptrsv_csr(
+            execution_mode="sync_free", threads_per_block=128,
+            thread_unroll=1, dependence_protocol="pull", **options)
+        result = solver(*by_row, csr.data, rhs, n)
+        assert relative_error(result, expected_csr) <= TOLERANCE
+
+
 CSR_VARIANTS = [
     dict(execution_mode="wavefront", threads_per_block=128, task_lanes=8),
     dict(execution_mode="wavefront", threads_per_block=128, n_warp=1,
