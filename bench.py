@@ -161,7 +161,7 @@ def main():
                         default=None)
     parser.add_argument("--spin-sleep", dest="spin_sleep", type=int,
                         default=None)
-    parser.add_argument("--cpu-seconds", type=float, default=5.0)
+    parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--tile-rows", dest="tile_rows", type=int, default=None,
                         help="tiled persistent executor: rows per tile")
     parser.add_argument("--slots", action="store_true",
