@@ -175,8 +175,9 @@ def parallel(**kwargs):
             raise ValueError(
                 "tile_rows must be None, 'auto' or a positive integer.")
 
-        def lower_variant(lowering_key, tile_rows=None, single_chunk=False):
-            variant_key = (lowering_key, tile_rows, single_chunk)
+        def lower_variant(lowering_key, tile_rows=None, single_chunk=False,
+                          task_records=True):
+            variant_key = (lowering_key, tile_rows, single_chunk, task_records)
             if variant_key not in lowered_variants:
                 (mode, threads_per_block, unroll, n_warp, protocol,
                  task_lanes) = lowering_key
@@ -206,14 +207,17 @@ def parallel(**kwargs):
                     gather_messages=kwargs.get("gather_messages", True),
                     segment_cache=kwargs.get("segment_cache", True),
                     tile_rows=tile_rows if mode == SYNC_FREE else None,
-                    task_records=kwargs.get("task_records", True),
+                    task_records=(task_records
+                                  and kwargs.get("task_records", True)),
                     single_chunk=single_chunk,
                 )
             return lowered_variants[variant_key]
 
-        def compile_variant(lowering_key, tile_rows=None, single_chunk=False):
-            lowering = lower_variant(lowering_key, tile_rows, single_chunk)
-            variant_key = (lowering_key, tile_rows, single_chunk)
+        def compile_variant(lowering_key, tile_rows=None, single_chunk=False,
+                            task_records=True):
+            lowering = lower_variant(lowering_key, tile_rows, single_chunk,
+                                     task_records)
+            variant_key = (lowering_key, tile_rows, single_chunk, task_records)
             if variant_key not in compiled_variants:
                 compiled_variants[variant_key] = compile_hip_module(
                     lowering, function_globals=function.__globals__)
@@ -378,6 +382,12 @@ def parallel(**kwargs):
                 schedule = scheduler.schedule(features, schedule_space)
             schedule, tile_rows = tiles_for(dag, schedule)
             lowering = lower_variant(schedule.lowering_key, tile_rows)
+            # the record arrays are indexed with 32 bits
+            records = (not lowering.task_record_lanes
+                       or dag.n * lowering.task_record_lanes < 2 ** 31)
+            if not records:
+                lowering = lower_variant(schedule.lowering_key, tile_rows,
+                                         task_records=False)
             execution_data = execution_data_from_device_dag(
                 dag, schedule.execution_mode, lowering.warp_mapped,
                 pushed=lowering.dependence_protocol == PUSH_DEPENDENCE,
@@ -393,7 +403,8 @@ def parallel(**kwargs):
                 # every task's incoming edges fit its record: the executor
                 # variant without the code for further chunks
                 single_chunk=bool(lowering.task_record_lanes)
-                and getattr(dag, "record_overflow", 1) == 0)
+                and getattr(dag, "record_overflow", 1) == 0,
+                task_records=records)
             plan_state[id(plan)] = {"resident": resident, "workspace": {}}
             return plan
 
@@ -434,7 +445,8 @@ def parallel(**kwargs):
             plan = plan_for(argument_values)
             lowering, compiled = compile_variant(plan.schedule.lowering_key,
                                                  plan.tile_rows,
-                                                 plan.single_chunk)
+                                                 plan.single_chunk,
+                                                 plan.task_records)
             publish_variant(plan.schedule, lowering, compiled)
             state = plan_state[id(plan)]
             values = dict(argument_values)

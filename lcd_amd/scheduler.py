@@ -156,6 +156,7 @@ class SchedulePlan:
     dag: object = None
     tile_rows: int | None = None     # tiled persistent executor, or None
     single_chunk: bool = False       # no task has more in-edges than lanes
+    task_records: bool = True        # record arrays fit 32-bit indices
 
 
 # Tiled executor, automatic choice: tiles of 4096 consecutive block-iterator
