@@ -80,6 +80,8 @@ def build_solver(work, args):
         options["spin_sleep"] = args.spin_sleep
     if args.tile_rows is not None:
         options["tile_rows"] = args.tile_rows or None
+    if args.no_queue_loads:
+        options["queue_node_loads"] = False
     if args.slots:
         options["gather_messages"] = False
         options["tile_rows"] = None
@@ -170,6 +172,9 @@ def main():
     parser.add_argument("--auto", action="store_true",
                         help="let the analytic scheduler choose the schedule "
                              "instead of the tuned defaults")
+    parser.add_argument("--no-queue-loads", action="store_true",
+                        help="read structure arrays through the task id "
+                             "instead of copies in task order")
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-check", action="store_true")
     parser.add_argument("--arch", action="store_true",

@@ -300,6 +300,16 @@ int lcdhip_lookup_build(const int32_t *d_ptr, const int32_t *d_idx, int64_t n,
                         int64_t idx_size, int32_t *d_positions,
                         lcdhip_stream stream);
 
+/* d_dst[q] = d_src[d_index[q] + offset] for q in [0, count): a structure
+ * array read in the order the executor visits the tasks, so that a task's
+ * loads of it (`Ap[i]`, `Ap[i + 1]`) have addresses that depend on the queue
+ * position alone.  Fails with LCDHIP_ERR_ARGUMENT when an index leaves
+ * [0, src_size).  (Layout of this backend's executors; the reference prefetches
+ * the same node loads through the task id, compiler/cuda_lowering.py:1991-2029.) */
+int lcdhip_gather_i32(int32_t *d_dst, const int32_t *d_src,
+                      const int32_t *d_index, int64_t offset, int64_t count,
+                      int64_t src_size, lcdhip_stream stream);
+
 /* 128-bit content digest of a device array; replaces the per-call blake2b of
  * the structure arrays (compiler/scheduler.py:678-711) for arrays that are
  * already resident. */

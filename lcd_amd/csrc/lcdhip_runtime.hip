@@ -914,3 +914,60 @@ extern "C" int lcdhip_measure_arch(lcdhip_arch *out)
     (void)hipEventDestroy(stop_event);
     return LCDHIP_OK;
 }
+
+__global__ void lcdhip_gather_kernel(int32_t *__restrict__ dst,
+                                     const int32_t *__restrict__ src,
+                                     const int32_t *__restrict__ index,
+                                     int64_t offset, int64_t count,
+                                     int64_t src_size, int32_t *status)
+{
+    int64_t q = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (q >= count)
+        return;
+    const int64_t at = static_cast<int64_t>(index[q]) + offset;
+    if (at < 0 || at >= src_size) {
+        atomicMax(status, 1);
+        dst[q] = 0;
+        return;
+    }
+    dst[q] = src[at];
+}
+
+extern "C" int lcdhip_gather_i32(int32_t *d_dst, const int32_t *d_src,
+                                 const int32_t *d_index, int64_t offset,
+                                 int64_t count, int64_t src_size,
+                                 lcdhip_stream stream)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (count < 0 || src_size < 0 ||
+        (count > 0 && (!d_dst || !d_src || !d_index))) {
+        set_error("bad argument to lcdhip_gather_i32");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    if (count == 0)
+        return LCDHIP_OK;
+    hipStream_t hip_stream = resolve_stream(stream);
+    int32_t *d_status = nullptr;
+    LCDHIP_CHECK(hipMalloc(&d_status, 4));
+    LCDHIP_CHECK(hipMemsetAsync(d_status, 0, 4, hip_stream));
+    hipLaunchKernelGGL(lcdhip_gather_kernel,
+                       dim3(static_cast<unsigned>((count + 255) / 256)),
+                       dim3(256), 0, hip_stream, d_dst, d_src, d_index, offset,
+                       count, src_size, d_status);
+    int32_t status = 0;
+    hipError_t copy_status = hipMemcpyAsync(&status, d_status, 4,
+                                            hipMemcpyDeviceToHost, hip_stream);
+    if (copy_status == hipSuccess)
+        copy_status = hipStreamSynchronize(hip_stream);
+    (void)hipFree(d_status);
+    if (copy_status != hipSuccess) {
+        set_error("gather kernel failed: %s", hipGetErrorString(copy_status));
+        return LCDHIP_ERR_HIP;
+    }
+    if (status) {
+        set_error("lcdhip_gather_i32: an index plus offset leaves the source "
+                  "array");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    return LCDHIP_OK;
+}

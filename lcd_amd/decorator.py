@@ -210,6 +210,7 @@ def parallel(**kwargs):
                     task_records=(task_records
                                   and kwargs.get("task_records", True)),
                     single_chunk=single_chunk,
+                    queue_node_loads=kwargs.get("queue_node_loads", True),
                 )
             return lowered_variants[variant_key]
 

@@ -29,6 +29,7 @@ from copy import deepcopy
 from dataclasses import dataclass, field
 import textwrap
 
+from lcd_amd.dependence import _split_offset
 from lcd_amd.structural_lookups import (
     match_segment_search,
     structure_aliases,
@@ -145,6 +146,7 @@ class HIPLoweringResult:
     # kernel that gathers position-indexed operands into consumer order at
     # the start of every launch (gathered mailbox), and its argument names
     task_record_lanes: int | None = None
+    queue_node_loads: tuple = ()     # (argument, structure array, offset)
     stage_kernel_name: str | None = None
     stage_kernel_arguments: tuple = ()
     # tiled persistent executor: block-iterator values per tile, or None
@@ -951,7 +953,11 @@ class HIPLowerer:
                  spin_sleep=1, promote_own_elements=True,
                  prefetch_node_loads=True, value_flags=True,
                  gather_messages=True, segment_cache=True, tile_rows=None,
-                 stage_operands=True, task_records=True, single_chunk=False):
+                 stage_operands=True, task_records=True, single_chunk=False,
+                 queue_node_loads=True):
+        self.queue_node_loads_enabled = queue_node_loads
+        self._queue_node_loads = []
+        self._queue_load_lines = []
         self.stage_operands = stage_operands
         self.task_records = task_records
         self.single_chunk = single_chunk
@@ -1429,6 +1435,11 @@ class HIPLowerer:
         self._lifted_parameters = list(lifted_loop_parameters)
         task_body = self._task_body(body, emitter, local_names, target_loop,
                                     arguments)
+        # structure arrays the tasks read in queue order (found while the
+        # node loads were hoisted) come last
+        for name, _, _ in self._queue_node_loads:
+            executor_arguments.append(name)
+            kernel_arguments.append(name)
         missing = ({sid for sid, _ in self.reductions.values()} - lowered_ids)
         if missing:
             raise HIPLoweringError(
@@ -1504,6 +1515,7 @@ class HIPLowerer:
             mailbox_index_array=(self._mailbox["index_array"]
                                  if self._mailbox else None),
             tile_rows=self._tile["rows"] if self._tile else None,
+            queue_node_loads=tuple(self._queue_node_loads),
             task_record_lanes=(
                 self.task_lanes if self._mailbox
                 and self._mailbox["gather"]
@@ -1863,9 +1875,16 @@ class HIPLowerer:
                 else f"{array}[_lcd_seg_base + _q]")
         store = (f"lcd_st(&{array}[_lcd_seg_base + _q], _lcd_seg[_q]);"
                  if coherent else f"{array}[_lcd_seg_base + _q] = _lcd_seg[_q];")
+        def bound(offset):
+            # the copy in task order when the node loads use one
+            for name, source, delta in self._queue_node_loads:
+                if (source, delta) == (pointer, offset):
+                    return f"{name}[_task]"
+            return f"{pointer}[{it} + {offset}]" if offset else f"{pointer}[{it}]"
+
         prologue = [
-            f"_lcd_seg_base = {pointer}[{it}];",
-            f"_lcd_seg_limit = {pointer}[{it} + 1] - _lcd_seg_base;",
+            f"_lcd_seg_base = {bound(0)};",
+            f"_lcd_seg_limit = {bound(1)} - _lcd_seg_base;",
             "if (_lcd_seg_limit > LCD_SEG_CAP) _lcd_seg_limit = 0;",
             "for (int _q = _lane; _q < _lcd_seg_limit; _q += LCD_TASK_LANES) "
             f"_lcd_seg[_q] = {load};",
@@ -2225,8 +2244,15 @@ class HIPLowerer:
         elif self.direct_dependence is not None:
             pass
         emitter = self._emitter
-        prefetch = [f"{temps[text][0]} = {emitter.expr(temps[text][1])};"
-                    for text in order[:node_count]]
+        prefetch = []
+        for text in order[:node_count]:
+            name, node = temps[text]
+            queued = self._queue_node_load(node)
+            if queued is not None:
+                # addressed by the queue position: issued with the task id
+                self._queue_load_lines.append(f"{name} = {queued}[_task];")
+            else:
+                prefetch.append(f"{name} = {emitter.expr(node)};")
         self._own_registers.extend(temps[text][0] for text in order)
         reload_lines = []
         if first_iteration:
@@ -2241,6 +2267,34 @@ class HIPLowerer:
         self._first_iteration_reload = reload_lines
         ast.fix_missing_locations(ast.Module(body=body, type_ignores=[]))
         return body, prefetch
+
+    def _queue_node_load(self, node):
+        """``P[i + c]`` of a structure array ``P`` (one whose contents are
+        part of the inspection fingerprint): read it from a copy in task
+        order, ``_lcd_qn_k[_task]``, which the runtime gathers once per
+        structure -- one load less on the chain in front of every task."""
+        # persistent executors with value hand-offs only: measured 1-2 %
+        # there; level launches lose 4 % (ILU0, 9-point grid) because rows of
+        # consecutive levels are neighbours, so `Ap[i]` is warm in L2 from the
+        # level before while a queue-ordered copy is cold at every level
+        if (not self.queue_node_loads_enabled or self.chain_tasks
+                or not self.warp_mapped or self.execution_mode != "sync_free"
+                or self.dependence_protocol == COUNTER_DEPENDENCE):
+            return None
+        array = node.value.id
+        properties = (self.function_props or {}).get(array, ())
+        if "monotonically_increasing" not in properties:
+            return None
+        base, offset = _split_offset(node.slice)
+        if not (isinstance(base, ast.Name) and base.id == self.loop_iterator):
+            return None
+        for name, source, delta in self._queue_node_loads:
+            if (source, delta) == (array, offset):
+                return name
+        name = f"_lcd_qn_{len(self._queue_node_loads)}"
+        self._queue_node_loads.append((name, array, offset))
+        self._kinds.arrays[name] = INT
+        return name
 
     def _task_body(self, body, emitter, local_names, target_loop, arguments):
         """C++ lines of one task (indent level 0), `i` already bound."""
@@ -2522,7 +2576,9 @@ class HIPLowerer:
                          f"{pad}    lcd_release_fence();",
                          f"{pad}    {self.group_sync}",
                          f"{pad}}}"])
-            return [f"{pad}{it} = task_nodes[_task];", *body_fn(indent)]
+            return [f"{pad}{it} = task_nodes[_task];",
+                    *[pad + line for line in self._queue_load_lines],
+                    *body_fn(indent)]
 
         if self.execution_mode == "plain":
             lower, _, _ = self._emitter.range_parts(target_loop)
@@ -2570,6 +2626,7 @@ class HIPLowerer:
                 "        __syncthreads();",
                 "        if (_task >= _task_count) return;",
                 f"        {it} = (lcd_index_t)task_nodes[_task];",
+                *["        " + line for line in self._queue_load_lines],
                 f"        if ({self._prefetch_guard}) {{",
                 *[f"            {line}" for line in self._prefetch_lines],
                 "        }",
@@ -2664,6 +2721,8 @@ class HIPLowerer:
             *fetch,
             *([f"        {it} = 0;"] if records else
               [f"        {it} = _pending ? (lcd_index_t)task_nodes[_task] : 0;"]),
+            *(["        if (_pending) { " + " ".join(self._queue_load_lines)
+               + " }"] if self._queue_load_lines and not records else []),
             # records are addressed by the queue position: their loads go
             # out with the task id, ahead of the loads that wait for it
             *(incoming + node_loads if records else node_loads),
@@ -2786,7 +2845,8 @@ class HIPLowerer:
                 "_mb_next = _lcd_rec_in[2 * _task]; "
                 "_mb_end = _lcd_rec_in[2 * _task + 1]; "
                 f"_g_pos = _lcd_rec_pos[{slot}]; "
-                f"_g_src = _lcd_rec_src[{slot}]; {decode}}}")
+                f"_g_src = _lcd_rec_src[{slot}]; {decode}"
+                + " ".join(self._queue_load_lines) + " }")
             lines.append(f"{pad}{head} {{ {loads} }}")
             if self.single_chunk:
                 lines += [
@@ -3139,7 +3199,8 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
                  spin_sleep=1, promote_own_elements=True,
                  prefetch_node_loads=True, value_flags=True,
                  gather_messages=True, segment_cache=True, tile_rows=None,
-                 stage_operands=True, task_records=True, single_chunk=False):
+                 stage_operands=True, task_records=True, single_chunk=False,
+                 queue_node_loads=True):
     """HIP counterpart of ``lower_to_numba_cuda``
     (compiler/cuda_lowering.py:2854-2884); same parameters plus
     ``task_lanes`` (lanes cooperating on one task, a power of two <= 64),
@@ -3161,5 +3222,6 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
         prefetch_node_loads=prefetch_node_loads, value_flags=value_flags,
         gather_messages=gather_messages, segment_cache=segment_cache,
         tile_rows=tile_rows, stage_operands=stage_operands,
-        task_records=task_records, single_chunk=single_chunk)
+        task_records=task_records, single_chunk=single_chunk,
+        queue_node_loads=queue_node_loads)
     return lowerer.lower(code)

@@ -130,7 +130,7 @@ EXPORTED_SYMBOLS = (
     "lcdhip_dag_download", "lcdhip_dag_destroy", "lcdhip_dag_band_chains",
     "lcdhip_dag_tile_order", "lcdhip_dag_tile_locality",
     "lcdhip_dag_task_records",
-    "lcdhip_lookup_build",
+    "lcdhip_lookup_build", "lcdhip_gather_i32",
     "lcdhip_digest",
 )
 
@@ -656,6 +656,18 @@ class HIPDevice:
             self.stream))
         return out
 
+    def gather_int32(self, source, index, offset=0):
+        """``source[index[q] + offset]`` for every ``q``, on the device."""
+        keep = []
+        d_src, src_size = self._resident_int32(source, keep)
+        d_index, count = self._resident_int32(index, keep)
+        out = self.empty((max(count, 0),), np.int32)
+        _check(self.lib.lcdhip_gather_i32(
+            ctypes.c_void_p(out.pointer), ctypes.c_void_p(d_src),
+            ctypes.c_void_p(d_index), ctypes.c_int64(int(offset)),
+            ctypes.c_int64(count), ctypes.c_int64(src_size), self.stream))
+        return out
+
     def digest(self, array):
         out = (ctypes.c_uint64 * 2)()
         shape, dtype = device_array_meta(array)
@@ -971,6 +983,15 @@ def prepare_hip_arguments(lowering, argument_values, execution_data,
         host_values[name] = cached
     execution_values = _execution_values(lowering.execution_mode, execution_data)
     host_values.update(execution_values)
+
+    # structure arrays in task order (once per plan: the workspace keeps them)
+    for name, source, offset in getattr(lowering, "queue_node_loads", ()):
+        cached = workspace.get(("queue", name))
+        if cached is None:
+            cached = device.gather_int32(host_values[source],
+                                         host_values["task_nodes"], offset)
+            workspace[("queue", name)] = cached
+        host_values[name] = cached
 
     # mutable executor state
     n_tasks = None

@@ -470,6 +470,9 @@ def lower(module, **options):
     plan = create_dag_plan(analysis.ordering_dependences, None, "i", [])
     thread = options.get("thread_loop_iterator")
     options.setdefault("direct_dependence", direct_dependence(plan, thread))
+    # argument lists and node loads as the reference shapes them; the copies
+    # of structure arrays in task order have a test of their own
+    options.setdefault("queue_node_loads", False)
     return lower_to_hip(module, "i", reductions=analysis,
                         function_props=function_props, **options)
 
@@ -669,6 +672,34 @@ def test_tiled_mailbox_reads_task_records():
     hip_runtime.compile_code(plain.source)
 
 
+def test_structure_arrays_are_read_in_task_order():
+    """``Ap[i]`` / ``Ap[i + 1]`` come from copies gathered into queue order
+    once per structure, loaded with the task id instead of after it."""
+    module = demo_source("sptrsv", "sptrsv_csr_loop")
+    result = lower(module, execution_mode="sync_free",
+                   thread_loop_iterator="j", task_lanes=8,
+                   dependence_protocol="pull", queue_node_loads=True)
+    assert result.queue_node_loads == (("_lcd_qn_0", "Ap", 0),
+                                       ("_lcd_qn_1", "Ap", 1))
+    assert result.kernel_arguments[-2:] == ["_lcd_qn_0", "_lcd_qn_1"]
+    assert result.launcher_arguments[-2:] == ["_lcd_qn_0", "_lcd_qn_1"]
+    kernel = result.kernel_source
+    assert ("if (_pending) { _nl_1 = _lcd_qn_0[_task]; "
+            "_nl_2 = _lcd_qn_1[_task]; }") in kernel
+    assert "= Ap[" not in kernel
+    assert "_nl_0 = b[i];" in kernel          # a value array stays as it is
+    hip_runtime.compile_code(result.source)
+    # level launches keep `Ap[i]` (warm in L2 from the level before), and so
+    # does the counter protocol
+    for options in (dict(execution_mode="wavefront"),
+                    dict(execution_mode="sync_free",
+                         dependence_protocol="counter")):
+        other = lower(module, thread_loop_iterator="j", task_lanes=8,
+                      queue_node_loads=True, **options)
+        assert other.queue_node_loads == ()
+        assert "_nl_1 = Ap[i];" in other.kernel_source
+
+
 def test_mailbox_needs_no_clear_of_the_solution():
     module = demo_source("sptrsv", "sptrsv_csc_loop")
     result = lower(module, execution_mode="sync_free",
@@ -823,6 +854,14 @@ def test_runtime_layer_accepts_an_injected_device():
         def synchronize(self):
             launches.append("sync")
 
+        def zeros(self, shape, dtype=np.float64):
+            return FakeArray(np.zeros(shape, dtype))
+
+        def gather_int32(self, source, index, offset=0):
+            launches.append(("gather", offset))
+            take = lambda a: a.data if isinstance(a, FakeArray) else np.asarray(a)
+            return FakeArray(take(source)[take(index) + offset])
+
     module = demo_source("sptrsv", "sptrsv_csc_loop")
     lowering = lower(module, execution_mode="wavefront",
                      thread_loop_iterator="j", task_lanes=4)
@@ -843,6 +882,23 @@ def test_runtime_layer_accepts_an_injected_device():
     result = hip_runtime.execute_hip_call(compiled, lowering, prepared,
                                           {"np": np})
     assert result.tolist() == [0.0, 0.0] and launches[-1] == "sync"
+    # structure arrays in task order are gathered by the device layer, once
+    # per workspace
+    queued = lower(module, execution_mode="sync_free",
+                   thread_loop_iterator="j", task_lanes=4,
+                   dependence_protocol="push", queue_node_loads=True)
+    assert [q[1:] for q in queued.queue_node_loads] == [("Ap", 0), ("Ap", 1)]
+    workspace = {}
+    for _ in range(2):
+        prepared = hip_runtime.prepare_hip_arguments(
+            queued,
+            {"Ap": np.array([0, 2, 3], dtype=np.int32),
+             "Ai": np.array([0, 1, 1], dtype=np.int32),
+             "Ax": np.ones(3), "b": np.ones(2), "n": 2},
+            data, {"np": np}, hip_module=FakeDevice(), workspace=workspace)
+    assert launches.count(("gather", 0)) == 1
+    assert launches.count(("gather", 1)) == 1
+    assert prepared.values["_lcd_qn_1"].data.tolist() == [2, 3]
     with pytest.raises(hip_runtime.HIPRuntimePreparationError,
                        match="level-ordered"):
         hip_runtime.prepare_hip_arguments(
