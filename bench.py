@@ -39,8 +39,8 @@ TUNED = {
     "c3": dict(execution_mode="sync_free", threads_per_block=128,
                task_lanes=64, thread_unroll=1,
                dependence_protocol="pull", tile_rows=None),
-    "c4": dict(execution_mode="wavefront", threads_per_block=64, task_lanes=8,
-               thread_unroll=1),
+    "c4": dict(execution_mode="sync_free", threads_per_block=64, task_lanes=8,
+               thread_unroll=1, dependence_protocol="pull"),
     "c5": dict(execution_mode="sync_free", threads_per_block=256, task_lanes=8,
                thread_unroll=1, dependence_protocol="mailbox",
                tile_rows=4096),
@@ -90,6 +90,11 @@ def build_solver(work, args):
         return sptrsv.compile_sptrsv_csc(**options)
     if work.kind == "sptrsv_csr":
         return sptrsv.compile_sptrsv_csr(**options)
+    if args.auto:
+        # the reference's demo fixes level launches with 128 threads; here the
+        # scheduler decides
+        options.setdefault("execution_mode", None)
+        options.setdefault("threads_per_block", None)
     return spilu0.compile_ilu0_csr(**options)
 
 
@@ -159,7 +164,7 @@ def main():
     parser.add_argument("--lanes", type=int, default=None)
     parser.add_argument("--unroll", type=int, default=None)
     parser.add_argument("--protocol", default=None)
-    parser.add_argument("--waves-per-cu", dest="waves_per_cu", type=int,
+    parser.add_argument("--waves-per-cu", dest="waves_per_cu", type=float,
                         default=None)
     parser.add_argument("--spin-sleep", dest="spin_sleep", type=int,
                         default=None)

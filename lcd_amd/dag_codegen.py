@@ -56,6 +56,11 @@ class DirectDependence:
     endpoint: ast.expr
     guard: ast.expr | None
     thread_loop: ast.For | None = field(default=None, compare=False)
+    # the edges are enumerated by a sequential loop of the task (over
+    # ``iterator``), not by the thread-mapped one: the task can wait for its
+    # producers one by one, in the order it uses them
+    sequential: bool = False
+    iterator: str | None = None
 
 
 def _normalize_execution_mode(execution_mode):
@@ -279,6 +284,22 @@ def direct_dependence(plan, thread_iterator, validate_endpoints=False):
     rule = plan.edge_rules[0]
     if not isinstance(rule, SegmentRule):
         return None
+    if (rule.iterators[0] == plan.parallel_iterator
+            and rule.iterators[1] != thread_iterator
+            and not rule.owner_is_source and not validate_endpoints):
+        # ILU0-CSR: `for k_ptr in <own segment>: k = idx[k_ptr]; if k >= i:
+        # break; ...` -- the task reads producer k inside iteration k_ptr only
+        endpoint = ast.parse(rule.endpoint_source(), mode="eval").body
+        lower, upper = _range_source(rule)
+        loop = ast.parse(
+            f"for {rule.inner_iterator} in range({lower}, {upper}):\n    pass"
+        ).body[0]
+        guard_text = _guard_source(rule)
+        return DirectDependence(
+            kind=PULL_DEPENDENCE, endpoint=endpoint,
+            guard=(ast.parse(guard_text, mode="eval").body
+                   if guard_text else None),
+            thread_loop=loop, sequential=True, iterator=rule.inner_iterator)
     if rule.iterators != [plan.parallel_iterator, thread_iterator]:
         return None
     if rule.break_at_owner:

@@ -234,15 +234,16 @@ def parallel(**kwargs):
                     else automatic_tile_rows(dag))
             if not rows:
                 return schedule, None
+            tiled = schedule
             if (tile_option == "auto" and thread_loop is not None
                     and kwargs.get("threads_per_block") is None
                     and not TILE_THREADS_PER_BLOCK % max(
                         schedule.task_lanes, 1)):
-                schedule = replace(
+                tiled = replace(
                     schedule, threads_per_block=TILE_THREADS_PER_BLOCK)
-            if lower_variant(schedule.lowering_key, rows).tile_rows is None:
-                return schedule, None
-            return schedule, rows
+            if lower_variant(tiled.lowering_key, rows).tile_rows is None:
+                return schedule, None        # tiles do not apply to this loop
+            return tiled, rows
 
         host_lowering = lower_variant(
             ScheduleSpace.from_options(**space_options).configurations()[0])

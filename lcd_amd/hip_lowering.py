@@ -968,6 +968,7 @@ class HIPLowerer:
         self.gather_messages = gather_messages
         self.value_flags = value_flags
         self._value_pull = None
+        self._sequential_pull = None
         self._own_zero_arrays = set()
         self.promote_own_elements = promote_own_elements
         self.prefetch_node_loads = prefetch_node_loads
@@ -1168,6 +1169,54 @@ class HIPLowerer:
                     return None
         return {"array": array, "endpoint_text": endpoint_text}
 
+    def _sequential_pull_plan(self, body):
+        """Pull protocol for a task whose producers are enumerated by one of
+        its own sequential loops (ILU0-CSR: ``for k_ptr in <row>: k =
+        A_indices[k_ptr]; if k >= i: break; ...``): instead of waiting until
+        every producer is done and then running the whole body, the loop is
+        made resumable and waits for producer ``k`` at the top of iteration
+        ``k_ptr``.  The work on early pivots overlaps the wait for the late
+        ones; what stays on the critical path is the last pivots' work.
+        9-point grid 1024^2: 35.4 ms (counters) -> 18.2 ms, against 23.1 ms
+        for level launches."""
+        dependence = self.direct_dependence
+        if (self.execution_mode != "sync_free" or self.block_task
+                or self.chain_tasks or dependence.iterator is None):
+            return None
+        loops = [statement for statement in body
+                 if isinstance(statement, ast.For)
+                 and isinstance(statement.target, ast.Name)
+                 and statement.target.id == dependence.iterator]
+        if len(loops) != 1 or not _is_range_loop(loops[0]) or (
+                len(loops[0].iter.args) != 2):
+            return None
+        loop = loops[0]
+        # the loop must be the rule's: same bounds once aliases are resolved
+        aliases = structure_aliases(ast.Module(body=body, type_ignores=[]))
+        expected = dependence.thread_loop.iter.args
+        for bound, wanted in zip(loop.iter.args, expected):
+            resolved = aliases.get(bound.id, bound) if isinstance(
+                bound, ast.Name) else bound
+            if ast.unparse(resolved) != ast.unparse(wanted):
+                return None
+        # the wait goes after the statements that leave the loop at the
+        # task's own entry (`if k >= i: break`)
+        split = 0
+        for position, statement in enumerate(loop.body):
+            if (isinstance(statement, ast.If) and len(statement.body) == 1
+                    and isinstance(statement.body[0], ast.Break)
+                    and not statement.orelse):
+                split = position + 1
+                break
+        for statement in loop.body[:split]:
+            for node in ast.walk(statement):
+                if isinstance(node, ast.Subscript) and isinstance(
+                        node.value, ast.Name) and (
+                            node.value.id in self._all_written):
+                    return None          # reads a producer before the wait
+        return {"iterator": dependence.iterator,
+                "endpoint": dependence.endpoint, "remaining": "_lcd_blocked"}
+
     def _gather_plan(self, box, arguments, lifted_loop_parameters):
         """Gathered form of the mailbox protocol: no message slots at all.
 
@@ -1367,7 +1416,13 @@ class HIPLowerer:
                 self.dependence_protocol = PUSH_DEPENDENCE
         self._fully_rewritten = self._fully_rewritten_arrays(
             body, target_loop, zero_initialised)
-        if (self.dependence_protocol == PULL_DEPENDENCE and self.value_flags
+        sequential = (self.direct_dependence is not None
+                      and getattr(self.direct_dependence, "sequential", False))
+        if self.dependence_protocol == PULL_DEPENDENCE and sequential:
+            self._sequential_pull = self._sequential_pull_plan(body)
+            if self._sequential_pull is None:
+                self.dependence_protocol = COUNTER_DEPENDENCE
+        elif (self.dependence_protocol == PULL_DEPENDENCE and self.value_flags
                 and self.execution_mode == "sync_free"):
             self._value_pull = self._value_pull_plan(body)
         if self._mailbox is not None and (
@@ -1422,7 +1477,8 @@ class HIPLowerer:
             if name not in user_arguments:
                 user_arguments.append(name)
         if (self.thread_loop_iterator is not None
-                and self.dependence_protocol != COUNTER_DEPENDENCE):
+                and self.dependence_protocol != COUNTER_DEPENDENCE
+                and self._sequential_pull is None):
             nested = self._find_mapped_loop(body)
             if nested not in body:
                 # hooks describe task-level edges; a nested work-sharing loop
@@ -2273,13 +2329,16 @@ class HIPLowerer:
         part of the inspection fingerprint): read it from a copy in task
         order, ``_lcd_qn_k[_task]``, which the runtime gathers once per
         structure -- one load less on the chain in front of every task."""
-        # persistent executors with value hand-offs only: measured 1-2 %
-        # there; level launches lose 4 % (ILU0, 9-point grid) because rows of
-        # consecutive levels are neighbours, so `Ap[i]` is warm in L2 from the
-        # level before while a queue-ordered copy is cold at every level
+        # persistent executors whose hand-offs are the values themselves
+        # only: measured 1-2 % there; level launches lose 4 % and the flagged
+        # pull 1 % (ILU0, 9-point grid) because rows of consecutive levels
+        # are neighbours, so `Ap[i]` is warm in L2 from the level before
+        # while a queue-ordered copy is cold at every level
+        value_flags = self._value_pull is not None or (
+            self._mailbox is not None and self._mailbox["gather"] is not None)
         if (not self.queue_node_loads_enabled or self.chain_tasks
                 or not self.warp_mapped or self.execution_mode != "sync_free"
-                or self.dependence_protocol == COUNTER_DEPENDENCE):
+                or not value_flags):
             return None
         array = node.value.id
         properties = (self.function_props or {}).get(array, ())
@@ -2394,6 +2453,11 @@ class HIPLowerer:
                     "Device loops must be `for name in range(...)`.")
             lower, upper, step = emitter.range_parts(node)
             name = node.target.id
+            plan = self._sequential_pull
+            if (plan is not None and indent == 0 and not plan.get("emitted")
+                    and name == plan["iterator"] and step == "1"):
+                return self._sequential_pull_lines(node, emitter, hooks,
+                                                   lower, upper)
             if step == "1":
                 head = f"{pad}for ({name} = {lower}; {name} < {upper}; ++{name}) {{"
             else:
@@ -2411,6 +2475,40 @@ class HIPLowerer:
             lines.append(f"{pad}}}")
             return lines
         return emitter.stmt(node, indent, hooks)
+
+    def _sequential_pull_lines(self, node, emitter, hooks, lower, upper):
+        """The task's loop over its producers, resumable: every iteration
+        first checks that its producer has published ``done`` and otherwise
+        leaves the loop with the position kept; the lines between the two
+        markers are re-entered by the executor's poll loop.  The task works
+        on the producers that are finished while it waits for the others."""
+        plan = self._sequential_pull
+        plan["emitted"] = True
+        name = node.target.id
+        # the wait goes after the statements that leave the loop at the
+        # task's own entry (`if k >= i: break`)
+        split = 0
+        for position, statement in enumerate(node.body):
+            if (isinstance(statement, ast.If) and len(statement.body) == 1
+                    and isinstance(statement.body[0], ast.Break)
+                    and not statement.orelse):
+                split = position + 1
+                break
+        endpoint = emitter.expr(plan["endpoint"])
+        waiting = f"lcd_load_relaxed(&done[{endpoint}]) == 0"
+        blocked = (f"!lcd_group_none({waiting})" if self.task_lanes > 1
+                   else waiting)
+        lines = [f"{name} = {lower};", VALUE_WAIT_BEGIN,
+                 "_lcd_blocked = false;",
+                 f"for (; {name} < {upper}; ++{name}) {{"]
+        for child in node.body[:split]:
+            lines += self._emit_guarded(child, emitter, 1, hooks)
+        lines += [f"    if ({blocked}) {{ _lcd_blocked = true; break; }}",
+                  "    lcd_acquire_fence();"]
+        for child in node.body[split:]:
+            lines += self._emit_guarded(child, emitter, 1, hooks)
+        lines += ["}", VALUE_WAIT_END]
+        return lines
 
     # ---- text assembly
     def _c_type(self, name, kind, is_array):
@@ -2543,6 +2641,8 @@ class HIPLowerer:
             ]
         lines.append(f"    lcd_index_t {it} = 0;")
         lines += self._declarations(local_names, 1)
+        if self._sequential_pull is not None:
+            lines.append("    bool _lcd_blocked = false;")
         guard = self._node_guard(target_loop)
 
         prefetch = list(self._prefetch_lines)
@@ -2558,7 +2658,7 @@ class HIPLowerer:
             out.append(f"{pad}}}")
             return out
 
-        if self._value_pull is not None:
+        if self._value_pull is not None or self._sequential_pull is not None:
             begin = task_body.index(VALUE_WAIT_BEGIN)
             end = task_body.index(VALUE_WAIT_END)
             self._value_segments = (task_body[:begin], task_body[begin + 1:end],
@@ -2732,7 +2832,9 @@ class HIPLowerer:
               if protocol == COUNTER_DEPENDENCE else []),
             *([] if records else incoming),
         ]
-        value = self._value_pull
+        value = self._value_pull or self._sequential_pull
+        publishes_done = (protocol == PULL_DEPENDENCE
+                          and self._value_pull is None)
         if value is not None:
             before, waiting, after = self._value_segments
             # everything ahead of the distributed loop reads nothing another
@@ -2746,7 +2848,8 @@ class HIPLowerer:
         if value is not None:
             missing = f"({value['remaining']})"
             none_left = (f"lcd_group_none({missing})"
-                         if 1 < self.task_lanes <= 64 else f"!{missing}")
+                         if 1 < self.task_lanes <= 64
+                         and self._sequential_pull is None else f"!{missing}")
             lines.append("                bool _ready = true;")
             lines += task(4, waiting + [f"_ready = {none_left};"])
         elif protocol == PULL_DEPENDENCE:
@@ -2774,7 +2877,7 @@ class HIPLowerer:
                 "_e < _release_end; _e += LCD_TASK_LANES)",
                 "                        lcd_atomic_sub(&dep_count[dag_index[_e]], 1);",
             ]
-        elif protocol == PULL_DEPENDENCE and value is None:
+        elif publishes_done:
             lines += [
                 f"                    {self.group_sync}",
                 "                    lcd_release_fence();",
@@ -3169,6 +3272,12 @@ class HIPLowerer:
                 # 128^3 grid with 4 lanes per task and on the power-law
                 # matrix with 32)
                 waves_per_cu = max(1, self.task_lanes)
+                if self._sequential_pull is not None:
+                    # tasks that work while they wait (a long body full of
+                    # device-coherent loads): one wavefront per CU measured
+                    # best on the 9-point grid (16.2 ms; 16.8 / 17.6 / 18.4
+                    # at 2 / 4 / 8, 17.5 at one per two CUs)
+                    waves_per_cu = 1
             if self._tile is not None:
                 # one workgroup per tile; residency is bounded by the LDS the
                 # tile takes, not by a polling budget

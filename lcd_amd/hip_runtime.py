@@ -808,8 +808,9 @@ class LaunchContext:
         blocks = self.device.resident_blocks(self.module.kernel(name), block)
         if waves_per_cu:
             waves_per_block = max(1, (block + 63) // 64)
-            cap = (self.device.props.compute_units * int(waves_per_cu)
-                   + waves_per_block - 1) // waves_per_block
+            # (a fraction leaves CUs without a workgroup: narrow DAGs)
+            cap = -(-int(self.device.props.compute_units
+                         * float(waves_per_cu)) // waves_per_block)
             blocks = min(blocks, max(cap, 1))
         return blocks
 

@@ -326,6 +326,13 @@ ILU_VARIANTS = [
     dict(execution_mode="sync_free", threads_per_block=128, n_warp=1),
     dict(execution_mode="wavefront", threads_per_block=128, n_warp=2),
     dict(execution_mode=None, threads_per_block=None),
+    # the task waits for its pivot rows one by one
+    dict(execution_mode="sync_free", threads_per_block=64, task_lanes=8,
+         dependence_protocol="pull"),
+    dict(execution_mode="sync_free", threads_per_block=128, task_lanes=1,
+         dependence_protocol="pull"),
+    dict(execution_mode="sync_free", threads_per_block=128, task_lanes=64,
+         dependence_protocol="pull", segment_cache=False),
 ]
 
 
@@ -345,6 +352,19 @@ def test_ilu0_csr_variants(oracle, options):
     assert len(factor.structural_lookups) == 1
     assert factor.structural_lookups[0].name in factor.hip_kernel_source
     assert "for (diag_ptr" not in factor.hip_kernel_source
+    if options.get("dependence_protocol") == "pull":
+        assert factor.hip_lowering.dependence_protocol == "pull"
+        assert "_lcd_blocked" in factor.hip_kernel_source
+        # irregular rows too: pivots near and far, empty lower parts
+        import scipy.sparse as sp
+        lower, diagonal, _ = random_lower_factor(2500, 11)
+        matrix = sp.csr_matrix(lower + lower.T * 0.5 + sp.diags(4 * diagonal))
+        matrix.sort_indices()
+        indptr = matrix.indptr.astype(np.int32)
+        indices = matrix.indices.astype(np.int32)
+        np.testing.assert_array_equal(
+            factor(matrix.data.copy(), indices, indptr),
+            oracle.ilu0_csr(matrix.data, indices, indptr))
 
 
 @pytest.mark.parametrize("mode", ["wavefront", "sync_free", None])

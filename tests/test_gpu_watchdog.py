@@ -109,3 +109,54 @@ def test_unsatisfiable_wait_trips_the_watchdog(oracle, name, props, protocol,
                                           {"np": np})
     scale = float(np.max(np.abs(expected)))
     assert float(np.max(np.abs(result - expected))) / scale <= 1e-12
+
+
+def test_ilu0_pivot_wait_trips_the_watchdog(oracle):
+    """The per-pivot wait of ILU0 (pull on the task's own loop): a producer
+    that never runs ends the launch through the watchdog, and the next call
+    with the intact queue factorises."""
+    from lcd_amd.demo import spilu0
+    from lcd_amd.structural_lookups import (create_structural_lookup_plan,
+                                            materialize_structural_lookups)
+    print("watchdog ilu0 pull", flush=True)
+    module = ast.parse(inspect.getsource(spilu0.ilu0_csr))
+    props = spilu0.FUNCTION_PROPS
+    analysis = analyze_dependences(module, "i", props)
+    plan = create_dag_plan(analysis.ordering_dependences, None, "i",
+                           ["A_data", "A_indices", "A_indptr", "n"])
+    lookups = create_structural_lookup_plan(module, props)
+    lowering = lower_to_hip(
+        module, "i", reductions=analysis, function_props=props,
+        execution_mode="sync_free", thread_loop_iterator="j_ptr",
+        task_lanes=8, wavefront_threads_per_block=64,
+        dependence_protocol="pull",
+        direct_dependence=direct_dependence(plan, "j_ptr"),
+        structural_lookups=lookups, spin_limit=3000)
+    assert lowering.dependence_protocol == "pull"
+    assert "_lcd_blocked" in lowering.kernel_source
+    compiled = hip_runtime.compile_hip_module(lowering, {"np": np})
+    work = workloads.configuration("c4", nx=40, ny=30)
+    device = hip_runtime.default_device()
+    dag = device.dag_build(
+        [oracle.rule_ilu0_csr(work.indptr, work.indices)], work.n, levels=True)
+    good = P.execution_data_from_device_dag(dag, "sync_free", True)
+    nodes = dag.host("wavefronts").copy()
+    assert nodes[0] == 0
+    nodes[0] = nodes[-1]
+    bad = replace(good, task_nodes=device.to_device(nodes))
+    arguments = {"A_data": work.data.copy(), "A_indices": work.indices,
+                 "A_indptr": work.indptr}
+    tables = materialize_structural_lookups(lookups, arguments, device)
+    prepared = hip_runtime.prepare_hip_arguments(
+        lowering, arguments, P.attach_auxiliary_values(bad, tables),
+        {"np": np})
+    with pytest.raises(hip_runtime.ExecutorWatchdogError):
+        hip_runtime.execute_hip_call(compiled, lowering, prepared, {"np": np})
+    arguments["A_data"] = work.data.copy()
+    prepared = hip_runtime.prepare_hip_arguments(
+        lowering, arguments, P.attach_auxiliary_values(good, tables),
+        {"np": np})
+    result = hip_runtime.execute_hip_call(compiled, lowering, prepared,
+                                          {"np": np})
+    np.testing.assert_array_equal(
+        result, oracle.ilu0_csr(work.data, work.indices, work.indptr))

@@ -700,6 +700,54 @@ def test_structure_arrays_are_read_in_task_order():
         assert "_nl_1 = Ap[i];" in other.kernel_source
 
 
+def test_ilu0_waits_for_its_pivots_one_by_one():
+    """The pull protocol on a sequential loop of the task: resumable, the
+    wait for row k sits at the top of the iteration that uses row k."""
+    module = demo_source("spilu0", "ilu0_csr")
+    analysis = analyze_dependences(module, "i", ILU_PROPS)
+    plan = create_dag_plan(analysis.ordering_dependences, None, "i", [])
+    dependence = direct_dependence(plan, "j_ptr")
+    assert dependence.kind == "pull" and dependence.sequential
+    assert dependence.iterator == "k_ptr"
+    assert ast.unparse(dependence.endpoint) == "A_indices[k_ptr]"
+    assert direct_dependence(plan, None) is None
+    lookups = create_structural_lookup_plan(module, ILU_PROPS)
+    result = lower(module, function_props=ILU_PROPS,
+                   execution_mode="sync_free", thread_loop_iterator="j_ptr",
+                   task_lanes=8, wavefront_threads_per_block=64,
+                   dependence_protocol="pull", structural_lookups=lookups)
+    kernel = result.kernel_source
+    assert result.dependence_protocol == "pull"
+    assert "done" in result.kernel_arguments
+    assert "dep_count" not in result.kernel_arguments
+    # staged once before the first poll, resumed inside the poll loop
+    before, inside = kernel.split("while (__ballot(_pending))")
+    assert "k_ptr = row_start;" in before and "_lcd_seg[_q] =" in before
+    assert "for (; k_ptr < row_end; ++k_ptr) {" in inside
+    assert inside.index("if ((k >= i)) {") < inside.index(
+        "if (!lcd_group_none(lcd_load_relaxed(&done[A_indices[k_ptr]]) == 0))"
+        " { _lcd_blocked = true; break; }") < inside.index("diag_val = 0.0;")
+    assert "_ready = !(_lcd_blocked);" in inside
+    assert "__hip_atomic_store(&done[i], 1" in inside
+    hip_runtime.compile_code(result.source)
+    # level launches and whole-workgroup tasks keep the counters
+    for options in (dict(execution_mode="wavefront"),
+                    dict(execution_mode="sync_free", n_warp=2,
+                         wavefront_threads_per_block=128)):
+        options.setdefault("wavefront_threads_per_block", 64)
+        if "n_warp" not in options:
+            options["task_lanes"] = 8
+        other = lower(module, function_props=ILU_PROPS,
+                      thread_loop_iterator="j_ptr",
+                      dependence_protocol="pull", structural_lookups=lookups,
+                      **options)
+        assert "_lcd_blocked" not in other.kernel_source
+    # the scheduler may now choose it
+    space = S.ScheduleSpace.from_options(thread_mapped=True,
+                                         direct_protocol="pull")
+    assert space.dependence_protocols == ("counter", "pull")
+
+
 def test_mailbox_needs_no_clear_of_the_solution():
     module = demo_source("sptrsv", "sptrsv_csc_loop")
     result = lower(module, execution_mode="sync_free",
@@ -884,9 +932,10 @@ def test_runtime_layer_accepts_an_injected_device():
     assert result.tolist() == [0.0, 0.0] and launches[-1] == "sync"
     # structure arrays in task order are gathered by the device layer, once
     # per workspace
-    queued = lower(module, execution_mode="sync_free",
-                   thread_loop_iterator="j", task_lanes=4,
-                   dependence_protocol="push", queue_node_loads=True)
+    queued = lower(demo_source("sptrsv", "sptrsv_csr_loop"),
+                   execution_mode="sync_free", thread_loop_iterator="j",
+                   task_lanes=4, dependence_protocol="pull",
+                   queue_node_loads=True)
     assert [q[1:] for q in queued.queue_node_loads] == [("Ap", 0), ("Ap", 1)]
     workspace = {}
     for _ in range(2):
