@@ -55,6 +55,7 @@ MEASURED_TRAFFIC = {
     ("c2", "sync_free", "push", 4): 1_937_433_319,
     ("c2", "sync_free", "mailbox", 4): 531_082_379,
     ("c3", "sync_free", "pull", 64): 1_529_588_218,
+    ("c4", "sync_free", "pull", 8): 1_223_430_234,
 }
 
 

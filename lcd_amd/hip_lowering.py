@@ -2494,6 +2494,21 @@ class HIPLowerer:
                     and not statement.orelse):
                 split = position + 1
                 break
+        # ... and after the plain assignments that follow and read nothing
+        # another task writes (`diag_ptr = lookup[k]`): structure loads that
+        # would otherwise sit between the wait and the first use of row k
+        while split < len(node.body):
+            statement = node.body[split]
+            if not (isinstance(statement, ast.Assign)
+                    and all(isinstance(t, ast.Name) for t in statement.targets)):
+                break
+            if any(isinstance(sub, ast.Call) or (
+                    isinstance(sub, ast.Subscript)
+                    and isinstance(sub.value, ast.Name)
+                    and sub.value.id in self._all_written)
+                   for sub in ast.walk(statement)):
+                break
+            split += 1
         endpoint = emitter.expr(plan["endpoint"])
         waiting = f"lcd_load_relaxed(&done[{endpoint}]) == 0"
         blocked = (f"!lcd_group_none({waiting})" if self.task_lanes > 1

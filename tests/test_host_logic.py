@@ -724,9 +724,13 @@ def test_ilu0_waits_for_its_pivots_one_by_one():
     before, inside = kernel.split("while (__ballot(_pending))")
     assert "k_ptr = row_start;" in before and "_lcd_seg[_q] =" in before
     assert "for (; k_ptr < row_end; ++k_ptr) {" in inside
+    # the wait sits after the break at the own entry and after the structure
+    # loads that follow, ahead of the first read of the pivot row
     assert inside.index("if ((k >= i)) {") < inside.index(
+        "diag_ptr = _lcd_lookup_position_0[k];") < inside.index(
         "if (!lcd_group_none(lcd_load_relaxed(&done[A_indices[k_ptr]]) == 0))"
-        " { _lcd_blocked = true; break; }") < inside.index("diag_val = 0.0;")
+        " { _lcd_blocked = true; break; }") < inside.index(
+        "diag_val = lcd_seg_ldc(A_data")
     assert "_ready = !(_lcd_blocked);" in inside
     assert "__hip_atomic_store(&done[i], 1" in inside
     hip_runtime.compile_code(result.source)
