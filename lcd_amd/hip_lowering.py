@@ -2509,14 +2509,30 @@ class HIPLowerer:
                    for sub in ast.walk(statement)):
                 break
             split += 1
+        early = self._locate_ahead_of_wait(node.body[split:], hooks)
         endpoint = emitter.expr(plan["endpoint"])
         waiting = f"lcd_load_relaxed(&done[{endpoint}]) == 0"
         blocked = (f"!lcd_group_none({waiting})" if self.task_lanes > 1
                    else waiting)
-        lines = [f"{name} = {lower};", VALUE_WAIT_BEGIN,
+        if early:
+            # once per iteration of the producer loop, not once per poll
+            self._own_registers.append("_sp_at")
+            self._kinds.locals["_sp_at"] = INT
+            early = [ast.fix_missing_locations(ast.If(
+                test=ast.Compare(left=ast.Name(id="_sp_at", ctx=ast.Load()),
+                                 ops=[ast.NotEq()],
+                                 comparators=[ast.Name(id=name, ctx=ast.Load())]),
+                body=[ast.Assign(
+                    targets=[ast.Name(id="_sp_at", ctx=ast.Store())],
+                    value=ast.Name(id=name, ctx=ast.Load())), *early],
+                orelse=[]))]
+        lines = [f"{name} = {lower};",
+                 *(["_sp_at = -1;"] if early else []), VALUE_WAIT_BEGIN,
                  "_lcd_blocked = false;",
                  f"for (; {name} < {upper}; ++{name}) {{"]
         for child in node.body[:split]:
+            lines += self._emit_guarded(child, emitter, 1, hooks)
+        for child in early:
             lines += self._emit_guarded(child, emitter, 1, hooks)
         lines += [f"    if ({blocked}) {{ _lcd_blocked = true; break; }}",
                   "    lcd_acquire_fence();"]
@@ -2524,6 +2540,89 @@ class HIPLowerer:
             lines += self._emit_guarded(child, emitter, 1, hooks)
         lines += ["}", VALUE_WAIT_END]
         return lines
+
+    def _locate_ahead_of_wait(self, statements, hooks):
+        """The thread-mapped loop nested in a resumable producer loop starts
+        with structure work (`j = A_indices[j_ptr]; kj_ptr = find(...)`)
+        that reads nothing another task writes.  For each lane's first
+        iteration it is done ahead of the wait for the producer (into
+        ``_sp_*`` registers the loop then picks up), which takes the search
+        of the pivot row off the chain between two levels.  Returns the
+        statements to run before the wait; the loop is rewritten in place."""
+        if hooks is None or self.thread_unroll_factor != 1:
+            return []
+        mapped = None
+        for statement in statements:
+            for sub in ast.walk(statement):
+                if isinstance(sub, ast.For) and hooks.is_mapped(sub):
+                    mapped = sub
+        if mapped is None or len(mapped.iter.args) != 2 or not isinstance(
+                mapped.target, ast.Name):
+            return []
+        iterator = mapped.target.id
+        structural = []
+        for statement in mapped.body:
+            if not (isinstance(statement, ast.Assign)
+                    and len(statement.targets) == 1
+                    and isinstance(statement.targets[0], ast.Name)):
+                break
+            reads_written = any(
+                isinstance(sub, ast.Subscript) and isinstance(sub.value, ast.Name)
+                and sub.value.id in self._all_written
+                for sub in ast.walk(statement))
+            calls = [sub for sub in ast.walk(statement)
+                     if isinstance(sub, ast.Call)]
+            if reads_written or any(
+                    not (isinstance(call.func, ast.Name)
+                         and call.func.id == "_lcd_sorted_find")
+                    for call in calls):
+                break
+            structural.append(statement)
+        if not structural:
+            return []
+        names = {statement.targets[0].id for statement in structural}
+        renamed = {name: f"_sp_{name}" for name in names}
+        renamed[iterator] = "_sp_first"
+
+        class Rename(ast.NodeTransformer):
+            def visit_Name(self, node):
+                if node.id in renamed:
+                    return ast.copy_location(
+                        ast.Name(id=renamed[node.id], ctx=node.ctx), node)
+                return node
+
+        kinds = self._kinds
+        for name in names:
+            kinds.locals[renamed[name]] = kinds.locals.get(name, INT)
+        kinds.locals["_sp_first"] = INT
+        self._own_registers.extend(["_sp_first", *sorted(
+            renamed[name] for name in names)])
+        lower, upper = mapped.iter.args
+        first = ast.Assign(
+            targets=[ast.Name(id="_sp_first", ctx=ast.Store())],
+            value=ast.BinOp(left=deepcopy(lower), op=ast.Add(),
+                            right=ast.Name(id="_lane", ctx=ast.Load())))
+        ahead = ast.If(
+            test=ast.Compare(left=ast.Name(id="_sp_first", ctx=ast.Load()),
+                             ops=[ast.Lt()], comparators=[deepcopy(upper)]),
+            body=[Rename().visit(deepcopy(statement))
+                  for statement in structural],
+            orelse=[])
+        pick_up = ast.If(
+            test=ast.Compare(left=ast.Name(id=iterator, ctx=ast.Load()),
+                             ops=[ast.Eq()],
+                             comparators=[ast.Name(id="_sp_first",
+                                                   ctx=ast.Load())]),
+            body=[ast.Assign(
+                targets=[ast.Name(id=statement.targets[0].id, ctx=ast.Store())],
+                value=ast.Name(id=renamed[statement.targets[0].id],
+                               ctx=ast.Load())) for statement in structural],
+            orelse=list(structural))
+        mapped.body = [pick_up] + mapped.body[len(structural):]
+        early = [first, ahead]
+        for statement in early + [pick_up]:
+            ast.fix_missing_locations(statement)
+        return early
 
     # ---- text assembly
     def _c_type(self, name, kind, is_array):
