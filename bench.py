@@ -39,8 +39,8 @@ TUNED = {
     "c3": dict(execution_mode="sync_free", threads_per_block=128,
                task_lanes=64, thread_unroll=1,
                dependence_protocol="pull", tile_rows=None),
-    "c4": dict(execution_mode="sync_free", threads_per_block=64, task_lanes=8,
-               thread_unroll=1, dependence_protocol="pull"),
+    "c4": dict(execution_mode="sync_free", threads_per_block=128,
+               task_lanes=64, thread_unroll=1, dependence_protocol="pull"),
     "c5": dict(execution_mode="sync_free", threads_per_block=256, task_lanes=8,
                thread_unroll=1, dependence_protocol="mailbox",
                tile_rows=4096),
@@ -55,7 +55,8 @@ MEASURED_TRAFFIC = {
     ("c2", "sync_free", "push", 4): 1_937_433_319,
     ("c2", "sync_free", "mailbox", 4): 531_082_379,
     ("c3", "sync_free", "pull", 64): 1_529_588_218,
-    ("c4", "sync_free", "pull", 8): 1_223_430_234,
+    ("c4", "sync_free", "pull", 64): 1_366_116_319,
+    
 }
 
 

@@ -272,7 +272,9 @@ def parallel(**kwargs):
         schedule_space = ScheduleSpace.from_options(
             **space_options,
             direct_protocol=None if dependence is None else dependence.kind,
-            dependence_protocol=kwargs.get("dependence_protocol"))
+            dependence_protocol=kwargs.get("dependence_protocol"),
+            sequential_pull=bool(dependence is not None
+                                 and dependence.sequential))
         lowered_variants.clear()   # protocols are known only now
         fixed_schedule = (schedule_space.fixed_schedule()
                           if schedule_space.is_fixed else None)

@@ -2509,7 +2509,7 @@ class HIPLowerer:
                    for sub in ast.walk(statement)):
                 break
             split += 1
-        early = self._locate_ahead_of_wait(node.body[split:], hooks)
+        early, fetched = self._locate_ahead_of_wait(node.body[split:], hooks)
         endpoint = emitter.expr(plan["endpoint"])
         waiting = f"lcd_load_relaxed(&done[{endpoint}]) == 0"
         blocked = (f"!lcd_group_none({waiting})" if self.task_lanes > 1
@@ -2536,6 +2536,8 @@ class HIPLowerer:
             lines += self._emit_guarded(child, emitter, 1, hooks)
         lines += [f"    if ({blocked}) {{ _lcd_blocked = true; break; }}",
                   "    lcd_acquire_fence();"]
+        for child in fetched:
+            lines += self._emit_guarded(child, emitter, 1, hooks)
         for child in node.body[split:]:
             lines += self._emit_guarded(child, emitter, 1, hooks)
         lines += ["}", VALUE_WAIT_END]
@@ -2550,7 +2552,7 @@ class HIPLowerer:
         of the pivot row off the chain between two levels.  Returns the
         statements to run before the wait; the loop is rewritten in place."""
         if hooks is None or self.thread_unroll_factor != 1:
-            return []
+            return [], []
         mapped = None
         for statement in statements:
             for sub in ast.walk(statement):
@@ -2558,7 +2560,7 @@ class HIPLowerer:
                     mapped = sub
         if mapped is None or len(mapped.iter.args) != 2 or not isinstance(
                 mapped.target, ast.Name):
-            return []
+            return [], []
         iterator = mapped.target.id
         structural = []
         for statement in mapped.body:
@@ -2579,7 +2581,7 @@ class HIPLowerer:
                 break
             structural.append(statement)
         if not structural:
-            return []
+            return [], []
         names = {statement.targets[0].id for statement in structural}
         renamed = {name: f"_sp_{name}" for name in names}
         renamed[iterator] = "_sp_first"
@@ -2618,11 +2620,88 @@ class HIPLowerer:
                 value=ast.Name(id=renamed[statement.targets[0].id],
                                ctx=ast.Load())) for statement in structural],
             orelse=list(structural))
-        mapped.body = [pick_up] + mapped.body[len(structural):]
+        rest = mapped.body[len(structural):]
+        fetched = self._fetch_behind_wait(rest, iterator, names, renamed, upper)
+        mapped.body = [pick_up] + rest
         early = [first, ahead]
-        for statement in early + [pick_up]:
+        for statement in early + fetched + [pick_up]:
             ast.fix_missing_locations(statement)
-        return early
+        return early, fetched
+
+    def _fetch_behind_wait(self, rest, iterator, names, renamed, upper):
+        """After the structure work the nested loop reads the producer's
+        values at the positions just found (`if kj_ptr >= 0: u = A[kj_ptr]`).
+        For each lane's first iteration those loads are issued right behind
+        the wait, together with the first load the task makes of the
+        producer (its diagonal), instead of one dependent round trip later.
+        Valid because a pull rule means the task writes only its own element
+        or segment: nothing it does in between changes what it reads here."""
+        if not (rest and isinstance(rest[0], ast.If) and not rest[0].orelse):
+            return []
+        guard = rest[0]
+        known = set(names)
+        for sub in ast.walk(guard.test):
+            if isinstance(sub, (ast.Subscript, ast.Call)) or (
+                    isinstance(sub, ast.Name) and sub.id == iterator):
+                return []
+        loads = {}
+
+        def eligible(node):
+            if not (isinstance(node, ast.Subscript)
+                    and isinstance(node.ctx, ast.Load)
+                    and isinstance(node.value, ast.Name)
+                    and node.value.id in self._all_written):
+                return False
+            used = {n.id for n in ast.walk(node.slice)
+                    if isinstance(n, ast.Name)}
+            if iterator in used or not (used & known):
+                return False
+            return not any(isinstance(n, (ast.Subscript, ast.Call))
+                           for n in ast.walk(node.slice))
+
+        class Hoist(ast.NodeTransformer):
+            def visit_Subscript(self, node):
+                if not eligible(node):
+                    return self.generic_visit(node)
+                text = ast.unparse(node)
+                if text not in loads:
+                    loads[text] = (f"_sp_ld_{len(loads)}", deepcopy(node))
+                return ast.copy_location(ast.IfExp(
+                    test=ast.Compare(
+                        left=ast.Name(id=iterator, ctx=ast.Load()),
+                        ops=[ast.Eq()],
+                        comparators=[ast.Name(id="_sp_first", ctx=ast.Load())]),
+                    body=ast.Name(id=loads[text][0], ctx=ast.Load()),
+                    orelse=node), node)
+
+        # only loads the guarded block makes unconditionally
+        guard.body = [
+            Hoist().visit(statement) if isinstance(
+                statement, (ast.Assign, ast.AugAssign)) else statement
+            for statement in guard.body]
+        if not loads:
+            return []
+
+        class Rename(ast.NodeTransformer):
+            def visit_Name(self, node):
+                if node.id in renamed:
+                    return ast.copy_location(
+                        ast.Name(id=renamed[node.id], ctx=node.ctx), node)
+                return node
+
+        kinds = self._kinds
+        body = []
+        for name, node in loads.values():
+            kinds.locals[name] = kinds.arrays.get(node.value.id, FLOAT)
+            self._own_registers.append(name)
+            body.append(ast.Assign(
+                targets=[ast.Name(id=name, ctx=ast.Store())],
+                value=Rename().visit(node)))
+        test = ast.BoolOp(op=ast.And(), values=[
+            ast.Compare(left=ast.Name(id="_sp_first", ctx=ast.Load()),
+                        ops=[ast.Lt()], comparators=[deepcopy(upper)]),
+            Rename().visit(deepcopy(guard.test))])
+        return [ast.If(test=test, body=body, orelse=[])]
 
     # ---- text assembly
     def _c_type(self, name, kind, is_array):
@@ -3388,10 +3467,12 @@ class HIPLowerer:
                 waves_per_cu = max(1, self.task_lanes)
                 if self._sequential_pull is not None:
                     # tasks that work while they wait (a long body full of
-                    # device-coherent loads): one wavefront per CU measured
-                    # best on the 9-point grid (16.2 ms; 16.8 / 17.6 / 18.4
-                    # at 2 / 4 / 8, 17.5 at one per two CUs)
-                    waves_per_cu = 1
+                    # device-coherent loads): about eight per CU measured
+                    # best on the 9-point grid (8 lanes per task: 16.2 ms at
+                    # one wavefront per CU, 16.8 / 17.6 / 18.4 at 2 / 4 / 8,
+                    # 17.5 at one per two CUs; 64 lanes: 10.8 / 10.9 / 11.2
+                    # at 6 / 8 / 12)
+                    waves_per_cu = max(1, self.task_lanes // 8)
             if self._tile is not None:
                 # one workgroup per tile; residency is bounded by the LDS the
                 # tile takes, not by a polling budget
