@@ -292,6 +292,11 @@ class ScheduleSpace:
             # (one hop per edge, deterministic sums); the lowering falls back
             # to the push protocol for loop shapes the mailbox cannot express
             protocols = (MAILBOX_DEPENDENCE,)
+        elif PULL_DEPENDENCE in available and sequential_pull:
+            # waiting for each producer where it is used beats waiting for
+            # all of them up front (ILU0: 10.9 ms against 35 ms); the
+            # lowering falls back to counters for loops it cannot resume
+            protocols = (PULL_DEPENDENCE,)
         elif PULL_DEPENDENCE in available and searched:
             protocols = (COUNTER_DEPENDENCE, PULL_DEPENDENCE)
         else:
