@@ -54,7 +54,7 @@ TUNED = {
 MEASURED_TRAFFIC = {
     ("c2", "sync_free", "push", 4): 1_937_433_319,
     ("c2", "sync_free", "mailbox", 4): 531_082_379,
-    ("c3", "sync_free", "pull", 64): 1_529_588_218,
+    ("c3", "sync_free", "pull", 64): 1_511_667_523,
     ("c4", "sync_free", "pull", 64): 1_366_116_319,
     
 }
@@ -84,6 +84,8 @@ def build_solver(work, args):
         options["tile_rows"] = args.tile_rows or None
     if args.no_queue_loads:
         options["queue_node_loads"] = False
+    if args.plain_first is not None:
+        options["plain_first_polls"] = bool(args.plain_first)
     if args.slots:
         options["gather_messages"] = False
         options["tile_rows"] = None
@@ -182,6 +184,9 @@ def main():
     parser.add_argument("--no-queue-loads", action="store_true",
                         help="read structure arrays through the task id "
                              "instead of copies in task order")
+    parser.add_argument("--plain-first", type=int, default=None,
+                        help="1: poll a producer's value with a plain load "
+                             "and confirm only the empty marker coherently")
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-check", action="store_true")
     parser.add_argument("--arch", action="store_true",

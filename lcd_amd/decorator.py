@@ -211,6 +211,7 @@ def parallel(**kwargs):
                                   and kwargs.get("task_records", True)),
                     single_chunk=single_chunk,
                     queue_node_loads=kwargs.get("queue_node_loads", True),
+                    plain_first_polls=kwargs.get("plain_first_polls"),
                 )
             return lowered_variants[variant_key]
 

@@ -504,6 +504,46 @@ def test_device_resident_operands(device, oracle):
     assert relative_error(result, expected) <= TOLERANCE
 
 
+PLAIN_FIRST_VARIANTS = [
+    ("c3", dict(execution_mode="sync_free", threads_per_block=128,
+                task_lanes=64, dependence_protocol="pull")),
+    ("c2", dict(execution_mode="sync_free", threads_per_block=256,
+                task_lanes=4, dependence_protocol="mailbox")),
+    ("c2", dict(execution_mode="sync_free", threads_per_block=128,
+                task_lanes=4, dependence_protocol="mailbox", tile_rows=None)),
+]
+
+
+@pytest.mark.parametrize("name,options", PLAIN_FIRST_VARIANTS, ids=lambda v: (
+    v if isinstance(v, str) else f"{v['dependence_protocol']}-"
+    f"{'flat' if 'tile_rows' in v else 'auto'}"))
+@pytest.mark.parametrize("grid", [12, 40])
+def test_plain_first_polls_see_no_value_of_an_earlier_launch(
+        device, oracle, name, options, grid):
+    """A poll that accepts a plain load's value must never meet the solution
+    of the launch before: one bound call is launched over and over with a new
+    right-hand side each time."""
+    csr = name == "c3"
+    work = (workloads.configuration(name, n=grid ** 3) if csr else
+            workloads.configuration(name, nx=grid, ny=grid, nz=grid))
+    compile_solver = (sptrsv.compile_sptrsv_csr if csr
+                      else sptrsv.compile_sptrsv_csc)
+    reference = oracle.sptrsv_csr if csr else oracle.sptrsv_csc
+    solver = compile_solver(plain_first_polls=True, **options)
+    operands = [device.to_device(a) for a in
+                (work.indptr, work.indices, work.data, work.rhs)]
+    call = solver.bind(*operands, work.n)
+    assert "lcd_ld_once(&" in solver.hip_lowering.kernel_source
+    rng = np.random.default_rng(grid)
+    for launch in range(6):
+        rhs = work.rhs * (launch + 1) + rng.random(work.n)
+        device.copy(operands[3], device.to_device(rhs))
+        call.launch()
+        call.synchronize()
+        expected = reference(work.indptr, work.indices, work.data, rhs, work.n)
+        assert relative_error(np.asarray(call.result()), expected) <= TOLERANCE
+
+
 FULL_SIZE = [("c2", "sptrsv_csc"), ("c4", "ilu0"), ("c3", "sptrsv_csr"),
              ("c5", "sptrsv_csc")]
 

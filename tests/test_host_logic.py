@@ -568,8 +568,13 @@ def test_csr_pull_polls_the_values_themselves():
     assert result.executor_initialised == ("x",)
     assert "done" not in result.kernel_arguments
     assert "done" not in kernel
-    assert "double _lcd_vf = lcd_ld(&x[" in kernel
+    # plain load first, the empty marker alone is confirmed coherently
+    assert "double _lcd_vf = lcd_ld_once(&x[" in kernel
     assert "if (lcd_is_empty(_lcd_vf))" in kernel
+    coherent = lower(module, execution_mode="sync_free",
+                     thread_loop_iterator="j", task_lanes=4,
+                     dependence_protocol="pull", plain_first_polls=False)
+    assert "double _lcd_vf = lcd_ld(&x[" in coherent.kernel_source
     assert "for (; j < " in kernel          # resumes, does not restart
     assert "lcd_release_fence" not in kernel.split("while (true)")[1]
     assert "_lcd_values[2 * t] = LCD_EMPTY_WORD" in result.source
