@@ -212,6 +212,8 @@ def parallel(**kwargs):
                     single_chunk=single_chunk,
                     queue_node_loads=kwargs.get("queue_node_loads", True),
                     plain_first_polls=kwargs.get("plain_first_polls"),
+                    publish_values=kwargs.get("publish_values", True),
+                    look_ahead=kwargs.get("look_ahead", True),
                 )
             return lowered_variants[variant_key]
 

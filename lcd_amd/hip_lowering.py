@@ -147,6 +147,7 @@ class HIPLoweringResult:
     # the start of every launch (gathered mailbox), and its argument names
     task_record_lanes: int | None = None
     queue_node_loads: tuple = ()     # (argument, structure array, offset)
+    published_array: str | None = None   # its final values go to _lcd_pub
     stage_kernel_name: str | None = None
     stage_kernel_arguments: tuple = ()
     # tiled persistent executor: block-iterator values per tile, or None
@@ -358,6 +359,7 @@ class _Emitter:
         self.mailbox = None
         self.lowerer = None
         self.segment = None     # own-segment staging plan (HIPLowerer)
+        self.published = None   # final values published to a flagged buffer
         self.tile = None        # tiled executor plan (HIPLowerer)
 
     # ---- expressions
@@ -378,6 +380,12 @@ class _Emitter:
                 raise HIPLoweringError("Only 1-D array indexing is supported.")
             element = f"{node.value.id}[{self.expr(node.slice)}]"
             segment = self.segment
+            if (segment is not None and node.value.id == segment["array"]
+                    and self.published is not None):
+                return (f"lcd_seg_ldp({node.value.id}, _lcd_pub, _lcd_seg, "
+                        "_lcd_seg_base, _lcd_seg_limit, _lcd_seg_own, "
+                        f"{self.expr(node.slice)}, {STATUS_ARGUMENT}, "
+                        "_task_aborted)")
             if segment is not None and node.value.id == segment["array"]:
                 name = ("lcd_seg_ldc" if node.value.id in self.coherent_arrays
                         else "lcd_seg_ld")
@@ -454,6 +462,16 @@ class _Emitter:
                 return f"(lcd_index_t)({args[0]})"
             if name == "_lcd_sorted_find" and len(args) == 4:
                 return f"lcd_sorted_find({', '.join(args)})"
+            if name == "_lcd_raw" and self.published is not None:
+                target = node.args[0]
+                return (f"lcd_seg_ldr({target.value.id}, _lcd_pub, _lcd_seg, "
+                        "_lcd_seg_base, _lcd_seg_limit, _lcd_seg_own, "
+                        f"{self.expr(target.slice)})")
+            if name == "_lcd_settle" and self.published is not None:
+                target = node.args[0]
+                return ("lcd_seg_settle(_lcd_pub, _lcd_seg_base, _lcd_seg_own, "
+                        f"{self.expr(target.slice)}, {args[1]}, "
+                        f"{STATUS_ARGUMENT}, _task_aborted)")
         raise HIPLoweringError(
             f"Unsupported expression in a device loop: {ast.unparse(node)!r}.")
 
@@ -719,6 +737,53 @@ __device__ __forceinline__ double lcd_ld_once(const double* p) {
     if (lcd_is_empty(v)) v = lcd_ld(p);
     return v;
 }
+// Published values: a task works on its own segment (staged in LDS, or in
+// place when it does not fit) and ends by storing the final values to a
+// buffer that started as the empty marker; a read of another task's element
+// polls that buffer.  With one task per wavefront in queue order the poll may
+// block: the producer sits earlier in the queue and waits for nobody behind.
+__device__ __forceinline__ double lcd_pull_settle(const double* pub, lcd_index_t p,
+                                                  double v, int* status, bool& aborted) {
+    unsigned spins = 0;
+    while (lcd_is_empty(v) && !aborted) {
+#if LCD_SPIN_SLEEP > 0
+        __builtin_amdgcn_s_sleep(LCD_SPIN_SLEEP);
+#endif
+        v = lcd_ld(&pub[p]);
+        if ((++spins & 1023u) == 0u && (spins > (unsigned)LCD_SPIN_LIMIT
+                                        || lcd_load_relaxed(status) != 0)) {
+            status[0] = 1;
+            aborted = true;
+            break;
+        }
+    }
+    return v;
+}
+// first attempt only: the load is in flight while the task does other work
+__device__ __forceinline__ double lcd_seg_ldr(const double* x, const double* pub,
+                                              const double* seg, lcd_index_t base,
+                                              lcd_index_t limit, lcd_index_t own,
+                                              lcd_index_t p) {
+    const unsigned off = (unsigned)(p - base);
+    if (off < (unsigned)limit) return seg[off];
+    return off < (unsigned)own ? lcd_ld(&x[p]) : lcd_ld(&pub[p]);
+}
+// ... and the wait for it where the value is used
+__device__ __forceinline__ double lcd_seg_settle(const double* pub, lcd_index_t base,
+                                                 lcd_index_t own, lcd_index_t p,
+                                                 double v, int* status, bool& aborted) {
+    const unsigned off = (unsigned)(p - base);
+    return off < (unsigned)own ? v : lcd_pull_settle(pub, p, v, status, aborted);
+}
+__device__ __forceinline__ double lcd_seg_ldp(const double* x, const double* pub,
+                                              const double* seg, lcd_index_t base,
+                                              lcd_index_t limit, lcd_index_t own,
+                                              lcd_index_t p, int* status, bool& aborted) {
+    const unsigned off = (unsigned)(p - base);
+    if (off < (unsigned)limit) return seg[off];
+    if (off < (unsigned)own) return lcd_ld(&x[p]);
+    return lcd_pull_settle(pub, p, lcd_ld(&pub[p]), status, aborted);
+}
 __device__ __forceinline__ double lcd_empty() {
     return __longlong_as_double((long long)0x7FF84C437FF84C43ull);
 }
@@ -962,8 +1027,12 @@ class HIPLowerer:
                  prefetch_node_loads=True, value_flags=True,
                  gather_messages=True, segment_cache=True, tile_rows=None,
                  stage_operands=True, task_records=True, single_chunk=False,
-                 queue_node_loads=True, plain_first_polls=None):
+                 queue_node_loads=True, plain_first_polls=None,
+                 publish_values=True, look_ahead=True):
+        self.look_ahead = look_ahead
         self.queue_node_loads_enabled = queue_node_loads
+        self.publish_values = publish_values
+        self._published = None
         self.plain_first_polls = plain_first_polls
         # accessors of a producer's value-flagged element.  Unless the option
         # says otherwise the pull loop tries a plain load first (the value is
@@ -1460,6 +1529,19 @@ class HIPLowerer:
             coherent.discard(self._mailbox["array"])
         if self.segment_cache and not self.block_task:
             self._segment = self._segment_plan(body, arguments)
+        if (self.publish_values and self._sequential_pull is not None
+                and self._segment is not None and self.task_lanes == 64
+                and set(self._all_written) == {self._segment["array"]}
+                and kinds.arrays.get(self._segment["array"]) == FLOAT):
+            # One row per wavefront, every write inside the task's own
+            # segment: the final values are the messages.  They go to a
+            # buffer of the array's size that starts as the empty marker, a
+            # read of another task's element polls it there, and `done`, the
+            # release fence ahead of it and the acquire behind the wait all
+            # disappear from the chain between two levels.
+            self._published = {"array": self._segment["array"],
+                               "buffer": "_lcd_pub"}
+            kinds.arrays["_lcd_pub"] = FLOAT
         if self.tile_rows:
             self._tile = self._tile_plan(target_loop)
         if (self.task_records and self._mailbox is not None
@@ -1479,6 +1561,7 @@ class HIPLowerer:
         emitter = _Emitter(kinds, self.reductions, lowered_ids,
                            coherent_arrays=coherent)
         emitter.segment = self._segment
+        emitter.published = self._published
         emitter.tile = self._tile
         emitter.mailbox = self._mailbox
         emitter.lowerer = self
@@ -1590,6 +1673,8 @@ class HIPLowerer:
                                  if self._mailbox else None),
             tile_rows=self._tile["rows"] if self._tile else None,
             queue_node_loads=tuple(self._queue_node_loads),
+            published_array=(self._published["array"]
+                             if self._published else None),
             task_record_lanes=(
                 self.task_lanes if self._mailbox
                 and self._mailbox["gather"]
@@ -1714,7 +1799,8 @@ class HIPLowerer:
                   and self._value_pull is not None):
                 names = list(VALUE_PULL_ARGUMENTS)
             elif self.dependence_protocol == PULL_DEPENDENCE:
-                names = list(PULL_ARGUMENTS)
+                names = ["_lcd_pub" if name == "done" and self._published
+                         else name for name in PULL_ARGUMENTS]
             elif (self.dependence_protocol == MAILBOX_DEPENDENCE
                   and self._mailbox["gather"] is not None):
                 gather = self._mailbox["gather"]
@@ -1959,6 +2045,7 @@ class HIPLowerer:
         prologue = [
             f"_lcd_seg_base = {bound(0)};",
             f"_lcd_seg_limit = {bound(1)} - _lcd_seg_base;",
+            *(["_lcd_seg_own = _lcd_seg_limit;"] if self._published else []),
             "if (_lcd_seg_limit > LCD_SEG_CAP) _lcd_seg_limit = 0;",
             "for (int _q = _lane; _q < _lcd_seg_limit; _q += LCD_TASK_LANES) "
             f"_lcd_seg[_q] = {load};",
@@ -1969,6 +2056,20 @@ class HIPLowerer:
             "for (int _q = _lane; _q < _lcd_seg_limit; _q += LCD_TASK_LANES) "
             + store,
         ]
+        if self._published:
+            # the messages first (consumers wait for them), then the array
+            # itself; a segment too long for LDS was updated in place and is
+            # read back
+            epilogue = [
+                self.group_sync,
+                "for (int _q = _lane; _q < _lcd_seg_limit; _q += LCD_TASK_LANES) "
+                "lcd_st(&_lcd_pub[_lcd_seg_base + _q], _lcd_seg[_q]);",
+                "if (_lcd_seg_limit == 0) for (int _q = _lane; _q < _lcd_seg_own; "
+                "_q += LCD_TASK_LANES) lcd_st(&_lcd_pub[_lcd_seg_base + _q], "
+                f"lcd_ld(&{array}[_lcd_seg_base + _q]));",
+                "for (int _q = _lane; _q < _lcd_seg_limit; _q += LCD_TASK_LANES) "
+                f"{array}[_lcd_seg_base + _q] = _lcd_seg[_q];",
+            ]
         return prologue, epilogue
 
     def _forward_stores(self, statements, mapped_loop):
@@ -2515,19 +2616,35 @@ class HIPLowerer:
         # ... and after the plain assignments that follow and read nothing
         # another task writes (`diag_ptr = lookup[k]`): structure loads that
         # would otherwise sit between the wait and the first use of row k
+        # From the first search on (`diag_ptr = find(row k, k)`) they run
+        # once per iteration instead of once per poll.
+        searches = None
         while split < len(node.body):
             statement = node.body[split]
             if not (isinstance(statement, ast.Assign)
                     and all(isinstance(t, ast.Name) for t in statement.targets)):
                 break
-            if any(isinstance(sub, ast.Call) or (
-                    isinstance(sub, ast.Subscript)
-                    and isinstance(sub.value, ast.Name)
-                    and sub.value.id in self._all_written)
+            if any(isinstance(sub, ast.Subscript)
+                   and isinstance(sub.value, ast.Name)
+                   and sub.value.id in self._all_written
                    for sub in ast.walk(statement)):
                 break
+            calls = [sub for sub in ast.walk(statement)
+                     if isinstance(sub, ast.Call)]
+            if any(not (isinstance(call.func, ast.Name)
+                        and call.func.id == "_lcd_sorted_find")
+                   for call in calls):
+                break
+            if calls and searches is None:
+                searches = split
             split += 1
+        once = [] if searches is None else node.body[searches:split]
+        every_poll = split if searches is None else searches
         early, fetched = self._locate_ahead_of_wait(node.body[split:], hooks)
+        early = list(once) + early
+        if self._published is not None and self.look_ahead:
+            return self._pipelined_pull_lines(
+                node, emitter, hooks, lower, every_poll, split, early, fetched)
         endpoint = emitter.expr(plan["endpoint"])
         waiting = f"lcd_load_relaxed(&done[{endpoint}]) == 0"
         blocked = (f"!lcd_group_none({waiting})" if self.task_lanes > 1
@@ -2548,18 +2665,149 @@ class HIPLowerer:
                  *(["_sp_at = -1;"] if early else []), VALUE_WAIT_BEGIN,
                  "_lcd_blocked = false;",
                  f"for (; {name} < {upper}; ++{name}) {{"]
-        for child in node.body[:split]:
+        for child in node.body[:every_poll]:
             lines += self._emit_guarded(child, emitter, 1, hooks)
         for child in early:
             lines += self._emit_guarded(child, emitter, 1, hooks)
-        lines += [f"    if ({blocked}) {{ _lcd_blocked = true; break; }}",
-                  "    lcd_acquire_fence();"]
+        if self._published is None:
+            lines += [f"    if ({blocked}) {{ _lcd_blocked = true; break; }}",
+                      "    lcd_acquire_fence();"]
         for child in fetched:
             lines += self._emit_guarded(child, emitter, 1, hooks)
         for child in node.body[split:]:
             lines += self._emit_guarded(child, emitter, 1, hooks)
         lines += ["}", VALUE_WAIT_END]
         return lines
+
+    def _pipelined_pull_lines(self, node, emitter, hooks, lower, every_poll,
+                              split, structure, fetched):
+        """The producer loop with published values, one iteration ahead in
+        its structure work.  An iteration issues the first loads of its
+        producer's values, then locates what the *next* iteration will read
+        (the next producer's row is searched while this one's values are on
+        their way or not even stored yet), then waits for its values and
+        works.  What is left between the arrival of a producer's values and
+        the publication of the task's own is arithmetic."""
+        name = node.target.id
+        upper = node.iter.args[1]
+        leading = list(node.body[:every_poll])
+        leave = next((position for position, statement in enumerate(leading)
+                      if isinstance(statement, ast.If)
+                      and len(statement.body) == 1
+                      and isinstance(statement.body[0], ast.Break)), None)
+        before = leading if leave is None else leading[:leave]
+        after = [] if leave is None else leading[leave + 1:]
+        located = [statement for statement in before
+                   if isinstance(statement, ast.Assign)] + list(structure)
+        names = []
+        for statement in located:
+            for sub in ast.walk(statement):
+                if (isinstance(sub, ast.Name) and isinstance(sub.ctx, ast.Store)
+                        and sub.id not in names):
+                    names.append(sub.id)
+        kinds = self._kinds
+        for local in names:
+            kinds.locals[f"_nx_{local}"] = kinds.locals.get(local, INT)
+            self._own_registers.append(f"_nx_{local}")
+
+        def ahead(offset):
+            position = (ast.Name(id=name, ctx=ast.Load()) if offset == 0 else
+                        ast.BinOp(left=ast.Name(id=name, ctx=ast.Load()),
+                                  op=ast.Add(), right=ast.Constant(value=offset)))
+
+            class Shift(ast.NodeTransformer):
+                def visit_Name(self, sub):
+                    if sub.id in names:
+                        return ast.copy_location(
+                            ast.Name(id=f"_nx_{sub.id}", ctx=sub.ctx), sub)
+                    if sub.id == name:
+                        return ast.copy_location(deepcopy(position), sub)
+                    return sub
+
+            shifted = [Shift().visit(deepcopy(statement))
+                       for statement in before if isinstance(statement, ast.Assign)]
+            body = [Shift().visit(deepcopy(statement)) for statement in structure]
+            if leave is not None:
+                body = [ast.If(test=ast.UnaryOp(
+                    op=ast.Not(), operand=Shift().visit(
+                        deepcopy(leading[leave].test))), body=body, orelse=[])]
+            return ast.fix_missing_locations(ast.If(
+                test=ast.Compare(left=deepcopy(position), ops=[ast.Lt()],
+                                 comparators=[deepcopy(upper)]),
+                body=shifted + body, orelse=[]))
+
+        take_over = [ast.fix_missing_locations(ast.Assign(
+            targets=[ast.Name(id=local, ctx=ast.Store())],
+            value=ast.Name(id=f"_nx_{local}", ctx=ast.Load())))
+            for local in names]
+        rest = list(node.body[split:])
+        first_loads = list(fetched) + self._split_leading_loads(rest)
+        lines = [f"{name} = {lower};"]
+        lines += self._emit_guarded(ahead(0), emitter, 0, hooks)
+        lines += [VALUE_WAIT_BEGIN, "_lcd_blocked = false;",
+                  f"for (; {name} < {emitter.expr(upper)}; ++{name}) {{"]
+        for child in take_over + ([] if leave is None else [leading[leave]]):
+            lines += self._emit_guarded(child, emitter, 1, hooks)
+        for child in [s for s in before if not isinstance(s, ast.Assign)] + after:
+            lines += self._emit_guarded(child, emitter, 1, hooks)
+        for child in first_loads + [ahead(1)] + rest:
+            lines += self._emit_guarded(child, emitter, 1, hooks)
+        lines += ["}", VALUE_WAIT_END]
+        return lines
+
+    def _split_leading_loads(self, rest):
+        """Leading statements of the form ``[if structure:] x = X[p]`` (the
+        producer's diagonal): the first attempt of the load is issued with
+        the other first loads and the statement waits for the value.
+        Returns the issuing statements; ``rest`` is rewritten in place."""
+        issued = []
+
+        def structural(expression):
+            return not any(
+                isinstance(sub, ast.Call) or (
+                    isinstance(sub, ast.Subscript)
+                    and isinstance(sub.value, ast.Name)
+                    and sub.value.id in self._all_written)
+                for sub in ast.walk(expression))
+
+        def split_assign(assign):
+            if not (isinstance(assign, ast.Assign) and len(assign.targets) == 1
+                    and isinstance(assign.targets[0], ast.Name)
+                    and isinstance(assign.value, ast.Subscript)
+                    and isinstance(assign.value.value, ast.Name)
+                    and assign.value.value.id == self._published["array"]
+                    and structural(assign.value.slice)):
+                return None
+            register = f"_sp_ld_h{len(issued)}"
+            self._kinds.locals[register] = FLOAT
+            self._own_registers.append(register)
+            load = ast.Assign(
+                targets=[ast.Name(id=register, ctx=ast.Store())],
+                value=ast.Call(func=ast.Name(id="_lcd_raw", ctx=ast.Load()),
+                               args=[deepcopy(assign.value)], keywords=[]))
+            assign.value = ast.Call(
+                func=ast.Name(id="_lcd_settle", ctx=ast.Load()),
+                args=[assign.value, ast.Name(id=register, ctx=ast.Load())],
+                keywords=[])
+            return load
+
+        for statement in rest:
+            if (isinstance(statement, ast.If) and not statement.orelse
+                    and structural(statement.test)
+                    and len(statement.body) == 1):
+                load = split_assign(statement.body[0])
+                if load is None:
+                    break
+                issued.append(ast.If(test=deepcopy(statement.test),
+                                     body=[load], orelse=[]))
+            else:
+                load = split_assign(statement)
+                if load is None:
+                    break
+                issued.append(load)
+        for statement in issued + rest:
+            ast.fix_missing_locations(statement)
+        return issued
 
     def _locate_ahead_of_wait(self, statements, hooks):
         """The thread-mapped loop nested in a resumable producer loop starts
@@ -2663,6 +2911,7 @@ class HIPLowerer:
                     isinstance(sub, ast.Name) and sub.id == iterator):
                 return []
         loads = {}
+        published = self._published is not None
 
         def eligible(node):
             if not (isinstance(node, ast.Subscript)
@@ -2684,13 +2933,18 @@ class HIPLowerer:
                 text = ast.unparse(node)
                 if text not in loads:
                     loads[text] = (f"_sp_ld_{len(loads)}", deepcopy(node))
+                held = ast.Name(id=loads[text][0], ctx=ast.Load())
+                if published:
+                    # the first attempt may have met the empty marker
+                    held = ast.Call(
+                        func=ast.Name(id="_lcd_settle", ctx=ast.Load()),
+                        args=[deepcopy(node), held], keywords=[])
                 return ast.copy_location(ast.IfExp(
                     test=ast.Compare(
                         left=ast.Name(id=iterator, ctx=ast.Load()),
                         ops=[ast.Eq()],
                         comparators=[ast.Name(id="_sp_first", ctx=ast.Load())]),
-                    body=ast.Name(id=loads[text][0], ctx=ast.Load()),
-                    orelse=node), node)
+                    body=held, orelse=node), node)
 
         # only loads the guarded block makes unconditionally
         guard.body = [
@@ -2712,9 +2966,12 @@ class HIPLowerer:
         for name, node in loads.values():
             kinds.locals[name] = kinds.arrays.get(node.value.id, FLOAT)
             self._own_registers.append(name)
+            value = Rename().visit(node)
+            if published:
+                value = ast.Call(func=ast.Name(id="_lcd_raw", ctx=ast.Load()),
+                                 args=[value], keywords=[])
             body.append(ast.Assign(
-                targets=[ast.Name(id=name, ctx=ast.Store())],
-                value=Rename().visit(node)))
+                targets=[ast.Name(id=name, ctx=ast.Store())], value=value))
         test = ast.BoolOp(op=ast.And(), values=[
             ast.Compare(left=ast.Name(id="_sp_first", ctx=ast.Load()),
                         ops=[ast.Lt()], comparators=[deepcopy(upper)]),
@@ -2783,7 +3040,7 @@ class HIPLowerer:
                    written_arrays):
         parts = []
         mutable_executor = {"dep_count", "task_counter", "done",
-                            STATUS_ARGUMENT, "_lcd_mailbox"}
+                            STATUS_ARGUMENT, "_lcd_mailbox", "_lcd_pub"}
         for name in kernel_arguments:
             if name in array_arguments:
                 const = (name not in written_arrays
@@ -2849,6 +3106,7 @@ class HIPLowerer:
                 f"    LCD_T_{array}* const _lcd_seg = &_lcd_seg_store["
                 "(threadIdx.x / LCD_TASK_LANES) * LCD_SEG_CAP];",
                 "    lcd_index_t _lcd_seg_base = 0, _lcd_seg_limit = 0;",
+                *(["    lcd_index_t _lcd_seg_own = 0;"] if self._published else []),
             ]
         lines.append(f"    lcd_index_t {it} = 0;")
         lines += self._declarations(local_names, 1)
@@ -3045,7 +3303,8 @@ class HIPLowerer:
         ]
         value = self._value_pull or self._sequential_pull
         publishes_done = (protocol == PULL_DEPENDENCE
-                          and self._value_pull is None)
+                          and self._value_pull is None
+                          and self._published is None)
         if value is not None:
             before, waiting, after = self._value_segments
             # everything ahead of the distributed loop reads nothing another
@@ -3384,7 +3643,7 @@ class HIPLowerer:
             signature = ("unsigned int* _lcd_mailbox, int* task_counter, "
                          "long long count")
         elif (self.dependence_protocol == PULL_DEPENDENCE
-              and self._value_pull is not None):
+              and (self._value_pull is not None or self._published)):
             body = ("    if (t < count) { _lcd_values[2 * t] = LCD_EMPTY_WORD; "
                     "_lcd_values[2 * t + 1] = LCD_EMPTY_WORD; }\n"
                     "    if (t == 0) { task_counter[0] = 0; }\n")
@@ -3446,11 +3705,12 @@ class HIPLowerer:
                                self.dependence_protocol, "dep_count")
             reset_count = "_count"
             if ((self.dependence_protocol == PULL_DEPENDENCE
-                 and self._value_pull is not None)
+                 and (self._value_pull is not None or self._published))
                     or (self.dependence_protocol == MAILBOX_DEPENDENCE
                         and self._mailbox["gather"] is not None)):
                 count_array = "task_nodes"
-                values = (self._value_pull or self._mailbox)["array"]
+                values = ("_lcd_pub" if self._published else
+                          (self._value_pull or self._mailbox)["array"])
                 reset_args = (f"({values}, task_counter, "
                               f"_hip.length({values}))")
                 reset_count = f"_hip.length({values})"
@@ -3522,7 +3782,8 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
                  prefetch_node_loads=True, value_flags=True,
                  gather_messages=True, segment_cache=True, tile_rows=None,
                  stage_operands=True, task_records=True, single_chunk=False,
-                 queue_node_loads=True, plain_first_polls=None):
+                 queue_node_loads=True, plain_first_polls=None,
+                 publish_values=True, look_ahead=True):
     """HIP counterpart of ``lower_to_numba_cuda``
     (compiler/cuda_lowering.py:2854-2884); same parameters plus
     ``task_lanes`` (lanes cooperating on one task, a power of two <= 64),
@@ -3546,5 +3807,6 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
         tile_rows=tile_rows, stage_operands=stage_operands,
         task_records=task_records, single_chunk=single_chunk,
         queue_node_loads=queue_node_loads,
-        plain_first_polls=plain_first_polls)
+        plain_first_polls=plain_first_polls, publish_values=publish_values,
+        look_ahead=look_ahead)
     return lowerer.lower(code)

@@ -1022,6 +1022,14 @@ def prepare_hip_arguments(lowering, argument_values, execution_data,
                 cached = device.empty((slots,), np.float64)
                 workspace[("state", "_lcd_mailbox")] = cached
             host_values["_lcd_mailbox"] = cached
+        if "_lcd_pub" in lowering.launcher_arguments:
+            # final values of the published array, one slot per element
+            slots = max(len(host_values[lowering.published_array]), 1)
+            cached = workspace.get(("state", "_lcd_pub"))
+            if cached is None or len(cached) != slots:
+                cached = device.empty((slots,), np.float64)
+                workspace[("state", "_lcd_pub")] = cached
+            host_values["_lcd_pub"] = cached
         for name in lowering.launcher_arguments:
             if not name.startswith("_lcd_staged_"):
                 continue

@@ -333,6 +333,11 @@ ILU_VARIANTS = [
          dependence_protocol="pull"),
     dict(execution_mode="sync_free", threads_per_block=128, task_lanes=64,
          dependence_protocol="pull", segment_cache=False),
+    # one row per wavefront: final values published, polled by the readers
+    dict(execution_mode="sync_free", threads_per_block=128, task_lanes=64,
+         dependence_protocol="pull"),
+    dict(execution_mode="sync_free", threads_per_block=256, task_lanes=64,
+         dependence_protocol="pull", publish_values=False),
 ]
 
 
@@ -355,6 +360,11 @@ def test_ilu0_csr_variants(oracle, options):
     if options.get("dependence_protocol") == "pull":
         assert factor.hip_lowering.dependence_protocol == "pull"
         assert "_lcd_blocked" in factor.hip_kernel_source
+        published = (options["task_lanes"] == 64
+                     and options.get("segment_cache", True)
+                     and options.get("publish_values", True))
+        assert ("_lcd_pub" in factor.hip_kernel_source) == published
+        assert ("done[" in factor.hip_kernel_source) != published
         # irregular rows too: pivots near and far, empty lower parts
         import scipy.sparse as sp
         lower, diagonal, _ = random_lower_factor(2500, 11)
@@ -417,6 +427,29 @@ def test_ilu0_dense_pattern_is_lu(oracle):
     lower = np.tril(result, -1) + np.eye(n)
     upper = np.triu(result)
     np.testing.assert_allclose(lower @ upper, dense, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("n", [24, 48, 150])
+def test_ilu0_published_values_on_long_rows(oracle, n):
+    """Rows that fit the staged segment, rows that are updated in place and
+    read back for publication, rows longer than a wavefront; the same bound
+    call factorises three matrices in a row."""
+    rng = np.random.default_rng(n)
+    indptr = np.arange(0, n * n + 1, n, dtype=np.int32)
+    indices = np.tile(np.arange(n, dtype=np.int32), n)
+    factor = spilu0.compile_ilu0_csr(execution_mode="sync_free",
+                                     threads_per_block=128, task_lanes=64,
+                                     dependence_protocol="pull")
+    for launch in range(3):
+        dense = rng.uniform(-1, 1, (n, n)) + n * np.eye(n)
+        result = factor(dense.ravel().copy(), indices, indptr)
+        assert "_lcd_pub" in factor.hip_kernel_source
+        np.testing.assert_array_equal(
+            result, oracle.ilu0_csr(dense.ravel(), indices, indptr))
+        result = result.reshape(n, n)
+        lower = np.tril(result, -1) + np.eye(n)
+        np.testing.assert_allclose(lower @ np.triu(result), dense,
+                                   rtol=1e-12, atol=1e-12)
 
 
 @pytest.mark.parametrize("variant", ["simple", "full"])

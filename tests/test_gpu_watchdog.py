@@ -111,14 +111,17 @@ def test_unsatisfiable_wait_trips_the_watchdog(oracle, name, props, protocol,
     assert float(np.max(np.abs(result - expected))) / scale <= 1e-12
 
 
-def test_ilu0_pivot_wait_trips_the_watchdog(oracle):
-    """The per-pivot wait of ILU0 (pull on the task's own loop): a producer
-    that never runs ends the launch through the watchdog, and the next call
-    with the intact queue factorises."""
+@pytest.mark.parametrize("lanes,tpb", [(8, 64), (64, 128)],
+                         ids=["done-flags", "published-values"])
+def test_ilu0_pivot_wait_trips_the_watchdog(oracle, lanes, tpb):
+    """The per-pivot wait of ILU0 (pull on the task's own loop; polls of the
+    producers' published values with one row per wavefront): a producer that
+    never runs ends the launch through the watchdog, and the next call with
+    the intact queue factorises."""
     from lcd_amd.demo import spilu0
     from lcd_amd.structural_lookups import (create_structural_lookup_plan,
                                             materialize_structural_lookups)
-    print("watchdog ilu0 pull", flush=True)
+    print("watchdog ilu0 pull", lanes, flush=True)
     module = ast.parse(inspect.getsource(spilu0.ilu0_csr))
     props = spilu0.FUNCTION_PROPS
     analysis = analyze_dependences(module, "i", props)
@@ -128,12 +131,13 @@ def test_ilu0_pivot_wait_trips_the_watchdog(oracle):
     lowering = lower_to_hip(
         module, "i", reductions=analysis, function_props=props,
         execution_mode="sync_free", thread_loop_iterator="j_ptr",
-        task_lanes=8, wavefront_threads_per_block=64,
+        task_lanes=lanes, wavefront_threads_per_block=tpb,
         dependence_protocol="pull",
         direct_dependence=direct_dependence(plan, "j_ptr"),
         structural_lookups=lookups, spin_limit=3000)
     assert lowering.dependence_protocol == "pull"
     assert "_lcd_blocked" in lowering.kernel_source
+    assert (lowering.published_array == "A_data") == (lanes == 64)
     compiled = hip_runtime.compile_hip_module(lowering, {"np": np})
     work = workloads.configuration("c4", nx=40, ny=30)
     device = hip_runtime.default_device()
