@@ -86,6 +86,10 @@ def build_solver(work, args):
         options["queue_node_loads"] = False
     if args.plain_first is not None:
         options["plain_first_polls"] = bool(args.plain_first)
+    if args.look_ahead is not None:
+        options["look_ahead"] = args.look_ahead == "1"
+    if args.no_publish:
+        options["publish_values"] = False
     if args.slots:
         options["gather_messages"] = False
         options["tile_rows"] = None
@@ -187,6 +191,12 @@ def main():
     parser.add_argument("--plain-first", type=int, default=None,
                         help="1: poll a producer's value with a plain load "
                              "and confirm only the empty marker coherently")
+    parser.add_argument("--look-ahead", default=None,
+                        choices=("0", "1"),
+                        help="published pull: locate the next producer's "
+                             "values while waiting for this one's (default 1)")
+    parser.add_argument("--no-publish", action="store_true",
+                        help="pull on a sequential loop through done flags")
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-check", action="store_true")
     parser.add_argument("--arch", action="store_true",
