@@ -55,7 +55,7 @@ MEASURED_TRAFFIC = {
     ("c2", "sync_free", "push", 4): 1_937_433_319,
     ("c2", "sync_free", "mailbox", 4): 531_082_379,
     ("c3", "sync_free", "pull", 64): 1_511_667_523,
-    ("c4", "sync_free", "pull", 64): 1_366_116_319,
+    ("c4", "sync_free", "pull", 64): 1_177_308_398,
     
 }
 
