@@ -214,6 +214,7 @@ def parallel(**kwargs):
                     plain_first_polls=kwargs.get("plain_first_polls"),
                     publish_values=kwargs.get("publish_values", True),
                     look_ahead=kwargs.get("look_ahead", True),
+                    segment_capacity=kwargs.get("segment_capacity"),
                 )
             return lowered_variants[variant_key]
 

@@ -1031,8 +1031,9 @@ class HIPLowerer:
                  gather_messages=True, segment_cache=True, tile_rows=None,
                  stage_operands=True, task_records=True, single_chunk=False,
                  queue_node_loads=True, plain_first_polls=None,
-                 publish_values=True, look_ahead=True):
+                 publish_values=True, look_ahead=True, segment_capacity=None):
         self.look_ahead = look_ahead
+        self.segment_capacity = segment_capacity
         self.queue_node_loads_enabled = queue_node_loads
         self.publish_values = publish_values
         self._published = None
@@ -2022,7 +2023,12 @@ class HIPLowerer:
         if len(pointers) != 1:
             return None
         groups = max(1, self.threads_per_block // self.task_lanes)
-        capacity = min(32, 4096 // groups)
+        # entries per task: 32 where a wavefront holds several tasks; with a
+        # wavefront per task the rows of real factors (hundreds of entries)
+        # fit as well -- 8 KB per wavefront, 64 KB per CU at eight resident
+        capacity = min(1024 if self.task_lanes == 64 else 32, 4096 // groups)
+        if self.segment_capacity is not None:
+            capacity = int(self.segment_capacity)
         if capacity < 8:
             return None
         return {"array": array, "pointer": next(iter(pointers)),
@@ -3797,7 +3803,7 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
                  gather_messages=True, segment_cache=True, tile_rows=None,
                  stage_operands=True, task_records=True, single_chunk=False,
                  queue_node_loads=True, plain_first_polls=None,
-                 publish_values=True, look_ahead=True):
+                 publish_values=True, look_ahead=True, segment_capacity=None):
     """HIP counterpart of ``lower_to_numba_cuda``
     (compiler/cuda_lowering.py:2854-2884); same parameters plus
     ``task_lanes`` (lanes cooperating on one task, a power of two <= 64),
@@ -3822,5 +3828,5 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
         task_records=task_records, single_chunk=single_chunk,
         queue_node_loads=queue_node_loads,
         plain_first_polls=plain_first_polls, publish_values=publish_values,
-        look_ahead=look_ahead)
+        look_ahead=look_ahead, segment_capacity=segment_capacity)
     return lowerer.lower(code)

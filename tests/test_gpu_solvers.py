@@ -429,17 +429,20 @@ def test_ilu0_dense_pattern_is_lu(oracle):
     np.testing.assert_allclose(lower @ upper, dense, rtol=1e-12, atol=1e-12)
 
 
-@pytest.mark.parametrize("n", [24, 48, 150])
-def test_ilu0_published_values_on_long_rows(oracle, n):
+@pytest.mark.parametrize("n,capacity", [(24, None), (48, 32), (150, 32),
+                                        (150, None)])
+def test_ilu0_published_values_on_long_rows(oracle, n, capacity):
     """Rows that fit the staged segment, rows that are updated in place and
-    read back for publication, rows longer than a wavefront; the same bound
-    call factorises three matrices in a row."""
+    read back for publication (a small staging capacity forces that path),
+    rows longer than a wavefront; the same bound call factorises three
+    matrices in a row."""
     rng = np.random.default_rng(n)
     indptr = np.arange(0, n * n + 1, n, dtype=np.int32)
     indices = np.tile(np.arange(n, dtype=np.int32), n)
     factor = spilu0.compile_ilu0_csr(execution_mode="sync_free",
                                      threads_per_block=128, task_lanes=64,
-                                     dependence_protocol="pull")
+                                     dependence_protocol="pull",
+                                     segment_capacity=capacity)
     for launch in range(3):
         dense = rng.uniform(-1, 1, (n, n)) + n * np.eye(n)
         result = factor(dense.ravel().copy(), indices, indptr)
