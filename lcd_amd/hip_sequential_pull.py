@@ -1,0 +1,411 @@
+"""Pull protocol on a sequential loop of the task (ILU0's pivot loop): the
+resumable loop with `done` flags and the pipelined loop over published
+values."""
+
+import ast
+
+from copy import deepcopy
+from lcd_amd.hip_emitter import (
+    FLOAT,
+    INT,
+    VALUE_WAIT_BEGIN,
+    VALUE_WAIT_END,
+)
+
+
+class SequentialPullMixin:
+    """Methods of ``HIPLowerer`` (lcd_amd/hip_lowering.py)."""
+
+    def _sequential_pull_lines(self, node, emitter, hooks, lower, upper):
+        """The task's loop over its producers, resumable: every iteration
+        first checks that its producer has published ``done`` and otherwise
+        leaves the loop with the position kept; the lines between the two
+        markers are re-entered by the executor's poll loop.  The task works
+        on the producers that are finished while it waits for the others."""
+        plan = self._sequential_pull
+        plan["emitted"] = True
+        name = node.target.id
+        # the wait goes after the statements that leave the loop at the
+        # task's own entry (`if k >= i: break`)
+        split = 0
+        for position, statement in enumerate(node.body):
+            if (isinstance(statement, ast.If) and len(statement.body) == 1
+                    and isinstance(statement.body[0], ast.Break)
+                    and not statement.orelse):
+                split = position + 1
+                break
+        # ... and after the plain assignments that follow and read nothing
+        # another task writes (`diag_ptr = lookup[k]`): structure loads that
+        # would otherwise sit between the wait and the first use of row k
+        # From the first search on (`diag_ptr = find(row k, k)`) they run
+        # once per iteration instead of once per poll.
+        searches = None
+        while split < len(node.body):
+            statement = node.body[split]
+            if not (isinstance(statement, ast.Assign)
+                    and all(isinstance(t, ast.Name) for t in statement.targets)):
+                break
+            if any(isinstance(sub, ast.Subscript)
+                   and isinstance(sub.value, ast.Name)
+                   and sub.value.id in self._all_written
+                   for sub in ast.walk(statement)):
+                break
+            calls = [sub for sub in ast.walk(statement)
+                     if isinstance(sub, ast.Call)]
+            if any(not (isinstance(call.func, ast.Name)
+                        and call.func.id == "_lcd_sorted_find")
+                   for call in calls):
+                break
+            if calls and searches is None:
+                searches = split
+            split += 1
+        once = [] if searches is None else node.body[searches:split]
+        every_poll = split if searches is None else searches
+        early, fetched = self._locate_ahead_of_wait(node.body[split:], hooks)
+        early = list(once) + early
+        if self._published is not None and self.look_ahead:
+            lines = self._pipelined_pull_lines(
+                node, emitter, hooks, lower, every_poll, split, early, fetched)
+            if lines is not None:
+                return lines
+        endpoint = emitter.expr(plan["endpoint"])
+        waiting = f"lcd_load_relaxed(&done[{endpoint}]) == 0"
+        blocked = (f"!lcd_group_none({waiting})" if self.task_lanes > 1
+                   else waiting)
+        if early:
+            # once per iteration of the producer loop, not once per poll
+            self._own_registers.append("_sp_at")
+            self._kinds.locals["_sp_at"] = INT
+            early = [ast.fix_missing_locations(ast.If(
+                test=ast.Compare(left=ast.Name(id="_sp_at", ctx=ast.Load()),
+                                 ops=[ast.NotEq()],
+                                 comparators=[ast.Name(id=name, ctx=ast.Load())]),
+                body=[ast.Assign(
+                    targets=[ast.Name(id="_sp_at", ctx=ast.Store())],
+                    value=ast.Name(id=name, ctx=ast.Load())), *early],
+                orelse=[]))]
+        lines = [f"{name} = {lower};",
+                 *(["_sp_at = -1;"] if early else []), VALUE_WAIT_BEGIN,
+                 "_lcd_blocked = false;",
+                 f"for (; {name} < {upper}; ++{name}) {{"]
+        for child in node.body[:every_poll]:
+            lines += self._emit_guarded(child, emitter, 1, hooks)
+        for child in early:
+            lines += self._emit_guarded(child, emitter, 1, hooks)
+        if self._published is None:
+            lines += [f"    if ({blocked}) {{ _lcd_blocked = true; break; }}",
+                      "    lcd_acquire_fence();"]
+        for child in fetched:
+            lines += self._emit_guarded(child, emitter, 1, hooks)
+        for child in node.body[split:]:
+            lines += self._emit_guarded(child, emitter, 1, hooks)
+        lines += ["}", VALUE_WAIT_END]
+        return lines
+
+    def _pipelined_pull_lines(self, node, emitter, hooks, lower, every_poll,
+                              split, structure, fetched):
+        """The producer loop with published values, one iteration ahead in
+        its structure work.  An iteration issues the first loads of its
+        producer's values, then locates what the *next* iteration will read
+        (the next producer's row is searched while this one's values are on
+        their way or not even stored yet), then waits for its values and
+        works.  What is left between the arrival of a producer's values and
+        the publication of the task's own is arithmetic."""
+        name = node.target.id
+        upper = node.iter.args[1]
+        leading = list(node.body[:every_poll])
+        leave = next((position for position, statement in enumerate(leading)
+                      if isinstance(statement, ast.If)
+                      and len(statement.body) == 1
+                      and isinstance(statement.body[0], ast.Break)), None)
+        before = leading if leave is None else leading[:leave]
+        after = [] if leave is None else leading[leave + 1:]
+        if not all(isinstance(statement, ast.Assign) and all(
+                isinstance(target, ast.Name) for target in statement.targets)
+                   for statement in before + after):
+            return None
+        # everything an iteration sets up before it reads its producer is
+        # located one iteration ahead, `diag_ptr = table[k]` included
+        structure = after + list(structure)
+        located = before + structure
+        names = []
+        for statement in located:
+            for sub in ast.walk(statement):
+                if (isinstance(sub, ast.Name) and isinstance(sub.ctx, ast.Store)
+                        and sub.id not in names):
+                    names.append(sub.id)
+        kinds = self._kinds
+        for local in names:
+            kinds.locals[f"_nx_{local}"] = kinds.locals.get(local, INT)
+            self._own_registers.append(f"_nx_{local}")
+
+        def ahead(offset):
+            position = (ast.Name(id=name, ctx=ast.Load()) if offset == 0 else
+                        ast.BinOp(left=ast.Name(id=name, ctx=ast.Load()),
+                                  op=ast.Add(), right=ast.Constant(value=offset)))
+
+            class Shift(ast.NodeTransformer):
+                def visit_Name(self, sub):
+                    if sub.id in names:
+                        return ast.copy_location(
+                            ast.Name(id=f"_nx_{sub.id}", ctx=sub.ctx), sub)
+                    if sub.id == name:
+                        return ast.copy_location(deepcopy(position), sub)
+                    return sub
+
+            shifted = [Shift().visit(deepcopy(statement))
+                       for statement in before]
+            body = [Shift().visit(deepcopy(statement)) for statement in structure]
+            if leave is not None:
+                body = [ast.If(test=ast.UnaryOp(
+                    op=ast.Not(), operand=Shift().visit(
+                        deepcopy(leading[leave].test))), body=body, orelse=[])]
+            return ast.fix_missing_locations(ast.If(
+                test=ast.Compare(left=deepcopy(position), ops=[ast.Lt()],
+                                 comparators=[deepcopy(upper)]),
+                body=shifted + body, orelse=[]))
+
+        rest = list(node.body[split:])
+        leading_loads = self._split_leading_loads(rest)
+        first_loads = list(fetched) + leading_loads
+        take_over = [ast.fix_missing_locations(ast.Assign(
+            targets=[ast.Name(id=local, ctx=ast.Store())],
+            value=ast.Name(id=f"_nx_{local}", ctx=ast.Load())))
+            for local in names]
+        lines = [f"{name} = {lower};"]
+        lines += self._emit_guarded(ahead(0), emitter, 0, hooks)
+        lines += [VALUE_WAIT_BEGIN, "_lcd_blocked = false;",
+                  f"for (; {name} < {emitter.expr(upper)}; ++{name}) {{"]
+        for child in take_over + ([] if leave is None else [leading[leave]]):
+            lines += self._emit_guarded(child, emitter, 1, hooks)
+        # the next producer's row is searched while this one's values are on
+        # their way.  (Sending the next one's first loads too, once these
+        # values are here, was slower: 8.2 against 7.2 ms on the 9-point
+        # grid -- the compiler waits for them where the guarded loads meet.)
+        for child in first_loads + [ahead(1)] + rest:
+            lines += self._emit_guarded(child, emitter, 1, hooks)
+        lines += ["}", VALUE_WAIT_END]
+        return lines
+
+    def _split_leading_loads(self, rest):
+        """Leading statements of the form ``[if structure:] x = X[p]`` (the
+        producer's diagonal): the first attempt of the load is issued with
+        the other first loads and the statement waits for the value.
+        Returns the issuing statements; ``rest`` is rewritten in place."""
+        issued = []
+
+        def structural(expression):
+            return not any(
+                isinstance(sub, ast.Call) or (
+                    isinstance(sub, ast.Subscript)
+                    and isinstance(sub.value, ast.Name)
+                    and sub.value.id in self._all_written)
+                for sub in ast.walk(expression))
+
+        def split_assign(assign):
+            if not (isinstance(assign, ast.Assign) and len(assign.targets) == 1
+                    and isinstance(assign.targets[0], ast.Name)
+                    and isinstance(assign.value, ast.Subscript)
+                    and isinstance(assign.value.value, ast.Name)
+                    and assign.value.value.id == self._published["array"]
+                    and structural(assign.value.slice)):
+                return None
+            register = f"_sp_ld_h{len(issued)}"
+            self._kinds.locals[register] = FLOAT
+            self._own_registers.append(register)
+            load = ast.Assign(
+                targets=[ast.Name(id=register, ctx=ast.Store())],
+                value=ast.Call(func=ast.Name(id="_lcd_raw", ctx=ast.Load()),
+                               args=[deepcopy(assign.value)], keywords=[]))
+            assign.value = ast.Call(
+                func=ast.Name(id="_lcd_settle", ctx=ast.Load()),
+                args=[assign.value, ast.Name(id=register, ctx=ast.Load())],
+                keywords=[])
+            return load
+
+        for statement in rest:
+            if (isinstance(statement, ast.If) and not statement.orelse
+                    and structural(statement.test)
+                    and len(statement.body) == 1):
+                load = split_assign(statement.body[0])
+                if load is None:
+                    break
+                issued.append(ast.If(test=deepcopy(statement.test),
+                                     body=[load], orelse=[]))
+            else:
+                load = split_assign(statement)
+                if load is None:
+                    break
+                issued.append(load)
+        for statement in issued + rest:
+            ast.fix_missing_locations(statement)
+        return issued
+
+    def _locate_ahead_of_wait(self, statements, hooks):
+        """The thread-mapped loop nested in a resumable producer loop starts
+        with structure work (`j = A_indices[j_ptr]; kj_ptr = find(...)`)
+        that reads nothing another task writes.  For each lane's first
+        iteration it is done ahead of the wait for the producer (into
+        ``_sp_*`` registers the loop then picks up), which takes the search
+        of the pivot row off the chain between two levels.  Returns the
+        statements to run before the wait; the loop is rewritten in place."""
+        if hooks is None or self.thread_unroll_factor != 1:
+            return [], []
+        mapped = None
+        for statement in statements:
+            for sub in ast.walk(statement):
+                if isinstance(sub, ast.For) and hooks.is_mapped(sub):
+                    mapped = sub
+        if mapped is None or len(mapped.iter.args) != 2 or not isinstance(
+                mapped.target, ast.Name):
+            return [], []
+        iterator = mapped.target.id
+        structural = []
+        for statement in mapped.body:
+            if not (isinstance(statement, ast.Assign)
+                    and len(statement.targets) == 1
+                    and isinstance(statement.targets[0], ast.Name)):
+                break
+            reads_written = any(
+                isinstance(sub, ast.Subscript) and isinstance(sub.value, ast.Name)
+                and sub.value.id in self._all_written
+                for sub in ast.walk(statement))
+            calls = [sub for sub in ast.walk(statement)
+                     if isinstance(sub, ast.Call)]
+            if reads_written or any(
+                    not (isinstance(call.func, ast.Name)
+                         and call.func.id == "_lcd_sorted_find")
+                    for call in calls):
+                break
+            structural.append(statement)
+        if not structural:
+            return [], []
+        names = {statement.targets[0].id for statement in structural}
+        renamed = {name: f"_sp_{name}" for name in names}
+        renamed[iterator] = "_sp_first"
+
+        class Rename(ast.NodeTransformer):
+            def visit_Name(self, node):
+                if node.id in renamed:
+                    return ast.copy_location(
+                        ast.Name(id=renamed[node.id], ctx=node.ctx), node)
+                return node
+
+        kinds = self._kinds
+        for name in names:
+            kinds.locals[renamed[name]] = kinds.locals.get(name, INT)
+        kinds.locals["_sp_first"] = INT
+        self._own_registers.extend(["_sp_first", *sorted(
+            renamed[name] for name in names)])
+        lower, upper = mapped.iter.args
+        first = ast.Assign(
+            targets=[ast.Name(id="_sp_first", ctx=ast.Store())],
+            value=ast.BinOp(left=deepcopy(lower), op=ast.Add(),
+                            right=ast.Name(id="_lane", ctx=ast.Load())))
+        ahead = ast.If(
+            test=ast.Compare(left=ast.Name(id="_sp_first", ctx=ast.Load()),
+                             ops=[ast.Lt()], comparators=[deepcopy(upper)]),
+            body=[Rename().visit(deepcopy(statement))
+                  for statement in structural],
+            orelse=[])
+        pick_up = ast.If(
+            test=ast.Compare(left=ast.Name(id=iterator, ctx=ast.Load()),
+                             ops=[ast.Eq()],
+                             comparators=[ast.Name(id="_sp_first",
+                                                   ctx=ast.Load())]),
+            body=[ast.Assign(
+                targets=[ast.Name(id=statement.targets[0].id, ctx=ast.Store())],
+                value=ast.Name(id=renamed[statement.targets[0].id],
+                               ctx=ast.Load())) for statement in structural],
+            orelse=list(structural))
+        rest = mapped.body[len(structural):]
+        fetched = self._fetch_behind_wait(rest, iterator, names, renamed, upper)
+        mapped.body = [pick_up] + rest
+        early = [first, ahead]
+        for statement in early + fetched + [pick_up]:
+            ast.fix_missing_locations(statement)
+        return early, fetched
+
+    def _fetch_behind_wait(self, rest, iterator, names, renamed, upper):
+        """After the structure work the nested loop reads the producer's
+        values at the positions just found (`if kj_ptr >= 0: u = A[kj_ptr]`).
+        For each lane's first iteration those loads are issued right behind
+        the wait, together with the first load the task makes of the
+        producer (its diagonal), instead of one dependent round trip later.
+        Valid because a pull rule means the task writes only its own element
+        or segment: nothing it does in between changes what it reads here."""
+        if not (rest and isinstance(rest[0], ast.If) and not rest[0].orelse):
+            return []
+        guard = rest[0]
+        known = set(names)
+        for sub in ast.walk(guard.test):
+            if isinstance(sub, (ast.Subscript, ast.Call)) or (
+                    isinstance(sub, ast.Name) and sub.id == iterator):
+                return []
+        loads = {}
+        published = self._published is not None
+
+        def eligible(node):
+            if not (isinstance(node, ast.Subscript)
+                    and isinstance(node.ctx, ast.Load)
+                    and isinstance(node.value, ast.Name)
+                    and node.value.id in self._all_written):
+                return False
+            used = {n.id for n in ast.walk(node.slice)
+                    if isinstance(n, ast.Name)}
+            if iterator in used or not (used & known):
+                return False
+            return not any(isinstance(n, (ast.Subscript, ast.Call))
+                           for n in ast.walk(node.slice))
+
+        class Hoist(ast.NodeTransformer):
+            def visit_Subscript(self, node):
+                if not eligible(node):
+                    return self.generic_visit(node)
+                text = ast.unparse(node)
+                if text not in loads:
+                    loads[text] = (f"_sp_ld_{len(loads)}", deepcopy(node))
+                held = ast.Name(id=loads[text][0], ctx=ast.Load())
+                if published:
+                    # the first attempt may have met the empty marker
+                    held = ast.Call(
+                        func=ast.Name(id="_lcd_settle", ctx=ast.Load()),
+                        args=[deepcopy(node), held], keywords=[])
+                return ast.copy_location(ast.IfExp(
+                    test=ast.Compare(
+                        left=ast.Name(id=iterator, ctx=ast.Load()),
+                        ops=[ast.Eq()],
+                        comparators=[ast.Name(id="_sp_first", ctx=ast.Load())]),
+                    body=held, orelse=node), node)
+
+        # only loads the guarded block makes unconditionally
+        guard.body = [
+            Hoist().visit(statement) if isinstance(
+                statement, (ast.Assign, ast.AugAssign)) else statement
+            for statement in guard.body]
+        if not loads:
+            return []
+
+        class Rename(ast.NodeTransformer):
+            def visit_Name(self, node):
+                if node.id in renamed:
+                    return ast.copy_location(
+                        ast.Name(id=renamed[node.id], ctx=node.ctx), node)
+                return node
+
+        kinds = self._kinds
+        body = []
+        for name, node in loads.values():
+            kinds.locals[name] = kinds.arrays.get(node.value.id, FLOAT)
+            self._own_registers.append(name)
+            value = Rename().visit(node)
+            if published:
+                value = ast.Call(func=ast.Name(id="_lcd_raw", ctx=ast.Load()),
+                                 args=[value], keywords=[])
+            body.append(ast.Assign(
+                targets=[ast.Name(id=name, ctx=ast.Store())], value=value))
+        test = ast.BoolOp(op=ast.And(), values=[
+            ast.Compare(left=ast.Name(id="_sp_first", ctx=ast.Load()),
+                        ops=[ast.Lt()], comparators=[deepcopy(upper)]),
+            Rename().visit(deepcopy(guard.test))])
+        return [ast.If(test=test, body=body, orelse=[])]
