@@ -16,6 +16,7 @@ import argparse
 import json
 import os
 import sys
+import threading
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -243,6 +244,19 @@ def main():
     step()
     call.synchronize()
     first_call_s = time.perf_counter() - t0
+    # a long run (the chain of configuration 5 takes seconds per step) says
+    # so once a minute on stderr; the timed region itself is not touched
+    finished = threading.Event()
+
+    def heartbeat():
+        began = time.perf_counter()
+        while not finished.wait(60.0):
+            print(f"bench: still running after "
+                  f"{time.perf_counter() - began:.0f} s "
+                  f"(first step took {first_call_s:.2f} s)",
+                  file=sys.stderr, flush=True)
+
+    threading.Thread(target=heartbeat, daemon=True).start()
     for _ in range(args.warmup):
         step()
     call.synchronize()
@@ -253,6 +267,7 @@ def main():
     device.record(stop)
     elapsed_ms = device.elapsed_ms(start, stop)
     call.synchronize()
+    finished.set()
     ms_per_step = elapsed_ms / args.steps
 
     launches_per_step = (plan.dag.levels
