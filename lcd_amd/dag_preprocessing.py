@@ -268,9 +268,9 @@ def execution_data_from_device_dag(dag, execution_mode, warp_mapped,
         # chain tasks: connected components inside bands of levels, built on
         # the device; only the band offsets come to the host (the launcher
         # iterates over them)
-        if execution_mode.replace("-", "_") != "wavefront":
+        if pushed or mailbox or tile_rows:
             raise DAGPreprocessingError(
-                "band_width > 1 (chain tasks) needs the wavefront executor.")
+                "band_width > 1 (chain tasks) runs on dependence counters.")
         dag.band_chains(band_width)
         return WarpTaskExecutionData(
             task_nodes=dag.array("task_nodes"), task_ptr=dag.array("task_ptr"),

@@ -203,8 +203,13 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
             if (direct_dependence is not None
                 and direct_dependence.kind == required_kind
                 and self.warp_mapped and self.execution_mode == "sync_free"
-                and sync_free_ready_count == 0)
+                and sync_free_ready_count == 0
+                # the members of a chain task wait on their counters one by
+                # one (compiler/cuda_lowering.py:1360-1410)
+                and not chain_tasks)
             else COUNTER_DEPENDENCE)
+        if chain_tasks:
+            self.tile_rows = None
         self._mailbox = None
         self.group_sync = (_GROUP_SYNC_BLOCK if self.block_task
                            else _GROUP_SYNC_WAVE)
@@ -939,9 +944,10 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
         """
         it = self.loop_iterator
         protocol = self.dependence_protocol
-        if self.chain_tasks:
+        if self.chain_tasks and self.block_task:
             raise HIPLoweringError(
-                "band_width > 1 (chain tasks) needs the wavefront executor.")
+                "band_width > 1 (chain tasks) needs one wavefront or less per "
+                "task in the persistent executor.")
         lines = ["    const int _task_count = (int)task_count;"]
         if self.block_task:
             lines += [
@@ -1043,10 +1049,24 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
             f"        if (_pending && ({self._prefetch_guard})) {{",
             *[f"            {line}" for line in self._prefetch_lines],
             "        }"]
+        chain = self.chain_tasks
+        # a chain task walks its members in order; each waits on its own
+        # counter, so the position in the chain survives between polls
+        member = ([f"{it} = (lcd_index_t)task_nodes[_pos];",
+                   f"if ({self._prefetch_guard}) {{",
+                   *[f"    {line}" for line in self._prefetch_lines],
+                   "}",
+                   f"_release_begin = dag_ptr[{it}]; "
+                   f"_release_end = dag_ptr[{it} + 1];"] if chain else [])
         lines += [
             "    const int _tasks_per_wave = 64 / LCD_TASK_LANES;",
             *fetch,
-            *([f"        {it} = 0;"] if records else
+            *(["        int _pos = 0, _pos_end = 0;",
+               "        if (_pending) { _pos = task_ptr[_task]; "
+               "_pos_end = task_ptr[_task + 1]; _pending = _pos < _pos_end; }",
+               f"        {it} = _pending ? (lcd_index_t)task_nodes[_pos] : 0;"]
+              if chain else
+              [f"        {it} = 0;"] if records else
               [f"        {it} = _pending ? (lcd_index_t)task_nodes[_task] : 0;"]),
             *(["        if (_pending) { " + " ".join(self._queue_load_lines)
                + " }"] if self._queue_load_lines and not records else []),
@@ -1113,7 +1133,12 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                 "__ATOMIC_RELAXED, LCD_AGENT);",
             ]
         lines += [
-            "                    _pending = false;",
+            *(["                    if (++_pos < _pos_end) {",
+               *[f"                        {line}" for line in member],
+               "                    } else {",
+               "                        _pending = false;",
+               "                    }"] if chain else
+              ["                    _pending = false;"]),
             "                } else {",
             "#if LCD_SPIN_SLEEP > 0",
             "                    __builtin_amdgcn_s_sleep(LCD_SPIN_SLEEP);",
@@ -1239,7 +1264,13 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
             else:
                 reset_args = ("(dep_count, initial_dep_count, task_counter, "
                               "_hip.length(dep_count))")
-            body.append(f"_count = _hip.length({count_array})")
+            if self.chain_tasks:
+                # tasks are chains; the counters are per node
+                reset_count = f"_hip.length({count_array})"
+                count_array = "task_ptr"
+                body.append("_count = _hip.length(task_ptr) - 1")
+            else:
+                body.append(f"_count = _hip.length({count_array})")
             body.append(f"_hip.launch({reset_name!r}, ({reset_count} + 255) // 256 or 1, "
                         f"256, {reset_args})")
             stage_name, stage_arguments = self._stage

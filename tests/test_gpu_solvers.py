@@ -277,15 +277,17 @@ def test_sptrsv_matches_scipy_and_manufactured_solution(oracle):
     np.testing.assert_allclose(result, reference, rtol=1e-10, atol=1e-12)
 
 
+@pytest.mark.parametrize("mode", ["wavefront", "sync_free"])
 @pytest.mark.parametrize("band_width", [2, 5, 64])
-def test_band_chains_run_in_the_wavefront_executor(oracle, band_width):
+def test_band_chains_run_in_both_executors(oracle, band_width, mode):
     """band_width > 1: one task per connected component of a band of levels,
-    members in sequence; fewer launches, same results."""
-    print("band chains", band_width, flush=True)
-    csc = sptrsv.compile_sptrsv_csc(execution_mode="wavefront",
+    members in sequence; fewer launches (level launches) or a poll per chain
+    member (persistent executor, on dependence counters), same results."""
+    print("band chains", band_width, mode, flush=True)
+    csc = sptrsv.compile_sptrsv_csc(execution_mode=mode,
                                     threads_per_block=128, task_lanes=4,
                                     band_width=band_width)
-    csr = sptrsv.compile_sptrsv_csr(execution_mode="wavefront",
+    csr = sptrsv.compile_sptrsv_csr(execution_mode=mode,
                                     threads_per_block=128, task_lanes=8,
                                     band_width=band_width)
     lane = sptrsv.compile_sptrsv_csc(execution_mode="wavefront",
@@ -299,22 +301,27 @@ def test_band_chains_run_in_the_wavefront_executor(oracle, band_width):
         solve_and_check(csc, work, expected)
         solve_and_check(lane, work, expected)
     assert "task_ptr[_task + 1]" in csc.hip_kernel_source
+    assert csc.hip_lowering.dependence_protocol == "counter"
+    assert csc.hip_lowering.tile_rows is None
     work = workloads.configuration("c3", n=20000)
     expected = oracle.sptrsv_csr(work.indptr, work.indices, work.data,
                                  work.rhs, work.n)
     solve_and_check(csr, work, expected)
-    factor = spilu0.compile_ilu0_csr(execution_mode="wavefront",
+    factor = spilu0.compile_ilu0_csr(execution_mode=mode,
                                      threads_per_block=128, task_lanes=8,
                                      thread_unroll=1, band_width=band_width)
     work = workloads.configuration("c4", nx=40, ny=36)
     expected = oracle.ilu0_csr(work.data, work.indices, work.indptr)
     np.testing.assert_array_equal(
         factor(work.data.copy(), work.indices, work.indptr), expected)
-    with pytest.raises(Exception, match="wavefront executor"):
-        sptrsv.compile_sptrsv_csc(
-            execution_mode="sync_free", threads_per_block=128, task_lanes=4,
-            band_width=band_width)(work.indptr, work.indices, work.data,
-                                   np.ones(work.n), work.n)
+    assert factor.hip_lowering.dependence_protocol == "counter"
+    if mode == "sync_free":
+        # a whole workgroup per task cannot walk a chain member by member
+        with pytest.raises(Exception, match="one wavefront or less"):
+            sptrsv.compile_sptrsv_csc(
+                execution_mode="sync_free", threads_per_block=128, n_warp=2,
+                band_width=band_width)(work.indptr, work.indices, work.data,
+                                       np.ones(work.n), work.n)
 
 
 ILU_VARIANTS = [
