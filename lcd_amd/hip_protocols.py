@@ -348,6 +348,17 @@ class ProtocolMixin:
                 + " ".join(self._queue_load_lines) + " }")
             lines.append(f"{pad}{head} {{ {loads} }}")
             if self.single_chunk:
+                # the first poll of a source outside the tile leaves with the
+                # operand loads instead of one round trip later, in the poll
+                # loop (128^3 grid: 0.354 -> 0.347 ms)
+                # (with the flat queue every source is outside and mostly not
+                # there yet at that time: 3 % slower, so tiles only)
+                array = self._mailbox["array"]
+                lines.append(f"{pad}double _g_early = lcd_empty();")
+                if self._tile is not None:
+                    lines.append(
+                        f"{pad}{head[:-1]} && !_g_in) {{ _g_early = "
+                        f"{self.poll_load}(&{array}[_g_src]); }}")
                 lines += [
                     f"{pad}const int _mb_have = (_mb_end - _mb_next) < "
                     "LCD_TASK_LANES ? (_mb_end - _mb_next) : LCD_TASK_LANES;",
@@ -407,7 +418,8 @@ class ProtocolMixin:
             # one chunk per task: what each lane still waits for is a flag
             # set when the task is fetched and cleared by its poll
             memory_poll = (
-                f"{{ const double _g_raw = {self.poll_load}(&{array}[_g_src]); "
+                "{ const double _g_raw = lcd_is_empty(_g_early) ? "
+                f"{self.poll_load}(&{array}[_g_src]) : _g_early; "
                 "if (!lcd_is_empty(_g_raw)) { _mb_value = _g_raw; "
                 "_need = false; } }")
             return [
