@@ -3,9 +3,9 @@ names, the result record, kind inference (integer or double) and the emitter
 that turns Python AST nodes of a loop body into HIP C++ text."""
 
 import ast
+from copy import deepcopy
 import textwrap
 
-from copy import deepcopy
 from dataclasses import (
     dataclass,
     field,

@@ -25,9 +25,9 @@ targeting CDNA4 rather than translating the CUDA code:
 """
 
 import ast
+from copy import deepcopy
 import textwrap
 
-from copy import deepcopy
 from lcd_amd.structural_lookups import (
     match_segment_search,
     rewrite_structural_lookups,

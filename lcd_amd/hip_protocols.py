@@ -2,8 +2,8 @@
 its gathered form): their plans and the readiness code a task polls."""
 
 import ast
-
 from copy import deepcopy
+
 from lcd_amd.structural_lookups import structure_aliases
 from lcd_amd.hip_emitter import (
     FLOAT,

@@ -3,8 +3,8 @@ resumable loop with `done` flags and the pipelined loop over published
 values."""
 
 import ast
-
 from copy import deepcopy
+
 from lcd_amd.hip_emitter import (
     FLOAT,
     INT,
@@ -21,7 +21,10 @@ class SequentialPullMixin:
         first checks that its producer has published ``done`` and otherwise
         leaves the loop with the position kept; the lines between the two
         markers are re-entered by the executor's poll loop.  The task works
-        on the producers that are finished while it waits for the others."""
+        on the producers that are finished while it waits for the others.
+        With published values there is no flag to wait for (the reads of the
+        producer's entries poll) and the loop runs through in one go, in its
+        pipelined form where the body allows."""
         plan = self._sequential_pull
         plan["emitted"] = True
         name = node.target.id

@@ -3,9 +3,8 @@ own segments and tiles, forwarded stores, promoted own elements, hoisted and
 queue-ordered node loads."""
 
 import ast
-
 from copy import deepcopy
-from dataclasses import field
+
 from lcd_amd.dependence import _split_offset
 from lcd_amd.hip_emitter import (
     FLOAT,
