@@ -4,12 +4,8 @@ that turns Python AST nodes of a loop body into HIP C++ text."""
 
 import ast
 from copy import deepcopy
+from dataclasses import dataclass, field
 import textwrap
-
-from dataclasses import (
-    dataclass,
-    field,
-)
 
 
 class HIPLoweringError(Exception):
