@@ -407,6 +407,15 @@ class ProtocolMixin:
                 f"{pad}        {{ const double _mb_in = lcd_quad_broadcast<{k}>(_mb_value); "
                 f"if ({k} < _mb_have) {own} = {own} + _mb_in; }}"
                 for k in range(4)]
+        elif self.task_lanes in (8, 16):
+            # the group's first lane takes the products one by one (DPP row
+            # shifts) and adds them in order; its total goes to the group
+            ordered = [
+                f"{pad}        {{ const double _mb_in = lcd_row_take<{k}>(_mb_value); "
+                f"if ({k} < _mb_have) {own} = {own} + _mb_in; }}"
+                for k in range(self.task_lanes)]
+            ordered.append(
+                f"{pad}        {own} = lcd_group_first<LCD_TASK_LANES>({own});")
         else:
             ordered = [
                 *unroll,
