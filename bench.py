@@ -91,6 +91,8 @@ def build_solver(work, args):
         options["look_ahead"] = args.look_ahead == "1"
     if args.no_publish:
         options["publish_values"] = False
+    if args.no_pipeline:
+        options["pipeline_fetch"] = False
     if args.slots:
         options["gather_messages"] = False
         options["tile_rows"] = None
@@ -198,6 +200,9 @@ def main():
                              "values while waiting for this one's (default 1)")
     parser.add_argument("--no-publish", action="store_true",
                         help="pull on a sequential loop through done flags")
+    parser.add_argument("--no-pipeline", action="store_true",
+                        help="tiled mailbox: load a round's records and "
+                             "operands when the round starts")
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-check", action="store_true")
     parser.add_argument("--arch", action="store_true",

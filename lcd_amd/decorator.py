@@ -215,6 +215,7 @@ def parallel(**kwargs):
                     publish_values=kwargs.get("publish_values", True),
                     look_ahead=kwargs.get("look_ahead", True),
                     segment_capacity=kwargs.get("segment_capacity"),
+                    pipeline_fetch=kwargs.get("pipeline_fetch", True),
                 )
             return lowered_variants[variant_key]
 

@@ -97,7 +97,9 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                  gather_messages=True, segment_cache=True, tile_rows=None,
                  stage_operands=True, task_records=True, single_chunk=False,
                  queue_node_loads=True, plain_first_polls=None,
-                 publish_values=True, look_ahead=True, segment_capacity=None):
+                 publish_values=True, look_ahead=True, segment_capacity=None,
+                 pipeline_fetch=True):
+        self.pipeline_fetch = pipeline_fetch
         self.look_ahead = look_ahead
         self.segment_capacity = segment_capacity
         self.queue_node_loads_enabled = queue_node_loads
@@ -1058,7 +1060,12 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                    "}",
                    f"_release_begin = dag_ptr[{it}]; "
                    f"_release_end = dag_ptr[{it} + 1];"] if chain else [])
-        lines += [
+        pipelined = (tiled and records and self.single_chunk
+                     and self.pipeline_fetch and not chain)
+        if pipelined:
+            lines += ["    const int _tasks_per_wave = 64 / LCD_TASK_LANES;",
+                      *self._pipelined_fetch_lines(fetch, it)]
+        lines += [] if pipelined else [
             "    const int _tasks_per_wave = 64 / LCD_TASK_LANES;",
             *fetch,
             *(["        int _pos = 0, _pos_end = 0;",
@@ -1330,7 +1337,8 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
                  gather_messages=True, segment_cache=True, tile_rows=None,
                  stage_operands=True, task_records=True, single_chunk=False,
                  queue_node_loads=True, plain_first_polls=None,
-                 publish_values=True, look_ahead=True, segment_capacity=None):
+                 publish_values=True, look_ahead=True, segment_capacity=None,
+                 pipeline_fetch=True):
     """HIP counterpart of ``lower_to_numba_cuda``
     (compiler/cuda_lowering.py:2854-2884); same parameters plus
     ``task_lanes`` (lanes cooperating on one task, a power of two <= 64),
@@ -1355,5 +1363,6 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
         task_records=task_records, single_chunk=single_chunk,
         queue_node_loads=queue_node_loads,
         plain_first_polls=plain_first_polls, publish_values=publish_values,
-        look_ahead=look_ahead, segment_capacity=segment_capacity)
+        look_ahead=look_ahead, segment_capacity=segment_capacity,
+        pipeline_fetch=pipeline_fetch)
     return lowerer.lower(code)
