@@ -1065,6 +1065,15 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
         if pipelined:
             lines += ["    const int _tasks_per_wave = 64 / LCD_TASK_LANES;",
                       *self._pipelined_fetch_lines(fetch, it)]
+        queue_pipelined = (
+            not pipelined and not tiled and not chain and self.pipeline_fetch
+            and protocol == PULL_DEPENDENCE and self._prefetch_lines
+            and (self._value_pull is not None
+                 or self._sequential_pull is not None))
+        if queue_pipelined:
+            lines += ["    const int _tasks_per_wave = 64 / LCD_TASK_LANES;",
+                      *self._pipelined_queue_fetch_lines(it)]
+            pipelined = True
         lines += [] if pipelined else [
             "    const int _tasks_per_wave = 64 / LCD_TASK_LANES;",
             *fetch,

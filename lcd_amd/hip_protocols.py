@@ -374,47 +374,30 @@ class ProtocolMixin:
             f"_g_src = _lcd_in_src[_mb_next + _lane]; {decode}{loads} }}")
         return lines
 
-    def _pipelined_fetch_lines(self, fetch, it):
-        """Tiled executor with task records: the loads a round of tasks starts
-        with, two rounds deep.  A wavefront's round began with two dependent
-        trips to memory (the records of its tasks, then the operands the
-        records name) during which it did nothing, and the tile advanced at
-        the rate its wavefronts got through those trips, not at the rate of
-        its LDS hand-offs.  Now a round takes over registers that were loaded
-        while the rounds before it ran: the records of round r + 2 and the
-        operands of round r + 1 are requested when round r starts.  (128^3
-        grid: 0.347 -> 0.32 ms.)"""
+    def _fetch_pipeline(self, it, first_loads, first_zero, first, second_blocks,
+                        task_of, bound, types):
+        """Pieces of a fetch that runs two rounds deep.  ``first_loads`` are
+        the loads addressed by the queue position alone (text over ``_t``),
+        ``first`` the registers they fill; ``second_blocks`` are (condition,
+        lines) pairs whose loads are named by the first ones.  Returns the
+        declarations, the two request blocks (per register set and round
+        expression) and the take-over lines."""
         import re
-        gather = self._mailbox["gather"]
-        array = self._mailbox["array"]
-        emitter = self._emitter
         kinds = self._kinds
-        split = next(index for index, line in enumerate(fetch)
-                     if "for (int _round = 0" in line)
-        queue_loads = list(self._queue_load_lines)
-        queue_names = [re.match(r"\s*(\w+) = ", line).group(1)
-                       for line in queue_loads]
-        operand_loads = [f"{name} = {emitter.expr(node)};"
-                         for name, node, _ in gather["operands"]]
-        node_lines = list(self._prefetch_lines)
         assigned = []
-        for line in node_lines:
-            for name in re.findall(r"(?<![=!<>\w])([A-Za-z_]\w*)\s*=(?!=)", line):
-                if name not in assigned:
-                    assigned.append(name)
-        first = [it, "_mb_next", "_mb_end", "_g_pos", "_g_src", *queue_names]
-        second = [name for name, _, _ in gather["operands"]]
-        second += [name for name in assigned
-                   if name not in first and name not in second]
+        for _, block in second_blocks:
+            for line in block:
+                for name in re.findall(
+                        r"(?<![=!<>\w])([A-Za-z_]\w*)\s*=(?!=)", line):
+                    if name not in assigned and name not in first:
+                        assigned.append(name)
+        second = assigned
 
         def ctype(name):
-            if name in ("_mb_next", "_mb_end"):
-                return "int"
-            if name in (it, "_g_pos", "_g_src"):
+            if name in types:
+                return types[name]
+            if name == it:
                 return "lcd_index_t"
-            for operand, _, kind in gather["operands"]:
-                if operand == name:
-                    return "lcd_index_t" if kind == INT else "double"
             return ("double" if kinds.locals.get(name, INT) == FLOAT
                     else "lcd_index_t")
 
@@ -429,66 +412,103 @@ class ProtocolMixin:
                     name, prefix + name)
             return pattern.sub(swap, text)
 
-        def task_of(rounds):
-            return (f"(_lcd_tile_row0 + (({rounds}) * (LCD_TPB / 64) + "
-                    "(int)(threadIdx.x >> 6)) * _tasks_per_wave + "
-                    "(int)(threadIdx.x & 63) / LCD_TASK_LANES)")
-
         def head(rounds):
             return (f"{{ const int _t = {task_of(rounds)}; const bool _v = "
-                    "_t < _lcd_tile_row0 + _lcd_tile_rows; (void)_v;")
+                    f"_t < {bound}; (void)_v;")
 
-        def records_of(prefix, rounds):
-            slot = "_t * LCD_TASK_LANES + _lane"
-            return (
-                f"{head(rounds)} {prefix}{it} = 0; {prefix}_mb_next = 0; "
-                f"{prefix}_mb_end = 0; if (_v) {{ {prefix}{it} = "
-                "(lcd_index_t)task_nodes[_t]; "
-                f"{prefix}_mb_next = _lcd_rec_in[2 * _t]; "
-                f"{prefix}_mb_end = _lcd_rec_in[2 * _t + 1]; "
-                f"{prefix}_g_pos = _lcd_rec_pos[{slot}]; "
-                f"{prefix}_g_src = _lcd_rec_src[{slot}]; "
-                + " ".join(renamed(line, prefix) for line in queue_loads)
-                + " } }")
+        def request_first(prefix, rounds):
+            return (f"{head(rounds)} "
+                    + " ".join(f"{prefix}{name} = 0;" for name in first_zero)
+                    + " if (_v) { "
+                    + " ".join(renamed(line, prefix) for line in first_loads)
+                    + " } }")
 
-        def operands_of(prefix, rounds):
-            return [
-                f"{head(rounds)}",
-                f"if (_v && {prefix}_mb_next + _lane < {prefix}_mb_end) {{ "
-                + " ".join(renamed(line, prefix) for line in operand_loads)
-                + " }",
-                f"if (_v && ({renamed(self._prefetch_guard, prefix)})) {{",
-                *["    " + renamed(line, prefix) for line in node_lines],
-                "} }"]
+        def request_second(prefix, rounds):
+            lines = [head(rounds)]
+            for condition, block in second_blocks:
+                lines.append(f"if (_v && ({renamed(condition, prefix)})) {{")
+                lines += ["    " + renamed(line, prefix) for line in block]
+                lines.append("}")
+            lines.append("}")
+            return lines
 
         declare = " ".join(
-            f"{ctype(name)} _a_{name} = 0;" for name in first) + " " + " ".join(
-            f"{ctype(name)} _b_{name} = 0;" for name in first + second)
+            [f"{ctype(name)} _a_{name} = 0;" for name in first]
+            + [f"{ctype(name)} _b_{name} = 0;" for name in first + second])
+        return {
+            "declare": declare, "second": second,
+            "request_first": request_first, "request_second": request_second,
+            "take_first": " ".join(f"{name} = _b_{name};" for name in first),
+            "take_second": " ".join(f"{name} = _b_{name};" for name in second),
+            "shift": " ".join(f"_b_{name} = _a_{name};" for name in first),
+        }
+
+    def _pipelined_fetch_lines(self, fetch, it):
+        """Tiled executor with task records: the loads a round of tasks starts
+        with, two rounds deep.  A wavefront's round began with two dependent
+        trips to memory (the records of its tasks, then the operands the
+        records name) during which it did nothing, and the tile advanced at
+        the rate its wavefronts got through those trips, not at the rate of
+        its LDS hand-offs.  Now a round takes over registers that were loaded
+        while the rounds before it ran: the records of round r + 2 and the
+        operands of round r + 1 are requested when round r starts.  (128^3
+        grid: 0.347 -> 0.327 ms.)"""
+        import re
+        gather = self._mailbox["gather"]
+        array = self._mailbox["array"]
+        emitter = self._emitter
+        split = next(index for index, line in enumerate(fetch)
+                     if "for (int _round = 0" in line)
+        queue_loads = list(self._queue_load_lines)
+        queue_names = [re.match(r"\s*(\w+) = ", line).group(1)
+                       for line in queue_loads]
+        slot = "_task * LCD_TASK_LANES + _lane"
+        first = [it, "_mb_next", "_mb_end", "_g_pos", "_g_src", *queue_names]
+        operands = [name for name, _, _ in gather["operands"]]
+        types = {"_mb_next": "int", "_mb_end": "int",
+                 "_g_pos": "lcd_index_t", "_g_src": "lcd_index_t"}
+        types.update({name: "lcd_index_t" if kind == INT else "double"
+                      for name, _, kind in gather["operands"]})
+        pipe = self._fetch_pipeline(
+            it,
+            [f"{it} = (lcd_index_t)task_nodes[_task];",
+             "_mb_next = _lcd_rec_in[2 * _task];",
+             "_mb_end = _lcd_rec_in[2 * _task + 1];",
+             f"_g_pos = _lcd_rec_pos[{slot}];",
+             f"_g_src = _lcd_rec_src[{slot}];", *queue_loads],
+            [it, "_mb_next", "_mb_end"], first,
+            [("_mb_next + _lane < _mb_end",
+              [f"{name} = {emitter.expr(node)};"
+               for name, node, _ in gather["operands"]]),
+             (self._prefetch_guard, list(self._prefetch_lines))],
+            lambda rounds: (
+                f"(_lcd_tile_row0 + (({rounds}) * (LCD_TPB / 64) + "
+                "(int)(threadIdx.x >> 6)) * _tasks_per_wave + "
+                "(int)(threadIdx.x & 63) / LCD_TASK_LANES)"),
+            "_lcd_tile_row0 + _lcd_tile_rows", types)
         tile_part, round_part = fetch[:split], fetch[split:]
         pad = "        "
         lines = list(tile_part)
-        lines += ["    " + declare,
-                  "    " + records_of("_b_", "0"),
-                  "    " + records_of("_a_", "1"),
-                  *["    " + line for line in operands_of("_b_", "0")]]
+        lines += ["    " + pipe["declare"],
+                  "    " + pipe["request_first"]("_b_", "0"),
+                  "    " + pipe["request_first"]("_a_", "1"),
+                  *["    " + line for line in pipe["request_second"]("_b_", "0")]]
         lines += round_part
         lines += [
             f"{pad}{it} = 0;",
             f"{pad}int _mb_next = 0, _mb_end = 0;",
             f"{pad}lcd_index_t _g_pos = 0, _g_src = 0;",
             f"{pad}double _mb_value = lcd_empty();",
-            *[f"{pad}{'lcd_index_t' if kind == INT else 'double'} {name} = 0;"
-              for name, _, kind in gather["operands"]],
+            *[f"{pad}{types[name]} {name} = 0;" for name in operands],
             f"{pad}unsigned _g_off = 0; bool _g_in = false;",
             # this round takes over what was loaded while the others ran
-            f"{pad}if (_pending) {{ " + " ".join(
-                f"{name} = _b_{name};" for name in first)
-            + " _g_off = (unsigned)(_g_src - _lcd_tile_row0); "
-              "_g_in = _g_off < (unsigned)_lcd_tile_rows; }",
-            f"{pad}" + " ".join(f"{name} = _b_{name};" for name in second),
-            f"{pad}" + " ".join(f"_b_{name} = _a_{name};" for name in first),
-            *[pad + line for line in operands_of("_b_", "_round + 1")],
-            pad + records_of("_a_", "_round + 2"),
+            f"{pad}if (_pending) {{ {pipe['take_first']} "
+            "_g_off = (unsigned)(_g_src - _lcd_tile_row0); "
+            "_g_in = _g_off < (unsigned)_lcd_tile_rows; }",
+            f"{pad}{pipe['take_second']}",
+            f"{pad}{pipe['shift']}",
+            *[pad + line for line in pipe["request_second"]("_b_", "_round + 1")],
+            pad + pipe["request_first"]("_a_", "_round + 2"),
             f"{pad}double _g_early = lcd_empty();",
             f"{pad}if (_pending && _mb_next + _lane < _mb_end && !_g_in) "
             f"{{ _g_early = {self.poll_load}(&{array}[_g_src]); }}",
@@ -498,6 +518,51 @@ class ProtocolMixin:
             f"{pad}const bool _fits = (_mb_end - _mb_next) <= LCD_TASK_LANES;",
         ]
         return lines
+
+    def _pipelined_queue_fetch_lines(self, it):
+        """The same two-round fetch for the flat level-ordered queue of the
+        pull protocols: the task id and the structure loads addressed by the
+        queue position for round r + 2, the node loads they name for round
+        r + 1.  Tasks are dealt out round-robin (no shared counter), so a
+        wavefront knows its later tasks.  (Power-law factor: 0.722 -> 0.69
+        ms.)"""
+        import re
+        queue_loads = list(self._queue_load_lines)
+        queue_names = [re.match(r"\s*(\w+) = ", line).group(1)
+                       for line in queue_loads]
+        first = [it, *queue_names]
+        pipe = self._fetch_pipeline(
+            it, [f"{it} = (lcd_index_t)task_nodes[_task];", *queue_loads],
+            [it], first,
+            [(self._prefetch_guard, list(self._prefetch_lines))],
+            lambda rounds: (
+                f"((({rounds}) * (int)(gridDim.x * (LCD_TPB / 64)) + "
+                "(int)(blockIdx.x * (LCD_TPB / 64) + (threadIdx.x >> 6))) * "
+                "_tasks_per_wave + (int)(threadIdx.x & 63) / LCD_TASK_LANES)"),
+            "_task_count", {})
+        pad = "        "
+        return [
+            "    int _round = 0;",
+            "    " + pipe["declare"],
+            "    " + pipe["request_first"]("_b_", "0"),
+            "    " + pipe["request_first"]("_a_", "1"),
+            *["    " + line for line in pipe["request_second"]("_b_", "0")],
+            "    while (true) {",
+            f"{pad}const int _base = (_round * (int)(gridDim.x * (LCD_TPB / 64)) + "
+            "(int)(blockIdx.x * (LCD_TPB / 64) + (threadIdx.x >> 6))) * "
+            "_tasks_per_wave;",
+            f"{pad}++_round;",
+            f"{pad}if (_base >= _task_count) return;",
+            f"{pad}const int _task = _base + (int)(threadIdx.x & 63) / "
+            "LCD_TASK_LANES;",
+            f"{pad}bool _pending = _task < _task_count;",
+            f"{pad}{it} = 0;",
+            f"{pad}if (_pending) {{ {pipe['take_first']} }}",
+            f"{pad}{pipe['take_second']}",
+            f"{pad}{pipe['shift']}",
+            *[pad + line for line in pipe["request_second"]("_b_", "_round")],
+            pad + pipe["request_first"]("_a_", "_round + 1"),
+        ]
 
     def _gather_ready_lines(self, indent):
         """Readiness for the gathered mailbox: lane ``l`` polls the final

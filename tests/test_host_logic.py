@@ -689,11 +689,20 @@ def test_structure_arrays_are_read_in_task_order():
     assert result.kernel_arguments[-2:] == ["_lcd_qn_0", "_lcd_qn_1"]
     assert result.launcher_arguments[-2:] == ["_lcd_qn_0", "_lcd_qn_1"]
     kernel = result.kernel_source
-    assert ("if (_pending) { _nl_1 = _lcd_qn_0[_task]; "
-            "_nl_2 = _lcd_qn_1[_task]; }") in kernel
+    # ... two rounds ahead, into the registers the round takes over
+    assert ("_a__nl_1 = _lcd_qn_0[_t]; _a__nl_2 = _lcd_qn_1[_t];") in kernel
+    assert "if (_pending) { i = _b_i; _nl_1 = _b__nl_1; _nl_2 = _b__nl_2; }" in kernel
     assert "= Ap[" not in kernel
-    assert "_nl_0 = b[i];" in kernel          # a value array stays as it is
+    assert "_b__nl_0 = b[_b_i];" in kernel     # a value array stays as it is
     hip_runtime.compile_code(result.source)
+    plain = lower(module, execution_mode="sync_free",
+                  thread_loop_iterator="j", task_lanes=8,
+                  dependence_protocol="pull", queue_node_loads=True,
+                  pipeline_fetch=False)
+    assert ("if (_pending) { _nl_1 = _lcd_qn_0[_task]; "
+            "_nl_2 = _lcd_qn_1[_task]; }") in plain.kernel_source
+    assert "_nl_0 = b[i];" in plain.kernel_source
+    hip_runtime.compile_code(plain.source)
     # level launches keep `Ap[i]` (warm in L2 from the level before), and so
     # does the counter protocol
     for options in (dict(execution_mode="wavefront"),
