@@ -184,7 +184,8 @@ class SequentialPullMixin:
         # the next producer's row is searched while this one's values are on
         # their way.  (Sending the next one's first loads too, once these
         # values are here, was slower: 8.2 against 7.2 ms on the 9-point
-        # grid -- the compiler waits for them where the guarded loads meet.)
+        # grid -- most come back empty, and every extra coherent load slows
+        # the hand-offs.)
         for child in first_loads + [ahead(1)] + rest:
             lines += self._emit_guarded(child, emitter, 1, hooks)
         lines += ["}", VALUE_WAIT_END]
