@@ -218,7 +218,10 @@ class TaskTransformMixin:
         array, pointer = plan["array"], plan["pointer"]
         it = self.loop_iterator
         coherent = array in self._emitter.coherent_arrays
-        load = (f"lcd_ld(&{array}[_lcd_seg_base + _q])" if coherent
+        # with published values nobody else writes the task's own segment of
+        # the array itself: its values are the input, a plain load will do
+        load = (f"lcd_ld(&{array}[_lcd_seg_base + _q])"
+                if coherent and not self._published
                 else f"{array}[_lcd_seg_base + _q]")
         store = (f"lcd_st(&{array}[_lcd_seg_base + _q], _lcd_seg[_q]);"
                  if coherent else f"{array}[_lcd_seg_base + _q] = _lcd_seg[_q];")
