@@ -666,6 +666,22 @@ def test_tiled_mailbox_reads_task_records():
     assert "bool _need = _pending && _lane < _mb_have;" in single.kernel_source
     assert "if (_fits && lcd_group_none(_need)) {" in single.kernel_source
     assert single.kernel_arguments == result.kernel_arguments
+    # ... and then the fetch runs two rounds deep: records of round r + 2
+    # and operands of round r + 1 requested when round r starts, the first
+    # poll of a source outside the tile issued with the task
+    text = single.kernel_source
+    assert "_a__g_src = _lcd_rec_src[_t * LCD_TASK_LANES + _lane];" in text
+    assert "_b__g_operand_0 = Ax[_b__g_pos];" in text
+    assert text.index("_mb_next = _b__mb_next;") < text.index(
+        "_b__mb_next = _a__mb_next;") < text.index(
+        "(_round + 1) * (LCD_TPB / 64)") < text.index(
+        "(_round + 2) * (LCD_TPB / 64)") < text.index("unsigned _spins = 0;")
+    assert "&& !_g_in) { _g_early = lcd_ld(&x[_g_src]); }" in text
+    eager = lower(module, single_chunk=True, pipeline_fetch=False, **options)
+    assert "_a__g_src" not in eager.kernel_source
+    assert "_g_src = _lcd_rec_src[_task * LCD_TASK_LANES + _lane];" in (
+        eager.kernel_source)
+    hip_runtime.compile_code(eager.source)
     # the watchdog looks up once in 1024 polls
     assert "(++_spins & 1023u) == 0u" in kernel
     for lowered in (result, single):
