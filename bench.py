@@ -56,7 +56,7 @@ MEASURED_TRAFFIC = {
     ("c2", "sync_free", "push", 4): 1_937_433_319,
     ("c2", "sync_free", "mailbox", 4): 535_916_978,
     ("c3", "sync_free", "pull", 64): 1_531_636_035,
-    ("c4", "sync_free", "pull", 64): 1_177_308_398,
+    ("c4", "sync_free", "pull", 64): 1_183_004_569,
     
 }
 
