@@ -1060,22 +1060,21 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                    "}",
                    f"_release_begin = dag_ptr[{it}]; "
                    f"_release_end = dag_ptr[{it} + 1];"] if chain else [])
-        pipelined = (tiled and records and self.single_chunk
-                     and self.pipeline_fetch and not chain)
-        if pipelined:
-            lines += ["    const int _tasks_per_wave = 64 / LCD_TASK_LANES;",
-                      *self._pipelined_fetch_lines(fetch, it)]
-        queue_pipelined = (
-            not pipelined and not tiled and not chain and self.pipeline_fetch
-            and protocol == PULL_DEPENDENCE and self._prefetch_lines
-            and (self._value_pull is not None
-                 or self._sequential_pull is not None))
-        if queue_pipelined:
-            lines += ["    const int _tasks_per_wave = 64 / LCD_TASK_LANES;",
-                      *self._pipelined_queue_fetch_lines(it)]
-            pipelined = True
-        lines += [] if pipelined else [
-            "    const int _tasks_per_wave = 64 / LCD_TASK_LANES;",
+        lines.append("    const int _tasks_per_wave = 64 / LCD_TASK_LANES;")
+        # what a round of tasks starts with is loaded two rounds deep where
+        # the later tasks of a wavefront are known in advance: the tiled
+        # mailbox with records, the pull protocols on the flat queue
+        if (self.pipeline_fetch and tiled and records and self.single_chunk
+                and not chain):
+            start = self._pipelined_fetch_lines(fetch, it)
+        elif (self.pipeline_fetch and not tiled and not chain
+              and protocol == PULL_DEPENDENCE and self._prefetch_lines
+              and (self._value_pull is not None
+                   or self._sequential_pull is not None)):
+            start = self._pipelined_queue_fetch_lines(it)
+        else:
+            start = None
+        lines += start if start is not None else [
             *fetch,
             *(["        int _pos = 0, _pos_end = 0;",
                "        if (_pending) { _pos = task_ptr[_task]; "
