@@ -861,6 +861,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
             lines += [
                 f"    __shared__ LCD_T_{self._tile['array']} "
                 "_lcd_tile[LCD_TILE_ROWS];",
+                "    __shared__ int _lcd_tile_slot;",
                 "    lcd_index_t _lcd_tile_row0 = 0, _lcd_tile_rows = 0;",
             ]
         if self._segment is not None:
@@ -999,10 +1000,27 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
             # one workgroup per tile of consecutive block-iterator values,
             # its wavefronts share the tile's tasks in (level, id) order;
             # tiles are taken in increasing order, so the lowest unfinished
-            # tile is always running and depends on finished tiles only
+            # tile is always running and depends on finished tiles only.
+            # With more tiles than workgroups the tiles are claimed from the
+            # task counter: a workgroup that holds a tile is running by
+            # construction, whereas tiles dealt out by block index wait for
+            # every workgroup of the grid to be resident at once -- and the
+            # occupancy query can promise more than the CUs then hold (six
+            # wavefronts per workgroup do not spread evenly over four SIMDs:
+            # a 256 x 256 x 128 grid stopped with a third of its tiles never
+            # started).
             fetch = [
-                "    for (int _tile = blockIdx.x; (long long)_tile * LCD_TILE_ROWS "
-                "< _task_count; _tile += gridDim.x) {",
+                "    const bool _lcd_claim = (long long)gridDim.x * LCD_TILE_ROWS "
+                "< _task_count;",
+                "    for (int _turn = 0; ; ++_turn) {",
+                "    int _tile = blockIdx.x;",
+                "    if (_lcd_claim) {",
+                "        if (threadIdx.x == 0) _lcd_tile_slot = "
+                "atomicAdd(&task_counter[0], 1);",
+                "        __syncthreads();",
+                "        _tile = _lcd_tile_slot;",
+                "    } else if (_turn) break;",
+                "    if ((long long)_tile * LCD_TILE_ROWS >= _task_count) break;",
                 "    _lcd_tile_row0 = _tile * LCD_TILE_ROWS;",
                 "    _lcd_tile_rows = _task_count - _lcd_tile_row0 < LCD_TILE_ROWS "
                 "? _task_count - _lcd_tile_row0 : LCD_TILE_ROWS;",

@@ -806,8 +806,17 @@ class LaunchContext:
         """Size of a persistent grid: every workgroup must be resident.
         ``waves_per_cu`` caps it below what occupancy allows."""
         blocks = self.device.resident_blocks(self.module.kernel(name), block)
+        waves_per_block = max(1, (block + 63) // 64)
+        if waves_per_block % 4 and waves_per_block > 4:
+            # the occupancy query counts wavefronts per CU; a workgroup whose
+            # wavefronts do not divide over the four SIMDs takes the larger
+            # share on some of them, and fewer such workgroups fit than the
+            # total suggests (measured: 4 promised, 3 resident at 6 per group)
+            per_cu = blocks // max(self.device.props.compute_units, 1)
+            per_simd = per_cu * waves_per_block // 4
+            fit = per_simd // -(-waves_per_block // 4)
+            blocks = max(1, min(per_cu, fit)) * self.device.props.compute_units
         if waves_per_cu:
-            waves_per_block = max(1, (block + 63) // 64)
             # (a fraction leaves CUs without a workgroup: narrow DAGs)
             cap = -(-int(self.device.props.compute_units
                          * float(waves_per_cu)) // waves_per_block)

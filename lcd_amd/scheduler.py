@@ -70,9 +70,10 @@ class ArchConstants:
 
 # The mailbox protocol's level time on a busy MI355X: 3.3 x the idle-GPU
 # hand-off (0.54 us -> 1.8 us per level from 1800 rows per level on), and
-# about 4.1 G tasks/s once levels are wider than that (8 M-row grids).
+# about 5.3 G tasks/s once levels are wider than that (192^3 grid: 2.4 us
+# per level of 12 K rows; 256^3: 3.8 us per level of 22 K rows).
 LOADED_HANDOFF_FACTOR = 3.3
-TASK_ISSUE_S = 2.4e-10
+TASK_ISSUE_S = 1.9e-10
 
 # Used when no device is available to measure (MI355X data-sheet scale).
 FALLBACK_ARCH_CONSTANTS = ArchConstants(
@@ -418,6 +419,11 @@ class CalibratedScheduler(AnalyticScheduler):
     since the task body then reads its operands through coherent loads)."""
 
     LEVEL_KERNEL_FACTOR = 2.3
+    # a wide level is bound by its rows, not by the launch: 3.9 us per level
+    # at 5.5 K rows per level (128^3 grid), 7.5 us at 22 K (256^3), i.e.
+    # 1.6 graph nodes + 0.215 ns per row
+    WIDE_LEVEL_FACTOR = 1.6
+    LEVEL_ROW_S = 2.15e-10
     HANDOFFS_PER_LEVEL = {
         MAILBOX_DEPENDENCE: LOADED_HANDOFF_FACTOR,
         PULL_DEPENDENCE: LOADED_HANDOFF_FACTOR,
@@ -441,8 +447,10 @@ class CalibratedScheduler(AnalyticScheduler):
                                 dependence_protocol, task_lanes)
         arch = self.arch_constants
         if execution_mode == WAVEFRONT:
-            return replace(base, launch_s=base.launch_s
-                           * self.LEVEL_KERNEL_FACTOR)
+            wide_s = (base.launch_s * self.WIDE_LEVEL_FACTOR
+                      + features.rows * self.LEVEL_ROW_S)
+            return replace(base, launch_s=max(
+                base.launch_s * self.LEVEL_KERNEL_FACTOR, wide_s))
         hops = self.HANDOFFS_PER_LEVEL.get(dependence_protocol,
                                            LOADED_HANDOFF_FACTOR)
         if dependence_protocol == MAILBOX_DEPENDENCE:

@@ -277,6 +277,36 @@ def test_sptrsv_matches_scipy_and_manufactured_solution(oracle):
     np.testing.assert_allclose(result, reference, rtol=1e-10, atol=1e-12)
 
 
+@pytest.mark.parametrize("tile_rows,tpb,waves_per_cu",
+                         [(128, 384, None), (64, 64, 1), (256, 192, 2)])
+def test_more_tiles_than_workgroups(oracle, tile_rows, tpb, waves_per_cu):
+    """More tiles than the persistent grid has workgroups: the tiles are
+    claimed from the task counter, so the run does not depend on every
+    workgroup of the grid being resident at the same time (six wavefronts
+    per workgroup do not spread evenly over four SIMDs, and the occupancy
+    query then promises more workgroups than the CUs hold). The first case
+    has 1536 tiles of six wavefronts each, more than any grid of them; the
+    others cap the grid far below their tile counts."""
+    work = workloads.configuration("c2", nx=64, ny=64, nz=48)
+    expected = oracle.sptrsv_csc(work.indptr, work.indices, work.data,
+                                 work.rhs, work.n)
+    csc = sptrsv.compile_sptrsv_csc(
+        execution_mode="sync_free", threads_per_block=tpb, task_lanes=4,
+        dependence_protocol="mailbox", tile_rows=tile_rows,
+        resident_waves_per_cu=waves_per_cu)
+    solve_and_check(csc, work, expected, exact=True)
+    assert "_lcd_claim" in csc.hip_kernel_source
+    matrix_rows = workloads.configuration("c3", n=150000)
+    csr = sptrsv.compile_sptrsv_csr(
+        execution_mode="sync_free", threads_per_block=tpb, task_lanes=8,
+        dependence_protocol="pull", tile_rows=tile_rows,
+        resident_waves_per_cu=waves_per_cu)
+    expected = oracle.sptrsv_csr(matrix_rows.indptr, matrix_rows.indices,
+                                 matrix_rows.data, matrix_rows.rhs,
+                                 matrix_rows.n)
+    solve_and_check(csr, matrix_rows, expected)
+
+
 @pytest.mark.parametrize("mode", ["wavefront", "sync_free"])
 @pytest.mark.parametrize("band_width", [2, 5, 64])
 def test_band_chains_run_in_both_executors(oracle, band_width, mode):

@@ -295,7 +295,21 @@ def test_calibrated_scheduler_prefers_what_measures_faster():
                               nonzeros=33423360, flops=5.8e7,
                               memory_bytes=568000000)
     assert engine.estimate(wide, "sync_free", 256, 1, 1, True, "mailbox",
-                           4).sync_s == pytest.approx(8388608 * 2.4e-10)
+                           4).sync_s == pytest.approx(8388608 * 1.9e-10)
+    # ... and so are the level launches (256^3 grid: 5.76 ms measured by
+    # levels, 2.4 to 2.9 ms by the persistent executors)
+    large = S.WorkloadFeatures(rows=16777216, edges=50135040, levels=766,
+                               nonzeros=66912256, flops=1.17e8,
+                               memory_bytes=1137000000,
+                               thread_work_items=50135040,
+                               thread_loop_invocations=16777216)
+    wave = engine.estimate(large, "wavefront", 128, 1, 1, True, "counter", 4)
+    assert wave.launch_s == pytest.approx(
+        766 * 1.6 * 1.7e-6 + 16777216 * 2.15e-10)
+    assert 5.0e-3 < wave.launch_s < 6.5e-3
+    chosen = engine.schedule(large, space)
+    assert (chosen.execution_mode, chosen.dependence_protocol) == (
+        "sync_free", "mailbox")
 
 
 def test_fingerprint_and_flops():
