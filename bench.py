@@ -54,7 +54,7 @@ TUNED = {
 # profiled reports null.
 MEASURED_TRAFFIC = {
     ("c2", "sync_free", "push", 4): 1_937_433_319,
-    ("c2", "sync_free", "mailbox", 4): 535_916_978,
+    ("c2", "sync_free", "mailbox", 4): 533_661_491,
     ("c3", "sync_free", "pull", 64): 1_531_636_035,
     ("c4", "sync_free", "pull", 64): 1_183_004_569,
     
