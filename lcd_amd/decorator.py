@@ -57,8 +57,8 @@ from lcd_amd.scheduler import (
     AnalyticScheduler,
     CalibratedScheduler,
     SchedulePlan,
-    TILE_THREADS_PER_BLOCK,
     automatic_tile_rows,
+    automatic_tile_threads,
     ScheduleSpace,
     count_inner_loop_flops,
     extract_workload_features,
@@ -240,12 +240,11 @@ def parallel(**kwargs):
             if not rows:
                 return schedule, None
             tiled = schedule
+            tile_threads = automatic_tile_threads(dag)
             if (tile_option == "auto" and thread_loop is not None
                     and kwargs.get("threads_per_block") is None
-                    and not TILE_THREADS_PER_BLOCK % max(
-                        schedule.task_lanes, 1)):
-                tiled = replace(
-                    schedule, threads_per_block=TILE_THREADS_PER_BLOCK)
+                    and not tile_threads % max(schedule.task_lanes, 1)):
+                tiled = replace(schedule, threads_per_block=tile_threads)
             if lower_variant(tiled.lowering_key, rows).tile_rows is None:
                 return schedule, None        # tiles do not apply to this loop
             return tiled, rows

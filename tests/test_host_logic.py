@@ -312,6 +312,29 @@ def test_calibrated_scheduler_prefers_what_measures_faster():
         "sync_free", "mailbox")
 
 
+def test_automatic_tiles_follow_problem_size():
+    """4096-row tiles of 384 threads while every tile can have a resident
+    workgroup; 2048 rows and 128 threads beyond (measured on 192^3 and 256^3
+    grids); smaller tiles for small problems; none without locality."""
+    class Dag:
+        topological_ids = True
+
+        def __init__(self, n, locality=0.66):
+            self.n, self.locality = n, locality
+
+        def tile_locality(self, rows):
+            return self.locality
+
+    assert S.automatic_tile_rows(Dag(128 ** 3)) == 4096
+    assert S.automatic_tile_threads(Dag(128 ** 3)) == 384
+    assert S.automatic_tile_rows(Dag(768 * 4096)) == 4096
+    assert S.automatic_tile_rows(Dag(192 ** 3)) == 2048
+    assert S.automatic_tile_threads(Dag(192 ** 3)) == 128
+    assert S.automatic_tile_rows(Dag(4096)) == 1024
+    assert S.automatic_tile_rows(Dag(1000)) is None
+    assert S.automatic_tile_rows(Dag(10 ** 6, locality=0.1)) is None
+
+
 def test_fingerprint_and_flops():
     a = np.arange(10, dtype=np.int32)
     values = {"Ap": a, "Ai": a.copy(), "Ax": np.ones(3), "n": 9}
