@@ -685,3 +685,95 @@ def test_full_size_headline_defaults(oracle):
     plan = solver.schedule_plan(work.indptr, work.indices, work.data,
                                 work.rhs, work.n)
     assert plan.tile_rows is None and plan.dag.tile_locality(4096) < 0.2
+
+
+def _random_lower_triangle(rng, kind, n):
+    """Strictly lower part scaled by 0.1 plus a diagonal in [1, 2): random
+    sparsity, a band, a 5-point grid, or an arrow (first column and last row
+    full: one task with n - 1 consumers, one with n - 1 producers)."""
+    import scipy.sparse as sp
+    if kind == "random":
+        per_row = float(rng.choice([0.5, 2, 6, 20]))
+        lower = sp.random(n, n, density=min(1.0, per_row / n),
+                          random_state=int(rng.integers(1 << 30)),
+                          format="csr")
+    elif kind == "band":
+        width = min(int(rng.integers(1, 12)), n - 1)
+        lower = sp.csr_matrix((n, n)) if width < 1 else sp.diags(
+            [rng.uniform(-1, 1, n)] * width,
+            [-k for k in range(1, width + 1)], shape=(n, n), format="csr")
+    elif kind == "grid":
+        side = max(1, int(np.sqrt(n)))
+        n = side * side
+        shift = sp.diags([np.ones(side)], [-1], shape=(side, side))
+        lower = (sp.kron(sp.identity(side), shift)
+                 + sp.kron(shift, sp.identity(side))).tocsr()
+    else:
+        lower = sp.lil_matrix((n, n))
+        lower[:, 0] = 1.0
+        lower[n - 1, :] = 1.0
+        lower = lower.tocsr()
+    return sp.tril(lower, -1) * 0.1 + sp.diags(rng.uniform(1, 2, n)), n
+
+
+@pytest.mark.parametrize("seed", [3, 4])
+def test_random_structures_under_random_schedules(oracle, seed):
+    """Random matrices (sizes 1 to 20 000 around the wavefront size and the
+    tile sizes) solved under randomly drawn executors, protocols, lanes per
+    task, tile sizes, grid caps and fetch variants, each against the oracle;
+    ILU0 of the symmetrised pattern bit-identical to the sequential loop."""
+    import scipy.sparse as sp
+    rng = np.random.default_rng(seed)
+    for trial in range(8):
+        n = int(rng.choice([1, 2, 63, 65, 300, 1000, 5000, 20000]))
+        kind = str(rng.choice(["random", "band", "grid", "arrow"]))
+        lower, n = _random_lower_triangle(rng, kind, n)
+        rhs = rng.standard_normal(n)
+        options = dict(
+            execution_mode=str(rng.choice(["sync_free", "wavefront"])),
+            threads_per_block=int(rng.choice([64, 128, 192, 256, 384])),
+            task_lanes=int(rng.choice([1, 2, 4, 8, 16, 64])))
+        persistent = options["execution_mode"] == "sync_free"
+        if persistent:
+            options["tile_rows"] = [None, 32, 64, 500, 4096][
+                int(rng.integers(5))]
+            options["resident_waves_per_cu"] = [None, 1, 0.25][
+                int(rng.integers(3))]
+            options["pipeline_fetch"] = bool(rng.integers(2))
+        print("random structure", seed, trial, kind, n, options, flush=True)
+        for storage, tiled, protocols in (
+                ("csc", "mailbox", ["mailbox", "push", "counter"]),
+                ("csr", "pull", ["pull", "counter"])):
+            matrix = (sp.csc_matrix(lower) if storage == "csc"
+                      else sp.csr_matrix(lower))
+            matrix.sort_indices()
+            indptr = matrix.indptr.astype(np.int32)
+            indices = matrix.indices.astype(np.int32)
+            solve = getattr(oracle, f"sptrsv_{storage}")
+            expected = solve(indptr, indices, matrix.data, rhs, n)
+            compile_solver = getattr(sptrsv, f"compile_sptrsv_{storage}")
+            for protocol in protocols if persistent else ["counter"]:
+                chosen = dict(options, dependence_protocol=protocol)
+                if protocol != tiled:
+                    chosen.pop("tile_rows", None)
+                result = compile_solver(**chosen)(
+                    indptr, indices, matrix.data, rhs, n)
+                assert relative_error(result, expected) <= TOLERANCE, (
+                    trial, storage, chosen)
+        if kind == "arrow":
+            continue
+        pattern = sp.csr_matrix(lower + lower.T * 0.5)
+        pattern.sort_indices()
+        indptr = pattern.indptr.astype(np.int32)
+        indices = pattern.indices.astype(np.int32)
+        expected = oracle.ilu0_csr(pattern.data.copy(), indices, indptr)
+        chosen = dict(execution_mode=options["execution_mode"],
+                      threads_per_block=int(rng.choice([64, 128, 256])))
+        if persistent:
+            chosen.update(task_lanes=int(rng.choice([8, 64])),
+                          dependence_protocol="pull",
+                          publish_values=bool(rng.integers(2)),
+                          look_ahead=bool(rng.integers(2)))
+        result = spilu0.compile_ilu0_csr(**chosen)(
+            pattern.data.copy(), indices, indptr)
+        np.testing.assert_array_equal(result, expected)
