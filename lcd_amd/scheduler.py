@@ -177,15 +177,24 @@ TILE_THREADS_PER_BLOCK = 384
 # than by hand-offs, and more, smaller tiles with fewer threads each measured
 # faster: 256^3 grid 1.91 ms with 2048 rows and 128 threads against 2.37 ms,
 # 192^3 1.05 against 1.23 ms; the 128^3 grid the other way round, 0.52 against
-# 0.33 ms.
+# 0.33 ms.  Only with wide levels, though: a 2048^2 grid has as many rows as
+# the 160^3 one but 4095 levels of at most 2048 rows, stays bound by
+# hand-offs and keeps the large tiles (3.86 ms against 4.07 ms).
 TILE_LARGE_PROBLEM_ROWS = 768 * TILE_ROWS
+TILE_LARGE_PROBLEM_WIDTH = 8192
 TILE_LARGE_ROWS = 2048
 TILE_LARGE_THREADS_PER_BLOCK = 128
 
 
+def _throughput_bound(dag):
+    levels = max(int(getattr(dag, "levels", 0) or 0), 1)
+    return (dag.n > TILE_LARGE_PROBLEM_ROWS
+            and dag.n / levels >= TILE_LARGE_PROBLEM_WIDTH)
+
+
 def automatic_tile_threads(dag):
     """Threads per tile that go with ``automatic_tile_rows``."""
-    return (TILE_LARGE_THREADS_PER_BLOCK if dag.n > TILE_LARGE_PROBLEM_ROWS
+    return (TILE_LARGE_THREADS_PER_BLOCK if _throughput_bound(dag)
             else TILE_THREADS_PER_BLOCK)
 
 
@@ -193,7 +202,7 @@ def automatic_tile_rows(dag):
     """Tile size for this DAG, or None when tiles would not pay."""
     if not getattr(dag, "topological_ids", False) or dag.n < 4 * TILE_MIN_ROWS:
         return None
-    rows = TILE_LARGE_ROWS if dag.n > TILE_LARGE_PROBLEM_ROWS else TILE_ROWS
+    rows = TILE_LARGE_ROWS if _throughput_bound(dag) else TILE_ROWS
     while rows > TILE_MIN_ROWS and dag.n < 4 * rows:
         rows //= 2
     if dag.tile_locality(rows) < TILE_MIN_LOCALITY:

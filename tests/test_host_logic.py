@@ -319,8 +319,9 @@ def test_automatic_tiles_follow_problem_size():
     class Dag:
         topological_ids = True
 
-        def __init__(self, n, locality=0.66):
+        def __init__(self, n, locality=0.66, levels=None):
             self.n, self.locality = n, locality
+            self.levels = levels or 3 * round(n ** (1 / 3)) - 2
 
         def tile_locality(self, rows):
             return self.locality
@@ -330,6 +331,9 @@ def test_automatic_tiles_follow_problem_size():
     assert S.automatic_tile_rows(Dag(768 * 4096)) == 4096
     assert S.automatic_tile_rows(Dag(192 ** 3)) == 2048
     assert S.automatic_tile_threads(Dag(192 ** 3)) == 128
+    flat_grid = Dag(2048 ** 2, levels=4095)      # narrow levels: hand-offs
+    assert S.automatic_tile_rows(flat_grid) == 4096
+    assert S.automatic_tile_threads(flat_grid) == 384
     assert S.automatic_tile_rows(Dag(4096)) == 1024
     assert S.automatic_tile_rows(Dag(1000)) is None
     assert S.automatic_tile_rows(Dag(10 ** 6, locality=0.1)) is None
