@@ -66,6 +66,7 @@ from lcd_amd.scheduler import (
     pointer_array_names,
     segment_trip_counts,
     compile_thread_trip_counter,
+    TRIP_PROBE_SAMPLE,
     measure_thread_trip_counts,
 )
 from lcd_amd.structural_lookups import (
@@ -351,13 +352,15 @@ def parallel(**kwargs):
                 return fast
             if trip_counter["probe"] is None:
                 trip_counter["probe"] = compile_thread_trip_counter(
-                    function_ast, thread_loop, function.__globals__)
+                    function_ast, thread_loop, function.__globals__,
+                    block_iterator=loop)
             host_values = {
                 name: (value.copy_to_host()
                        if hasattr(value, "copy_to_host") else value)
                 for name, value in dag_values.items()}
             return measure_thread_trip_counts(
-                trip_counter["probe"], host_values, argument_names)
+                trip_counter["probe"], host_values, argument_names,
+                sample_limit=TRIP_PROBE_SAMPLE)
 
         def create_schedule_plan(dag_values):
             device = get_device()

@@ -160,6 +160,29 @@ def update(data, indices, indptr):
     np.testing.assert_array_equal(data, original)
     with pytest.raises(S.SchedulerError, match="Could not find"):
         S.compile_thread_trip_counter(ast.parse(source), "missing")
+    # long block loops are sampled with a stride and the totals scaled
+    # (band matrix: rows from 3 on all alike, so the estimate is close)
+    n, width = 4000, 3
+    rows = [list(range(max(0, i - width), i + 1)) for i in range(n)]
+    arrays = {"data": np.ones(sum(map(len, rows))),
+              "indices": np.concatenate(rows),
+              "indptr": np.cumsum([0] + [len(r) for r in rows])}
+    names = ("data", "indices", "indptr")
+    sampling = S.compile_thread_trip_counter(ast.parse(source), "j_ptr",
+                                             block_iterator="i")
+    exact = S.measure_thread_trip_counts(sampling, arrays, names)
+    assert exact == S.measure_thread_trip_counts(
+        S.compile_thread_trip_counter(ast.parse(source), "j_ptr"),
+        arrays, names)
+    assert S.measure_thread_trip_counts(sampling, arrays, names,
+                                        sample_limit=n) == exact
+    estimate = S.measure_thread_trip_counts(sampling, arrays, names,
+                                            sample_limit=500)
+    assert estimate["invocations"] == pytest.approx(len(exact), rel=0.01)
+    assert estimate["work_items"] == pytest.approx(sum(exact), rel=0.01)
+    assert estimate["work_squares"] == pytest.approx(
+        sum(c * c for c in exact), rel=0.01)
+    assert S.measure_thread_trip_counts(sampling, arrays, names) == exact
 
 
 def test_workload_features_and_unroll_choice():
