@@ -608,11 +608,19 @@ __device__ inline uint64_t lcdhip_mix64(uint64_t x)
     return x;
 }
 
-// Position-salted word hashes combined with + and ^ (both commutative, so the
-// digest does not depend on the order in which waves finish).
-__global__ void lcdhip_digest_kernel(const uint32_t *__restrict__ words,
-                                     size_t count, unsigned long long *out)
+// Position-salted word hashes combined with + and ^ (both commutative and
+// associative, so the digest does not depend on how the words are dealt out to
+// lanes and workgroups).  Every workgroup leaves one pair of partial results
+// in partial[2 * blockIdx.x ..]; no atomics, nothing to clear beforehand.
+#define LCDHIP_DIGEST_MAX_BLOCKS 1024
+#define LCDHIP_DIGEST_THREADS 256
+
+__global__ void __launch_bounds__(LCDHIP_DIGEST_THREADS)
+lcdhip_digest_partial_kernel(const uint32_t *__restrict__ words, size_t count,
+                             unsigned long long *__restrict__ partial)
 {
+    __shared__ unsigned long long wave_sum[LCDHIP_DIGEST_THREADS / 64];
+    __shared__ unsigned long long wave_mix[LCDHIP_DIGEST_THREADS / 64];
     size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
     size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
     uint64_t sum = 0, mixed = 0;
@@ -627,41 +635,105 @@ __global__ void lcdhip_digest_kernel(const uint32_t *__restrict__ words,
         mixed ^= __shfl_down(mixed, offset);
     }
     if ((threadIdx.x & 63) == 0) {
-        atomicAdd(&out[0], static_cast<unsigned long long>(sum));
-        atomicXor(&out[1], static_cast<unsigned long long>(mixed));
+        wave_sum[threadIdx.x >> 6] = sum;
+        wave_mix[threadIdx.x >> 6] = mixed;
     }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < LCDHIP_DIGEST_THREADS / 64; ++w) {
+            sum += wave_sum[w];
+            mixed ^= wave_mix[w];
+        }
+        partial[2 * blockIdx.x] = sum;
+        partial[2 * blockIdx.x + 1] = mixed;
+    }
+}
+
+// One workgroup folds the first `blocks` pairs (whatever lies behind them is
+// ignored) and salts the sum with the length.
+__global__ void __launch_bounds__(LCDHIP_DIGEST_THREADS)
+lcdhip_digest_final_kernel(const unsigned long long *__restrict__ partial,
+                           int blocks, unsigned long long bytes,
+                           unsigned long long *__restrict__ out)
+{
+    __shared__ unsigned long long wave_sum[LCDHIP_DIGEST_THREADS / 64];
+    __shared__ unsigned long long wave_mix[LCDHIP_DIGEST_THREADS / 64];
+    uint64_t sum = 0, mixed = 0;
+    for (int b = threadIdx.x; b < blocks; b += LCDHIP_DIGEST_THREADS) {
+        sum += partial[2 * b];
+        mixed ^= partial[2 * b + 1];
+    }
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        sum += __shfl_down(sum, offset);
+        mixed ^= __shfl_down(mixed, offset);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        wave_sum[threadIdx.x >> 6] = sum;
+        wave_mix[threadIdx.x >> 6] = mixed;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < LCDHIP_DIGEST_THREADS / 64; ++w) {
+            sum += wave_sum[w];
+            mixed ^= wave_mix[w];
+        }
+        out[0] = sum ^ (bytes * 0x9e3779b97f4a7c15ull);
+        out[1] = mixed;
+    }
+}
+
+// Both digest entry points: partial results into `d_partial` (room for
+// 2 * LCDHIP_DIGEST_MAX_BLOCKS words), the digest into d_out[0..1].
+static int digest_enqueue(const void *d_data, size_t bytes,
+                          unsigned long long *d_partial,
+                          unsigned long long *d_out, hipStream_t hip_stream)
+{
+    size_t count = bytes / 4;
+    int blocks = static_cast<int>(std::min<size_t>(
+        (count + LCDHIP_DIGEST_THREADS - 1) / LCDHIP_DIGEST_THREADS,
+        LCDHIP_DIGEST_MAX_BLOCKS));
+    if (blocks) {
+        hipLaunchKernelGGL(lcdhip_digest_partial_kernel, dim3(blocks),
+                           dim3(LCDHIP_DIGEST_THREADS), 0, hip_stream,
+                           static_cast<const uint32_t *>(d_data), count,
+                           d_partial);
+        LCDHIP_CHECK(hipGetLastError());
+    }
+    hipLaunchKernelGGL(lcdhip_digest_final_kernel, dim3(1),
+                       dim3(LCDHIP_DIGEST_THREADS), 0, hip_stream, d_partial,
+                       blocks, static_cast<unsigned long long>(bytes), d_out);
+    LCDHIP_CHECK(hipGetLastError());
+    return LCDHIP_OK;
 }
 
 extern "C" int lcdhip_digest(const void *d_data, size_t bytes, uint64_t out[2],
                              lcdhip_stream stream)
 {
     LCDHIP_REQUIRE_INIT();
-    if (!out || (bytes & 3)) {
-        set_error("digest needs out and a multiple of 4 bytes");
+    if (!out || (bytes & 3) || (bytes && !d_data)) {
+        set_error("digest needs data, out and a multiple of 4 bytes");
         return LCDHIP_ERR_ARGUMENT;
     }
     hipStream_t hip_stream = resolve_stream(stream);
-    unsigned long long *d_out = nullptr;
-    LCDHIP_CHECK(hipMalloc(&d_out, 16));
-    LCDHIP_CHECK(hipMemsetAsync(d_out, 0, 16, hip_stream));
-    size_t count = bytes / 4;
-    if (count) {
-        unsigned blocks = static_cast<unsigned>(
-            std::min<size_t>((count + 255) / 256, 8192));
-        hipLaunchKernelGGL(lcdhip_digest_kernel, dim3(blocks), dim3(256), 0,
-                           hip_stream, static_cast<const uint32_t *>(d_data),
-                           count, d_out);
+    unsigned long long *d_work = nullptr;   // partial results, then the digest
+    const size_t partial_words = 2 * LCDHIP_DIGEST_MAX_BLOCKS;
+    LCDHIP_CHECK(hipMalloc(&d_work, (partial_words + 2) * 8));
+    int enqueued = digest_enqueue(d_data, bytes, d_work, d_work + partial_words,
+                                  hip_stream);
+    hipError_t status = hipSuccess;
+    if (enqueued == LCDHIP_OK) {
+        status = hipMemcpyAsync(out, d_work + partial_words, 16,
+                                hipMemcpyDeviceToHost, hip_stream);
+        if (status == hipSuccess)
+            status = hipStreamSynchronize(hip_stream);
     }
-    hipError_t status = hipMemcpyAsync(out, d_out, 16, hipMemcpyDeviceToHost,
-                                       hip_stream);
-    if (status == hipSuccess)
-        status = hipStreamSynchronize(hip_stream);
-    (void)hipFree(d_out);
+    (void)hipFree(d_work);
+    if (enqueued != LCDHIP_OK)
+        return enqueued;
     if (status != hipSuccess) {
         set_error("digest failed: %s", hipGetErrorString(status));
         return LCDHIP_ERR_HIP;
     }
-    out[0] ^= static_cast<uint64_t>(bytes) * 0x9e3779b97f4a7c15ull;
     return LCDHIP_OK;
 }
 

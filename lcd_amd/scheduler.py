@@ -20,7 +20,6 @@ import ast
 import hashlib
 import itertools
 import math
-from collections import deque
 from copy import deepcopy
 from dataclasses import dataclass, replace
 
@@ -731,61 +730,62 @@ def _array_bytes(argument_values):
 
 def count_inner_loop_flops(function_ast, block_iterator,
                            thread_loop_iterator=None):
-    block_loop = _find_loop(function_ast, block_iterator)
+    """Arithmetic operators in one iteration of the loop that the cost model
+    prices (same result as compiler/scheduler.py:617-629): the thread-mapped
+    loop when it is named and present, otherwise the most deeply nested
+    ``for`` below the block loop; never less than 1."""
+    block_loop = _loop_over(function_ast, block_iterator)
     if block_loop is None:
         return 1
-    inner = None
+    priced = None
     if thread_loop_iterator is not None:
-        inner = _find_loop(block_loop, thread_loop_iterator)
-    if inner is None:
-        inner = _deepest_loop(block_loop)
-    counter = _ArithmeticCounter()
-    for statement in inner.body:
-        counter.visit(statement)
-    return max(counter.count, 1)
+        priced = _loop_over(block_loop, thread_loop_iterator)
+    if priced is None:
+        priced = _innermost_loop(block_loop)
+    return max(sum(_arithmetic_ops(statement) for statement in priced.body), 1)
 
 
-def _find_loop(tree, iterator):
-    for node in ast.walk(tree):
-        if (isinstance(node, ast.For) and isinstance(node.target, ast.Name)
-                and node.target.id == iterator):
-            return node
-    return None
+def _loop_over(tree, iterator):
+    """First ``for <iterator> in ...`` of ``tree`` in breadth-first order."""
+    return next((node for node in ast.walk(tree)
+                 if isinstance(node, ast.For)
+                 and isinstance(node.target, ast.Name)
+                 and node.target.id == iterator), None)
 
 
-def _deepest_loop(loop):
-    best_depth, best = 0, loop
-    pending = deque([(loop, 0)])
-    while pending:
-        node, depth = pending.popleft()
+def _innermost_loop(loop):
+    """The ``for`` with the most enclosing loops below ``loop`` (``loop``
+    itself when it has none); among equals the one nearest the root of the
+    syntax tree, then the leftmost."""
+    ranked = []
+
+    def descend(node, loops, depth):
         for child in ast.iter_child_nodes(node):
-            child_depth = depth + isinstance(child, ast.For)
-            if isinstance(child, ast.For) and child_depth > best_depth:
-                best_depth, best = child_depth, child
-            pending.append((child, child_depth))
-    return best
+            inside = loops + isinstance(child, ast.For)
+            if isinstance(child, ast.For):
+                ranked.append((-inside, depth + 1, len(ranked), child))
+            descend(child, inside, depth + 1)
+
+    descend(loop, 0, 0)
+    return min(ranked)[3] if ranked else loop
 
 
-class _ArithmeticCounter(ast.NodeVisitor):
-    def __init__(self):
-        self.count = 0
-
-    def visit_BinOp(self, node):
-        if isinstance(node.op, ARITHMETIC_OPERATORS):
-            self.count += 1
-        self.generic_visit(node)
-
-    def visit_AugAssign(self, node):
-        if isinstance(node.op, ARITHMETIC_OPERATORS):
-            self.count += 1
-        self.visit(node.value)
-
-    def visit_Subscript(self, node):
-        self.visit(node.value)
-
-    def visit_For(self, node):
-        for statement in node.body:
-            self.visit(statement)
+def _arithmetic_ops(node):
+    """Arithmetic operators that ``node`` executes once.  Index expressions
+    of subscripts and the headers of nested loops are address and control
+    work, not floating-point work, and are left out; an augmented assignment
+    counts its operator and its right-hand side."""
+    if isinstance(node, ast.Subscript):
+        return _arithmetic_ops(node.value)
+    if isinstance(node, ast.For):
+        return sum(_arithmetic_ops(statement) for statement in node.body)
+    if isinstance(node, ast.AugAssign):
+        return (isinstance(node.op, ARITHMETIC_OPERATORS)
+                + _arithmetic_ops(node.value))
+    own = (isinstance(node, ast.BinOp)
+           and isinstance(node.op, ARITHMETIC_OPERATORS))
+    return own + sum(_arithmetic_ops(child)
+                     for child in ast.iter_child_nodes(node))
 
 
 # ---- plan cache keys -------------------------------------------------------
