@@ -316,6 +316,20 @@ int lcdhip_gather_i32(int32_t *d_dst, const int32_t *d_src,
 int lcdhip_digest(const void *d_data, size_t bytes, uint64_t out[2],
                   lcdhip_stream stream);
 
+/* The same digest for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc); it has no
+ * counterpart in the reference.  Calls no hipMalloc/hipFree and does not
+ * synchronise: two kernels are enqueued on `stream` and the 16-byte digest is
+ * stored to the device buffer d_out[0..1], equal to what lcdhip_digest
+ * returns for the same bytes.  The per-workgroup partial results go to a
+ * 16 KiB work area inside the library, one per GPU, held until the process
+ * ends and shared by every call on that GPU: calls that overlap on one GPU
+ * (two streams) race.  bytes must be a multiple of 4 and at most
+ * LCDHIP_DIGEST_NOALLOC_MAX_BYTES. */
+#define LCDHIP_DIGEST_NOALLOC_MAX_BYTES ((size_t)1 << 36)
+int lcdhip_digest_noalloc(const void *d_data, size_t bytes, uint64_t *d_out,
+                          lcdhip_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

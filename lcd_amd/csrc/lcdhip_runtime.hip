@@ -79,6 +79,17 @@ extern "C" int lcdhip_device_count(int *count)
     return LCDHIP_OK;
 }
 
+// Work area of lcdhip_digest_noalloc: the per-workgroup partial results of
+// the digest kernels (16 KiB).  One copy per GPU, held until the process
+// ends.  The array's name is only a host-side handle; its address on a device
+// comes from hipGetSymbolAddress while that device is current (lcdhip_init)
+// and is what host code passes on.
+#define LCDHIP_DIGEST_SCRATCH_WORDS (2 * 1024)
+static __device__ __align__(256) unsigned long long
+    lcdhip_digest_scratch[LCDHIP_DIGEST_SCRATCH_WORDS];
+#define LCDHIP_MAX_DEVICES 64
+static unsigned long long *g_digest_scratch[LCDHIP_MAX_DEVICES] = {};
+
 extern "C" int lcdhip_init(int device)
 {
     auto &ctx = context();
@@ -97,6 +108,12 @@ extern "C" int lcdhip_init(int device)
     LCDHIP_CHECK(hipGetDeviceProperties(&ctx.props, device));
     if (ctx.stream == nullptr)
         LCDHIP_CHECK(hipStreamCreateWithFlags(&ctx.stream, hipStreamNonBlocking));
+    if (device < LCDHIP_MAX_DEVICES && g_digest_scratch[device] == nullptr) {
+        void *address = nullptr;
+        LCDHIP_CHECK(hipGetSymbolAddress(&address,
+                                         HIP_SYMBOL(lcdhip_digest_scratch)));
+        g_digest_scratch[device] = static_cast<unsigned long long *>(address);
+    }
     ctx.device = device;
     ctx.ready = true;
     return LCDHIP_OK;
@@ -735,6 +752,35 @@ extern "C" int lcdhip_digest(const void *d_data, size_t bytes, uint64_t out[2],
         return LCDHIP_ERR_HIP;
     }
     return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_digest_noalloc(const void *d_data, size_t bytes,
+                                     uint64_t *d_out, lcdhip_stream stream)
+{
+    LCDHIP_REQUIRE_INIT();
+    static_assert(LCDHIP_DIGEST_SCRATCH_WORDS >= 2 * LCDHIP_DIGEST_MAX_BLOCKS,
+                  "scratch must hold one pair per workgroup");
+    if (!d_out || (bytes & 3) || (bytes && !d_data)) {
+        set_error("lcdhip_digest_noalloc needs data, d_out and a multiple of "
+                  "4 bytes");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    if (bytes > LCDHIP_DIGEST_NOALLOC_MAX_BYTES) {
+        set_error("lcdhip_digest_noalloc: %zu bytes exceed the limit of %zu",
+                  bytes, static_cast<size_t>(LCDHIP_DIGEST_NOALLOC_MAX_BYTES));
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    const int device = context().device;
+    unsigned long long *scratch =
+        device >= 0 && device < LCDHIP_MAX_DEVICES ? g_digest_scratch[device]
+                                                   : nullptr;
+    if (!scratch) {
+        set_error("lcdhip_digest_noalloc: no work area on device %d", device);
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    return digest_enqueue(d_data, bytes, scratch,
+                          reinterpret_cast<unsigned long long *>(d_out),
+                          resolve_stream(stream));
 }
 
 // ---------------------------------------------------- machine constants ----

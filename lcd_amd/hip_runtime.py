@@ -131,7 +131,7 @@ EXPORTED_SYMBOLS = (
     "lcdhip_dag_tile_order", "lcdhip_dag_tile_locality",
     "lcdhip_dag_task_records",
     "lcdhip_lookup_build", "lcdhip_gather_i32",
-    "lcdhip_digest",
+    "lcdhip_digest", "lcdhip_digest_noalloc",
 )
 
 _library = None
@@ -676,6 +676,20 @@ class HIPDevice:
             ctypes.c_void_p(device_pointer(array)), ctypes.c_size_t(nbytes),
             out, self.stream))
         return int(out[0]), int(out[1])
+
+    def digest_noalloc(self, array, out):
+        """Enqueue the digest of ``array`` into the device array ``out``
+        (two uint64) without allocating or synchronising
+        (``lcdhip_digest_noalloc``)."""
+        shape, dtype = device_array_meta(array)
+        nbytes = int(np.prod(shape)) * dtype.itemsize
+        out_shape, out_dtype = device_array_meta(out)
+        if int(np.prod(out_shape)) * out_dtype.itemsize < 16:
+            raise HIPRuntimePreparationError(
+                "digest_noalloc needs 16 bytes of device memory for the result")
+        _check(self.lib.lcdhip_digest_noalloc(
+            ctypes.c_void_p(device_pointer(array)), ctypes.c_size_t(nbytes),
+            ctypes.c_void_p(device_pointer(out)), self.stream))
 
 
 _default_device = None
