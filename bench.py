@@ -8,11 +8,21 @@ kernels run (all replayed from one hipGraph).  Host/device copies, the DAG
 inspection and hiprtc compilation happen before the timed region and are
 reported separately.
 
-Default workload: configuration 2 of BASELINE.json (SpTRSV-CSC on the lower
-factor of the 3-D 7-point Laplacian, 128^3).  Prints ONE JSON line.
+Headline workload (``value``, ``ms_per_step``, ``roofline``,
+``cpu_baseline``): configuration 2 of BASELINE.json (SpTRSV-CSC on the lower
+factor of the 3-D 7-point Laplacian, 128^3).  Without ``--config`` the same
+JSON line also carries, under ``configs``, one record for each of the five
+configurations and for configuration 2 under the level-launched (wavefront)
+executor: solve time, GFLOP/s, GB/s, roofline fraction of the dominant kernel
+with its measured traffic, the dependency-latency bound ``levels x hand-off``,
+the single-core CPU baseline and the error against the sequential loop, the
+way the reference's harness reports per matrix
+(benchmark/sptrsv_benchmark.py:420-431,626, benchmark/spilu0_benchmark.py:767).
+Prints ONE JSON line.
 """
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -48,25 +58,50 @@ TUNED = {
 }
 
 
-# HBM bytes per launch of the dominant kernel from rocprofv3 --pmc FETCH_SIZE /
-# WRITE_SIZE (scaled by the copy-probe kernel); source: the summaries under
-# profiles/.  Keyed by (config, mode, protocol, task_lanes); anything not
-# profiled reports null.
-MEASURED_TRAFFIC = {
-    ("c2", "sync_free", "push", 4): 1_937_433_319,
-    ("c2", "sync_free", "mailbox", 4): 533_661_491,
-    ("c3", "sync_free", "pull", 64): 1_531_636_035,
-    ("c4", "sync_free", "pull", 64): 1_183_004_569,
-    
-}
+# HBM bytes per launch of the dominant kernel, from rocprofv3 --pmc FETCH_SIZE /
+# WRITE_SIZE runs scaled by the copy-probe kernel: profiles/traffic.json holds
+# one entry per profiled (configuration, executor settings) next to the
+# summary it was taken from; anything not profiled reports null.
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+OVERRIDE_VARIABLES = ("LCD_HIP_OVERRIDE_DIR", "LCD_HIP_EXTRA_OPTIONS")
+# Steps of the sub-records (the headline uses --steps / --warmup): the chain
+# of configuration 5 takes long per solve.
+SUB_STEPS = {"c1": (50, 10), "c2": (50, 10), "c3": (50, 10), "c4": (20, 3),
+             "c5": (3, 1)}
+CPU_SECONDS_SUB = 3.0
+RTOL, ATOL_SCALE = 1e-12, 1e-15
 
 
-def build_solver(work, args):
+def traffic_key(config, mode, protocol, lanes, tile_rows):
+    return f"{config}|{mode}|{protocol}|lanes={lanes}|tile_rows={tile_rows or 0}"
+
+
+def measured_traffic(key):
+    try:
+        with open(TRAFFIC_FILE) as handle:
+            entry = json.load(handle).get(key)
+    except (OSError, ValueError):
+        return None
+    return None if entry is None else int(entry["bytes_per_launch"])
+
+
+def elementwise_error(got, expected):
+    """max_i |got_i - ref_i| / (|ref_i| + 1e-3 max|ref|): at most 1e-12 exactly
+    when |got - ref| <= 1e-12 |ref| + 1e-15 max|ref| holds for every element
+    (the reference's own check is element-wise with rtol 1e-10 / atol 1e-12,
+    compiler/e2e_tests/test_sptrsv_e2e.py:64-69; this one is tighter)."""
+    floor = float(np.max(np.abs(expected))) * ATOL_SCALE / RTOL
+    return float(np.max(np.abs(got - expected) / (np.abs(expected) + floor)))
+
+
+def build_solver(work, args, config):
     from lcd_amd.demo import spilu0, sptrsv
-    options = {} if args.auto else dict(TUNED[args.config])
+    options = {} if args.auto else dict(TUNED[config])
     if args.mode:
         options["execution_mode"] = args.mode
-        if args.mode != TUNED[args.config]["execution_mode"] and not args.auto:
+        if args.mode != TUNED[config]["execution_mode"] and not args.auto:
+            options.pop("tile_rows", None)
+            options.pop("spin_sleep", None)
             options.pop("resident_waves_per_cu", None)
             options.pop("dependence_protocol", None)
     if args.tpb:
@@ -143,7 +178,6 @@ def cpu_baseline(work, seconds):
 
 def python_loop_baseline(work, rows):
     """The undecorated Python loop on the leading ``rows`` tasks."""
-    from oracle import lcd_oracle
     rows = min(rows, work.n)
     ptr = work.indptr[:rows + 1].tolist()
     if work.kind != "sptrsv_csc":
@@ -156,11 +190,204 @@ def python_loop_baseline(work, rows):
         for j in range(ptr[i] + 1, ptr[i + 1]):
             x[idx[j]] += val[j] * x[i]
     elapsed = time.perf_counter() - start
-    del lcd_oracle
     return {"rows": rows, "seconds": round(elapsed, 4),
             "projected_full_solve_ms": round(elapsed / rows * work.n * 1e3, 1),
             "note": "CPython list-based restatement of the README loop, "
                     "one core; numba is not installed on this image"}
+
+
+def oracle_result(work):
+    from oracle import lcd_oracle
+    if work.kind == "sptrsv_csc":
+        return lcd_oracle.sptrsv_csc(work.indptr, work.indices, work.data,
+                                     work.rhs, work.n)
+    if work.kind == "sptrsv_csr":
+        return lcd_oracle.sptrsv_csr(work.indptr, work.indices, work.data,
+                                     work.rhs, work.n)
+    return lcd_oracle.ilu0_csr(work.data, work.indices, work.indptr)
+
+
+def run_configuration(config, args, device, steps, warmup, handoff_s,
+                      cpu_seconds, python_loop=False):
+    """Time one configuration; returns its record (see the module text)."""
+    from lcd_amd import workloads
+    from lcd_amd.dag_codegen import build_device_dag
+    t0 = time.perf_counter()
+    work = workloads.configuration(config)
+    generate_s = time.perf_counter() - t0
+
+    solver = build_solver(work, args, config)
+    t0 = time.perf_counter()
+    if work.kind == "ilu0_csr":
+        pristine = device.to_device(work.data)
+        operands = [device.to_device(work.data),
+                    device.to_device(work.indices),
+                    device.to_device(work.indptr)]
+        scalars = []
+    else:
+        pristine = None
+        operands = [device.to_device(a) for a in
+                    (work.indptr, work.indices, work.data, work.rhs)]
+        scalars = [work.n]
+    upload_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    call = solver.bind(*operands, *scalars)
+    device.synchronize()
+    inspect_s = time.perf_counter() - t0
+    schedule = solver.current_schedule
+    plan = solver.schedule_plan(*operands, *scalars)
+    lowering = solver.hip_lowering
+
+    def step():
+        if work.kind == "ilu0_csr":
+            device.copy(operands[0], pristine)   # factorisation is in place
+        call.launch()
+
+    t0 = time.perf_counter()
+    step()
+    call.synchronize()
+    first_call_s = time.perf_counter() - t0
+    # a long run (the chain of configuration 5 takes seconds per step) says
+    # so once a minute on stderr; the timed region itself is not touched
+    finished = threading.Event()
+
+    def heartbeat():
+        began = time.perf_counter()
+        while not finished.wait(60.0):
+            print(f"bench: {config} still running after "
+                  f"{time.perf_counter() - began:.0f} s "
+                  f"(first step took {first_call_s:.2f} s)",
+                  file=sys.stderr, flush=True)
+
+    threading.Thread(target=heartbeat, daemon=True).start()
+    for _ in range(warmup):
+        step()
+    call.synchronize()
+    start, stop = device.event(), device.event()
+    device.record(start)
+    for _ in range(steps):
+        step()
+    device.record(stop)
+    elapsed_ms = device.elapsed_ms(start, stop)
+    call.synchronize()
+    finished.set()
+    ms_per_step = elapsed_ms / steps
+
+    launches_per_step = (plan.dag.levels
+                         if schedule.execution_mode == "wavefront" else 1)
+    gbps = work.algorithmic_bytes / (ms_per_step * 1e-3) / 1e9
+    tile_rows = getattr(lowering, "tile_rows", None)
+    record = {
+        "value": round(gbps, 3),
+        "unit": "GB/s",
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "config": {
+            "workload": work.name, "kind": work.kind, "n": work.n,
+            "nnz": work.nnz, "levels": plan.dag.levels,
+            "dag_edges": plan.dag.edges, "seed": work.seed,
+            "execution_mode": schedule.execution_mode,
+            "threads_per_block": schedule.threads_per_block,
+            "task_lanes": lowering.task_lanes,
+            "thread_unroll": schedule.thread_unroll,
+            "dependence_protocol": lowering.dependence_protocol,
+            "tile_rows": tile_rows,
+        },
+        "roofline_pct": round(100.0 * gbps / HBM_PEAK_GBPS, 3),
+        "algorithmic_bytes": work.algorithmic_bytes,
+        "setup": {
+            "generate_s": round(generate_s, 3), "upload_s": round(upload_s, 3),
+            "inspect_compile_bind_s": round(inspect_s, 3),
+            "first_call_s": round(first_call_s, 4),
+        },
+    }
+    # the on-device inspector alone (edges, counts, level sets and, for the
+    # mailbox protocol, the incoming listing), operands resident
+    names = solver.dag_plan.arguments
+    values = dict(zip(names, list(operands) + scalars))
+    if work.kind == "ilu0_csr":
+        values["n"] = work.n
+    mailbox = lowering.dependence_protocol == "mailbox"
+    inspector = []
+    for _ in range(1 if config == "c5" else 3):
+        device.synchronize()
+        t0 = time.perf_counter()
+        dag = build_device_dag(solver.dag_plan, values, device, levels=True,
+                               incoming=mailbox)
+        device.synchronize()
+        inspector.append(time.perf_counter() - t0)
+        dag.destroy()
+    record["setup"]["inspector_ms"] = round(min(inspector) * 1e3, 3)
+    record["gflops"] = round(
+        work.true_flops / (ms_per_step * 1e-3) / 1e9, 3)
+    record["true_flops"] = int(work.true_flops)
+    record["gflops_reference_formula"] = round(
+        work.reference_style_flops / (ms_per_step * 1e-3) / 1e9, 3)
+
+    kernel_ms = ms_per_step / launches_per_step
+    if schedule.execution_mode == "sync_free":
+        # the persistent executor is one launch per step: time that launch
+        # alone with HIP events on the library stream (eager launches, so the
+        # events sit directly around the kernel; the step above also holds
+        # the reset and operand-staging kernels)
+        device.kernel_timing = {"name": lowering.kernel_name}
+        try:
+            for _ in range(min(steps, 20)):
+                if work.kind == "ilu0_csr":
+                    device.copy(operands[0], pristine)
+                call.launch(use_graph=False)
+            call.synchronize()
+            pairs = device.kernel_timing.get("events", [])
+            if pairs:
+                kernel_ms = sum(device.elapsed_ms(a, b)
+                                for a, b in pairs) / len(pairs)
+        finally:
+            device.kernel_timing = None
+    bytes_per_launch = work.algorithmic_bytes / launches_per_step
+    achieved = bytes_per_launch / (kernel_ms * 1e-3) / 1e9
+    key = traffic_key(config, schedule.execution_mode,
+                      lowering.dependence_protocol, lowering.task_lanes,
+                      tile_rows)
+    record["roofline"] = {
+        "bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBPS,
+        "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 6),
+        "traffic": measured_traffic(key),
+        "traffic_key": key,
+        "kernel": lowering.kernel_name,
+        "launches_per_step": launches_per_step,
+        "avg_launch_ms": round(kernel_ms, 6),
+        "dependency_levels": plan.dag.levels,
+        # what the dependences alone allow: every level waits for one
+        # release->acquire hand-off between workgroups (idle-machine figure)
+        "handoff_us": round(handoff_s * 1e6, 4),
+        "latency_bound_ms": round(plan.dag.levels * handoff_s * 1e3, 5),
+    }
+
+    if not args.no_check:
+        expected = oracle_result(work)
+        if work.kind == "ilu0_csr":
+            call.synchronize()
+            got = operands[0].copy_to_host()
+        else:
+            got = call.result()
+        error = elementwise_error(got, expected)
+        record["max_rel_error_vs_oracle"] = error
+        record["bit_identical_to_sequential_loop"] = bool(
+            np.array_equal(got, expected))
+        record["parity_ok"] = bool(error <= RTOL)
+        del got, expected
+    if not args.no_cpu:
+        record["cpu_baseline"] = cpu_baseline(work, cpu_seconds)
+        if python_loop:
+            loop = python_loop_baseline(work, 200_000)
+            if loop is not None:
+                record["cpu_python_loop"] = loop
+    # release the device memory of this configuration before the next one
+    del call, plan, solver, operands, pristine, values, work
+    gc.collect()
+    device.synchronize()
+    return record
 
 
 def main():
@@ -168,8 +395,11 @@ def main():
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=10)
-    parser.add_argument("--config", default="c2",
-                        choices=["c1", "c2", "c3", "c4", "c5"])
+    parser.add_argument("--config", default=None,
+                        choices=["c1", "c2", "c3", "c4", "c5"],
+                        help="time this configuration only (default: "
+                             "configuration 2 as the headline plus a record "
+                             "for every configuration)")
     parser.add_argument("--mode", default=None)
     parser.add_argument("--tpb", type=int, default=None)
     parser.add_argument("--lanes", type=int, default=None)
@@ -206,196 +436,86 @@ def main():
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-check", action="store_true")
     parser.add_argument("--arch", action="store_true",
-                        help="also report measured machine constants")
+                        help="also report every measured machine constant")
     args = parser.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this path (one sparse triangular "
               "DAG) runs on a single MI355X; --gpus must be 1.",
               file=sys.stderr)
         return 2
+    overrides = {name: os.environ[name] for name in OVERRIDE_VARIABLES
+                 if os.environ.get(name)}
+    if overrides:
+        print(f"bench: generated kernels are modified by {overrides}; the "
+              "record says so", file=sys.stderr)
 
-    from lcd_amd import hip_runtime, workloads
+    from lcd_amd import hip_runtime
     device = hip_runtime.default_device()
-    t0 = time.perf_counter()
-    work = workloads.configuration(args.config)
-    generate_s = time.perf_counter() - t0
+    arch = device.measure_arch()
+    handoff_s = float(arch["handoff_s"])
 
-    solver = build_solver(work, args)
-    t0 = time.perf_counter()
-    if work.kind == "ilu0_csr":
-        pristine = device.to_device(work.data)
-        operands = [device.to_device(work.data),
-                    device.to_device(work.indices),
-                    device.to_device(work.indptr)]
-        scalars = []
-    else:
-        operands = [device.to_device(a) for a in
-                    (work.indptr, work.indices, work.data, work.rhs)]
-        scalars = [work.n]
-    upload_s = time.perf_counter() - t0
-    t0 = time.perf_counter()
-    call = solver.bind(*operands, *scalars)
-    device.synchronize()
-    inspect_s = time.perf_counter() - t0
-    schedule = solver.current_schedule
-    plan = solver.schedule_plan(*operands, *scalars)
-
-    def step():
-        if work.kind == "ilu0_csr":
-            device.copy(operands[0], pristine)   # factorisation is in place
-        call.launch()
-
-    t0 = time.perf_counter()
-    step()
-    call.synchronize()
-    first_call_s = time.perf_counter() - t0
-    # a long run (the chain of configuration 5 takes seconds per step) says
-    # so once a minute on stderr; the timed region itself is not touched
-    finished = threading.Event()
-
-    def heartbeat():
-        began = time.perf_counter()
-        while not finished.wait(60.0):
-            print(f"bench: still running after "
-                  f"{time.perf_counter() - began:.0f} s "
-                  f"(first step took {first_call_s:.2f} s)",
-                  file=sys.stderr, flush=True)
-
-    threading.Thread(target=heartbeat, daemon=True).start()
-    for _ in range(args.warmup):
-        step()
-    call.synchronize()
-    start, stop = device.event(), device.event()
-    device.record(start)
-    for _ in range(args.steps):
-        step()
-    device.record(stop)
-    elapsed_ms = device.elapsed_ms(start, stop)
-    call.synchronize()
-    finished.set()
-    ms_per_step = elapsed_ms / args.steps
-
-    launches_per_step = (plan.dag.levels
-                         if schedule.execution_mode == "wavefront" else 1)
-    gbps = work.algorithmic_bytes / (ms_per_step * 1e-3) / 1e9
+    headline = args.config or "c2"
+    everything = args.config is None
+    head = run_configuration(headline, args, device, args.steps, args.warmup,
+                             handoff_s, args.cpu_seconds, python_loop=True)
     result = {
         "metric": METRIC,
-        "value": round(gbps, 3),
+        "value": head["value"],
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f64",
         "data": "synthetic",
-        "config": {
-            "workload": work.name, "kind": work.kind, "n": work.n,
-            "nnz": work.nnz, "levels": plan.dag.levels,
-            "dag_edges": plan.dag.edges, "seed": work.seed,
-            "execution_mode": schedule.execution_mode,
-            "threads_per_block": schedule.threads_per_block,
-            "task_lanes": solver.hip_lowering.task_lanes,
-            "thread_unroll": schedule.thread_unroll,
-            "dependence_protocol": solver.hip_lowering.dependence_protocol,
-        },
-        "solve_ms": round(ms_per_step, 5),
-        "roofline_pct": round(100.0 * gbps / HBM_PEAK_GBPS, 3),
-        "algorithmic_bytes": work.algorithmic_bytes,
-        "setup": {
-            "generate_s": round(generate_s, 3), "upload_s": round(upload_s, 3),
-            "inspect_compile_bind_s": round(inspect_s, 3),
-            "first_call_s": round(first_call_s, 4),
-        },
+        "config": head["config"],
+        "solve_ms": head["ms_per_step"],
     }
-    # the on-device inspector alone (edges, counts, level sets and, for the
-    # mailbox protocol, the incoming listing), operands resident
-    from lcd_amd.dag_codegen import build_device_dag
-    names = solver.dag_plan.arguments
-    values = dict(zip(names, list(operands) + scalars))
-    if work.kind == "ilu0_csr":
-        values["n"] = work.n
-    mailbox = solver.hip_lowering.dependence_protocol == "mailbox"
-    inspector = []
-    for _ in range(3):
-        device.synchronize()
-        t0 = time.perf_counter()
-        dag = build_device_dag(solver.dag_plan, values, device, levels=True,
-                               incoming=mailbox)
-        device.synchronize()
-        inspector.append(time.perf_counter() - t0)
-        dag.destroy()
-    result["setup"]["inspector_ms"] = round(min(inspector) * 1e3, 3)
-    if work.true_flops is not None:
-        result["gflops"] = round(work.true_flops / (ms_per_step * 1e-3) / 1e9, 3)
-    result["gflops_reference_formula"] = round(
-        work.reference_style_flops / (ms_per_step * 1e-3) / 1e9, 3)
-
-    kernel_ms = ms_per_step / launches_per_step
-    if schedule.execution_mode == "sync_free":
-        # the persistent executor is one launch per step: time that launch
-        # alone with HIP events on the library stream (eager launches, so the
-        # events sit directly around the kernel; the step above also holds
-        # the reset and operand-staging kernels)
-        device.kernel_timing = {"name": solver.hip_lowering.kernel_name}
-        try:
-            for _ in range(min(args.steps, 20)):
-                if work.kind == "ilu0_csr":
-                    device.copy(operands[0], pristine)
-                call.launch(use_graph=False)
-            call.synchronize()
-            pairs = device.kernel_timing.get("events", [])
-            if pairs:
-                kernel_ms = sum(device.elapsed_ms(a, b)
-                                for a, b in pairs) / len(pairs)
-        finally:
-            device.kernel_timing = None
-    bytes_per_launch = work.algorithmic_bytes / launches_per_step
-    achieved = bytes_per_launch / (kernel_ms * 1e-3) / 1e9
-    result["roofline"] = {
-        "bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBPS,
-        "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 6),
-        "traffic": MEASURED_TRAFFIC.get(
-            (args.config, schedule.execution_mode,
-             solver.hip_lowering.dependence_protocol,
-             solver.hip_lowering.task_lanes)),
-        "kernel": solver.hip_lowering.kernel_name,
-        "launches_per_step": launches_per_step,
-        "avg_launch_ms": round(kernel_ms, 6),
-        "dependency_levels": plan.dag.levels,
-    }
-
-    if not args.no_check:
-        from oracle import lcd_oracle
-        if work.kind == "sptrsv_csc":
-            expected = lcd_oracle.sptrsv_csc(work.indptr, work.indices,
-                                             work.data, work.rhs, work.n)
-            got = call.result()
-        elif work.kind == "sptrsv_csr":
-            expected = lcd_oracle.sptrsv_csr(work.indptr, work.indices,
-                                             work.data, work.rhs, work.n)
-            got = call.result()
-        else:
-            expected = lcd_oracle.ilu0_csr(work.data, work.indices,
-                                           work.indptr)
-            call.synchronize()
-            got = operands[0].copy_to_host()
-        error = float(np.max(np.abs(got - expected))) / float(
-            np.max(np.abs(expected)))
-        result["max_rel_error_vs_oracle"] = error
-        if error > 1e-12:
-            print(f"parity check failed: {error}", file=sys.stderr)
-            return 1
-    if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(work, args.cpu_seconds)
-        python_loop = python_loop_baseline(work, 200_000)
-        if python_loop is not None:
-            result["cpu_python_loop"] = python_loop
-    if args.arch:
-        result["arch_constants"] = device.measure_arch()
+    for key, value in head.items():
+        result.setdefault(key, value)
+    result["kernel_overrides"] = overrides or None
+    result["error_measure"] = (
+        "max_i |x_i - ref_i| / (|ref_i| + 1e-3 max|ref|) against the "
+        "sequential loop; passes at <= 1e-12")
+    failed = [] if head.get("parity_ok", True) else [headline]
+    if everything:
+        sub_args = argparse.Namespace(**vars(args))
+        for name in ("mode", "tpb", "lanes", "unroll", "protocol",
+                     "waves_per_cu", "spin_sleep", "tile_rows",
+                     "plain_first", "look_ahead"):
+            setattr(sub_args, name, None)
+        for name in ("slots", "no_queue_loads", "no_publish", "no_pipeline"):
+            setattr(sub_args, name, False)
+        records = {}
+        for config in ("c1", "c2", "c3", "c4", "c5"):
+            if config == headline and vars(sub_args) == vars(args):
+                records[config] = {k: v for k, v in head.items()
+                                   if k != "cpu_python_loop"}
+                continue
+            print(f"bench: {config}", file=sys.stderr, flush=True)
+            steps, warmup = SUB_STEPS[config]
+            records[config] = run_configuration(
+                config, sub_args, device, steps, warmup, handoff_s,
+                CPU_SECONDS_SUB)
+        # configuration 2 under the level-launched executor, the mode
+        # BASELINE.json names for it (one captured graph of `levels` launches)
+        print("bench: c2 wavefront", file=sys.stderr, flush=True)
+        sub_args.mode = "wavefront"
+        records["c2_wavefront"] = run_configuration(
+            "c2", sub_args, device, 20, 3, handoff_s, 0.0)
+        records["c2_wavefront"].pop("cpu_baseline", None)
+        result["configs"] = records
+        failed += [name for name, record in records.items()
+                   if not record.get("parity_ok", True)]
+    if args.arch or everything:
+        result["arch_constants"] = arch
     print(json.dumps(result))
+    if failed:
+        print(f"parity check failed for {failed}", file=sys.stderr)
+        return 1
     return 0
 
 

@@ -217,6 +217,8 @@ def parallel(**kwargs):
                     look_ahead=kwargs.get("look_ahead", True),
                     segment_capacity=kwargs.get("segment_capacity"),
                     pipeline_fetch=kwargs.get("pipeline_fetch", True),
+                    full_fences=kwargs.get("full_fences", False),
+                    dynamic_fetch=kwargs.get("dynamic_fetch", False),
                 )
             return lowered_variants[variant_key]
 

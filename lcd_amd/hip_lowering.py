@@ -98,7 +98,17 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                  stage_operands=True, task_records=True, single_chunk=False,
                  queue_node_loads=True, plain_first_polls=None,
                  publish_values=True, look_ahead=True, segment_capacity=None,
-                 pipeline_fetch=True):
+                 pipeline_fetch=True, full_fences=False,
+                 dynamic_fetch=False):
+        # full_fences: agent-scope release/acquire fences of the HIP memory
+        # model (L2 write-back / invalidate per hand-off) instead of the
+        # wait-for-completion scheme; dynamic_fetch: the flat queue hands out
+        # task batches from the global counter instead of round-robin, which
+        # needs no exact residency of the grid.  Both are the conservative
+        # forms to select when the machine is shared or a new part is brought
+        # up; the defaults are faster.
+        self.full_fences = bool(full_fences)
+        self.dynamic_fetch = bool(dynamic_fetch)
         self.pipeline_fetch = pipeline_fetch
         self.look_ahead = look_ahead
         self.segment_capacity = segment_capacity
@@ -750,6 +760,8 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
     def _module_text(self, array_arguments, scalar_arguments, reset_text,
                      kernel_text):
         defines = [
+            *(["#define LCD_FULL_FENCES 1"] if self.full_fences else []),
+            *(["#define LCD_DYNAMIC_FETCH 1"] if self.dynamic_fetch else []),
             "#ifndef LCD_INDEX_TYPE", "#define LCD_INDEX_TYPE int", "#endif",
             f"#define LCD_TPB {self.threads_per_block}",
             f"#define LCD_TASK_LANES {self.task_lanes}",
@@ -1086,6 +1098,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                 and not chain):
             start = self._pipelined_fetch_lines(fetch, it)
         elif (self.pipeline_fetch and not tiled and not chain
+              and not self.dynamic_fetch
               and protocol == PULL_DEPENDENCE and self._prefetch_lines
               and (self._value_pull is not None
                    or self._sequential_pull is not None)):
@@ -1364,7 +1377,7 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
                  stage_operands=True, task_records=True, single_chunk=False,
                  queue_node_loads=True, plain_first_polls=None,
                  publish_values=True, look_ahead=True, segment_capacity=None,
-                 pipeline_fetch=True):
+                 pipeline_fetch=True, full_fences=False, dynamic_fetch=False):
     """HIP counterpart of ``lower_to_numba_cuda``
     (compiler/cuda_lowering.py:2854-2884); same parameters plus
     ``task_lanes`` (lanes cooperating on one task, a power of two <= 64),
@@ -1390,5 +1403,6 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
         queue_node_loads=queue_node_loads,
         plain_first_polls=plain_first_polls, publish_values=publish_values,
         look_ahead=look_ahead, segment_capacity=segment_capacity,
-        pipeline_fetch=pipeline_fetch)
+        pipeline_fetch=pipeline_fetch, full_fences=full_fences,
+        dynamic_fetch=dynamic_fetch)
     return lowerer.lower(code)

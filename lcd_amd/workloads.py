@@ -52,8 +52,14 @@ class Workload:
 
     @property
     def true_flops(self):
+        """Floating-point operations of the sequential loop: SpTRSV one
+        division per row and a multiply-add per off-diagonal entry; ILU0
+        counted on the pattern (``ilu0_true_flops``)."""
         if self.kind == "ilu0_csr":
-            return None
+            if "true_flops" not in self.meta:
+                self.meta["true_flops"] = ilu0_true_flops(
+                    self.indptr, self.indices, self.n)
+            return self.meta["true_flops"]
         return 2 * (self.nnz - self.n) + self.n
 
     @property
@@ -64,6 +70,22 @@ class Workload:
         if self.kind == "ilu0_csr":
             return 2 * self.nnz
         return self.n + 2 * self.nnz
+
+
+def ilu0_true_flops(indptr, indices, n):
+    """Operation count of in-place ILU0 on a CSR pattern with sorted rows
+    (compiler/demo/spilu0.py:21-47): for every entry (i, k) below the
+    diagonal one division, and one multiply-subtract (2 flops) for every
+    j > k that rows i and k both hold.  Counted with sparse pattern algebra:
+    (L U)[i, j] = number of pivots k < i with (i, k) and (k, j > k) present,
+    summed over the positions of the pattern itself."""
+    from scipy import sparse
+    ones = np.ones(len(indices), dtype=np.int64)
+    pattern = sparse.csr_matrix((ones, indices, indptr), shape=(n, n))
+    lower = sparse.tril(pattern, k=-1, format="csr")
+    upper = sparse.triu(pattern, k=1, format="csr")
+    updates = (lower @ upper).multiply(pattern).sum()
+    return int(lower.nnz) + 2 * int(updates)
 
 
 def _grid_coordinates(shape):

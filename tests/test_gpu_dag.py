@@ -64,6 +64,32 @@ def test_dag_matches_oracle(device, oracle, name, overrides, force_kahn):
             assert dag.levels == sum(grid) - len(grid) + 1
 
 
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4", "c5"])
+def test_dag_matches_oracle_at_full_size(device, oracle, name):
+    """BASELINE.json's sizes: edges, unique in-degrees, multiplicities, CSR
+    successors, levels and level sets bit-exact against the oracle, plus the
+    closed forms the stencils and the band have."""
+    work = workloads.configuration(name)
+    print("dag full size", name, work.n, work.nnz, flush=True)
+    dag, expected = _check_dag(device, oracle, _rule_for(oracle, work), work.n)
+    grid = work.meta.get("grid")
+    if name in ("c1", "c2"):
+        assert dag.levels == sum(grid) - len(grid) + 1
+        coordinates = np.unravel_index(np.arange(work.n), grid[::-1])
+        np.testing.assert_array_equal(dag.host("level_of"),
+                                      sum(coordinates).astype(np.int32))
+    elif name == "c4":
+        nx, ny = grid
+        assert dag.levels == nx + 2 * ny - 2
+    elif name == "c5":
+        assert dag.levels == work.n
+        np.testing.assert_array_equal(
+            dag.host("dep_count"),
+            np.minimum(np.arange(work.n), work.meta["bandwidth"]))
+    assert dag.edges == expected.edges == int(dag.host("dep_count").sum())
+    dag.destroy()
+
+
 @pytest.mark.parametrize("name,overrides", SMALL)
 def test_band_chains_match_oracle(device, oracle, name, overrides):
     """Chain tasks (band_width > 1): connected components inside bands of

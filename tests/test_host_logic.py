@@ -56,6 +56,30 @@ def test_library_exports_every_declared_symbol():
     assert b"gfx950" in library.lcdhip_version()
 
 
+def test_struct_layouts_follow_the_header():
+    """The ctypes mirrors of the C structs (the package's and the stub shown
+    in INTEGRATION.md) list the header's fields in the header's order."""
+    header = open(os.path.join(ROOT, "include", "lcdhip.h")).read()
+
+    def fields_of(struct_name):
+        body = re.search(r"typedef struct \{([^}]*)\} " + struct_name + ";",
+                         header).group(1)
+        body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+        return [re.search(r"(\w+)(\[\d+\])?\s*$", line.strip()).group(1)
+                for line in body.split(";") if line.strip()]
+
+    for mirror, struct_name in ((hip_runtime._DagRule, "lcdhip_dag_rule"),
+                                (hip_runtime._DagInfo, "lcdhip_dag_info"),
+                                (hip_runtime._Props, "lcdhip_props"),
+                                (hip_runtime._Arch, "lcdhip_arch")):
+        assert [name for name, _ in mirror._fields_] == fields_of(struct_name)
+    guide = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    stub = guide[guide.index("class Rule(ctypes.Structure)"):]
+    stub = stub[:stub.index("def upload")]
+    assert re.findall(r'\("(\w+)", ctypes', stub) == fields_of(
+        "lcdhip_dag_rule")
+
+
 def test_compute_entry_points_fail_loudly_without_init():
     library = hip_runtime.load_library()
     if hip_runtime.device_available():

@@ -306,6 +306,94 @@ def test_band_chains_against_literal():
     del rng
 
 
+def _components_per_band(dag, band_width):
+    """Chain tasks from first principles: cut the level sets into bands of
+    ``band_width`` levels, take the subgraph the band's nodes induce, and let
+    SciPy label its connected components (undirected).  A chain is one
+    component, members in band order (level, then id); chains are listed by
+    their first member."""
+    from scipy.sparse import coo_matrix
+    from scipy.sparse.csgraph import connected_components
+    sources = np.repeat(np.arange(dag.n), np.diff(dag.dag_ptr))
+    targets = dag.dag_index
+    nodes, ptr, bands = [], [0], [0]
+    for first in range(0, dag.levels, band_width):
+        last = min(first + band_width, dag.levels)
+        band = dag.wavefronts[dag.wavefront_ptr[first]:dag.wavefront_ptr[last]]
+        position = np.full(dag.n, -1)
+        position[band] = np.arange(len(band))
+        inside = (position[sources] >= 0) & (position[targets] >= 0)
+        graph = coo_matrix(
+            (np.ones(int(inside.sum())),
+             (position[sources[inside]], position[targets[inside]])),
+            shape=(len(band), len(band)))
+        count, label = connected_components(graph, directed=False)
+        first_member = np.full(count, len(band))
+        np.minimum.at(first_member, label, np.arange(len(band)))
+        for component in np.argsort(first_member):
+            members = band[label == component]
+            nodes.extend(members.tolist())
+            ptr.append(len(nodes))
+        bands.append(len(ptr) - 1)
+    return nodes, ptr, bands
+
+
+@pytest.mark.parametrize("case", ["stencil", "ilu", "random", "banded"])
+def test_band_chains_are_connected_components(case):
+    rng = np.random.default_rng(21)
+    if case == "stencil":
+        work = workloads.configuration("c2", nx=6, ny=5, nz=4)
+        rule = O.rule_sptrsv_csc(work.indptr, work.indices)
+        n = work.n
+    elif case == "ilu":
+        work = workloads.configuration("c4", nx=9, ny=7)
+        rule = O.rule_ilu0_csr(work.indptr, work.indices)
+        n = work.n
+    elif case == "banded":
+        work = workloads.configuration("c5", n=300)
+        rule = O.rule_sptrsv_csc(work.indptr, work.indices)
+        n = work.n
+    else:
+        n = 400
+        counts = rng.integers(0, 3, n)
+        ptr = np.zeros(n + 1, dtype=np.int32)
+        np.cumsum(counts, out=ptr[1:])
+        idx = np.minimum(np.repeat(np.arange(n), counts)
+                         + rng.integers(1, 60, int(ptr[-1])),
+                         n - 1).astype(np.int32)
+        rule = O.make_rule(ptr, idx, True, guard=O.GUARD_GREATER)
+    dag = O.dag_build([rule], n)
+    for band_width in (1, 2, 3, 7, 10 ** 6):
+        nodes, ptr, bands = dag.band_chains(band_width)
+        expected = _components_per_band(dag, band_width)
+        assert nodes.tolist() == expected[0], (case, band_width)
+        assert ptr.tolist() == expected[1], (case, band_width)
+        assert bands.tolist() == expected[2], (case, band_width)
+
+
+def test_ilu0_flop_count():
+    """The oracle's operation count of ILU0 against the dense closed form
+    (every k < i: one division and n - 1 - k multiply-subtracts) and against
+    the sparse pattern algebra of the workload generator."""
+    n = 9
+    indptr = np.arange(0, n * n + 1, n, dtype=np.int32)
+    indices = np.tile(np.arange(n, dtype=np.int32), n)
+    closed = sum(1 + 2 * (n - 1 - k) for i in range(n) for k in range(i))
+    assert O.ilu0_csr_flops(indices, indptr) == closed
+    assert workloads.ilu0_true_flops(indptr, indices, n) == closed
+    # tridiagonal: one division and one update per row after the first
+    rows = 50
+    work_ptr = np.concatenate([[0], np.cumsum(
+        [2] + [3] * (rows - 2) + [2])]).astype(np.int32)
+    work_idx = np.concatenate(
+        [[0, 1]] + [[i - 1, i, i + 1] for i in range(1, rows - 1)]
+        + [[rows - 2, rows - 1]]).astype(np.int32)
+    assert O.ilu0_csr_flops(work_idx, work_ptr) == 3 * (rows - 1)
+    for nx, ny in ((7, 5), (16, 11)):
+        work = workloads.configuration("c4", nx=nx, ny=ny)
+        assert O.ilu0_csr_flops(work.indices, work.indptr) == work.true_flops
+
+
 def test_gauss_seidel_is_repeated_forward_substitution():
     work = workloads.configuration("c4", nx=6, ny=5)
     from scipy.sparse import csr_matrix, tril
