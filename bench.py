@@ -241,7 +241,7 @@ def run_configuration(config, args, device, steps, warmup, handoff_s,
     def step():
         if work.kind == "ilu0_csr":
             device.copy(operands[0], pristine)   # factorisation is in place
-        call.launch()
+        call.launch(use_graph=not args.no_graph)
 
     t0 = time.perf_counter()
     step()
@@ -293,6 +293,7 @@ def run_configuration(config, args, device, steps, warmup, handoff_s,
             "thread_unroll": schedule.thread_unroll,
             "dependence_protocol": lowering.dependence_protocol,
             "tile_rows": tile_rows,
+            "replayed_from_graph": not args.no_graph,
         },
         "roofline_pct": round(100.0 * gbps / HBM_PEAK_GBPS, 3),
         "algorithmic_bytes": work.algorithmic_bytes,
@@ -433,6 +434,9 @@ def main():
     parser.add_argument("--no-pipeline", action="store_true",
                         help="tiled mailbox: load a round's records and "
                              "operands when the round starts")
+    parser.add_argument("--no-graph", action="store_true",
+                        help="issue every launch of a step eagerly instead "
+                             "of replaying the captured graph")
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-check", action="store_true")
     parser.add_argument("--arch", action="store_true",
@@ -487,7 +491,8 @@ def main():
                      "waves_per_cu", "spin_sleep", "tile_rows",
                      "plain_first", "look_ahead"):
             setattr(sub_args, name, None)
-        for name in ("slots", "no_queue_loads", "no_publish", "no_pipeline"):
+        for name in ("slots", "no_queue_loads", "no_publish", "no_pipeline",
+                     "no_graph"):
             setattr(sub_args, name, False)
         records = {}
         for config in ("c1", "c2", "c3", "c4", "c5"):
