@@ -15,6 +15,7 @@ import ast
 import ctypes
 import hashlib
 import os
+import sys
 from copy import deepcopy
 from dataclasses import dataclass, field
 
@@ -1207,6 +1208,36 @@ def _load_for_values(compiled, lowering, prepared, device):
     return compiled.loaded[cache_key]
 
 
+# A captured level loop is one graph with a kernel node per level.  Replaying
+# such a graph of about three thousand nodes under rocprofv3's kernel trace
+# ended in a segmentation fault inside hipGraphLaunch once (the same graph
+# replays correctly without the tracer, graphs of a few hundred nodes replay
+# correctly with it, and nothing of this library is dereferenced during the
+# launch), and no cause could be shown.  With a rocprofiler tool library
+# loaded, level loops beyond this many launches are therefore issued eagerly.
+TRACED_GRAPH_NODE_LIMIT = 1024
+_traced_graph_notice = []
+
+
+def profiler_attached():
+    """True when the process was started under rocprofv3 (its tool library
+    is named in the environment it sets up)."""
+    return bool(os.environ.get("ROCP_TOOL_LIBRARIES")) or (
+        "rocprofiler" in os.environ.get("LD_PRELOAD", ""))
+
+
+def _level_launches(lowering, prepared):
+    if getattr(lowering, "execution_mode", None) != "wavefront":
+        return 0
+    for name in ("band_ptr", "wavefront_ptr"):
+        pointers = prepared.values.get(name)
+        if pointers is None:
+            pointers = prepared.host_values.get(name)
+        if pointers is not None and hasattr(pointers, "__len__"):
+            return max(len(pointers) - 1, 0)
+    return 0
+
+
 def launch_hip_call(compiled_module, lowering, prepared_arguments,
                     use_graph=True):
     """Enqueue one execution of the prepared call (no host synchronisation).
@@ -1223,6 +1254,17 @@ def launch_hip_call(compiled_module, lowering, prepared_arguments,
                                   device)
         prepared.module = module
     real_device = isinstance(device, HIPDevice)
+    if (use_graph and real_device and profiler_attached()
+            and _level_launches(lowering, prepared)
+            > TRACED_GRAPH_NODE_LIMIT):
+        if not _traced_graph_notice:
+            _traced_graph_notice.append(True)
+            print(f"lcd_amd: a profiler is attached; the level loop of "
+                  f"{lowering.function_name} "
+                  f"({_level_launches(lowering, prepared)} launches) is "
+                  "issued eagerly instead of replayed from a graph",
+                  file=sys.stderr, flush=True)
+        use_graph = False
     if use_graph and real_device and prepared.graph is not None:
         prepared.graph.launch(device.stream)
         return

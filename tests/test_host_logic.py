@@ -1077,3 +1077,27 @@ def test_runtime_layer_accepts_an_injected_device():
             {"Ap": None, "Ai": None, "Ax": None, "b": None, "n": 2},
             P.preprocess_sync_free([[1], []], [0, 1]), {"np": np},
             hip_module=FakeDevice())
+
+
+def test_large_level_graphs_are_not_replayed_under_a_profiler(monkeypatch):
+    """With rocprofv3's tool library in the environment a level loop of more
+    than TRACED_GRAPH_NODE_LIMIT launches is issued eagerly; shorter loops and
+    untraced processes keep the graph."""
+    from types import SimpleNamespace
+    lowering = SimpleNamespace(execution_mode="wavefront",
+                               function_name="loop")
+    long_loop = SimpleNamespace(values={"band_ptr": np.arange(3071)},
+                                host_values={})
+    short_loop = SimpleNamespace(values={}, host_values={
+        "wavefront_ptr": np.arange(383)})
+    assert hip_runtime._level_launches(lowering, long_loop) == 3070
+    assert hip_runtime._level_launches(lowering, short_loop) == 382
+    persistent = SimpleNamespace(execution_mode="sync_free")
+    assert hip_runtime._level_launches(persistent, long_loop) == 0
+    monkeypatch.delenv("ROCP_TOOL_LIBRARIES", raising=False)
+    monkeypatch.setenv("LD_PRELOAD", "")
+    assert not hip_runtime.profiler_attached()
+    monkeypatch.setenv("ROCP_TOOL_LIBRARIES",
+                       "/opt/rocm/lib/rocprofiler-sdk/librocprofiler-sdk-tool.so")
+    assert hip_runtime.profiler_attached()
+    assert 382 <= hip_runtime.TRACED_GRAPH_NODE_LIMIT < 3070
