@@ -178,9 +178,18 @@ int lcdhip_graph_destroy(lcdhip_graph *graph);
  * compiler/transform_tests/test_spilu0_codegen.py:146-150).  It yields
  * (n - lower_offset)(n - lower_offset + 1) / 2 edges, so it is meant for
  * small n; LCDHIP_DAG_INCOMING cannot be combined with it.
+ *
+ * A rule with relation LCDHIP_RULE_NEXT (no structure arrays either) yields
+ * the single edge seg -> seg + lower_offset (lower_offset >= 1).  With
+ * lower_offset == 1 it is the transitive reduction of the complete order:
+ * what the inspector is given when a dependence could not be refuted and
+ * cannot be enumerated either, the counterpart of the reference keeping every
+ * dependence its solver does not refute in time
+ * (compiler/legality_check.py:431-443).  Any n; no LCDHIP_DAG_INCOMING.
  */
 #define LCDHIP_RULE_SEGMENT 0
 #define LCDHIP_RULE_LATER 1
+#define LCDHIP_RULE_NEXT 2
 #define LCDHIP_GUARD_NONE 0
 #define LCDHIP_GUARD_GREATER 1
 #define LCDHIP_GUARD_NOT_EQUAL 2
@@ -194,7 +203,7 @@ typedef struct {
     int32_t upper_offset;
     int32_t guard;
     int32_t break_at_owner;
-    int32_t relation;        /* LCDHIP_RULE_SEGMENT or LCDHIP_RULE_LATER */
+    int32_t relation;        /* LCDHIP_RULE_SEGMENT, _LATER or _NEXT */
 } lcdhip_dag_rule;
 
 #define LCDHIP_DAG_LEVELS 1u        /* also build level sets / wavefronts */

@@ -113,6 +113,23 @@ __global__ void emit_later_keys_kernel(int64_t n, int32_t first,
         atomicAdd(candidates, static_cast<unsigned long long>(n - j));
 }
 
+// Chain rule: task seg releases task seg + step only (the transitive
+// reduction of the complete order when step == 1).
+__global__ void emit_next_keys_kernel(int64_t n, int32_t step,
+                                      unsigned long long *__restrict__ keys,
+                                      int32_t *__restrict__ edge_count,
+                                      unsigned long long *__restrict__ candidates)
+{
+    int64_t seg = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (seg + step >= n)
+        return;
+    keys[seg] = (static_cast<unsigned long long>(seg) << 32) |
+                static_cast<unsigned long long>(seg + step);
+    atomicAdd(&edge_count[seg + step], 1);
+    if (seg == 0)
+        atomicAdd(candidates, static_cast<unsigned long long>(n - step));
+}
+
 // From the sorted unique keys: successor array, unique in-degree and the
 // out-degree histogram (scanned into dag_ptr afterwards).
 __global__ void split_edges_kernel(const unsigned long long *__restrict__ keys,
@@ -509,6 +526,13 @@ extern "C" int lcdhip_dag_build(const lcdhip_dag_rule *rules, int rule_count,
             }
             int64_t span = std::max<int64_t>(n - rules[r].lower_offset, 0);
             rule_keys[r] = span * (span + 1) / 2;
+        } else if (rules[r].relation == LCDHIP_RULE_NEXT) {
+            if (rules[r].lower_offset < 1 || (flags & LCDHIP_DAG_INCOMING)) {
+                set_error("rule %d: a chain rule needs lower_offset >= 1 and "
+                          "no incoming listing", r);
+                return LCDHIP_ERR_ARGUMENT;
+            }
+            rule_keys[r] = std::max<int64_t>(n - rules[r].lower_offset, 0);
         } else if (rules[r].relation != LCDHIP_RULE_SEGMENT) {
             set_error("rule %d has an unknown relation %d", r,
                       rules[r].relation);
@@ -566,6 +590,15 @@ extern "C" int lcdhip_dag_build(const lcdhip_dag_rule *rules, int rule_count,
                          static_cast<unsigned>(n - rules[r].lower_offset)),
                     dim3(kBlock), 0, stream, n, rules[r].lower_offset,
                     keys + offset, edge_count, d_candidates);
+            offset += rule_keys[r];
+            continue;
+        }
+        if (rules[r].relation == LCDHIP_RULE_NEXT) {
+            if (rule_keys[r] > 0)
+                hipLaunchKernelGGL(emit_next_keys_kernel,
+                                   dim3(blocks_for(rule_keys[r])), dim3(kBlock),
+                                   0, stream, n, rules[r].lower_offset,
+                                   keys + offset, edge_count, d_candidates);
             offset += rule_keys[r];
             continue;
         }

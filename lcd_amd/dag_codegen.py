@@ -20,6 +20,7 @@ from lcd_amd.dependence import (
     GUARD_NONE,
     GUARD_NOT_EQUAL,
     LaterRule,
+    NextRule,
     SegmentRule,
 )
 
@@ -86,9 +87,10 @@ def create_dag_plan(ordering_dependences, node_data=None,
         if getattr(dependence, "kind", None) == "reduction":
             raise DAGCodegenError(
                 "Reduction dependences cannot be lowered to DAG edges.")
-        if not isinstance(dependence, (SegmentRule, LaterRule)):
+        if not isinstance(dependence, (SegmentRule, LaterRule, NextRule)):
             raise DAGCodegenError(
-                "Edge rules must be SegmentRule or LaterRule objects; got "
+                "Edge rules must be SegmentRule, LaterRule or NextRule "
+                "objects; got "
                 f"{type(dependence).__name__}.")
         if dependence not in rules:
             rules.append(dependence)
@@ -134,9 +136,11 @@ def generate_dag_source(plan, function_name="extract_dag",
         it, inner = rule.block_iterator, rule.inner_iterator
         source, destination = f"_dag_source_{index}", f"_dag_destination_{index}"
         lines.append(f"    for {it} in range({plan.node_lower}, {n}):")
-        if isinstance(rule, LaterRule):
+        if isinstance(rule, (LaterRule, NextRule)):
+            upper = n if isinstance(rule, LaterRule) else (
+                f"min({it} + {rule.lower_offset + 1}, {n})")
             lines.append(f"        for {inner} in range({it} + "
-                         f"{rule.lower_offset}, {n}):")
+                         f"{rule.lower_offset}, {upper}):")
             lines.append(f"            {source} = {it}")
             lines.append(f"            {destination} = {inner}")
             lines.append(f"            _dag_successors[{source}]"
@@ -202,7 +206,7 @@ def device_rules(plan, argument_values):
     """Bind the plan's rules to concrete structure arrays."""
     bound = []
     for rule in plan.edge_rules:
-        if isinstance(rule, LaterRule):
+        if isinstance(rule, (LaterRule, NextRule)):
             bound.append(dict(relation=rule.relation,
                               lower_offset=rule.lower_offset))
             continue
@@ -327,6 +331,7 @@ __all__ = [
     "MAILBOX_DEPENDENCE",
     "DEPENDENCE_PROTOCOLS", "DAGCodegenError", "DAGPlan", "DirectDependence",
     "EdgeRule", "GUARD_GREATER", "GUARD_NONE", "GUARD_NOT_EQUAL", "LaterRule",
+    "NextRule",
     "build_device_dag", "compile_dag_builder", "create_dag_plan",
     "direct_dependence", "generate_dag_source",
 ]

@@ -137,8 +137,22 @@ def parallel(**kwargs):
                 ordering_dependences=list(kwargs["edge_rules"]))
         else:
             dependence_analysis = analyze_dependences(
-                function_ast, loop, function_props)
+                function_ast, loop, function_props,
+                strict=kwargs.get("strict_dependences", False))
+            if dependence_analysis.conservative:
+                import warnings
+                kept = [str(d) for d in dependence_analysis.kept_dependences
+                        if getattr(d.rule, "relation", 0) == 2]
+                warnings.warn(
+                    f"@parallel({function.__name__}): a dependence could be "
+                    "neither refuted nor enumerated and is kept as the "
+                    "complete order (the iterations run one after the "
+                    "other): " + "; ".join(kept) + ".  Pass edge_rules= to "
+                    "state the dependences, or strict_dependences=True to "
+                    "get an error instead.", stacklevel=2)
         if verbose:
+            for dependence in dependence_analysis.raw_dependences:
+                print(dependence)
             for rule in dependence_analysis.ordering_dependences:
                 print(rule.describe())
             print("Reduction dependences:")

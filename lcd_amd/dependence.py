@@ -24,8 +24,31 @@ supported solver loops to, and produces the same edge rules:
   whose entries name the rows it updates there (ILU0-CSC;
   test_spilu0_codegen.py:146-150)
 
-Anything else raises :class:`DependenceAnalysisError` rather than guessing;
-callers can pass ``edge_rules=`` to the decorator explicitly in that case.
+The analysis runs in the reference's three stages
+(compiler/legality_check.py:172-383):
+
+1. *candidates*: per array, the last write of every distinct access
+   expression against the first read of every distinct access expression
+   (plus the target of every associative augmented update, whose
+   self-dependence must not be hidden by first-read filtering); a pair is a
+   candidate when its index expressions differ or go through an index array.
+   Statements are numbered S0, S1, ... over the function's assignments in
+   source order, as the reference's frontend does (compiler/spf_raising.py:
+   266-277).
+2. *refutation*: the reference hands every candidate to Z3 with the
+   ``function_props`` as axioms.  Here the structural facts are applied
+   directly: different tasks own disjoint segments (monotone pointers); a
+   task's own segment lies before every segment it visits through
+   ``range(i + c, n)``; inside one sorted segment the entries below, at and
+   above the owner's index are disjoint.  A self-dependence of an
+   associative update becomes a reduction.
+3. *projection*: every surviving dependence is mapped to an edge rule the
+   inspector can enumerate.  A survivor that has no such rule is kept, as
+   the reference keeps what its solver does not refute in time
+   (compiler/legality_check.py:431-443): it is over-approximated by the
+   chain ``i -> i + 1`` (:class:`NextRule`), whose closure is the complete
+   order, unless ``strict=True`` asks for :class:`DependenceAnalysisError`
+   instead.  Callers can also pass ``edge_rules=`` to the decorator.
 """
 
 import ast
@@ -104,6 +127,50 @@ class LaterRule:
 
 
 @dataclass(frozen=True)
+class NextRule:
+    """``seg -> seg + lower_offset``: with offset 1 the chain whose closure is
+    the complete order, the safe over-approximation of a dependence that
+    could be neither refuted nor enumerated."""
+
+    lower_offset: int = 1
+    block_iterator: str = "i"
+    inner_iterator: str = "_lcd_next"
+    carried_by: str = ""
+    relation = 2
+
+    @property
+    def iterators(self):
+        return [self.block_iterator, self.inner_iterator]
+
+    def describe(self):
+        return (f"RAW on {self.carried_by}: kept without an enumerable rule; "
+                f"{self.block_iterator} -> {self.block_iterator} + "
+                f"{self.lower_offset} (complete order)")
+
+
+@dataclass(frozen=True)
+class RawDependence:
+    """One read-after-write candidate between two statements of the block
+    loop and what became of it."""
+
+    array: str
+    from_statement_id: str        # the writer
+    to_statement_id: str          # the reader
+    write_index: str
+    read_index: str
+    kind: str = "RAW"             # "RAW" | "reduction"
+    verdict: str = "kept"         # "kept" | "refuted"
+    reason: str = ""
+    rule: object = None           # SegmentRule | LaterRule | NextRule | None
+
+    def __str__(self):
+        return (f"{self.kind} on {self.array}: {self.from_statement_id}"
+                f"[{self.write_index}] -> {self.to_statement_id}"
+                f"[{self.read_index}] ({self.verdict}"
+                f"{': ' + self.reason if self.reason else ''})")
+
+
+@dataclass(frozen=True)
 class ReductionSite:
     statement_id: str
     operator: str
@@ -113,9 +180,28 @@ class ReductionSite:
 
 @dataclass
 class DependenceAnalysis:
+    """``ordering_dependences`` holds the distinct edge rules (what the DAG
+    planner consumes); ``raw_dependences`` every candidate with its verdict.
+    The reference's ``analysis.ordering_dependences`` (one entry per
+    dependence that survived its solver) corresponds to
+    ``kept_dependences``, its ``reduction_dependences`` to
+    ``reduction_candidates``."""
+
     ordering_dependences: list = field(default_factory=list)
     reduction_dependences: list = field(default_factory=list)
     reductions: dict = field(default_factory=dict)
+    raw_dependences: list = field(default_factory=list)
+    statement_ids: dict = field(default_factory=dict)   # (line, col) -> "Sk"
+    conservative: bool = False    # a NextRule stands in for a kept candidate
+
+    @property
+    def kept_dependences(self):
+        return [d for d in self.raw_dependences
+                if d.verdict == "kept" and d.kind == "RAW"]
+
+    @property
+    def reduction_candidates(self):
+        return [d for d in self.raw_dependences if d.kind == "reduction"]
 
     @property
     def atomic_statements(self):
@@ -131,6 +217,8 @@ class _Segment:
     lower_offset: int
     upper_offset: int
     lower_is_position: bool = False
+    position_base: str = ""       # range(<position_base> + c, end)
+    position_offset: int = 0
 
 
 def _const_int(node):
@@ -227,10 +315,49 @@ def find_block_loop(function, block_iterator):
     return matches[0]
 
 
+def sorted_segment_pairs(function_props):
+    """(pointer array, index array) pairs whose segments are sorted
+    (``segmented_monotonically_increasing``)."""
+    pairs = set()
+    for key, properties in (function_props or {}).items():
+        if not (isinstance(key, tuple) and len(key) == 2):
+            continue
+        for entry in properties:
+            name = entry[0] if isinstance(entry, (tuple, list)) else entry
+            if name == "segmented_monotonically_increasing":
+                pairs.add(tuple(key))
+    return pairs
+
+
+def triangular_pairs(function_props):
+    """(pointer array, index array) pairs with the ``triangularity``
+    property: every position behind a segment's first holds an index above
+    the segment's owner (compiler/SMT_Generator.py:309-310)."""
+    return {tuple(key) for key, properties in (function_props or {}).items()
+            if isinstance(key, tuple) and len(key) == 2
+            and "triangularity" in [entry[0] if isinstance(entry, (tuple, list))
+                                    else entry for entry in properties]}
+
+
+def number_statements(function):
+    """S0, S1, ... for the assignments of ``function`` in source order
+    (compiler/spf_raising.py:266-277): (line, column) -> id."""
+    found = sorted(
+        (node.lineno, node.col_offset) for node in ast.walk(function)
+        if isinstance(node, (ast.Assign, ast.AugAssign, ast.AnnAssign)))
+    return {location: f"S{k}" for k, location in enumerate(found)}
+
+
 class _Analyzer:
-    def __init__(self, function, block_iterator, function_props):
+    def __init__(self, function, block_iterator, function_props,
+                 strict=False):
         self.function = function
         self.block = block_iterator
+        self.strict = strict
+        self.sorted_pairs = sorted_segment_pairs(function_props)
+        self.triangular = triangular_pairs(function_props)
+        self.statement_ids = number_statements(function)
+        self.current_statement = None
         self.aliases = _AliasTable(function)
         self.pointers = set(pointer_arrays(function_props))
         self.segments = {}     # iterator -> _Segment
@@ -272,7 +399,9 @@ class _Analyzer:
             if (outer.pointer_array == pointer
                     and _same(outer.owner, owner_plus) and lower_offset >= 0):
                 return _Segment(pointer, owner_plus, outer.lower_offset,
-                                upper_offset, lower_is_position=True)
+                                upper_offset, lower_is_position=True,
+                                position_base=lower_base.id,
+                                position_offset=lower_offset)
         return None
 
     # ---- access classification -------------------------------------------
@@ -350,10 +479,13 @@ class _Analyzer:
             if (isinstance(sub, ast.Subscript) and isinstance(sub.ctx, ast.Load)
                     and isinstance(sub.value, ast.Name)
                     and sub.value.id in written_arrays):
-                self.reads.append((sub.value.id, self._classify(sub.slice)))
+                self.reads.append((sub.value.id, self._classify(sub.slice),
+                                   sub, self.current_statement))
 
     def _visit(self, statements, written_arrays, loop_stack):
         for statement in statements:
+            if not isinstance(statement, (ast.Assign, ast.AugAssign)):
+                self.current_statement = None
             if isinstance(statement, ast.For):
                 segment = None
                 if isinstance(statement.target, ast.Name):
@@ -385,6 +517,7 @@ class _Analyzer:
                 self._record_reads(statement.test, written_arrays)
                 self._visit(statement.body, written_arrays, loop_stack)
             elif isinstance(statement, ast.Assign):
+                self.current_statement = statement
                 self._record_reads(statement.value, written_arrays)
                 for target in statement.targets:
                     if isinstance(target, ast.Subscript) and isinstance(
@@ -394,11 +527,17 @@ class _Analyzer:
                             target.value.id, self._classify(target.slice),
                             statement, False))
             elif isinstance(statement, ast.AugAssign):
+                self.current_statement = statement
                 self._record_reads(statement.value, written_arrays)
                 target = statement.target
                 if isinstance(target, ast.Subscript) and isinstance(
                         target.value, ast.Name):
                     self._record_reads(target.slice, written_arrays)
+                    if target.value.id in written_arrays:
+                        # an update reads its own target
+                        self.reads.append((
+                            target.value.id, self._classify(target.slice),
+                            target, statement))
                     self.writes.append((
                         target.value.id, self._classify(target.slice),
                         statement, True))
@@ -469,15 +608,117 @@ class _Analyzer:
             return None
         return self._rule(True, kind[1], kind[2], array)
 
+    # ---- column classes inside one sorted segment -----------------------
+    def _index_array_of(self, iterator):
+        """The index array whose entries the loop over ``iterator`` tests
+        (break test or search needle), if any."""
+        for test in self.breaks.get(iterator, []):
+            if (isinstance(test, ast.Compare)
+                    and isinstance(test.left, ast.Subscript)
+                    and isinstance(test.left.value, ast.Name)):
+                return test.left.value.id
+        return None
+
+    def _own_class(self, iterator):
+        """Where the entry at an own-segment position lies relative to the
+        task's index: "below" when the loop leaves at the first entry that
+        is not below it (``if I[p] >= i: break`` on a sorted segment)."""
+        segment = self.segments.get(iterator)
+        if segment is None or segment.lower_is_position:
+            return "any"
+        index_array = self._index_array_of(iterator)
+        if index_array is None or (segment.pointer_array,
+                                   index_array) not in self.sorted_pairs:
+            return "any"
+        try:
+            return "below" if self._break_at_owner(iterator, index_array) \
+                else "any"
+        except DependenceAnalysisError:
+            return "any"
+
+    def _other_class(self, index_array, outer, iterator):
+        """Where the entry found by the search loop over ``iterator`` (in the
+        segment of ``index_array[outer]``) lies relative to that segment's
+        owner: "diag" when the search matches the owner itself, "above" when
+        it matches a later entry of the sorted own segment than the owner's
+        (``range(outer + c, end)`` with ``c >= 1``)."""
+        needle = self.needles.get(iterator)
+        if needle is None:
+            return "any"
+        owner = self.aliases.resolve(self.segments[iterator].owner)
+        if _same(needle, owner):
+            return "diag"
+        if (isinstance(needle, ast.Subscript)
+                and isinstance(needle.value, ast.Name)
+                and needle.value.id == index_array
+                and isinstance(needle.slice, ast.Name)):
+            later = self.segments.get(needle.slice.id)
+            if (later is not None and later.lower_is_position
+                    and later.position_base == outer
+                    and later.position_offset >= 1
+                    and (later.pointer_array, index_array) in self.sorted_pairs):
+                return "above"
+        return "any"
+
+    # ---- stage 2 and 3 for one candidate --------------------------------
+    def _decide(self, array, write_kind, read_kind, statement, is_update,
+                same_statement):
+        """(verdict, reason, rule, kind) of one write/read pair."""
+        own = ("self", "own_position")
+        if write_kind[0] == "unknown" or read_kind[0] == "unknown":
+            which = write_kind if write_kind[0] == "unknown" else read_kind
+            return ("kept", f"index {which[1]} is not a recognised shape",
+                    None, "RAW")
+        if write_kind[0] == "indirect" and read_kind[0] == "indirect":
+            if same_statement and is_update and type(
+                    statement.op) in ASSOCIATIVE_UPDATE_OPERATIONS:
+                return ("kept", "associative update of a shared element",
+                        None, "reduction")
+            return ("refuted", "read-modify-write of the update itself", None,
+                    "RAW")
+        if write_kind[0] in own and read_kind[0] in own:
+            return ("refuted", "different tasks own disjoint segments", None,
+                    "RAW")
+        if write_kind[0] in own and read_kind[0] == "later_position":
+            return ("refuted", "the segments a task visits through "
+                    "range(i + c, n) lie behind the reader, the writer's own "
+                    "segment before it", None, "RAW")
+        if write_kind == ("self",) and read_kind[0] == "indirect":
+            segment = self.segments[read_kind[2]]
+            if ((segment.pointer_array, read_kind[1]) in self.triangular
+                    and segment.lower_offset >= 1):
+                return ("refuted", "the entries behind a segment's first lie "
+                        "above the reader's index (triangularity), the "
+                        "writer's below it", None, "RAW")
+            return ("kept", "", self._rule(False, read_kind[1], read_kind[2],
+                                           array), "RAW")
+        if write_kind[0] == "indirect" and read_kind == ("self",):
+            return ("kept", "", self._rule(True, write_kind[1], write_kind[2],
+                                           array), "RAW")
+        if write_kind[0] == "own_position" and read_kind[0] == "other_position":
+            written = self._own_class(write_kind[1])
+            read = self._other_class(read_kind[1], read_kind[2], read_kind[3])
+            if "any" not in (written, read) and written != read:
+                return ("refuted", f"entries {written} the owner's index are "
+                        f"written, the entry {read} it is read", None, "RAW")
+            return ("kept", "", self._rule(False, read_kind[1], read_kind[2],
+                                           array), "RAW")
+        if write_kind[0] == "later_position" and read_kind[0] == "later_position":
+            rule = self._row_rule(write_kind, read_kind, array)
+            if rule is None:
+                return ("kept", "two later segments meet at entries that "
+                        "cannot be enumerated", None, "RAW")
+            return ("kept", "", rule, "RAW")
+        if write_kind[0] == "later_position" and read_kind[0] in own:
+            return ("kept", "", self._later_rule(write_kind[1], array), "RAW")
+        return ("kept", f"write {write_kind[0]} / read {read_kind[0]} has no "
+                "enumerable rule", None, "RAW")
+
     def run(self):
         loop = find_block_loop(self.function, self.block)
         if (isinstance(loop.iter, ast.Call) and loop.iter.args
                 and not loop.iter.keywords):
             self.node_count = self.aliases.resolve(loop.iter.args[-1])
-        local_names = set()
-        for node in ast.walk(loop):
-            if isinstance(node, ast.Name) and isinstance(node.ctx, ast.Store):
-                local_names.add(node.id)
         written_arrays = set()
         for node in ast.walk(loop):
             target = None
@@ -492,17 +733,56 @@ class _Analyzer:
                 written_arrays.add(target.value.id)
         self._visit(loop.body, written_arrays, [loop])
 
-        rules, reductions, reduction_rules = [], {}, []
-        for array, write_kind, statement, is_update in self.writes:
-            if write_kind[0] == "unknown":
-                raise DependenceAnalysisError(
-                    f"Cannot tell which task owns the write "
-                    f"{ast.unparse(statement)!r} (index {write_kind[1]}).")
-            if write_kind[0] == "other_position":
+        def sid(statement):
+            if statement is None:
+                return "-"
+            return self.statement_ids.get(
+                (statement.lineno, statement.col_offset), "-")
+
+        def text(node):
+            return ast.unparse(node.slice if isinstance(node, ast.Subscript)
+                               else node)
+
+        def indirect(node):
+            index = node.slice if isinstance(node, ast.Subscript) else node
+            return any(isinstance(sub, ast.Subscript)
+                       for sub in ast.walk(self.aliases.resolve(index)))
+
+        # stage 1: last write and first read of every access expression
+        last_writes = {}
+        for array, kind, statement, is_update in self.writes:
+            target = (statement.target if isinstance(statement, ast.AugAssign)
+                      else next(t for t in statement.targets
+                                if isinstance(t, ast.Subscript)
+                                and t.value.id == array))
+            last_writes[(array, text(target))] = (
+                array, kind, statement, is_update, target)
+        first_reads, update_reads = {}, []
+        for array, kind, node, statement in self.reads:
+            key = (array, text(node))
+            own_target = (isinstance(statement, ast.AugAssign)
+                          and node is statement.target)
+            if own_target:
+                if type(statement.op) in ASSOCIATIVE_UPDATE_OPERATIONS:
+                    update_reads.append((array, kind, node, statement))
+                if key not in first_reads:
+                    first_reads[key] = (array, kind, node, statement)
+                continue
+            first_reads.setdefault(key, (array, kind, node, statement))
+        selected = list(first_reads.values())
+        chosen = {(id(statement), array, text(node))
+                  for array, _, node, statement in selected}
+        selected += [read for read in update_reads
+                     if (id(read[3]), read[0], text(read[2])) not in chosen]
+
+        # scattered plain writes cannot be ordered by any rule
+        reductions, reduction_rules = {}, []
+        for array, kind, statement, is_update, _ in last_writes.values():
+            if kind[0] == "other_position":
                 raise DependenceAnalysisError(
                     f"{ast.unparse(statement)!r} writes another task's "
                     "segment; this pattern is not supported.")
-            if write_kind[0] == "indirect":
+            if kind[0] == "indirect":
                 operator = ASSOCIATIVE_UPDATE_OPERATIONS.get(
                     type(statement.op)) if is_update else None
                 if operator is None:
@@ -511,64 +791,63 @@ class _Analyzer:
                         "non-associative write to other tasks' elements.")
                 location = (statement.lineno, statement.col_offset)
                 if location not in reductions:
-                    site = ReductionSite(
+                    reductions[location] = ReductionSite(
                         statement_id=f"S{len(reductions) + 1}",
                         operator=operator, location=location, array=array)
-                    reductions[location] = site
                     reduction_rules.append(
-                        f"reduction on {array}[{write_kind[1]}"
-                        f"[{write_kind[2]}]] ({operator}=)")
-            for read_array, read_kind in self.reads:
+                        f"reduction on {array}[{kind[1]}[{kind[2]}]] "
+                        f"({operator}=)")
+
+        # stages 2 and 3
+        raw, rules, conservative = [], [], False
+        for array, write_kind, statement, is_update, target in (
+                last_writes.values()):
+            for read_array, read_kind, node, reader in selected:
                 if read_array != array:
                     continue
-                rule = None
-                if write_kind == ("self",) and read_kind[0] == "indirect":
-                    rule = self._rule(False, read_kind[1], read_kind[2], array)
-                elif write_kind[0] == "indirect" and read_kind == ("self",):
-                    rule = self._rule(True, write_kind[1], write_kind[2], array)
-                elif (write_kind[0] == "own_position"
-                      and read_kind[0] == "other_position"):
-                    rule = self._rule(False, read_kind[1], read_kind[2], array)
-                elif "later_position" in (write_kind[0], read_kind[0]):
-                    if write_kind[0] == read_kind[0]:
-                        rule = self._row_rule(write_kind, read_kind, array)
-                    elif {write_kind[0], read_kind[0]} <= {
-                            "later_position", "self", "own_position"}:
-                        later = (write_kind if write_kind[0] == "later_position"
-                                 else read_kind)
-                        rule = self._later_rule(later[1], array)
-                    else:
+                if text(node) == text(target) and not indirect(node):
+                    continue        # the same element of the same iteration
+                verdict, reason, rule, kind = self._decide(
+                    array, write_kind, read_kind, statement, is_update,
+                    reader is statement)
+                if verdict == "kept" and kind == "RAW" and rule is None:
+                    if self.strict:
                         raise DependenceAnalysisError(
-                            f"Unsupported dependence on {array!r}: write "
-                            f"{write_kind[0]} / read {read_kind[0]}.")
-                elif write_kind[0] in ("self", "own_position") and (
-                        read_kind[0] in ("self", "own_position")):
-                    rule = None          # same task
-                elif write_kind[0] == "indirect" and read_kind[0] == "indirect":
-                    rule = None          # the update's own read-modify-write
-                elif read_kind[0] == "unknown":
-                    raise DependenceAnalysisError(
-                        f"Cannot tell which task produced the value read as "
-                        f"{array}[{read_kind[1]}].")
-                else:
-                    raise DependenceAnalysisError(
-                        f"Unsupported dependence on {array!r}: write "
-                        f"{write_kind[0]} / read {read_kind[0]}.")
+                            f"Unsupported dependence on {array!r} between "
+                            f"{ast.unparse(statement)!r} and the read "
+                            f"{array}[{text(node)}]: {reason}.")
+                    rule = NextRule(block_iterator=self.block,
+                                    carried_by=array)
+                    conservative = True
+                raw.append(RawDependence(
+                    array=array, from_statement_id=sid(statement),
+                    to_statement_id=sid(reader), write_index=text(target),
+                    read_index=text(node), kind=kind, verdict=verdict,
+                    reason=reason, rule=rule))
                 if rule is not None and rule not in rules:
                     rules.append(rule)
-        rules.sort(key=lambda rule: isinstance(rule, LaterRule))
+        if any(isinstance(rule, NextRule) for rule in rules):
+            # the chain already orders everything
+            rules = [rule for rule in rules if isinstance(rule, NextRule)][:1]
+        rules.sort(key=lambda rule: isinstance(rule, (LaterRule, NextRule)))
         return DependenceAnalysis(
             ordering_dependences=rules,
             reduction_dependences=reduction_rules,
             reductions=reductions,
+            raw_dependences=raw,
+            statement_ids=dict(self.statement_ids),
+            conservative=conservative,
         )
 
 
-def analyze_dependences(function_ast, block_iterator, function_props=None):
+def analyze_dependences(function_ast, block_iterator, function_props=None,
+                        strict=False):
     """Return the :class:`DependenceAnalysis` of the block loop.
 
     ``function_ast`` is an ``ast.Module`` holding one function, or the
-    ``ast.FunctionDef`` itself.
+    ``ast.FunctionDef`` itself.  ``strict=True`` raises
+    :class:`DependenceAnalysisError` for a dependence that has no
+    enumerable edge rule instead of keeping it as the complete order.
     """
     function = function_ast
     if isinstance(function_ast, ast.Module):
@@ -577,4 +856,4 @@ def analyze_dependences(function_ast, block_iterator, function_props=None):
         if len(functions) != 1:
             raise DependenceAnalysisError("Expected exactly one function.")
         function = functions[0]
-    return _Analyzer(function, block_iterator, function_props).run()
+    return _Analyzer(function, block_iterator, function_props, strict).run()

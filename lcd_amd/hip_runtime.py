@@ -91,7 +91,7 @@ class _Arch(ctypes.Structure):
         "lane_flops_per_s", "handoff_s", "barrier_s", "graph_node_s")]
 
 
-RULE_SEGMENT, RULE_LATER = 0, 1
+RULE_SEGMENT, RULE_LATER, RULE_NEXT = 0, 1, 2
 
 
 class _DagRule(ctypes.Structure):
@@ -619,14 +619,15 @@ class HIPDevice:
         ptr, idx, owner_is_source, lower_offset, upper_offset, guard,
         break_at_owner (ptr/idx host or device arrays), or, for the
         relational rule ``seg -> every j >= seg + lower_offset``, with
-        ``relation=RULE_LATER`` and ``lower_offset`` only."""
+        ``relation=RULE_LATER`` and ``lower_offset`` only (``RULE_NEXT``: the
+        single edge ``seg -> seg + lower_offset``)."""
         keep = []
         array = (_DagRule * max(len(rules), 1))()
         for slot, rule in zip(array, rules):
             get = rule.get if isinstance(rule, dict) else (
                 lambda key, r=rule: getattr(r, key, None))
-            if int(get("relation") or 0) == RULE_LATER:
-                slot.relation = RULE_LATER
+            if int(get("relation") or 0) in (RULE_LATER, RULE_NEXT):
+                slot.relation = int(get("relation"))
                 slot.lower_offset = int(get("lower_offset"))
                 continue
             slot.d_ptr, _ = self._resident_int32(get("ptr"), keep)

@@ -230,6 +230,12 @@ static int enumerate_rule(const oracle_rule *r, int64_t n, edge_fn fn, void *st)
                 fn(st, seg, j);
         return 0;
     }
+    if (r->relation == 2) {
+        /* chain rule: seg -> seg + lower_offset */
+        for (int64_t seg = 0; seg + r->lower_offset < n; ++seg)
+            fn(st, seg, seg + r->lower_offset);
+        return 0;
+    }
     for (int64_t seg = 0; seg < n; ++seg) {
         int64_t lo = (int64_t)r->ptr[seg] + r->lower_offset;
         int64_t hi = (int64_t)r->ptr[seg + 1] + r->upper_offset;

@@ -234,6 +234,11 @@ def rule_later(lower_offset=1):
     return dict(relation=1, lower_offset=int(lower_offset))
 
 
+def rule_next(lower_offset=1):
+    """The chain rule: seg -> seg + lower_offset."""
+    return dict(relation=2, lower_offset=int(lower_offset))
+
+
 def rules_ilu0_csc(A_indptr, A_indices):
     """The two rules of CSC ILU0
     (compiler/transform_tests/test_spilu0_codegen.py:146-150)."""
@@ -291,6 +296,11 @@ def literal_extract_dag(rule, n, execution_mode="sync_free",
     successors = [set() for _ in range(n)]
     edge_count = [0 for _ in range(n)]
     for rule in (rule if isinstance(rule, (list, tuple)) else [rule]):
+        if rule.get("relation") == 2:
+            for seg in range(0, n - rule["lower_offset"]):
+                successors[seg].add(seg + rule["lower_offset"])
+                edge_count[seg + rule["lower_offset"]] += 1
+            continue
         if rule.get("relation"):
             for seg in range(0, n):
                 for later in range(seg + rule["lower_offset"], n):

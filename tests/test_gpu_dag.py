@@ -136,6 +136,30 @@ def test_band_chains_of_a_random_dag(device, oracle):
         np.testing.assert_array_equal(dag.host("band_ptr"), band_ptr)
 
 
+def test_chain_rule_matches_oracle(device, oracle):
+    """LCDHIP_RULE_NEXT: seg -> seg + offset, alone and beside a segment
+    rule (duplicates of an edge the other rule already yields are merged)."""
+    for n, offset in ((1, 1), (2, 1), (1000, 1), (1000, 3), (5, 7)):
+        expected = oracle.dag_build([oracle.rule_next(offset)], n)
+        dag = device.dag_build([oracle.rule_next(offset)], n, levels=True)
+        assert dag.edges == expected.edges == max(n - offset, 0)
+        for name in ("dag_ptr", "dag_index", "dep_count", "edge_count",
+                     "level_of", "wavefronts", "wavefront_ptr"):
+            np.testing.assert_array_equal(dag.host(name),
+                                          getattr(expected, name))
+    work = workloads.configuration("c5", n=3000)
+    rules = [oracle.rule_sptrsv_csc(work.indptr, work.indices),
+             oracle.rule_next(1)]
+    expected = oracle.dag_build(rules, work.n)
+    dag = device.dag_build(rules, work.n, levels=True)
+    assert dag.edges == expected.edges
+    np.testing.assert_array_equal(dag.host("dag_index"), expected.dag_index)
+    np.testing.assert_array_equal(dag.host("edge_count"), expected.edge_count)
+    np.testing.assert_array_equal(dag.host("level_of"), expected.level_of)
+    with pytest.raises(hip_runtime.HIPRuntimeError, match="chain rule"):
+        device.dag_build([dict(relation=2, lower_offset=0)], 10)
+
+
 def test_golden_vectors(device, oracle):
     with open(GOLDEN) as handle:
         golden = json.load(handle)

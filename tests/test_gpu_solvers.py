@@ -835,6 +835,35 @@ def test_plain_kernel_on_an_edge_free_matrix(oracle):
         np.testing.assert_array_equal(result, expected)
 
 
+def _smooth(x, w, n):
+    for i in range(n):
+        x[i] = x[i] + w[i] * x[(i * 7) % n]
+    return x
+
+
+@pytest.mark.parametrize("mode", ["sync_free", "wavefront"])
+def test_unrecognised_dependence_runs_in_sequential_order(mode):
+    """A loop whose dependence no edge rule enumerates is kept as the
+    complete order (chain i -> i + 1): the decorated function runs, one
+    iteration after the other, and equals the undecorated loop bit for bit."""
+    import warnings
+
+    from lcd_amd import parallel
+    with warnings.catch_warnings(record=True) as caught:
+        warnings.simplefilter("always")
+        solver = parallel(loop="i", execution_mode=mode)(_smooth)
+    assert any("complete order" in str(w.message) for w in caught)
+    rng = np.random.default_rng(3)
+    n = 700
+    x0, w = rng.standard_normal(n), rng.uniform(-0.5, 0.5, n)
+    print("conservative", mode, n, flush=True)
+    expected = _smooth(x0.copy(), w, n)
+    result = solver(x0.copy(), w, n)
+    np.testing.assert_array_equal(result, expected)
+    successors, _ = solver.build_dag(x0, w, n)
+    assert successors == [[k + 1] for k in range(n - 1)] + [[]]
+
+
 def _random_lower_triangle(rng, kind, n):
     """Strictly lower part scaled by 0.1 plus a diagonal in [1, 2): random
     sparsity, a band, a 5-point grid, or an arrow (first column and last row

@@ -26,6 +26,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 GOLDEN = json.load(open(os.path.join(ROOT, "tests", "golden",
                                      "reference_vectors.json")))
 
+CSR_PROPS = {"Ap": ["monotonically_increasing"], "Ai": []}
 CSC_PROPS = {"Ap": ["monotonically_increasing"], "Ai": [],
              ("Ap", "Ai"): ["triangularity"]}
 ILU_PROPS = {"A_indptr": ["monotonically_increasing"], "A_indices": [],
@@ -496,7 +497,13 @@ def test_column_ilu0_gets_the_push_rule_and_the_relational_rule():
     module = ast.parse(ast.unparse(demo_source("spilu0", "ilu0_csc")).replace(
         "range(k + 1, n)", "range(k + 1, n - 1)"))
     with pytest.raises(DependenceAnalysisError):
-        analyze_dependences(module, "k", ILU_PROPS)
+        analyze_dependences(module, "k", ILU_PROPS, strict=True)
+    # ... by default the dependence is kept as the complete order instead
+    from lcd_amd.dependence import NextRule
+    kept = analyze_dependences(module, "k", ILU_PROPS)
+    assert kept.conservative
+    assert kept.ordering_dependences == [NextRule(1, "k", "_lcd_next",
+                                                  "A_data")]
 
 
 def test_generated_inspector_text_matches_the_reference_shape():
@@ -1101,3 +1108,81 @@ def test_large_level_graphs_are_not_replayed_under_a_profiler(monkeypatch):
                        "/opt/rocm/lib/rocprofiler-sdk/librocprofiler-sdk-tool.so")
     assert hip_runtime.profiler_attached()
     assert 382 <= hip_runtime.TRACED_GRAPH_NODE_LIMIT < 3070
+
+
+def test_raw_candidates_and_survivors_match_the_reference_records():
+    """Statement numbering, first-read x last-write candidates and what
+    survives refutation, against what the reference's tests record for its
+    SPF/Z3 pipeline: SpTRSV-CSR keeps S3 -> S2 (``i1 = Ai[j2]``), SpTRSV-CSC
+    keeps S2 -> S1 and the reduction S2 -> S2
+    (compiler/transform_tests/test_dag_codegen.py:58-99); ILU0 keeps two
+    ordering dependences on CSR and three on CSC, no reduction, and nothing
+    from S2 to S3 (test_spilu0_codegen.py:63-88)."""
+    csr = analyze_dependences(demo_source("sptrsv", "simple_sptrsv_csr"), "i",
+                              CSR_PROPS)
+    assert [(d.from_statement_id, d.to_statement_id, d.read_index)
+            for d in csr.kept_dependences] == [("S3", "S2", "Ai[j]")]
+    assert not csr.reduction_candidates
+    csc = analyze_dependences(demo_source("sptrsv", "simple_sptrsv_csc"), "i",
+                              CSC_PROPS)
+    assert [(d.from_statement_id, d.to_statement_id, d.write_index)
+            for d in csc.kept_dependences] == [("S2", "S1", "Ai[j]")]
+    assert [(d.from_statement_id, d.to_statement_id)
+            for d in csc.reduction_candidates] == [("S2", "S2")]
+    refuted = [d for d in csc.raw_dependences if d.verdict == "refuted"]
+    assert [(d.from_statement_id, d.to_statement_id) for d in refuted] == [
+        ("S1", "S2")] and "triangularity" in refuted[0].reason
+    for storage, iterator, kept in (("ilu0_csr", "i", 2), ("ilu0_csc", "k", 3)):
+        analysis = analyze_dependences(demo_source("spilu0", storage),
+                                       iterator, ILU_PROPS)
+        assert len(analysis.kept_dependences) == kept
+        assert not analysis.reduction_candidates and not analysis.reductions
+        assert len(analysis.raw_dependences) == 6
+        assert not analysis.conservative
+        pairs = {(d.from_statement_id, d.to_statement_id)
+                 for d in analysis.kept_dependences}
+        assert ("S2", "S3") not in pairs
+    csr_ilu = analyze_dependences(demo_source("spilu0", "ilu0_csr"), "i",
+                                  ILU_PROPS)
+    # the survivors are the update of the row's later entries read as a
+    # pivot row's diagonal and as its entries right of the pivot
+    assert {(d.write_index, d.read_index)
+            for d in csr_ilu.kept_dependences} == {
+        ("j_ptr", "diag_ptr"), ("j_ptr", "kj_ptr")}
+    # without the sorted-segment property nothing tells the entries of a
+    # segment apart: the scaled entries left of the diagonal stay candidates
+    loose = analyze_dependences(
+        demo_source("spilu0", "ilu0_csr"), "i",
+        {"A_indptr": ["monotonically_increasing"], "A_indices": []})
+    assert len(loose.kept_dependences) == 4
+
+
+def test_unrecognised_dependence_is_kept_as_the_complete_order():
+    """A loop whose access shape no rule enumerates (here a strided
+    neighbour) still runs: the dependence is kept and ordered by the chain
+    i -> i + 1, the closure of which contains every possible dependence."""
+    from lcd_amd.dependence import NextRule
+    source = (
+        "def smooth(x, w, n):\n"
+        "    for i in range(n):\n"
+        "        x[i] = x[i] + w[i] * x[(i * 7) % n]\n"
+        "    return x\n")
+    analysis = analyze_dependences(ast.parse(source), "i", {})
+    assert analysis.conservative
+    assert analysis.ordering_dependences == [NextRule(1, "i", "_lcd_next", "x")]
+    assert [d.verdict for d in analysis.raw_dependences] == ["kept"]
+    with pytest.raises(DependenceAnalysisError, match="not a recognised"):
+        analyze_dependences(ast.parse(source), "i", {}, strict=True)
+    plan = create_dag_plan(analysis.ordering_dependences, None, "i",
+                           ["x", "w", "n"])
+    text = generate_dag_source(plan)
+    assert "for _lcd_next in range(i + 1, min(i + 2, n)):" in text
+    namespace = {}
+    exec(compile(text, "<dag>", "exec"), namespace)
+    dag, dep_count = namespace["extract_dag"](None, None, 5)
+    assert dag == [[1], [2], [3], [4], []] and dep_count == [0, 1, 1, 1, 1]
+    from oracle import lcd_oracle
+    chain = lcd_oracle.dag_build([lcd_oracle.rule_next(1)], 5)
+    assert chain.successors() == dag and chain.levels == 5
+    assert lcd_oracle.literal_extract_dag(lcd_oracle.rule_next(2), 5)[0] == [
+        [2], [3], [4], [], []]
