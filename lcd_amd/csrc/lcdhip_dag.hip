@@ -435,6 +435,39 @@ sweep_levels_kernel(const int32_t *__restrict__ pred_ptr,
         atomicMax(&state[2], highest);
 }
 
+// Shortcut of the ordered sweep for chains.  With ids in topological order
+// level(v) <= v, and a node whose predecessors include v - 1 has
+// level(v) >= level(v - 1) + 1; so on the longest prefix [0, m) in which every
+// node v >= 1 has the predecessor v - 1 the level is the id itself.
+// Predecessor lists are sorted, so v - 1 can only be the last entry.
+// state[3] receives m (the host sets it to n beforehand).
+__global__ void chain_prefix_kernel(const int32_t *__restrict__ pred_ptr,
+                                    const int32_t *__restrict__ pred_index,
+                                    int64_t n, int32_t *state)
+{
+    int64_t v = 1 + blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (v >= n)
+        return;
+    const int32_t end = pred_ptr[v + 1];
+    if (end == pred_ptr[v] || pred_index[end - 1] != v - 1)
+        atomicMin(&state[3], static_cast<int32_t>(v));
+}
+
+// level_of[v] = v on the chain prefix; the sweep's chunk counter starts at the
+// chunk that holds the first node behind it.
+__global__ void chain_fill_kernel(int64_t n, int32_t *__restrict__ level_of,
+                                  int32_t *state)
+{
+    const int32_t m = state[3];
+    int64_t v = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (v == 0) {
+        state[0] = m / 64;
+        atomicMax(&state[2], m);
+    }
+    if (v < m)
+        level_of[v] = static_cast<int32_t>(v);
+}
+
 __global__ void level_histogram_kernel(const int32_t *__restrict__ level_of,
                                        int64_t n, int32_t *__restrict__ hist)
 {
@@ -834,6 +867,17 @@ static int build_levels(lcdhip_dag *dag, const unsigned long long *d_transposed,
                                dim3(kBlock), 0, stream, sorted, edges,
                                pred_index);
         }
+        // chain prefix: its levels are known without sweeping (`whole` stays
+        // alive until the synchronisation behind the sweep)
+        const int32_t whole = static_cast<int32_t>(n);
+        LCDHIP_CHECK(hipMemcpyAsync(state + 3, &whole, 4, hipMemcpyHostToDevice,
+                                    stream));
+        if (n > 1)
+            hipLaunchKernelGGL(chain_prefix_kernel, dim3(blocks_for(n - 1)),
+                               dim3(kBlock), 0, stream, pred_ptr, pred_index, n,
+                               state);
+        hipLaunchKernelGGL(chain_fill_kernel, dim3(blocks_for(n)), dim3(kBlock),
+                           0, stream, n, level_of, state);
         const int64_t chunks = (n + 63) / 64;
         const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(
             (chunks + 3) / 4,

@@ -160,6 +160,26 @@ def test_chain_rule_matches_oracle(device, oracle):
         device.dag_build([dict(relation=2, lower_offset=0)], 10)
 
 
+@pytest.mark.parametrize("gap", [1, 63, 64, 1234, 2999])
+def test_levels_behind_a_chain_prefix(device, oracle, gap):
+    """The level sweep skips the longest prefix in which every node follows
+    its predecessor in the numbering (level = id there); behind the first
+    node that does not, levels come from the sweep."""
+    import scipy.sparse as sp
+    work = workloads.configuration("c5", n=3000)
+    matrix = sp.csc_matrix((work.data, work.indices, work.indptr),
+                           shape=(work.n, work.n)).tolil()
+    matrix[gap:, gap - 1] = 0.0        # node `gap` loses the predecessor gap - 1
+    matrix = matrix.tocsc()
+    matrix.eliminate_zeros()
+    matrix.sort_indices()
+    rule = oracle.rule_sptrsv_csc(matrix.indptr.astype(np.int32),
+                                  matrix.indices.astype(np.int32))
+    print("chain prefix", gap, flush=True)
+    dag, expected = _check_dag(device, oracle, rule, work.n)
+    assert dag.levels < work.n
+
+
 def test_golden_vectors(device, oracle):
     with open(GOLDEN) as handle:
         golden = json.load(handle)
