@@ -122,6 +122,7 @@ class HIPLoweringResult:
     stage_kernel_arguments: tuple = ()
     # tiled persistent executor: block-iterator values per tile, or None
     tile_rows: int | None = None
+    spin_limit: int = DEFAULT_SPIN_LIMIT   # watchdog limit the caller chose
 
     @property
     def module_source(self):
@@ -355,7 +356,7 @@ class _Emitter:
                 return (f"lcd_seg_ldp({node.value.id}, _lcd_pub, _lcd_seg, "
                         "_lcd_seg_base, _lcd_seg_limit, _lcd_seg_own, "
                         f"{self.expr(node.slice)}, {STATUS_ARGUMENT}, "
-                        "_task_aborted)")
+                        "_task_aborted, _lcd_t0)")
             if segment is not None and node.value.id == segment["array"]:
                 name = ("lcd_seg_ldc" if node.value.id in self.coherent_arrays
                         else "lcd_seg_ld")
@@ -441,7 +442,7 @@ class _Emitter:
                 target = node.args[0]
                 return ("lcd_seg_settle(_lcd_pub, _lcd_seg_base, _lcd_seg_own, "
                         f"{self.expr(target.slice)}, {args[1]}, "
-                        f"{STATUS_ARGUMENT}, _task_aborted)")
+                        f"{STATUS_ARGUMENT}, _task_aborted, _lcd_t0)")
         raise HIPLoweringError(
             f"Unsupported expression in a device loop: {ast.unparse(node)!r}.")
 

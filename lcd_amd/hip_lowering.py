@@ -467,6 +467,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
             mailbox_index_array=(self._mailbox["index_array"]
                                  if self._mailbox else None),
             tile_rows=self._tile["rows"] if self._tile else None,
+            spin_limit=self.spin_limit,
             queue_node_loads=tuple(self._queue_node_loads),
             published_array=(self._published["array"]
                              if self._published else None),
@@ -966,6 +967,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
         lines = ["    const int _task_count = (int)task_count;"]
         if self.block_task:
             lines += [
+                "    const long long _lcd_t0 = (long long)wall_clock64();",
                 "    while (true) {",
                 "        if (threadIdx.x == 0)",
                 "            _lcd_task_slot = atomicAdd(&task_counter[0], 1);",
@@ -983,7 +985,8 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                 "            int _ok = 1;",
                 f"            while (lcd_load_relaxed(&dep_count[{it}]) != LCD_READY_COUNT) {{",
                 "                __builtin_amdgcn_s_sleep(LCD_SPIN_SLEEP);",
-                "                if (++_spins > LCD_SPIN_LIMIT || ((_spins & 255) == 0 && "
+                "                if ((++_spins & 255) == 0 && ("
+                f"lcd_gave_up(_spins, {STATUS_ARGUMENT}, _lcd_t0) || "
                 f"lcd_load_relaxed(&{STATUS_ARGUMENT}[0]) != 0)) {{",
                 f"                    {STATUS_ARGUMENT}[0] = 1;",
                 "                    _ok = 0;",
@@ -1192,8 +1195,8 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
             # the watchdog looks up once in 1024 polls (a 32-bit counter, one
             # test per poll): kept out of the way of the hand-offs, it costs
             # 3 % on the 128^3 grid where the test per poll cost 8 %
-            "                    if ((++_spins & 1023u) == 0u && (_spins > "
-            "(unsigned)LCD_SPIN_LIMIT || "
+            "                    if ((++_spins & 1023u) == 0u && ("
+            f"lcd_gave_up(_spins, {STATUS_ARGUMENT}, _lcd_t0) || "
             f"lcd_load_relaxed(&{STATUS_ARGUMENT}[0]) != 0)) {{",
             f"                        {STATUS_ARGUMENT}[0] = 1;",
             "                        _pending = false;",
@@ -1210,6 +1213,8 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                "    }"]),
         ]
         lines.insert(1, "    bool _task_aborted = false;")
+        lines.insert(1, "    const long long _lcd_t0 = (long long)wall_clock64();"
+                        " (void)_lcd_t0;")
         return lines
 
     def _reset_kernel_text(self, reset_name):

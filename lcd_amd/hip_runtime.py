@@ -966,6 +966,38 @@ def _execution_values(execution_mode, execution_data):
     return values
 
 
+WATCHDOG_UNIT_TICKS = 1 << 20        # of the 100 MHz device wall clock
+
+
+def watchdog_budget(lowering, execution_data):
+    """Time budget of one launch of a persistent executor for this plan, in
+    units of 2^20 ticks of the 100 MHz wall clock (about 10.5 ms): two
+    seconds plus 8 us per level of the DAG (per node for chain tasks, which
+    run their members one after the other), at most five minutes.  A stuck
+    schedule on a DAG of a few hundred levels then gives up after two seconds
+    instead of the twenty-odd the poll count alone took, and a chain of
+    millions of levels, whose launch legitimately runs for seconds, keeps
+    the time it needs.  0 (= poll count only) when the caller chose
+    ``spin_limit`` or the depth is not known."""
+    from lcd_amd.hip_emitter import DEFAULT_SPIN_LIMIT
+    if getattr(lowering, "spin_limit", DEFAULT_SPIN_LIMIT) != DEFAULT_SPIN_LIMIT:
+        return 0
+    bands = getattr(execution_data, "band_ptr", None)
+    if bands is None:
+        bands = getattr(execution_data, "wavefront_ptr", None)
+    try:
+        depth = len(bands) - 1
+        nodes = getattr(execution_data, "task_nodes", None)
+        chains = getattr(execution_data, "task_ptr", None)
+        if (nodes is not None and chains is not None
+                and len(chains) - 1 != len(nodes)):
+            depth = len(nodes)
+    except TypeError:
+        return 0
+    seconds = min(2.0 + 8.0e-6 * max(depth, 0), 300.0)
+    return int(seconds * 1.0e8 / WATCHDOG_UNIT_TICKS) + 1
+
+
 def _scalar_ctype(value):
     if isinstance(value, (bool, np.bool_)):
         return "long long"
@@ -1071,7 +1103,13 @@ def prepare_hip_arguments(lowering, argument_values, execution_data,
         for name in ("task_counter", STATUS_ARGUMENT):
             cached = workspace.get(("state", name))
             if cached is None:
-                cached = device.zeros((4,), np.int32)
+                if name == STATUS_ARGUMENT and hasattr(device, "to_device"):
+                    # word 0: abort flag; word 1: time budget of this plan
+                    cached = device.to_device(np.array(
+                        [0, watchdog_budget(lowering, execution_data),
+                         0, 0], dtype=np.int32))
+                else:
+                    cached = device.zeros((4,), np.int32)
                 workspace[("state", name)] = cached
             host_values[name] = cached
 
@@ -1300,7 +1338,11 @@ def check_executor_status(lowering, prepared_arguments):
         return
     host = status.copy_to_host()
     if int(host[0]) != 0:
-        prepared_arguments.device.fill_zero(status)
+        # re-arm the flag; the plan's time budget in word 1 stays
+        device = prepared_arguments.device
+        _check(device.lib.lcdhip_buffer_fill32(
+            ctypes.c_void_p(status.pointer), ctypes.c_uint32(0),
+            ctypes.c_size_t(1), device.stream))
         raise ExecutorWatchdogError(
             f"The sync-free executor of {lowering.function_name} gave up "
             "waiting for a dependence (cyclic or inconsistent schedule).",

@@ -49,7 +49,29 @@ CASES = [
          "mailbox-staged", "mailbox-tiled", "pull-values", "pull-flags", "pull-tiled"])
 def test_unsatisfiable_wait_trips_the_watchdog(oracle, name, props, protocol,
                                                extra):
-    print("watchdog", name, protocol, extra, flush=True)
+    _trip_and_recover(oracle, name, props, protocol, extra,
+                      dict(spin_limit=3000))
+
+
+@pytest.mark.parametrize("protocol,extra", [
+    ("counter", {}), ("mailbox", dict(tile_rows=512)), ("pull", {})])
+def test_default_watchdog_gives_up_within_seconds(oracle, protocol, extra):
+    """Without a caller-chosen spin limit the plan's own limit (scaled to
+    the 127 levels of this DAG) applies: the stuck launch ends in seconds,
+    not in the twenty-odd the fixed default took."""
+    import time
+    name, props = (("sptrsv_csr_loop", sptrsv.FUNCTION_PROPS_CSR)
+                   if protocol == "pull"
+                   else ("sptrsv_csc_loop", sptrsv.FUNCTION_PROPS_CSC))
+    start = time.perf_counter()
+    _trip_and_recover(oracle, name, props, protocol, extra, {})
+    elapsed = time.perf_counter() - start
+    print(f"default watchdog {protocol}: {elapsed:.2f} s", flush=True)
+    assert elapsed < 10.0
+
+
+def _trip_and_recover(oracle, name, props, protocol, extra, limit):
+    print("watchdog", name, protocol, extra, limit, flush=True)
     function = getattr(sptrsv, name)
     module = ast.parse(inspect.getsource(function))
     analysis = analyze_dependences(module, "i", props)
@@ -61,7 +83,7 @@ def test_unsatisfiable_wait_trips_the_watchdog(oracle, name, props, protocol,
         wavefront_threads_per_block=64, dependence_protocol=protocol,
         direct_dependence=(None if protocol == "counter"
                            else direct_dependence(plan, "j")),
-        spin_limit=3000, **extra)
+        **limit, **extra)
     assert lowering.dependence_protocol == protocol
     compiled = hip_runtime.compile_hip_module(lowering, {"np": np})
 
