@@ -50,8 +50,9 @@ TUNED = {
     "c3": dict(execution_mode="sync_free", threads_per_block=128,
                task_lanes=64, thread_unroll=1,
                dependence_protocol="pull", tile_rows=None),
-    "c4": dict(execution_mode="sync_free", threads_per_block=128,
-               task_lanes=64, thread_unroll=1, dependence_protocol="pull"),
+    "c4": dict(execution_mode="sync_free", threads_per_block=512,
+               task_lanes=64, thread_unroll=1, dependence_protocol="pull",
+               tile_rows=1024, tile_positions=9216, segment_capacity=64),
     "c5": dict(execution_mode="sync_free", threads_per_block=256, task_lanes=8,
                thread_unroll=1, dependence_protocol="mailbox",
                tile_rows=4096),
@@ -118,6 +119,10 @@ def build_solver(work, args, config):
         options["spin_sleep"] = args.spin_sleep
     if args.tile_rows is not None:
         options["tile_rows"] = args.tile_rows or None
+    if args.tile_positions:
+        options["tile_positions"] = args.tile_positions
+    if args.segment_capacity:
+        options["segment_capacity"] = args.segment_capacity
     if args.no_queue_loads:
         options["queue_node_loads"] = False
     if args.plain_first is not None:
@@ -413,6 +418,13 @@ def main():
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--tile-rows", dest="tile_rows", type=int, default=None,
                         help="tiled persistent executor: rows per tile")
+    parser.add_argument("--tile-positions", dest="tile_positions", type=int,
+                        default=None,
+                        help="tiled published pull (ILU0): entries of the "
+                             "publication buffer a tile mirrors in LDS")
+    parser.add_argument("--segment-capacity", dest="segment_capacity",
+                        type=int, default=None,
+                        help="entries of a task's own segment staged in LDS")
     parser.add_argument("--slots", action="store_true",
                         help="message slots instead of the gathered form of "
                              "the mailbox protocol (implies no tiles)")
@@ -489,7 +501,8 @@ def main():
         sub_args = argparse.Namespace(**vars(args))
         for name in ("mode", "tpb", "lanes", "unroll", "protocol",
                      "waves_per_cu", "spin_sleep", "tile_rows",
-                     "plain_first", "look_ahead"):
+                     "plain_first", "look_ahead", "tile_positions",
+                     "segment_capacity"):
             setattr(sub_args, name, None)
         for name in ("slots", "no_queue_loads", "no_publish", "no_pipeline",
                      "no_graph"):

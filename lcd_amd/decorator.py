@@ -231,6 +231,7 @@ def parallel(**kwargs):
                     look_ahead=kwargs.get("look_ahead", True),
                     segment_capacity=kwargs.get("segment_capacity"),
                     pipeline_fetch=kwargs.get("pipeline_fetch", True),
+                    tile_positions=kwargs.get("tile_positions"),
                     full_fences=kwargs.get("full_fences", False),
                     dynamic_fetch=kwargs.get("dynamic_fetch", False),
                 )
@@ -262,8 +263,15 @@ def parallel(**kwargs):
                     and kwargs.get("threads_per_block") is None
                     and not tile_threads % max(schedule.task_lanes, 1)):
                 tiled = replace(schedule, threads_per_block=tile_threads)
-            if lower_variant(tiled.lowering_key, rows).tile_rows is None:
+            variant = lower_variant(tiled.lowering_key, rows)
+            if variant.tile_rows is None:
                 return schedule, None        # tiles do not apply to this loop
+            if tile_option == "auto" and variant.published_array is not None:
+                # published pull (ILU0): tiles pay only with many wavefronts
+                # per tile and rows sized to the grid lines (6.4 against
+                # 7.1 ms on the 9-point 1024^2 grid at 1024 rows and 512
+                # threads, 38 ms at the sizes chosen for SpTRSV): by request
+                return schedule, None
             return tiled, rows
 
         host_lowering = lower_variant(

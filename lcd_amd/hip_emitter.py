@@ -356,7 +356,8 @@ class _Emitter:
                 return (f"lcd_seg_ldp({node.value.id}, _lcd_pub, _lcd_seg, "
                         "_lcd_seg_base, _lcd_seg_limit, _lcd_seg_own, "
                         f"{self.expr(node.slice)}, {STATUS_ARGUMENT}, "
-                        "_task_aborted, _lcd_t0)")
+                        "_task_aborted, _lcd_t0, _lcd_ptile, _lcd_tpos0, "
+                        "_lcd_tlen)")
             if segment is not None and node.value.id == segment["array"]:
                 name = ("lcd_seg_ldc" if node.value.id in self.coherent_arrays
                         else "lcd_seg_ld")
@@ -437,12 +438,14 @@ class _Emitter:
                 target = node.args[0]
                 return (f"lcd_seg_ldr({target.value.id}, _lcd_pub, _lcd_seg, "
                         "_lcd_seg_base, _lcd_seg_limit, _lcd_seg_own, "
-                        f"{self.expr(target.slice)})")
+                        f"{self.expr(target.slice)}, _lcd_ptile, _lcd_tpos0, "
+                        "_lcd_tlen)")
             if name == "_lcd_settle" and self.published is not None:
                 target = node.args[0]
                 return ("lcd_seg_settle(_lcd_pub, _lcd_seg_base, _lcd_seg_own, "
                         f"{self.expr(target.slice)}, {args[1]}, "
-                        f"{STATUS_ARGUMENT}, _task_aborted, _lcd_t0)")
+                        f"{STATUS_ARGUMENT}, _task_aborted, _lcd_t0, "
+                        "_lcd_ptile, _lcd_tpos0, _lcd_tlen)")
         raise HIPLoweringError(
             f"Unsupported expression in a device loop: {ast.unparse(node)!r}.")
 

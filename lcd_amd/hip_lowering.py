@@ -99,7 +99,8 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                  queue_node_loads=True, plain_first_polls=None,
                  publish_values=True, look_ahead=True, segment_capacity=None,
                  pipeline_fetch=True, full_fences=False,
-                 dynamic_fetch=False):
+                 dynamic_fetch=False, tile_positions=None):
+        self.tile_positions = tile_positions
         # full_fences: agent-scope release/acquire fences of the HIP memory
         # model (L2 write-back / invalidate per hand-off) instead of the
         # wait-for-completion scheme; dynamic_fetch: the flat queue hands out
@@ -357,7 +358,10 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                            coherent_arrays=coherent)
         emitter.segment = self._segment
         emitter.published = self._published
-        emitter.tile = self._tile
+        # (the tile of a published pull mirrors the publication buffer, not
+        # the array itself: its accesses go through the segment accessors)
+        emitter.tile = (None if self._tile and self._tile.get("published")
+                        else self._tile)
         emitter.mailbox = self._mailbox
         emitter.lowerer = self
         self._emitter = emitter
@@ -780,6 +784,9 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
             defines.append(f"#define LCD_SEG_CAP {self._segment['capacity']}")
         if self._tile is not None:
             defines.append(f"#define LCD_TILE_ROWS {self._tile['rows']}")
+            if self._tile.get("published"):
+                defines.append(
+                    f"#define LCD_TILE_POS {self._tile['positions']}")
             # a poll of memory stalls the whole wavefront for a memory round
             # trip; sources outside the running tile are polled on every
             # (mask + 1)-th pass only, LDS on every pass
@@ -870,12 +877,28 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
             lines.append("    __shared__ int _lcd_task_slot;")
         lines.append("    const int _lane = threadIdx.x % LCD_TASK_LANES;")
         lines.append("    (void)_lane;")
-        if self._tile is not None:
+        if self._tile is not None and self._tile.get("published"):
+            lines += [
+                f"    __shared__ LCD_T_{self._tile['array']} "
+                "_lcd_ptile[LCD_TILE_POS];",
+                "    __shared__ int _lcd_tile_slot;",
+                "    lcd_index_t _lcd_tile_row0 = 0, _lcd_tile_rows = 0;",
+                "    lcd_index_t _lcd_tpos0 = 0, _lcd_tlen = 0;",
+            ]
+        elif self._tile is not None:
             lines += [
                 f"    __shared__ LCD_T_{self._tile['array']} "
                 "_lcd_tile[LCD_TILE_ROWS];",
                 "    __shared__ int _lcd_tile_slot;",
                 "    lcd_index_t _lcd_tile_row0 = 0, _lcd_tile_rows = 0;",
+            ]
+        if self._published is not None and not (
+                self._tile is not None and self._tile.get("published")):
+            # no tile: the published accessors never look for an LDS copy
+            lines += [
+                f"    LCD_T_{self._published['array']}* const _lcd_ptile = nullptr;",
+                "    const lcd_index_t _lcd_tpos0 = 0, _lcd_tlen = 0;",
+                "    (void)_lcd_ptile; (void)_lcd_tpos0; (void)_lcd_tlen;",
             ]
         if self._segment is not None:
             array = self._segment["array"]
@@ -1039,8 +1062,19 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                 "    _lcd_tile_row0 = _tile * LCD_TILE_ROWS;",
                 "    _lcd_tile_rows = _task_count - _lcd_tile_row0 < LCD_TILE_ROWS "
                 "? _task_count - _lcd_tile_row0 : LCD_TILE_ROWS;",
-                "    for (int _s = threadIdx.x; _s < _lcd_tile_rows; _s += LCD_TPB) "
-                "_lcd_tile[_s] = lcd_empty();",
+                *([
+                    # the tile's slice of the publication buffer
+                    f"    _lcd_tpos0 = (lcd_index_t){self._tile['pointer']}"
+                    "[_lcd_tile_row0];",
+                    f"    _lcd_tlen = (lcd_index_t){self._tile['pointer']}"
+                    "[_lcd_tile_row0 + _lcd_tile_rows] - _lcd_tpos0;",
+                    "    if (_lcd_tlen > LCD_TILE_POS) _lcd_tlen = 0;",
+                    "    for (int _s = threadIdx.x; _s < _lcd_tlen; _s += LCD_TPB) "
+                    "_lcd_ptile[_s] = lcd_empty();",
+                ] if self._tile.get("published") else [
+                    "    for (int _s = threadIdx.x; _s < _lcd_tile_rows; "
+                    "_s += LCD_TPB) _lcd_tile[_s] = lcd_empty();",
+                ]),
                 "    __syncthreads();",
                 "    for (int _round = 0; ; ++_round) {",
                 "        const int _local = (_round * (LCD_TPB / 64) + "
@@ -1382,7 +1416,8 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
                  stage_operands=True, task_records=True, single_chunk=False,
                  queue_node_loads=True, plain_first_polls=None,
                  publish_values=True, look_ahead=True, segment_capacity=None,
-                 pipeline_fetch=True, full_fences=False, dynamic_fetch=False):
+                 pipeline_fetch=True, full_fences=False, dynamic_fetch=False,
+                 tile_positions=None):
     """HIP counterpart of ``lower_to_numba_cuda``
     (compiler/cuda_lowering.py:2854-2884); same parameters plus
     ``task_lanes`` (lanes cooperating on one task, a power of two <= 64),
@@ -1409,5 +1444,5 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
         plain_first_polls=plain_first_polls, publish_values=publish_values,
         look_ahead=look_ahead, segment_capacity=segment_capacity,
         pipeline_fetch=pipeline_fetch, full_fences=full_fences,
-        dynamic_fetch=dynamic_fetch)
+        dynamic_fetch=dynamic_fetch, tile_positions=tile_positions)
     return lowerer.lower(code)

@@ -95,6 +95,20 @@ class TaskTransformMixin:
             raise HIPLoweringError(
                 "tile_rows must be a positive integer of at most 8192 "
                 "(64 KB of LDS).")
+        if (self._published is not None and self._segment is not None
+                and self.execution_mode == "sync_free"
+                and len(target_loop.iter.args) == 1):
+            # published pull (ILU0): the tile's slice of the publication
+            # buffer, positions P[row0] .. P[row0 + rows), has a copy in LDS;
+            # a tile whose slice is longer than the copy runs without it
+            positions = self.tile_positions or min(16 * rows, 8192)
+            if not isinstance(positions, int) or not 0 < positions <= 16384:
+                raise HIPLoweringError(
+                    "tile_positions must be a positive integer of at most "
+                    "16384 (128 KB of LDS).")
+            return {"array": self._published["array"], "rows": rows,
+                    "published": True, "positions": positions,
+                    "pointer": self._segment["pointer"]}
         array = None
         if self._value_pull is not None:
             array = self._value_pull["array"]
@@ -253,9 +267,11 @@ class TaskTransformMixin:
             epilogue = [
                 self.group_sync,
                 "for (int _q = _lane; _q < _lcd_seg_limit; _q += LCD_TASK_LANES) "
-                "lcd_st(&_lcd_pub[_lcd_seg_base + _q], _lcd_seg[_q]);",
+                "lcd_pub_st(_lcd_pub, _lcd_ptile, _lcd_tpos0, _lcd_tlen, "
+                "_lcd_seg_base + _q, _lcd_seg[_q]);",
                 "if (_lcd_seg_limit == 0) for (int _q = _lane; _q < _lcd_seg_own; "
-                "_q += LCD_TASK_LANES) lcd_st(&_lcd_pub[_lcd_seg_base + _q], "
+                "_q += LCD_TASK_LANES) lcd_pub_st(_lcd_pub, _lcd_ptile, "
+                "_lcd_tpos0, _lcd_tlen, _lcd_seg_base + _q, "
                 f"lcd_ld(&{array}[_lcd_seg_base + _q]));",
                 "for (int _q = _lane; _q < _lcd_seg_limit; _q += LCD_TASK_LANES) "
                 f"{array}[_lcd_seg_base + _q] = _lcd_seg[_q];",

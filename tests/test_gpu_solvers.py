@@ -394,6 +394,16 @@ ILU_VARIANTS = [
          dependence_protocol="pull"),
     dict(execution_mode="sync_free", threads_per_block=256, task_lanes=64,
          dependence_protocol="pull", publish_values=False),
+    # published values in tiles: a workgroup owns consecutive rows and keeps
+    # their slice of the publication buffer in LDS (tiles that are not whole
+    # grid lines; a copy too small for a tile, which then runs without it)
+    dict(execution_mode="sync_free", threads_per_block=256, task_lanes=64,
+         dependence_protocol="pull", tile_rows=100, tile_positions=1024,
+         segment_capacity=64),
+    dict(execution_mode="sync_free", threads_per_block=64, task_lanes=64,
+         dependence_protocol="pull", tile_rows=72, tile_positions=700),
+    dict(execution_mode="sync_free", threads_per_block=128, task_lanes=64,
+         dependence_protocol="pull", tile_rows=256, tile_positions=512),
 ]
 
 
@@ -420,6 +430,9 @@ def test_ilu0_csr_variants(oracle, options):
                      and options.get("segment_cache", True)
                      and options.get("publish_values", True))
         assert ("_lcd_pub" in factor.hip_kernel_source) == published
+        if "tile_rows" in options:
+            assert factor.hip_lowering.tile_rows == options["tile_rows"]
+            assert "_lcd_ptile[LCD_TILE_POS]" in factor.hip_kernel_source
         assert ("done[" in factor.hip_kernel_source) != published
         # irregular rows too: pivots near and far, empty lower parts
         import scipy.sparse as sp
