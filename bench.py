@@ -44,7 +44,8 @@ TUNED = {
     "c1": dict(execution_mode="sync_free", threads_per_block=256, task_lanes=4,
                thread_unroll=1, dependence_protocol="mailbox",
                tile_rows=1024, spin_sleep=0),
-    "c2": dict(execution_mode="sync_free", threads_per_block=384, task_lanes=4,
+    # (tiles are boxes of 128 x 8 x 4 grid points: the default tile_box="auto")
+    "c2": dict(execution_mode="sync_free", threads_per_block=512, task_lanes=4,
                thread_unroll=1, dependence_protocol="mailbox",
                tile_rows=4096, spin_sleep=0),
     "c3": dict(execution_mode="sync_free", threads_per_block=128,
@@ -73,8 +74,11 @@ CPU_SECONDS_SUB = 3.0
 RTOL, ATOL_SCALE = 1e-12, 1e-15
 
 
-def traffic_key(config, mode, protocol, lanes, tile_rows):
-    return f"{config}|{mode}|{protocol}|lanes={lanes}|tile_rows={tile_rows or 0}"
+def traffic_key(config, mode, protocol, lanes, tile_rows, tile_box=None):
+    key = f"{config}|{mode}|{protocol}|lanes={lanes}|tile_rows={tile_rows or 0}"
+    if tile_box:
+        key += "|box=" + "x".join(str(extent) for extent in tile_box)
+    return key
 
 
 def measured_traffic(key):
@@ -121,6 +125,11 @@ def build_solver(work, args, config):
         options["tile_rows"] = args.tile_rows or None
     if args.tile_positions:
         options["tile_positions"] = args.tile_positions
+    if args.tile_box:
+        options["tile_box"] = (
+            None if args.tile_box == "none" else "auto"
+            if args.tile_box == "auto"
+            else tuple(int(extent) for extent in args.tile_box.split("x")))
     if args.segment_capacity:
         options["segment_capacity"] = args.segment_capacity
     if args.no_queue_loads:
@@ -298,6 +307,8 @@ def run_configuration(config, args, device, steps, warmup, handoff_s,
             "thread_unroll": schedule.thread_unroll,
             "dependence_protocol": lowering.dependence_protocol,
             "tile_rows": tile_rows,
+            "tile_box": (list(plan.tile_boxes[1])
+                         if getattr(plan, "tile_boxes", None) else None),
             "replayed_from_graph": not args.no_graph,
         },
         "roofline_pct": round(100.0 * gbps / HBM_PEAK_GBPS, 3),
@@ -354,7 +365,9 @@ def run_configuration(config, args, device, steps, warmup, handoff_s,
     achieved = bytes_per_launch / (kernel_ms * 1e-3) / 1e9
     key = traffic_key(config, schedule.execution_mode,
                       lowering.dependence_protocol, lowering.task_lanes,
-                      tile_rows)
+                      tile_rows,
+                      plan.tile_boxes[1] if getattr(plan, "tile_boxes", None)
+                      else None)
     record["roofline"] = {
         "bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBPS,
         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 6),
@@ -422,6 +435,9 @@ def main():
                         default=None,
                         help="tiled published pull (ILU0): entries of the "
                              "publication buffer a tile mirrors in LDS")
+    parser.add_argument("--tile-box", dest="tile_box", default=None,
+                        help="tiles over boxes of a structured grid: "
+                             "'auto', 'none' or extents as 32x8x16")
     parser.add_argument("--segment-capacity", dest="segment_capacity",
                         type=int, default=None,
                         help="entries of a task's own segment staged in LDS")
@@ -502,7 +518,7 @@ def main():
         for name in ("mode", "tpb", "lanes", "unroll", "protocol",
                      "waves_per_cu", "spin_sleep", "tile_rows",
                      "plain_first", "look_ahead", "tile_positions",
-                     "segment_capacity"):
+                     "segment_capacity", "tile_box"):
             setattr(sub_args, name, None)
         for name in ("slots", "no_queue_loads", "no_publish", "no_pipeline",
                      "no_graph"):

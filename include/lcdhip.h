@@ -254,7 +254,9 @@ typedef struct {
 #define LCDHIP_DAG_REC_IN 15        /* 2 n: in_ptr[v], in_ptr[v + 1] of task q */
 #define LCDHIP_DAG_REC_SRC 16       /* n * lanes: in_src of its first edges */
 #define LCDHIP_DAG_REC_POS 17       /* n * lanes: in_pos of its first edges */
-#define LCDHIP_DAG_ARRAYS 18
+/* After lcdhip_dag_tile_order / lcdhip_dag_box_order: */
+#define LCDHIP_DAG_TILE_POS 18      /* n: position of every node in TILE_NODES */
+#define LCDHIP_DAG_ARRAYS 19
 
 int lcdhip_dag_build(const lcdhip_dag_rule *rules, int rule_count, int64_t n,
                      uint32_t flags, lcdhip_stream stream, lcdhip_dag **out);
@@ -275,18 +277,48 @@ int lcdhip_dag_band_chains(lcdhip_dag *dag, int64_t band_width,
  * Needs LCDHIP_DAG_LEVELS and level sets that cover every node. */
 int lcdhip_dag_tile_order(lcdhip_dag *dag, int64_t tile_rows,
                           lcdhip_stream stream);
+/* Task order of the tiled persistent executor over boxes of a structured grid
+ * (no counterpart in the reference): node id = x + grid[0] * (y + grid[1] * z);
+ * the nodes of one box of box[0] x box[1] x box[2] grid points are listed
+ * together, boxes in (z, y, x) order, inside a box in (level, id) order.  The
+ * executor cuts the list into tiles of box[0] * box[1] * box[2] positions, so
+ * with extents that divide the grid a tile is a box, and the hand-offs along
+ * all three axes stay inside a workgroup except at box faces (consecutive ids
+ * keep one axis at most).  Builds TILE_NODES and TILE_POS.  The list must be a
+ * topological order for the executor to finish: lcdhip_dag_task_records with
+ * LCDHIP_RECORDS_TILE_POSITIONS checks that and fails otherwise (any stencil
+ * whose edges go from a lower to a higher id in natural order passes).
+ * grid[0] * grid[1] * grid[2] must equal n. */
+int lcdhip_dag_box_order(lcdhip_dag *dag, const int64_t grid[3],
+                         const int64_t box[3], lcdhip_stream stream);
+/* The distinct values of (destination - source) over the unique edges,
+ * ascending, with the number of edges of each: what tells a structured grid
+ * in natural order (a 7-point stencil has the offsets 1, nx, nx * ny) from a
+ * general matrix.  Up to `capacity` values are written to the host arrays;
+ * *distinct_out receives how many there are.  (Decision input of this
+ * backend's scheduler; no counterpart in the reference.) */
+int lcdhip_dag_edge_offsets(const lcdhip_dag *dag, int64_t capacity,
+                            int64_t *offsets_out, int64_t *counts_out,
+                            int64_t *distinct_out, lcdhip_stream stream);
 /* Number of (unique) edges whose two endpoints lie in the same tile of
  * tile_rows consecutive ids: the share of hand-offs a tiled executor keeps
  * inside a workgroup.  (Decision input of this backend's scheduler; no
  * counterpart in the reference.) */
 int lcdhip_dag_tile_locality(const lcdhip_dag *dag, int64_t tile_rows,
                              lcdhip_stream stream, int64_t *local_edges_out);
+#define LCDHIP_RECORDS_LEVEL_ORDER 0     /* tasks in WAVEFRONTS order */
+#define LCDHIP_RECORDS_TILE_ORDER 1      /* tasks in TILE_NODES order */
+#define LCDHIP_RECORDS_TILE_POSITIONS 2  /* the same, sources as positions */
 /* Fixed-size records of the incoming listing in the order the persistent
- * executor visits the tasks (tiled != 0: TILE_NODES, which
- * lcdhip_dag_tile_order must have built; else WAVEFRONTS): for the task at
- * position q, REC_IN holds its range of the
+ * executor visits the tasks (`tiled` is one of LCDHIP_RECORDS_*; the tile
+ * orders need lcdhip_dag_tile_order or lcdhip_dag_box_order first): for the
+ * task at position q, REC_IN holds its range of the
  * incoming listing and REC_SRC / REC_POS[q * lanes + l] the source and the
- * position of its l-th incoming edge (0 beyond its in-degree).  A wavefront
+ * position of its l-th incoming edge (0 beyond its in-degree).  With
+ * LCDHIP_RECORDS_TILE_POSITIONS a source is named by its position in
+ * TILE_NODES instead of its id (tiles that do not follow the ids address their
+ * LDS copy that way), and the call fails when a source does not come before
+ * its consumer in that order.  A wavefront
  * then fetches everything its tasks need to start polling with loads whose
  * addresses depend on q alone.  *overflow_tasks_out (may be NULL) receives
  * the number of tasks with more than `lanes` incoming edges, whose further

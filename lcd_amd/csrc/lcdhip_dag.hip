@@ -306,6 +306,46 @@ __global__ void tile_keys_kernel(const int32_t *__restrict__ wavefronts,
         keys[p] = static_cast<uint32_t>(wavefronts[p] / tile_rows);
 }
 
+// box of a structured grid that holds the node id = x + nx * (y + ny * z);
+// boxes are numbered in (z, y, x) order
+__global__ void box_keys_kernel(const int32_t *__restrict__ wavefronts,
+                                int64_t n, int32_t nx, int32_t ny,
+                                int32_t bx, int32_t by, int32_t bz,
+                                int32_t boxes_x, int32_t boxes_y,
+                                uint32_t *__restrict__ keys)
+{
+    int64_t p = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (p >= n)
+        return;
+    const int32_t id = wavefronts[p];
+    const int32_t x = id % nx, rest = id / nx;
+    const int32_t y = rest % ny, z = rest / ny;
+    keys[p] = static_cast<uint32_t>(((z / bz) * boxes_y + y / by) * boxes_x +
+                                    x / bx);
+}
+
+__global__ void inverse_order_kernel(const int32_t *__restrict__ order,
+                                     int64_t n, int32_t *__restrict__ position)
+{
+    int64_t q = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (q < n)
+        position[order[q]] = static_cast<int32_t>(q);
+}
+
+// destination - source of every unique edge, biased so that unsigned order is
+// signed order
+__global__ void edge_offsets_kernel(const int32_t *__restrict__ dag_ptr,
+                                    const int32_t *__restrict__ dag_index,
+                                    int64_t n, uint32_t *__restrict__ offsets)
+{
+    int64_t u = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (u >= n)
+        return;
+    for (int32_t e = dag_ptr[u]; e < dag_ptr[u + 1]; ++e)
+        offsets[e] = static_cast<uint32_t>(dag_index[e] - static_cast<int32_t>(u)) +
+                     0x80000000u;
+}
+
 __global__ void low_words_kernel(const unsigned long long *__restrict__ keys,
                                  int64_t count, int32_t *__restrict__ out)
 {
@@ -1157,38 +1197,30 @@ extern "C" int lcdhip_dag_tile_locality(const lcdhip_dag *dag, int64_t tile_rows
     return LCDHIP_OK;
 }
 
-extern "C" int lcdhip_dag_tile_order(lcdhip_dag *dag, int64_t tile_rows,
-                                     lcdhip_stream stream_handle)
+namespace {
+
+void dag_release(lcdhip_dag *dag, int which)
 {
-    LCDHIP_REQUIRE_INIT();
-    if (!dag || tile_rows <= 0 || tile_rows > 0x7fffffff) {
-        set_error("The tile size must be a positive integer.");
-        return LCDHIP_ERR_ARGUMENT;
+    if (dag->arrays[which]) {
+        (void)hipFree(dag->arrays[which]);
+        dag->arrays[which] = nullptr;
+        dag->counts[which] = 0;
     }
-    if (!dag->arrays[LCDHIP_DAG_WAVEFRONTS] ||
-        dag->info.scheduled != dag->info.n) {
-        set_error("tiles need level sets that cover every node");
-        return LCDHIP_ERR_ARGUMENT;
-    }
-    hipStream_t stream = resolve_stream(stream_handle);
+}
+
+// TILE_NODES = the level-ordered node list sorted (stably) by `keys`, one key
+// per position of WAVEFRONTS; TILE_POS = its inverse.
+int tile_order_from_keys(lcdhip_dag *dag, Scratch &scratch, uint32_t *keys,
+                         uint64_t key_count, hipStream_t stream)
+{
     const int64_t n = dag->info.n;
-    if (dag->arrays[LCDHIP_DAG_TILE_NODES]) {
-        (void)hipFree(dag->arrays[LCDHIP_DAG_TILE_NODES]);
-        dag->arrays[LCDHIP_DAG_TILE_NODES] = nullptr;
-    }
     int status;
     if ((status = dag_alloc(dag, LCDHIP_DAG_TILE_NODES, n))) return status;
-    if (n == 0)
-        return LCDHIP_OK;
-    Scratch scratch;
-    uint32_t *keys = nullptr, *sorted_keys = nullptr;
-    LCDHIP_CHECK(scratch.alloc(&keys, n));
+    if ((status = dag_alloc(dag, LCDHIP_DAG_TILE_POS, n))) return status;
+    uint32_t *sorted_keys = nullptr;
     LCDHIP_CHECK(scratch.alloc(&sorted_keys, n));
-    hipLaunchKernelGGL(tile_keys_kernel, dim3(blocks_for(n)), dim3(kBlock), 0,
-                       stream, dag->arrays[LCDHIP_DAG_WAVEFRONTS], n,
-                       static_cast<int32_t>(tile_rows), keys);
     // stable: inside a tile the (level, id) order of the level sets stays
-    const int end_bit = bits_for(static_cast<uint64_t>((n + tile_rows - 1) / tile_rows));
+    const int end_bit = bits_for(key_count);
     size_t sort_bytes = 0;
     char *sort_temp = nullptr;
     LCDHIP_CHECK(rocprim::radix_sort_pairs(
@@ -1200,8 +1232,172 @@ extern "C" int lcdhip_dag_tile_order(lcdhip_dag *dag, int64_t tile_rows,
         sort_temp, sort_bytes, keys, sorted_keys,
         dag->arrays[LCDHIP_DAG_WAVEFRONTS], dag->arrays[LCDHIP_DAG_TILE_NODES],
         static_cast<size_t>(n), 0, end_bit, stream));
+    hipLaunchKernelGGL(inverse_order_kernel, dim3(blocks_for(n)), dim3(kBlock),
+                       0, stream, dag->arrays[LCDHIP_DAG_TILE_NODES], n,
+                       dag->arrays[LCDHIP_DAG_TILE_POS]);
     LCDHIP_CHECK(hipGetLastError());
     LCDHIP_CHECK(hipStreamSynchronize(stream));
+    return LCDHIP_OK;
+}
+
+int tile_order_ready(lcdhip_dag *dag)
+{
+    if (!dag->arrays[LCDHIP_DAG_WAVEFRONTS] ||
+        dag->info.scheduled != dag->info.n) {
+        set_error("tiles need level sets that cover every node");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    dag_release(dag, LCDHIP_DAG_TILE_NODES);
+    dag_release(dag, LCDHIP_DAG_TILE_POS);
+    return LCDHIP_OK;
+}
+
+}
+
+extern "C" int lcdhip_dag_tile_order(lcdhip_dag *dag, int64_t tile_rows,
+                                     lcdhip_stream stream_handle)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (!dag || tile_rows <= 0 || tile_rows > 0x7fffffff) {
+        set_error("The tile size must be a positive integer.");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    int status;
+    if ((status = tile_order_ready(dag))) return status;
+    hipStream_t stream = resolve_stream(stream_handle);
+    const int64_t n = dag->info.n;
+    if (n == 0) {
+        if ((status = dag_alloc(dag, LCDHIP_DAG_TILE_NODES, 0))) return status;
+        return dag_alloc(dag, LCDHIP_DAG_TILE_POS, 0);
+    }
+    Scratch scratch;
+    uint32_t *keys = nullptr;
+    LCDHIP_CHECK(scratch.alloc(&keys, n));
+    hipLaunchKernelGGL(tile_keys_kernel, dim3(blocks_for(n)), dim3(kBlock), 0,
+                       stream, dag->arrays[LCDHIP_DAG_WAVEFRONTS], n,
+                       static_cast<int32_t>(tile_rows), keys);
+    return tile_order_from_keys(
+        dag, scratch, keys,
+        static_cast<uint64_t>((n + tile_rows - 1) / tile_rows), stream);
+}
+
+extern "C" int lcdhip_dag_box_order(lcdhip_dag *dag, const int64_t grid[3],
+                                    const int64_t box[3],
+                                    lcdhip_stream stream_handle)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (!dag || !grid || !box) {
+        set_error("dag/grid/box must not be NULL");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    const int64_t n = dag->info.n;
+    int64_t boxes[3];
+    for (int axis = 0; axis < 3; ++axis) {
+        if (grid[axis] <= 0 || box[axis] <= 0 || grid[axis] > 0x7fffffff ||
+            box[axis] > 0x7fffffff) {
+            set_error("grid and box extents must be positive 32-bit integers");
+            return LCDHIP_ERR_ARGUMENT;
+        }
+        boxes[axis] = (grid[axis] + box[axis] - 1) / box[axis];
+    }
+    // (division, not the product: the product of three extents can overflow)
+    if (n % grid[0] || (n / grid[0]) % grid[1] ||
+        n / grid[0] / grid[1] != grid[2]) {
+        set_error("a grid of %lld x %lld x %lld points does not have %lld nodes",
+                  static_cast<long long>(grid[0]), static_cast<long long>(grid[1]),
+                  static_cast<long long>(grid[2]), static_cast<long long>(n));
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    int status;
+    if ((status = tile_order_ready(dag))) return status;
+    hipStream_t stream = resolve_stream(stream_handle);
+    if (n == 0) {
+        if ((status = dag_alloc(dag, LCDHIP_DAG_TILE_NODES, 0))) return status;
+        return dag_alloc(dag, LCDHIP_DAG_TILE_POS, 0);
+    }
+    Scratch scratch;
+    uint32_t *keys = nullptr;
+    LCDHIP_CHECK(scratch.alloc(&keys, n));
+    hipLaunchKernelGGL(box_keys_kernel, dim3(blocks_for(n)), dim3(kBlock), 0,
+                       stream, dag->arrays[LCDHIP_DAG_WAVEFRONTS], n,
+                       static_cast<int32_t>(grid[0]), static_cast<int32_t>(grid[1]),
+                       static_cast<int32_t>(box[0]), static_cast<int32_t>(box[1]),
+                       static_cast<int32_t>(box[2]),
+                       static_cast<int32_t>(boxes[0]), static_cast<int32_t>(boxes[1]),
+                       keys);
+    // n nodes make at most n boxes
+    return tile_order_from_keys(
+        dag, scratch, keys,
+        static_cast<uint64_t>(boxes[0] * boxes[1] * boxes[2]), stream);
+}
+
+extern "C" int lcdhip_dag_edge_offsets(const lcdhip_dag *dag, int64_t capacity,
+                                       int64_t *offsets_out, int64_t *counts_out,
+                                       int64_t *distinct_out,
+                                       lcdhip_stream stream_handle)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (!dag || capacity < 0 || !distinct_out ||
+        (capacity > 0 && (!offsets_out || !counts_out))) {
+        set_error("bad argument to lcdhip_dag_edge_offsets");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    hipStream_t stream = resolve_stream(stream_handle);
+    const int64_t n = dag->info.n, edges = dag->info.edges;
+    *distinct_out = 0;
+    if (n == 0 || edges == 0)
+        return LCDHIP_OK;
+    if (edges > 0xffffffffll) {
+        set_error("edge offsets of more than 2^32 edges");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    Scratch scratch;
+    uint32_t *offsets = nullptr, *sorted = nullptr, *unique = nullptr,
+             *counts = nullptr, *runs = nullptr;
+    LCDHIP_CHECK(scratch.alloc(&offsets, edges));
+    LCDHIP_CHECK(scratch.alloc(&sorted, edges));
+    LCDHIP_CHECK(scratch.alloc(&unique, edges));
+    LCDHIP_CHECK(scratch.alloc(&counts, edges));
+    LCDHIP_CHECK(scratch.alloc(&runs, 1));
+    hipLaunchKernelGGL(edge_offsets_kernel, dim3(blocks_for(n)), dim3(kBlock), 0,
+                       stream, dag->arrays[LCDHIP_DAG_PTR],
+                       dag->arrays[LCDHIP_DAG_INDEX], n, offsets);
+    size_t bytes = 0;
+    char *temp = nullptr;
+    LCDHIP_CHECK(rocprim::radix_sort_keys(nullptr, bytes, offsets, sorted,
+                                          static_cast<size_t>(edges), 0, 32,
+                                          stream));
+    LCDHIP_CHECK(scratch.alloc(&temp, bytes));
+    LCDHIP_CHECK(rocprim::radix_sort_keys(temp, bytes, offsets, sorted,
+                                          static_cast<size_t>(edges), 0, 32,
+                                          stream));
+    size_t rle_bytes = 0;
+    char *rle_temp = nullptr;
+    LCDHIP_CHECK(rocprim::run_length_encode(
+        nullptr, rle_bytes, sorted, static_cast<unsigned int>(edges), unique,
+        counts, runs, stream));
+    LCDHIP_CHECK(scratch.alloc(&rle_temp, rle_bytes));
+    LCDHIP_CHECK(rocprim::run_length_encode(
+        rle_temp, rle_bytes, sorted, static_cast<unsigned int>(edges), unique,
+        counts, runs, stream));
+    LCDHIP_CHECK(hipGetLastError());
+    uint32_t distinct = 0;
+    LCDHIP_CHECK(hipMemcpyAsync(&distinct, runs, 4, hipMemcpyDeviceToHost,
+                                stream));
+    LCDHIP_CHECK(hipStreamSynchronize(stream));
+    *distinct_out = distinct;
+    const int64_t take = std::min<int64_t>(capacity, distinct);
+    if (take > 0) {
+        std::vector<uint32_t> host_unique(take), host_counts(take);
+        LCDHIP_CHECK(hipMemcpy(host_unique.data(), unique, take * 4,
+                               hipMemcpyDeviceToHost));
+        LCDHIP_CHECK(hipMemcpy(host_counts.data(), counts, take * 4,
+                               hipMemcpyDeviceToHost));
+        for (int64_t k = 0; k < take; ++k) {
+            offsets_out[k] = static_cast<int64_t>(host_unique[k]) - 0x80000000ll;
+            counts_out[k] = host_counts[k];
+        }
+    }
     return LCDHIP_OK;
 }
 
@@ -1211,6 +1407,7 @@ __global__ void task_records_kernel(const int32_t *__restrict__ order,
                                     const int32_t *__restrict__ in_ptr,
                                     const int32_t *__restrict__ in_src,
                                     const int32_t *__restrict__ in_pos,
+                                    const int32_t *__restrict__ position,
                                     int64_t n, int lanes,
                                     int32_t *__restrict__ rec_in,
                                     int32_t *__restrict__ rec_src,
@@ -1231,7 +1428,19 @@ __global__ void task_records_kernel(const int32_t *__restrict__ order,
             atomicAdd(overflow, 1ull);
     }
     const bool has = begin + lane < end;
-    rec_src[slot] = has ? in_src[begin + lane] : 0;
+    int32_t source = has ? in_src[begin + lane] : 0;
+    if (position) {
+        // sources by their place in the task order; one that does not come
+        // before its consumer would be waited for by a tile that runs first
+        source = has ? position[source] : 0;
+        if (has && source >= q)
+            atomicAdd(overflow + 1, 1ull);
+        if (lane == 0)
+            for (int32_t e = begin + lanes; e < end; ++e)
+                if (position[in_src[e]] >= q)
+                    atomicAdd(overflow + 1, 1ull);
+    }
+    rec_src[slot] = source;
     rec_pos[slot] = has ? in_pos[begin + lane] : 0;
 }
 
@@ -1242,14 +1451,19 @@ extern "C" int lcdhip_dag_task_records(lcdhip_dag *dag, int lanes, int tiled,
                                        int64_t *overflow_tasks_out)
 {
     LCDHIP_REQUIRE_INIT();
-    if (!dag || lanes < 1 || lanes > 64) {
-        set_error("task records need a dag and 1 to 64 lanes per task");
+    if (!dag || lanes < 1 || lanes > 64 || tiled < LCDHIP_RECORDS_LEVEL_ORDER ||
+        tiled > LCDHIP_RECORDS_TILE_POSITIONS) {
+        set_error("task records need a dag, 1 to 64 lanes per task and one of "
+                  "the LCDHIP_RECORDS_* orders");
         return LCDHIP_ERR_ARGUMENT;
     }
     const int32_t *order = dag->arrays[tiled ? LCDHIP_DAG_TILE_NODES
                                              : LCDHIP_DAG_WAVEFRONTS];
+    const int32_t *position = tiled == LCDHIP_RECORDS_TILE_POSITIONS
+                                  ? dag->arrays[LCDHIP_DAG_TILE_POS] : nullptr;
     if (!order || dag->info.scheduled != dag->info.n ||
-        !dag->arrays[LCDHIP_DAG_IN_PTR]) {
+        !dag->arrays[LCDHIP_DAG_IN_PTR] ||
+        (tiled == LCDHIP_RECORDS_TILE_POSITIONS && !position)) {
         set_error("task records need level sets that cover every node, the "
                   "incoming listing and, when tiled, the tile order");
         return LCDHIP_ERR_ARGUMENT;
@@ -1262,10 +1476,7 @@ extern "C" int lcdhip_dag_task_records(lcdhip_dag *dag, int lanes, int tiled,
         return LCDHIP_ERR_ARGUMENT;
     }
     for (int which : {LCDHIP_DAG_REC_IN, LCDHIP_DAG_REC_SRC, LCDHIP_DAG_REC_POS})
-        if (dag->arrays[which]) {
-            (void)hipFree(dag->arrays[which]);
-            dag->arrays[which] = nullptr;
-        }
+        dag_release(dag, which);
     int status;
     if ((status = dag_alloc(dag, LCDHIP_DAG_REC_IN, 2 * n))) return status;
     if ((status = dag_alloc(dag, LCDHIP_DAG_REC_SRC, n * lanes))) return status;
@@ -1276,23 +1487,31 @@ extern "C" int lcdhip_dag_task_records(lcdhip_dag *dag, int lanes, int tiled,
         return LCDHIP_OK;
     Scratch scratch;
     unsigned long long *d_overflow = nullptr;
-    LCDHIP_CHECK(scratch.alloc(&d_overflow, 1));
-    LCDHIP_CHECK(hipMemsetAsync(d_overflow, 0, 8, stream));
+    LCDHIP_CHECK(scratch.alloc(&d_overflow, 2));
+    LCDHIP_CHECK(hipMemsetAsync(d_overflow, 0, 16, stream));
     hipLaunchKernelGGL(task_records_kernel, dim3(blocks_for(n * lanes)),
                        dim3(kBlock), 0, stream, order,
                        dag->arrays[LCDHIP_DAG_IN_PTR],
                        dag->arrays[LCDHIP_DAG_IN_SRC],
-                       dag->arrays[LCDHIP_DAG_IN_POS], n, lanes,
+                       dag->arrays[LCDHIP_DAG_IN_POS], position, n, lanes,
                        dag->arrays[LCDHIP_DAG_REC_IN],
                        dag->arrays[LCDHIP_DAG_REC_SRC],
                        dag->arrays[LCDHIP_DAG_REC_POS], d_overflow);
     LCDHIP_CHECK(hipGetLastError());
-    unsigned long long overflow = 0;
-    LCDHIP_CHECK(hipMemcpyAsync(&overflow, d_overflow, 8, hipMemcpyDeviceToHost,
+    unsigned long long overflow[2] = {0, 0};
+    LCDHIP_CHECK(hipMemcpyAsync(overflow, d_overflow, 16, hipMemcpyDeviceToHost,
                                 stream));
     LCDHIP_CHECK(hipStreamSynchronize(stream));
+    if (overflow[1]) {
+        for (int which : {LCDHIP_DAG_REC_IN, LCDHIP_DAG_REC_SRC, LCDHIP_DAG_REC_POS})
+            dag_release(dag, which);
+        set_error("the tile order is not a topological order: %llu edges come "
+                  "from a later position",
+                  static_cast<unsigned long long>(overflow[1]));
+        return LCDHIP_ERR_ARGUMENT;
+    }
     if (overflow_tasks_out)
-        *overflow_tasks_out = static_cast<int64_t>(overflow);
+        *overflow_tasks_out = static_cast<int64_t>(overflow[0]);
     return LCDHIP_OK;
 }
 

@@ -253,7 +253,8 @@ def band_chains(nodes, level_ptr, dag_ptr, dag_index, band_width):
 
 def execution_data_from_device_dag(dag, execution_mode, warp_mapped,
                                    pushed=False, band_width=1, mailbox=False,
-                                   tile_rows=None, record_lanes=None):
+                                   tile_rows=None, record_lanes=None,
+                                   tile_boxes=None):
     """Executor arrays straight from the on-device inspector (no host copy
     except the level offsets the launcher iterates over)."""
     if not isinstance(band_width, int) or band_width <= 0:
@@ -284,7 +285,17 @@ def execution_data_from_device_dag(dag, execution_mode, warp_mapped,
             raise DAGPreprocessingError(
                 "The tiled executor needs every edge to go from a lower to a "
                 "higher node id.")
-        task_nodes = dag.tile_order(int(tile_rows))
+        if tile_boxes is not None:
+            # boxes of a structured grid; sources by their place in the queue
+            grid, box = tile_boxes
+            if not (mailbox and record_lanes) or (
+                    int(np.prod(box)) != int(tile_rows)):
+                raise DAGPreprocessingError(
+                    "Box tiles need the mailbox protocol with task records "
+                    "and tile_rows equal to the points of a box.")
+            task_nodes = dag.box_order(grid, box)
+        else:
+            task_nodes = dag.tile_order(int(tile_rows))
     if mailbox:
         # destination v reads message slots in_ptr[v] .. in_ptr[v+1); the
         # entry at position p writes slot out_slot[p]; slot k carries the
@@ -296,8 +307,9 @@ def execution_data_from_device_dag(dag, execution_mode, warp_mapped,
         if record_lanes:
             # the first `record_lanes` incoming edges of every task, in the
             # order the executor visits the tasks
-            records = dag.task_records(int(record_lanes),
-                                       tiled=bool(tile_rows))
+            records = dag.task_records(
+                int(record_lanes),
+                tiled=(2 if tile_boxes is not None else bool(tile_rows)))
             auxiliary.update(zip(
                 ("_lcd_rec_in", "_lcd_rec_src", "_lcd_rec_pos"), records))
         return WarpTaskExecutionData(

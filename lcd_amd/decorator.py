@@ -43,6 +43,7 @@ from lcd_amd.dag_preprocessing import (
     execution_data_from_device_dag,
 )
 from lcd_amd.dependence import DependenceAnalysis, analyze_dependences
+from lcd_amd.hip_emitter import HIPLoweringError
 from lcd_amd.hip_lowering import lower_to_hip
 from lcd_amd.hip_runtime import (
     compile_hip_module,
@@ -57,7 +58,9 @@ from lcd_amd.scheduler import (
     AnalyticScheduler,
     CalibratedScheduler,
     SchedulePlan,
+    automatic_tile_box,
     automatic_tile_rows,
+    structured_grid,
     automatic_tile_threads,
     ScheduleSpace,
     count_inner_loop_flops,
@@ -190,9 +193,19 @@ def parallel(**kwargs):
             raise ValueError(
                 "tile_rows must be None, 'auto' or a positive integer.")
 
+        tile_box_option = kwargs.get("tile_box", "auto")
+        if not (tile_box_option in (None, "auto") or (
+                isinstance(tile_box_option, (tuple, list))
+                and len(tile_box_option) == 3
+                and all(isinstance(extent, int) and extent > 0
+                        for extent in tile_box_option))):
+            raise ValueError(
+                "tile_box must be None, 'auto' or three positive integers.")
+
         def lower_variant(lowering_key, tile_rows=None, single_chunk=False,
-                          task_records=True):
-            variant_key = (lowering_key, tile_rows, single_chunk, task_records)
+                          task_records=True, by_position=False):
+            variant_key = (lowering_key, tile_rows, single_chunk, task_records,
+                           by_position)
             if variant_key not in lowered_variants:
                 (mode, threads_per_block, unroll, n_warp, protocol,
                  task_lanes) = lowering_key
@@ -232,16 +245,18 @@ def parallel(**kwargs):
                     segment_capacity=kwargs.get("segment_capacity"),
                     pipeline_fetch=kwargs.get("pipeline_fetch", True),
                     tile_positions=kwargs.get("tile_positions"),
+                    tile_by_position=by_position,
                     full_fences=kwargs.get("full_fences", False),
                     dynamic_fetch=kwargs.get("dynamic_fetch", False),
                 )
             return lowered_variants[variant_key]
 
         def compile_variant(lowering_key, tile_rows=None, single_chunk=False,
-                            task_records=True):
+                            task_records=True, by_position=False):
             lowering = lower_variant(lowering_key, tile_rows, single_chunk,
-                                     task_records)
-            variant_key = (lowering_key, tile_rows, single_chunk, task_records)
+                                     task_records, by_position)
+            variant_key = (lowering_key, tile_rows, single_chunk, task_records,
+                           by_position)
             if variant_key not in compiled_variants:
                 compiled_variants[variant_key] = compile_hip_module(
                     lowering, function_globals=function.__globals__)
@@ -273,6 +288,31 @@ def parallel(**kwargs):
                 # threads, 38 ms at the sizes chosen for SpTRSV): by request
                 return schedule, None
             return tiled, rows
+
+        def boxes_for(dag, schedule, rows):
+            """(grid, box) when the tiles of this plan are boxes of a
+            structured grid: asked for with ``tile_box``, the grid given as
+            ``tile_grid`` or recognised from the DAG's edge offsets."""
+            if not rows or tile_box_option is None:
+                return None
+            grid = kwargs.get("tile_grid") or structured_grid(dag)
+            if grid is None:
+                return None
+            grid = tuple(int(extent) for extent in grid)
+            box = (automatic_tile_box(grid, rows) if tile_box_option == "auto"
+                   else tuple(tile_box_option))
+            if box is None:
+                return None
+            points = box[0] * box[1] * box[2]
+            try:
+                variant = lower_variant(schedule.lowering_key, points, True,
+                                        True, True)
+            except HIPLoweringError:
+                return None
+            if not variant.tile_by_position or (
+                    dag.n * variant.task_record_lanes >= 2 ** 31):
+                return None
+            return grid, box
 
         host_lowering = lower_variant(
             ScheduleSpace.from_options(**space_options).configurations()[0])
@@ -423,13 +463,35 @@ def parallel(**kwargs):
             if not records:
                 lowering = lower_variant(schedule.lowering_key, tile_rows,
                                          task_records=False)
-            execution_data = execution_data_from_device_dag(
-                dag, schedule.execution_mode, lowering.warp_mapped,
-                pushed=lowering.dependence_protocol == PUSH_DEPENDENCE,
-                band_width=band_width,
-                mailbox=lowering.dependence_protocol == MAILBOX_DEPENDENCE,
-                tile_rows=lowering.tile_rows,
-                record_lanes=lowering.task_record_lanes)
+            execution_data, tile_boxes = None, boxes_for(dag, schedule,
+                                                         tile_rows)
+            if tile_boxes is not None:
+                # a box order that is not topological, or a task with more
+                # incoming edges than its record holds: tiles of consecutive
+                # ids instead
+                points = int(np.prod(tile_boxes[1]))
+                try:
+                    execution_data = execution_data_from_device_dag(
+                        dag, schedule.execution_mode, lowering.warp_mapped,
+                        band_width=band_width, mailbox=True, tile_rows=points,
+                        record_lanes=lowering.task_record_lanes,
+                        tile_boxes=tile_boxes)
+                except hip_runtime.HIPRuntimeError:
+                    execution_data = None
+                if execution_data is None or dag.record_overflow:
+                    execution_data = tile_boxes = None
+                else:
+                    tile_rows = points
+                    lowering = lower_variant(schedule.lowering_key, points,
+                                             True, True, True)
+            if execution_data is None:
+                execution_data = execution_data_from_device_dag(
+                    dag, schedule.execution_mode, lowering.warp_mapped,
+                    pushed=lowering.dependence_protocol == PUSH_DEPENDENCE,
+                    band_width=band_width,
+                    mailbox=lowering.dependence_protocol == MAILBOX_DEPENDENCE,
+                    tile_rows=lowering.tile_rows,
+                    record_lanes=lowering.task_record_lanes)
             plan = SchedulePlan(
                 schedule=schedule,
                 execution_data=attach_auxiliary_values(
@@ -439,7 +501,7 @@ def parallel(**kwargs):
                 # variant without the code for further chunks
                 single_chunk=bool(lowering.task_record_lanes)
                 and getattr(dag, "record_overflow", 1) == 0,
-                task_records=records)
+                task_records=records, tile_boxes=tile_boxes)
             plan_state[id(plan)] = {"resident": resident, "workspace": {}}
             return plan
 
@@ -481,7 +543,8 @@ def parallel(**kwargs):
             lowering, compiled = compile_variant(plan.schedule.lowering_key,
                                                  plan.tile_rows,
                                                  plan.single_chunk,
-                                                 plan.task_records)
+                                                 plan.task_records,
+                                                 plan.tile_boxes is not None)
             publish_variant(plan.schedule, lowering, compiled)
             state = plan_state[id(plan)]
             values = dict(argument_values)

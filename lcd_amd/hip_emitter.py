@@ -111,6 +111,9 @@ class HIPLoweringResult:
     # pull protocol without flags: consumers poll the producers' elements of
     # this array, which the reset kernel fills with the empty marker
     value_flag_array: str | None = None
+    # tiled executor whose LDS copy and flag array are indexed by the place
+    # of a task in the queue (tiles that do not follow the ids)
+    tile_by_position: bool = False
     # lifted zero-initialised arrays the executor needs no host-side clear for
     executor_initialised: tuple = ()
     # kernel that gathers position-indexed operands into consumer order at
@@ -459,11 +462,26 @@ class _Emitter:
     def tile_load(self, index_text):
         """Read of the value-flagged array: LDS inside the running tile."""
         array = self.tile["array"]
+        if self.tile.get("by_position"):
+            raise HIPLoweringError(
+                "Tiles addressed by queue position serve tasks that read "
+                f"{array} through the incoming listing only.")
         return (f"lcd_tile_ld({array}, _lcd_tile, _lcd_tile_row0, "
                 f"_lcd_tile_rows, {index_text})")
 
     def store(self, target, value_text):
         element = self.element(target)
+        if (self.tile is not None and target.value.id == self.tile["array"]
+                and self.tile.get("by_position")):
+            # the flag copy (LDS slot and memory) is indexed by the task's
+            # place in the queue; the array itself gets a plain store
+            if self.expr(target.slice) != self.lowerer.loop_iterator:
+                raise HIPLoweringError(
+                    "Tiles addressed by queue position need tasks that "
+                    f"write their own element of {target.value.id} only.")
+            return ("{ lcd_tile_st(_lcd_xq, _lcd_tile, _lcd_tile_row0, "
+                    f"_lcd_tile_rows, (lcd_index_t)_task, {value_text}); "
+                    f"{element} = {value_text}; }}")
         if self.tile is not None and target.value.id == self.tile["array"]:
             return (f"lcd_tile_st({target.value.id}, _lcd_tile, _lcd_tile_row0, "
                     f"_lcd_tile_rows, {self.expr(target.slice)}, {value_text});")

@@ -99,8 +99,10 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                  queue_node_loads=True, plain_first_polls=None,
                  publish_values=True, look_ahead=True, segment_capacity=None,
                  pipeline_fetch=True, full_fences=False,
-                 dynamic_fetch=False, tile_positions=None):
+                 dynamic_fetch=False, tile_positions=None,
+                 tile_by_position=False):
         self.tile_positions = tile_positions
+        self.tile_by_position = tile_by_position
         # full_fences: agent-scope release/acquire fences of the HIP memory
         # model (L2 write-back / invalidate per hand-off) instead of the
         # wait-for-completion scheme; dynamic_fetch: the flat queue hands out
@@ -354,6 +356,8 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
             gather["staged"] = {}
             gather["needs_position"] = True
             gather["records"] = True
+        if self.tile_by_position:
+            self._tile_by_position_plan()
         emitter = _Emitter(kinds, self.reductions, lowered_ids,
                            coherent_arrays=coherent)
         emitter.segment = self._segment
@@ -471,6 +475,8 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
             mailbox_index_array=(self._mailbox["index_array"]
                                  if self._mailbox else None),
             tile_rows=self._tile["rows"] if self._tile else None,
+            tile_by_position=bool(self._tile
+                                  and self._tile.get("by_position")),
             spin_limit=self.spin_limit,
             queue_node_loads=tuple(self._queue_node_loads),
             published_array=(self._published["array"]
@@ -610,6 +616,8 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                 if gather.get("records"):
                     position = names.index("_lcd_in_src") + 1
                     names[position:position] = list(RECORD_ARGUMENTS)
+                if self._tile is not None and self._tile.get("by_position"):
+                    names.append("_lcd_xq")
             elif self.dependence_protocol == MAILBOX_DEPENDENCE:
                 names = list(MAILBOX_ARGUMENTS)
             else:
@@ -825,7 +833,8 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                    written_arrays):
         parts = []
         mutable_executor = {"dep_count", "task_counter", "done",
-                            STATUS_ARGUMENT, "_lcd_mailbox", "_lcd_pub"}
+                            STATUS_ARGUMENT, "_lcd_mailbox", "_lcd_pub",
+                            "_lcd_xq"}
         for name in kernel_arguments:
             if name in array_arguments:
                 const = (name not in written_arrays
@@ -1336,6 +1345,8 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                         and self._mailbox["gather"] is not None)):
                 count_array = "task_nodes"
                 values = ("_lcd_pub" if self._published else
+                          "_lcd_xq" if self._tile is not None
+                          and self._tile.get("by_position") else
                           (self._value_pull or self._mailbox)["array"])
                 reset_args = (f"({values}, task_counter, "
                               f"_hip.length({values}))")
@@ -1417,7 +1428,7 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
                  queue_node_loads=True, plain_first_polls=None,
                  publish_values=True, look_ahead=True, segment_capacity=None,
                  pipeline_fetch=True, full_fences=False, dynamic_fetch=False,
-                 tile_positions=None):
+                 tile_positions=None, tile_by_position=False):
     """HIP counterpart of ``lower_to_numba_cuda``
     (compiler/cuda_lowering.py:2854-2884); same parameters plus
     ``task_lanes`` (lanes cooperating on one task, a power of two <= 64),
@@ -1444,5 +1455,6 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
         plain_first_polls=plain_first_polls, publish_values=publish_values,
         look_ahead=look_ahead, segment_capacity=segment_capacity,
         pipeline_fetch=pipeline_fetch, full_fences=full_fences,
-        dynamic_fetch=dynamic_fetch, tile_positions=tile_positions)
+        dynamic_fetch=dynamic_fetch, tile_positions=tile_positions,
+        tile_by_position=tile_by_position)
     return lowerer.lower(code)

@@ -309,6 +309,14 @@ class ProtocolMixin:
             lines.append(f"{pad}lcd_atomic_sub(&dep_count[{endpoint}], 1);")
         return lines
 
+    def _gather_poll_array(self):
+        """What a consumer polls for a source outside its tile: the array
+        itself, or its copy in queue order when sources are named by their
+        place in the queue."""
+        if self._tile is not None and self._tile.get("by_position"):
+            return "_lcd_xq"
+        return self._mailbox["array"]
+
     def _gather_fetch_lines(self, indent, declare=False, records=False):
         """Position, source and read-only operands of the incoming edge this
         lane handles next (slot ``_mb_next + _lane``); with ``records`` the
@@ -353,7 +361,7 @@ class ProtocolMixin:
                 # loop (128^3 grid: 0.354 -> 0.347 ms)
                 # (with the flat queue every source is outside and mostly not
                 # there yet at that time: 3 % slower, so tiles only)
-                array = self._mailbox["array"]
+                array = self._gather_poll_array()
                 lines.append(f"{pad}double _g_early = lcd_empty();")
                 if self._tile is not None:
                     lines.append(
@@ -455,7 +463,7 @@ class ProtocolMixin:
         grid: 0.347 -> 0.327 ms.)"""
         import re
         gather = self._mailbox["gather"]
-        array = self._mailbox["array"]
+        array = self._gather_poll_array()
         emitter = self._emitter
         split = next(index for index, line in enumerate(fetch)
                      if "for (int _round = 0" in line)
@@ -573,7 +581,7 @@ class ProtocolMixin:
         pad = "    " * indent
         own = self._mailbox["register"]
         gather = self._mailbox["gather"]
-        array = self._mailbox["array"]
+        array = self._gather_poll_array()
         value = self._emitter.expr(gather["value"])
         if gather["negate"]:
             value = f"(-({value}))"

@@ -38,7 +38,9 @@ DAG_PTR, DAG_INDEX, DAG_DEP_COUNT, DAG_EDGE_COUNT = 0, 1, 2, 3
 DAG_LEVEL_OF, DAG_WAVEFRONTS, DAG_WAVEFRONT_PTR = 4, 5, 6
 DAG_IN_PTR, DAG_IN_POS, DAG_OUT_SLOT, DAG_IN_SRC = 7, 8, 9, 10
 DAG_TASK_NODES, DAG_TASK_PTR, DAG_BAND_PTR, DAG_TILE_NODES = 11, 12, 13, 14
-DAG_REC_IN, DAG_REC_SRC, DAG_REC_POS = 15, 16, 17
+DAG_REC_IN, DAG_REC_SRC, DAG_REC_POS, DAG_TILE_POS = 15, 16, 17, 18
+# orders of lcdhip_dag_task_records
+RECORDS_LEVEL_ORDER, RECORDS_TILE_ORDER, RECORDS_TILE_POSITIONS = 0, 1, 2
 DAG_FLAG_LEVELS, DAG_FLAG_FORCE_KAHN, DAG_FLAG_INCOMING = 1, 2, 4
 
 DEVICE_COMPILE_OPTIONS = (
@@ -130,6 +132,7 @@ EXPORTED_SYMBOLS = (
     "lcdhip_dag_build", "lcdhip_dag_get_info", "lcdhip_dag_array",
     "lcdhip_dag_download", "lcdhip_dag_destroy", "lcdhip_dag_band_chains",
     "lcdhip_dag_tile_order", "lcdhip_dag_tile_locality",
+    "lcdhip_dag_box_order", "lcdhip_dag_edge_offsets",
     "lcdhip_dag_task_records",
     "lcdhip_lookup_build", "lcdhip_gather_i32",
     "lcdhip_digest", "lcdhip_digest_noalloc",
@@ -322,7 +325,8 @@ class DeviceDag:
               "in_src": DAG_IN_SRC, "task_nodes": DAG_TASK_NODES,
               "task_ptr": DAG_TASK_PTR, "band_ptr": DAG_BAND_PTR,
               "tile_nodes": DAG_TILE_NODES, "rec_in": DAG_REC_IN,
-              "rec_src": DAG_REC_SRC, "rec_pos": DAG_REC_POS}
+              "rec_src": DAG_REC_SRC, "rec_pos": DAG_REC_POS,
+              "tile_pos": DAG_TILE_POS}
     CHAIN_ARRAYS = ("task_nodes", "task_ptr", "band_ptr")
 
     def __init__(self, device, handle):
@@ -394,18 +398,58 @@ class DeviceDag:
         if not isinstance(tile_rows, int) or tile_rows <= 0:
             raise HIPRuntimeError("The tile size must be a positive integer.",
                                   ERR_ARGUMENT)
-        self._views.pop("tile_nodes", None)
-        self._host.pop("tile_nodes", None)
+        for name in ("tile_nodes", "tile_pos"):
+            self._views.pop(name, None)
+            self._host.pop(name, None)
         _check(load_library().lcdhip_dag_tile_order(
             self.handle, ctypes.c_int64(tile_rows), self.device.stream))
         self.tile_rows = tile_rows
         return self.array("tile_nodes")
 
+    def box_order(self, grid, box):
+        """Order the nodes of a structured grid (id = x + nx * (y + ny * z))
+        by (box, level, id), boxes of ``box`` grid points in (z, y, x) order;
+        afterwards ``tile_nodes`` and ``tile_pos`` (its inverse) are arrays
+        of this DAG."""
+        grid, box = tuple(grid), tuple(box)
+        if len(grid) != 3 or len(box) != 3 or not all(
+                isinstance(extent, (int, np.integer)) and extent > 0
+                for extent in grid + box):
+            raise HIPRuntimeError(
+                "Grid and box are three positive integers each.", ERR_ARGUMENT)
+        for name in ("tile_nodes", "tile_pos"):
+            self._views.pop(name, None)
+            self._host.pop(name, None)
+        extents = ctypes.c_int64 * 3
+        _check(load_library().lcdhip_dag_box_order(
+            self.handle, extents(*map(int, grid)), extents(*map(int, box)),
+            self.device.stream))
+        self.tile_rows = int(box[0]) * int(box[1]) * int(box[2])
+        return self.array("tile_nodes")
+
+    def edge_offsets(self, capacity=16):
+        """``(offsets, counts, distinct)``: the distinct values of
+        destination - source over the edges (the first ``capacity`` of them,
+        ascending), how many edges have each, and how many values there
+        are."""
+        offsets = (ctypes.c_int64 * max(capacity, 1))()
+        counts = (ctypes.c_int64 * max(capacity, 1))()
+        distinct = ctypes.c_int64()
+        _check(load_library().lcdhip_dag_edge_offsets(
+            self.handle, ctypes.c_int64(capacity), offsets, counts,
+            ctypes.byref(distinct), self.device.stream))
+        take = min(capacity, distinct.value)
+        return (list(offsets[:take]), list(counts[:take]),
+                int(distinct.value))
+
     def task_records(self, lanes, tiled=False):
         """Fixed-size records of the incoming listing in task order
         (``tile_nodes`` when ``tiled``, else ``wavefronts``):
         afterwards ``rec_in`` (2 per task), ``rec_src`` and ``rec_pos``
-        (``lanes`` per task) are arrays of this DAG."""
+        (``lanes`` per task) are arrays of this DAG.  ``tiled`` may be
+        ``RECORDS_TILE_POSITIONS``: sources are then named by their position
+        in ``tile_nodes``, and an order that is not topological is an
+        error."""
         if not isinstance(lanes, int) or not 1 <= lanes <= 64:
             raise HIPRuntimeError(
                 "Task records need 1 to 64 lanes per task.", ERR_ARGUMENT)
@@ -414,7 +458,8 @@ class DeviceDag:
             self._host.pop(name, None)
         overflow = ctypes.c_int64()
         _check(load_library().lcdhip_dag_task_records(
-            self.handle, ctypes.c_int(lanes), ctypes.c_int(int(bool(tiled))),
+            self.handle, ctypes.c_int(lanes),
+            ctypes.c_int(int(tiled)),   # False / True / RECORDS_*
             self.device.stream, ctypes.byref(overflow)))
         self.record_lanes = lanes
         # tasks whose incoming edges do not all fit their record
@@ -1087,6 +1132,13 @@ def prepare_hip_arguments(lowering, argument_values, execution_data,
                 cached = device.empty((slots,), np.float64)
                 workspace[("state", "_lcd_pub")] = cached
             host_values["_lcd_pub"] = cached
+        if "_lcd_xq" in lowering.launcher_arguments:
+            # the value-as-flag copy in queue order, one slot per task
+            cached = workspace.get(("state", "_lcd_xq"))
+            if cached is None or len(cached) != max(n_tasks, 1):
+                cached = device.empty((max(n_tasks, 1),), np.float64)
+                workspace[("state", "_lcd_xq")] = cached
+            host_values["_lcd_xq"] = cached
         for name in lowering.launcher_arguments:
             if not name.startswith("_lcd_staged_"):
                 continue

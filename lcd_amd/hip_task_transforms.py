@@ -119,6 +119,28 @@ class TaskTransformMixin:
             return None      # the flat queue serves every other combination
         return {"array": array, "rows": rows}
 
+    def _tile_by_position_plan(self):
+        """Tiles that do not follow the ids (boxes of a grid): a tile is
+        ``tile_rows`` consecutive places of the task queue, whatever ids sit
+        there.  The task records then name a source by its place in the
+        queue, the LDS slot of a source is its place minus the tile's first,
+        and the value-as-flag copy that other tiles poll is a buffer in queue
+        order (``_lcd_xq``); the array itself gets plain stores and needs no
+        reset.  Needs the gathered mailbox with task records that hold every
+        incoming edge, and products that do not use the producer's id."""
+        tile, mailbox = self._tile, self._mailbox
+        gather = mailbox["gather"] if mailbox is not None else None
+        if (tile is None or tile.get("published") or gather is None
+                or not gather.get("records") or not self.single_chunk):
+            return
+        names = set(_names_in(gather["value"]))
+        for _, node, _ in gather["operands"]:
+            names |= set(_names_in(node))
+        if "_g_src" in names:
+            return
+        tile["by_position"] = True
+        self._kinds.arrays["_lcd_xq"] = FLOAT
+
     def _segment_plan(self, body, arguments):
         """In-place updates of the task's own segment ``X[P[i] .. P[i+1])``
         (ILU0 rewrites row ``i`` once per pivot) are staged in LDS: the

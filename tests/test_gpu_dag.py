@@ -264,6 +264,104 @@ def test_task_records(device, oracle, lanes, tile_rows):
         plain.task_records(lanes)          # no incoming listing
 
 
+@pytest.mark.parametrize("grid,box", [((12, 10, 9), (4, 5, 3)),
+                                      ((12, 10, 9), (8, 4, 4)),     # ragged
+                                      ((16, 6, 1), (4, 2, 1)),
+                                      ((7, 5, 3), (7, 5, 3))])
+def test_box_order_and_position_records(device, oracle, grid, box):
+    """Tiles over boxes of a grid: the task order is (box, level, id) with
+    boxes in (z, y, x) order -- restated here with numpy from the level sets
+    -- its inverse, and task records that name sources by their place in that
+    order; every source comes before its consumer."""
+    print("box order", grid, box, flush=True)
+    nx, ny, nz = grid
+    work = workloads.configuration("c2", nx=nx, ny=ny, nz=nz)
+    rule = oracle.rule_sptrsv_csc(work.indptr, work.indices)
+    dag = device.dag_build([rule], work.n, levels=True, incoming=True)
+    with pytest.raises(hip_runtime.HIPRuntimeError):
+        dag.task_records(4, tiled=hip_runtime.RECORDS_TILE_POSITIONS)
+    order = dag.box_order(grid, box).copy_to_host()
+    ids = np.arange(work.n)
+    x, y, z = ids % nx, ids // nx % ny, ids // (nx * ny)
+    boxes_x, boxes_y = -(-nx // box[0]), -(-ny // box[1])
+    box_of = ((z // box[2]) * boxes_y + y // box[1]) * boxes_x + x // box[0]
+    level_of = dag.host("level_of")
+    expected = np.lexsort((ids, level_of, box_of))
+    np.testing.assert_array_equal(order, expected)
+    position = dag.host("tile_pos")
+    np.testing.assert_array_equal(position[order], ids)
+    lanes = 4
+    rec_in, rec_src, rec_pos = (
+        a.copy_to_host() for a in dag.task_records(
+            lanes, tiled=hip_runtime.RECORDS_TILE_POSITIONS))
+    in_ptr, in_src, in_pos = (dag.host(name)
+                              for name in ("in_ptr", "in_src", "in_pos"))
+    expected_src = np.zeros((work.n, lanes), dtype=np.int32)
+    expected_pos = np.zeros((work.n, lanes), dtype=np.int32)
+    for q, node in enumerate(order):
+        count = min(in_ptr[node + 1] - in_ptr[node], lanes)
+        sources = in_src[in_ptr[node]:in_ptr[node] + count]
+        expected_src[q, :count] = position[sources]
+        assert np.all(position[sources] < q)
+        expected_pos[q, :count] = in_pos[in_ptr[node]:in_ptr[node] + count]
+    np.testing.assert_array_equal(rec_src.reshape(-1, lanes), expected_src)
+    np.testing.assert_array_equal(rec_pos.reshape(-1, lanes), expected_pos)
+    assert dag.record_overflow == 0
+    with pytest.raises(hip_runtime.HIPRuntimeError):
+        dag.box_order((nx, ny, nz + 1), box)         # not n nodes
+    with pytest.raises(hip_runtime.HIPRuntimeError):
+        dag.box_order(grid, (0, 1, 1))
+
+
+def test_position_records_refuse_an_order_that_is_not_topological(device,
+                                                                  oracle):
+    """A grid read with the wrong line length: an x step of the real grid
+    then leads from a box to an earlier one, and the records say so instead
+    of leaving an executor to wait for ever."""
+    nx, ny, nz = 8, 4, 3
+    work = workloads.configuration("c2", nx=nx, ny=ny, nz=nz)
+    rule = oracle.rule_sptrsv_csc(work.indptr, work.indices)
+    dag = device.dag_build([rule], work.n, levels=True, incoming=True)
+    # boxes of four consecutive ids: any order by id is topological
+    dag.box_order((nx * ny, nz, 1), (4, 1, 1))
+    dag.task_records(4, tiled=hip_runtime.RECORDS_TILE_POSITIONS)  # still fine
+    # lines of four: the edge 3 -> 4 goes from box 1 back to box 0
+    dag.box_order((4, 2, 12), (2, 2, 1))
+    with pytest.raises(hip_runtime.HIPRuntimeError, match="topological"):
+        dag.task_records(4, tiled=hip_runtime.RECORDS_TILE_POSITIONS)
+
+
+def test_edge_offsets(device, oracle):
+    """destination - source over the unique edges: 1, nx and nx * ny on the
+    7-point grid, with the counts of a full stencil; what the scheduler reads
+    a structured grid from."""
+    from lcd_amd.scheduler import structured_grid
+    nx, ny, nz = 12, 10, 9
+    work = workloads.configuration("c2", nx=nx, ny=ny, nz=nz)
+    rule = oracle.rule_sptrsv_csc(work.indptr, work.indices)
+    dag = device.dag_build([rule], work.n, levels=True)
+    offsets, counts, distinct = dag.edge_offsets(8)
+    assert (offsets, distinct) == ([1, nx, nx * ny], 3)
+    assert counts == [(nx - 1) * ny * nz, nx * (ny - 1) * nz,
+                      nx * ny * (nz - 1)]
+    assert dag.edge_offsets(2) == ([1, nx], counts[:2], 3)
+    assert dag.edge_offsets(0) == ([], [], 3)
+    assert structured_grid(dag) == (nx, ny, nz)
+    # a general matrix: every offset against a numpy histogram
+    work = workloads.configuration("c3", n=500, seed=4)
+    rule = oracle.rule_sptrsv_csr(work.indptr, work.indices)
+    dag = device.dag_build([rule], work.n, levels=True)
+    ptr, index = dag.host("dag_ptr"), dag.host("dag_index")
+    sources = np.repeat(np.arange(work.n), np.diff(ptr))
+    values, expected = np.unique(index - sources, return_counts=True)
+    offsets, counts, distinct = dag.edge_offsets(len(values) + 3)
+    assert distinct == len(values)
+    assert offsets == values.tolist() and counts == expected.tolist()
+    assert structured_grid(dag) is None
+    empty = device.dag_build([], 5, levels=True)
+    assert empty.edge_offsets(4) == ([], [], 0)
+
+
 def test_incoming_positions(device, oracle):
     """Per destination, the positions whose entries produce its edges, by
     (source, position), duplicates kept."""

@@ -132,7 +132,7 @@ def test_tiled_executor(oracle, tile_rows, lanes, tpb):
     csc = sptrsv.compile_sptrsv_csc(
         execution_mode="sync_free", threads_per_block=tpb, task_lanes=lanes,
         thread_unroll=1, dependence_protocol="mailbox", gather_messages=True,
-        tile_rows=tile_rows)
+        tile_rows=tile_rows, tile_box=None)      # tiles of consecutive ids
     assert csr.hip_lowering.tile_rows == tile_rows
     assert csc.hip_lowering.tile_rows == tile_rows
     assert "lcd_tile_ld(x, _lcd_tile" in csr.hip_kernel_source
@@ -165,6 +165,60 @@ def test_tiled_executor(oracle, tile_rows, lanes, tpb):
         execution_mode="sync_free", threads_per_block=128, task_lanes=4,
         thread_unroll=1, dependence_protocol="push", tile_rows=tile_rows)
     assert pushed.hip_lowering.tile_rows is None
+
+
+@pytest.mark.parametrize("box,lanes,tpb", [((8, 4, 4), 4, 128),
+                                           ((20, 3, 2), 4, 64),
+                                           ((5, 5, 5), 8, 256),    # ragged
+                                           ("auto", 4, 256)])
+def test_box_tiles(oracle, box, lanes, tpb):
+    """Tiles over boxes of the grid: the LDS copy and the value-as-flag
+    buffer are addressed by the place of a task in the queue, the result is
+    that of the sequential loop bit for bit; structures that are no grid, or
+    whose tasks have more incoming edges than lanes, keep tiles of
+    consecutive ids."""
+    print("box tiles", box, lanes, tpb, flush=True)
+    csc = sptrsv.compile_sptrsv_csc(
+        execution_mode="sync_free", threads_per_block=tpb, task_lanes=lanes,
+        thread_unroll=1, dependence_protocol="mailbox", tile_rows=256,
+        tile_box=box)
+    for name, overrides, boxed in (
+            ("c2", dict(nx=20, ny=18, nz=16), True),
+            # two axes: a box chosen by the scheduler would be consecutive
+            # lines, which tiles of consecutive ids are already
+            ("c1", {}, box != "auto"),
+            ("c5", dict(n=6000), False)):          # a band, no grid
+        work = workloads.configuration(name, **overrides)
+        expected = oracle.sptrsv_csc(work.indptr, work.indices, work.data,
+                                     work.rhs, work.n)
+        for _ in range(2):      # the second call reuses the plan's buffers
+            solve_and_check(csc, work, expected, exact=True)
+        plan = csc.schedule_plan(work.indptr, work.indices, work.data,
+                                 work.rhs, work.n)
+        assert (plan.tile_boxes is not None) == boxed, name
+        assert csc.hip_lowering.tile_by_position == boxed
+        assert ("_lcd_xq[" in csc.hip_kernel_source) == boxed
+        if boxed and name == "c2":
+            assert plan.tile_boxes[0] == (20, 18, 16)
+            if box != "auto":
+                assert plan.tile_boxes[1] == box
+                assert plan.tile_rows == box[0] * box[1] * box[2]
+            else:
+                assert np.prod(plan.tile_boxes[1]) <= 256
+    with pytest.raises(ValueError):
+        sptrsv.compile_sptrsv_csc(tile_box=(4, 4))
+    # a grid given by the caller that the structure does not have: the
+    # order is not topological, the plan falls back to consecutive ids
+    wrong = sptrsv.compile_sptrsv_csc(
+        execution_mode="sync_free", threads_per_block=128, task_lanes=4,
+        thread_unroll=1, dependence_protocol="mailbox", tile_rows=256,
+        tile_box=(2, 2, 1), tile_grid=(4, 2, 720))
+    work = workloads.configuration("c2", nx=20, ny=18, nz=16)
+    expected = oracle.sptrsv_csc(work.indptr, work.indices, work.data,
+                                 work.rhs, work.n)
+    solve_and_check(wrong, work, expected, exact=True)
+    assert wrong.schedule_plan(work.indptr, work.indices, work.data, work.rhs,
+                               work.n).tile_boxes is None
 
 
 def random_lower_factor(n, seed):

@@ -788,6 +788,84 @@ def test_tiled_mailbox_reads_task_records():
     hip_runtime.compile_code(plain.source)
 
 
+def test_tiles_addressed_by_queue_position():
+    """Tiles that do not follow the ids (boxes of a grid): sources, LDS slots
+    and the value-as-flag copy are addressed by the place in the queue."""
+    module = demo_source("sptrsv", "sptrsv_csc_loop")
+    options = dict(execution_mode="sync_free", thread_loop_iterator="j",
+                   task_lanes=4, wavefront_threads_per_block=128,
+                   dependence_protocol="mailbox", tile_rows=1024)
+    result = lower(module, single_chunk=True, tile_by_position=True,
+                   **options)
+    assert result.tile_by_position and result.tile_rows == 1024
+    assert result.kernel_arguments.count("_lcd_xq") == 1
+    kernel = result.kernel_source
+    assert "LCD_T__lcd_xq* _lcd_xq" in kernel          # written: not const
+    # the flag copy is polled and written by queue position, x gets a plain
+    # store and is not reset
+    assert "_g_early = lcd_ld(&_lcd_xq[_g_src]);" in kernel
+    assert "lcd_ld(&x[" not in kernel
+    assert ("lcd_tile_st(_lcd_xq, _lcd_tile, _lcd_tile_row0, _lcd_tile_rows, "
+            "(lcd_index_t)_task, _lcd_own_0); x[i] = _lcd_own_0;") in kernel
+    assert "(_lcd_xq, task_counter, _hip.length(_lcd_xq))" in (
+        result.launcher_source)
+    hip_runtime.compile_code(result.source)
+    # without the guarantee that a record holds every incoming edge the
+    # further chunks would name sources by id: ids stay in charge
+    chunks = lower(module, tile_by_position=True, **options)
+    assert not chunks.tile_by_position
+    assert "_lcd_xq" not in chunks.kernel_arguments
+    # the pull protocol reads x[Ai[j]] by id
+    pull = lower(demo_source("sptrsv", "sptrsv_csr_loop"),
+                 execution_mode="sync_free", thread_loop_iterator="j",
+                 task_lanes=8, dependence_protocol="pull", tile_rows=512,
+                 single_chunk=True, tile_by_position=True)
+    assert pull.tile_rows == 512 and not pull.tile_by_position
+
+
+def test_structured_grid_and_box_choice():
+    """What the scheduler reads a grid from (edge offsets 1, nx, nx * ny with
+    the counts of a full stencil) and the box it picks: the fewest box faces
+    along the critical path."""
+    from lcd_amd.scheduler import automatic_tile_box, structured_grid
+
+    class Dag:
+        def __init__(self, n, offsets, counts):
+            self.n, self.offsets, self.counts = n, offsets, counts
+
+        def edge_offsets(self, capacity):
+            return (self.offsets[:capacity], self.counts[:capacity],
+                    len(self.offsets))
+
+    nx, ny, nz = 12, 10, 9
+    n = nx * ny * nz
+    full = [(nx - 1) * ny * nz, nx * (ny - 1) * nz, nx * ny * (nz - 1)]
+    assert structured_grid(Dag(n, [1, nx, nx * ny], full)) == (nx, ny, nz)
+    assert structured_grid(Dag(nx * ny, [1, nx], [(nx - 1) * ny,
+                                                  nx * (ny - 1)])) == (
+        nx, ny, 1)
+    # a missing edge, a stray offset, a chain, offsets that do not nest
+    assert structured_grid(Dag(n, [1, nx, nx * ny],
+                               [full[0] - 1, *full[1:]])) is None
+    assert structured_grid(Dag(n, [1, nx, nx * ny, 500], full + [1])) is None
+    assert structured_grid(Dag(n, [1], [n - 1])) is None
+    assert structured_grid(Dag(n, [2, nx, nx * ny], full)) is None
+    assert structured_grid(Dag(n, [1, 7, nx * ny], full)) is None
+    assert structured_grid(Dag(0, [], [])) is None
+    # whole lines along x, the rest split between y and z: 128^3 with 4096
+    # points crosses 15 + 31 faces
+    assert automatic_tile_box((128, 128, 128), 4096) == (128, 8, 4)
+    assert automatic_tile_box((128, 128, 128), 8192) == (128, 8, 8)
+    assert automatic_tile_box((128, 128, 128), 2048) == (128, 4, 4)
+    assert automatic_tile_box((20, 18, 16), 256) == (20, 4, 2)
+    assert automatic_tile_box((5, 3, 2), 4096) == (5, 3, 2)
+    # two dimensions, lines longer than half a tile, boxes one plane thick:
+    # tiles of consecutive ids are the same thing
+    assert automatic_tile_box((64, 64, 1), 1024) is None
+    assert automatic_tile_box((128, 128, 128), 200) is None
+    assert automatic_tile_box((128, 128, 128), 256) is None
+
+
 def test_structure_arrays_are_read_in_task_order():
     """``Ap[i]`` / ``Ap[i + 1]`` come from copies gathered into queue order
     once per structure, loaded with the task id instead of after it."""
