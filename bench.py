@@ -54,9 +54,9 @@ TUNED = {
     "c4": dict(execution_mode="sync_free", threads_per_block=512,
                task_lanes=64, thread_unroll=1, dependence_protocol="pull",
                tile_rows=1024, tile_positions=9216, segment_capacity=64),
-    "c5": dict(execution_mode="sync_free", threads_per_block=256, task_lanes=8,
+    "c5": dict(execution_mode="sync_free", threads_per_block=128, task_lanes=8,
                thread_unroll=1, dependence_protocol="mailbox",
-               tile_rows=4096),
+               tile_rows=8192),
 }
 
 
