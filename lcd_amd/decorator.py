@@ -58,6 +58,8 @@ from lcd_amd.scheduler import (
     AnalyticScheduler,
     CalibratedScheduler,
     SchedulePlan,
+    TILE_BOX_THREADS_PER_BLOCK,
+    TILE_THREADS_PER_BLOCK,
     automatic_tile_box,
     automatic_tile_rows,
     structured_grid,
@@ -202,10 +204,15 @@ def parallel(**kwargs):
             raise ValueError(
                 "tile_box must be None, 'auto' or three positive integers.")
 
+        registers_option = kwargs.get("segment_registers", "auto")
+        if registers_option not in ("auto", True, False):
+            raise ValueError("segment_registers must be 'auto', True or False.")
+
         def lower_variant(lowering_key, tile_rows=None, single_chunk=False,
-                          task_records=True, by_position=False):
+                          task_records=True, by_position=False,
+                          registers=False):
             variant_key = (lowering_key, tile_rows, single_chunk, task_records,
-                           by_position)
+                           by_position, registers)
             if variant_key not in lowered_variants:
                 (mode, threads_per_block, unroll, n_warp, protocol,
                  task_lanes) = lowering_key
@@ -246,17 +253,19 @@ def parallel(**kwargs):
                     pipeline_fetch=kwargs.get("pipeline_fetch", True),
                     tile_positions=kwargs.get("tile_positions"),
                     tile_by_position=by_position,
+                    segment_registers=registers,
                     full_fences=kwargs.get("full_fences", False),
                     dynamic_fetch=kwargs.get("dynamic_fetch", False),
                 )
             return lowered_variants[variant_key]
 
         def compile_variant(lowering_key, tile_rows=None, single_chunk=False,
-                            task_records=True, by_position=False):
+                            task_records=True, by_position=False,
+                            registers=False):
             lowering = lower_variant(lowering_key, tile_rows, single_chunk,
-                                     task_records, by_position)
+                                     task_records, by_position, registers)
             variant_key = (lowering_key, tile_rows, single_chunk, task_records,
-                           by_position)
+                           by_position, registers)
             if variant_key not in compiled_variants:
                 compiled_variants[variant_key] = compile_hip_module(
                     lowering, function_globals=function.__globals__)
@@ -288,6 +297,34 @@ def parallel(**kwargs):
                 # threads, 38 ms at the sizes chosen for SpTRSV): by request
                 return schedule, None
             return tiled, rows
+
+        def registers_for(schedule, rows, values):
+            """True when this plan keeps the tasks' own segments (ILU0's
+            rows) in registers: the loop allows it and no segment of this
+            structure has more than 64 entries."""
+            if registers_option is False:
+                return False
+            try:
+                variant = lower_variant(schedule.lowering_key, rows,
+                                        registers=True)
+            except HIPLoweringError:
+                return False
+            if not variant.segment_registers:
+                return False
+            pointers = values.get(variant.segment_pointer)
+            if pointers is None:
+                return False
+            if hip_runtime.is_device_array(pointers):
+                pointers = pointers.copy_to_host()
+            pointers = np.asarray(pointers)
+            longest = int(np.max(np.diff(pointers))) if len(pointers) > 1 else 0
+            if longest > 64:
+                if registers_option is True:
+                    raise ValueError(
+                        "segment_registers=True needs segments of at most 64 "
+                        f"entries; the longest has {longest}.")
+                return False
+            return True
 
         def boxes_for(dag, schedule, rows):
             """(grid, box) when the tiles of this plan are boxes of a
@@ -465,6 +502,14 @@ def parallel(**kwargs):
                                          task_records=False)
             execution_data, tile_boxes = None, boxes_for(dag, schedule,
                                                          tile_rows)
+            if (tile_boxes is not None and tile_option == "auto"
+                    and kwargs.get("threads_per_block") is None
+                    and schedule.threads_per_block == TILE_THREADS_PER_BLOCK):
+                wider = replace(schedule,
+                                threads_per_block=TILE_BOX_THREADS_PER_BLOCK)
+                if boxes_for(dag, wider, tile_rows) == tile_boxes:
+                    schedule = wider
+                    lowering = lower_variant(schedule.lowering_key, tile_rows)
             if tile_boxes is not None:
                 # a box order that is not topological, or a task with more
                 # incoming edges than its record holds: tiles of consecutive
@@ -492,6 +537,8 @@ def parallel(**kwargs):
                     mailbox=lowering.dependence_protocol == MAILBOX_DEPENDENCE,
                     tile_rows=lowering.tile_rows,
                     record_lanes=lowering.task_record_lanes)
+            segment_registers = (tile_boxes is None and registers_for(
+                schedule, tile_rows, device_values))
             plan = SchedulePlan(
                 schedule=schedule,
                 execution_data=attach_auxiliary_values(
@@ -501,7 +548,8 @@ def parallel(**kwargs):
                 # variant without the code for further chunks
                 single_chunk=bool(lowering.task_record_lanes)
                 and getattr(dag, "record_overflow", 1) == 0,
-                task_records=records, tile_boxes=tile_boxes)
+                task_records=records, tile_boxes=tile_boxes,
+                segment_registers=segment_registers)
             plan_state[id(plan)] = {"resident": resident, "workspace": {}}
             return plan
 
@@ -544,7 +592,8 @@ def parallel(**kwargs):
                                                  plan.tile_rows,
                                                  plan.single_chunk,
                                                  plan.task_records,
-                                                 plan.tile_boxes is not None)
+                                                 plan.tile_boxes is not None,
+                                                 plan.segment_registers)
             publish_variant(plan.schedule, lowering, compiled)
             state = plan_state[id(plan)]
             values = dict(argument_values)

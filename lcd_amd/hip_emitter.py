@@ -114,6 +114,10 @@ class HIPLoweringResult:
     # tiled executor whose LDS copy and flag array are indexed by the place
     # of a task in the queue (tiles that do not follow the ids)
     tile_by_position: bool = False
+    # the pointer array of the task's own segment (ILU0's row), and whether
+    # that segment is kept in registers (segments of at most 64 entries)
+    segment_pointer: str | None = None
+    segment_registers: bool = False
     # lifted zero-initialised arrays the executor needs no host-side clear for
     executor_initialised: tuple = ()
     # kernel that gathers position-indexed operands into consumer order at
@@ -311,7 +315,8 @@ class _Kinds:
         if isinstance(node, ast.Call) and isinstance(node.func, ast.Name):
             if node.func.id in ("float",):
                 return FLOAT
-            if node.func.id in ("int", "len", "_lcd_sorted_find"):
+            if node.func.id in ("int", "len", "_lcd_sorted_find",
+                                "_lcd_rseg_first"):
                 return INT
             if node.func.id in ("abs", "min", "max"):
                 kinds = [self.kind(a) for a in node.args]
@@ -335,6 +340,19 @@ class _Emitter:
         self.segment = None     # own-segment staging plan (HIPLowerer)
         self.published = None   # final values published to a flagged buffer
         self.tile = None        # tiled executor plan (HIPLowerer)
+        self.in_mapped = None   # iterator of the distributed loop being emitted
+
+    def _register_position(self, index):
+        """How a position of the own segment kept in registers is reached:
+        'lane' for the distributed loop's own iterator inside that loop
+        (lane l works on entry l), 'uniform' for a loop variable that walks
+        the segment in the task's uniform code, None for anything else."""
+        segment = self.segment
+        if not (isinstance(index, ast.Name) and index.id in segment["owned"]):
+            return None
+        if self.in_mapped is None:
+            return "uniform"
+        return "lane" if self.in_mapped == index.id else None
 
     # ---- expressions
     def expr(self, node):
@@ -354,6 +372,18 @@ class _Emitter:
                 raise HIPLoweringError("Only 1-D array indexing is supported.")
             element = f"{node.value.id}[{self.expr(node.slice)}]"
             segment = self.segment
+            if (segment is not None and node.value.id == segment["array"]
+                    and segment.get("registers")):
+                place = self._register_position(node.slice)
+                if place == "lane":
+                    return "_lcd_rseg"
+                if place == "uniform":
+                    return (f"lcd_rseg_uni(_lcd_rseg, {node.slice.id} - "
+                            "_lcd_seg_base)")
+                return ("lcd_rseg_ldp(_lcd_pub, _lcd_seg, _lcd_seg_base, "
+                        f"_lcd_seg_own, {self.expr(node.slice)}, "
+                        f"{STATUS_ARGUMENT}, _task_aborted, _lcd_t0, "
+                        "_lcd_ptile, _lcd_tpos0, _lcd_tlen)")
             if (segment is not None and node.value.id == segment["array"]
                     and self.published is not None):
                 return (f"lcd_seg_ldp({node.value.id}, _lcd_pub, _lcd_seg, "
@@ -437,6 +467,14 @@ class _Emitter:
                 return f"(lcd_index_t)({args[0]})"
             if name == "_lcd_sorted_find" and len(args) == 4:
                 return f"lcd_sorted_find({', '.join(args)})"
+            if name == "_lcd_rseg_first" and len(args) == 1:
+                return f"lcd_rseg_first({args[0]}, _lcd_seg_base)"
+            if (name == "_lcd_raw" and self.published is not None
+                    and self.segment.get("registers")):
+                target = node.args[0]
+                return ("lcd_rseg_ldr(_lcd_pub, _lcd_seg, _lcd_seg_base, "
+                        f"_lcd_seg_own, {self.expr(target.slice)}, _lcd_ptile, "
+                        "_lcd_tpos0, _lcd_tlen)")
             if name == "_lcd_raw" and self.published is not None:
                 target = node.args[0]
                 return (f"lcd_seg_ldr({target.value.id}, _lcd_pub, _lcd_seg, "
@@ -486,6 +524,19 @@ class _Emitter:
             return (f"lcd_tile_st({target.value.id}, _lcd_tile, _lcd_tile_row0, "
                     f"_lcd_tile_rows, {self.expr(target.slice)}, {value_text});")
         segment = self.segment
+        if (segment is not None and target.value.id == segment["array"]
+                and segment.get("registers")):
+            place = self._register_position(target.slice)
+            offset = f"{self.expr(target.slice)} - _lcd_seg_base"
+            if place == "lane":
+                return (f"{{ _lcd_rseg = {value_text}; "
+                        f"_lcd_seg[{offset}] = _lcd_rseg; }}")
+            if place == "uniform":
+                return (f"lcd_rseg_put(_lcd_rseg, _lcd_seg, {offset}, "
+                        f"{value_text});")
+            raise HIPLoweringError(
+                "A segment kept in registers is written through the loop "
+                f"variables that walk it; got {ast.unparse(target)!r}.")
         if segment is not None and target.value.id == segment["array"]:
             name = ("lcd_seg_stc" if target.value.id in self.coherent_arrays
                     else "lcd_seg_st")
@@ -653,8 +704,28 @@ class _MappedLoopHooks:
             lines.append(f"{pad}{partial} = 0.0;")
         if self.value_pull is not None:
             return self._value_pull_loop(node, body, indent, lines, stores)
-        body_lines = emitter.block(body, indent + (2 if unroll > 1 else 1), None)
+        registers = (emitter.segment is not None
+                     and emitter.segment.get("registers")
+                     and name in emitter.segment["owned"])
+        emitter.in_mapped = name
+        try:
+            body_lines = emitter.block(
+                body, indent + (2 if unroll > 1 else 1), None)
+        finally:
+            emitter.in_mapped = None
         hook_lines = low.push_hook_lines(indent + (2 if unroll > 1 else 1))
+        if registers:
+            # lane l works on entry l of the segment (at most 64 entries:
+            # one trip), so the entry a lane updates is its own register
+            if unroll != 1 or low._first_iteration_reload:
+                raise HIPLoweringError(
+                    "A segment in registers needs the plain distributed loop.")
+            lines.append(f"{pad}{name} = lcd_rseg_first({lower}, _lcd_seg_base);")
+            lines.append(f"{pad}if ({name} < {upper}) {{")
+            lines += body_lines + hook_lines
+            lines.append(f"{pad}}}")
+            # (register updates need no fence)
+            return lines + self._after_loop(pad, False)
         if unroll == 1:
             lines.append(f"{pad}for ({name} = ({lower}) + _lane; {name} < {upper}; "
                          f"{name} += {lanes}) {{")

@@ -100,9 +100,10 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                  publish_values=True, look_ahead=True, segment_capacity=None,
                  pipeline_fetch=True, full_fences=False,
                  dynamic_fetch=False, tile_positions=None,
-                 tile_by_position=False):
+                 tile_by_position=False, segment_registers=False):
         self.tile_positions = tile_positions
         self.tile_by_position = tile_by_position
+        self.segment_registers = segment_registers
         # full_fences: agent-scope release/acquire fences of the HIP memory
         # model (L2 write-back / invalidate per hand-off) instead of the
         # wait-for-completion scheme; dynamic_fetch: the flat queue hands out
@@ -340,6 +341,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
             self._published = {"array": self._segment["array"],
                                "buffer": "_lcd_pub"}
             kinds.arrays["_lcd_pub"] = FLOAT
+        self._segment_registers_plan(body)
         if self.tile_rows:
             self._tile = self._tile_plan(target_loop)
         if (self.task_records and self._mailbox is not None
@@ -477,6 +479,10 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
             tile_rows=self._tile["rows"] if self._tile else None,
             tile_by_position=bool(self._tile
                                   and self._tile.get("by_position")),
+            segment_pointer=(self._segment["pointer"]
+                             if self._segment else None),
+            segment_registers=bool(self._segment
+                                   and self._segment.get("registers")),
             spin_limit=self.spin_limit,
             queue_node_loads=tuple(self._queue_node_loads),
             published_array=(self._published["array"]
@@ -722,6 +728,17 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
 
     def _emit_guarded(self, node, emitter, indent, hooks):
         pad = "    " * indent
+        if (isinstance(node, ast.If) and getattr(node, "_lcd_store_guard", False)
+                and self._segment is not None
+                and self._segment.get("registers")
+                and all(isinstance(child, ast.Assign)
+                        and isinstance(child.targets[0], ast.Subscript)
+                        and isinstance(child.targets[0].value, ast.Name)
+                        and child.targets[0].value.id == self._segment["array"]
+                        for child in node.body)):
+            # the lane that holds the entry takes the value: every lane runs
+            # the statement, nothing to fence
+            return emitter.block(node.body, indent, None)
         if isinstance(node, ast.If) and getattr(node, "_lcd_store_guard", False):
             inner = emitter.block(node.body, indent + 1, None)
             self._pending_sync = False
@@ -918,6 +935,9 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                 "(threadIdx.x / LCD_TASK_LANES) * LCD_SEG_CAP];",
                 "    lcd_index_t _lcd_seg_base = 0, _lcd_seg_limit = 0;",
                 *(["    lcd_index_t _lcd_seg_own = 0;"] if self._published else []),
+                *([f"    LCD_T_{array} _lcd_rseg = 0.0;",
+                   "    (void)_lcd_seg_limit;"]
+                  if self._segment.get("registers") else []),
             ]
         lines.append(f"    lcd_index_t {it} = 0;")
         lines += self._declarations(local_names, 1)
@@ -1428,7 +1448,8 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
                  queue_node_loads=True, plain_first_polls=None,
                  publish_values=True, look_ahead=True, segment_capacity=None,
                  pipeline_fetch=True, full_fences=False, dynamic_fetch=False,
-                 tile_positions=None, tile_by_position=False):
+                 tile_positions=None, tile_by_position=False,
+                 segment_registers=False):
     """HIP counterpart of ``lower_to_numba_cuda``
     (compiler/cuda_lowering.py:2854-2884); same parameters plus
     ``task_lanes`` (lanes cooperating on one task, a power of two <= 64),
@@ -1456,5 +1477,6 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
         look_ahead=look_ahead, segment_capacity=segment_capacity,
         pipeline_fetch=pipeline_fetch, full_fences=full_fences,
         dynamic_fetch=dynamic_fetch, tile_positions=tile_positions,
-        tile_by_position=tile_by_position)
+        tile_by_position=tile_by_position,
+        segment_registers=segment_registers)
     return lowerer.lower(code)

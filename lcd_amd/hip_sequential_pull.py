@@ -302,10 +302,21 @@ class SequentialPullMixin:
         self._own_registers.extend(["_sp_first", *sorted(
             renamed[name] for name in names)])
         lower, upper = mapped.iter.args
-        first = ast.Assign(
-            targets=[ast.Name(id="_sp_first", ctx=ast.Store())],
-            value=ast.BinOp(left=deepcopy(lower), op=ast.Add(),
-                            right=ast.Name(id="_lane", ctx=ast.Load())))
+        registers = (self._segment is not None
+                     and self._segment.get("registers")
+                     and iterator in self._segment["owned"])
+        if registers:
+            # lane l works on entry l of the segment, once
+            first = ast.Assign(
+                targets=[ast.Name(id="_sp_first", ctx=ast.Store())],
+                value=ast.Call(
+                    func=ast.Name(id="_lcd_rseg_first", ctx=ast.Load()),
+                    args=[deepcopy(lower)], keywords=[]))
+        else:
+            first = ast.Assign(
+                targets=[ast.Name(id="_sp_first", ctx=ast.Store())],
+                value=ast.BinOp(left=deepcopy(lower), op=ast.Add(),
+                                right=ast.Name(id="_lane", ctx=ast.Load())))
         ahead = ast.If(
             test=ast.Compare(left=ast.Name(id="_sp_first", ctx=ast.Load()),
                              ops=[ast.Lt()], comparators=[deepcopy(upper)]),
@@ -322,15 +333,21 @@ class SequentialPullMixin:
                 value=ast.Name(id=renamed[statement.targets[0].id],
                                ctx=ast.Load())) for statement in structural],
             orelse=list(structural))
+        if registers:
+            # the lane's only iteration is the one located ahead of the wait
+            pick_up = ast.If(test=ast.Constant(value=True),
+                             body=pick_up.body, orelse=[])
         rest = mapped.body[len(structural):]
-        fetched = self._fetch_behind_wait(rest, iterator, names, renamed, upper)
+        fetched = self._fetch_behind_wait(rest, iterator, names, renamed, upper,
+                                          single_trip=registers)
         mapped.body = [pick_up] + rest
         early = [first, ahead]
         for statement in early + fetched + [pick_up]:
             ast.fix_missing_locations(statement)
         return early, fetched
 
-    def _fetch_behind_wait(self, rest, iterator, names, renamed, upper):
+    def _fetch_behind_wait(self, rest, iterator, names, renamed, upper,
+                           single_trip=False):
         """After the structure work the nested loop reads the producer's
         values at the positions just found (`if kj_ptr >= 0: u = A[kj_ptr]`).
         For each lane's first iteration those loads are issued right behind
@@ -375,6 +392,8 @@ class SequentialPullMixin:
                     held = ast.Call(
                         func=ast.Name(id="_lcd_settle", ctx=ast.Load()),
                         args=[deepcopy(node), held], keywords=[])
+                if single_trip:
+                    return ast.copy_location(held, node)
                 return ast.copy_location(ast.IfExp(
                     test=ast.Compare(
                         left=ast.Name(id=iterator, ctx=ast.Load()),

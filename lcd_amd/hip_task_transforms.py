@@ -10,6 +10,7 @@ from lcd_amd.hip_emitter import (
     FLOAT,
     HIPLoweringError,
     INT,
+    STATUS_ARGUMENT,
     _is_range_loop,
     _names_in,
     _stored_names,
@@ -245,8 +246,45 @@ class TaskTransformMixin:
             capacity = int(self.segment_capacity)
         if capacity < 8:
             return None
-        return {"array": array, "pointer": next(iter(pointers)),
-                "capacity": capacity}
+        plan = {"array": array, "pointer": next(iter(pointers)),
+                "capacity": capacity, "owned": set(owned), "registers": False}
+        if self.segment_registers and self.task_lanes == 64:
+            # (decided once the protocol is known: `_segment_registers_plan`)
+            plan["capacity"] = 64
+        return plan
+
+    def _segment_registers_plan(self, body):
+        """Keeps the task's own segment in registers instead of LDS: lane l
+        of the task's wavefront holds entry l.  For a caller that knows every
+        segment has at most 64 entries (``segment_registers=True``), with one
+        wavefront per task and published values; every store to the array
+        must go through a loop variable that walks the segment.  The chain
+        between two levels loses its LDS round trips (store -> fence -> load
+        per update) and the distributed loop its second path: a lane visits
+        one entry, the one it holds."""
+        plan = self._segment
+        if not (self.segment_registers and plan is not None
+                and self._published is not None and self.task_lanes == 64
+                and self._sequential_pull is not None
+                and self.thread_unroll_factor == 1):
+            return
+        array, owned = plan["array"], plan["owned"]
+        for statement in body:
+            for node in ast.walk(statement):
+                targets = []
+                if isinstance(node, ast.Assign):
+                    targets = node.targets
+                elif isinstance(node, ast.AugAssign):
+                    targets = [node.target]
+                for target in targets:
+                    if (isinstance(target, ast.Subscript)
+                            and isinstance(target.value, ast.Name)
+                            and target.value.id == array
+                            and not (isinstance(target.slice, ast.Name)
+                                     and target.slice.id in owned)):
+                        return
+        plan["registers"] = True
+        plan["capacity"] = 64
 
     def _segment_lines(self):
         """(prologue, epilogue) of a task that stages its own segment."""
@@ -268,6 +306,24 @@ class TaskTransformMixin:
                     return f"{name}[_task]"
             return f"{pointer}[{it} + {offset}]" if offset else f"{pointer}[{it}]"
 
+        if plan.get("registers"):
+            # (segments longer than 64 entries are excluded by the caller; one
+            # that is longer anyway stops the launch through the status word)
+            prologue = [
+                f"_lcd_seg_base = {bound(0)};",
+                f"_lcd_seg_own = {bound(1)} - _lcd_seg_base;",
+                f"if (_lcd_seg_own > 64) {{ {STATUS_ARGUMENT}[0] = 1; "
+                "_task_aborted = true; _lcd_seg_own = 0; }",
+                f"_lcd_rseg = _lane < _lcd_seg_own ? {array}[_lcd_seg_base + "
+                "_lane] : 0.0;",
+                "if (_lane < _lcd_seg_own) _lcd_seg[_lane] = _lcd_rseg;",
+            ]
+            epilogue = [
+                "if (_lane < _lcd_seg_own) { lcd_pub_st(_lcd_pub, _lcd_ptile, "
+                "_lcd_tpos0, _lcd_tlen, _lcd_seg_base + _lane, _lcd_rseg); "
+                f"{array}[_lcd_seg_base + _lane] = _lcd_rseg; }}",
+            ]
+            return prologue, epilogue
         prologue = [
             f"_lcd_seg_base = {bound(0)};",
             f"_lcd_seg_limit = {bound(1)} - _lcd_seg_base;",

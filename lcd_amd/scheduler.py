@@ -158,6 +158,7 @@ class SchedulePlan:
     single_chunk: bool = False       # no task has more in-edges than lanes
     task_records: bool = True        # record arrays fit 32-bit indices
     tile_boxes: tuple | None = None  # (grid, box): tiles are boxes of a grid
+    segment_registers: bool = False  # own segments (<= 64 entries) in registers
 
 
 # Tiled executor, automatic choice: tiles of 4096 consecutive block-iterator
@@ -172,6 +173,11 @@ TILE_ROWS = 4096
 TILE_MIN_ROWS = 256
 TILE_MIN_LOCALITY = 0.5
 TILE_THREADS_PER_BLOCK = 384
+# Box tiles keep their eight wavefronts busy (whole lines: 32 tasks per level,
+# two wavefronts per level, four levels in flight): 128^3 with boxes of
+# 128 x 8 x 4 runs in 0.287 / 0.247 / 0.238 / 0.305 ms at 256 / 384 / 512 / 640
+# threads.
+TILE_BOX_THREADS_PER_BLOCK = 512
 # Once there are more such tiles than workgroups of 384 threads can be
 # resident (three per CU on 256 CUs), the solve is bound by throughput rather
 # than by hand-offs, and more, smaller tiles with fewer threads each measured

@@ -458,6 +458,12 @@ ILU_VARIANTS = [
          dependence_protocol="pull", tile_rows=72, tile_positions=700),
     dict(execution_mode="sync_free", threads_per_block=128, task_lanes=64,
          dependence_protocol="pull", tile_rows=256, tile_positions=512),
+    # the own row staged in LDS although it would fit the registers
+    dict(execution_mode="sync_free", threads_per_block=128, task_lanes=64,
+         dependence_protocol="pull", segment_registers=False),
+    dict(execution_mode="sync_free", threads_per_block=256, task_lanes=64,
+         dependence_protocol="pull", tile_rows=100, tile_positions=1024,
+         segment_registers=False),
 ]
 
 
@@ -488,6 +494,10 @@ def test_ilu0_csr_variants(oracle, options):
             assert factor.hip_lowering.tile_rows == options["tile_rows"]
             assert "_lcd_ptile[LCD_TILE_POS]" in factor.hip_kernel_source
         assert ("done[" in factor.hip_kernel_source) != published
+        # rows of at most 64 entries live in registers, one entry per lane
+        registers = published and options.get("segment_registers", True)
+        assert factor.hip_lowering.segment_registers == registers
+        assert ("lcd_rseg_uni(_lcd_rseg" in factor.hip_kernel_source) == registers
         # irregular rows too: pivots near and far, empty lower parts
         import scipy.sparse as sp
         lower, diagonal, _ = random_lower_factor(2500, 11)
@@ -498,6 +508,13 @@ def test_ilu0_csr_variants(oracle, options):
         np.testing.assert_array_equal(
             factor(matrix.data.copy(), indices, indptr),
             oracle.ilu0_csr(matrix.data, indices, indptr))
+        # (rows of up to 300 entries: staged in LDS or updated in place)
+        assert not factor.hip_lowering.segment_registers
+        if published:
+            forced = spilu0.compile_ilu0_csr(**{**options,
+                                                "segment_registers": True})
+            with pytest.raises(ValueError, match="at most 64"):
+                forced(matrix.data.copy(), indices, indptr)
 
 
 @pytest.mark.parametrize("mode", ["wavefront", "sync_free", None])

@@ -823,6 +823,60 @@ def test_tiles_addressed_by_queue_position():
     assert pull.tile_rows == 512 and not pull.tile_by_position
 
 
+def test_own_segment_in_registers():
+    """ILU0 with one row per wavefront and rows of at most 64 entries: the
+    row lives in one register per lane; the pivot entry is read with
+    read-lanes, a lane updates the entry it holds, and the distributed loop
+    is one aligned trip."""
+    module = demo_source("spilu0", "ilu0_csr")
+    props = {"A_indptr": ["monotonically_increasing"],
+             ("A_indptr", "A_indices"): ["segmented_monotonically_increasing"]}
+    from lcd_amd.dag_codegen import create_dag_plan, direct_dependence
+    from lcd_amd.dependence import analyze_dependences
+    from lcd_amd.structural_lookups import (create_structural_lookup_plan,
+                                            rewrite_structural_lookups)
+    function = module.body[0]
+    lookups = create_structural_lookup_plan(function, props)
+    analysis = analyze_dependences(function, "i", props)
+    plan = create_dag_plan(analysis.ordering_dependences, None,
+                           parallel_iterator="i",
+                           arguments=["A_data", "A_indices", "A_indptr"],
+                           function_props=props, node_count="n")
+    dependence = direct_dependence(plan, "j_ptr")
+    options = dict(loop_iterator="i", reductions=analysis,
+                   execution_mode="sync_free", thread_loop_iterator="j_ptr",
+                   task_lanes=64, wavefront_threads_per_block=128,
+                   dependence_protocol="pull", direct_dependence=dependence,
+                   function_props=props, structural_lookups=lookups)
+    from lcd_amd.hip_lowering import lower_to_hip
+    staged = lower_to_hip(module, **options)
+    held = lower_to_hip(module, segment_registers=True, **options)
+    assert staged.segment_pointer == held.segment_pointer == "A_indptr"
+    assert not staged.segment_registers and held.segment_registers
+    text = held.kernel_source
+    assert "_lcd_rseg = _lane < _lcd_seg_own ? A_data[_lcd_seg_base + _lane]" in text
+    assert "(lcd_rseg_uni(_lcd_rseg, k_ptr - _lcd_seg_base) / diag_val)" in text
+    assert "lcd_rseg_put(_lcd_rseg, _lcd_seg, k_ptr - _lcd_seg_base, _lcd_fw_0);" in text
+    assert "j_ptr = lcd_rseg_first((k_ptr + 1), _lcd_seg_base);" in text
+    assert "_lcd_rseg = (_lcd_rseg - (l_ik * u_kj));" in text
+    # one trip: no second path that searches the pivot row inside the loop
+    assert text.count("lcd_sorted_find(") == 2 < staged.kernel_source.count(
+        "lcd_sorted_find(")
+    assert "j_ptr += LCD_TASK_LANES" not in text
+    # reads at computed positions keep an own-range check (LDS copy)
+    assert "lcd_rseg_ldr(_lcd_pub, _lcd_seg, _lcd_seg_base, _lcd_seg_own, diag_ptr" in text
+    # the row is published from the registers
+    assert ("lcd_pub_st(_lcd_pub, _lcd_ptile, _lcd_tpos0, _lcd_tlen, "
+            "_lcd_seg_base + _lane, _lcd_rseg)") in text
+    # a row that is longer after all stops the launch
+    assert "if (_lcd_seg_own > 64) { _lcd_status[0] = 1;" in text
+    hip_runtime.compile_code(held.source)
+    # eight lanes per row: rows share a wavefront, registers do not apply
+    narrow = lower_to_hip(module, segment_registers=True,
+                          **{**options, "task_lanes": 8})
+    assert not narrow.segment_registers
+
+
 def test_structured_grid_and_box_choice():
     """What the scheduler reads a grid from (edge offsets 1, nx, nx * ny with
     the counts of a full stencil) and the box it picks: the fewest box faces
