@@ -51,9 +51,11 @@ TUNED = {
     "c3": dict(execution_mode="sync_free", threads_per_block=128,
                task_lanes=64, thread_unroll=1,
                dependence_protocol="pull", tile_rows=None),
-    "c4": dict(execution_mode="sync_free", threads_per_block=512,
+    # (rows of nine entries: the row lives in registers and the searches of
+    # the pivot loop come from the inspector's tables, both chosen per plan)
+    "c4": dict(execution_mode="sync_free", threads_per_block=640,
                task_lanes=64, thread_unroll=1, dependence_protocol="pull",
-               tile_rows=1024, tile_positions=9216, segment_capacity=64),
+               tile_rows=1024, tile_positions=9216),
     "c5": dict(execution_mode="sync_free", threads_per_block=128, task_lanes=8,
                thread_unroll=1, dependence_protocol="mailbox",
                tile_rows=8192),

@@ -341,6 +341,24 @@ int lcdhip_lookup_build(const int32_t *d_ptr, const int32_t *d_idx, int64_t n,
                         int64_t idx_size, int32_t *d_positions,
                         lcdhip_stream stream);
 
+/* Pair table of a segmented structure (d_ptr[n + 1], d_idx[idx_size], segments
+ * sorted): for segment s with entries a, b in [0, len_s),
+ * d_table[d_base[s] + a * len_s + b] = first position in segment
+ * d_idx[d_ptr[s] + a] whose index equals d_idx[d_ptr[s] + b], or -1;
+ * d_base[s] = sum of len^2 over the segments before s (n + 1 entries).  It
+ * holds the results of the searches ILU0 makes per pivot and updated entry
+ * (`for kj_ptr in range(A_indptr[k], A_indptr[k + 1]): if A_indices[kj_ptr] ==
+ * j`, reference compiler/demo/spilu0.py:38-46): they depend on the structure
+ * only, and read from a table their addresses depend on the task's own
+ * positions alone.  Extends the diagonal table of
+ * compiler/structural_lookups.py:279-333 to pairs.  Call with d_table = NULL
+ * to get *entries_out (the sum of len^2, which must stay below 2^31), then
+ * with buffers of n + 1 and `capacity` >= that many int32. */
+int lcdhip_pair_lookup_build(const int32_t *d_ptr, const int32_t *d_idx, int64_t n,
+                             int64_t idx_size, int32_t *d_base, int32_t *d_table,
+                             int64_t capacity, int64_t *entries_out,
+                             lcdhip_stream stream);
+
 /* d_dst[q] = d_src[d_index[q] + offset] for q in [0, count): a structure
  * array read in the order the executor visits the tasks, so that a task's
  * loads of it (`Ap[i]`, `Ap[i + 1]`) have addresses that depend on the queue

@@ -613,6 +613,164 @@ extern "C" int lcdhip_lookup_build(const int32_t *d_ptr, const int32_t *d_idx,
     return LCDHIP_OK;
 }
 
+// ---- pair table: where segment idx[p] holds the entries of p's own segment
+// base[s] = sum over the segments before s of (their length)^2; for the
+// segment s with entries a, b in [0, len): table[base[s] + a * len + b] = first
+// position in segment idx[ptr[s] + a] whose index equals idx[ptr[s] + b], or -1.
+
+__global__ void lcdhip_pair_square_kernel(const int32_t *__restrict__ ptr,
+                                          int64_t n, int64_t idx_size,
+                                          unsigned long long *__restrict__ total,
+                                          int32_t *status)
+{
+    int64_t s = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    unsigned long long mine = 0;
+    if (s < n) {
+        const int64_t start = ptr[s], end = ptr[s + 1];
+        if (start < 0 || end < start || end > idx_size)
+            atomicMax(status, 1);
+        else
+            mine = static_cast<unsigned long long>(end - start) * (end - start);
+    }
+    for (int offset = 32; offset > 0; offset >>= 1)
+        mine += __shfl_xor(mine, offset, 64);
+    if ((threadIdx.x & 63) == 0 && mine)
+        atomicAdd(total, mine);
+}
+
+// one workgroup scans the squares; 2^31 entries at most, so 32-bit sums do
+__global__ void __launch_bounds__(1024)
+lcdhip_pair_base_kernel(const int32_t *__restrict__ ptr, int64_t n,
+                        int32_t *__restrict__ base)
+{
+    __shared__ unsigned int carry, wave_total[16];
+    if (threadIdx.x == 0)
+        carry = 0;
+    __syncthreads();
+    for (int64_t first = 0; first < n; first += 1024) {
+        const int64_t s = first + threadIdx.x;
+        unsigned int len = s < n ? static_cast<unsigned int>(ptr[s + 1] - ptr[s]) : 0u;
+        unsigned int value = len * len, scan = value;
+        for (int offset = 1; offset < 64; offset <<= 1) {
+            const unsigned int up = __shfl_up(scan, offset, 64);
+            if ((threadIdx.x & 63) >= offset)
+                scan += up;
+        }
+        if ((threadIdx.x & 63) == 63)
+            wave_total[threadIdx.x >> 6] = scan;
+        __syncthreads();
+        unsigned int before = carry;
+        for (unsigned w = 0; w < (threadIdx.x >> 6); ++w)
+            before += wave_total[w];
+        if (s < n)
+            base[s] = static_cast<int32_t>(before + scan - value);
+        __syncthreads();
+        if (threadIdx.x == 1023)
+            carry = before + scan;
+        __syncthreads();
+    }
+    if (threadIdx.x == 0)
+        base[n] = static_cast<int32_t>(carry);
+}
+
+__global__ void lcdhip_pair_fill_kernel(const int32_t *__restrict__ ptr,
+                                        const int32_t *__restrict__ idx,
+                                        int64_t n, int64_t idx_size,
+                                        const int32_t *__restrict__ base,
+                                        int32_t *__restrict__ table)
+{
+    int64_t p = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+    if (p >= idx_size || p < ptr[0] || p >= ptr[n])
+        return;
+    // the segment that holds position p
+    int64_t lo = 0, hi = n;
+    while (hi - lo > 1) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (ptr[mid] <= p)
+            lo = mid;
+        else
+            hi = mid;
+    }
+    const int64_t s = lo, start = ptr[s], len = ptr[s + 1] - start;
+    const int64_t k = idx[p];
+    int32_t *row = table + base[s] + (p - start) * len;
+    const bool valid = k >= 0 && k < n;
+    const int64_t k_start = valid ? ptr[k] : 0, k_end = valid ? ptr[k + 1] : 0;
+    for (int64_t b = 0; b < len; ++b) {
+        const int32_t key = idx[start + b];
+        int64_t left = k_start, right = k_end;
+        while (left < right) {
+            const int64_t mid = (left + right) >> 1;
+            if (idx[mid] < key)
+                left = mid + 1;
+            else
+                right = mid;
+        }
+        row[b] = (left < k_end && idx[left] == key) ? static_cast<int32_t>(left) : -1;
+    }
+}
+
+extern "C" int lcdhip_pair_lookup_build(const int32_t *d_ptr, const int32_t *d_idx,
+                                        int64_t n, int64_t idx_size,
+                                        int32_t *d_base, int32_t *d_table,
+                                        int64_t capacity, int64_t *entries_out,
+                                        lcdhip_stream stream)
+{
+    LCDHIP_REQUIRE_INIT();
+    if (n < 0 || idx_size < 0 || capacity < 0 || !d_ptr || !entries_out ||
+        (idx_size > 0 && !d_idx) || (d_table && !d_base)) {
+        set_error("bad argument to lcdhip_pair_lookup_build");
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    hipStream_t hip_stream = resolve_stream(stream);
+    *entries_out = 0;
+    unsigned long long *d_total = nullptr;
+    LCDHIP_CHECK(hipMalloc(&d_total, 16));
+    int32_t *d_status = reinterpret_cast<int32_t *>(d_total + 1);
+    hipError_t error = hipMemsetAsync(d_total, 0, 16, hip_stream);
+    unsigned long long host[2] = {0, 0};
+    if (error == hipSuccess && n > 0)
+        hipLaunchKernelGGL(lcdhip_pair_square_kernel,
+                           dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256),
+                           0, hip_stream, d_ptr, n, idx_size, d_total, d_status);
+    if (error == hipSuccess)
+        error = hipMemcpyAsync(host, d_total, 16, hipMemcpyDeviceToHost, hip_stream);
+    if (error == hipSuccess)
+        error = hipStreamSynchronize(hip_stream);
+    (void)hipFree(d_total);
+    if (error != hipSuccess) {
+        set_error("pair table sizing failed: %s", hipGetErrorString(error));
+        return LCDHIP_ERR_HIP;
+    }
+    if (static_cast<int32_t>(host[1] & 0xffffffffu) != 0) {
+        set_error("invalid pointer segment in the structural lookup arrays");
+        return LCDHIP_ERR_LOOKUP_POINTER;
+    }
+    if (host[0] >= (1ull << 31)) {
+        set_error("a pair table of %llu entries exceeds 2^31", host[0]);
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    *entries_out = static_cast<int64_t>(host[0]);
+    if (!d_table)
+        return LCDHIP_OK;
+    if (capacity < *entries_out) {
+        set_error("pair table buffer too small: %lld < %lld",
+                  static_cast<long long>(capacity),
+                  static_cast<long long>(*entries_out));
+        return LCDHIP_ERR_ARGUMENT;
+    }
+    hipLaunchKernelGGL(lcdhip_pair_base_kernel, dim3(1), dim3(1024), 0, hip_stream,
+                       d_ptr, n, d_base);
+    if (idx_size > 0 && n > 0)
+        hipLaunchKernelGGL(lcdhip_pair_fill_kernel,
+                           dim3(static_cast<unsigned>((idx_size + 255) / 256)),
+                           dim3(256), 0, hip_stream, d_ptr, d_idx, n, idx_size,
+                           d_base, d_table);
+    LCDHIP_CHECK(hipGetLastError());
+    LCDHIP_CHECK(hipStreamSynchronize(hip_stream));
+    return LCDHIP_OK;
+}
+
 // -------------------------------------------------------------- digest ----
 
 __device__ inline uint64_t lcdhip_mix64(uint64_t x)

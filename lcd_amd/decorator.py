@@ -58,6 +58,7 @@ from lcd_amd.scheduler import (
     AnalyticScheduler,
     CalibratedScheduler,
     SchedulePlan,
+    PAIR_TABLE_ENTRIES_PER_POSITION,
     TILE_BOX_THREADS_PER_BLOCK,
     TILE_THREADS_PER_BLOCK,
     automatic_tile_box,
@@ -253,7 +254,8 @@ def parallel(**kwargs):
                     pipeline_fetch=kwargs.get("pipeline_fetch", True),
                     tile_positions=kwargs.get("tile_positions"),
                     tile_by_position=by_position,
-                    segment_registers=registers,
+                    segment_registers=bool(registers),
+                    pair_tables=registers == 2,
                     full_fences=kwargs.get("full_fences", False),
                     dynamic_fetch=kwargs.get("dynamic_fetch", False),
                 )
@@ -298,33 +300,63 @@ def parallel(**kwargs):
                 return schedule, None
             return tiled, rows
 
-        def registers_for(schedule, rows, values):
-            """True when this plan keeps the tasks' own segments (ILU0's
-            rows) in registers: the loop allows it and no segment of this
-            structure has more than 64 entries."""
+        def registers_for(schedule, rows, values, lookups):
+            """(level, tables) for this plan.  Level 1: the tasks' own
+            segments (ILU0's rows) live in registers -- the loop allows it
+            and no segment of this structure has more than 64 entries.  Level
+            2: the structure searches of the producer loop are read from
+            tables as well (``pair_tables``, built here, at most
+            PAIR_TABLE_ENTRIES_PER_POSITION entries per stored position).
+            Level 0: neither."""
             if registers_option is False:
-                return False
+                return 0, {}
             try:
                 variant = lower_variant(schedule.lowering_key, rows,
-                                        registers=True)
+                                        registers=1)
             except HIPLoweringError:
-                return False
+                return 0, {}
             if not variant.segment_registers:
-                return False
+                return 0, {}
             pointers = values.get(variant.segment_pointer)
             if pointers is None:
-                return False
-            if hip_runtime.is_device_array(pointers):
-                pointers = pointers.copy_to_host()
-            pointers = np.asarray(pointers)
-            longest = int(np.max(np.diff(pointers))) if len(pointers) > 1 else 0
+                return 0, {}
+            host_pointers = (pointers.copy_to_host()
+                             if hip_runtime.is_device_array(pointers)
+                             else np.asarray(pointers))
+            longest = (int(np.max(np.diff(host_pointers)))
+                       if len(host_pointers) > 1 else 0)
             if longest > 64:
                 if registers_option is True:
                     raise ValueError(
                         "segment_registers=True needs segments of at most 64 "
                         f"entries; the longest has {longest}.")
-                return False
-            return True
+                return 0, {}
+            if not kwargs.get("pair_tables", True):
+                return 1, {}
+            variant = lower_variant(schedule.lowering_key, rows, registers=2)
+            if not variant.structure_tables:
+                return 1, {}
+            device = get_device()
+            tables = {}
+            try:
+                for entry in variant.structure_tables:
+                    if entry[0] == "at":
+                        _, name, lookup, index_array = entry
+                        tables[name] = device.gather_int32(
+                            lookups[lookup], values[index_array])
+                    else:
+                        _, name, pointer_array, index_array = entry
+                        positions = max(int(host_pointers[-1]), 1)
+                        entries = device.pair_lookup_entries(
+                            values[pointer_array], values[index_array])
+                        if entries > PAIR_TABLE_ENTRIES_PER_POSITION * positions:
+                            return 1, {}
+                        tables["_lcd_pair_base"], tables[name] = (
+                            device.pair_lookup_build(values[pointer_array],
+                                                     values[index_array]))
+            except (hip_runtime.HIPRuntimeError, KeyError):
+                return 1, {}
+            return 2, tables
 
         def boxes_for(dag, schedule, rows):
             """(grid, box) when the tiles of this plan are boxes of a
@@ -537,12 +569,13 @@ def parallel(**kwargs):
                     mailbox=lowering.dependence_protocol == MAILBOX_DEPENDENCE,
                     tile_rows=lowering.tile_rows,
                     record_lanes=lowering.task_record_lanes)
-            segment_registers = (tile_boxes is None and registers_for(
-                schedule, tile_rows, device_values))
+            segment_registers, structure_tables = (
+                registers_for(schedule, tile_rows, device_values, lookup_values)
+                if tile_boxes is None else (0, {}))
             plan = SchedulePlan(
                 schedule=schedule,
                 execution_data=attach_auxiliary_values(
-                    execution_data, lookup_values),
+                    execution_data, {**lookup_values, **structure_tables}),
                 features=features, dag=dag, tile_rows=tile_rows,
                 # every task's incoming edges fit its record: the executor
                 # variant without the code for further chunks

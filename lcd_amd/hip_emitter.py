@@ -118,6 +118,10 @@ class HIPLoweringResult:
     # that segment is kept in registers (segments of at most 64 entries)
     segment_pointer: str | None = None
     segment_registers: bool = False
+    # tables of structure searches keyed by the task's own positions:
+    # ("at", name, lookup table, index array) = lookup[index[p]] by p;
+    # ("pair", "_lcd_pair", pointer array, index array) with "_lcd_pair_base"
+    structure_tables: tuple = ()
     # lifted zero-initialised arrays the executor needs no host-side clear for
     executor_initialised: tuple = ()
     # kernel that gathers position-indexed operands into consumer order at
@@ -316,7 +320,7 @@ class _Kinds:
             if node.func.id in ("float",):
                 return FLOAT
             if node.func.id in ("int", "len", "_lcd_sorted_find",
-                                "_lcd_rseg_first"):
+                                "_lcd_rseg_first", "_lcd_pair_at"):
                 return INT
             if node.func.id in ("abs", "min", "max"):
                 kinds = [self.kind(a) for a in node.args]
@@ -469,6 +473,9 @@ class _Emitter:
                 return f"lcd_sorted_find({', '.join(args)})"
             if name == "_lcd_rseg_first" and len(args) == 1:
                 return f"lcd_rseg_first({args[0]}, _lcd_seg_base)"
+            if name == "_lcd_pair_at" and len(args) == 2:
+                return (f"_lcd_pair[_lcd_pair_row + (({args[0]}) - _lcd_seg_base)"
+                        f" * _lcd_seg_own + (({args[1]}) - _lcd_seg_base)]")
             if (name == "_lcd_raw" and self.published is not None
                     and self.segment.get("registers")):
                 target = node.args[0]

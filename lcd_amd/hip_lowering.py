@@ -100,10 +100,12 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                  publish_values=True, look_ahead=True, segment_capacity=None,
                  pipeline_fetch=True, full_fences=False,
                  dynamic_fetch=False, tile_positions=None,
-                 tile_by_position=False, segment_registers=False):
+                 tile_by_position=False, segment_registers=False,
+                 pair_tables=True):
         self.tile_positions = tile_positions
         self.tile_by_position = tile_by_position
         self.segment_registers = segment_registers
+        self.pair_tables = pair_tables
         # full_fences: agent-scope release/acquire fences of the HIP memory
         # model (L2 write-back / invalidate per hand-off) instead of the
         # wait-for-completion scheme; dynamic_fetch: the flat queue hands out
@@ -342,6 +344,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                                "buffer": "_lcd_pub"}
             kinds.arrays["_lcd_pub"] = FLOAT
         self._segment_registers_plan(body)
+        self._structure_tables = self._pair_table_plan(body)
         if self.tile_rows:
             self._tile = self._tile_plan(target_loop)
         if (self.task_records and self._mailbox is not None
@@ -382,6 +385,10 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
         for name in lookup_names:
             if name not in user_arguments:
                 user_arguments.append(name)
+        for entry in self._structure_tables:
+            user_arguments.append(entry[1])
+            if entry[0] == "pair":
+                user_arguments.append("_lcd_pair_base")
         if (self.thread_loop_iterator is not None
                 and self.dependence_protocol != COUNTER_DEPENDENCE
                 and self._sequential_pull is None):
@@ -483,6 +490,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                              if self._segment else None),
             segment_registers=bool(self._segment
                                    and self._segment.get("registers")),
+            structure_tables=tuple(self._structure_tables),
             spin_limit=self.spin_limit,
             queue_node_loads=tuple(self._queue_node_loads),
             published_array=(self._published["array"]
@@ -938,6 +946,8 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                 *([f"    LCD_T_{array} _lcd_rseg = 0.0;",
                    "    (void)_lcd_seg_limit;"]
                   if self._segment.get("registers") else []),
+                *(["    lcd_index_t _lcd_pair_row = 0;"]
+                  if self._segment.get("pair_row") else []),
             ]
         lines.append(f"    lcd_index_t {it} = 0;")
         lines += self._declarations(local_names, 1)
@@ -1449,7 +1459,7 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
                  publish_values=True, look_ahead=True, segment_capacity=None,
                  pipeline_fetch=True, full_fences=False, dynamic_fetch=False,
                  tile_positions=None, tile_by_position=False,
-                 segment_registers=False):
+                 segment_registers=False, pair_tables=True):
     """HIP counterpart of ``lower_to_numba_cuda``
     (compiler/cuda_lowering.py:2854-2884); same parameters plus
     ``task_lanes`` (lanes cooperating on one task, a power of two <= 64),
@@ -1478,5 +1488,5 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
         pipeline_fetch=pipeline_fetch, full_fences=full_fences,
         dynamic_fetch=dynamic_fetch, tile_positions=tile_positions,
         tile_by_position=tile_by_position,
-        segment_registers=segment_registers)
+        segment_registers=segment_registers, pair_tables=pair_tables)
     return lowerer.lower(code)

@@ -133,6 +133,7 @@ EXPORTED_SYMBOLS = (
     "lcdhip_dag_download", "lcdhip_dag_destroy", "lcdhip_dag_band_chains",
     "lcdhip_dag_tile_order", "lcdhip_dag_tile_locality",
     "lcdhip_dag_box_order", "lcdhip_dag_edge_offsets",
+    "lcdhip_pair_lookup_build",
     "lcdhip_dag_task_records",
     "lcdhip_lookup_build", "lcdhip_gather_i32",
     "lcdhip_digest", "lcdhip_digest_noalloc",
@@ -702,6 +703,38 @@ class HIPDevice:
             ctypes.c_int64(idx_size), ctypes.c_void_p(out.pointer),
             self.stream))
         return out
+
+    def pair_lookup_entries(self, pointers, indices):
+        """Entries a pair table of this structure would have (the sum of the
+        squared segment lengths)."""
+        keep = []
+        d_ptr, ptr_size = self._resident_int32(pointers, keep)
+        d_idx, idx_size = self._resident_int32(indices, keep)
+        entries = ctypes.c_int64()
+        _check(self.lib.lcdhip_pair_lookup_build(
+            ctypes.c_void_p(d_ptr), ctypes.c_void_p(d_idx),
+            ctypes.c_int64(ptr_size - 1), ctypes.c_int64(idx_size), None, None,
+            ctypes.c_int64(0), ctypes.byref(entries), self.stream))
+        return int(entries.value)
+
+    def pair_lookup_build(self, pointers, indices):
+        """``(base, table)``: for segment s with entries a, b,
+        ``table[base[s] + a * len + b]`` is the position in segment
+        ``indices[pointers[s] + a]`` of the index ``indices[pointers[s] +
+        b]``, or -1."""
+        keep = []
+        d_ptr, ptr_size = self._resident_int32(pointers, keep)
+        d_idx, idx_size = self._resident_int32(indices, keep)
+        n = ptr_size - 1
+        entries = self.pair_lookup_entries(pointers, indices)
+        base = self.empty((n + 1,), np.int32)
+        table = self.empty((max(entries, 1),), np.int32)
+        _check(self.lib.lcdhip_pair_lookup_build(
+            ctypes.c_void_p(d_ptr), ctypes.c_void_p(d_idx), ctypes.c_int64(n),
+            ctypes.c_int64(idx_size), ctypes.c_void_p(base.pointer),
+            ctypes.c_void_p(table.pointer), ctypes.c_int64(entries),
+            ctypes.byref(entries_out := ctypes.c_int64()), self.stream))
+        return base, table
 
     def gather_int32(self, source, index, offset=0):
         """``source[index[q] + offset]`` for every ``q``, on the device."""

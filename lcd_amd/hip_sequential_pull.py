@@ -56,7 +56,8 @@ class SequentialPullMixin:
             calls = [sub for sub in ast.walk(statement)
                      if isinstance(sub, ast.Call)]
             if any(not (isinstance(call.func, ast.Name)
-                        and call.func.id == "_lcd_sorted_find")
+                        and call.func.id in ("_lcd_sorted_find",
+                                             "_lcd_pair_at"))
                    for call in calls):
                 break
             if calls and searches is None:
@@ -141,6 +142,8 @@ class SequentialPullMixin:
         for local in names:
             kinds.locals[f"_nx_{local}"] = kinds.locals.get(local, INT)
             self._own_registers.append(f"_nx_{local}")
+        table_names = {entry[1] for entry in self._structure_tables}
+        index_arrays = {entry[3] for entry in self._structure_tables}
 
         def ahead(offset):
             position = (ast.Name(id=name, ctx=ast.Load()) if offset == 0 else
@@ -159,7 +162,7 @@ class SequentialPullMixin:
             shifted = [Shift().visit(deepcopy(statement))
                        for statement in before]
             body = [Shift().visit(deepcopy(statement)) for statement in structure]
-            if leave is not None:
+            if leave is not None and not speculative:
                 body = [ast.If(test=ast.UnaryOp(
                     op=ast.Not(), operand=Shift().visit(
                         deepcopy(leading[leave].test))), body=body, orelse=[])]
@@ -168,6 +171,19 @@ class SequentialPullMixin:
                                  comparators=[deepcopy(upper)]),
                 body=shifted + body, orelse=[]))
 
+        # With the structure searches in tables every address the located
+        # statements read depends on positions of the task's own segment
+        # (inside it whenever the position is): they need not wait for the
+        # test that leaves the loop, which depends on a load itself.
+        speculative = bool(self._structure_tables) and not any(
+            isinstance(sub, ast.Call) and isinstance(sub.func, ast.Name)
+            and sub.func.id == "_lcd_sorted_find"
+            for statement in structure for sub in ast.walk(statement)) and all(
+                isinstance(sub.value, ast.Name)
+                and (sub.value.id in table_names
+                     or sub.value.id in index_arrays)
+                for statement in structure for sub in ast.walk(statement)
+                if isinstance(sub, ast.Subscript))
         rest = list(node.body[split:])
         leading_loads = self._split_leading_loads(rest)
         first_loads = list(fetched) + leading_loads
@@ -278,7 +294,8 @@ class SequentialPullMixin:
                      if isinstance(sub, ast.Call)]
             if reads_written or any(
                     not (isinstance(call.func, ast.Name)
-                         and call.func.id == "_lcd_sorted_find")
+                         and call.func.id in ("_lcd_sorted_find",
+                                              "_lcd_pair_at"))
                     for call in calls):
                 break
             structural.append(statement)

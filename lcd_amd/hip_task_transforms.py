@@ -286,6 +286,127 @@ class TaskTransformMixin:
         plan["registers"] = True
         plan["capacity"] = 64
 
+    def _pair_table_plan(self, body):
+        """With the own segment in registers (every segment of the structure
+        has at most 64 entries) the searches the task makes per producer are
+        read from tables the inspector builds once per structure:
+
+        * ``L[k]`` with ``k = IDX[p]``, ``p`` the position in the own segment
+          the sequential producer loop is at and ``L`` a structural lookup
+          table over (PTR, IDX): ``_lcd_at_<L>[p]`` (the table gathered
+          through IDX);
+        * ``find(IDX, PTR[k], PTR[k + 1], j)`` with ``j = IDX[q]``, ``q`` the
+          distributed loop's position in the own segment:
+          ``_lcd_pair[_lcd_pair_base[i] + (p - PTR[i]) * len + (q - PTR[i])]``.
+
+        Every address then depends on the task's own positions alone: the
+        chain producer id -> its segment bounds -> its entries (three
+        dependent loads per producer) is gone.  The rewrite is in place;
+        returns the tables the runtime has to provide."""
+        plan, pull = self._segment, self._sequential_pull
+        if not (self.pair_tables and plan is not None and plan.get("registers")
+                and pull is not None and self.thread_loop_iterator is not None):
+            return ()
+        pointer, owned = plan["pointer"], plan["owned"]
+        outer_name, inner_name = pull["iterator"], self.thread_loop_iterator
+        if outer_name not in owned or inner_name not in owned:
+            return ()
+        outer = next((s for s in body if isinstance(s, ast.For)
+                      and isinstance(s.target, ast.Name)
+                      and s.target.id == outer_name), None)
+        if outer is None:
+            return ()
+        inner = next((n for n in ast.walk(outer) if isinstance(n, ast.For)
+                      and isinstance(n.target, ast.Name)
+                      and n.target.id == inner_name), None)
+        written = self._all_written
+        lookups = {lookup.name: lookup for lookup in self.structural_lookups}
+
+        def gathered(statements, position):
+            """name -> IDX for the single assignments ``name = IDX[position]``
+            of a loop body."""
+            found, counts = {}, {}
+            for node in ast.walk(ast.Module(body=list(statements),
+                                            type_ignores=[])):
+                if isinstance(node, ast.Name) and isinstance(node.ctx, ast.Store):
+                    counts[node.id] = counts.get(node.id, 0) + 1
+            for statement in statements:
+                if (isinstance(statement, ast.Assign)
+                        and len(statement.targets) == 1
+                        and isinstance(statement.targets[0], ast.Name)
+                        and isinstance(statement.value, ast.Subscript)
+                        and isinstance(statement.value.value, ast.Name)
+                        and statement.value.value.id not in written
+                        and isinstance(statement.value.slice, ast.Name)
+                        and statement.value.slice.id == position
+                        and counts.get(statement.targets[0].id) == 1):
+                    found[statement.targets[0].id] = statement.value.value.id
+            return found
+
+        producers = gathered(outer.body, outer_name)
+        columns = gathered(inner.body, inner_name) if inner is not None else {}
+        tables = []
+
+        def table_for(kind, *key):
+            for entry in tables:
+                if entry[0] == kind and entry[2:] == key:
+                    return entry[1]
+            name = (f"_lcd_at_{key[0]}" if kind == "at" else "_lcd_pair")
+            tables.append((kind, name, *key))
+            return name
+
+        class Rewrite(ast.NodeTransformer):
+            def visit_Subscript(self, node):
+                node = self.generic_visit(node)
+                lookup = (lookups.get(node.value.id)
+                          if isinstance(node.value, ast.Name) else None)
+                if (lookup is not None and isinstance(node.slice, ast.Name)
+                        and producers.get(node.slice.id) == lookup.index_array
+                        and isinstance(node.ctx, ast.Load)):
+                    name = table_for("at", lookup.name, lookup.index_array)
+                    return ast.copy_location(ast.Subscript(
+                        value=ast.Name(id=name, ctx=ast.Load()),
+                        slice=ast.Name(id=outer_name, ctx=ast.Load()),
+                        ctx=ast.Load()), node)
+                return node
+
+            def visit_Call(self, node):
+                node = self.generic_visit(node)
+                if not (isinstance(node.func, ast.Name)
+                        and node.func.id == "_lcd_sorted_find"
+                        and len(node.args) == 4):
+                    return node
+                index, low, high, key = node.args
+                if not (isinstance(index, ast.Name)
+                        and isinstance(key, ast.Name)
+                        and columns.get(key.id) == index.id
+                        and isinstance(low, ast.Subscript)
+                        and isinstance(low.value, ast.Name)
+                        and low.value.id == pointer
+                        and isinstance(low.slice, ast.Name)
+                        and producers.get(low.slice.id) == index.id
+                        and isinstance(high, ast.Subscript)
+                        and ast.unparse(high) == f"{pointer}[{low.slice.id} + 1]"):
+                    return node
+                table_for("pair", pointer, index.id)
+                return ast.copy_location(ast.Call(
+                    func=ast.Name(id="_lcd_pair_at", ctx=ast.Load()),
+                    args=[ast.Name(id=outer_name, ctx=ast.Load()),
+                          ast.Name(id=inner_name, ctx=ast.Load())],
+                    keywords=[]), node)
+
+        Rewrite().visit(outer)
+        ast.fix_missing_locations(outer)
+        if not any(entry[0] == "pair" for entry in tables):
+            # (the gathered lookup alone moves one load; not worth a table)
+            pass
+        for entry in tables:
+            self._kinds.arrays[entry[1]] = INT
+        if any(entry[0] == "pair" for entry in tables):
+            self._kinds.arrays["_lcd_pair_base"] = INT
+            plan["pair_row"] = True
+        return tuple(tables)
+
     def _segment_lines(self):
         """(prologue, epilogue) of a task that stages its own segment."""
         plan = self._segment
@@ -317,6 +438,8 @@ class TaskTransformMixin:
                 f"_lcd_rseg = _lane < _lcd_seg_own ? {array}[_lcd_seg_base + "
                 "_lane] : 0.0;",
                 "if (_lane < _lcd_seg_own) _lcd_seg[_lane] = _lcd_rseg;",
+                *([f"_lcd_pair_row = _lcd_pair_base[{it}];"]
+                  if plan.get("pair_row") else []),
             ]
             epilogue = [
                 "if (_lane < _lcd_seg_own) { lcd_pub_st(_lcd_pub, _lcd_ptile, "

@@ -158,7 +158,9 @@ class SchedulePlan:
     single_chunk: bool = False       # no task has more in-edges than lanes
     task_records: bool = True        # record arrays fit 32-bit indices
     tile_boxes: tuple | None = None  # (grid, box): tiles are boxes of a grid
-    segment_registers: bool = False  # own segments (<= 64 entries) in registers
+    # own segments (<= 64 entries) in registers: 0 no, 1 yes, 2 with the
+    # structure searches of the producer loop read from tables
+    segment_registers: int = 0
 
 
 # Tiled executor, automatic choice: tiles of 4096 consecutive block-iterator
@@ -214,6 +216,13 @@ def automatic_tile_rows(dag):
     if dag.tile_locality(rows) < TILE_MIN_LOCALITY:
         return None
     return rows
+
+
+# Pair tables hold one entry per pair of positions of a segment (9-point grid:
+# 81 per row, 8.6 per stored position; 64 at most with segments of up to 64
+# entries).  Beyond this many per stored position the structure keeps its
+# searches in the kernel.
+PAIR_TABLE_ENTRIES_PER_POSITION = 24
 
 
 def structured_grid(dag):

@@ -488,6 +488,61 @@ def test_lookup_table(device, oracle):
     assert info.value.code == hip_runtime.ERR_LOOKUP_ORDER
 
 
+def test_pair_lookup_table(device):
+    """For every pair of entries (a, b) of a segment: where segment
+    indices[a] holds the index indices[b] -- what ILU0 searches per pivot and
+    updated entry -- against a literal search over the rows."""
+    from lcd_amd import hip_runtime
+
+    def literal(indptr, indices):
+        n = len(indptr) - 1
+        lengths = np.diff(indptr)
+        base = np.zeros(n + 1, dtype=np.int64)
+        np.cumsum(lengths.astype(np.int64) ** 2, out=base[1:])
+        table = np.full(int(base[-1]), -1, dtype=np.int32)
+        for s in range(n):
+            start, length = indptr[s], lengths[s]
+            for a in range(length):
+                k = indices[start + a]
+                if not 0 <= k < n:
+                    continue
+                row = indices[indptr[k]:indptr[k + 1]].tolist()
+                for b in range(length):
+                    key = indices[start + b]
+                    if key in row:
+                        table[base[s] + a * length + b] = indptr[k] + row.index(key)
+        return base, table
+
+    cases = [workloads.configuration("c4", nx=9, ny=7),
+             workloads.configuration("c3", n=300, seed=5)]
+    for work in cases:
+        print("pair table", work.name, flush=True)
+        expected_base, expected = literal(work.indptr, work.indices)
+        assert device.pair_lookup_entries(work.indptr, work.indices) == len(expected)
+        base, table = device.pair_lookup_build(work.indptr, work.indices)
+        np.testing.assert_array_equal(base.copy_to_host(), expected_base)
+        np.testing.assert_array_equal(table.copy_to_host()[:len(expected)],
+                                      expected)
+    # an empty segment, an index beyond the segments (no segment to search)
+    indptr = np.array([0, 2, 2, 5], dtype=np.int32)
+    indices = np.array([0, 2, 0, 1, 7], dtype=np.int32)
+    base, table = device.pair_lookup_build(indptr, indices)
+    assert base.copy_to_host().tolist() == [0, 4, 4, 13]
+    assert table.copy_to_host()[:13].tolist() == [
+        0, 1, 2, -1,                     # segment 0: rows 0 and 2 searched
+        0, -1, -1, -1, -1, -1, -1, -1, -1]   # segment 2: rows 0, 1 (empty), 7
+    # more than 1024 segments: the scan of the squares runs in chunks
+    work = workloads.configuration("c1")
+    expected_base, expected = literal(work.indptr, work.indices)
+    base, table = device.pair_lookup_build(work.indptr, work.indices)
+    np.testing.assert_array_equal(base.copy_to_host(), expected_base)
+    np.testing.assert_array_equal(table.copy_to_host()[:len(expected)], expected)
+    assert device.pair_lookup_entries([0], np.zeros(0, dtype=np.int32)) == 0
+    with pytest.raises(hip_runtime.HIPRuntimeError) as info:
+        device.pair_lookup_build([0, 3, 2], [0, 1, 2])
+    assert info.value.code == hip_runtime.ERR_LOOKUP_POINTER
+
+
 def test_digest_is_content_sensitive(device):
     a = device.to_device(np.arange(10000, dtype=np.int32))
     b = device.to_device(np.arange(10000, dtype=np.int32))

@@ -850,7 +850,8 @@ def test_own_segment_in_registers():
                    function_props=props, structural_lookups=lookups)
     from lcd_amd.hip_lowering import lower_to_hip
     staged = lower_to_hip(module, **options)
-    held = lower_to_hip(module, segment_registers=True, **options)
+    held = lower_to_hip(module, segment_registers=True, pair_tables=False,
+                        **options)
     assert staged.segment_pointer == held.segment_pointer == "A_indptr"
     assert not staged.segment_registers and held.segment_registers
     text = held.kernel_source
@@ -871,6 +872,29 @@ def test_own_segment_in_registers():
     # a row that is longer after all stops the launch
     assert "if (_lcd_seg_own > 64) { _lcd_status[0] = 1;" in text
     hip_runtime.compile_code(held.source)
+    assert held.structure_tables == () == staged.structure_tables
+    # ... and with it the searches of the pivot loop come from tables keyed
+    # by the task's own positions: the diagonal of pivot row A_indices[k_ptr]
+    # by k_ptr, the place of column A_indices[j_ptr] in that row by the pair
+    tabled = lower_to_hip(module, segment_registers=True, **options)
+    assert tabled.structure_tables == (
+        ("at", "_lcd_at__lcd_lookup_position_0", "_lcd_lookup_position_0",
+         "A_indices"),
+        ("pair", "_lcd_pair", "A_indptr", "A_indices"))
+    for name in ("_lcd_at__lcd_lookup_position_0", "_lcd_pair",
+                 "_lcd_pair_base"):
+        assert tabled.kernel_arguments.count(name) == 1
+        assert name in tabled.launcher_arguments
+    text = tabled.kernel_source
+    assert "lcd_sorted_find(" not in text
+    assert "_lcd_pair_row = _lcd_pair_base[i];" in text
+    assert "_nx_diag_ptr = _lcd_at__lcd_lookup_position_0[(k_ptr + 1)];" in text
+    assert ("_nx__sp_kj_ptr = _lcd_pair[_lcd_pair_row + (((k_ptr + 1)) - "
+            "_lcd_seg_base) * _lcd_seg_own + ((_nx__sp_first) - "
+            "_lcd_seg_base)];") in text
+    hip_runtime.compile_code(tabled.source)
+    # (without registers the tables are not used: segments may be long)
+    assert lower_to_hip(module, **options).structure_tables == ()
     # eight lanes per row: rows share a wavefront, registers do not apply
     narrow = lower_to_hip(module, segment_registers=True,
                           **{**options, "task_lanes": 8})
