@@ -8,6 +8,7 @@ from copy import deepcopy
 from lcd_amd.hip_emitter import (
     FLOAT,
     INT,
+    STATUS_ARGUMENT,
     VALUE_WAIT_BEGIN,
     VALUE_WAIT_END,
 )
@@ -202,10 +203,48 @@ class SequentialPullMixin:
         # values are here, was slower: 8.2 against 7.2 ms on the 9-point
         # grid -- most come back empty, and every extra coherent load slows
         # the hand-offs.)
-        for child in first_loads + [ahead(1)] + rest:
+        for child in first_loads + [ahead(1)]:
             lines += self._emit_guarded(child, emitter, 1, hooks)
+        # the statements that wait for the leading loads (the producer's
+        # diagonal) come first in the rest; behind the last of them the
+        # lanes' own first loads get their second attempt
+        again = (self._second_attempts(fetched, emitter)
+                 if leading_loads else [])
+        for position, child in enumerate(rest):
+            lines += self._emit_guarded(child, emitter, 1, hooks)
+            if position == len(leading_loads) - 1:
+                for guard, register, load in again:
+                    lines.append(f"    if (({guard}) && lcd_is_empty({register})) "
+                                 f"{register} = {load};")
         lines += ["}", VALUE_WAIT_END]
         return lines
+
+    def _second_attempts(self, first_loads, emitter):
+        """Second attempt of an iteration's first loads, once, behind the
+        wait for the first of them.  A producer stores its entries with one
+        instruction, so a diagonal that was not there yet means the lane's
+        other entry was not either; its second attempt used to start where
+        the value is used, behind the division, one more round trip on the
+        chain between two levels.  Now it leaves as soon as the diagonal is
+        in and arrives while the division runs.  (Polling all of them in one
+        loop until the last has arrived was slower, 4.92 against 4.20 ms on
+        the 9-point grid: every additional coherent load per poll slows
+        everybody's hand-offs.)"""
+        waits = []
+        for statement in first_loads:
+            guard = "1"
+            if isinstance(statement, ast.If):
+                guard = emitter.expr(statement.test)
+                statement = statement.body[0]
+            if not (isinstance(statement, ast.Assign)
+                    and isinstance(statement.targets[0], ast.Name)
+                    and isinstance(statement.value, ast.Call)
+                    and isinstance(statement.value.func, ast.Name)
+                    and statement.value.func.id == "_lcd_raw"):
+                return []
+            waits.append((guard, statement.targets[0].id,
+                          emitter.expr(statement.value)))
+        return waits
 
     def _split_leading_loads(self, rest):
         """Leading statements of the form ``[if structure:] x = X[p]`` (the
