@@ -595,6 +595,65 @@ def test_ilu0_published_values_on_long_rows(oracle, n, capacity):
                                    rtol=1e-12, atol=1e-12)
 
 
+@pytest.mark.parametrize("seed,tiles", [(1, None), (2, 300), (3, None)])
+def test_ilu0_irregular_rows_in_registers(oracle, seed, tiles):
+    """Rows in registers and searches from the inspector's tables on a
+    structure that is no stencil: unsymmetric random pattern with rows of 0 to
+    30 entries, rows without a diagonal entry (the pivot is skipped), exact
+    zeros on the diagonal (skipped as well), pivot rows that lack most of the
+    columns a row holds; the same plan factorises two sets of values."""
+    import scipy.sparse as sp
+    print("irregular ilu0", seed, tiles, flush=True)
+    rng = np.random.default_rng(seed)
+    n = 4000
+    rows, cols = [], []
+    for i in range(n):
+        count = int(rng.integers(0, 25))
+        near = rng.integers(max(0, i - 60), min(n, i + 60), size=count)
+        far = rng.integers(0, n, size=count // 6)
+        picks = set(np.concatenate([near, far]).tolist())
+        if rng.random() < 0.9:
+            picks.add(i)              # most rows have their diagonal entry
+        picks = sorted(picks)[:64]
+        rows += [i] * len(picks)
+        cols += picks
+    values = rng.uniform(-1.0, 1.0, len(rows))
+    matrix = sp.csr_matrix((values, (rows, cols)), shape=(n, n))
+    matrix.sort_indices()
+    indptr = matrix.indptr.astype(np.int32)
+    indices = matrix.indices.astype(np.int32)
+    assert np.diff(indptr).max() <= 64 and np.diff(indptr).min() == 0
+    factor = spilu0.compile_ilu0_csr(
+        execution_mode="sync_free", threads_per_block=256, task_lanes=64,
+        dependence_protocol="pull",
+        **({"tile_rows": tiles, "tile_positions": 8192} if tiles else {}))
+    for launch in range(2):
+        data = rng.uniform(-1.0, 1.0, len(values))
+        diagonal = indices == np.repeat(np.arange(n), np.diff(indptr))
+        data[diagonal] += 8.0 * np.sign(data[diagonal])
+        # exact zeros on some diagonals: those pivots are left alone
+        data[np.nonzero(diagonal)[0][::17]] = 0.0
+        expected = oracle.ilu0_csr(data.copy(), indices, indptr)
+        assert np.all(np.isfinite(expected))
+        result = factor(data.copy(), indices, indptr)
+        np.testing.assert_array_equal(result, expected)
+    plan = factor.schedule_plan(data, indices, indptr)
+    assert plan.segment_registers == 2
+    assert factor.hip_lowering.segment_registers
+    assert factor.hip_lowering.structure_tables
+    assert "lcd_sorted_find(" not in factor.hip_kernel_source
+    # the same structure with the searches left in the kernel, and with the
+    # rows staged in LDS: the same bits
+    for options in (dict(pair_tables=False), dict(segment_registers=False)):
+        other = spilu0.compile_ilu0_csr(
+            execution_mode="sync_free", threads_per_block=128, task_lanes=64,
+            dependence_protocol="pull", **options)
+        np.testing.assert_array_equal(other(data.copy(), indices, indptr),
+                                      expected)
+        assert other.schedule_plan(data, indices, indptr).segment_registers == (
+            1 if "pair_tables" in options else 0)
+
+
 @pytest.mark.parametrize("variant", ["simple", "full"])
 def test_gauss_seidel_two_sweeps(oracle, variant):
     from scipy.sparse import csr_matrix
