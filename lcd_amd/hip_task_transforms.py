@@ -103,10 +103,10 @@ class TaskTransformMixin:
             # buffer, positions P[row0] .. P[row0 + rows), has a copy in LDS;
             # a tile whose slice is longer than the copy runs without it
             positions = self.tile_positions or min(16 * rows, 8192)
-            if not isinstance(positions, int) or not 0 < positions <= 16384:
+            if not isinstance(positions, int) or not 0 < positions <= 19456:
                 raise HIPLoweringError(
                     "tile_positions must be a positive integer of at most "
-                    "16384 (128 KB of LDS).")
+                    "19456 (152 KB of LDS).")
             return {"array": self._published["array"], "rows": rows,
                     "published": True, "positions": positions,
                     "pointer": self._segment["pointer"]}
