@@ -107,6 +107,14 @@ class TaskTransformMixin:
                 raise HIPLoweringError(
                     "tile_positions must be a positive integer of at most "
                     "19456 (152 KB of LDS).")
+            # the staged rows share the workgroup's LDS (160 KB) with the copy
+            groups = max(1, self.threads_per_block // self.task_lanes)
+            room = (160 * 1024 - 1024 - 8 * positions) // (8 * groups)
+            if room < 8:
+                raise HIPLoweringError(
+                    f"tile_positions={positions} leaves no LDS for the rows "
+                    f"of {groups} tasks per workgroup.")
+            self._segment["capacity"] = min(self._segment["capacity"], room)
             return {"array": self._published["array"], "rows": rows,
                     "published": True, "positions": positions,
                     "pointer": self._segment["pointer"]}
