@@ -59,6 +59,9 @@ from lcd_amd.scheduler import (
     CalibratedScheduler,
     SchedulePlan,
     PAIR_TABLE_ENTRIES_PER_POSITION,
+    PUBLISHED_TILE_MIN_LOCALITY,
+    PUBLISHED_TILE_POSITIONS,
+    PUBLISHED_TILE_THREADS_PER_BLOCK,
     TILE_BOX_THREADS_PER_BLOCK,
     TILE_THREADS_PER_BLOCK,
     automatic_tile_box,
@@ -273,7 +276,20 @@ def parallel(**kwargs):
                     lowering, function_globals=function.__globals__)
             return lowering, compiled_variants[variant_key]
 
-        def tiles_for(dag, schedule):
+        def segment_lengths(pointer_name, values):
+            """(longest, mean) segment length of a pointer array of this
+            structure, or None when the array is not among the values."""
+            pointers = values.get(pointer_name)
+            if pointers is None:
+                return None
+            if hip_runtime.is_device_array(pointers):
+                pointers = pointers.copy_to_host()
+            lengths = np.diff(np.asarray(pointers))
+            if len(lengths) == 0:
+                return 0, 0.0
+            return int(lengths.max()), float(lengths.mean())
+
+        def tiles_for(dag, schedule, values):
             """(schedule, tile_rows): the tiled persistent executor when it
             is asked for, or pays for this DAG, and the loop allows it."""
             if (schedule.execution_mode != SYNC_FREE or band_width != 1
@@ -293,14 +309,34 @@ def parallel(**kwargs):
             if variant.tile_rows is None:
                 return schedule, None        # tiles do not apply to this loop
             if tile_option == "auto" and variant.published_array is not None:
-                # published pull (ILU0): tiles pay only with many wavefronts
-                # per tile and rows sized to the grid lines (6.4 against
-                # 7.1 ms on the 9-point 1024^2 grid at 1024 rows and 512
-                # threads, 38 ms at the sizes chosen for SpTRSV): by request
-                return schedule, None
+                # published pull (ILU0): tiles pay with many wavefronts per
+                # tile, rows short enough to live in registers, a tile whose
+                # slice of the publication buffer fits the LDS copy, and a
+                # structure in which consecutive rows depend on each other
+                # (9-point 1024^2 grid: 4.1 against 5.4 ms; 38 ms at the
+                # sizes chosen for SpTRSV)
+                if registers_option is False:
+                    return schedule, None
+                stats = segment_lengths(variant.segment_pointer, values)
+                if stats is None or stats[0] > 64 or stats[1] <= 0:
+                    return schedule, None
+                rows = int(0.9 * PUBLISHED_TILE_POSITIONS / stats[1])
+                rows = max(64, min(rows, 2048))
+                if (dag.n < 4 * rows
+                        or dag.tile_locality(rows) < PUBLISHED_TILE_MIN_LOCALITY):
+                    return schedule, None
+                tiled = schedule
+                if (kwargs.get("threads_per_block") is None
+                        and not PUBLISHED_TILE_THREADS_PER_BLOCK
+                        % max(schedule.task_lanes, 1)):
+                    tiled = replace(schedule, threads_per_block=(
+                        PUBLISHED_TILE_THREADS_PER_BLOCK))
+                variant = lower_variant(tiled.lowering_key, rows)
+                if variant.tile_rows is None:
+                    return schedule, None
             return tiled, rows
 
-        def registers_for(schedule, rows, values, lookups):
+        def registers_for(schedule, rows, values, lookups, dag_rows):
             """(level, tables) for this plan.  Level 1: the tasks' own
             segments (ILU0's rows) live in registers -- the loop allows it
             and no segment of this structure has more than 64 entries.  Level
@@ -317,14 +353,10 @@ def parallel(**kwargs):
                 return 0, {}
             if not variant.segment_registers:
                 return 0, {}
-            pointers = values.get(variant.segment_pointer)
-            if pointers is None:
+            stats = segment_lengths(variant.segment_pointer, values)
+            if stats is None:
                 return 0, {}
-            host_pointers = (pointers.copy_to_host()
-                             if hip_runtime.is_device_array(pointers)
-                             else np.asarray(pointers))
-            longest = (int(np.max(np.diff(host_pointers)))
-                       if len(host_pointers) > 1 else 0)
+            longest = stats[0]
             if longest > 64:
                 if registers_option is True:
                     raise ValueError(
@@ -346,7 +378,7 @@ def parallel(**kwargs):
                             lookups[lookup], values[index_array])
                     else:
                         _, name, pointer_array, index_array = entry
-                        positions = max(int(host_pointers[-1]), 1)
+                        positions = max(int(round(stats[1] * dag_rows)), 1)
                         entries = device.pair_lookup_entries(
                             values[pointer_array], values[index_array])
                         if entries > PAIR_TABLE_ENTRIES_PER_POSITION * positions:
@@ -524,7 +556,7 @@ def parallel(**kwargs):
                     thread_trip_counts=trip_counts(dag_values),
                     edges=dag.edges)
                 schedule = scheduler.schedule(features, schedule_space)
-            schedule, tile_rows = tiles_for(dag, schedule)
+            schedule, tile_rows = tiles_for(dag, schedule, device_values)
             lowering = lower_variant(schedule.lowering_key, tile_rows)
             # the record arrays are indexed with 32 bits
             records = (not lowering.task_record_lanes
@@ -570,7 +602,8 @@ def parallel(**kwargs):
                     tile_rows=lowering.tile_rows,
                     record_lanes=lowering.task_record_lanes)
             segment_registers, structure_tables = (
-                registers_for(schedule, tile_rows, device_values, lookup_values)
+                registers_for(schedule, tile_rows, device_values, lookup_values,
+                              dag.n)
                 if tile_boxes is None else (0, {}))
             plan = SchedulePlan(
                 schedule=schedule,

@@ -102,7 +102,7 @@ class TaskTransformMixin:
             # published pull (ILU0): the tile's slice of the publication
             # buffer, positions P[row0] .. P[row0 + rows), has a copy in LDS;
             # a tile whose slice is longer than the copy runs without it
-            positions = self.tile_positions or min(16 * rows, 8192)
+            positions = self.tile_positions or min(16 * rows, 9216)
             if not isinstance(positions, int) or not 0 < positions <= 19456:
                 raise HIPLoweringError(
                     "tile_positions must be a positive integer of at most "

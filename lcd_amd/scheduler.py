@@ -225,6 +225,16 @@ def automatic_tile_rows(dag):
 PAIR_TABLE_ENTRIES_PER_POSITION = 24
 
 
+# Tiles of the published pull (ILU0), automatic choice: a tile's slice of the
+# publication buffer has a copy of 9216 entries in LDS (72 KB: two workgroups
+# per CU), so a tile holds 0.9 x 9216 / (mean row length) rows; ten wavefronts
+# per tile; only where at least a fifth of the DAG's edges stay inside such a
+# tile (the 9-point grid keeps one in four: the row before).
+PUBLISHED_TILE_POSITIONS = 9216
+PUBLISHED_TILE_THREADS_PER_BLOCK = 640
+PUBLISHED_TILE_MIN_LOCALITY = 0.2
+
+
 def structured_grid(dag):
     """``(nx, ny, nz)`` when the DAG's edges are those of an axis stencil on
     a grid in natural order (id = x + nx * (y + ny * z)): every edge goes
