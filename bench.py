@@ -58,7 +58,7 @@ TUNED = {
                tile_rows=1024, tile_positions=9216),
     "c5": dict(execution_mode="sync_free", threads_per_block=128, task_lanes=8,
                thread_unroll=1, dependence_protocol="mailbox",
-               tile_rows=8192),
+               tile_rows=8192, spin_sleep=0),
 }
 
 
