@@ -134,6 +134,8 @@ def build_solver(work, args, config):
             else tuple(int(extent) for extent in args.tile_box.split("x")))
     if args.segment_capacity:
         options["segment_capacity"] = args.segment_capacity
+    if args.level_gather:
+        options["level_gather"] = True
     if args.no_queue_loads:
         options["queue_node_loads"] = False
     if args.plain_first is not None:
@@ -443,6 +445,10 @@ def main():
     parser.add_argument("--segment-capacity", dest="segment_capacity",
                         type=int, default=None,
                         help="entries of a task's own segment staged in LDS")
+    parser.add_argument("--level-gather", dest="level_gather",
+                        action="store_true",
+                        help="level launches gather incoming products "
+                             "instead of pushing them with atomics")
     parser.add_argument("--slots", action="store_true",
                         help="message slots instead of the gathered form of "
                              "the mailbox protocol (implies no tiles)")
@@ -523,7 +529,7 @@ def main():
                      "segment_capacity", "tile_box"):
             setattr(sub_args, name, None)
         for name in ("slots", "no_queue_loads", "no_publish", "no_pipeline",
-                     "no_graph"):
+                     "no_graph", "level_gather"):
             setattr(sub_args, name, False)
         records = {}
         for config in ("c1", "c2", "c3", "c4", "c5"):

@@ -183,6 +183,8 @@ def parallel(**kwargs):
             task_lanes=kwargs.get("task_lanes"),
         )
         band_width = kwargs.get("band_width", 1)
+        if band_width == 1:
+            space_options["level_gather"] = kwargs.get("level_gather", True)
         scheduler = kwargs.get("scheduler") or CalibratedScheduler(
             kwargs.get("arch_constants"))
         device_layer = kwargs.get("device")

@@ -216,6 +216,14 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
         required_kind = (PUSH_DEPENDENCE
                          if dependence_protocol == MAILBOX_DEPENDENCE
                          else dependence_protocol)
+        # level launches with the mailbox protocol: a task gathers its
+        # incoming products (no polls: its producers ran in earlier launches)
+        self.level_gather = (
+            dependence_protocol == MAILBOX_DEPENDENCE
+            and direct_dependence is not None
+            and direct_dependence.kind == PUSH_DEPENDENCE
+            and self.warp_mapped and self.execution_mode == "wavefront"
+            and not chain_tasks)
         self.dependence_protocol = (
             dependence_protocol
             if (direct_dependence is not None
@@ -224,7 +232,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                 and sync_free_ready_count == 0
                 # the members of a chain task wait on their counters one by
                 # one (compiler/cuda_lowering.py:1360-1410)
-                and not chain_tasks)
+                and not chain_tasks) or self.level_gather
             else COUNTER_DEPENDENCE)
         if chain_tasks:
             self.tile_rows = None
@@ -301,7 +309,10 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
         if self.dependence_protocol == MAILBOX_DEPENDENCE:
             self._mailbox = self._mailbox_plan(body)
             if self._mailbox is None:
-                self.dependence_protocol = PUSH_DEPENDENCE
+                self.dependence_protocol = (COUNTER_DEPENDENCE
+                                            if self.level_gather
+                                            else PUSH_DEPENDENCE)
+                self.level_gather = False
         self._fully_rewritten = self._fully_rewritten_arrays(
             body, target_loop, zero_initialised)
         sequential = (self.direct_dependence is not None
@@ -343,12 +354,28 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
             self._published = {"array": self._segment["array"],
                                "buffer": "_lcd_pub"}
             kinds.arrays["_lcd_pub"] = FLOAT
+        if self.level_gather:
+            if self._mailbox["gather"] is None:
+                # the loop does not fit the gathered form: atomics as before
+                self._mailbox = None
+                self.dependence_protocol = COUNTER_DEPENDENCE
+                self.level_gather = False
+            else:
+                gather = self._mailbox["gather"]
+                for name in gather["staged"].values():
+                    kinds.arrays.pop(name, None)
+                gather["staged"] = {}
+                gather["needs_position"] = True
+                self.single_chunk = False
+                # (a plain load: nothing here is still being written)
+                self.poll_load = "lcd_ld_once"
         self._segment_registers_plan(body)
         self._structure_tables = self._pair_table_plan(body)
         if self.tile_rows:
             self._tile = self._tile_plan(target_loop)
         if (self.task_records and self._mailbox is not None
-                and self._mailbox["gather"] is not None):
+                and self._mailbox["gather"] is not None
+                and not self.level_gather):
             # the first incoming edges of every task sit in fixed-size
             # records in task order, so everything a wavefront needs to start
             # polling is fetched with loads whose addresses depend on the
@@ -638,7 +665,9 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                 names = list(SYNC_FREE_ARGUMENTS)
             return names + [STATUS_ARGUMENT]
         if self.execution_mode == "wavefront":
-            return list(WAVEFRONT_ARGUMENTS)
+            return list(WAVEFRONT_ARGUMENTS) + (
+                ["_lcd_in_ptr", "_lcd_in_pos", "_lcd_in_src"]
+                if self.level_gather else [])
         return []
 
     # ---- task body
@@ -963,6 +992,24 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
             out = [f"{pad}if ({guard}) {{"]
             if self.execution_mode != "sync_free":
                 out += [pad + "    " + line for line in prefetch]
+            if self.level_gather:
+                # the producers ran in earlier launches: their values are
+                # there, the products are added in (source, position) order
+                out += [
+                    f"{pad}    const bool _pending = true;",
+                    f"{pad}    int _mb_next = _lcd_in_ptr[{it}], "
+                    f"_mb_end = _lcd_in_ptr[{it} + 1];",
+                    *self._gather_fetch_lines(indent + 1, declare=True),
+                    # (one turn per chunk of incoming edges; bounded, so that
+                    # no content of the array can keep a launch from ending)
+                    f"{pad}    const int _mb_turns = (_mb_end - _mb_next) / "
+                    "LCD_TASK_LANES + 2;",
+                    f"{pad}    for (int _mb_turn = 0; _mb_turn < _mb_turns; "
+                    "++_mb_turn) {",
+                    *self._gather_ready_lines(indent + 2),
+                    f"{pad}        if (_ready) break;",
+                    f"{pad}    }}",
+                ]
             out += [pad + "    " + line for line in (
                 task_body if body_lines is None else body_lines)]
             out.append(f"{pad}}}")

@@ -330,12 +330,17 @@ class ScheduleSpace:
     # so such a task gets a wavefront of its own (ILU0, 9-point grid:
     # 14.1 ms with 8 lanes per task, 10.9 ms with 64)
     sequential_pull: bool = False
+    # level launches of a push-shaped loop gather their incoming products
+    # instead of pushing them with atomics (the mailbox protocol's listing,
+    # without polls): deterministic sums, bit-identical to the sequential loop
+    level_gather: bool = False
 
     @classmethod
     def from_options(cls, execution_mode=None, threads_per_block=None,
                      thread_unroll=None, thread_mapped=False, n_warp=None,
                      direct_protocol=None, dependence_protocol=None,
-                     task_lanes=None, sequential_pull=False):
+                     task_lanes=None, sequential_pull=False,
+                     level_gather=False):
         mode = normalize_execution_mode(execution_mode)
         if n_warp is not None and (not isinstance(n_warp, int) or n_warp <= 0):
             raise SchedulerError("n_warp must be a positive integer.")
@@ -415,7 +420,9 @@ class ScheduleSpace:
                    unroll_factors=unroll_factors, n_warps=n_warps,
                    thread_mapped=thread_mapped,
                    dependence_protocols=protocols, task_lanes=lanes,
-                   sequential_pull=bool(sequential_pull))
+                   sequential_pull=bool(sequential_pull),
+                   level_gather=bool(level_gather)
+                   and MAILBOX_DEPENDENCE in protocols)
 
     def configurations(self):
         result = []
@@ -427,6 +434,9 @@ class ScheduleSpace:
             protocols = (
                 self.dependence_protocols
                 if (mode == SYNC_FREE and self.thread_mapped
+                    and _wave_task(block, n_warp))
+                else (MAILBOX_DEPENDENCE,)
+                if (self.level_gather and self.thread_mapped
                     and _wave_task(block, n_warp))
                 else (COUNTER_DEPENDENCE,))
             for protocol in protocols:

@@ -119,6 +119,50 @@ def test_sptrsv_csc_variants(oracle, options):
         assert "_lcd_mailbox" not in solver.hip_kernel_source
 
 
+@pytest.mark.parametrize("lanes", [1, 4, 8, 64])
+def test_level_launches_gather_their_products(oracle, lanes):
+    """Level launches of the CSC solve: a task adds the products of its
+    incoming entries itself, in the order of the sequential loop, instead of
+    its producers pushing them with atomics -- no atomics, the same bits in
+    every run and as the sequential loop; in-degrees below, at and above the
+    lanes of a task (several chunks)."""
+    print("level gather", lanes, flush=True)
+    gathered = sptrsv.compile_sptrsv_csc(
+        execution_mode="wavefront", threads_per_block=128, task_lanes=lanes,
+        thread_unroll=1)
+    pushed = sptrsv.compile_sptrsv_csc(
+        execution_mode="wavefront", threads_per_block=128, task_lanes=lanes,
+        thread_unroll=1, level_gather=False)
+    assert gathered.hip_lowering.dependence_protocol == "mailbox"
+    assert pushed.hip_lowering.dependence_protocol == "counter"
+    assert "lcd_atomic" not in gathered.hip_kernel_source
+    assert "_lcd_in_src[" in gathered.hip_kernel_source
+    assert "lcd_atomic_add" in pushed.hip_kernel_source
+    for name, overrides in (("c1", {}), ("c2", dict(nx=20, ny=18, nz=16)),
+                            ("c5", dict(n=6000))):
+        work = workloads.configuration(name, **overrides)
+        expected = oracle.sptrsv_csc(work.indptr, work.indices, work.data,
+                                     work.rhs, work.n)
+        for _ in range(2):
+            solve_and_check(gathered, work, expected, exact=True)
+        solve_and_check(pushed, work, expected)
+    # a power-law factor: hundreds of incoming entries for some rows
+    lower, diagonal, rhs = random_lower_factor(3000, 7)
+    import scipy.sparse as sp
+    matrix = sp.csc_matrix(lower + sp.diags(diagonal))
+    matrix.sort_indices()
+    indptr, indices = (matrix.indptr.astype(np.int32),
+                       matrix.indices.astype(np.int32))
+    expected = oracle.sptrsv_csc(indptr, indices, matrix.data, rhs, 3000)
+    np.testing.assert_array_equal(
+        gathered(indptr, indices, matrix.data, rhs, 3000), expected)
+    # chain tasks (band_width > 1) keep their counters
+    banded = sptrsv.compile_sptrsv_csc(
+        execution_mode="wavefront", threads_per_block=128, task_lanes=lanes,
+        thread_unroll=1, band_width=4)
+    assert banded.hip_lowering.dependence_protocol == "counter"
+
+
 @pytest.mark.parametrize("tile_rows,lanes,tpb", [(64, 4, 64), (500, 8, 128),
                                                  (4096, 4, 256), (8192, 16, 512),
                                                  (256, 2, 128)])

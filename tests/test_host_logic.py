@@ -788,6 +788,37 @@ def test_tiled_mailbox_reads_task_records():
     hip_runtime.compile_code(plain.source)
 
 
+def test_level_launches_gather_incoming_products():
+    """The level executor of a push-shaped loop with the mailbox listing: the
+    producer's loop is gone, the task walks its incoming entries in (source,
+    position) order with plain loads, in a loop that ends whatever it reads."""
+    module = demo_source("sptrsv", "sptrsv_csc_loop")
+    result = lower(module, execution_mode="wavefront",
+                   thread_loop_iterator="j", task_lanes=4,
+                   wavefront_threads_per_block=128,
+                   dependence_protocol="mailbox")
+    assert result.dependence_protocol == "mailbox"
+    assert result.kernel_arguments[-3:] == ["_lcd_in_ptr", "_lcd_in_pos",
+                                            "_lcd_in_src"]
+    assert result.reset_kernel_name is None and result.stage_kernel_name is None
+    kernel = result.kernel_source
+    assert "lcd_atomic" not in kernel and "for (j = " not in kernel
+    assert "int _mb_next = _lcd_in_ptr[i], _mb_end = _lcd_in_ptr[i + 1];" in kernel
+    assert "const double _g_value = lcd_ld_once(&x[_g_src]);" in kernel
+    assert ("for (int _mb_turn = 0; _mb_turn < _mb_turns; ++_mb_turn) {"
+            in kernel)
+    assert "if (_lane == 0) x[i] = _lcd_own_0;" in kernel
+    assert "launch_levels" in result.launcher_source
+    hip_runtime.compile_code(result.source)
+    # chain tasks wait on counters member by member: no gathered form
+    chains = lower(module, execution_mode="wavefront",
+                   thread_loop_iterator="j", task_lanes=4,
+                   wavefront_threads_per_block=128,
+                   dependence_protocol="mailbox", chain_tasks=True)
+    assert chains.dependence_protocol == "counter"
+    assert "lcd_atomic_add" in chains.kernel_source
+
+
 def test_tiles_addressed_by_queue_position():
     """Tiles that do not follow the ids (boxes of a grid): sources, LDS slots
     and the value-as-flag copy are addressed by the place in the queue."""
