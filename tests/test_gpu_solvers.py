@@ -698,6 +698,74 @@ def test_ilu0_irregular_rows_in_registers(oracle, seed, tiles):
             1 if "pair_tables" in options else 0)
 
 
+def ilu0_own_diagonal(A_data, A_indices, A_indptr):
+    """ILU0 whose updates are scaled by the row's own diagonal entry as it
+    stands at that pivot: a read of the task's own row at a position that is
+    searched for, not walked by a loop."""
+    n = len(A_indptr) - 1
+    for i in range(n):
+        row_start = A_indptr[i]
+        row_end = A_indptr[i + 1]
+        for k_ptr in range(row_start, row_end):
+            k = A_indices[k_ptr]
+            if k >= i:
+                break
+            diag_val = 0.0
+            for diag_ptr in range(A_indptr[k], A_indptr[k + 1]):
+                if A_indices[diag_ptr] == k:
+                    diag_val = A_data[diag_ptr]
+                    break
+            own = 1.0
+            for own_ptr in range(A_indptr[i], A_indptr[i + 1]):
+                if A_indices[own_ptr] == i:
+                    own = A_data[own_ptr]
+                    break
+            if diag_val != 0.0:
+                A_data[k_ptr] = A_data[k_ptr] / diag_val
+                l_ik = A_data[k_ptr]
+                for j_ptr in range(k_ptr + 1, row_end):
+                    j = A_indices[j_ptr]
+                    for kj_ptr in range(A_indptr[k], A_indptr[k + 1]):
+                        if A_indices[kj_ptr] == j:
+                            u_kj = A_data[kj_ptr]
+                            A_data[j_ptr] = (
+                                A_data[j_ptr] - l_ik * u_kj * own
+                            )
+                            break
+    return A_data
+
+
+@pytest.mark.parametrize("registers", [True, False])
+def test_own_row_read_at_a_searched_position(registers):
+    """With the own row in registers, a read of it at a computed position
+    goes to the write-only copy in LDS and sees every update made so far;
+    against the loop itself run by CPython."""
+    from lcd_amd import parallel
+    print("own row at a searched position", registers, flush=True)
+    work = workloads.configuration("c4", nx=24, ny=20)
+    rng = np.random.default_rng(9)
+    data = work.data * rng.uniform(0.05, 0.1, len(work.data))
+    diagonal = work.indices == np.repeat(np.arange(work.n),
+                                         np.diff(work.indptr))
+    data[diagonal] = rng.uniform(1.0, 1.5, int(diagonal.sum()))
+    expected = ilu0_own_diagonal(data.copy(), work.indices, work.indptr)
+    assert np.all(np.isfinite(expected))
+    factor = parallel(
+        block_map="i", thread_map="j_ptr",
+        function_props=spilu0.FUNCTION_PROPS, execution_mode="sync_free",
+        threads_per_block=128, task_lanes=64, thread_unroll=1,
+        dependence_protocol="pull",
+        segment_registers=registers)(ilu0_own_diagonal)
+    for _ in range(2):
+        result = factor(data.copy(), work.indices, work.indptr)
+        np.testing.assert_array_equal(result, expected)
+    assert factor.hip_lowering.segment_registers == registers
+    assert len(factor.structural_lookups) == 1
+    if registers:
+        assert ("own = lcd_rseg_ldp(_lcd_pub, _lcd_seg, _lcd_seg_base, "
+                "_lcd_seg_own, own_ptr") in factor.hip_kernel_source
+
+
 @pytest.mark.parametrize("variant", ["simple", "full"])
 def test_gauss_seidel_two_sweeps(oracle, variant):
     from scipy.sparse import csr_matrix
