@@ -366,7 +366,9 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                     kinds.arrays.pop(name, None)
                 gather["staged"] = {}
                 gather["needs_position"] = True
-                self.single_chunk = False
+                # the first incoming entries of a task from its record in
+                # level order: one dependent load less in front of every task
+                gather["records"] = bool(self.task_records)
                 # (a plain load: nothing here is still being written)
                 self.poll_load = "lcd_ld_once"
         self._segment_registers_plan(body)
@@ -666,7 +668,9 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
             return names + [STATUS_ARGUMENT]
         if self.execution_mode == "wavefront":
             return list(WAVEFRONT_ARGUMENTS) + (
-                ["_lcd_in_ptr", "_lcd_in_pos", "_lcd_in_src"]
+                ["_lcd_in_ptr", "_lcd_in_pos", "_lcd_in_src",
+                 *(RECORD_ARGUMENTS if self._mailbox["gather"].get("records")
+                   else ())]
                 if self.level_gather else [])
         return []
 
@@ -995,11 +999,15 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
             if self.level_gather:
                 # the producers ran in earlier launches: their values are
                 # there, the products are added in (source, position) order
+                records = self._mailbox["gather"].get("records", False)
                 out += [
-                    f"{pad}    const bool _pending = true;",
-                    f"{pad}    int _mb_next = _lcd_in_ptr[{it}], "
-                    f"_mb_end = _lcd_in_ptr[{it} + 1];",
-                    *self._gather_fetch_lines(indent + 1, declare=True),
+                    # (with records the fetch sits in front of the task,
+                    # beside the load of its id)
+                    *([] if records else
+                      [f"{pad}    const bool _pending = true;",
+                       f"{pad}    int _mb_next = _lcd_in_ptr[{it}], "
+                       f"_mb_end = _lcd_in_ptr[{it} + 1];",
+                       *self._gather_fetch_lines(indent + 1, declare=True)]),
                     # (one turn per chunk of incoming edges; bounded, so that
                     # no content of the array can keep a launch from ending)
                     f"{pad}    const int _mb_turns = (_mb_end - _mb_next) / "
@@ -1033,7 +1041,16 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                          f"{pad}    lcd_release_fence();",
                          f"{pad}    {self.group_sync}",
                          f"{pad}}}"])
+            fetch = []
+            if self.level_gather and self._mailbox["gather"].get("records"):
+                # the record of the task is addressed by its place in the
+                # level order: its loads leave with the load of the task id
+                fetch = [f"{pad}const bool _pending = true;",
+                         f"{pad}int _mb_next = 0, _mb_end = 0;",
+                         *self._gather_fetch_lines(indent, declare=True,
+                                                   records=True)]
             return [f"{pad}{it} = task_nodes[_task];",
+                    *fetch,
                     *[pad + line for line in self._queue_load_lines],
                     *body_fn(indent)]
 

@@ -798,12 +798,26 @@ def test_level_launches_gather_incoming_products():
                    wavefront_threads_per_block=128,
                    dependence_protocol="mailbox")
     assert result.dependence_protocol == "mailbox"
-    assert result.kernel_arguments[-3:] == ["_lcd_in_ptr", "_lcd_in_pos",
-                                            "_lcd_in_src"]
+    assert result.kernel_arguments[-6:] == [
+        "_lcd_in_ptr", "_lcd_in_pos", "_lcd_in_src", "_lcd_rec_in",
+        "_lcd_rec_src", "_lcd_rec_pos"]
+    assert result.task_record_lanes == 4
     assert result.reset_kernel_name is None and result.stage_kernel_name is None
     kernel = result.kernel_source
     assert "lcd_atomic" not in kernel and "for (j = " not in kernel
-    assert "int _mb_next = _lcd_in_ptr[i], _mb_end = _lcd_in_ptr[i + 1];" in kernel
+    # the first incoming entries come from the task's record in level order,
+    # fetched beside the task id, ahead of the guard on it
+    assert kernel.index("_mb_next = _lcd_rec_in[2 * _task];") < kernel.index(
+        "if (i < n) {")
+    assert "_g_src = _lcd_in_src[_mb_next + _lane];" in kernel   # further chunks
+    plain = lower(module, execution_mode="wavefront",
+                  thread_loop_iterator="j", task_lanes=4,
+                  wavefront_threads_per_block=128,
+                  dependence_protocol="mailbox", task_records=False)
+    assert plain.task_record_lanes is None
+    assert ("int _mb_next = _lcd_in_ptr[i], _mb_end = _lcd_in_ptr[i + 1];"
+            in plain.kernel_source)
+    hip_runtime.compile_code(plain.source)
     assert "const double _g_value = lcd_ld_once(&x[_g_src]);" in kernel
     assert ("for (int _mb_turn = 0; _mb_turn < _mb_turns; ++_mb_turn) {"
             in kernel)
