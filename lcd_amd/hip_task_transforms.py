@@ -871,8 +871,9 @@ class TaskTransformMixin:
         value_flags = self._value_pull is not None or (
             self._mailbox is not None and self._mailbox["gather"] is not None)
         if (not self.queue_node_loads_enabled or self.chain_tasks
-                or not self.warp_mapped or self.execution_mode != "sync_free"
-                or not value_flags):
+                or not self.warp_mapped or not value_flags
+                or (self.execution_mode != "sync_free"
+                    and not self.level_gather)):
             return None
         array = node.value.id
         properties = (self.function_props or {}).get(array, ())
