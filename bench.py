@@ -56,9 +56,10 @@ TUNED = {
     "c4": dict(execution_mode="sync_free", threads_per_block=640,
                task_lanes=64, thread_unroll=1, dependence_protocol="pull",
                tile_rows=1024, tile_positions=9216),
-    "c5": dict(execution_mode="sync_free", threads_per_block=128, task_lanes=8,
-               thread_unroll=1, dependence_protocol="mailbox",
-               tile_rows=8192, spin_sleep=0),
+    # (a chain: the band walker, one wavefront in program order, chosen per
+    # plan; --band-walker 0 gives the tiles of 8192 rows with 128 threads)
+    "c5": dict(execution_mode="sync_free", task_lanes=8,
+               thread_unroll=1, dependence_protocol="mailbox", spin_sleep=0),
 }
 
 
@@ -76,8 +77,11 @@ CPU_SECONDS_SUB = 3.0
 RTOL, ATOL_SCALE = 1e-12, 1e-15
 
 
-def traffic_key(config, mode, protocol, lanes, tile_rows, tile_box=None):
+def traffic_key(config, mode, protocol, lanes, tile_rows, tile_box=None,
+                walker=False):
     key = f"{config}|{mode}|{protocol}|lanes={lanes}|tile_rows={tile_rows or 0}"
+    if walker:
+        key = f"{config}|{mode}|{protocol}|band_walker"
     if tile_box:
         key += "|box=" + "x".join(str(extent) for extent in tile_box)
     return key
@@ -136,6 +140,11 @@ def build_solver(work, args, config):
         options["segment_capacity"] = args.segment_capacity
     if args.level_gather:
         options["level_gather"] = True
+    if args.band_walker is not None:
+        options["band_walker"] = bool(args.band_walker)
+        if not args.band_walker and config == "c5" and not args.auto:
+            options.setdefault("threads_per_block", 128)
+            options.setdefault("tile_rows", 8192)
     if args.no_queue_loads:
         options["queue_node_loads"] = False
     if args.plain_first is not None:
@@ -313,6 +322,7 @@ def run_configuration(config, args, device, steps, warmup, handoff_s,
             "tile_rows": tile_rows,
             "tile_box": (list(plan.tile_boxes[1])
                          if getattr(plan, "tile_boxes", None) else None),
+            "band_walker": bool(getattr(plan, "band_walker", False)),
             "replayed_from_graph": not args.no_graph,
         },
         "roofline_pct": round(100.0 * gbps / HBM_PEAK_GBPS, 3),
@@ -371,7 +381,7 @@ def run_configuration(config, args, device, steps, warmup, handoff_s,
                       lowering.dependence_protocol, lowering.task_lanes,
                       tile_rows,
                       plan.tile_boxes[1] if getattr(plan, "tile_boxes", None)
-                      else None)
+                      else None, bool(getattr(plan, "band_walker", False)))
     record["roofline"] = {
         "bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBPS,
         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 6),
@@ -439,6 +449,10 @@ def main():
                         default=None,
                         help="tiled published pull (ILU0): entries of the "
                              "publication buffer a tile mirrors in LDS")
+    parser.add_argument("--band-walker", dest="band_walker", type=int,
+                        default=None, choices=(0, 1),
+                        help="1: run chain-like DAGs on one wavefront in "
+                             "program order; 0: never (default: per plan)")
     parser.add_argument("--tile-box", dest="tile_box", default=None,
                         help="tiles over boxes of a structured grid: "
                              "'auto', 'none' or extents as 32x8x16")
@@ -526,7 +540,7 @@ def main():
         for name in ("mode", "tpb", "lanes", "unroll", "protocol",
                      "waves_per_cu", "spin_sleep", "tile_rows",
                      "plain_first", "look_ahead", "tile_positions",
-                     "segment_capacity", "tile_box"):
+                     "segment_capacity", "tile_box", "band_walker"):
             setattr(sub_args, name, None)
         for name in ("slots", "no_queue_loads", "no_publish", "no_pipeline",
                      "no_graph", "level_gather"):

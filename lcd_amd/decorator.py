@@ -58,6 +58,7 @@ from lcd_amd.scheduler import (
     AnalyticScheduler,
     CalibratedScheduler,
     SchedulePlan,
+    BAND_WALKER_THREADS_PER_BLOCK,
     PAIR_TABLE_ENTRIES_PER_POSITION,
     PUBLISHED_TILE_MIN_LOCALITY,
     PUBLISHED_TILE_POSITIONS,
@@ -65,6 +66,7 @@ from lcd_amd.scheduler import (
     TILE_BOX_THREADS_PER_BLOCK,
     TILE_THREADS_PER_BLOCK,
     automatic_tile_box,
+    band_walker_applies,
     automatic_tile_rows,
     structured_grid,
     automatic_tile_threads,
@@ -210,15 +212,19 @@ def parallel(**kwargs):
             raise ValueError(
                 "tile_box must be None, 'auto' or three positive integers.")
 
+        walker_option = kwargs.get("band_walker", "auto")
+        if walker_option not in ("auto", True, False):
+            raise ValueError("band_walker must be 'auto', True or False.")
+
         registers_option = kwargs.get("segment_registers", "auto")
         if registers_option not in ("auto", True, False):
             raise ValueError("segment_registers must be 'auto', True or False.")
 
         def lower_variant(lowering_key, tile_rows=None, single_chunk=False,
                           task_records=True, by_position=False,
-                          registers=False):
+                          registers=False, walker=False):
             variant_key = (lowering_key, tile_rows, single_chunk, task_records,
-                           by_position, registers)
+                           by_position, registers, walker)
             if variant_key not in lowered_variants:
                 (mode, threads_per_block, unroll, n_warp, protocol,
                  task_lanes) = lowering_key
@@ -265,6 +271,7 @@ def parallel(**kwargs):
                     tile_by_position=by_position,
                     segment_registers=bool(registers),
                     pair_tables=registers == 2,
+                    band_walker=walker,
                     full_fences=kwargs.get("full_fences", False),
                     dynamic_fetch=kwargs.get("dynamic_fetch", False),
                 )
@@ -272,11 +279,12 @@ def parallel(**kwargs):
 
         def compile_variant(lowering_key, tile_rows=None, single_chunk=False,
                             task_records=True, by_position=False,
-                            registers=False):
+                            registers=False, walker=False):
             lowering = lower_variant(lowering_key, tile_rows, single_chunk,
-                                     task_records, by_position, registers)
+                                     task_records, by_position, registers,
+                                     walker)
             variant_key = (lowering_key, tile_rows, single_chunk, task_records,
-                           by_position, registers)
+                           by_position, registers, walker)
             if variant_key not in compiled_variants:
                 compiled_variants[variant_key] = compile_hip_module(
                     lowering, function_globals=function.__globals__)
@@ -395,6 +403,42 @@ def parallel(**kwargs):
             except (hip_runtime.HIPRuntimeError, KeyError):
                 return 1, {}
             return 2, tables
+
+        def walker_for(dag, schedule):
+            """(schedule, lowering) when this plan runs on the band walker:
+            asked for with ``band_walker=True``, or chosen for a DAG that is
+            close to a chain (unless the call fixes a tile size)."""
+            if walker_option is False:
+                return None
+            forced = walker_option is True
+            usable = (schedule.execution_mode == SYNC_FREE and band_width == 1
+                      and schedule.lowering_key[4] == MAILBOX_DEPENDENCE
+                      and (forced or not isinstance(tile_option, int)))
+            if usable and not band_walker_applies(dag, forced=forced):
+                usable = False
+            candidate = schedule
+            lowering = None
+            if usable:
+                if kwargs.get("threads_per_block") is None:
+                    candidate = replace(
+                        schedule,
+                        threads_per_block=BAND_WALKER_THREADS_PER_BLOCK)
+                try:
+                    lowering = lower_variant(candidate.lowering_key, None,
+                                             False, False, False, 0, True)
+                except HIPLoweringError:
+                    if forced:
+                        raise
+                    usable = False
+            if not usable:
+                if forced:
+                    raise ValueError(
+                        "band_walker=True needs the persistent executor with "
+                        "the mailbox protocol (execution_mode='sync_free', "
+                        "band_width=1) and a DAG whose edges all span fewer "
+                        "than 64 iterations.")
+                return None
+            return candidate, lowering
 
         def boxes_for(dag, schedule, rows):
             """(grid, box) when the tiles of this plan are boxes of a
@@ -562,6 +606,22 @@ def parallel(**kwargs):
                     thread_trip_counts=trip_counts(dag_values),
                     edges=dag.edges)
                 schedule = scheduler.schedule(features, schedule_space)
+            walker = walker_for(dag, schedule)
+            if walker is not None:
+                schedule, lowering = walker
+                execution_data = execution_data_from_device_dag(
+                    dag, schedule.execution_mode, lowering.warp_mapped,
+                    band_width=band_width, mailbox=True, tile_rows=None,
+                    record_lanes=None)
+                plan = SchedulePlan(
+                    schedule=schedule,
+                    execution_data=attach_auxiliary_values(
+                        execution_data, lookup_values),
+                    features=features, dag=dag, tile_rows=None,
+                    single_chunk=False, task_records=False,
+                    band_walker=True)
+                plan_state[id(plan)] = {"resident": resident, "workspace": {}}
+                return plan
             schedule, tile_rows = tiles_for(dag, schedule, device_values)
             lowering = lower_variant(schedule.lowering_key, tile_rows)
             # the record arrays are indexed with 32 bits
@@ -665,7 +725,8 @@ def parallel(**kwargs):
                                                  plan.single_chunk,
                                                  plan.task_records,
                                                  plan.tile_boxes is not None,
-                                                 plan.segment_registers)
+                                                 plan.segment_registers,
+                                                 plan.band_walker)
             publish_variant(plan.schedule, lowering, compiled)
             state = plan_state[id(plan)]
             values = dict(argument_values)

@@ -1,0 +1,325 @@
+"""Band walker: the executor for dependence DAGs that are (nearly) a chain.
+
+When every level of the DAG holds about one task there is nothing to run in
+parallel and a hand-off between wavefronts (a store, a poll, a load) per task
+is all the persistent executor does.  The walker runs the tasks in program
+order on ONE wavefront instead: lane ``t % 64`` holds task ``t``, a finished
+value goes to the other lanes with two read-lanes, nothing is polled and
+nothing waits.  It serves loops in the gathered mailbox form (the CSC solve:
+``x[i] = f(x[i]); for j in column i: x[Ai[j]] += Ax[j] * x[i]``) whose edges
+all span fewer than 64 iterations.
+
+What stays on the chain between two tasks is the task's own arithmetic.  The
+rest of the workgroup prepares it: per block of 64 tasks the other wavefronts
+write a dense table ``tab[source step][lane]`` of the coefficients (zero
+where there is no edge), the node loads of every task, and the reciprocal of
+a divisor that is known ahead, into LDS, one block ahead of the walker.  The
+walker's step is then: finish task ``s`` (uniform operands from LDS),
+broadcast its value, ``acc += tab[s][lane] * value`` in every lane.  A missing
+edge adds ``0 * value``, which changes nothing while the value is finite; a
+block whose values are not finite, or whose division the prepared reciprocal
+does not cover, is run again with the general division and the products of
+real edges only, so the result is the sequential loop's bit for bit either
+way.  The reference's answer to chains is the warp task (``_band_chains``,
+compiler/dag_preprocessing.py:258-298, executed by
+compiler/cuda_lowering.py:1360-1410), whose members still wait on counters.
+"""
+
+import ast
+import re
+
+from lcd_amd.hip_emitter import FLOAT, INT
+
+WALKER_SPAN = 64            # an edge must span fewer iterations than this
+
+
+class BandWalkerMixin:
+    """Methods of ``HIPLowerer`` (lcd_amd/hip_lowering.py)."""
+
+    def _band_walker_plan(self, target_loop):
+        """The walker applies to the persistent executor's gathered mailbox
+        when the tasks are the iterations 0 .. count - 1, the reduced array
+        starts as zeros, and a product is ``operand * value`` with one
+        read-only operand (a missing edge must contribute exactly nothing)."""
+        box = self._mailbox
+        if (self.execution_mode != "sync_free" or box is None
+                or box["gather"] is None or self.block_task
+                or self.chain_tasks or len(target_loop.iter.args) != 1
+                or box["array"] not in self._own_zero_arrays):
+            return None
+        gather = box["gather"]
+        value = gather["value"]
+        if len(gather["operands"]) != 1 or gather["operands"][0][2] != FLOAT:
+            return None
+        operand = gather["operands"][0][0]
+        if not (isinstance(value, ast.BinOp) and isinstance(value.op, ast.Mult)
+                and isinstance(value.left, ast.Name)
+                and isinstance(value.right, ast.Name)
+                and {value.left.id, value.right.id} == {operand, "_g_value"}):
+            return None
+        return {"operand": operand, "division": False, "quotient_is_value": False}
+
+    def _band_walker_division(self, body):
+        """``a / d`` with ``d`` one of the task's node loads (known a block
+        ahead) becomes the tail of the division sequence over a reciprocal
+        the other wavefronts prepared; the first such division only."""
+        plan, lowerer = self._walker, self
+        node_loads = {name for name, kind in self._kinds.locals.items()
+                      if name.startswith("_nl_") and kind == FLOAT}
+
+        class Rewrite(ast.NodeTransformer):
+            def visit_BinOp(self, node):
+                node = self.generic_visit(node)
+                if (not plan["division"] and isinstance(node.op, ast.Div)
+                        and isinstance(node.right, ast.Name)
+                        and node.right.id in node_loads):
+                    plan["division"] = node.right.id
+                    return ast.copy_location(ast.Call(
+                        func=ast.Name(id="_lcd_wdiv", ctx=ast.Load()),
+                        args=[node.left, node.right], keywords=[]), node)
+                return node
+
+        rewritten = []
+        for statement in body:
+            before = plan["division"]
+            statement = Rewrite().visit(statement)
+            if (not before and plan["division"]
+                    and isinstance(statement, ast.Assign)
+                    and isinstance(statement.value, ast.Call)
+                    and isinstance(statement.value.func, ast.Name)
+                    and statement.value.func.id == "_lcd_wdiv"
+                    and len(statement.targets) == 1
+                    and isinstance(statement.targets[0], ast.Name)
+                    and statement.targets[0].id.startswith("_lcd_own_")):
+                # the quotient is the task's value: one capture serves both
+                plan["quotient_is_value"] = True
+            rewritten.append(statement)
+        ast.fix_missing_locations(ast.Module(body=rewritten, type_ignores=[]))
+        lowerer._kinds.locals["_lcd_wr"] = FLOAT
+        return rewritten
+
+    def _band_walker_store(self, lines):
+        """The task's final store: the value stays in the lane (it leaves for
+        memory with the block's 64 values), captured under the step's mask."""
+        register = self._mailbox["register"]
+        array = self._mailbox["array"]
+        store = re.compile(
+            r"^if \(_lane == 0\) (?:" + re.escape(array) + r"\[[^\]]*\] = "
+            + re.escape(register) + r"|lcd_st\(&" + re.escape(array)
+            + r"\[[^\]]*\], " + re.escape(register) + r"\));$")
+        out, found = [], 0
+        for line in lines:
+            if store.match(line.strip()):
+                found += 1
+                out.append(f"_lcd_wout = lcd_bfi(_lcd_wmask, {register}, "
+                           "_lcd_wout);")
+            else:
+                out.append(line)
+        if found != 1:
+            return None
+        return out
+
+    def _band_walker_text(self, task_lines):
+        """Kernel body of the walker (everything after the declarations)."""
+        plan = self._walker
+        it = self.loop_iterator
+        box = self._mailbox
+        gather = box["gather"]
+        emitter = self._emitter
+        register = box["register"]
+        array = box["array"]
+        operand, operand_node, _ = gather["operands"][0]
+        sign = "-" if gather["negate"] else "+"
+        product = emitter.expr(gather["value"])
+        # what the other wavefronts evaluate per task: the node loads; the
+        # own element starts as zero in the lane itself
+        assign = re.compile(r"^(\w+) = (.*);$")
+        stage_lines, staged = [], []
+        for line in self._prefetch_lines:
+            match = assign.match(line.strip())
+            if match is None:
+                return None
+            if match.group(1) == register:
+                if match.group(2) != "0.0":
+                    return None
+                continue
+            stage_lines.append(line.strip())
+            staged.append(match.group(1))
+        tail_text = "\n".join(task_lines)
+        used = [name for name in staged
+                if re.search(r"\b" + re.escape(name) + r"\b", tail_text)]
+        slots = [(name, self._kinds.locals.get(name, FLOAT)) for name in used]
+        division = plan["division"]
+        if division:
+            slots.append(("_lcd_wr", FLOAT))
+        width = max(2, len(slots) + (len(slots) & 1))
+        own_is_quotient = bool(division) and plan["quotient_is_value"]
+        general_tail = [line.replace("_lcd_wdiv(", "_lcd_wdiv_general(")
+                        for line in task_lines]
+
+        def put(name, kind, where):
+            return (f"{where} = (double){name};" if kind == INT
+                    else f"{where} = {name};")
+
+        def take(name, kind, what):
+            return (f"{name} = (lcd_index_t){what};" if kind == INT
+                    else f"{name} = {what};")
+
+        def body(lines, pad):
+            return [pad + line for line in lines]
+
+        p2, p3, p4, p5 = " " * 8, " " * 12, " " * 16, " " * 20
+        lines = [
+            "    // ---- band walker: one wavefront runs the tasks in order, the",
+            "    // others stage what it needs one block of 64 tasks ahead",
+            "    if (blockIdx.x != 0) return;",
+            "    const int _w_lane = threadIdx.x & 63;",
+            "    const int _w_wave = threadIdx.x >> 6;",
+            "    const int _w_n = (int)task_count;",
+            "    const int _w_blocks = (_w_n + 63) / 64;",
+            "    const int _w_stagers = LCD_TPB - 64;",
+            "    __shared__ double _w_tab[3][64][64];",
+            f"    __shared__ double _w_uni[3][64][{width}];",
+            "    __shared__ int _w_ptr[3][132];",
+            "    __shared__ unsigned long long _w_msk[3][64];",
+            "    __shared__ int _w_flag[3];",
+            "    lcd_index_t _g_pos = 0, _g_src = 0; double _g_value = 0.0;",
+            f"    double {operand} = 0.0;",
+            "    double _lcd_wout = 0.0, _lcd_wq = 0.0; int _lcd_wmask = 0;",
+            "    (void)_g_pos; (void)_g_src; (void)_lcd_wq;",
+            "    auto _lcd_wdiv = [&](double a, double d, double r) {",
+            "        const double q = lcd_div_prepared(a, d, r);",
+            *([] if own_is_quotient or not division else
+              ["        _lcd_wq = lcd_bfi(_lcd_wmask, q, _lcd_wq);"]),
+            "        return q;",
+            "    };",
+            "    auto _lcd_wdiv_general = [&](double a, double d, double r) {",
+            "        (void)r; return a / d;",
+            "    };",
+            "    (void)_lcd_wdiv; (void)_lcd_wdiv_general;",
+            # ---- staging
+            "    auto _w_clear = [&](int m, int first, int step) {",
+            "        double* cells = &_w_tab[m % 3][0][0];",
+            "        for (int c = first; c < 64 * 64; c += step) cells[c] = 0.0;",
+            "        for (int c = first; c < 64; c += step) _w_msk[m % 3][c] = 0ull;",
+            "        if (first == 0) _w_flag[m % 3] = 0;",
+            "    };",
+            "    auto _w_stage_ptr = [&](int m, int first, int step) {",
+            "        // bounds of the incoming listing of the tasks 64 m + 1 .. 64 m + 129",
+            "        if (m >= _w_blocks) return;",
+            "        for (int l = first; l < 130; l += step) {",
+            "            const int t = m * 64 + 1 + l < _w_n ? m * 64 + 1 + l : _w_n;",
+            "            _w_ptr[m % 3][l] = _lcd_in_ptr[t];",
+            "        }",
+            "    };",
+            "    auto _w_stage = [&](int m, int first, int step) {",
+            "        if (m >= _w_blocks) return;",
+            "        const int buf = m % 3, s0 = m * 64;",
+            "        const int* ptr = _w_ptr[buf];",
+            "        // the edges out of the tasks s0 .. s0 + 63 end in s0 + 1 .. s0 + 126",
+            "        const int e0 = ptr[0], e1 = ptr[126];",
+            "        for (int e = e0 + first; e < e1; e += step) {",
+            "            _g_src = (lcd_index_t)_lcd_in_src[e];",
+            "            if ((unsigned)(_g_src - s0) < 64u) {",
+            "                _g_pos = (lcd_index_t)_lcd_in_pos[e];",
+            f"                {operand} = {emitter.expr(operand_node)};",
+            "                int lo = 0, hi = 126;     // the task: last l with ptr[l] <= e",
+            "                while (hi - lo > 1) { const int mid = (lo + hi) >> 1; "
+            "if (ptr[mid] <= e) lo = mid; else hi = mid; }",
+            "                const int t = s0 + 1 + lo;",
+            "                const unsigned long long bit = 1ull << (t & 63);",
+            "                // an edge the table has no cell for: longer than the window, or a",
+            "                // second edge between the same two tasks",
+            "                if (t - _g_src >= 64 || (atomicOr(&_w_msk[buf][_g_src - s0], bit) & bit))",
+            "                    _lcd_status[0] = 2;",
+            f"                _w_tab[buf][_g_src - s0][t & 63] = {operand};",
+            "            }",
+            "        }",
+            "        for (int l = first; l < 64; l += step) {",
+            f"            {it} = (lcd_index_t)(s0 + l);",
+            f"            if ({it} < _w_n) {{",
+            *body(stage_lines, p4),
+            *([f"{p4}_lcd_wr = lcd_div_prepare({division});",
+               f"{p4}if (!lcd_div_plain_divisor({division})) _w_flag[buf] = 1;"]
+              if division else []),
+            *[p4 + put(name, kind, f"_w_uni[buf][l][{k}]")
+              for k, (name, kind) in enumerate(slots)],
+            "            }",
+            "        }",
+            "    };",
+            "    _w_clear(0, threadIdx.x, LCD_TPB); _w_clear(1, threadIdx.x, LCD_TPB); "
+            "_w_clear(2, threadIdx.x, LCD_TPB);",
+            "    _w_stage_ptr(0, threadIdx.x, LCD_TPB); _w_stage_ptr(1, threadIdx.x, LCD_TPB);",
+            "    __syncthreads();",
+            "    _w_stage(0, threadIdx.x, LCD_TPB);",
+            "    __syncthreads();",
+            f"    {register} = 0.0;",
+            "    for (int _w_m = 0; _w_m < _w_blocks; ++_w_m) {",
+            "        if (_w_wave == 0) {",
+            "            const int base = _w_m * 64;",
+            "            const int steps = _w_n - base < 64 ? _w_n - base : 64;",
+            "            const int cb = _w_m % 3;",
+            f"            const double _w_acc0 = {register};",
+            "            _lcd_wmask = _w_lane == 0 ? -1 : 0;",
+            "            if (steps == 64) {",
+            "                double _w_w = _w_tab[cb][0][_w_lane];",
+            *[f"{p4}double _w_u{k} = _w_uni[cb][0][{k}];"
+              for k in range(len(slots))],
+            "#pragma unroll 4",
+            "                for (int l = 0; l < 64; ++l) {",
+            "                    const int ln = (l + 1) & 63;",
+            f"                    {it} = (lcd_index_t)(base + l);",
+            *[p5 + take(name, kind, f"_w_u{k}")
+              for k, (name, kind) in enumerate(slots)],
+            f"                    const double _w_acc = {register};",
+            *body(task_lines, p5),
+            f"                    const double _w_xs = lcd_rseg_uni({register}, (lcd_index_t)l);",
+            "                    const double _w_wn = _w_tab[cb][ln][_w_lane];",
+            *[f"{p5}const double _w_n{k} = _w_uni[cb][ln][{k}];"
+              for k in range(len(slots))],
+            # the lane of the finished task starts its next one at zero; its
+            # cell of this row is empty
+            f"                    {register} = lcd_bfi(_lcd_wmask, 0.0, _w_acc);",
+            "                    _lcd_wmask = lcd_next_lane(_lcd_wmask);",
+            f"                    _g_value = _w_xs; {operand} = _w_w;",
+            f"                    {register} = {register} {sign} {product};",
+            "                    _w_w = _w_wn;",
+            *[f"{p5}_w_u{k} = _w_n{k};" for k in range(len(slots))],
+            "                }",
+            "            }",
+            # the check and the second, general pass
+            "            bool _w_again = steps < 64 || _w_flag[cb] != 0;",
+            (f"            _w_again = _w_again || __ballot(!lcd_div_plain_quotient("
+             f"{'_lcd_wout' if own_is_quotient else '_lcd_wq'}) "
+             "|| !lcd_finite(_lcd_wout)) != 0ull;" if division else
+             "            _w_again = _w_again || __ballot(!lcd_finite(_lcd_wout)) != 0ull;"),
+            "            if (_w_again) {",
+            "                // the general division, and the products of real edges only",
+            f"                {register} = _w_acc0;",
+            "                _lcd_wmask = _w_lane == 0 ? -1 : 0;",
+            "                for (int l = 0; l < steps; ++l) {",
+            f"                    {it} = (lcd_index_t)(base + l);",
+            *[p5 + take(name, kind, f"_w_uni[cb][l][{k}]")
+              for k, (name, kind) in enumerate(slots)],
+            f"                    const double _w_acc = {register};",
+            *body(general_tail, p5),
+            f"                    const double _w_xs = lcd_rseg_uni({register}, (lcd_index_t)l);",
+            f"                    {register} = lcd_bfi(_lcd_wmask, 0.0, _w_acc);",
+            "                    _lcd_wmask = lcd_next_lane(_lcd_wmask);",
+            "                    if ((_w_msk[cb][l] >> _w_lane) & 1ull) {",
+            f"                        _g_value = _w_xs; {operand} = _w_tab[cb][l][_w_lane];",
+            f"                        {register} = {register} {sign} {product};",
+            "                    }",
+            "                }",
+            "            }",
+            f"            if (_w_lane < steps) {array}[base + _w_lane] = _lcd_wout;",
+            "        } else {",
+            "            const int first = threadIdx.x - 64;",
+            "            _w_stage(_w_m + 1, first, _w_stagers);",
+            "            _w_clear(_w_m + 2, first, _w_stagers);",
+            "            _w_stage_ptr(_w_m + 2, first, _w_stagers);",
+            "        }",
+            "        __syncthreads();",
+            "    }",
+        ]
+        return lines

@@ -114,6 +114,9 @@ class HIPLoweringResult:
     # tiled executor whose LDS copy and flag array are indexed by the place
     # of a task in the queue (tiles that do not follow the ids)
     tile_by_position: bool = False
+    # one wavefront runs the tasks in program order (chain-like DAGs whose
+    # edges span fewer than 64 iterations)
+    band_walker: bool = False
     # the pointer array of the task's own segment (ILU0's row), and whether
     # that segment is kept in registers (segments of at most 64 entries)
     segment_pointer: str | None = None
@@ -473,6 +476,9 @@ class _Emitter:
                 return f"lcd_sorted_find({', '.join(args)})"
             if name == "_lcd_rseg_first" and len(args) == 1:
                 return f"lcd_rseg_first({args[0]}, _lcd_seg_base)"
+            if name == "_lcd_wdiv" and len(args) == 2:
+                # (band walker) a division whose divisor was known ahead
+                return f"_lcd_wdiv({args[0]}, {args[1]}, _lcd_wr)"
             if name == "_lcd_pair_at" and len(args) == 2:
                 return (f"_lcd_pair[_lcd_pair_row + (({args[0]}) - _lcd_seg_base)"
                         f" * _lcd_seg_own + (({args[1]}) - _lcd_seg_base)]")

@@ -81,9 +81,11 @@ from lcd_amd.hip_emitter import (  # noqa: F401  (re-exported)
 from lcd_amd.hip_protocols import ProtocolMixin
 from lcd_amd.hip_sequential_pull import SequentialPullMixin
 from lcd_amd.hip_task_transforms import TaskTransformMixin
+from lcd_amd.hip_band_walker import BandWalkerMixin
 
 
-class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
+class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
+                 BandWalkerMixin):
     def __init__(self, loop_iterator, reductions=None, kernel_name=None,
                  execution_mode="plain", sync_free_ready_count=0,
                  wavefront_threads_per_block=128, thread_loop_iterator=None,
@@ -101,8 +103,10 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                  pipeline_fetch=True, full_fences=False,
                  dynamic_fetch=False, tile_positions=None,
                  tile_by_position=False, segment_registers=False,
-                 pair_tables=True):
+                 pair_tables=True, band_walker=False):
         self.tile_positions = tile_positions
+        self.band_walker = bool(band_walker)
+        self._walker = None
         self.tile_by_position = tile_by_position
         self.segment_registers = segment_registers
         self.pair_tables = pair_tables
@@ -330,6 +334,23 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
             if self.gather_messages and self.value_flags:
                 self._mailbox["gather"] = self._gather_plan(
                     self._mailbox, arguments, lifted_loop_parameters)
+        if self.band_walker:
+            self._walker = self._band_walker_plan(target_loop)
+            if self._walker is None:
+                raise HIPLoweringError(
+                    "The band walker needs the persistent executor's gathered "
+                    "mailbox form: a loop over range(count) whose tasks add "
+                    "`operand[j] * X[i]` to later elements of a zero-"
+                    "initialised X.")
+            gather = self._mailbox["gather"]
+            for name in gather["staged"].values():
+                kinds.arrays.pop(name, None)
+            gather["staged"] = {}
+            gather["needs_position"] = True
+            self.tile_rows = None
+            self.task_records = False
+            self.segment_cache = False
+            self.queue_node_loads_enabled = False
         # arrays other tasks of the same launch write go through coherent
         # accessors: always in the persistent executor, and in a level launch
         # when a chain task reads what its earlier members wrote
@@ -515,6 +536,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
             tile_rows=self._tile["rows"] if self._tile else None,
             tile_by_position=bool(self._tile
                                   and self._tile.get("by_position")),
+            band_walker=self._walker is not None,
             segment_pointer=(self._segment["pointer"]
                              if self._segment else None),
             segment_registers=bool(self._segment
@@ -731,6 +753,8 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
         if self.prefetch_node_loads:
             body, self._prefetch_lines = self._hoist_node_loads(
                 body, mapped, arguments)
+        if self._walker is not None:
+            body = self._band_walker_division(body)
         if self._value_pull is not None:
             own = self._own_map.get(
                 f"{self._value_pull['array']}[{self.loop_iterator}]")
@@ -765,6 +789,12 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
         for statement in body:
             lines.extend(self._emit_guarded(statement, emitter, 0, hooks))
         lines.extend(epilogue)
+        if self._walker is not None:
+            lines = self._band_walker_store(lines)
+            if lines is None:
+                raise HIPLoweringError(
+                    "The band walker needs a task that ends with the one "
+                    "store of its own element.")
         return lines
 
     def _emit_guarded(self, node, emitter, indent, hooks):
@@ -1067,6 +1097,14 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                          "/ LCD_TASK_LANES;")
             lines.append("    if (_task >= band_end) return;")
             lines += node_loop(1, task)
+        elif self._walker is not None:
+            walker = self._band_walker_text(task_body)
+            if walker is None:
+                raise HIPLoweringError(
+                    "The band walker cannot stage this task's node loads.")
+            if self._walker["division"]:
+                lines.append("    double _lcd_wr = 0.0;")
+            lines += walker
         else:
             lines += self._sync_free_text(task, node_loop)
         lines.append("}")
@@ -1493,9 +1531,13 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin):
                 # tile takes, not by a polling budget
                 tasks_per_block = self._tile["rows"]
                 waves_per_cu = self.resident_waves_per_cu
-            body.append(f"_blocks = min((_count + {tasks_per_block} - 1) // "
-                        f"{tasks_per_block}, _hip.resident_blocks({kernel_name!r}, "
-                        f"{self.threads_per_block}, {waves_per_cu!r}))")
+            if self._walker is not None:
+                # one workgroup: the walker and the wavefronts that stage for it
+                body.append("_blocks = 1")
+            else:
+                body.append(f"_blocks = min((_count + {tasks_per_block} - 1) // "
+                            f"{tasks_per_block}, _hip.resident_blocks({kernel_name!r}, "
+                            f"{self.threads_per_block}, {waves_per_cu!r}))")
             body.append(f"_hip.launch({kernel_name!r}, max(_blocks, 1), "
                         f"{self.threads_per_block}, {call_args})")
         for loop in reversed(self.host_loops):
@@ -1523,7 +1565,7 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
                  publish_values=True, look_ahead=True, segment_capacity=None,
                  pipeline_fetch=True, full_fences=False, dynamic_fetch=False,
                  tile_positions=None, tile_by_position=False,
-                 segment_registers=False, pair_tables=True):
+                 segment_registers=False, pair_tables=True, band_walker=False):
     """HIP counterpart of ``lower_to_numba_cuda``
     (compiler/cuda_lowering.py:2854-2884); same parameters plus
     ``task_lanes`` (lanes cooperating on one task, a power of two <= 64),
@@ -1552,5 +1594,6 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
         pipeline_fetch=pipeline_fetch, full_fences=full_fences,
         dynamic_fetch=dynamic_fetch, tile_positions=tile_positions,
         tile_by_position=tile_by_position,
-        segment_registers=segment_registers, pair_tables=pair_tables)
+        segment_registers=segment_registers, pair_tables=pair_tables,
+        band_walker=band_walker)
     return lowerer.lower(code)
