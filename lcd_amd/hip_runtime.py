@@ -1428,6 +1428,13 @@ def check_executor_status(lowering, prepared_arguments):
         _check(device.lib.lcdhip_buffer_fill32(
             ctypes.c_void_p(status.pointer), ctypes.c_uint32(0),
             ctypes.c_size_t(1), device.stream))
+        if int(host[0]) == 2 and getattr(lowering, "band_walker", False):
+            raise HIPRuntimeError(
+                f"The band walker of {lowering.function_name} met an edge its "
+                "table has no cell for: one that spans 64 iterations or "
+                "more, or a second edge between the same two iterations. "
+                "The result is not valid; run with band_walker=False.",
+                ERR_ARGUMENT)
         raise ExecutorWatchdogError(
             f"The sync-free executor of {lowering.function_name} gave up "
             "waiting for a dependence (cyclic or inconsistent schedule).",

@@ -806,6 +806,190 @@ def test_gauss_seidel_two_sweeps(oracle, variant):
         np.testing.assert_array_equal(result, expected)
 
 
+def band_factor(n, offsets_per_column, seed, diagonal=(0.5, 2.0)):
+    """Lower-triangular CSC factor whose column i holds the diagonal first and
+    then rows i + d for a random subset of the distances d in 1 .. span."""
+    rng = np.random.default_rng(seed)
+    span, keep = offsets_per_column
+    indptr, indices, data = [0], [], []
+    for i in range(n):
+        distances = np.arange(1, min(span, n - 1 - i) + 1)
+        if keep < 1.0 and len(distances):
+            distances = distances[rng.random(len(distances)) < keep]
+        indices.append(i)
+        data.append(rng.uniform(*diagonal))
+        indices.extend((i + distances).tolist())
+        data.extend(rng.uniform(-0.3, 0.3, len(distances)).tolist())
+        indptr.append(len(indices))
+    return (np.asarray(indptr, dtype=np.int32),
+            np.asarray(indices, dtype=np.int32), np.asarray(data))
+
+
+WALKER = dict(execution_mode="sync_free", dependence_protocol="mailbox",
+              task_lanes=4, band_walker=True)
+
+
+@pytest.mark.parametrize("n,span,keep,tpb", [
+    (2, 1, 1.0, 128), (50, 3, 1.0, 128), (64, 8, 1.0, 256), (65, 1, 1.0, 128),
+    (129, 63, 1.0, 1024), (1000, 8, 1.0, None), (4113, 63, 0.3, 512),
+    (5000, 40, 0.1, None), (3000, 63, 1.0, 256)])
+def test_band_walker(oracle, n, span, keep, tpb):
+    """One wavefront runs the tasks in program order: results are the
+    sequential loop's bit for bit, whatever the block boundaries (n below,
+    at and off multiples of 64), the band (1 to 63, full or sparse) and the
+    number of wavefronts that stage for the walker."""
+    print("band walker", n, span, keep, tpb, flush=True)
+    options = dict(WALKER)
+    if tpb:
+        options["threads_per_block"] = tpb
+    solver = sptrsv.compile_sptrsv_csc(**options)
+    indptr, indices, data = band_factor(n, (span, keep), seed=n + span)
+    rhs = np.random.default_rng(n).standard_normal(n)
+    expected = oracle.sptrsv_csc(indptr, indices, data, rhs, n)
+    for _ in range(2):       # the second call replays the captured graph
+        result = solver(indptr, indices, data, rhs, n)
+        np.testing.assert_array_equal(result, expected)
+    plan = solver.schedule_plan(indptr, indices, data, rhs, n)
+    assert plan.band_walker and plan.tile_rows is None
+    assert solver.hip_lowering.band_walker
+    assert "lcd_div_prepare(" in solver.hip_kernel_source
+    assert plan.schedule.threads_per_block == (tpb or 1024)
+
+
+def test_band_walker_divides_again_where_the_prepared_reciprocal_does_not_apply(
+        oracle):
+    """Zero, tiny, huge and non-finite numerators and divisors: the blocks
+    they fall in run a second time with the general division (and with the
+    products of real edges only, so 0 * inf of a missing edge never shows);
+    an explicitly stored zero coefficient still gives 0 * inf = NaN as in
+    the sequential loop."""
+    n = 1000
+    indptr, indices, data = band_factor(n, (8, 1.0), seed=3)
+    solver = sptrsv.compile_sptrsv_csc(**WALKER)
+    rng = np.random.default_rng(11)
+    cases = {}
+    rhs = rng.standard_normal(n)
+    rhs[:130] = 0.0                      # exact zeros: x = 0 over two blocks
+    cases["zeros"] = (data.copy(), rhs)
+    rhs = rng.standard_normal(n)
+    rhs[200] = 1e-305                    # quotient far down the range
+    rhs[400] = 1e300
+    cases["range"] = (data.copy(), rhs)
+    values = data.copy()
+    values[indptr[300]] = 1e-200         # divisors the sequence scales
+    values[indptr[301]] = 1e250
+    values[indptr[500]] = 5e-324
+    cases["divisors"] = (values, rng.standard_normal(n))
+    rhs = rng.standard_normal(n)
+    rhs[600] = np.inf
+    rhs[900] = np.nan
+    cases["not finite"] = (data.copy(), rhs)
+    values = data.copy()
+    values[indptr[700]] = 0.0            # x[700] = b / 0
+    values[indptr[700] + 3] = 0.0        # ... times a stored zero: NaN
+    cases["zero pivot"] = (values, rng.standard_normal(n))
+    for name, (values, rhs) in cases.items():
+        print("band walker,", name, flush=True)
+        with np.errstate(all="ignore"):
+            expected = oracle.sptrsv_csc(indptr, indices, values, rhs, n)
+        result = solver(indptr, indices, values, rhs, n)
+        np.testing.assert_array_equal(result, expected, err_msg=name)
+        # (also the signs of zeros; the sign of a NaN is the machine's)
+        valid = ~np.isnan(expected)
+        np.testing.assert_array_equal(np.signbit(result[valid]),
+                                      np.signbit(expected[valid]), err_msg=name)
+
+
+def test_band_walker_is_chosen_for_chains_only(oracle):
+    """The automatic choice: close to one task per level and every edge
+    shorter than 64 iterations."""
+    solver = sptrsv.compile_sptrsv_csc(execution_mode="sync_free",
+                                       dependence_protocol="mailbox",
+                                       task_lanes=4)
+    chain = workloads.configuration("c5", n=3000)
+    grid = workloads.configuration("c1")
+    wide = band_factor(2000, (64, 1.0), seed=5)      # one edge too long
+    forks = band_factor(4000, (12, 0.02), seed=6)    # many tasks per level
+    for work, walks in ((chain, True), (grid, False)):
+        plan = solver.schedule_plan(work.indptr, work.indices, work.data,
+                                    work.rhs, work.n)
+        assert plan.band_walker == walks
+        expected = oracle.sptrsv_csc(work.indptr, work.indices, work.data,
+                                     work.rhs, work.n)
+        solve_and_check(solver, work, expected, exact=True)
+    for (indptr, indices, data), n in ((wide, 2000), (forks, 4000)):
+        rhs = np.ones(n)
+        plan = solver.schedule_plan(indptr, indices, data, rhs, n)
+        assert not plan.band_walker
+        np.testing.assert_array_equal(
+            solver(indptr, indices, data, rhs, n),
+            oracle.sptrsv_csc(indptr, indices, data, rhs, n))
+    never = sptrsv.compile_sptrsv_csc(execution_mode="sync_free",
+                                      dependence_protocol="mailbox",
+                                      task_lanes=4, band_walker=False)
+    assert not never.schedule_plan(chain.indptr, chain.indices, chain.data,
+                                   chain.rhs, chain.n).band_walker
+    forced = sptrsv.compile_sptrsv_csc(**WALKER)
+    with pytest.raises(ValueError, match="fewer than 64 iterations"):
+        forced(wide[0], wide[1], wide[2], np.ones(2000), 2000)
+    # asked for by name it also runs a DAG with many tasks per level
+    indptr, indices, data = forks
+    np.testing.assert_array_equal(
+        forced(indptr, indices, data, np.ones(4000), 4000),
+        oracle.sptrsv_csc(indptr, indices, data, np.ones(4000), 4000))
+
+
+def test_band_walker_refuses_a_repeated_edge():
+    """Two entries of one column with the same row index are two edges
+    between the same two tasks; the walker's table has one cell for them and
+    says so instead of returning a wrong result."""
+    from lcd_amd import hip_runtime
+    n = 200
+    indptr, indices, data = band_factor(n, (4, 1.0), seed=9)
+    indices = indices.copy()
+    indices[indptr[50] + 2] = indices[indptr[50] + 1]
+    solver = sptrsv.compile_sptrsv_csc(**WALKER)
+    with pytest.raises(hip_runtime.HIPRuntimeError, match="band walker"):
+        solver(indptr, indices, data, np.ones(n), n)
+
+
+def walker_unit_lower(Ap, Ai, Ax, b, n):
+    x = np.zeros(n)
+    for i in range(n):
+        x[i] = b[i] - x[i]
+        for j in range(Ap[i] + 1, Ap[i + 1]):
+            x[Ai[j]] += Ax[j] * x[i]
+    return x
+
+
+def walker_subtracting(Ap, Ai, Ax, b, n):
+    x = np.zeros(n)
+    for i in range(n):
+        x[i] = (b[i] + x[i]) / Ax[Ap[i]] + 0.5 * b[i]
+        for j in range(Ap[i] + 1, Ap[i + 1]):
+            x[Ai[j]] -= x[i] * Ax[j]
+    return x
+
+
+@pytest.mark.parametrize("loop", [walker_unit_lower, walker_subtracting])
+def test_band_walker_other_loops(loop):
+    """Loops of the same form with no division at all, with a division that
+    is not the task's value, and with products that are subtracted, against
+    the loop itself run by CPython."""
+    from lcd_amd import parallel
+    solver = parallel(block_map="i", thread_map="j",
+                      function_props=sptrsv.FUNCTION_PROPS_CSC, **WALKER)(loop)
+    n = 700
+    indptr, indices, data = band_factor(n, (9, 0.7), seed=21)
+    rhs = np.random.default_rng(4).standard_normal(n)
+    expected = loop(indptr, indices, data, rhs, n)
+    result = solver(indptr, indices, data, rhs, n)
+    np.testing.assert_array_equal(result, expected)
+    assert solver.hip_lowering.band_walker
+    assert ("lcd_div_prepare(" in solver.hip_kernel_source) == (
+        loop is walker_subtracting)
+
+
 def test_edge_cases(oracle):
     solver = sptrsv.compile_sptrsv_csc(execution_mode="sync_free",
                                        threads_per_block=128, task_lanes=4)

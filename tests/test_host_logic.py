@@ -833,6 +833,66 @@ def test_level_launches_gather_incoming_products():
     assert "lcd_atomic_add" in chains.kernel_source
 
 
+def test_band_walker_lowering_and_choice():
+    """The executor for chains: one wavefront runs the tasks in program
+    order, nothing is polled; what it takes and when it is chosen."""
+    from lcd_amd.hip_emitter import HIPLoweringError
+    from lcd_amd.scheduler import band_walker_applies
+    module = demo_source("sptrsv", "sptrsv_csc_loop")
+    result = lower(module, execution_mode="sync_free",
+                   thread_loop_iterator="j", task_lanes=8,
+                   wavefront_threads_per_block=1024,
+                   dependence_protocol="mailbox", band_walker=True,
+                   tile_rows=4096)
+    assert result.band_walker and result.tile_rows is None
+    assert result.task_record_lanes is None and result.stage_kernel_name is None
+    assert result.kernel_arguments == [
+        "Ap", "Ai", "Ax", "b", "n", "x", "_lcd_in_ptr", "_lcd_in_pos",
+        "_lcd_in_src", "task_nodes", "task_ptr", "task_counter", "task_count",
+        "_lcd_status"]
+    kernel = result.kernel_source
+    # no poll, no spin, no atomics on the data; one workgroup
+    for absent in ("lcd_ld(", "_spins", "lcd_atomic", "s_sleep"):
+        assert absent not in kernel
+    assert "_blocks = 1" in result.launcher_source
+    # the division by the diagonal uses the reciprocal prepared a block ahead
+    # and is checked per block; the general division is the second pass
+    assert "_lcd_own_0 = _lcd_wdiv((_nl_0 - _lcd_own_0), _nl_2, _lcd_wr);" in kernel
+    assert "_lcd_wr = lcd_div_prepare(_nl_2);" in kernel
+    assert "_lcd_own_0 = _lcd_wdiv_general((_nl_0 - _lcd_own_0), _nl_2, _lcd_wr);" in kernel
+    assert "lcd_div_plain_quotient(_lcd_wout)" in kernel
+    # the value stays in its lane; the block's 64 values leave together
+    assert "_lcd_wout = lcd_bfi(_lcd_wmask, _lcd_own_0, _lcd_wout);" in kernel
+    assert "if (_w_lane < steps) x[base + _w_lane] = _lcd_wout;" in kernel
+    assert "_lcd_own_0 = _lcd_own_0 + (_g_operand_0 * _g_value);" in kernel
+    hip_runtime.compile_code(result.source)
+    # loops the walker does not take: a pull-shaped solve, chain tasks
+    csr = demo_source("sptrsv", "sptrsv_csr_loop")
+    with pytest.raises(HIPLoweringError, match="band walker"):
+        lower(csr, function_props=CSR_PROPS, execution_mode="sync_free",
+              thread_loop_iterator="j", task_lanes=8,
+              dependence_protocol="pull", band_walker=True)
+
+    class Dag:
+        def __init__(self, n, levels, offsets):
+            self.n, self.levels, self.offsets = n, levels, offsets
+            self.edges = len(offsets)
+
+        def edge_offsets(self, capacity):
+            return (self.offsets[:capacity], [1] * min(capacity, len(self.offsets)),
+                    len(self.offsets))
+
+    assert band_walker_applies(Dag(1000, 1000, [1, 2, 8]))
+    assert band_walker_applies(Dag(1000, 200, list(range(1, 64))))
+    assert not band_walker_applies(Dag(1000, 100, [1, 2, 8]))       # wide levels
+    assert band_walker_applies(Dag(1000, 100, [1, 2, 8]), forced=True)
+    assert not band_walker_applies(Dag(1000, 1000, [1, 64]))         # too long
+    assert not band_walker_applies(Dag(1000, 1000, [1, 64]), forced=True)
+    assert not band_walker_applies(Dag(1000, 1000, list(range(1, 70))))
+    assert not band_walker_applies(Dag(1000, 1, []))                 # no edges
+    assert not band_walker_applies(Dag(0, 0, []))
+
+
 def test_tiles_addressed_by_queue_position():
     """Tiles that do not follow the ids (boxes of a grid): sources, LDS slots
     and the value-as-flag copy are addressed by the place in the queue."""
