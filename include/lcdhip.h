@@ -359,6 +359,20 @@ int lcdhip_pair_lookup_build(const int32_t *d_ptr, const int32_t *d_idx, int64_t
                              int64_t capacity, int64_t *entries_out,
                              lcdhip_stream stream);
 
+/* The same table with one byte per entry: the OFFSET of the found position
+ * from the start of the segment searched (d_ptr[d_idx[d_ptr[s] + a]]), or -1;
+ * every segment must have at most 127 entries (LCDHIP_ERR_ARGUMENT
+ * otherwise).  A quarter of the bytes of lcdhip_pair_lookup_build for the
+ * structures whose segments live in registers (at most 64 entries): on the
+ * 9-point 1024^2 grid 81 MB instead of 324 MB, read once per factorization.
+ * The caller adds the segment's start, which it has gathered by its own
+ * positions (lcdhip_gather_i32 of d_ptr through d_idx).  Same reference
+ * lines as above. */
+int lcdhip_pair_offsets_build(const int32_t *d_ptr, const int32_t *d_idx, int64_t n,
+                              int64_t idx_size, int32_t *d_base, int8_t *d_table,
+                              int64_t capacity, int64_t *entries_out,
+                              lcdhip_stream stream);
+
 /* d_dst[q] = d_src[d_index[q] + offset] for q in [0, count): a structure
  * array read in the order the executor visits the tasks, so that a task's
  * loads of it (`Ap[i]`, `Ap[i + 1]`) have addresses that depend on the queue

@@ -620,6 +620,7 @@ extern "C" int lcdhip_lookup_build(const int32_t *d_ptr, const int32_t *d_idx,
 
 __global__ void lcdhip_pair_square_kernel(const int32_t *__restrict__ ptr,
                                           int64_t n, int64_t idx_size,
+                                          int64_t longest,
                                           unsigned long long *__restrict__ total,
                                           int32_t *status)
 {
@@ -628,6 +629,8 @@ __global__ void lcdhip_pair_square_kernel(const int32_t *__restrict__ ptr,
     if (s < n) {
         const int64_t start = ptr[s], end = ptr[s + 1];
         if (start < 0 || end < start || end > idx_size)
+            atomicMax(status, 2);
+        else if (end - start > longest)
             atomicMax(status, 1);
         else
             mine = static_cast<unsigned long long>(end - start) * (end - start);
@@ -673,11 +676,14 @@ lcdhip_pair_base_kernel(const int32_t *__restrict__ ptr, int64_t n,
         base[n] = static_cast<int32_t>(carry);
 }
 
+// T = int32_t: positions in idx; T = int8_t: offsets from the start of the
+// segment searched (segments of at most 127 entries)
+template <class T>
 __global__ void lcdhip_pair_fill_kernel(const int32_t *__restrict__ ptr,
                                         const int32_t *__restrict__ idx,
                                         int64_t n, int64_t idx_size,
                                         const int32_t *__restrict__ base,
-                                        int32_t *__restrict__ table)
+                                        T *__restrict__ table)
 {
     int64_t p = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
     if (p >= idx_size || p < ptr[0] || p >= ptr[n])
@@ -693,7 +699,7 @@ __global__ void lcdhip_pair_fill_kernel(const int32_t *__restrict__ ptr,
     }
     const int64_t s = lo, start = ptr[s], len = ptr[s + 1] - start;
     const int64_t k = idx[p];
-    int32_t *row = table + base[s] + (p - start) * len;
+    T *row = table + base[s] + (p - start) * len;
     const bool valid = k >= 0 && k < n;
     const int64_t k_start = valid ? ptr[k] : 0, k_end = valid ? ptr[k + 1] : 0;
     for (int64_t b = 0; b < len; ++b) {
@@ -706,22 +712,23 @@ __global__ void lcdhip_pair_fill_kernel(const int32_t *__restrict__ ptr,
             else
                 right = mid;
         }
-        row[b] = (left < k_end && idx[left] == key) ? static_cast<int32_t>(left) : -1;
+        const bool found = left < k_end && idx[left] == key;
+        row[b] = static_cast<T>(!found ? -1 : sizeof(T) == 1 ? left - k_start : left);
     }
 }
 
-extern "C" int lcdhip_pair_lookup_build(const int32_t *d_ptr, const int32_t *d_idx,
-                                        int64_t n, int64_t idx_size,
-                                        int32_t *d_base, int32_t *d_table,
-                                        int64_t capacity, int64_t *entries_out,
-                                        lcdhip_stream stream)
+static int pair_table_build(const int32_t *d_ptr, const int32_t *d_idx, int64_t n,
+                            int64_t idx_size, int32_t *d_base, void *d_table,
+                            int element_bytes, int64_t capacity,
+                            int64_t *entries_out, lcdhip_stream stream)
 {
     LCDHIP_REQUIRE_INIT();
     if (n < 0 || idx_size < 0 || capacity < 0 || !d_ptr || !entries_out ||
         (idx_size > 0 && !d_idx) || (d_table && !d_base)) {
-        set_error("bad argument to lcdhip_pair_lookup_build");
+        set_error("bad argument to the pair table build");
         return LCDHIP_ERR_ARGUMENT;
     }
+    const int64_t longest = element_bytes == 1 ? 127 : INT64_MAX;
     hipStream_t hip_stream = resolve_stream(stream);
     *entries_out = 0;
     unsigned long long *d_total = nullptr;
@@ -732,7 +739,8 @@ extern "C" int lcdhip_pair_lookup_build(const int32_t *d_ptr, const int32_t *d_i
     if (error == hipSuccess && n > 0)
         hipLaunchKernelGGL(lcdhip_pair_square_kernel,
                            dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256),
-                           0, hip_stream, d_ptr, n, idx_size, d_total, d_status);
+                           0, hip_stream, d_ptr, n, idx_size, longest, d_total,
+                           d_status);
     if (error == hipSuccess)
         error = hipMemcpyAsync(host, d_total, 16, hipMemcpyDeviceToHost, hip_stream);
     if (error == hipSuccess)
@@ -742,9 +750,13 @@ extern "C" int lcdhip_pair_lookup_build(const int32_t *d_ptr, const int32_t *d_i
         set_error("pair table sizing failed: %s", hipGetErrorString(error));
         return LCDHIP_ERR_HIP;
     }
-    if (static_cast<int32_t>(host[1] & 0xffffffffu) != 0) {
+    if (static_cast<int32_t>(host[1] & 0xffffffffu) == 2) {
         set_error("invalid pointer segment in the structural lookup arrays");
         return LCDHIP_ERR_LOOKUP_POINTER;
+    }
+    if (static_cast<int32_t>(host[1] & 0xffffffffu) == 1) {
+        set_error("a segment of more than 127 entries: its offsets do not fit a byte");
+        return LCDHIP_ERR_ARGUMENT;
     }
     if (host[0] >= (1ull << 31)) {
         set_error("a pair table of %llu entries exceeds 2^31", host[0]);
@@ -761,14 +773,39 @@ extern "C" int lcdhip_pair_lookup_build(const int32_t *d_ptr, const int32_t *d_i
     }
     hipLaunchKernelGGL(lcdhip_pair_base_kernel, dim3(1), dim3(1024), 0, hip_stream,
                        d_ptr, n, d_base);
-    if (idx_size > 0 && n > 0)
-        hipLaunchKernelGGL(lcdhip_pair_fill_kernel,
+    if (idx_size > 0 && n > 0 && element_bytes == 1)
+        hipLaunchKernelGGL(lcdhip_pair_fill_kernel<int8_t>,
                            dim3(static_cast<unsigned>((idx_size + 255) / 256)),
                            dim3(256), 0, hip_stream, d_ptr, d_idx, n, idx_size,
-                           d_base, d_table);
+                           d_base, static_cast<int8_t *>(d_table));
+    else if (idx_size > 0 && n > 0)
+        hipLaunchKernelGGL(lcdhip_pair_fill_kernel<int32_t>,
+                           dim3(static_cast<unsigned>((idx_size + 255) / 256)),
+                           dim3(256), 0, hip_stream, d_ptr, d_idx, n, idx_size,
+                           d_base, static_cast<int32_t *>(d_table));
     LCDHIP_CHECK(hipGetLastError());
     LCDHIP_CHECK(hipStreamSynchronize(hip_stream));
     return LCDHIP_OK;
+}
+
+extern "C" int lcdhip_pair_lookup_build(const int32_t *d_ptr, const int32_t *d_idx,
+                                        int64_t n, int64_t idx_size,
+                                        int32_t *d_base, int32_t *d_table,
+                                        int64_t capacity, int64_t *entries_out,
+                                        lcdhip_stream stream)
+{
+    return pair_table_build(d_ptr, d_idx, n, idx_size, d_base, d_table, 4,
+                            capacity, entries_out, stream);
+}
+
+extern "C" int lcdhip_pair_offsets_build(const int32_t *d_ptr, const int32_t *d_idx,
+                                         int64_t n, int64_t idx_size,
+                                         int32_t *d_base, int8_t *d_table,
+                                         int64_t capacity, int64_t *entries_out,
+                                         lcdhip_stream stream)
+{
+    return pair_table_build(d_ptr, d_idx, n, idx_size, d_base, d_table, 1,
+                            capacity, entries_out, stream);
 }
 
 // -------------------------------------------------------------- digest ----

@@ -390,6 +390,10 @@ def parallel(**kwargs):
                         _, name, lookup, index_array = entry
                         tables[name] = device.gather_int32(
                             lookups[lookup], values[index_array])
+                    elif entry[0] == "start":
+                        _, name, pointer_array, index_array = entry
+                        tables[name] = device.gather_int32(
+                            values[pointer_array], values[index_array])
                     else:
                         _, name, pointer_array, index_array = entry
                         positions = max(int(round(stats[1] * dag_rows)), 1)
@@ -399,7 +403,8 @@ def parallel(**kwargs):
                             return 1, {}
                         tables["_lcd_pair_base"], tables[name] = (
                             device.pair_lookup_build(values[pointer_array],
-                                                     values[index_array]))
+                                                     values[index_array],
+                                                     offsets=True))
             except (hip_runtime.HIPRuntimeError, KeyError):
                 return 1, {}
             return 2, tables

@@ -123,7 +123,9 @@ class HIPLoweringResult:
     segment_registers: bool = False
     # tables of structure searches keyed by the task's own positions:
     # ("at", name, lookup table, index array) = lookup[index[p]] by p;
-    # ("pair", "_lcd_pair", pointer array, index array) with "_lcd_pair_base"
+    # ("pair", "_lcd_pair", pointer array, index array) with "_lcd_pair_base":
+    # byte offsets; ("start", "_lcd_pair_start", pointer array, index array) =
+    # pointer[index[p]] by p
     structure_tables: tuple = ()
     # lifted zero-initialised arrays the executor needs no host-side clear for
     executor_initialised: tuple = ()
@@ -480,8 +482,9 @@ class _Emitter:
                 # (band walker) a division whose divisor was known ahead
                 return f"_lcd_wdiv({args[0]}, {args[1]}, _lcd_wr)"
             if name == "_lcd_pair_at" and len(args) == 2:
-                return (f"_lcd_pair[_lcd_pair_row + (({args[0]}) - _lcd_seg_base)"
-                        f" * _lcd_seg_own + (({args[1]}) - _lcd_seg_base)]")
+                return (f"lcd_pair_pos(_lcd_pair[_lcd_pair_row + (({args[0]}) - "
+                        f"_lcd_seg_base) * _lcd_seg_own + (({args[1]}) - "
+                        f"_lcd_seg_base)], _lcd_pair_start[{args[0]}])")
             if (name == "_lcd_raw" and self.published is not None
                     and self.segment.get("registers")):
                 target = node.args[0]

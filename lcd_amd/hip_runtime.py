@@ -134,6 +134,7 @@ EXPORTED_SYMBOLS = (
     "lcdhip_dag_tile_order", "lcdhip_dag_tile_locality",
     "lcdhip_dag_box_order", "lcdhip_dag_edge_offsets",
     "lcdhip_pair_lookup_build",
+    "lcdhip_pair_offsets_build",
     "lcdhip_dag_task_records",
     "lcdhip_lookup_build", "lcdhip_gather_i32",
     "lcdhip_digest", "lcdhip_digest_noalloc",
@@ -201,7 +202,8 @@ def compile_code(source, name="lcd_generated.hip", options=()):
 
 _CTYPES = {"int": ctypes.c_int32, "long long": ctypes.c_int64,
            "double": ctypes.c_double, "float": ctypes.c_float}
-_DTYPE_TO_C = {"int32": "int", "int64": "long long", "float64": "double",
+_DTYPE_TO_C = {"int8": "signed char", "int32": "int", "int64": "long long",
+               "float64": "double",
                "float32": "float", "uint32": "unsigned int",
                "uint64": "unsigned long long"}
 
@@ -717,19 +719,24 @@ class HIPDevice:
             ctypes.c_int64(0), ctypes.byref(entries), self.stream))
         return int(entries.value)
 
-    def pair_lookup_build(self, pointers, indices):
+    def pair_lookup_build(self, pointers, indices, offsets=False):
         """``(base, table)``: for segment s with entries a, b,
         ``table[base[s] + a * len + b]`` is the position in segment
         ``indices[pointers[s] + a]`` of the index ``indices[pointers[s] +
-        b]``, or -1."""
+        b]``, or -1.  With ``offsets`` the table holds one byte per entry:
+        the position's offset from the start of the segment searched
+        (segments of at most 127 entries)."""
         keep = []
         d_ptr, ptr_size = self._resident_int32(pointers, keep)
         d_idx, idx_size = self._resident_int32(indices, keep)
         n = ptr_size - 1
         entries = self.pair_lookup_entries(pointers, indices)
         base = self.empty((n + 1,), np.int32)
-        table = self.empty((max(entries, 1),), np.int32)
-        _check(self.lib.lcdhip_pair_lookup_build(
+        table = self.empty((max(entries, 1),),
+                           np.int8 if offsets else np.int32)
+        build = (self.lib.lcdhip_pair_offsets_build if offsets
+                 else self.lib.lcdhip_pair_lookup_build)
+        _check(build(
             ctypes.c_void_p(d_ptr), ctypes.c_void_p(d_idx), ctypes.c_int64(n),
             ctypes.c_int64(idx_size), ctypes.c_void_p(base.pointer),
             ctypes.c_void_p(table.pointer), ctypes.c_int64(entries),

@@ -305,7 +305,9 @@ class TaskTransformMixin:
           through IDX);
         * ``find(IDX, PTR[k], PTR[k + 1], j)`` with ``j = IDX[q]``, ``q`` the
           distributed loop's position in the own segment:
-          ``_lcd_pair[_lcd_pair_base[i] + (p - PTR[i]) * len + (q - PTR[i])]``.
+          ``_lcd_pair_start[p] + _lcd_pair[_lcd_pair_base[i] + (p - PTR[i]) * len
+          + (q - PTR[i])]`` (a table of byte offsets, -1 where there is none,
+          and ``_lcd_pair_start[p] = PTR[IDX[p]]``).
 
         Every address then depends on the task's own positions alone: the
         chain producer id -> its segment bounds -> its entries (three
@@ -359,7 +361,8 @@ class TaskTransformMixin:
             for entry in tables:
                 if entry[0] == kind and entry[2:] == key:
                     return entry[1]
-            name = (f"_lcd_at_{key[0]}" if kind == "at" else "_lcd_pair")
+            name = (f"_lcd_at_{key[0]}" if kind == "at" else
+                    "_lcd_pair_start" if kind == "start" else "_lcd_pair")
             tables.append((kind, name, *key))
             return name
 
@@ -396,7 +399,10 @@ class TaskTransformMixin:
                         and isinstance(high, ast.Subscript)
                         and ast.unparse(high) == f"{pointer}[{low.slice.id} + 1]"):
                     return node
+                # one byte per pair: the offset in the segment searched, whose
+                # start is gathered by the task's own positions
                 table_for("pair", pointer, index.id)
+                table_for("start", pointer, index.id)
                 return ast.copy_location(ast.Call(
                     func=ast.Name(id="_lcd_pair_at", ctx=ast.Load()),
                     args=[ast.Name(id=outer_name, ctx=ast.Load()),

@@ -523,6 +523,26 @@ def test_pair_lookup_table(device):
         np.testing.assert_array_equal(base.copy_to_host(), expected_base)
         np.testing.assert_array_equal(table.copy_to_host()[:len(expected)],
                                       expected)
+        # the same table in bytes: offsets from the start of the segment
+        # searched (segments of at most 127 entries)
+        if np.diff(work.indptr).max() <= 127:
+            lengths = np.diff(work.indptr)
+            searched = np.concatenate([
+                np.repeat(work.indices[work.indptr[s]:work.indptr[s + 1]],
+                          lengths[s]) for s in range(work.n)])
+            offsets = np.where(expected < 0, -1,
+                               expected - work.indptr[searched]).astype(np.int8)
+            base, table = device.pair_lookup_build(work.indptr, work.indices,
+                                                   offsets=True)
+            assert table.dtype == np.int8
+            np.testing.assert_array_equal(base.copy_to_host(), expected_base)
+            np.testing.assert_array_equal(
+                table.copy_to_host()[:len(expected)], offsets)
+        else:
+            with pytest.raises(hip_runtime.HIPRuntimeError,
+                               match="127 entries"):
+                device.pair_lookup_build(work.indptr, work.indices,
+                                         offsets=True)
     # an empty segment, an index beyond the segments (no segment to search)
     indptr = np.array([0, 2, 2, 5], dtype=np.int32)
     indices = np.array([0, 2, 0, 1, 7], dtype=np.int32)

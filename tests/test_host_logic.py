@@ -985,18 +985,22 @@ def test_own_segment_in_registers():
     assert tabled.structure_tables == (
         ("at", "_lcd_at__lcd_lookup_position_0", "_lcd_lookup_position_0",
          "A_indices"),
-        ("pair", "_lcd_pair", "A_indptr", "A_indices"))
+        ("pair", "_lcd_pair", "A_indptr", "A_indices"),
+        ("start", "_lcd_pair_start", "A_indptr", "A_indices"))
     for name in ("_lcd_at__lcd_lookup_position_0", "_lcd_pair",
-                 "_lcd_pair_base"):
+                 "_lcd_pair_base", "_lcd_pair_start"):
         assert tabled.kernel_arguments.count(name) == 1
         assert name in tabled.launcher_arguments
     text = tabled.kernel_source
     assert "lcd_sorted_find(" not in text
     assert "_lcd_pair_row = _lcd_pair_base[i];" in text
     assert "_nx_diag_ptr = _lcd_at__lcd_lookup_position_0[(k_ptr + 1)];" in text
-    assert ("_nx__sp_kj_ptr = _lcd_pair[_lcd_pair_row + (((k_ptr + 1)) - "
-            "_lcd_seg_base) * _lcd_seg_own + ((_nx__sp_first) - "
-            "_lcd_seg_base)];") in text
+    # (one byte per pair: the offset in the pivot row, whose start is
+    # gathered by the task's own position as well)
+    assert ("_nx__sp_kj_ptr = lcd_pair_pos(_lcd_pair[_lcd_pair_row + "
+            "(((k_ptr + 1)) - _lcd_seg_base) * _lcd_seg_own + "
+            "((_nx__sp_first) - _lcd_seg_base)], "
+            "_lcd_pair_start[(k_ptr + 1)]);") in text
     hip_runtime.compile_code(tabled.source)
     # (without registers the tables are not used: segments may be long)
     assert lower_to_hip(module, **options).structure_tables == ()
