@@ -42,6 +42,8 @@ class BandWalkerMixin:
         starts as zeros, and a product is ``operand * value`` with one
         read-only operand (a missing edge must contribute exactly nothing)."""
         box = self._mailbox
+        if self.threads_per_block < 128 or self.threads_per_block % 64:
+            return None      # the walker's wavefront and at least one that stages
         if (self.execution_mode != "sync_free" or box is None
                 or box["gather"] is None or self.block_task
                 or self.chain_tasks or len(target_loop.iter.args) != 1

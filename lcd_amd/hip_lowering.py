@@ -341,7 +341,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                     "The band walker needs the persistent executor's gathered "
                     "mailbox form: a loop over range(count) whose tasks add "
                     "`operand[j] * X[i]` to later elements of a zero-"
-                    "initialised X.")
+                    "initialised X, and at least two wavefronts per workgroup.")
             gather = self._mailbox["gather"]
             for name in gather["staged"].values():
                 kinds.arrays.pop(name, None)

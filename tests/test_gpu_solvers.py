@@ -929,6 +929,18 @@ def test_band_walker_is_chosen_for_chains_only(oracle):
                                       task_lanes=4, band_walker=False)
     assert not never.schedule_plan(chain.indptr, chain.indices, chain.data,
                                    chain.rhs, chain.n).band_walker
+    # a workgroup of one wavefront has nobody to stage for the walker
+    single = sptrsv.compile_sptrsv_csc(execution_mode="sync_free",
+                                       dependence_protocol="mailbox",
+                                       task_lanes=4, threads_per_block=64)
+    assert not single.schedule_plan(chain.indptr, chain.indices, chain.data,
+                                    chain.rhs, chain.n).band_walker
+    solve_and_check(single, chain, oracle.sptrsv_csc(
+        chain.indptr, chain.indices, chain.data, chain.rhs, chain.n),
+        exact=True)
+    with pytest.raises(Exception, match="two wavefronts"):
+        sptrsv.compile_sptrsv_csc(threads_per_block=64, **WALKER)(
+            chain.indptr, chain.indices, chain.data, chain.rhs, chain.n)
     forced = sptrsv.compile_sptrsv_csc(**WALKER)
     with pytest.raises(ValueError, match="fewer than 64 iterations"):
         forced(wide[0], wide[1], wide[2], np.ones(2000), 2000)

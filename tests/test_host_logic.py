@@ -873,6 +873,12 @@ def test_band_walker_lowering_and_choice():
               thread_loop_iterator="j", task_lanes=8,
               dependence_protocol="pull", band_walker=True)
 
+    # a workgroup of one wavefront has nobody to stage for the walker
+    with pytest.raises(HIPLoweringError, match="two wavefronts"):
+        lower(module, execution_mode="sync_free", thread_loop_iterator="j",
+              task_lanes=8, wavefront_threads_per_block=64,
+              dependence_protocol="mailbox", band_walker=True)
+
     class Dag:
         def __init__(self, n, levels, offsets):
             self.n, self.levels, self.offsets = n, levels, offsets
