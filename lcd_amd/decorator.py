@@ -31,6 +31,7 @@ from lcd_amd import hip_runtime
 from lcd_amd.dag_codegen import (
     COUNTER_DEPENDENCE,
     MAILBOX_DEPENDENCE,
+    PULL_DEPENDENCE,
     PUSH_DEPENDENCE,
     build_device_dag,
     compile_dag_builder,
@@ -417,16 +418,20 @@ def parallel(**kwargs):
                 return None
             forced = walker_option is True
             usable = (schedule.execution_mode == SYNC_FREE and band_width == 1
-                      and schedule.lowering_key[4] == MAILBOX_DEPENDENCE
+                      and schedule.lowering_key[4] in (MAILBOX_DEPENDENCE,
+                                                       PULL_DEPENDENCE)
                       and (forced or not isinstance(tile_option, int)))
             if usable and not band_walker_applies(dag, forced=forced):
                 usable = False
             candidate = schedule
             lowering = None
             if usable:
+                # (the distributed loop is gone from the walker's kernel:
+                # nothing to unroll)
+                candidate = replace(schedule, thread_unroll=1)
                 if kwargs.get("threads_per_block") is None:
                     candidate = replace(
-                        schedule,
+                        candidate,
                         threads_per_block=BAND_WALKER_THREADS_PER_BLOCK)
                 try:
                     lowering = lower_variant(candidate.lowering_key, None,
@@ -439,9 +444,9 @@ def parallel(**kwargs):
                 if forced:
                     raise ValueError(
                         "band_walker=True needs the persistent executor with "
-                        "the mailbox protocol (execution_mode='sync_free', "
-                        "band_width=1) and a DAG whose edges all span fewer "
-                        "than 64 iterations.")
+                        "the mailbox or pull protocol (execution_mode="
+                        "'sync_free', band_width=1) and a DAG whose edges all "
+                        "span fewer than 64 iterations.")
                 return None
             return candidate, lowering
 
@@ -614,6 +619,11 @@ def parallel(**kwargs):
             walker = walker_for(dag, schedule)
             if walker is not None:
                 schedule, lowering = walker
+                if not incoming_positions:
+                    # (a pull-shaped loop: the walker reads the rows through
+                    # the incoming listing, which this DAG was built without)
+                    dag = build_device_dag(dag_plan, device_values, device,
+                                           levels=True, incoming=True)
                 execution_data = execution_data_from_device_dag(
                     dag, schedule.execution_mode, lowering.warp_mapped,
                     band_width=band_width, mailbox=True, tile_rows=None,

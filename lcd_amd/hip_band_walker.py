@@ -27,6 +27,7 @@ compiler/cuda_lowering.py:1360-1410), whose members still wait on counters.
 
 import ast
 import re
+from copy import deepcopy
 
 from lcd_amd.hip_emitter import FLOAT, INT
 
@@ -81,6 +82,21 @@ class BandWalkerMixin:
                         args=[node.left, node.right], keywords=[]), node)
                 return node
 
+            def visit_AugAssign(self, node):
+                node = self.generic_visit(node)
+                if (not plan["division"] and isinstance(node.op, ast.Div)
+                        and isinstance(node.target, ast.Name)
+                        and isinstance(node.value, ast.Name)
+                        and node.value.id in node_loads):
+                    plan["division"] = node.value.id
+                    return ast.copy_location(ast.Assign(
+                        targets=[ast.Name(id=node.target.id, ctx=ast.Store())],
+                        value=ast.Call(
+                            func=ast.Name(id="_lcd_wdiv", ctx=ast.Load()),
+                            args=[ast.Name(id=node.target.id, ctx=ast.Load()),
+                                  node.value], keywords=[])), node)
+                return node
+
         rewritten = []
         for statement in body:
             before = plan["division"]
@@ -121,6 +137,74 @@ class BandWalkerMixin:
             return None
         return out
 
+    def _band_walker_pull_box(self, body):
+        """The pull-shaped form of the same loop (the CSR solve: ``x[i] = b[i];
+        for j in row i: x[i] -= Ax[j] * x[Ai[j]]; x[i] /= d``) described the
+        way the gathered mailbox describes the push-shaped one, so that one
+        walker serves both: the incoming listing is the row itself."""
+        plan, dependence = self._value_pull, self.direct_dependence
+        mapped = self._find_mapped_loop(body)
+        if (plan is None or mapped is None or mapped not in body
+                or len(mapped.body) != 1 or self.block_task):
+            return None
+        site, array = mapped.body[0], plan["array"]
+        own_text = f"{array}[{self.loop_iterator}]"
+        endpoint = dependence.endpoint
+        if not (isinstance(site, ast.AugAssign)
+                and isinstance(site.op, (ast.Add, ast.Sub))
+                and ast.unparse(site.target) == own_text
+                and isinstance(endpoint, ast.Subscript)
+                and isinstance(endpoint.value, ast.Name)):
+            return None
+        kinds = self._kinds
+        readonly = {name for name in kinds.arrays
+                    if name not in self._all_written}
+        position = mapped.target.id
+        endpoint_text = ast.unparse(endpoint)
+
+        class Substitute(ast.NodeTransformer):
+            def visit_Subscript(self, node):
+                if (isinstance(node.value, ast.Name) and node.value.id == array
+                        and ast.unparse(node.slice) == endpoint_text):
+                    return ast.Name(id="_g_value", ctx=ast.Load())
+                return self.generic_visit(node)
+
+            def visit_Name(self, node):
+                if node.id == position:
+                    return ast.Name(id="_g_pos", ctx=node.ctx)
+                return node
+
+        value = ast.fix_missing_locations(
+            Substitute().visit(deepcopy(site.value)))
+        operands = []
+
+        class Operands(ast.NodeTransformer):
+            def visit_Subscript(self, node):
+                node = self.generic_visit(node)
+                if (isinstance(node.value, ast.Name)
+                        and node.value.id in readonly):
+                    name = f"_g_operand_{len(operands)}"
+                    operands.append((name, deepcopy(node),
+                                     kinds.arrays.get(node.value.id, FLOAT)))
+                    return ast.Name(id=name, ctx=ast.Load())
+                return node
+
+        value = ast.fix_missing_locations(Operands().visit(value))
+        for node in ast.walk(value):
+            if isinstance(node, (ast.Subscript, ast.Call)):
+                return None
+        for name, _, kind in operands:
+            kinds.locals[name] = kind
+        kinds.locals["_g_value"] = FLOAT
+        kinds.locals["_g_pos"] = INT
+        kinds.locals["_g_src"] = INT
+        return {"array": array, "position": deepcopy(endpoint.slice),
+                "index_array": endpoint.value.id, "own_text": own_text,
+                "sites": [site], "mapped": mapped, "pulled": True,
+                "gather": {"value": value, "operands": operands, "staged": {},
+                           "needs_position": True,
+                           "negate": isinstance(site.op, ast.Sub)}}
+
     def _band_walker_text(self, task_lines):
         """Kernel body of the walker (everything after the declarations)."""
         plan = self._walker
@@ -133,10 +217,17 @@ class BandWalkerMixin:
         operand, operand_node, _ = gather["operands"][0]
         sign = "-" if gather["negate"] else "+"
         product = emitter.expr(gather["value"])
-        # what the other wavefronts evaluate per task: the node loads; the
-        # own element starts as zero in the lane itself
+        # the task's text around the place of its distributed loop: what
+        # comes before it gives the element its first value, what comes after
+        # finishes it
+        # (a push-shaped task receives its products ahead of all its own
+        # statements: it has no head)
+        split = plan.get("split", 0) if box.get("pulled") else 0
+        head_lines, tail_lines = task_lines[:split], task_lines[split:]
+        # what the other wavefronts evaluate per task: the node loads (and
+        # the head); an element that starts as zero does so in the lane itself
         assign = re.compile(r"^(\w+) = (.*);$")
-        stage_lines, staged = [], []
+        stage_lines, staged, zero_start = [], [], False
         for line in self._prefetch_lines:
             match = assign.match(line.strip())
             if match is None:
@@ -144,20 +235,37 @@ class BandWalkerMixin:
             if match.group(1) == register:
                 if match.group(2) != "0.0":
                     return None
+                zero_start = True
                 continue
             stage_lines.append(line.strip())
             staged.append(match.group(1))
-        tail_text = "\n".join(task_lines)
-        used = [name for name in staged
+        if not head_lines and not zero_start:
+            return None
+        for line in head_lines:
+            # (whatever else the head computes for the tail is staged with
+            # the node loads)
+            match = assign.match(line.strip())
+            if match is None:
+                return None
+            if match.group(1) != register:
+                staged.append(match.group(1))
+        tail_text = "\n".join(tail_lines)
+        used = [name for name in dict.fromkeys(staged)
                 if re.search(r"\b" + re.escape(name) + r"\b", tail_text)]
         slots = [(name, self._kinds.locals.get(name, FLOAT)) for name in used]
         division = plan["division"]
         if division:
             slots.append(("_lcd_wr", FLOAT))
+        if head_lines:
+            # (the last slot: the element's first value, taken per lane)
+            slots.append((register, FLOAT))
+        uniform = len(slots) - (1 if head_lines else 0)
         width = max(2, len(slots) + (len(slots) & 1))
         own_is_quotient = bool(division) and plan["quotient_is_value"]
         general_tail = [line.replace("_lcd_wdiv(", "_lcd_wdiv_general(")
-                        for line in task_lines]
+                        for line in tail_lines]
+        start = (f"_w_uni[(_w_m + 1) & 3][_w_lane][{uniform}]" if head_lines
+                 else "0.0")
 
         def put(name, kind, where):
             return (f"{where} = (double){name};" if kind == INT
@@ -170,10 +278,10 @@ class BandWalkerMixin:
         def body(lines, pad):
             return [pad + line for line in lines]
 
-        p2, p3, p4, p5 = " " * 8, " " * 12, " " * 16, " " * 20
+        p4, p5 = " " * 16, " " * 20
         lines = [
             "    // ---- band walker: one wavefront runs the tasks in order, the",
-            "    // others stage what it needs one block of 64 tasks ahead",
+            "    // others stage what it needs a block of 64 tasks or two ahead",
             "    if (blockIdx.x != 0) return;",
             "    const int _w_lane = threadIdx.x & 63;",
             "    const int _w_wave = threadIdx.x >> 6;",
@@ -181,10 +289,10 @@ class BandWalkerMixin:
             "    const int _w_blocks = (_w_n + 63) / 64;",
             "    const int _w_stagers = LCD_TPB - 64;",
             "    __shared__ double _w_tab[3][64][64];",
-            f"    __shared__ double _w_uni[3][64][{width}];",
+            f"    __shared__ double _w_uni[4][64][{width}];",
             "    __shared__ int _w_ptr[3][132];",
             "    __shared__ unsigned long long _w_msk[3][64];",
-            "    __shared__ int _w_flag[3];",
+            "    __shared__ int _w_odd[4][64];",
             "    lcd_index_t _g_pos = 0, _g_src = 0; double _g_value = 0.0;",
             f"    double {operand} = 0.0;",
             "    double _lcd_wout = 0.0, _lcd_wq = 0.0; int _lcd_wmask = 0;",
@@ -204,7 +312,6 @@ class BandWalkerMixin:
             "        double* cells = &_w_tab[m % 3][0][0];",
             "        for (int c = first; c < 64 * 64; c += step) cells[c] = 0.0;",
             "        for (int c = first; c < 64; c += step) _w_msk[m % 3][c] = 0ull;",
-            "        if (first == 0) _w_flag[m % 3] = 0;",
             "    };",
             "    auto _w_stage_ptr = [&](int m, int first, int step) {",
             "        // bounds of the incoming listing of the tasks 64 m + 1 .. 64 m + 129",
@@ -215,10 +322,11 @@ class BandWalkerMixin:
             "        }",
             "    };",
             "    auto _w_stage = [&](int m, int first, int step) {",
+            "        // the coefficients of the edges out of the tasks s0 .. s0 + 63, which",
+            "        // end in s0 + 1 .. s0 + 126, by (source, lane of the destination)",
             "        if (m >= _w_blocks) return;",
             "        const int buf = m % 3, s0 = m * 64;",
             "        const int* ptr = _w_ptr[buf];",
-            "        // the edges out of the tasks s0 .. s0 + 63 end in s0 + 1 .. s0 + 126",
             "        const int e0 = ptr[0], e1 = ptr[126];",
             "        for (int e = e0 + first; e < e1; e += step) {",
             "            _g_src = (lcd_index_t)_lcd_in_src[e];",
@@ -237,14 +345,21 @@ class BandWalkerMixin:
             f"                _w_tab[buf][_g_src - s0][t & 63] = {operand};",
             "            }",
             "        }",
+            "    };",
+            "    auto _w_stage_tasks = [&](int m, int first, int step) {",
+            "        // per task: its node loads" + (
+                ", the prepared reciprocal of its divisor" if division else "")
+            + (", its element's first value" if head_lines else ""),
+            "        if (m >= _w_blocks) return;",
             "        for (int l = first; l < 64; l += step) {",
-            f"            {it} = (lcd_index_t)(s0 + l);",
+            f"            {it} = (lcd_index_t)(m * 64 + l);",
             f"            if ({it} < _w_n) {{",
             *body(stage_lines, p4),
+            *body(head_lines, p4),
             *([f"{p4}_lcd_wr = lcd_div_prepare({division});",
-               f"{p4}if (!lcd_div_plain_divisor({division})) _w_flag[buf] = 1;"]
-              if division else []),
-            *[p4 + put(name, kind, f"_w_uni[buf][l][{k}]")
+               f"{p4}_w_odd[m & 3][l] = !lcd_div_plain_divisor({division});"]
+              if division else [f"{p4}_w_odd[m & 3][l] = 0;"]),
+            *[p4 + put(name, kind, f"_w_uni[m & 3][l][{k}]")
               for k, (name, kind) in enumerate(slots)],
             "            }",
             "        }",
@@ -252,46 +367,51 @@ class BandWalkerMixin:
             "    _w_clear(0, threadIdx.x, LCD_TPB); _w_clear(1, threadIdx.x, LCD_TPB); "
             "_w_clear(2, threadIdx.x, LCD_TPB);",
             "    _w_stage_ptr(0, threadIdx.x, LCD_TPB); _w_stage_ptr(1, threadIdx.x, LCD_TPB);",
+            "    _w_stage_tasks(0, threadIdx.x, LCD_TPB); _w_stage_tasks(1, threadIdx.x, LCD_TPB);",
             "    __syncthreads();",
             "    _w_stage(0, threadIdx.x, LCD_TPB);",
             "    __syncthreads();",
-            f"    {register} = 0.0;",
+            (f"    {register} = _w_uni[0][_w_lane][{uniform}];" if head_lines
+             else f"    {register} = 0.0;"),
             "    for (int _w_m = 0; _w_m < _w_blocks; ++_w_m) {",
             "        if (_w_wave == 0) {",
             "            const int base = _w_m * 64;",
             "            const int steps = _w_n - base < 64 ? _w_n - base : 64;",
-            "            const int cb = _w_m % 3;",
+            "            const int cb = _w_m % 3, ub = _w_m & 3;",
             f"            const double _w_acc0 = {register};",
+            # the value the lane's next task (64 later) starts from
+            f"            const double _w_start = {start};",
             "            _lcd_wmask = _w_lane == 0 ? -1 : 0;",
             "            if (steps == 64) {",
             "                double _w_w = _w_tab[cb][0][_w_lane];",
-            *[f"{p4}double _w_u{k} = _w_uni[cb][0][{k}];"
-              for k in range(len(slots))],
+            *[f"{p4}double _w_u{k} = _w_uni[ub][0][{k}];"
+              for k in range(uniform)],
             "#pragma unroll 4",
             "                for (int l = 0; l < 64; ++l) {",
             "                    const int ln = (l + 1) & 63;",
             f"                    {it} = (lcd_index_t)(base + l);",
             *[p5 + take(name, kind, f"_w_u{k}")
-              for k, (name, kind) in enumerate(slots)],
+              for k, (name, kind) in enumerate(slots[:uniform])],
             f"                    const double _w_acc = {register};",
-            *body(task_lines, p5),
+            *body(tail_lines, p5),
             f"                    const double _w_xs = lcd_rseg_uni({register}, (lcd_index_t)l);",
             "                    const double _w_wn = _w_tab[cb][ln][_w_lane];",
-            *[f"{p5}const double _w_n{k} = _w_uni[cb][ln][{k}];"
-              for k in range(len(slots))],
-            # the lane of the finished task starts its next one at zero; its
-            # cell of this row is empty
-            f"                    {register} = lcd_bfi(_lcd_wmask, 0.0, _w_acc);",
+            *[f"{p5}const double _w_n{k} = _w_uni[ub][ln][{k}];"
+              for k in range(uniform)],
+            # the lane of the finished task starts its next one; its cell of
+            # this row is empty
+            f"                    {register} = lcd_bfi(_lcd_wmask, _w_start, _w_acc);",
             "                    _lcd_wmask = lcd_next_lane(_lcd_wmask);",
             f"                    _g_value = _w_xs; {operand} = _w_w;",
             f"                    {register} = {register} {sign} {product};",
             "                    _w_w = _w_wn;",
-            *[f"{p5}_w_u{k} = _w_n{k};" for k in range(len(slots))],
+            *[f"{p5}_w_u{k} = _w_n{k};" for k in range(uniform)],
             "                }",
             "            }",
             # the check and the second, general pass
-            "            bool _w_again = steps < 64 || _w_flag[cb] != 0;",
-            (f"            _w_again = _w_again || __ballot(!lcd_div_plain_quotient("
+            "            bool _w_again = steps < 64;",
+            (f"            _w_again = _w_again || __ballot(_w_odd[ub][_w_lane] != 0 "
+             f"|| !lcd_div_plain_quotient("
              f"{'_lcd_wout' if own_is_quotient else '_lcd_wq'}) "
              "|| !lcd_finite(_lcd_wout)) != 0ull;" if division else
              "            _w_again = _w_again || __ballot(!lcd_finite(_lcd_wout)) != 0ull;"),
@@ -301,12 +421,12 @@ class BandWalkerMixin:
             "                _lcd_wmask = _w_lane == 0 ? -1 : 0;",
             "                for (int l = 0; l < steps; ++l) {",
             f"                    {it} = (lcd_index_t)(base + l);",
-            *[p5 + take(name, kind, f"_w_uni[cb][l][{k}]")
-              for k, (name, kind) in enumerate(slots)],
+            *[p5 + take(name, kind, f"_w_uni[ub][l][{k}]")
+              for k, (name, kind) in enumerate(slots[:uniform])],
             f"                    const double _w_acc = {register};",
             *body(general_tail, p5),
             f"                    const double _w_xs = lcd_rseg_uni({register}, (lcd_index_t)l);",
-            f"                    {register} = lcd_bfi(_lcd_wmask, 0.0, _w_acc);",
+            f"                    {register} = lcd_bfi(_lcd_wmask, _w_start, _w_acc);",
             "                    _lcd_wmask = lcd_next_lane(_lcd_wmask);",
             "                    if ((_w_msk[cb][l] >> _w_lane) & 1ull) {",
             f"                        _g_value = _w_xs; {operand} = _w_tab[cb][l][_w_lane];",
@@ -320,6 +440,7 @@ class BandWalkerMixin:
             "            _w_stage(_w_m + 1, first, _w_stagers);",
             "            _w_clear(_w_m + 2, first, _w_stagers);",
             "            _w_stage_ptr(_w_m + 2, first, _w_stagers);",
+            "            _w_stage_tasks(_w_m + 2, first, _w_stagers);",
             "        }",
             "        __syncthreads();",
             "    }",

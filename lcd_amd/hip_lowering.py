@@ -328,10 +328,19 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
         elif (self.dependence_protocol == PULL_DEPENDENCE and self.value_flags
                 and self.execution_mode == "sync_free"):
             self._value_pull = self._value_pull_plan(body)
+        if (self.band_walker and self._value_pull is not None
+                and self.dependence_protocol == PULL_DEPENDENCE):
+            # the pull-shaped solve in the terms of the gathered mailbox: the
+            # walker serves both
+            self._mailbox = self._band_walker_pull_box(body)
+            if self._mailbox is not None:
+                self.dependence_protocol = MAILBOX_DEPENDENCE
+                self._value_pull = None
         if self._mailbox is not None and (
                 self._mailbox["array"] in self._fully_rewritten):
             self._own_zero_arrays.add(self._mailbox["array"])
-            if self.gather_messages and self.value_flags:
+            if (self.gather_messages and self.value_flags
+                    and self._mailbox["gather"] is None):
                 self._mailbox["gather"] = self._gather_plan(
                     self._mailbox, arguments, lifted_loop_parameters)
         if self.band_walker:
@@ -721,9 +730,18 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
             # the consumers form the products themselves: the producer's
             # distributed loop is gone
             site = self._mailbox["sites"][0]
-            body = [s for s in body if s is not self._mailbox["mapped"]]
-            emitter.lowered_ids.add(
-                self.reductions[(site.lineno, site.col_offset)][0])
+            if self._walker is not None:
+                # (the walker wants to know where the loop was: what comes
+                # before it starts the task's element, what comes after ends it)
+                marker = ast.Pass()
+                marker._lcd_walker_split = True
+                body = [marker if s is self._mailbox["mapped"] else s
+                        for s in body]
+            else:
+                body = [s for s in body if s is not self._mailbox["mapped"]]
+            location = (site.lineno, site.col_offset)
+            if location in self.reductions:
+                emitter.lowered_ids.add(self.reductions[location][0])
             mapped = None
         else:
             mapped = self._find_mapped_loop(body)
@@ -765,7 +783,8 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
             hooks.value_pull = self._value_pull
         if self._mailbox is not None:
             own = self._own_map.get(self._mailbox["own_text"])
-            if own is None or own[1] != "read":
+            if own is None or (own[1] != "read"
+                               and not self._mailbox.get("pulled")):
                 raise HIPLoweringError(
                     "The mailbox protocol needs the task's own element of "
                     f"{self._mailbox['array']!r} in a register.")
@@ -787,6 +806,9 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
             lines += stage
             epilogue = list(write_back) + list(epilogue)
         for statement in body:
+            if getattr(statement, "_lcd_walker_split", False):
+                self._walker["split"] = len(lines)
+                continue
             lines.extend(self._emit_guarded(statement, emitter, 0, hooks))
         lines.extend(epilogue)
         if self._walker is not None:

@@ -856,6 +856,50 @@ def test_band_walker(oracle, n, span, keep, tpb):
     assert plan.schedule.threads_per_block == (tpb or 1024)
 
 
+@pytest.mark.parametrize("n,span,keep,tpb", [
+    (3, 2, 1.0, 128), (64, 8, 1.0, 256), (130, 63, 1.0, None),
+    (1000, 8, 1.0, None), (4113, 63, 0.3, 512), (5000, 40, 0.1, None)])
+def test_band_walker_csr(oracle, n, span, keep, tpb):
+    """The pull-shaped solve on the walker: a task's element starts as b[i]
+    (staged per task, taken by the lane with the task), the row's products
+    are subtracted as their sources finish, the division by the diagonal
+    ends it -- the sequential loop's order, so bit for bit its result (the
+    other CSR executors sum a row's products first)."""
+    import scipy.sparse as sp
+    print("band walker, CSR", n, span, keep, tpb, flush=True)
+    indptr, indices, data = band_factor(n, (span, keep), seed=2 * n + span)
+    lower = sp.csc_matrix((data, indices, indptr), shape=(n, n)).tocsr()
+    lower.sort_indices()
+    rp, ci = lower.indptr.astype(np.int32), lower.indices.astype(np.int32)
+    rhs = np.random.default_rng(n + 1).standard_normal(n)
+    options = dict(execution_mode="sync_free", dependence_protocol="pull",
+                   task_lanes=8, band_walker=True)
+    if tpb:
+        options["threads_per_block"] = tpb
+    solver = sptrsv.compile_sptrsv_csr(**options)
+    expected = sptrsv.sptrsv_csr_loop(rp, ci, lower.data, rhs, n)
+    for _ in range(2):
+        result = solver(rp, ci, lower.data, rhs, n)
+        np.testing.assert_array_equal(result, expected)
+    assert relative_error(result, oracle.sptrsv_csr(rp, ci, lower.data, rhs,
+                                                    n)) <= TOLERANCE
+    plan = solver.schedule_plan(rp, ci, lower.data, rhs, n)
+    assert plan.band_walker and solver.hip_lowering.band_walker
+    # values the prepared reciprocal does not cover: the second pass
+    rhs[n // 2] = 0.0 if n < 200 else np.inf
+    with np.errstate(all="ignore"):
+        expected = sptrsv.sptrsv_csr_loop(rp, ci, lower.data, rhs, n)
+    np.testing.assert_array_equal(solver(rp, ci, lower.data, rhs, n), expected)
+    # chosen by itself for a chain in CSR form, not for a power-law matrix
+    auto = sptrsv.compile_sptrsv_csr(execution_mode="sync_free",
+                                     dependence_protocol="pull", task_lanes=8)
+    if keep == 1.0:
+        assert auto.schedule_plan(rp, ci, lower.data, rhs, n).band_walker
+    grid = workloads.configuration("c3", n=2000)
+    assert not auto.schedule_plan(grid.indptr, grid.indices, grid.data,
+                                  grid.rhs, grid.n).band_walker
+
+
 def test_band_walker_divides_again_where_the_prepared_reciprocal_does_not_apply(
         oracle):
     """Zero, tiny, huge and non-finite numerators and divisors: the blocks

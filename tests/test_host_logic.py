@@ -866,12 +866,37 @@ def test_band_walker_lowering_and_choice():
     assert "if (_w_lane < steps) x[base + _w_lane] = _lcd_wout;" in kernel
     assert "_lcd_own_0 = _lcd_own_0 + (_g_operand_0 * _g_value);" in kernel
     hip_runtime.compile_code(result.source)
-    # loops the walker does not take: a pull-shaped solve, chain tasks
-    csr = demo_source("sptrsv", "sptrsv_csr_loop")
+    # the pull-shaped solve (CSR) runs on the same walker: its row is the
+    # incoming listing, what precedes the row loop gives the element its
+    # first value (staged per task, taken by the lane when it starts the
+    # task), what follows finishes it
+    csr = lower(demo_source("sptrsv", "sptrsv_csr_loop"),
+                function_props=CSR_PROPS, execution_mode="sync_free",
+                thread_loop_iterator="j", task_lanes=8,
+                wavefront_threads_per_block=512, dependence_protocol="pull",
+                band_walker=True)
+    assert csr.band_walker and csr.dependence_protocol == "mailbox"
+    assert csr.kernel_arguments[6:9] == ["_lcd_in_ptr", "_lcd_in_pos",
+                                         "_lcd_in_src"]
+    kernel = csr.kernel_source
+    stage = kernel[kernel.index("auto _w_stage_tasks"):]
+    assert stage.index("_lcd_own_0 = _nl_0;") < stage.index(
+        "_w_uni[m & 3][l][2] = _lcd_own_0;")
+    assert "const double _w_start = _w_uni[(_w_m + 1) & 3][_w_lane][2];" in kernel
+    assert "_lcd_own_0 = lcd_bfi(_lcd_wmask, _w_start, _w_acc);" in kernel
+    assert "_lcd_own_0 = _lcd_wdiv(_lcd_own_0, _nl_2, _lcd_wr);" in kernel
+    assert "_lcd_own_0 = _lcd_own_0 - (_g_operand_0 * _g_value);" in kernel
+    assert "_thread_partial" not in kernel and "lcd_ld" not in kernel
+    hip_runtime.compile_code(csr.source)
+    # a loop the walker does not take: ILU0 (its producers are enumerated by
+    # a sequential loop of the task)
+    ilu = demo_source("spilu0", "ilu0_csr")
     with pytest.raises(HIPLoweringError, match="band walker"):
-        lower(csr, function_props=CSR_PROPS, execution_mode="sync_free",
-              thread_loop_iterator="j", task_lanes=8,
-              dependence_protocol="pull", band_walker=True)
+        lower(ilu, function_props={
+            "A_indptr": ["monotonically_increasing"],
+            ("A_indptr", "A_indices"): ["segmented_monotonically_increasing"]},
+            execution_mode="sync_free", thread_loop_iterator="j_ptr",
+            task_lanes=8, dependence_protocol="pull", band_walker=True)
 
     # a workgroup of one wavefront has nobody to stage for the walker
     with pytest.raises(HIPLoweringError, match="two wavefronts"):
