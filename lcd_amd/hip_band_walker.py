@@ -6,8 +6,9 @@ is all the persistent executor does.  The walker runs the tasks in program
 order on ONE wavefront instead: lane ``t % 64`` holds task ``t``, a finished
 value goes to the other lanes with two read-lanes, nothing is polled and
 nothing waits.  It serves loops in the gathered mailbox form (the CSC solve:
-``x[i] = f(x[i]); for j in column i: x[Ai[j]] += Ax[j] * x[i]``) whose edges
-all span fewer than 64 iterations.
+``x[i] = f(x[i]); for j in column i: x[Ai[j]] += Ax[j] * x[i]``) and their
+pull-shaped twins (the CSR solve: ``x[i] = b[i]; for j in row i: x[i] -=
+Ax[j] * x[Ai[j]]; x[i] /= d``) whose edges all span fewer than 64 iterations.
 
 What stays on the chain between two tasks is the task's own arithmetic.  The
 rest of the workgroup prepares it: per block of 64 tasks the other wavefronts
