@@ -41,9 +41,11 @@ METRIC = "SpTRSV/SpILU0 solve ms, GFLOP/s, HBM GB/s (% roofline) on 1 MI355X"
 # Executor settings per configuration (the fastest measured on MI355X; every
 # one can be overridden on the command line).
 TUNED = {
-    "c1": dict(execution_mode="sync_free", threads_per_block=256, task_lanes=4,
-               thread_unroll=1, dependence_protocol="mailbox",
-               tile_rows=1024, spin_sleep=0),
+    # (a small DAG with narrow levels: the level walker, one wavefront that
+    # takes a level per step, chosen per plan; --level-walker 0 gives the tiles
+    # of 1024 rows with 256 threads)
+    "c1": dict(execution_mode="sync_free", task_lanes=4,
+               thread_unroll=1, dependence_protocol="mailbox", spin_sleep=0),
     # (tiles are boxes of 128 x 8 x 4 grid points: the default tile_box="auto")
     "c2": dict(execution_mode="sync_free", threads_per_block=512, task_lanes=4,
                thread_unroll=1, dependence_protocol="mailbox",
@@ -81,7 +83,7 @@ def traffic_key(config, mode, protocol, lanes, tile_rows, tile_box=None,
                 walker=False):
     key = f"{config}|{mode}|{protocol}|lanes={lanes}|tile_rows={tile_rows or 0}"
     if walker:
-        key = f"{config}|{mode}|{protocol}|band_walker"
+        key = f"{config}|{mode}|{protocol}|{walker}"
     if tile_box:
         key += "|box=" + "x".join(str(extent) for extent in tile_box)
     return key
@@ -145,6 +147,11 @@ def build_solver(work, args, config):
         if not args.band_walker and config == "c5" and not args.auto:
             options.setdefault("threads_per_block", 128)
             options.setdefault("tile_rows", 8192)
+    if args.level_walker is not None:
+        options["level_walker"] = bool(args.level_walker)
+        if not args.level_walker and config == "c1" and not args.auto:
+            options.setdefault("threads_per_block", 256)
+            options.setdefault("tile_rows", 1024)
     if args.no_queue_loads:
         options["queue_node_loads"] = False
     if args.plain_first is not None:
@@ -323,6 +330,7 @@ def run_configuration(config, args, device, steps, warmup, handoff_s,
             "tile_box": (list(plan.tile_boxes[1])
                          if getattr(plan, "tile_boxes", None) else None),
             "band_walker": bool(getattr(plan, "band_walker", False)),
+            "level_walker": bool(getattr(plan, "level_walker", 0)),
             "replayed_from_graph": not args.no_graph,
         },
         "roofline_pct": round(100.0 * gbps / HBM_PEAK_GBPS, 3),
@@ -381,7 +389,10 @@ def run_configuration(config, args, device, steps, warmup, handoff_s,
                       lowering.dependence_protocol, lowering.task_lanes,
                       tile_rows,
                       plan.tile_boxes[1] if getattr(plan, "tile_boxes", None)
-                      else None, bool(getattr(plan, "band_walker", False)))
+                      else None,
+                      "band_walker" if getattr(plan, "band_walker", False)
+                      else "level_walker" if getattr(plan, "level_walker", 0)
+                      else False)
     record["roofline"] = {
         "bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBPS,
         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 6),
@@ -453,6 +464,11 @@ def main():
                         default=None, choices=(0, 1),
                         help="1: run chain-like DAGs on one wavefront in "
                              "program order; 0: never (default: per plan)")
+    parser.add_argument("--level-walker", dest="level_walker", type=int,
+                        default=None, choices=(0, 1),
+                        help="1: run small DAGs with narrow levels on one "
+                             "wavefront, a level per step; 0: never (default: "
+                             "per plan)")
     parser.add_argument("--tile-box", dest="tile_box", default=None,
                         help="tiles over boxes of a structured grid: "
                              "'auto', 'none' or extents as 32x8x16")
@@ -540,7 +556,8 @@ def main():
         for name in ("mode", "tpb", "lanes", "unroll", "protocol",
                      "waves_per_cu", "spin_sleep", "tile_rows",
                      "plain_first", "look_ahead", "tile_positions",
-                     "segment_capacity", "tile_box", "band_walker"):
+                     "segment_capacity", "tile_box", "band_walker",
+                     "level_walker"):
             setattr(sub_args, name, None)
         for name in ("slots", "no_queue_loads", "no_publish", "no_pipeline",
                      "no_graph", "level_gather"):

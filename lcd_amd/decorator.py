@@ -44,7 +44,12 @@ from lcd_amd.dag_preprocessing import (
     execution_data_from_device_dag,
 )
 from lcd_amd.dependence import DependenceAnalysis, analyze_dependences
-from lcd_amd.hip_emitter import HIPLoweringError
+from lcd_amd.hip_emitter import (
+    HIPLoweringError,
+    LEVEL_WALKER_ARGUMENTS,
+    LEVEL_WALKER_ENTRIES,
+    LEVEL_WALKER_TASKS,
+)
 from lcd_amd.hip_lowering import lower_to_hip
 from lcd_amd.hip_runtime import (
     compile_hip_module,
@@ -68,6 +73,7 @@ from lcd_amd.scheduler import (
     TILE_THREADS_PER_BLOCK,
     automatic_tile_box,
     band_walker_applies,
+    level_walker_records,
     automatic_tile_rows,
     structured_grid,
     automatic_tile_threads,
@@ -216,6 +222,9 @@ def parallel(**kwargs):
         walker_option = kwargs.get("band_walker", "auto")
         if walker_option not in ("auto", True, False):
             raise ValueError("band_walker must be 'auto', True or False.")
+        level_option = kwargs.get("level_walker", "auto")
+        if level_option not in ("auto", True, False):
+            raise ValueError("level_walker must be 'auto', True or False.")
 
         registers_option = kwargs.get("segment_registers", "auto")
         if registers_option not in ("auto", True, False):
@@ -223,9 +232,9 @@ def parallel(**kwargs):
 
         def lower_variant(lowering_key, tile_rows=None, single_chunk=False,
                           task_records=True, by_position=False,
-                          registers=False, walker=False):
+                          registers=False, walker=False, level=0):
             variant_key = (lowering_key, tile_rows, single_chunk, task_records,
-                           by_position, registers, walker)
+                           by_position, registers, walker, level)
             if variant_key not in lowered_variants:
                 (mode, threads_per_block, unroll, n_warp, protocol,
                  task_lanes) = lowering_key
@@ -273,6 +282,7 @@ def parallel(**kwargs):
                     segment_registers=bool(registers),
                     pair_tables=registers == 2,
                     band_walker=walker,
+                    level_walker=level,
                     full_fences=kwargs.get("full_fences", False),
                     dynamic_fetch=kwargs.get("dynamic_fetch", False),
                 )
@@ -280,12 +290,12 @@ def parallel(**kwargs):
 
         def compile_variant(lowering_key, tile_rows=None, single_chunk=False,
                             task_records=True, by_position=False,
-                            registers=False, walker=False):
+                            registers=False, walker=False, level=0):
             lowering = lower_variant(lowering_key, tile_rows, single_chunk,
                                      task_records, by_position, registers,
-                                     walker)
+                                     walker, level)
             variant_key = (lowering_key, tile_rows, single_chunk, task_records,
-                           by_position, registers, walker)
+                           by_position, registers, walker, level)
             if variant_key not in compiled_variants:
                 compiled_variants[variant_key] = compile_hip_module(
                     lowering, function_globals=function.__globals__)
@@ -449,6 +459,54 @@ def parallel(**kwargs):
                         "span fewer than 64 iterations.")
                 return None
             return candidate, lowering
+
+        def level_walker_for(dag, schedule, build_incoming):
+            """(schedule, lowering, dag, tables) when this plan runs on the
+            level walker: a small DAG with narrow levels and few incoming
+            entries per task (``level_walker=True`` asks for it, the
+            default takes it unless the call fixes a tile size)."""
+            if level_option is False:
+                return None
+            forced = level_option is True
+            usable = (schedule.execution_mode == SYNC_FREE and band_width == 1
+                      and schedule.lowering_key[4] in (MAILBOX_DEPENDENCE,
+                                                       PULL_DEPENDENCE)
+                      and (forced or not isinstance(tile_option, int))
+                      and 0 < dag.n <= LEVEL_WALKER_TASKS and dag.edges > 0)
+            records = lowering = None
+            candidate = schedule
+            if usable:
+                if not incoming_positions:
+                    dag = build_incoming()
+                records = level_walker_records(dag, LEVEL_WALKER_TASKS,
+                                               LEVEL_WALKER_ENTRIES)
+                usable = records is not None
+            if usable:
+                candidate = replace(schedule, thread_unroll=1)
+                if kwargs.get("threads_per_block") is None:
+                    candidate = replace(
+                        candidate,
+                        threads_per_block=BAND_WALKER_THREADS_PER_BLOCK)
+                try:
+                    lowering = lower_variant(candidate.lowering_key, None,
+                                             False, False, False, 0, False,
+                                             records[0])
+                except HIPLoweringError:
+                    if forced:
+                        raise
+                    usable = False
+            if not usable:
+                if forced:
+                    raise ValueError(
+                        "level_walker=True needs the persistent executor with "
+                        "the mailbox or pull protocol and a DAG of at most "
+                        f"{LEVEL_WALKER_TASKS} tasks, 64 per level, "
+                        f"{LEVEL_WALKER_ENTRIES} incoming entries per task.")
+                return None
+            device = get_device()
+            tables = {name: device.to_device(values) for name, values in zip(
+                LEVEL_WALKER_ARGUMENTS, records[1:])}
+            return candidate, lowering, dag, tables, records[0]
 
         def boxes_for(dag, schedule, rows):
             """(grid, box) when the tiles of this plan are boxes of a
@@ -616,7 +674,10 @@ def parallel(**kwargs):
                     thread_trip_counts=trip_counts(dag_values),
                     edges=dag.edges)
                 schedule = scheduler.schedule(features, schedule_space)
-            walker = walker_for(dag, schedule)
+            # (a walker asked for by name goes before the other's automatic
+            # choice)
+            walker = (None if level_option is True and walker_option != True
+                      else walker_for(dag, schedule))
             if walker is not None:
                 schedule, lowering = walker
                 if not incoming_positions:
@@ -635,6 +696,25 @@ def parallel(**kwargs):
                     features=features, dag=dag, tile_rows=None,
                     single_chunk=False, task_records=False,
                     band_walker=True)
+                plan_state[id(plan)] = {"resident": resident, "workspace": {}}
+                return plan
+            level = level_walker_for(
+                dag, schedule, lambda: build_device_dag(
+                    dag_plan, device_values, device, levels=True,
+                    incoming=True))
+            if level is not None:
+                schedule, lowering, dag, tables, entries = level
+                execution_data = execution_data_from_device_dag(
+                    dag, schedule.execution_mode, lowering.warp_mapped,
+                    band_width=band_width, mailbox=True, tile_rows=None,
+                    record_lanes=None)
+                plan = SchedulePlan(
+                    schedule=schedule,
+                    execution_data=attach_auxiliary_values(
+                        execution_data, {**lookup_values, **tables}),
+                    features=features, dag=dag, tile_rows=None,
+                    single_chunk=False, task_records=False,
+                    level_walker=entries)
                 plan_state[id(plan)] = {"resident": resident, "workspace": {}}
                 return plan
             schedule, tile_rows = tiles_for(dag, schedule, device_values)
@@ -741,7 +821,8 @@ def parallel(**kwargs):
                                                  plan.task_records,
                                                  plan.tile_boxes is not None,
                                                  plan.segment_registers,
-                                                 plan.band_walker)
+                                                 plan.band_walker,
+                                                 plan.level_walker)
             publish_variant(plan.schedule, lowering, compiled)
             state = plan_state[id(plan)]
             values = dict(argument_values)

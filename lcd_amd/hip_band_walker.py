@@ -61,7 +61,8 @@ class BandWalkerMixin:
                 and isinstance(value.right, ast.Name)
                 and {value.left.id, value.right.id} == {operand, "_g_value"}):
             return None
-        return {"operand": operand, "division": False, "quotient_is_value": False}
+        return {"operand": operand, "division": False,
+                "quotient_is_value": False, "kind": "band"}
 
     def _band_walker_division(self, body):
         """``a / d`` with ``d`` one of the task's node loads (known a block
@@ -130,7 +131,9 @@ class BandWalkerMixin:
         for line in lines:
             if store.match(line.strip()):
                 found += 1
-                out.append(f"_lcd_wout = lcd_bfi(_lcd_wmask, {register}, "
+                out.append(f"_lcd_wout = {register};"
+                           if self._walker.get("kind") == "level" else
+                           f"_lcd_wout = lcd_bfi(_lcd_wmask, {register}, "
                            "_lcd_wout);")
             else:
                 out.append(line)
@@ -442,6 +445,183 @@ class BandWalkerMixin:
             "            _w_clear(_w_m + 2, first, _w_stagers);",
             "            _w_stage_ptr(_w_m + 2, first, _w_stagers);",
             "            _w_stage_tasks(_w_m + 2, first, _w_stagers);",
+            "        }",
+            "        __syncthreads();",
+            "    }",
+        ]
+        return lines
+
+    # ---- the level walker: small DAGs with narrow levels
+    def _level_walker_text(self, task_lines):
+        """Kernel body for a DAG of at most LCD_LW_TASKS tasks whose levels
+        hold at most 64 of them and whose tasks have at most LCD_LW_ENTRIES
+        incoming entries: ONE wavefront takes a level per step, one task per
+        lane.  The values live in LDS; a level's reads follow the stores of
+        the levels before it in program order, so nothing is polled.  The
+        structure comes level-major from the inspector (``_lcd_lw_task``: the
+        task of (level, lane) or -1; ``_lcd_lw_src`` / ``_lcd_lw_pos``: the
+        source and the operand position of its k-th incoming entry, in the
+        listing's order, or the dummy slot / -1); the other wavefronts gather
+        operands and node loads into an LDS ring, blocks of eight levels, two
+        blocks ahead.  No arithmetic differs from the sequential loop's."""
+        plan = self._walker
+        it = self.loop_iterator
+        box = self._mailbox
+        gather = box["gather"]
+        emitter = self._emitter
+        register = box["register"]
+        array = box["array"]
+        operand, operand_node, _ = gather["operands"][0]
+        sign = "-" if gather["negate"] else "+"
+        product = emitter.expr(gather["value"])
+        entries = int(plan["entries"])
+        split = plan.get("split", 0) if box.get("pulled") else 0
+        head_lines, tail_lines = task_lines[:split], task_lines[split:]
+        assign = re.compile(r"^(\w+) = (.*);$")
+        stage_lines, staged, zero_start = [], [], False
+        for line in self._prefetch_lines:
+            match = assign.match(line.strip())
+            if match is None:
+                return None
+            if match.group(1) == register:
+                if match.group(2) != "0.0":
+                    return None
+                zero_start = True
+                continue
+            stage_lines.append(line.strip())
+            staged.append(match.group(1))
+        if not head_lines and not zero_start:
+            return None
+        for line in head_lines:
+            match = assign.match(line.strip())
+            if match is None:
+                return None
+            if match.group(1) != register:
+                staged.append(match.group(1))
+        tail_text = "\n".join(tail_lines)
+        slots = [(name, self._kinds.locals.get(name, FLOAT))
+                 for name in dict.fromkeys(staged)
+                 if re.search(r"\b" + re.escape(name) + r"\b", tail_text)]
+        if head_lines:
+            slots.append((register, FLOAT))
+        width = max(1, len(slots))
+
+        def put(name, kind, where):
+            return (f"{where} = (double){name};" if kind == INT
+                    else f"{where} = {name};")
+
+        def take(name, kind, what):
+            return (f"{name} = (lcd_index_t){what};" if kind == INT
+                    else f"{name} = {what};")
+
+        p3, p4 = " " * 12, " " * 16
+        first_value = (f"_w_uni[rb][l][{len(slots) - 1}][_w_lane]" if head_lines
+                       else "0.0")
+        lines = [
+            "    // ---- level walker: one wavefront takes a level per step",
+            "    if (blockIdx.x != 0) return;",
+            "    const int _w_lane = threadIdx.x & 63;",
+            "    const int _w_wave = threadIdx.x >> 6;",
+            "    const int _w_n = (int)task_count;",
+            f"    constexpr int LW_K = {entries}, LW_B = 8;",
+            "    const int _w_levels = (int)_lcd_lw_levels;",
+            "    const int _w_blocks = (_w_levels + LW_B - 1) / LW_B;",
+            "    const int _w_helpers = LCD_TPB - 64;",
+            "    __shared__ double _w_x[LCD_LW_TASKS + 1];",
+            "    __shared__ double _w_coef[3][LW_B][LW_K][64];",
+            "    __shared__ short _w_src[3][LW_B][LW_K][64];",
+            f"    __shared__ double _w_uni[3][LW_B][{width}][64];",
+            "    __shared__ int _w_task[3][LW_B][64];",
+            "    lcd_index_t _g_pos = 0, _g_src = 0; double _g_value = 0.0;",
+            f"    double {operand} = 0.0; double _lcd_wout = 0.0;",
+            "    (void)_g_pos; (void)_g_src;",
+            "    if (_w_n > LCD_LW_TASKS) { if (threadIdx.x == 0) _lcd_status[0] = 2; return; }",
+            "    auto _w_stage = [&](int m, int first, int step) {",
+            "        // block m of the levels: tasks, node loads, sources and operands",
+            "        if (m >= _w_blocks) return;",
+            "        const int rb = m % 3;",
+            "        for (int c = first; c < LW_B * 64; c += step) {",
+            "            const int l = c >> 6, lane = c & 63, level = m * LW_B + l;",
+            "            const int task = level < _w_levels ? "
+            "(int)_lcd_lw_task[level * 64 + lane] : -1;",
+            "            _w_task[rb][l][lane] = task;",
+            "            if (task >= 0) {",
+            f"                {it} = (lcd_index_t)task;",
+            *[p4 + line for line in stage_lines],
+            *[p4 + line for line in head_lines],
+            *[p4 + put(name, kind, f"_w_uni[rb][l][{k}][lane]")
+              for k, (name, kind) in enumerate(slots)],
+            "            }",
+            "        }",
+            "        for (int c = first; c < LW_B * LW_K * 64; c += step) {",
+            "            const int lane = c & 63, k = (c >> 6) % LW_K, l = c / (64 * LW_K);",
+            "            const int level = m * LW_B + l;",
+            # (x + -0.0 and x - +0.0 leave every x as it is, signed zeros included)
+            "            int src = LCD_LW_TASKS; double coef = "
+            + ("-0.0" if sign == "+" else "0.0") + ";",
+            "            if (level < _w_levels) {",
+            "                const long long at = ((long long)level * LW_K + k) * 64 + lane;",
+            "                _g_pos = (lcd_index_t)_lcd_lw_pos[at];",
+            "                if (_g_pos >= 0) {",
+            "                    _g_src = (lcd_index_t)_lcd_lw_src[at]; src = (int)_g_src;",
+            f"                    coef = {emitter.expr(operand_node)};",
+            "                }",
+            "            }",
+            "            _w_src[rb][l][k][lane] = (short)src;",
+            "            _w_coef[rb][l][k][lane] = coef;",
+            "        }",
+            "    };",
+            "    // (an entry that is not there reads the slot past the last task, which",
+            "    // holds zero, with a zero operand)",
+            "    for (int c = threadIdx.x; c < LCD_LW_TASKS + 1; c += LCD_TPB) _w_x[c] = 0.0;",
+            "    _w_stage(0, threadIdx.x, LCD_TPB); _w_stage(1, threadIdx.x, LCD_TPB);",
+            "    __syncthreads();",
+            "    for (int _w_m = 0; _w_m < _w_blocks; ++_w_m) {",
+            "        if (_w_wave == 0) {",
+            "            const int rb = _w_m % 3;",
+            # what a level reads from the ring is in registers a level ahead:
+            # the step then waits for one trip to LDS (the sources' values)
+            "            int _w_t = _w_task[rb][0][_w_lane];",
+            "            short _w_s[LW_K]; double _w_c[LW_K];",
+            f"            double _w_u[{width}];",
+            "#pragma unroll",
+            "            for (int k = 0; k < LW_K; ++k) { _w_s[k] = _w_src[rb][0][k][_w_lane]; "
+            "_w_c[k] = _w_coef[rb][0][k][_w_lane]; }",
+            "#pragma unroll",
+            f"            for (int k = 0; k < {width}; ++k) _w_u[k] = _w_uni[rb][0][k][_w_lane];",
+            "#pragma unroll 2",
+            "            for (int l = 0; l < LW_B; ++l) {",
+            "                const int ln = l + 1 < LW_B ? l + 1 : l;",
+            "                const int task = _w_t;",
+            "                double _w_v[LW_K];",
+            "#pragma unroll",
+            "                for (int k = 0; k < LW_K; ++k) _w_v[k] = _w_x[_w_s[k]];",
+            f"                {it} = (lcd_index_t)(task < 0 ? 0 : task);",
+            f"                {register} = " + (f"_w_u[{len(slots) - 1}]" if head_lines else "0.0") + ";",
+            *[p4 + take(name, kind, f"_w_u[{k}]")
+              for k, (name, kind) in enumerate(slots)
+              if not (head_lines and k == len(slots) - 1)],
+            "                double _w_cc[LW_K];",
+            "#pragma unroll",
+            "                for (int k = 0; k < LW_K; ++k) _w_cc[k] = _w_c[k];",
+            "                _w_t = _w_task[rb][ln][_w_lane];",
+            "#pragma unroll",
+            "                for (int k = 0; k < LW_K; ++k) { _w_s[k] = _w_src[rb][ln][k][_w_lane]; "
+            "_w_c[k] = _w_coef[rb][ln][k][_w_lane]; }",
+            "#pragma unroll",
+            f"                for (int k = 0; k < {width}; ++k) _w_u[k] = _w_uni[rb][ln][k][_w_lane];",
+            "#pragma unroll",
+            "                for (int k = 0; k < LW_K; ++k) {",
+            f"                    _g_value = _w_v[k]; {operand} = _w_cc[k];",
+            f"                    {register} = {register} {sign} {product};",
+            "                }",
+            *[p4 + line for line in tail_lines],
+            "                if (task >= 0) {",
+            f"                    _w_x[task] = _lcd_wout; {array}[task] = _lcd_wout;",
+            "                }",
+            "            }",
+            "        } else {",
+            "            _w_stage(_w_m + 2, threadIdx.x - 64, _w_helpers);",
             "        }",
             "        __syncthreads();",
             "    }",

@@ -36,6 +36,13 @@ PULL_ARGUMENTS = ("done", "task_nodes", "task_ptr", "task_counter",
 GATHER_ARGUMENTS = ("_lcd_in_ptr", "_lcd_in_pos", "_lcd_in_src",
                     "task_nodes", "task_ptr", "task_counter", "task_count")
 VALUE_PULL_ARGUMENTS = ("task_nodes", "task_ptr", "task_counter", "task_count")
+# level walker: the structure level-major from the inspector (task of (level,
+# lane); source and operand position of its k-th incoming entry) and the
+# number of levels
+LEVEL_WALKER_ARGUMENTS = ("_lcd_lw_task", "_lcd_lw_src", "_lcd_lw_pos")
+LEVEL_WALKER_LEVELS = "_lcd_lw_levels"
+LEVEL_WALKER_TASKS = 4096      # tasks whose values fit the LDS copy
+LEVEL_WALKER_ENTRIES = 4       # incoming entries per task the ring has room for
 VALUE_WAIT_BEGIN = "//@lcd-wait-begin"
 VALUE_WAIT_END = "//@lcd-wait-end"
 MAILBOX_ARGUMENTS = ("_lcd_mailbox", "_lcd_in_ptr", "_lcd_out_slot",
@@ -117,6 +124,9 @@ class HIPLoweringResult:
     # one wavefront runs the tasks in program order (chain-like DAGs whose
     # edges span fewer than 64 iterations)
     band_walker: bool = False
+    # one wavefront takes a level per step (small DAGs with narrow levels):
+    # the incoming entries per task it has room for, or 0
+    level_walker: int = 0
     # the pointer array of the task's own segment (ILU0's row), and whether
     # that segment is kept in registers (segments of at most 64 entries)
     segment_pointer: str | None = None

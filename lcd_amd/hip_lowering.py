@@ -44,6 +44,9 @@ from lcd_amd.hip_emitter import (
     HIPLoweringError,
     HIPLoweringResult,
     INT,
+    LEVEL_WALKER_ARGUMENTS,
+    LEVEL_WALKER_LEVELS,
+    LEVEL_WALKER_TASKS,
     MAILBOX_ARGUMENTS,
     MAILBOX_DEPENDENCE,
     PULL_ARGUMENTS,
@@ -103,9 +106,11 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                  pipeline_fetch=True, full_fences=False,
                  dynamic_fetch=False, tile_positions=None,
                  tile_by_position=False, segment_registers=False,
-                 pair_tables=True, band_walker=False):
+                 pair_tables=True, band_walker=False, level_walker=0):
         self.tile_positions = tile_positions
         self.band_walker = bool(band_walker)
+        # > 0: the level walker, with room for this many incoming entries per task
+        self.level_walker = int(level_walker or 0)
         self._walker = None
         self.tile_by_position = tile_by_position
         self.segment_registers = segment_registers
@@ -328,7 +333,8 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
         elif (self.dependence_protocol == PULL_DEPENDENCE and self.value_flags
                 and self.execution_mode == "sync_free"):
             self._value_pull = self._value_pull_plan(body)
-        if (self.band_walker and self._value_pull is not None
+        if ((self.band_walker or self.level_walker)
+                and self._value_pull is not None
                 and self.dependence_protocol == PULL_DEPENDENCE):
             # the pull-shaped solve in the terms of the gathered mailbox: the
             # walker serves both
@@ -343,8 +349,13 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                     and self._mailbox["gather"] is None):
                 self._mailbox["gather"] = self._gather_plan(
                     self._mailbox, arguments, lifted_loop_parameters)
-        if self.band_walker:
+        if self.band_walker or self.level_walker:
             self._walker = self._band_walker_plan(target_loop)
+            if self._walker is not None and self.level_walker:
+                self._walker.update(kind="level", entries=self.level_walker)
+                for name in LEVEL_WALKER_ARGUMENTS:
+                    kinds.arrays[name] = INT
+                kinds.scalars[LEVEL_WALKER_LEVELS] = INT
             if self._walker is None:
                 raise HIPLoweringError(
                     "The band walker needs the persistent executor's gathered "
@@ -448,6 +459,8 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
             user_arguments.append(entry[1])
             if entry[0] == "pair":
                 user_arguments.append("_lcd_pair_base")
+        if self._walker is not None and self._walker["kind"] == "level":
+            user_arguments += [*LEVEL_WALKER_ARGUMENTS, LEVEL_WALKER_LEVELS]
         if (self.thread_loop_iterator is not None
                 and self.dependence_protocol != COUNTER_DEPENDENCE
                 and self._sequential_pull is None):
@@ -545,7 +558,10 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
             tile_rows=self._tile["rows"] if self._tile else None,
             tile_by_position=bool(self._tile
                                   and self._tile.get("by_position")),
-            band_walker=self._walker is not None,
+            band_walker=bool(self._walker
+                             and self._walker["kind"] == "band"),
+            level_walker=(self.level_walker if self._walker
+                          and self._walker["kind"] == "level" else 0),
             segment_pointer=(self._segment["pointer"]
                              if self._segment else None),
             segment_registers=bool(self._segment
@@ -771,7 +787,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
         if self.prefetch_node_loads:
             body, self._prefetch_lines = self._hoist_node_loads(
                 body, mapped, arguments)
-        if self._walker is not None:
+        if self._walker is not None and self._walker["kind"] == "band":
             body = self._band_walker_division(body)
         if self._value_pull is not None:
             own = self._own_map.get(
@@ -898,6 +914,8 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
             "#ifndef LCD_SPIN_SLEEP",
             f"#define LCD_SPIN_SLEEP {self.spin_sleep}", "#endif",
         ]
+        if self._walker is not None and self._walker["kind"] == "level":
+            defines.append(f"#define LCD_LW_TASKS {LEVEL_WALKER_TASKS}")
         if self._segment is not None:
             defines.append(f"#define LCD_SEG_CAP {self._segment['capacity']}")
         if self._tile is not None:
@@ -1120,7 +1138,9 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
             lines.append("    if (_task >= band_end) return;")
             lines += node_loop(1, task)
         elif self._walker is not None:
-            walker = self._band_walker_text(task_body)
+            walker = (self._level_walker_text(task_body)
+                      if self._walker["kind"] == "level"
+                      else self._band_walker_text(task_body))
             if walker is None:
                 raise HIPLoweringError(
                     "The band walker cannot stage this task's node loads.")
@@ -1460,7 +1480,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                 if "band_ptr" not in launcher_arguments:
                     launcher_arguments.append("band_ptr")
                 continue
-            if name == "task_count":
+            if name in ("task_count", LEVEL_WALKER_LEVELS):
                 continue
             launcher_arguments.append(name)
         args = []
@@ -1469,6 +1489,8 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                 args.append("0")
             elif name == "task_count":
                 args.append("_count")
+            elif name == LEVEL_WALKER_LEVELS:
+                args.append(f"_hip.length({LEVEL_WALKER_ARGUMENTS[0]}) // 64")
             else:
                 args.append(name)
         call_args = "(" + ", ".join(args) + ("," if len(args) == 1 else "") + ")"
@@ -1521,8 +1543,11 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                 body.append("_count = _hip.length(task_ptr) - 1")
             else:
                 body.append(f"_count = _hip.length({count_array})")
-            body.append(f"_hip.launch({reset_name!r}, ({reset_count} + 255) // 256 or 1, "
-                        f"256, {reset_args})")
+            if self._walker is None:
+                # (a walker polls nothing and writes every element: nothing
+                # to restore before a launch)
+                body.append(f"_hip.launch({reset_name!r}, ({reset_count} + 255) "
+                            f"// 256 or 1, 256, {reset_args})")
             stage_name, stage_arguments = self._stage
             if stage_name is not None:
                 for name in stage_arguments:
@@ -1587,7 +1612,8 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
                  publish_values=True, look_ahead=True, segment_capacity=None,
                  pipeline_fetch=True, full_fences=False, dynamic_fetch=False,
                  tile_positions=None, tile_by_position=False,
-                 segment_registers=False, pair_tables=True, band_walker=False):
+                 segment_registers=False, pair_tables=True, band_walker=False,
+                 level_walker=0):
     """HIP counterpart of ``lower_to_numba_cuda``
     (compiler/cuda_lowering.py:2854-2884); same parameters plus
     ``task_lanes`` (lanes cooperating on one task, a power of two <= 64),
@@ -1617,5 +1643,5 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
         dynamic_fetch=dynamic_fetch, tile_positions=tile_positions,
         tile_by_position=tile_by_position,
         segment_registers=segment_registers, pair_tables=pair_tables,
-        band_walker=band_walker)
+        band_walker=band_walker, level_walker=level_walker)
     return lowerer.lower(code)

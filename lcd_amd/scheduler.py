@@ -163,6 +163,9 @@ class SchedulePlan:
     segment_registers: int = 0
     # one wavefront runs the tasks in program order (chain-like DAGs)
     band_walker: bool = False
+    # one wavefront takes a level per step (small DAGs with narrow levels):
+    # the incoming entries per task it has room for, or 0
+    level_walker: int = 0
 
 
 # Tiled executor, automatic choice: tiles of 4096 consecutive block-iterator
@@ -259,6 +262,53 @@ def band_walker_applies(dag, forced=False):
     offsets, _, distinct = dag.edge_offsets(BAND_WALKER_SPAN)
     return (0 < distinct < BAND_WALKER_SPAN and offsets[0] >= 1
             and offsets[-1] < BAND_WALKER_SPAN)
+
+
+# Level walker, automatic choice: a DAG small enough for its values to live in
+# one workgroup's LDS (4096 tasks), with at most 64 tasks per level and four
+# incoming entries per task.  One wavefront then takes a level per step in
+# about 0.1 us (232 cycles measured on the bare step) where the persistent
+# executors pay a polled hand-off of 0.5 us per level: the 64 x 64 grid of
+# configuration 1, 127 levels.
+LEVEL_WALKER_WIDTH = 64
+
+
+def level_walker_records(dag, max_tasks, max_entries, forced=False):
+    """The structure level-major for the level walker -- ``(entries, task,
+    source, position)`` with ``task[level * 64 + lane]``, ``source`` and
+    ``position[(level * entries + k) * 64 + lane]`` (-1: no task, no entry;
+    the dummy source is ``max_tasks``) -- or None when the DAG does not fit:
+    more than ``max_tasks`` tasks, a level of more than 64, a task with more
+    than ``max_entries`` incoming entries.  Built on the host: the DAG is
+    small by definition."""
+    if dag.n == 0 or dag.n > max_tasks or dag.edges == 0:
+        return None
+    pointer = np.asarray(dag.host("wavefront_ptr"), dtype=np.int64)
+    widths = np.diff(pointer)
+    if len(widths) == 0 or widths.max() > LEVEL_WALKER_WIDTH:
+        return None
+    in_ptr = np.asarray(dag.host("in_ptr"), dtype=np.int64)
+    counts = np.diff(in_ptr)
+    entries = int(counts.max()) if len(counts) else 0
+    if entries < 1 or entries > max_entries:
+        return None
+    nodes = np.asarray(dag.host("wavefronts"), dtype=np.int64)
+    in_src = np.asarray(dag.host("in_src"), dtype=np.int32)
+    in_pos = np.asarray(dag.host("in_pos"), dtype=np.int32)
+    levels = len(widths)
+    level_of = np.repeat(np.arange(levels), widths)
+    lane_of = np.arange(len(nodes)) - pointer[level_of]
+    task = np.full(levels * 64, -1, dtype=np.int32)
+    task[level_of * 64 + lane_of] = nodes
+    source = np.full(levels * entries * 64, max_tasks, dtype=np.int32)
+    position = np.full(levels * entries * 64, -1, dtype=np.int32)
+    for k in range(entries):
+        has = counts[nodes] > k
+        at = (level_of[has] * entries + k) * 64 + lane_of[has]
+        which = in_ptr[nodes[has]] + k
+        source[at] = in_src[which]
+        position[at] = in_pos[which]
+    return entries, task, source, position
 
 
 def structured_grid(dag):

@@ -1046,6 +1046,77 @@ def test_band_walker_other_loops(loop):
         loop is walker_subtracting)
 
 
+def test_level_walker(oracle):
+    """Small DAGs with narrow levels run on one wavefront, a level per step,
+    values in LDS: no poll, the sequential loop's arithmetic, bit for bit --
+    for the push-shaped solve (CSC) and the pull-shaped one (CSR, against the
+    loop itself run by CPython)."""
+    import scipy.sparse as sp
+    walker = dict(execution_mode="sync_free", task_lanes=4, level_walker=True)
+    csc = sptrsv.compile_sptrsv_csc(dependence_protocol="mailbox", **walker)
+    csr = sptrsv.compile_sptrsv_csr(dependence_protocol="pull", **walker)
+    cases = [workloads.configuration("c1"),
+             workloads.configuration("c1", nx=37, ny=11),
+             workloads.configuration("c2", nx=6, ny=5, nz=7),
+             workloads.configuration("c5", n=300, bandwidth=3)]
+    for work in cases:
+        print("level walker", work.name, flush=True)
+        expected = oracle.sptrsv_csc(work.indptr, work.indices, work.data,
+                                     work.rhs, work.n)
+        for _ in range(2):
+            solve_and_check(csc, work, expected, exact=True)
+        plan = csc.schedule_plan(work.indptr, work.indices, work.data,
+                                 work.rhs, work.n)
+        assert plan.level_walker >= 1 and csc.hip_lowering.level_walker
+        assert "lcd_ld" not in csc.hip_kernel_source
+        lower = sp.csc_matrix((work.data, work.indices, work.indptr),
+                              shape=(work.n, work.n)).tocsr()
+        lower.sort_indices()
+        rp = lower.indptr.astype(np.int32)
+        ci = lower.indices.astype(np.int32)
+        np.testing.assert_array_equal(
+            csr(rp, ci, lower.data, work.rhs, work.n),
+            sptrsv.sptrsv_csr_loop(rp, ci, lower.data, work.rhs, work.n))
+        assert csr.hip_lowering.level_walker
+    # values that are not finite, zeros and their signs
+    work = cases[1]
+    rhs = work.rhs.copy()
+    rhs[5], rhs[40], rhs[100:140] = np.inf, -0.0, 0.0
+    with np.errstate(all="ignore"):
+        expected = oracle.sptrsv_csc(work.indptr, work.indices, work.data,
+                                     rhs, work.n)
+    result = csc(work.indptr, work.indices, work.data, rhs, work.n)
+    np.testing.assert_array_equal(result, expected)
+    valid = ~np.isnan(expected)
+    np.testing.assert_array_equal(np.signbit(result[valid]),
+                                  np.signbit(expected[valid]))
+    # chosen by itself for such a DAG; not for one with wide levels, too many
+    # tasks, or too many incoming entries per task (then the tiles)
+    auto = sptrsv.compile_sptrsv_csc(execution_mode="sync_free",
+                                     dependence_protocol="mailbox",
+                                     task_lanes=4)
+    for work, walks in ((cases[0], True),
+                        (workloads.configuration("c1", nx=80, ny=80), False),
+                        (workloads.configuration("c2", nx=20, ny=20, nz=4),
+                         False),
+                        (workloads.configuration("c5", n=3000), False)):
+        plan = auto.schedule_plan(work.indptr, work.indices, work.data,
+                                  work.rhs, work.n)
+        assert bool(plan.level_walker) == walks, work.name
+        expected = oracle.sptrsv_csc(work.indptr, work.indices, work.data,
+                                     work.rhs, work.n)
+        solve_and_check(auto, work, expected, exact=True)
+    with pytest.raises(ValueError, match="level_walker=True needs"):
+        big = workloads.configuration("c1", nx=80, ny=80)
+        csc(big.indptr, big.indices, big.data, big.rhs, big.n)
+    never = sptrsv.compile_sptrsv_csc(execution_mode="sync_free",
+                                      dependence_protocol="mailbox",
+                                      task_lanes=4, level_walker=False)
+    first = cases[0]
+    assert not never.schedule_plan(first.indptr, first.indices, first.data,
+                                   first.rhs, first.n).level_walker
+
+
 def test_edge_cases(oracle):
     solver = sptrsv.compile_sptrsv_csc(execution_mode="sync_free",
                                        threads_per_block=128, task_lanes=4)
@@ -1233,9 +1304,11 @@ def test_full_size_under_bench_settings(oracle, name):
         expected = oracle.sptrsv_csc(work.indptr, work.indices, work.data,
                                      work.rhs, work.n)
         solve_and_check(solver, work, expected, exact=True)
-        if name == "c5":
-            # the chain: the plan is the band walker, with its own workgroup
-            assert solver.hip_lowering.band_walker
+        if name in ("c1", "c5"):
+            # the chain runs on the band walker, the small grid on the level
+            # walker, each with its own workgroup
+            assert (solver.hip_lowering.band_walker if name == "c5"
+                    else solver.hip_lowering.level_walker)
             assert solver.hip_lowering.tile_rows is None
             assert solver.current_schedule.threads_per_block == 1024
             return

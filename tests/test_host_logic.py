@@ -924,6 +924,71 @@ def test_band_walker_lowering_and_choice():
     assert not band_walker_applies(Dag(0, 0, []))
 
 
+def test_level_walker_lowering_and_records():
+    """The executor for small DAGs with narrow levels: one wavefront takes a
+    level per step, the values live in LDS, the structure comes level-major
+    from the inspector."""
+    from lcd_amd.scheduler import level_walker_records
+    module = demo_source("sptrsv", "sptrsv_csc_loop")
+    result = lower(module, execution_mode="sync_free",
+                   thread_loop_iterator="j", task_lanes=4,
+                   wavefront_threads_per_block=1024,
+                   dependence_protocol="mailbox", level_walker=3)
+    assert result.level_walker == 3 and not result.band_walker
+    assert result.kernel_arguments[6:10] == [
+        "_lcd_lw_task", "_lcd_lw_src", "_lcd_lw_pos", "_lcd_lw_levels"]
+    kernel = result.kernel_source
+    for absent in ("lcd_ld(", "_spins", "lcd_atomic", "s_sleep"):
+        assert absent not in kernel
+    assert "constexpr int LW_K = 3, LW_B = 8;" in kernel
+    assert "_lcd_own_0 = ((_nl_0 - _lcd_own_0) / _nl_2);" in kernel
+    assert "_w_x[task] = _lcd_wout; x[task] = _lcd_wout;" in kernel
+    # an entry that is not there adds -0.0: x + -0.0 is x for every x
+    assert "int src = LCD_LW_TASKS; double coef = -0.0;" in kernel
+    launcher = result.launcher_source
+    assert "_hip.length(_lcd_lw_task) // 64" in launcher
+    assert "_blocks = 1" in launcher and "_hip_reset" not in launcher
+    hip_runtime.compile_code(result.source)
+    csr = lower(demo_source("sptrsv", "sptrsv_csr_loop"),
+                function_props=CSR_PROPS, execution_mode="sync_free",
+                thread_loop_iterator="j", task_lanes=4,
+                wavefront_threads_per_block=256, dependence_protocol="pull",
+                level_walker=2)
+    assert csr.level_walker == 2 and csr.dependence_protocol == "mailbox"
+    text = csr.kernel_source
+    assert "_lcd_own_0 = _lcd_own_0 - (_g_operand_0 * _g_value);" in text
+    assert "int src = LCD_LW_TASKS; double coef = 0.0;" in text    # x - 0.0
+    hip_runtime.compile_code(csr.source)
+
+    class Dag:
+        """Four tasks: 0 -> 1, 0 -> 2, (1, 2) -> 3 (two entries from 2)."""
+        n, edges = 4, 4
+        arrays = {"wavefront_ptr": [0, 1, 3, 4], "wavefronts": [0, 1, 2, 3],
+                  "in_ptr": [0, 0, 1, 2, 5], "in_src": [0, 0, 1, 2, 2],
+                  "in_pos": [7, 8, 9, 10, 11]}
+
+        def host(self, name):
+            return np.asarray(self.arrays[name], dtype=np.int32)
+
+    entries, task, source, position = level_walker_records(Dag(), 4096, 4)
+    assert entries == 3 and len(task) == 3 * 64
+    assert task[:2].tolist() == [0, -1] and task[64:67].tolist() == [1, 2, -1]
+    assert task[128] == 3
+    at = lambda level, k, lane: (level * 3 + k) * 64 + lane   # noqa: E731
+    assert [source[at(2, k, 0)] for k in range(3)] == [1, 2, 2]
+    assert [position[at(2, k, 0)] for k in range(3)] == [9, 10, 11]
+    assert source[at(1, 0, 1)] == 0 and position[at(1, 0, 1)] == 8
+    assert source[at(1, 1, 0)] == 4096 and position[at(1, 1, 0)] == -1
+    assert level_walker_records(Dag(), 3, 4) is None          # too many tasks
+    assert level_walker_records(Dag(), 4096, 2) is None       # too many entries
+    wide = Dag()
+    wide.arrays = dict(Dag.arrays, wavefront_ptr=[0, 70],
+                       wavefronts=list(range(70)),
+                       in_ptr=[0] * 70 + [1], in_src=[0], in_pos=[0])
+    wide.n = 70
+    assert level_walker_records(wide, 4096, 4) is None        # a level of 70
+
+
 def test_tiles_addressed_by_queue_position():
     """Tiles that do not follow the ids (boxes of a grid): sources, LDS slots
     and the value-as-flag copy are addressed by the place in the queue."""
