@@ -616,14 +616,14 @@ class BandWalkerMixin:
             f"                    {register} = {register} {sign} {product};",
             "                }",
             *[p4 + line for line in tail_lines],
-            "                if (task >= 0) {",
-            f"                    _w_x[task] = _lcd_wout; {array}[task] = _lcd_wout;",
-            "                }",
+            "                if (task >= 0) _w_x[task] = _lcd_wout;",
             "            }",
             "        } else {",
             "            _w_stage(_w_m + 2, threadIdx.x - 64, _w_helpers);",
             "        }",
             "        __syncthreads();",
             "    }",
+            # the values leave LDS together, every thread of the workgroup a few
+            f"    for (int c = threadIdx.x; c < _w_n; c += LCD_TPB) {array}[c] = _w_x[c];",
         ]
         return lines

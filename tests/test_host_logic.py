@@ -942,7 +942,8 @@ def test_level_walker_lowering_and_records():
         assert absent not in kernel
     assert "constexpr int LW_K = 3, LW_B = 8;" in kernel
     assert "_lcd_own_0 = ((_nl_0 - _lcd_own_0) / _nl_2);" in kernel
-    assert "_w_x[task] = _lcd_wout; x[task] = _lcd_wout;" in kernel
+    assert "if (task >= 0) _w_x[task] = _lcd_wout;" in kernel
+    assert "for (int c = threadIdx.x; c < _w_n; c += LCD_TPB) x[c] = _w_x[c];" in kernel
     # an entry that is not there adds -0.0: x + -0.0 is x for every x
     assert "int src = LCD_LW_TASKS; double coef = -0.0;" in kernel
     launcher = result.launcher_source
