@@ -479,7 +479,8 @@ def parallel(**kwargs):
                 if not incoming_positions:
                     dag = build_incoming()
                 records = level_walker_records(dag, LEVEL_WALKER_TASKS,
-                                               LEVEL_WALKER_ENTRIES)
+                                               LEVEL_WALKER_ENTRIES,
+                                               forced=forced)
                 usable = records is not None
             if usable:
                 candidate = replace(schedule, thread_unroll=1)
@@ -500,8 +501,8 @@ def parallel(**kwargs):
                     raise ValueError(
                         "level_walker=True needs the persistent executor with "
                         "the mailbox or pull protocol and a DAG of at most "
-                        f"{LEVEL_WALKER_TASKS} tasks, 64 per level, "
-                        f"{LEVEL_WALKER_ENTRIES} incoming entries per task.")
+                        f"{LEVEL_WALKER_TASKS} tasks with at most "
+                        f"{LEVEL_WALKER_ENTRIES} incoming entries each.")
                 return None
             device = get_device()
             tables = {name: device.to_device(values) for name, values in zip(

@@ -265,27 +265,35 @@ def band_walker_applies(dag, forced=False):
 
 
 # Level walker, automatic choice: a DAG small enough for its values to live in
-# one workgroup's LDS (4096 tasks), with at most 64 tasks per level and four
-# incoming entries per task.  One wavefront then takes a level per step in
-# about 0.1 us (232 cycles measured on the bare step) where the persistent
-# executors pay a polled hand-off of 0.5 us per level: the 64 x 64 grid of
-# configuration 1, 127 levels.
+# one workgroup's LDS (4096 tasks) whose tasks have at most four incoming
+# entries.  One wavefront then takes a step of up to 64 tasks of one level in
+# about 0.15 us (369 cycles measured on the 64 x 64 grid of configuration 1,
+# 127 levels) where the persistent executors pay a polled hand-off of 0.5 us
+# per level; a level of more than 64 tasks takes several steps, and the
+# walker is chosen while it has at most three steps per level on average.
 LEVEL_WALKER_WIDTH = 64
+LEVEL_WALKER_STEPS_PER_LEVEL = 3
 
 
 def level_walker_records(dag, max_tasks, max_entries, forced=False):
-    """The structure level-major for the level walker -- ``(entries, task,
-    source, position)`` with ``task[level * 64 + lane]``, ``source`` and
-    ``position[(level * entries + k) * 64 + lane]`` (-1: no task, no entry;
-    the dummy source is ``max_tasks``) -- or None when the DAG does not fit:
-    more than ``max_tasks`` tasks, a level of more than 64, a task with more
-    than ``max_entries`` incoming entries.  Built on the host: the DAG is
-    small by definition."""
+    """The structure step-major for the level walker -- ``(entries, task,
+    source, position)`` with ``task[step * 64 + lane]``, ``source`` and
+    ``position[(step * entries + k) * 64 + lane]`` (-1: no task, no entry;
+    the dummy source is ``max_tasks``); a step is up to 64 tasks of one level
+    (tasks of a level do not depend on each other) -- or None when the DAG
+    does not fit: more than ``max_tasks`` tasks, a task with more than
+    ``max_entries`` incoming entries, or (unless ``forced``) more than
+    LEVEL_WALKER_STEPS_PER_LEVEL steps per level on average.  Built on the
+    host: the DAG is small by definition."""
     if dag.n == 0 or dag.n > max_tasks or dag.edges == 0:
         return None
     pointer = np.asarray(dag.host("wavefront_ptr"), dtype=np.int64)
     widths = np.diff(pointer)
-    if len(widths) == 0 or widths.max() > LEVEL_WALKER_WIDTH:
+    if len(widths) == 0:
+        return None
+    chunks = -(-widths // LEVEL_WALKER_WIDTH)
+    steps = int(chunks.sum())
+    if not forced and steps > LEVEL_WALKER_STEPS_PER_LEVEL * len(widths):
         return None
     in_ptr = np.asarray(dag.host("in_ptr"), dtype=np.int64)
     counts = np.diff(in_ptr)
@@ -295,16 +303,18 @@ def level_walker_records(dag, max_tasks, max_entries, forced=False):
     nodes = np.asarray(dag.host("wavefronts"), dtype=np.int64)
     in_src = np.asarray(dag.host("in_src"), dtype=np.int32)
     in_pos = np.asarray(dag.host("in_pos"), dtype=np.int32)
-    levels = len(widths)
-    level_of = np.repeat(np.arange(levels), widths)
-    lane_of = np.arange(len(nodes)) - pointer[level_of]
-    task = np.full(levels * 64, -1, dtype=np.int32)
-    task[level_of * 64 + lane_of] = nodes
-    source = np.full(levels * entries * 64, max_tasks, dtype=np.int32)
-    position = np.full(levels * entries * 64, -1, dtype=np.int32)
+    level_of = np.repeat(np.arange(len(widths)), widths)
+    within = np.arange(len(nodes)) - pointer[level_of]
+    first_step = np.concatenate([[0], np.cumsum(chunks)[:-1]])
+    step_of = first_step[level_of] + within // LEVEL_WALKER_WIDTH
+    lane_of = within % LEVEL_WALKER_WIDTH
+    task = np.full(steps * 64, -1, dtype=np.int32)
+    task[step_of * 64 + lane_of] = nodes
+    source = np.full(steps * entries * 64, max_tasks, dtype=np.int32)
+    position = np.full(steps * entries * 64, -1, dtype=np.int32)
     for k in range(entries):
         has = counts[nodes] > k
-        at = (level_of[has] * entries + k) * 64 + lane_of[has]
+        at = (step_of[has] * entries + k) * 64 + lane_of[has]
         which = in_ptr[nodes[has]] + k
         source[at] = in_src[which]
         position[at] = in_pos[which]

@@ -1058,6 +1058,7 @@ def test_level_walker(oracle):
     cases = [workloads.configuration("c1"),
              workloads.configuration("c1", nx=37, ny=11),
              workloads.configuration("c2", nx=6, ny=5, nz=7),
+             workloads.configuration("c2", nx=16, ny=16, nz=16),
              workloads.configuration("c5", n=300, bandwidth=3)]
     for work in cases:
         print("level walker", work.name, flush=True)
@@ -1097,8 +1098,9 @@ def test_level_walker(oracle):
                                      task_lanes=4)
     for work, walks in ((cases[0], True),
                         (workloads.configuration("c1", nx=80, ny=80), False),
-                        (workloads.configuration("c2", nx=20, ny=20, nz=4),
-                         False),
+                        # levels of up to 100 tasks: two steps each
+                        (workloads.configuration("c2", nx=15, ny=15, nz=15),
+                         True),
                         (workloads.configuration("c5", n=3000), False)):
         plan = auto.schedule_plan(work.indptr, work.indices, work.data,
                                   work.rhs, work.n)

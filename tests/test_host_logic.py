@@ -982,12 +982,27 @@ def test_level_walker_lowering_and_records():
     assert source[at(1, 1, 0)] == 4096 and position[at(1, 1, 0)] == -1
     assert level_walker_records(Dag(), 3, 4) is None          # too many tasks
     assert level_walker_records(Dag(), 4096, 2) is None       # too many entries
+    # a level of more than 64 tasks takes several steps (its tasks do not
+    # depend on each other); too many steps per level and the tiles are
+    # the better executor, unless the walker is asked for by name
     wide = Dag()
-    wide.arrays = dict(Dag.arrays, wavefront_ptr=[0, 70],
-                       wavefronts=list(range(70)),
-                       in_ptr=[0] * 70 + [1], in_src=[0], in_pos=[0])
-    wide.n = 70
-    assert level_walker_records(wide, 4096, 4) is None        # a level of 70
+    wide.arrays = dict(wavefront_ptr=[0, 1, 201], wavefronts=list(range(201)),
+                       in_ptr=[0] + list(range(201)), in_src=[0] * 200,
+                       in_pos=list(range(200)))
+    wide.n, wide.edges = 201, 200
+    entries, task, source, position = level_walker_records(wide, 4096, 4)
+    assert entries == 1 and len(task) == 5 * 64          # 1 + ceil(200 / 64)
+    assert task[0] == 0 and task[64:128].tolist() == list(range(1, 65))
+    assert task[4 * 64:4 * 64 + 9].tolist() == list(range(193, 201)) + [-1]
+    assert position[4 * 64 + 7] == 199 and position[4 * 64 + 8] == -1
+    wider = Dag()
+    wider.arrays = dict(wavefront_ptr=[0, 1, 1001],
+                        wavefronts=list(range(1001)),
+                        in_ptr=[0] + list(range(1001)), in_src=[0] * 1000,
+                        in_pos=list(range(1000)))
+    wider.n, wider.edges = 1001, 1000
+    assert level_walker_records(wider, 4096, 4) is None       # 17 steps, 2 levels
+    assert level_walker_records(wider, 4096, 4, forced=True)[0] == 1
 
 
 def test_tiles_addressed_by_queue_position():
