@@ -1,4 +1,8 @@
-"""Band walker: the executor for dependence DAGs that are (nearly) a chain.
+"""Walkers: executors in which ONE wavefront runs the tasks and nothing is
+polled -- the band walker for dependence DAGs that are (nearly) a chain, the
+level walker (``_level_walker_text``, at the end) for small DAGs.
+
+Band walker.
 
 When every level of the DAG holds about one task there is nothing to run in
 parallel and a hand-off between wavefronts (a store, a poll, a load) per task
@@ -31,8 +35,6 @@ import re
 from copy import deepcopy
 
 from lcd_amd.hip_emitter import FLOAT, INT
-
-WALKER_SPAN = 64            # an edge must span fewer iterations than this
 
 
 class BandWalkerMixin:
