@@ -504,9 +504,16 @@ class BandWalkerMixin:
         slots = [(name, self._kinds.locals.get(name, FLOAT))
                  for name in dict.fromkeys(staged)
                  if re.search(r"\b" + re.escape(name) + r"\b", tail_text)]
+        division = plan["division"]
+        if division:
+            # (the prepared reciprocal of the task's divisor, per lane; not a
+            # number where the divisor is outside the range it serves)
+            slots.append(("_lcd_wr", FLOAT))
         if head_lines:
             slots.append((register, FLOAT))
         width = max(1, len(slots))
+        general_tail = [line.replace("_lcd_wdiv(", "_lcd_wdiv_general(")
+                        for line in tail_lines]
 
         def put(name, kind, where):
             return (f"{where} = (double){name};" if kind == INT
@@ -517,72 +524,9 @@ class BandWalkerMixin:
                     else f"{name} = {what};")
 
         p3, p4 = " " * 12, " " * 16
-        first_value = (f"_w_uni[rb][l][{len(slots) - 1}][_w_lane]" if head_lines
-                       else "0.0")
-        lines = [
-            "    // ---- level walker: one wavefront takes a level per step",
-            "    if (blockIdx.x != 0) return;",
-            "    const int _w_lane = threadIdx.x & 63;",
-            "    const int _w_wave = threadIdx.x >> 6;",
-            "    const int _w_n = (int)task_count;",
-            f"    constexpr int LW_K = {entries}, LW_B = 8;",
-            "    const int _w_levels = (int)_lcd_lw_levels;",
-            "    const int _w_blocks = (_w_levels + LW_B - 1) / LW_B;",
-            "    const int _w_helpers = LCD_TPB - 64;",
-            "    __shared__ double _w_x[LCD_LW_TASKS + 1];",
-            "    __shared__ double _w_coef[3][LW_B][LW_K][64];",
-            "    __shared__ short _w_src[3][LW_B][LW_K][64];",
-            f"    __shared__ double _w_uni[3][LW_B][{width}][64];",
-            "    __shared__ int _w_task[3][LW_B][64];",
-            "    lcd_index_t _g_pos = 0, _g_src = 0; double _g_value = 0.0;",
-            f"    double {operand} = 0.0; double _lcd_wout = 0.0;",
-            "    (void)_g_pos; (void)_g_src;",
-            "    if (_w_n > LCD_LW_TASKS) { if (threadIdx.x == 0) _lcd_status[0] = 2; return; }",
-            "    auto _w_stage = [&](int m, int first, int step) {",
-            "        // block m of the levels: tasks, node loads, sources and operands",
-            "        if (m >= _w_blocks) return;",
-            "        const int rb = m % 3;",
-            "        for (int c = first; c < LW_B * 64; c += step) {",
-            "            const int l = c >> 6, lane = c & 63, level = m * LW_B + l;",
-            "            const int task = level < _w_levels ? "
-            "(int)_lcd_lw_task[level * 64 + lane] : -1;",
-            "            _w_task[rb][l][lane] = task;",
-            "            if (task >= 0) {",
-            f"                {it} = (lcd_index_t)task;",
-            *[p4 + line for line in stage_lines],
-            *[p4 + line for line in head_lines],
-            *[p4 + put(name, kind, f"_w_uni[rb][l][{k}][lane]")
-              for k, (name, kind) in enumerate(slots)],
-            "            }",
-            "        }",
-            "        for (int c = first; c < LW_B * LW_K * 64; c += step) {",
-            "            const int lane = c & 63, k = (c >> 6) % LW_K, l = c / (64 * LW_K);",
-            "            const int level = m * LW_B + l;",
-            # (x + -0.0 and x - +0.0 leave every x as it is, signed zeros included)
-            "            int src = LCD_LW_TASKS; double coef = "
-            + ("-0.0" if sign == "+" else "0.0") + ";",
-            "            if (level < _w_levels) {",
-            "                const long long at = ((long long)level * LW_K + k) * 64 + lane;",
-            "                _g_pos = (lcd_index_t)_lcd_lw_pos[at];",
-            "                if (_g_pos >= 0) {",
-            "                    _g_src = (lcd_index_t)_lcd_lw_src[at]; src = (int)_g_src;",
-            f"                    coef = {emitter.expr(operand_node)};",
-            "                }",
-            "            }",
-            "            _w_src[rb][l][k][lane] = (short)src;",
-            "            _w_coef[rb][l][k][lane] = coef;",
-            "        }",
-            "    };",
-            "    // (an entry that is not there reads the slot past the last task, which",
-            "    // holds zero, with a zero operand)",
-            "    for (int c = threadIdx.x; c < LCD_LW_TASKS + 1; c += LCD_TPB) _w_x[c] = 0.0;",
-            "    _w_stage(0, threadIdx.x, LCD_TPB); _w_stage(1, threadIdx.x, LCD_TPB);",
-            "    __syncthreads();",
-            "    for (int _w_m = 0; _w_m < _w_blocks; ++_w_m) {",
-            "        if (_w_wave == 0) {",
-            "            const int rb = _w_m % 3;",
-            # what a level reads from the ring is in registers a level ahead:
-            # the step then waits for one trip to LDS (the sources' values)
+
+        def steps(tail):
+            return [
             "            int _w_t = _w_task[rb][0][_w_lane];",
             "            short _w_s[LW_K]; double _w_c[LW_K];",
             f"            double _w_u[{width}];",
@@ -617,9 +561,106 @@ class BandWalkerMixin:
             f"                    _g_value = _w_v[k]; {operand} = _w_cc[k];",
             f"                    {register} = {register} {sign} {product};",
             "                }",
-            *[p4 + line for line in tail_lines],
+            *[p4 + line for line in tail],
             "                if (task >= 0) _w_x[task] = _lcd_wout;",
             "            }",
+            ]
+
+        first_value = (f"_w_uni[rb][l][{len(slots) - 1}][_w_lane]" if head_lines
+                       else "0.0")
+        lines = [
+            "    // ---- level walker: one wavefront takes a level per step",
+            "    if (blockIdx.x != 0) return;",
+            "    const int _w_lane = threadIdx.x & 63;",
+            "    const int _w_wave = threadIdx.x >> 6;",
+            "    const int _w_n = (int)task_count;",
+            f"    constexpr int LW_K = {entries}, LW_B = 8;",
+            "    const int _w_levels = (int)_lcd_lw_levels;",
+            "    const int _w_blocks = (_w_levels + LW_B - 1) / LW_B;",
+            "    const int _w_helpers = LCD_TPB - 64;",
+            "    __shared__ double _w_x[LCD_LW_TASKS + 1];",
+            "    __shared__ double _w_coef[3][LW_B][LW_K][64];",
+            "    __shared__ short _w_src[3][LW_B][LW_K][64];",
+            f"    __shared__ double _w_uni[3][LW_B][{width}][64];",
+            "    __shared__ int _w_task[3][LW_B][64];",
+            "    lcd_index_t _g_pos = 0, _g_src = 0; double _g_value = 0.0;",
+            f"    double {operand} = 0.0; double _lcd_wout = 0.0;",
+            "    unsigned _lcd_wbad = 0; (void)_lcd_wbad;",
+            "    (void)_g_pos; (void)_g_src;",
+            # the division over the prepared reciprocal; how far its quotient is
+            # from the range in which that is the division is kept per lane and
+            # looked at once per block
+            "    auto _lcd_wdiv = [&](double a, double d, double r) {",
+            "        const double q = lcd_div_prepared(a, d, r);",
+            "        const unsigned off = ((((unsigned)(__double_as_longlong(q) >> 32)) >> 20) "
+            "& 0x7ffu) - 164u;",
+            "        _lcd_wbad = off > _lcd_wbad ? off : _lcd_wbad;",
+            "        return q;",
+            "    };",
+            "    auto _lcd_wdiv_general = [&](double a, double d, double r) {",
+            "        (void)r; return a / d;",
+            "    };",
+            "    (void)_lcd_wdiv; (void)_lcd_wdiv_general;",
+            "    if (_w_n > LCD_LW_TASKS) { if (threadIdx.x == 0) _lcd_status[0] = 2; return; }",
+            "    auto _w_stage = [&](int m, int first, int step) {",
+            "        // block m of the levels: tasks, node loads, sources and operands",
+            "        if (m >= _w_blocks) return;",
+            "        const int rb = m % 3;",
+            "        for (int c = first; c < LW_B * 64; c += step) {",
+            "            const int l = c >> 6, lane = c & 63, level = m * LW_B + l;",
+            "            const int task = level < _w_levels ? "
+            "(int)_lcd_lw_task[level * 64 + lane] : -1;",
+            "            _w_task[rb][l][lane] = task;",
+            # (a lane without a task computes on ones: nothing out of range)
+            f"            for (int k = 0; k < {width}; ++k) _w_uni[rb][l][k][lane] = 1.0;",
+            "            if (task >= 0) {",
+            f"                {it} = (lcd_index_t)task;",
+            *[p4 + line for line in stage_lines],
+            *[p4 + line for line in head_lines],
+            *([f"{p4}_lcd_wr = lcd_div_plain_divisor({division}) ? "
+               f"lcd_div_prepare({division}) : lcd_empty();"]
+              if division else []),
+            *[p4 + put(name, kind, f"_w_uni[rb][l][{k}][lane]")
+              for k, (name, kind) in enumerate(slots)],
+            "            }",
+            "        }",
+            "        for (int c = first; c < LW_B * LW_K * 64; c += step) {",
+            "            const int lane = c & 63, k = (c >> 6) % LW_K, l = c / (64 * LW_K);",
+            "            const int level = m * LW_B + l;",
+            # (x + -0.0 and x - +0.0 leave every x as it is, signed zeros included)
+            "            int src = LCD_LW_TASKS; double coef = "
+            + ("-0.0" if sign == "+" else "0.0") + ";",
+            "            if (level < _w_levels) {",
+            "                const long long at = ((long long)level * LW_K + k) * 64 + lane;",
+            "                _g_pos = (lcd_index_t)_lcd_lw_pos[at];",
+            "                if (_g_pos >= 0) {",
+            "                    _g_src = (lcd_index_t)_lcd_lw_src[at]; src = (int)_g_src;",
+            f"                    coef = {emitter.expr(operand_node)};",
+            "                }",
+            "            }",
+            "            _w_src[rb][l][k][lane] = (short)src;",
+            "            _w_coef[rb][l][k][lane] = coef;",
+            "        }",
+            "    };",
+            "    // (an entry that is not there reads the slot past the last task, which",
+            "    // holds zero, with a zero operand)",
+            "    for (int c = threadIdx.x; c < LCD_LW_TASKS + 1; c += LCD_TPB) _w_x[c] = 0.0;",
+            "    _w_stage(0, threadIdx.x, LCD_TPB); _w_stage(1, threadIdx.x, LCD_TPB);",
+            "    __syncthreads();",
+            "    for (int _w_m = 0; _w_m < _w_blocks; ++_w_m) {",
+            "        if (_w_wave == 0) {",
+            "            const int rb = _w_m % 3;",
+            "            _lcd_wbad = 0;",
+            # what a level reads from the ring is in registers a level ahead:
+            # the step then waits for one trip to LDS (the sources' values)
+            *steps(tail_lines),
+            *([
+                "            if (__ballot(_lcd_wbad > 1518u) != 0ull) {",
+                "                // a quotient (or a divisor) the prepared reciprocal does not",
+                "                // serve: the block again with the general division",
+                *["    " + line for line in steps(general_tail)],
+                "            }",
+            ] if division else []),
             "        } else {",
             "            _w_stage(_w_m + 2, threadIdx.x - 64, _w_helpers);",
             "        }",

@@ -787,7 +787,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
         if self.prefetch_node_loads:
             body, self._prefetch_lines = self._hoist_node_loads(
                 body, mapped, arguments)
-        if self._walker is not None and self._walker["kind"] == "band":
+        if self._walker is not None:
             body = self._band_walker_division(body)
         if self._value_pull is not None:
             own = self._own_map.get(

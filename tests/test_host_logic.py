@@ -941,7 +941,14 @@ def test_level_walker_lowering_and_records():
     for absent in ("lcd_ld(", "_spins", "lcd_atomic", "s_sleep"):
         assert absent not in kernel
     assert "constexpr int LW_K = 3, LW_B = 8;" in kernel
-    assert "_lcd_own_0 = ((_nl_0 - _lcd_own_0) / _nl_2);" in kernel
+    # the division runs over a reciprocal the helpers prepared; a block whose
+    # quotients leave the range in which that is the division runs again
+    assert "_lcd_own_0 = _lcd_wdiv((_nl_0 - _lcd_own_0), _nl_2, _lcd_wr);" in kernel
+    assert ("_lcd_wr = lcd_div_plain_divisor(_nl_2) ? lcd_div_prepare(_nl_2) "
+            ": lcd_empty();") in kernel
+    assert "if (__ballot(_lcd_wbad > 1518u) != 0ull) {" in kernel
+    assert ("_lcd_own_0 = _lcd_wdiv_general((_nl_0 - _lcd_own_0), _nl_2, "
+            "_lcd_wr);") in kernel
     assert "if (task >= 0) _w_x[task] = _lcd_wout;" in kernel
     assert "for (int c = threadIdx.x; c < _w_n; c += LCD_TPB) x[c] = _w_x[c];" in kernel
     # an entry that is not there adds -0.0: x + -0.0 is x for every x
