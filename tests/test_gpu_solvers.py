@@ -1091,6 +1091,19 @@ def test_level_walker(oracle):
     valid = ~np.isnan(expected)
     np.testing.assert_array_equal(np.signbit(result[valid]),
                                   np.signbit(expected[valid]))
+    # divisors and quotients the prepared reciprocal does not serve: their
+    # blocks run again with the general division
+    values = work.data.copy()
+    values[work.indptr[50]] = 1e-200
+    values[work.indptr[51]] = 1e250
+    values[work.indptr[200]] = 5e-324
+    rhs = work.rhs.copy()
+    rhs[300] = 1e-305
+    with np.errstate(all="ignore"):
+        expected = oracle.sptrsv_csc(work.indptr, work.indices, values, rhs,
+                                     work.n)
+    np.testing.assert_array_equal(
+        csc(work.indptr, work.indices, values, rhs, work.n), expected)
     # chosen by itself for such a DAG; not for one with wide levels, too many
     # tasks, or too many incoming entries per task (then the tiles)
     auto = sptrsv.compile_sptrsv_csc(execution_mode="sync_free",
