@@ -808,9 +808,20 @@ class _MappedLoopHooks:
         low._kinds.locals["_lcd_vf"] = FLOAT
         body_lines = emitter.block(body, indent + 1, None)
         lines.append(f"{pad}{name} = ({lower}) + _lane;")
+        reload = list(low._first_iteration_reload)
+        first = f"if ({name} != ({lower}) + _lane) {{"
+        if len(reload) == 1 and reload[0].startswith(first):
+            # the entries of a position stay in their registers across polls:
+            # they are fetched again only for a new position
+            low._kinds.locals["_lcd_vat"] = INT
+            if "_lcd_vat" not in low._extra_locals:
+                low._extra_locals.append("_lcd_vat")
+            lines.append(f"{pad}_lcd_vat = {name};")
+            reload = [f"if ({name} != _lcd_vat) {{ _lcd_vat = {name};"
+                      + reload[0][len(first):]]
         lines.append(VALUE_WAIT_BEGIN)
         lines.append(f"{pad}for (; {name} < {upper}; {name} += LCD_TASK_LANES) {{")
-        lines += [f"{pad}    {line}" for line in low._first_iteration_reload]
+        lines += [f"{pad}    {line}" for line in reload]
         load = (emitter.tile_load(emitter.expr(endpoint))
                 if emitter.tile is not None and emitter.tile["array"] == array
                 else f"{low.pull_load}(&{array}[{emitter.expr(endpoint)}])")

@@ -112,6 +112,8 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
         # > 0: the level walker, with room for this many incoming entries per task
         self.level_walker = int(level_walker or 0)
         self._walker = None
+        # locals the emitter adds while it writes the task (declared with the rest)
+        self._extra_locals = []
         self.tile_by_position = tile_by_position
         self.segment_registers = segment_registers
         self.pair_tables = pair_tables
@@ -979,7 +981,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
         lines = []
         declared = set()
         for name in (list(local_names) + [p for p, _, _ in self._partials]
-                     + list(self._own_registers)):
+                     + list(self._own_registers) + list(self._extra_locals)):
             if name in declared or name == self.loop_iterator:
                 continue
             declared.add(name)
