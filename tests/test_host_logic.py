@@ -671,6 +671,10 @@ def test_csr_pull_polls_the_values_themselves():
                      dependence_protocol="pull", plain_first_polls=False)
     assert "double _lcd_vf = lcd_ld(&x[" in coherent.kernel_source
     assert "for (; j < " in kernel          # resumes, does not restart
+    # ... with the entries of the position it waits at still in registers:
+    # they are fetched again for a new position only
+    assert "_lcd_vat = j;" in kernel
+    assert "if (j != _lcd_vat) { _lcd_vat = j; _pf_" in kernel
     assert "lcd_release_fence" not in kernel.split("while (true)")[1]
     assert "_lcd_values[2 * t] = LCD_EMPTY_WORD" in result.source
     assert "(x, task_counter, _hip.length(x))" in result.launcher_source
