@@ -34,7 +34,10 @@ import ast
 import re
 from copy import deepcopy
 
-from lcd_amd.hip_emitter import FLOAT, INT
+from lcd_amd.hip_emitter import FLOAT, INT, LEVEL_WALKER_TASKS
+
+# LDS a workgroup of gfx950 can have
+LDS_BYTES = 160 * 1024
 
 
 class BandWalkerMixin:
@@ -267,6 +270,10 @@ class BandWalkerMixin:
             slots.append((register, FLOAT))
         uniform = len(slots) - (1 if head_lines else 0)
         width = max(2, len(slots) + (len(slots) & 1))
+        # (the table, the node loads, pointers, masks and flags of the ring)
+        if (3 * 64 * 64 * 8 + 4 * 64 * width * 8 + 3 * 132 * 4 + 3 * 64 * 8
+                + 4 * 64 * 4 > LDS_BYTES):
+            return None
         own_is_quotient = bool(division) and plan["quotient_is_value"]
         general_tail = [line.replace("_lcd_wdiv(", "_lcd_wdiv_general(")
                         for line in tail_lines]
@@ -512,6 +519,11 @@ class BandWalkerMixin:
         if head_lines:
             slots.append((register, FLOAT))
         width = max(1, len(slots))
+        # (the values, then three blocks of eight levels: operands, sources,
+        # node loads and tasks)
+        if ((LEVEL_WALKER_TASKS + 1) * 8 + 3 * 8 * 64 * (
+                entries * (8 + 2) + width * 8 + 4) > LDS_BYTES):
+            return None
         general_tail = [line.replace("_lcd_wdiv(", "_lcd_wdiv_general(")
                         for line in tail_lines]
 

@@ -2,6 +2,7 @@
 plans, dependence analysis, lowering structure, and the C-ABI surface."""
 
 import ast
+import textwrap
 import ctypes
 import json
 import os
@@ -971,6 +972,25 @@ def test_level_walker_lowering_and_records():
     assert "_lcd_own_0 = _lcd_own_0 - (_g_operand_0 * _g_value);" in text
     assert "int src = LCD_LW_TASKS; double coef = 0.0;" in text    # x - 0.0
     hip_runtime.compile_code(csr.source)
+
+    # a task with more node loads than the ring has LDS for is refused (the
+    # decorator then takes the polling executors)
+    wide = ast.parse(textwrap.dedent("""
+        def solve(Ap, Ai, Ax, b, c, d, e, f, n):
+            x = np.zeros(n)
+            for i in range(n):
+                x[i] = (b[i] + c[i] * d[i] + e[i] * f[i] - x[i]) / Ax[Ap[i]]
+                for j in range(Ap[i] + 1, Ap[i + 1]):
+                    x[Ai[j]] += Ax[j] * x[i]
+            return x
+    """))
+    with pytest.raises(HIPLoweringError, match="cannot stage"):
+        lower(wide, execution_mode="sync_free", thread_loop_iterator="j",
+              task_lanes=4, wavefront_threads_per_block=1024,
+              dependence_protocol="mailbox", level_walker=4)
+    assert lower(wide, execution_mode="sync_free", thread_loop_iterator="j",
+                 task_lanes=4, wavefront_threads_per_block=1024,
+                 dependence_protocol="mailbox", level_walker=1).level_walker == 1
 
     class Dag:
         """Four tasks: 0 -> 1, 0 -> 2, (1, 2) -> 3 (two entries from 2)."""
