@@ -521,7 +521,7 @@ class BandWalkerMixin:
         width = max(1, len(slots))
         # (the values, then three blocks of eight levels: operands, sources,
         # node loads and tasks)
-        if ((LEVEL_WALKER_TASKS + 1) * 8 + 3 * 8 * 64 * (
+        if ((LEVEL_WALKER_TASKS + 2) * 8 + 3 * 8 * 64 * (
                 entries * (8 + 2) + width * 8 + 4) > LDS_BYTES):
             return None
         general_tail = [line.replace("_lcd_wdiv(", "_lcd_wdiv_general(")
@@ -574,7 +574,9 @@ class BandWalkerMixin:
             f"                    {register} = {register} {sign} {product};",
             "                }",
             *[p4 + line for line in tail],
-            "                if (task >= 0) _w_x[task] = _lcd_wout;",
+            # (a lane without a task writes the slot nobody reads: no branch
+            # between the division and the store)
+            "                _w_x[task < 0 ? LCD_LW_TASKS + 1 : task] = _lcd_wout;",
             "            }",
             ]
 
@@ -590,7 +592,7 @@ class BandWalkerMixin:
             "    const int _w_levels = (int)_lcd_lw_levels;",
             "    const int _w_blocks = (_w_levels + LW_B - 1) / LW_B;",
             "    const int _w_helpers = LCD_TPB - 64;",
-            "    __shared__ double _w_x[LCD_LW_TASKS + 1];",
+            "    __shared__ double _w_x[LCD_LW_TASKS + 2];",
             "    __shared__ double _w_coef[3][LW_B][LW_K][64];",
             "    __shared__ short _w_src[3][LW_B][LW_K][64];",
             f"    __shared__ double _w_uni[3][LW_B][{width}][64];",

@@ -954,7 +954,7 @@ def test_level_walker_lowering_and_records():
     assert "if (__ballot(_lcd_wbad > 1518u) != 0ull) {" in kernel
     assert ("_lcd_own_0 = _lcd_wdiv_general((_nl_0 - _lcd_own_0), _nl_2, "
             "_lcd_wr);") in kernel
-    assert "if (task >= 0) _w_x[task] = _lcd_wout;" in kernel
+    assert "_w_x[task < 0 ? LCD_LW_TASKS + 1 : task] = _lcd_wout;" in kernel
     assert "for (int c = threadIdx.x; c < _w_n; c += LCD_TPB) x[c] = _w_x[c];" in kernel
     # an entry that is not there adds -0.0: x + -0.0 is x for every x
     assert "int src = LCD_LW_TASKS; double coef = -0.0;" in kernel
