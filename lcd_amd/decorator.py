@@ -283,6 +283,7 @@ def parallel(**kwargs):
                     pair_tables=registers == 2,
                     band_walker=walker,
                     level_walker=level,
+                    prepared_division=kwargs.get("prepared_division", True),
                     full_fences=kwargs.get("full_fences", False),
                     dynamic_fetch=kwargs.get("dynamic_fetch", False),
                 )

@@ -123,6 +123,51 @@ class BandWalkerMixin:
         lowerer._kinds.locals["_lcd_wr"] = FLOAT
         return rewritten
 
+    def _prepared_division(self, body):
+        """The polling executors' share of the same idea: the first ``a / d``
+        whose divisor is one of the task's node loads becomes ``lcd_pdiv(a,
+        d, _lcd_rcp)``, the plain division unless a pipelined fetch prepares
+        the reciprocal a round ahead (LCD_PREPARED_DIVISION)."""
+        lowerer = self
+        node_loads = {name for name, kind in self._kinds.locals.items()
+                      if name.startswith("_nl_") and kind == FLOAT}
+
+        class Rewrite(ast.NodeTransformer):
+            def visit_BinOp(self, node):
+                node = self.generic_visit(node)
+                if (lowerer._prepared_divisor is None
+                        and isinstance(node.op, ast.Div)
+                        and isinstance(node.right, ast.Name)
+                        and node.right.id in node_loads):
+                    lowerer._prepared_divisor = node.right.id
+                    return ast.copy_location(ast.Call(
+                        func=ast.Name(id="_lcd_pdiv", ctx=ast.Load()),
+                        args=[node.left, node.right], keywords=[]), node)
+                return node
+
+            def visit_AugAssign(self, node):
+                node = self.generic_visit(node)
+                if (lowerer._prepared_divisor is None
+                        and isinstance(node.op, ast.Div)
+                        and isinstance(node.target, ast.Name)
+                        and isinstance(node.value, ast.Name)
+                        and node.value.id in node_loads):
+                    lowerer._prepared_divisor = node.value.id
+                    return ast.copy_location(ast.Assign(
+                        targets=[ast.Name(id=node.target.id, ctx=ast.Store())],
+                        value=ast.Call(
+                            func=ast.Name(id="_lcd_pdiv", ctx=ast.Load()),
+                            args=[ast.Name(id=node.target.id, ctx=ast.Load()),
+                                  node.value], keywords=[])), node)
+                return node
+
+        rewritten = [Rewrite().visit(statement) for statement in body]
+        ast.fix_missing_locations(ast.Module(body=rewritten, type_ignores=[]))
+        if self._prepared_divisor is not None:
+            self._kinds.locals["_lcd_rcp"] = FLOAT
+            self._extra_locals.append("_lcd_rcp")
+        return rewritten
+
     def _band_walker_store(self, lines):
         """The task's final store: the value stays in the lane (it leaves for
         memory with the block's 64 values), captured under the step's mask."""

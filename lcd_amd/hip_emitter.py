@@ -507,6 +507,8 @@ class _Emitter:
                         "_lcd_seg_base, _lcd_seg_limit, _lcd_seg_own, "
                         f"{self.expr(target.slice)}, _lcd_ptile, _lcd_tpos0, "
                         "_lcd_tlen)")
+            if name == "_lcd_pdiv":
+                return f"lcd_pdiv({args[0]}, {args[1]}, _lcd_rcp)"
             if name == "_lcd_settle" and self.published is not None:
                 target = node.args[0]
                 return ("lcd_seg_settle(_lcd_pub, _lcd_seg_base, _lcd_seg_own, "

@@ -106,7 +106,8 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                  pipeline_fetch=True, full_fences=False,
                  dynamic_fetch=False, tile_positions=None,
                  tile_by_position=False, segment_registers=False,
-                 pair_tables=True, band_walker=False, level_walker=0):
+                 pair_tables=True, band_walker=False, level_walker=0,
+                 prepared_division=True):
         self.tile_positions = tile_positions
         self.band_walker = bool(band_walker)
         # > 0: the level walker, with room for this many incoming entries per task
@@ -114,6 +115,11 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
         self._walker = None
         # locals the emitter adds while it writes the task (declared with the rest)
         self._extra_locals = []
+        # the node load a task divides by (its reciprocal is prepared where
+        # the pipelined fetch takes the load over), and whether a fetch did so
+        self.prepared_division = prepared_division
+        self._prepared_divisor = None
+        self._prepared_division_active = False
         self.tile_by_position = tile_by_position
         self.segment_registers = segment_registers
         self.pair_tables = pair_tables
@@ -791,6 +797,9 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                 body, mapped, arguments)
         if self._walker is not None:
             body = self._band_walker_division(body)
+        elif (self.prepared_division and self.execution_mode == "sync_free"
+              and self.pipeline_fetch and self.prefetch_node_loads):
+            body = self._prepared_division(body)
         if self._value_pull is not None:
             own = self._own_map.get(
                 f"{self._value_pull['array']}[{self.loop_iterator}]")
@@ -902,6 +911,8 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                      kernel_text):
         defines = [
             *(["#define LCD_FULL_FENCES 1"] if self.full_fences else []),
+            *(["#define LCD_PREPARED_DIVISION 1"]
+              if self._prepared_division_active else []),
             *(["#define LCD_DYNAMIC_FETCH 1"] if self.dynamic_fetch else []),
             "#ifndef LCD_INDEX_TYPE", "#define LCD_INDEX_TYPE int", "#endif",
             f"#define LCD_TPB {self.threads_per_block}",
@@ -1615,7 +1626,7 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
                  pipeline_fetch=True, full_fences=False, dynamic_fetch=False,
                  tile_positions=None, tile_by_position=False,
                  segment_registers=False, pair_tables=True, band_walker=False,
-                 level_walker=0):
+                 level_walker=0, prepared_division=True):
     """HIP counterpart of ``lower_to_numba_cuda``
     (compiler/cuda_lowering.py:2854-2884); same parameters plus
     ``task_lanes`` (lanes cooperating on one task, a power of two <= 64),
@@ -1645,5 +1656,6 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
         dynamic_fetch=dynamic_fetch, tile_positions=tile_positions,
         tile_by_position=tile_by_position,
         segment_registers=segment_registers, pair_tables=pair_tables,
-        band_walker=band_walker, level_walker=level_walker)
+        band_walker=band_walker, level_walker=level_walker,
+        prepared_division=prepared_division)
     return lowerer.lower(code)

@@ -451,6 +451,20 @@ class ProtocolMixin:
             "shift": " ".join(f"_b_{name} = _a_{name};" for name in first),
         }
 
+    def _prepared_reciprocal(self, taken):
+        """The reciprocal of the task's divisor, prepared where a round takes
+        over the node loads that were requested a round ago: the wavefront is
+        about to wait for its producers, and the division that follows the
+        wait -- on the chain between two levels -- shrinks to its last three
+        operations and a range check (lcd_div_checked).  128^3 grid in box
+        tiles: 0.238 -> 0.233 ms, bit for bit."""
+        divisor = self._prepared_divisor
+        if divisor is None or divisor not in taken:
+            return []
+        self._prepared_division_active = True
+        return [f"_lcd_rcp = lcd_div_plain_divisor({divisor}) ? "
+                f"lcd_div_prepare({divisor}) : lcd_empty();"]
+
     def _pipelined_fetch_lines(self, fetch, it):
         """Tiled executor with task records: the loads a round of tasks starts
         with, two rounds deep.  A wavefront's round began with two dependent
@@ -514,6 +528,7 @@ class ProtocolMixin:
             "_g_off = (unsigned)(_g_src - _lcd_tile_row0); "
             "_g_in = _g_off < (unsigned)_lcd_tile_rows; }",
             f"{pad}{pipe['take_second']}",
+            *[pad + line for line in self._prepared_reciprocal(pipe["second"])],
             f"{pad}{pipe['shift']}",
             *[pad + line for line in pipe["request_second"]("_b_", "_round + 1")],
             pad + pipe["request_first"]("_a_", "_round + 2"),
@@ -567,6 +582,9 @@ class ProtocolMixin:
             f"{pad}{it} = 0;",
             f"{pad}if (_pending) {{ {pipe['take_first']} }}",
             f"{pad}{pipe['take_second']}",
+            # (no reciprocal prepared here: on the power-law factor it costs
+            # more wavefront time than the shorter division gives back, 0.666
+            # against 0.659 ms)
             f"{pad}{pipe['shift']}",
             *[pad + line for line in pipe["request_second"]("_b_", "_round")],
             pad + pipe["request_first"]("_a_", "_round + 1"),

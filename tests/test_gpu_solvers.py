@@ -265,6 +265,41 @@ def test_box_tiles(oracle, box, lanes, tpb):
                                work.n).tile_boxes is None
 
 
+def test_box_tiles_divide_again_outside_the_prepared_range(oracle):
+    """The box tiles divide over a reciprocal prepared a round ahead; a
+    divisor or a quotient outside the range that serves (tiny, huge,
+    denormal, zero, not finite) is divided again in full, per lane: the
+    sequential loop's bits, and the same bits without the preparation."""
+    work = workloads.configuration("c2", nx=20, ny=18, nz=16)
+    options = dict(execution_mode="sync_free", threads_per_block=128,
+                   task_lanes=4, thread_unroll=1,
+                   dependence_protocol="mailbox", tile_rows=256,
+                   tile_box=(20, 3, 2))
+    prepared = sptrsv.compile_sptrsv_csc(**options)
+    plain = sptrsv.compile_sptrsv_csc(prepared_division=False, **options)
+    values = work.data.copy()
+    rhs = work.rhs.copy()
+    diagonal = work.indptr[:-1]
+    values[diagonal[50]] = 1e-200
+    values[diagonal[51]] = 1e250
+    values[diagonal[200]] = 5e-324
+    values[diagonal[777]] = -3e-120
+    values[diagonal[1500]] = 2.0 ** 100
+    rhs[300], rhs[301], rhs[4000] = 1e-305, 0.0, -0.0
+    rhs[2500] = np.inf
+    with np.errstate(all="ignore"):
+        expected = oracle.sptrsv_csc(work.indptr, work.indices, values, rhs,
+                                     work.n)
+    for solver in (prepared, plain):
+        result = solver(work.indptr, work.indices, values, rhs, work.n)
+        np.testing.assert_array_equal(result, expected)
+        valid = ~np.isnan(expected)
+        np.testing.assert_array_equal(np.signbit(result[valid]),
+                                      np.signbit(expected[valid]))
+    assert "LCD_PREPARED_DIVISION 1" in prepared.hip_lowering.source
+    assert "LCD_PREPARED_DIVISION 1" not in plain.hip_lowering.source
+
+
 def random_lower_factor(n, seed):
     """Lower-triangular factor with a skewed row-length mix: empty rows,
     short rows and a few rows with up to 300 entries (more incoming edges

@@ -594,8 +594,11 @@ def test_csc_argument_lists_and_protocols():
         assert line in result.kernel_source
     assert result.kernel_source.index("_nl_0 = b[i];") < (
         result.kernel_source.index("lcd_load_relaxed(&dep_count[i])"))
-    assert "_lcd_own_0 = ((_nl_0 - _lcd_own_0) / _nl_2);" in (
+    # (the plain division here: only a tiled fetch pipeline prepares the
+    # divisor's reciprocal and defines LCD_PREPARED_DIVISION)
+    assert "_lcd_own_0 = lcd_pdiv((_nl_0 - _lcd_own_0), _nl_2, _lcd_rcp);" in (
         result.kernel_source)
+    assert "LCD_PREPARED_DIVISION 1" not in result.source
     assert "lcd_atomic_add(&x[_pf_5], (_pf_4 * _lcd_own_0));" in (
         result.kernel_source)
     # sync-free kernels reach arrays that other tasks write through
@@ -1057,6 +1060,19 @@ def test_tiles_addressed_by_queue_position():
             "(lcd_index_t)_task, _lcd_own_0); x[i] = _lcd_own_0;") in kernel
     assert "(_lcd_xq, task_counter, _hip.length(_lcd_xq))" in (
         result.launcher_source)
+    # the reciprocal of the task's divisor is prepared where the round takes
+    # over the node loads it asked for a round ago; the division behind the
+    # wait is its tail plus a range check, the full division where that fails
+    assert "#define LCD_PREPARED_DIVISION 1" in result.source
+    take = kernel.index("_nl_2 = _b__nl_2;")
+    prepare = kernel.index("_lcd_rcp = lcd_div_plain_divisor(_nl_2) ? "
+                           "lcd_div_prepare(_nl_2) : lcd_empty();")
+    assert take < prepare < kernel.index("while (__ballot(_pending))")
+    assert "_lcd_own_0 = lcd_pdiv((_nl_0 - _lcd_own_0), _nl_2, _lcd_rcp);" in kernel
+    plain = lower(module, single_chunk=True, tile_by_position=True,
+                  prepared_division=False, **options)
+    assert "LCD_PREPARED_DIVISION" not in plain.source.split("#ifdef")[0]
+    assert "_lcd_own_0 = ((_nl_0 - _lcd_own_0) / _nl_2);" in plain.kernel_source
     hip_runtime.compile_code(result.source)
     # without the guarantee that a record holds every incoming edge the
     # further chunks would name sources by id: ids stay in charge
