@@ -59,8 +59,9 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_struct_layouts_follow_the_header():
-    """The ctypes mirrors of the C structs (the package's and the stub shown
-    in INTEGRATION.md) list the header's fields in the header's order."""
+    """The ctypes mirrors of the C structs (the package's and the stub the
+    integration guide shows) list the header's fields in the header's
+    order."""
     header = open(os.path.join(ROOT, "include", "lcdhip.h")).read()
 
     def fields_of(struct_name):
