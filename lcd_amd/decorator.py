@@ -65,6 +65,7 @@ from lcd_amd.scheduler import (
     CalibratedScheduler,
     SchedulePlan,
     BAND_WALKER_THREADS_PER_BLOCK,
+    GRID_SWEEP_SHAPE,
     PAIR_TABLE_ENTRIES_PER_POSITION,
     PUBLISHED_TILE_MIN_LOCALITY,
     PUBLISHED_TILE_POSITIONS,
@@ -86,6 +87,11 @@ from lcd_amd.scheduler import (
     compile_thread_trip_counter,
     TRIP_PROBE_SAMPLE,
     measure_thread_trip_counts,
+)
+from lcd_amd.hip_grid_sweep import (
+    SWEEP_MAX_LINE,
+    sweep_applies,
+    sweep_geometry,
 )
 from lcd_amd.structural_lookups import (
     create_structural_lookup_plan,
@@ -226,15 +232,25 @@ def parallel(**kwargs):
         if level_option not in ("auto", True, False):
             raise ValueError("level_walker must be 'auto', True or False.")
 
+        sweep_option = kwargs.get("grid_sweep", "auto")
+        if sweep_option not in ("auto", True, False):
+            raise ValueError("grid_sweep must be 'auto', True or False.")
+        sweep_shape = tuple(kwargs.get("sweep_shape", GRID_SWEEP_SHAPE))
+        if len(sweep_shape) != 4:
+            raise ValueError(
+                "sweep_shape must be (WY, GY, GZ, SKZ): lines of a bundle "
+                "along y, bundles of a workgroup along y and z, steps "
+                "between the z rows of a bundle.")
+
         registers_option = kwargs.get("segment_registers", "auto")
         if registers_option not in ("auto", True, False):
             raise ValueError("segment_registers must be 'auto', True or False.")
 
         def lower_variant(lowering_key, tile_rows=None, single_chunk=False,
                           task_records=True, by_position=False,
-                          registers=False, walker=False, level=0):
+                          registers=False, walker=False, level=0, sweep=None):
             variant_key = (lowering_key, tile_rows, single_chunk, task_records,
-                           by_position, registers, walker, level)
+                           by_position, registers, walker, level, sweep)
             if variant_key not in lowered_variants:
                 (mode, threads_per_block, unroll, n_warp, protocol,
                  task_lanes) = lowering_key
@@ -283,6 +299,7 @@ def parallel(**kwargs):
                     pair_tables=registers == 2,
                     band_walker=walker,
                     level_walker=level,
+                    grid_sweep=sweep,
                     prepared_division=kwargs.get("prepared_division", True),
                     full_fences=kwargs.get("full_fences", False),
                     dynamic_fetch=kwargs.get("dynamic_fetch", False),
@@ -291,12 +308,13 @@ def parallel(**kwargs):
 
         def compile_variant(lowering_key, tile_rows=None, single_chunk=False,
                             task_records=True, by_position=False,
-                            registers=False, walker=False, level=0):
+                            registers=False, walker=False, level=0,
+                            sweep=None):
             lowering = lower_variant(lowering_key, tile_rows, single_chunk,
                                      task_records, by_position, registers,
-                                     walker, level)
+                                     walker, level, sweep)
             variant_key = (lowering_key, tile_rows, single_chunk, task_records,
-                           by_position, registers, walker, level)
+                           by_position, registers, walker, level, sweep)
             if variant_key not in compiled_variants:
                 compiled_variants[variant_key] = compile_hip_module(
                     lowering, function_globals=function.__globals__)
@@ -510,6 +528,54 @@ def parallel(**kwargs):
                 LEVEL_WALKER_ARGUMENTS, records[1:])}
             return candidate, lowering, dag, tables, records[0]
 
+        def sweep_for(dag, schedule, build_incoming):
+            """(schedule, lowering, dag, shape) when this plan runs on the
+            grid sweep: the DAG is an axis stencil on a three-dimensional
+            grid in natural order whose lines the sweep's face arrays hold
+            (``grid_sweep=True`` asks for it; the default takes it for any
+            such DAG beyond the level walker's size unless the call fixes a
+            tile size)."""
+            if sweep_option is False:
+                return None
+            forced = sweep_option is True
+            usable = (schedule.execution_mode == SYNC_FREE and band_width == 1
+                      and schedule.lowering_key[4] in (MAILBOX_DEPENDENCE,
+                                                       PULL_DEPENDENCE)
+                      and (forced or (not isinstance(tile_option, int)
+                                      and dag.n > LEVEL_WALKER_TASKS))
+                      and dag.edges > 0)
+            grid = (kwargs.get("tile_grid") or structured_grid(dag)
+                    if usable else None)
+            shape = None
+            if grid is not None:
+                grid = tuple(int(extent) for extent in grid)
+                if len(grid) == 3 and sweep_applies(grid, *sweep_shape):
+                    shape = grid + sweep_shape
+            lowering, candidate = None, schedule
+            if shape is not None:
+                geometry = sweep_geometry(grid, *sweep_shape)
+                candidate = replace(schedule, thread_unroll=1,
+                                    threads_per_block=geometry["threads"])
+                try:
+                    lowering = lower_variant(candidate.lowering_key, None,
+                                             False, False, False, 0, False, 0,
+                                             shape)
+                except HIPLoweringError:
+                    if forced:
+                        raise
+                    lowering = None
+            if lowering is None:
+                if forced:
+                    raise ValueError(
+                        "grid_sweep=True needs the persistent executor with "
+                        "the mailbox or pull protocol and a DAG that is an "
+                        "axis stencil on a three-dimensional grid in natural "
+                        f"order with lines of at most {SWEEP_MAX_LINE} points.")
+                return None
+            if not incoming_positions:
+                dag = build_incoming()
+            return candidate, lowering, dag, shape
+
         def boxes_for(dag, schedule, rows):
             """(grid, box) when the tiles of this plan are boxes of a
             structured grid: asked for with ``tile_box``, the grid given as
@@ -700,6 +766,25 @@ def parallel(**kwargs):
                     band_walker=True)
                 plan_state[id(plan)] = {"resident": resident, "workspace": {}}
                 return plan
+            sweep = sweep_for(
+                dag, schedule, lambda: build_device_dag(
+                    dag_plan, device_values, device, levels=True,
+                    incoming=True))
+            if sweep is not None:
+                schedule, lowering, dag, shape = sweep
+                execution_data = execution_data_from_device_dag(
+                    dag, schedule.execution_mode, lowering.warp_mapped,
+                    band_width=band_width, mailbox=True, tile_rows=None,
+                    record_lanes=None)
+                plan = SchedulePlan(
+                    schedule=schedule,
+                    execution_data=attach_auxiliary_values(
+                        execution_data, lookup_values),
+                    features=features, dag=dag, tile_rows=None,
+                    single_chunk=False, task_records=False,
+                    grid_sweep=shape)
+                plan_state[id(plan)] = {"resident": resident, "workspace": {}}
+                return plan
             level = level_walker_for(
                 dag, schedule, lambda: build_device_dag(
                     dag_plan, device_values, device, levels=True,
@@ -824,7 +909,8 @@ def parallel(**kwargs):
                                                  plan.tile_boxes is not None,
                                                  plan.segment_registers,
                                                  plan.band_walker,
-                                                 plan.level_walker)
+                                                 plan.level_walker,
+                                                 plan.grid_sweep)
             publish_variant(plan.schedule, lowering, compiled)
             state = plan_state[id(plan)]
             values = dict(argument_values)
@@ -905,6 +991,17 @@ class BoundCall:
 
     def launch(self, use_graph=True):
         launch_hip_call(self.compiled, self.lowering, self.prepared, use_graph)
+
+    def update_values(self):
+        """Tell the call that the contents of the matrix arrays have changed
+        in place since it was bound (executors that keep a copy of them in
+        their own layout -- the grid sweep -- lay it out again; the arrays
+        named in ``lowering.sweep_static_arrays``).  Everything else, the
+        right-hand side included, is read at every launch."""
+        if getattr(self.lowering, "grid_sweep", None):
+            hip_runtime.stage_sweep_values(
+                self.compiled, self.lowering, self.prepared.values,
+                self.prepared.module, self.prepared.device)
 
     def synchronize(self):
         self.prepared.device.synchronize()

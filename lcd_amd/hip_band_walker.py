@@ -182,7 +182,7 @@ class BandWalkerMixin:
             if store.match(line.strip()):
                 found += 1
                 out.append(f"_lcd_wout = {register};"
-                           if self._walker.get("kind") == "level" else
+                           if self._walker.get("kind") in ("level", "sweep") else
                            f"_lcd_wout = lcd_bfi(_lcd_wmask, {register}, "
                            "_lcd_wout);")
             else:

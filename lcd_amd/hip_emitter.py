@@ -127,6 +127,15 @@ class HIPLoweringResult:
     # one wavefront takes a level per step (small DAGs with narrow levels):
     # the incoming entries per task it has room for, or 0
     level_walker: int = 0
+    # grid sweep (lcd_amd/hip_grid_sweep.py): its geometry, the names of the
+    # staging kernels (matrix part, other part, solution back to its array),
+    # whether anything is staged per launch, the arrays the matrix part reads
+    # and the launcher function that stages the matrix part
+    grid_sweep: dict | None = None
+    sweep_kernels: tuple = ()
+    sweep_dynamic: bool = False
+    sweep_static_arrays: tuple = ()
+    sweep_launcher_name: str | None = None
     # the pointer array of the task's own segment (ILU0's row), and whether
     # that segment is kept in registers (segments of at most 64 entries)
     segment_pointer: str | None = None

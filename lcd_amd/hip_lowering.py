@@ -85,10 +85,15 @@ from lcd_amd.hip_protocols import ProtocolMixin
 from lcd_amd.hip_sequential_pull import SequentialPullMixin
 from lcd_amd.hip_task_transforms import TaskTransformMixin
 from lcd_amd.hip_band_walker import BandWalkerMixin
+from lcd_amd.hip_grid_sweep import (
+    SWEEP_ARGUMENTS,
+    SWEEP_FLOAT_ARGUMENTS,
+    GridSweepMixin,
+)
 
 
 class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
-                 BandWalkerMixin):
+                 BandWalkerMixin, GridSweepMixin):
     def __init__(self, loop_iterator, reductions=None, kernel_name=None,
                  execution_mode="plain", sync_free_ready_count=0,
                  wavefront_threads_per_block=128, thread_loop_iterator=None,
@@ -107,8 +112,11 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                  dynamic_fetch=False, tile_positions=None,
                  tile_by_position=False, segment_registers=False,
                  pair_tables=True, band_walker=False, level_walker=0,
-                 prepared_division=True):
+                 prepared_division=True, grid_sweep=None):
         self.tile_positions = tile_positions
+        # (nx, ny, nz, WY, GY, GZ, SKZ): the grid sweep over this grid
+        self.grid_sweep = tuple(grid_sweep) if grid_sweep else None
+        self._sweep = None
         self.band_walker = bool(band_walker)
         # > 0: the level walker, with room for this many incoming entries per task
         self.level_walker = int(level_walker or 0)
@@ -341,7 +349,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
         elif (self.dependence_protocol == PULL_DEPENDENCE and self.value_flags
                 and self.execution_mode == "sync_free"):
             self._value_pull = self._value_pull_plan(body)
-        if ((self.band_walker or self.level_walker)
+        if ((self.band_walker or self.level_walker or self.grid_sweep)
                 and self._value_pull is not None
                 and self.dependence_protocol == PULL_DEPENDENCE):
             # the pull-shaped solve in the terms of the gathered mailbox: the
@@ -357,9 +365,14 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                     and self._mailbox["gather"] is None):
                 self._mailbox["gather"] = self._gather_plan(
                     self._mailbox, arguments, lifted_loop_parameters)
-        if self.band_walker or self.level_walker:
+        if self.band_walker or self.level_walker or self.grid_sweep:
             self._walker = self._band_walker_plan(target_loop)
-            if self._walker is not None and self.level_walker:
+            if self._walker is not None and self.grid_sweep:
+                self._walker.update(kind="sweep")
+                for name in SWEEP_ARGUMENTS:
+                    kinds.arrays[name] = (FLOAT if name in SWEEP_FLOAT_ARGUMENTS
+                                          else INT)
+            elif self._walker is not None and self.level_walker:
                 self._walker.update(kind="level", entries=self.level_walker)
                 for name in LEVEL_WALKER_ARGUMENTS:
                     kinds.arrays[name] = INT
@@ -469,6 +482,8 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                 user_arguments.append("_lcd_pair_base")
         if self._walker is not None and self._walker["kind"] == "level":
             user_arguments += [*LEVEL_WALKER_ARGUMENTS, LEVEL_WALKER_LEVELS]
+        if self._walker is not None and self._walker["kind"] == "sweep":
+            user_arguments += list(SWEEP_ARGUMENTS)
         if (self.thread_loop_iterator is not None
                 and self.dependence_protocol != COUNTER_DEPENDENCE
                 and self._sequential_pull is None):
@@ -496,6 +511,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                 + ", ".join(sorted(missing)))
 
         function_name = function.name
+        self._sweep_function_name = function_name
         kernel_name = self.kernel_name or function_name + "_hip_kernel"
         launcher_name = function_name + "_hip_launch"
         reset_name = None
@@ -570,6 +586,14 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                              and self._walker["kind"] == "band"),
             level_walker=(self.level_walker if self._walker
                           and self._walker["kind"] == "level" else 0),
+            grid_sweep=(dict(self._sweep["geometry"]) if self._sweep else None),
+            sweep_kernels=(tuple(self._sweep["kernels"]) if self._sweep
+                           else ()),
+            sweep_dynamic=bool(self._sweep and self._sweep["dynamic_kernel"]),
+            sweep_static_arrays=(tuple(self._sweep["static_arrays"])
+                                 if self._sweep else ()),
+            sweep_launcher_name=(function_name + "_hip_sweep_restage"
+                                 if self._sweep else None),
             segment_pointer=(self._segment["pointer"]
                              if self._segment else None),
             segment_registers=bool(self._segment
@@ -975,7 +999,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
         parts = []
         mutable_executor = {"dep_count", "task_counter", "done",
                             STATUS_ARGUMENT, "_lcd_mailbox", "_lcd_pub",
-                            "_lcd_xq"}
+                            "_lcd_xq", *SWEEP_ARGUMENTS}
         for name in kernel_arguments:
             if name in array_arguments:
                 const = (name not in written_arrays
@@ -1153,13 +1177,27 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
         elif self._walker is not None:
             walker = (self._level_walker_text(task_body)
                       if self._walker["kind"] == "level"
+                      else self._grid_sweep_text(task_body)
+                      if self._walker["kind"] == "sweep"
                       else self._band_walker_text(task_body))
             if walker is None:
                 raise HIPLoweringError(
-                    "The band walker cannot stage this task's node loads.")
+                    "The band walker cannot stage this task's node loads."
+                    if self._walker["kind"] != "sweep" else
+                    "The grid sweep needs a task whose tail is arithmetic "
+                    "over its node loads (+, -, *, one division by a node "
+                    "load), a workgroup of (GY * GZ + GY + GZ) wavefronts "
+                    "and face arrays that fit the LDS.")
             if self._walker["division"]:
                 lines.append("    double _lcd_wr = 0.0;")
             lines += walker
+            if self._walker["kind"] == "sweep":
+                # the staging kernels share the signature and the locals
+                lines.append("}")
+                return (self._grid_sweep_kernels(
+                    self._sweep_function_name, signature,
+                    self._declarations(local_names, 1))
+                        + "\n".join(lines) + "\n")
         else:
             lines += self._sync_free_text(task, node_loop)
         lines.append("}")
@@ -1591,6 +1629,30 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                 # tile takes, not by a polling budget
                 tasks_per_block = self._tile["rows"]
                 waves_per_cu = self.resident_waves_per_cu
+            if self._sweep is not None:
+                # one workgroup per GY x GZ bundles of grid lines; the part of
+                # a step's record that is not the matrix's goes in first, the
+                # solution comes back out of the wavefronts' order last
+                geometry = self._sweep["geometry"]
+                blocks = (geometry["slots"] + 255) // 256
+                static, dynamic, unstage = self._sweep["kernels"]
+                if self._sweep["dynamic_kernel"]:
+                    body.append(f"_hip.launch({dynamic!r}, {blocks}, 256, "
+                                f"{call_args})")
+                body.append(f"_hip.launch({kernel_name!r}, "
+                            f"{geometry['workgroups']}, "
+                            f"{self.threads_per_block}, {call_args})")
+                body.append(f"_hip.launch({unstage!r}, {blocks}, 256, "
+                            f"{call_args})")
+                restage = [f"_count = _hip.length({count_array})",
+                           f"_hip.launch({static!r}, {blocks}, 256, {call_args})"]
+                text = (f"def {launcher_name}(_hip, "
+                        + ", ".join(launcher_arguments) + "):\n"
+                        + "\n".join("    " + line for line in body) + "\n"
+                        f"\n\ndef {self._sweep_function_name}_hip_sweep_restage"
+                        "(_hip, " + ", ".join(launcher_arguments) + "):\n"
+                        + "\n".join("    " + line for line in restage) + "\n")
+                return text, launcher_arguments
             if self._walker is not None:
                 # one workgroup: the walker and the wavefronts that stage for it
                 body.append("_blocks = 1")
@@ -1626,7 +1688,7 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
                  pipeline_fetch=True, full_fences=False, dynamic_fetch=False,
                  tile_positions=None, tile_by_position=False,
                  segment_registers=False, pair_tables=True, band_walker=False,
-                 level_walker=0, prepared_division=True):
+                 level_walker=0, prepared_division=True, grid_sweep=None):
     """HIP counterpart of ``lower_to_numba_cuda``
     (compiler/cuda_lowering.py:2854-2884); same parameters plus
     ``task_lanes`` (lanes cooperating on one task, a power of two <= 64),
@@ -1657,5 +1719,5 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
         tile_by_position=tile_by_position,
         segment_registers=segment_registers, pair_tables=pair_tables,
         band_walker=band_walker, level_walker=level_walker,
-        prepared_division=prepared_division)
+        prepared_division=prepared_division, grid_sweep=grid_sweep)
     return lowerer.lower(code)

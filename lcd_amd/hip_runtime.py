@@ -1192,6 +1192,8 @@ def prepare_hip_arguments(lowering, argument_values, execution_data,
                 cached = device.empty((slots,), dtype)
                 workspace[("state", name)] = cached
             host_values[name] = cached
+        if getattr(lowering, "grid_sweep", None):
+            host_values.update(_sweep_buffers(lowering, device, workspace))
         for name in ("task_counter", STATUS_ARGUMENT):
             cached = workspace.get(("state", name))
             if cached is None:
@@ -1226,6 +1228,16 @@ def prepare_hip_arguments(lowering, argument_values, execution_data,
     module = None
     if compiled_module is not None:
         module = _load_for_values(compiled_module, lowering, prepared, device)
+    if (getattr(lowering, "grid_sweep", None) and module is not None
+            and isinstance(device, HIPDevice)):
+        # the matrix's share of the sweep's records: staged again when the
+        # contents of its arrays have changed since the last time
+        digests = tuple(device.digest(prepared[name])
+                        for name in lowering.sweep_static_arrays)
+        if workspace.get(("sweep", "digests")) != digests:
+            stage_sweep_values(compiled_module, lowering, prepared, module,
+                               device)
+            workspace[("sweep", "digests")] = digests
     # a captured graph stays valid while every pointer and scalar is unchanged
     graph_key = ("graph", lowering.kernel_name) + tuple(
         (name, device_pointer(value)) if is_device_array(value)
@@ -1335,8 +1347,64 @@ def _load_for_values(compiled, lowering, prepared, device):
                     stage.append(ctypes.c_void_p)
             argument_ctypes[lowering.stage_kernel_name] = stage + [
                 ctypes.c_int64]
+        for name in getattr(lowering, "sweep_kernels", ()):
+            # the staging kernels of the grid sweep share the signature
+            argument_ctypes[name] = list(ctypes_of)
         compiled.loaded[cache_key] = device.load_module(code, argument_ctypes)
     return compiled.loaded[cache_key]
+
+
+EMPTY_MARKER_WORD = 0x7FF84C43       # both halves of the empty marker (a NaN)
+
+
+def _sweep_buffers(lowering, device, workspace):
+    """Device memory of the grid sweep, once per plan: the records in the
+    wavefronts' order, the solution in the same order, the faces between
+    workgroups (every slot the empty marker: a slot is filled and emptied
+    again within one launch) and the two counters of a launch."""
+    geometry = lowering.grid_sweep
+    cached = workspace.get(("sweep", "buffers"))
+    if cached is None:
+        slots = geometry["slots"]
+        faces = geometry["bundles"] + geometry["nby"] + 1
+        cached = {
+            "_lcd_sw_ops": device.empty((slots * geometry["pairs"] * 2,),
+                                        np.float64),
+            "_lcd_sw_out": device.empty((slots,), np.float64),
+            "_lcd_sw_yface": device.empty(
+                (faces * geometry["yrows"] * geometry["wz"],), np.float64),
+            "_lcd_sw_zface": device.empty(
+                (faces * geometry["zrows"] * geometry["wy"],), np.float64),
+            "_lcd_sw_claim": device.zeros((4,), np.int32),
+        }
+        workspace[("sweep", "buffers")] = cached
+        _sweep_reset(cached, device)
+    return cached
+
+
+def _sweep_reset(buffers, device):
+    """Every face slot empty, both counters zero: the state a launch of
+    the sweep starts from and, unless it is abandoned, ends in."""
+    if not isinstance(device, HIPDevice):
+        return
+    for name in ("_lcd_sw_yface", "_lcd_sw_zface"):
+        array = buffers[name]
+        _check(device.lib.lcdhip_buffer_fill32(
+            ctypes.c_void_p(array.pointer), ctypes.c_uint32(EMPTY_MARKER_WORD),
+            ctypes.c_size_t(array.nbytes // 4), device.stream))
+    device.fill_zero(buffers["_lcd_sw_claim"])
+
+
+def stage_sweep_values(compiled_module, lowering, prepared_values, module,
+                       device):
+    """Lay the matrix's share of the grid sweep's records out again (the
+    coefficients by direction, the node loads that come from the matrix
+    arrays, the prepared reciprocals): to be called whenever the contents of
+    ``lowering.sweep_static_arrays`` have changed."""
+    launcher = compiled_module.namespace[lowering.sweep_launcher_name]
+    context = LaunchContext(device, module, None)
+    launcher(context, *[prepared_values[name]
+                        for name in lowering.launcher_arguments])
 
 
 # A captured level loop is one graph with a kernel node per level.  Replaying
@@ -1435,6 +1503,17 @@ def check_executor_status(lowering, prepared_arguments):
         _check(device.lib.lcdhip_buffer_fill32(
             ctypes.c_void_p(status.pointer), ctypes.c_uint32(0),
             ctypes.c_size_t(1), device.stream))
+        if getattr(lowering, "grid_sweep", None):
+            # an abandoned launch leaves faces and counters half used
+            _sweep_reset({name: prepared_arguments.values[name]
+                          for name in ("_lcd_sw_yface", "_lcd_sw_zface",
+                                       "_lcd_sw_claim")}, device)
+            if int(host[0]) == 3:
+                raise HIPRuntimeError(
+                    f"The grid sweep of {lowering.function_name} met an "
+                    "incoming entry that is not one step down along an axis "
+                    "of the grid.  The result is not valid; run with "
+                    "grid_sweep=False.", ERR_ARGUMENT)
         if int(host[0]) == 2 and getattr(lowering, "band_walker", False):
             raise HIPRuntimeError(
                 f"The band walker of {lowering.function_name} met an edge its "

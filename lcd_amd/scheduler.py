@@ -166,6 +166,17 @@ class SchedulePlan:
     # one wavefront takes a level per step (small DAGs with narrow levels):
     # the incoming entries per task it has room for, or 0
     level_walker: int = 0
+    # the grid sweep: (nx, ny, nz, WY, GY, GZ, SKZ), or None
+    grid_sweep: tuple | None = None
+
+
+# Grid sweep, automatic choice: bundles of 16 x 4 grid lines per wavefront,
+# two bundles stacked along z per workgroup, two steps between the z rows of
+# a bundle.  Measured on the 128^3 grid (sweep kernel alone): 121 us with this
+# shape, 137 us with one bundle per workgroup (more faces through memory),
+# 156 us with four (four streams of operands share one CU's path to memory),
+# 125 us with bundles of 8 x 8 lines.
+GRID_SWEEP_SHAPE = (16, 1, 2, 2)
 
 
 # Tiled executor, automatic choice: tiles of 4096 consecutive block-iterator
