@@ -43,6 +43,7 @@ import re
 from lcd_amd.hip_emitter import FLOAT, INT
 
 SWEEP_DEPTH = 8                 # steps of operands a wavefront has in flight
+SWEEP_TILE_STEPS = 32           # steps of a bundle one staging workgroup handles
 SWEEP_MAX_LINE = 384            # longest grid line the LDS face arrays hold
 SWEEP_ARGUMENTS = ("_lcd_sw_ops", "_lcd_sw_out", "_lcd_sw_yface",
                    "_lcd_sw_zface", "_lcd_sw_claim")
@@ -63,16 +64,20 @@ def sweep_geometry(grid, wy=16, gy=1, gz=2, skz=2, components=6):
     sp = -(-steps // SWEEP_DEPTH) * SWEEP_DEPTH
     ylag, zlag = wy - 1, (wz - 1) * skz
     pairs = -(-int(components) // 2)
+    # (records per bundle: the loop's steps, the steps the prefetch runs
+    # ahead, rounded up to the tiles of the staging kernels)
+    spa = -(-(sp + SWEEP_DEPTH) // SWEEP_TILE_STEPS) * SWEEP_TILE_STEPS
     geometry = dict(
         nx=nx, ny=ny, nz=nz, wy=wy, wz=wz, gy=gy, gz=gz, skz=skz,
         nby=nby, nbz=nbz, bundles=nby * nbz, steps=steps, sp=sp,
-        spa=sp + SWEEP_DEPTH, wgy=-(-nby // gy), wgz=-(-nbz // gz),
+        spa=spa, wgy=-(-nby // gy), wgz=-(-nbz // gz),
         waves=gy * gz, helpers=gy + gz, ylag=ylag, zlag=zlag,
         yrows=ylag + sp + 1, zrows=zlag + sp + 1, pairs=pairs,
         components=int(components))
     geometry["workgroups"] = geometry["wgy"] * geometry["wgz"]
     geometry["threads"] = (geometry["waves"] + geometry["helpers"]) * 64
     geometry["slots"] = geometry["bundles"] * geometry["spa"] * 64
+    geometry["tiles"] = geometry["bundles"] * (spa // SWEEP_TILE_STEPS)
     geometry["lds_bytes"] = 8 * (
         geometry["waves"] * (geometry["yrows"] * wz + geometry["zrows"] * wy
                              + 8 * 64)
@@ -320,6 +325,28 @@ _SWEEP_SLOT = r"""
 """
 
 
+_SWEEP_TILE = r"""
+    // one workgroup of 256 threads per tile of 32 steps x 64 lanes of a bundle:
+    // memory is touched in runs along the grid lines on one side and along the
+    // lanes of a record on the other, the tile turns in LDS between the two
+    constexpr int SW_NX = @nx@, SW_NY = @ny@, SW_NZ = @nz@, SW_WY = @wy@, SW_WZ = @wz@;
+    constexpr int SW_SKZ = @skz@, SW_SPA = @spa@, SW_P = @pairs@, SW_NBY = @nby@;
+    constexpr int SW_TS = @tile_steps@;
+    const int _s_beta = (int)(blockIdx.x / (SW_SPA / SW_TS));
+    const int _s_s0 = (int)(blockIdx.x % (SW_SPA / SW_TS)) * SW_TS;
+    const int _s_by = _s_beta % SW_NBY, _s_bz = _s_beta / SW_NBY;
+    const long long _s_row0 = (long long)_s_beta * SW_SPA + _s_s0;
+    (void)_lane; (void)_s_row0;
+    // (lane of the bundle, step of the tile) -> is there a task, and which
+    auto _s_task = [&](int lane, int st, bool& active) {
+        const int y = _s_by * SW_WY + lane % SW_WY, z = _s_bz * SW_WZ + lane / SW_WY;
+        const int x = _s_s0 + st - lane % SW_WY - SW_SKZ * (lane / SW_WY);
+        active = x >= 0 && x < SW_NX && y < SW_NY && z < SW_NZ;
+        return active ? (lcd_index_t)(x + SW_NX * (y + (long long)SW_NY * z)) : (lcd_index_t)0;
+    };
+"""
+
+
 class GridSweepMixin:
     """Methods of ``HIPLowerer`` (lcd_amd/hip_lowering.py)."""
 
@@ -531,20 +558,60 @@ class GridSweepMixin:
             *([f"    {component(parts['components'])} = 0.0;"]
               if parts["components"] % 2 else []),
         ]
+        tile_head = _SWEEP_TILE
+        for key, value in dict(geometry, tile_steps=SWEEP_TILE_STEPS).items():
+            tile_head = tile_head.replace(f"@{key}@", str(value))
+
+        def tile_kernel(name, body):
+            return [f'extern "C" __global__ void __launch_bounds__(256) {name}(',
+                    f"        {signature})", "{",
+                    "    const int _lane = 0;", f"    lcd_index_t {it} = 0;",
+                    *declarations,
+                    *(["    double _lcd_wr = 0.0; (void)_lcd_wr;"]
+                      if division else []),
+                    *tile_head.strip("\n").split("\n"), *body, "}", ""]
+
+        count = max(len(dynamic_slots), 1)
         dynamic_body = [
-            "    if (_s_active) {",
-            *["        " + line for line in all_lines],
-            *(["        " + line for line in reciprocal]
+            f"    __shared__ double _s_tile[{count}][SW_TS][65];",
+            "    for (int p = 0; p < 8; ++p) {",
+            "        const int lane = p * 8 + (int)(threadIdx.x >> 5), st = (int)(threadIdx.x & 31);",
+            "        bool active;",
+            f"        {it} = _s_task(lane, st, active);",
+            "        if (active) {",
+            *["            " + line for line in all_lines],
+            *(["            " + line for line in reciprocal]
               if division and "_lcd_wr" in parts["dynamic"] else []),
+            "        }",
+            # (a lane without a task computes on ones)
+            *[f"        _s_tile[{q}][st][lane] = active ? {put(name, kind)} : 1.0;"
+              for q, (k, (name, kind)) in enumerate(dynamic_slots)],
             "    }",
-            *[f"    {component(entries + k)} = _s_active ? {put(name, kind)} : 1.0;"
-              for k, (name, kind) in dynamic_slots],
+            "    __syncthreads();",
+            "    for (int u = 0; u < 8; ++u) {",
+            "        const int at = u * 256 + (int)threadIdx.x, st = at >> 6, lane = at & 63;",
+            "        double* const _s_rec = _lcd_sw_ops + (_s_row0 + st) * (SW_P * 128) + lane * 2;",
+            *[f"        {component(entries + k)} = _s_tile[{q}][st][lane];"
+              for q, (k, _) in enumerate(dynamic_slots)],
+            "    }",
         ]
         unstage_body = [
-            f"    if (_s_active) {box['array']}[{it}] = _lcd_sw_out[_s_t];",
+            "    __shared__ double _s_tile[SW_TS][65];",
+            "    for (int u = 0; u < 8; ++u) {",
+            "        const int at = u * 256 + (int)threadIdx.x, st = at >> 6, lane = at & 63;",
+            "        _s_tile[st][lane] = _lcd_sw_out[(_s_row0 + st) * 64 + lane];",
+            "    }",
+            "    __syncthreads();",
+            "    for (int p = 0; p < 8; ++p) {",
+            "        const int lane = p * 8 + (int)(threadIdx.x >> 5), st = (int)(threadIdx.x & 31);",
+            "        bool active;",
+            f"        {it} = _s_task(lane, st, active);",
+            f"        if (active) {box['array']}[{it}] = _s_tile[st][lane];",
+            "    }",
         ]
-        lines = (kernel(names[0], static_body) + kernel(names[1], dynamic_body)
-                 + kernel(names[2], unstage_body))
+        lines = (kernel(names[0], static_body)
+                 + tile_kernel(names[1], dynamic_body)
+                 + tile_kernel(names[2], unstage_body))
         self._sweep["kernels"] = names
         self._sweep["dynamic_kernel"] = bool(dynamic_slots)
         return "\n".join(lines) + "\n"

@@ -1636,13 +1636,14 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                 geometry = self._sweep["geometry"]
                 blocks = (geometry["slots"] + 255) // 256
                 static, dynamic, unstage = self._sweep["kernels"]
+                tiles = geometry["tiles"]
                 if self._sweep["dynamic_kernel"]:
-                    body.append(f"_hip.launch({dynamic!r}, {blocks}, 256, "
+                    body.append(f"_hip.launch({dynamic!r}, {tiles}, 256, "
                                 f"{call_args})")
                 body.append(f"_hip.launch({kernel_name!r}, "
                             f"{geometry['workgroups']}, "
                             f"{self.threads_per_block}, {call_args})")
-                body.append(f"_hip.launch({unstage!r}, {blocks}, 256, "
+                body.append(f"_hip.launch({unstage!r}, {tiles}, 256, "
                             f"{call_args})")
                 restage = [f"_count = _hip.length({count_array})",
                            f"_hip.launch({static!r}, {blocks}, 256, {call_args})"]
