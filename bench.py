@@ -46,10 +46,11 @@ TUNED = {
     # of 1024 rows with 256 threads)
     "c1": dict(execution_mode="sync_free", task_lanes=4,
                thread_unroll=1, dependence_protocol="mailbox", spin_sleep=0),
-    # (tiles are boxes of 128 x 8 x 4 grid points: the default tile_box="auto")
-    "c2": dict(execution_mode="sync_free", threads_per_block=512, task_lanes=4,
-               thread_unroll=1, dependence_protocol="mailbox",
-               tile_rows=4096, spin_sleep=0),
+    # (an axis stencil on a grid: the grid sweep, chosen per plan -- a lane per
+    # grid line, a wavefront per bundle of 8 x 8 lines; --grid-sweep 0 gives
+    # the box tiles of 128 x 8 x 4 points with 512 threads)
+    "c2": dict(execution_mode="sync_free", task_lanes=4, thread_unroll=1,
+               dependence_protocol="mailbox", spin_sleep=0),
     "c3": dict(execution_mode="sync_free", threads_per_block=128,
                task_lanes=64, thread_unroll=1,
                dependence_protocol="pull", tile_rows=None),
@@ -147,6 +148,14 @@ def build_solver(work, args, config):
         if not args.band_walker and config == "c5" and not args.auto:
             options.setdefault("threads_per_block", 128)
             options.setdefault("tile_rows", 8192)
+    if args.grid_sweep is not None:
+        options["grid_sweep"] = bool(args.grid_sweep)
+        if not args.grid_sweep and config == "c2" and not args.auto:
+            options.setdefault("threads_per_block", 512)
+            options.setdefault("tile_rows", 4096)
+    if args.sweep_shape:
+        options["sweep_shape"] = tuple(
+            int(extent) for extent in args.sweep_shape.split(","))
     if args.level_walker is not None:
         options["level_walker"] = bool(args.level_walker)
         if not args.level_walker and config == "c1" and not args.auto:
@@ -331,6 +340,8 @@ def run_configuration(config, args, device, steps, warmup, handoff_s,
                          if getattr(plan, "tile_boxes", None) else None),
             "band_walker": bool(getattr(plan, "band_walker", False)),
             "level_walker": bool(getattr(plan, "level_walker", 0)),
+            "grid_sweep": (list(plan.grid_sweep)
+                           if getattr(plan, "grid_sweep", None) else None),
             "replayed_from_graph": not args.no_graph,
         },
         "roofline_pct": round(100.0 * gbps / HBM_PEAK_GBPS, 3),
@@ -395,6 +406,7 @@ def run_configuration(config, args, device, steps, warmup, handoff_s,
                       else None,
                       "band_walker" if getattr(plan, "band_walker", False)
                       else "level_walker" if getattr(plan, "level_walker", 0)
+                      else "grid_sweep" if getattr(plan, "grid_sweep", None)
                       else False)
     record["roofline"] = {
         "bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBPS,
@@ -472,6 +484,15 @@ def main():
                         help="1: run small DAGs with narrow levels on one "
                              "wavefront, a level per step; 0: never (default: "
                              "per plan)")
+    parser.add_argument("--grid-sweep", dest="grid_sweep", type=int,
+                        default=None, choices=(0, 1),
+                        help="1: run axis stencils on a 3-D grid on the grid "
+                             "sweep (a lane per grid line); 0: never "
+                             "(default: per plan)")
+    parser.add_argument("--sweep-shape", dest="sweep_shape", default=None,
+                        help="grid sweep: WY,GY,GZ,SKZ (lines of a bundle "
+                             "along y, bundles of a workgroup along y and z, "
+                             "steps between the z rows of a bundle)")
     parser.add_argument("--tile-box", dest="tile_box", default=None,
                         help="tiles over boxes of a structured grid: "
                              "'auto', 'none' or extents as 32x8x16")
@@ -560,7 +581,7 @@ def main():
                      "waves_per_cu", "spin_sleep", "tile_rows",
                      "plain_first", "look_ahead", "tile_positions",
                      "segment_capacity", "tile_box", "band_walker",
-                     "level_walker"):
+                     "level_walker", "grid_sweep", "sweep_shape"):
             setattr(sub_args, name, None)
         for name in ("slots", "no_queue_loads", "no_publish", "no_pipeline",
                      "no_graph", "level_gather"):

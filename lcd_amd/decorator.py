@@ -744,7 +744,8 @@ def parallel(**kwargs):
                 schedule = scheduler.schedule(features, schedule_space)
             # (a walker asked for by name goes before the other's automatic
             # choice)
-            walker = (None if level_option is True and walker_option != True
+            walker = (None if (level_option is True or sweep_option is True)
+                      and walker_option != True
                       else walker_for(dag, schedule))
             if walker is not None:
                 schedule, lowering = walker

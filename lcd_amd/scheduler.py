@@ -170,13 +170,17 @@ class SchedulePlan:
     grid_sweep: tuple | None = None
 
 
-# Grid sweep, automatic choice: bundles of 16 x 4 grid lines per wavefront,
-# two bundles stacked along z per workgroup, two steps between the z rows of
-# a bundle.  Measured on the 128^3 grid (sweep kernel alone): 121 us with this
-# shape, 137 us with one bundle per workgroup (more faces through memory),
-# 156 us with four (four streams of operands share one CU's path to memory),
-# 125 us with bundles of 8 x 8 lines.
-GRID_SWEEP_SHAPE = (16, 1, 2, 2)
+# Grid sweep, automatic choice (WY, GY, GZ, SKZ): bundles of 8 x 8 grid lines
+# per wavefront, two bundles stacked along z per workgroup, one step between
+# the z rows of a bundle.  Measured on the 128^3 grid (one solve: staging of
+# the right-hand side, sweep, solution back to its array): 125 us with this
+# shape; 126 us with the two bundles side by side along y; 128 us with one
+# bundle per workgroup (more faces through memory); 139 us with four (four
+# streams of operands share one CU's path to memory); 132 us with bundles of
+# 16 x 4 lines; two steps between the z rows (the z value is then read from
+# LDS a step ahead of its use, but a bundle takes 14 steps more and the path
+# through the grid 127) 143 us with 8 x 8 lines and 162 us with 16 x 4.
+GRID_SWEEP_SHAPE = (8, 1, 2, 1)
 
 
 # Tiled executor, automatic choice: tiles of 4096 consecutive block-iterator

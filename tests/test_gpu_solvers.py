@@ -1237,9 +1237,10 @@ def test_plain_first_polls_see_no_value_of_an_earlier_launch(
     compile_solver = (sptrsv.compile_sptrsv_csr if csr
                       else sptrsv.compile_sptrsv_csc)
     reference = oracle.sptrsv_csr if csr else oracle.sptrsv_csc
-    # (the walkers poll nothing: the executors that do are what is tested)
+    # (the walkers and the grid sweep poll no value of the solution: the
+    # executors that do are what is tested)
     solver = compile_solver(plain_first_polls=True, level_walker=False,
-                            band_walker=False, **options)
+                            band_walker=False, grid_sweep=False, **options)
     operands = [device.to_device(a) for a in
                 (work.indptr, work.indices, work.data, work.rhs)]
     call = solver.bind(*operands, work.n)
@@ -1295,8 +1296,9 @@ def test_full_size_configurations(oracle, name, kind):
 
 
 def test_full_size_headline_defaults(oracle):
-    """Configuration 2 as bench.py runs it (tiled gathered mailbox) and as the
-    decorator chooses by itself: bit-identical to the sequential loop."""
+    """Configuration 2 on the tiled gathered mailbox and as the decorator
+    chooses by itself (the grid sweep; box tiles without it): bit-identical
+    to the sequential loop."""
     work = workloads.configuration("c2")
     expected = oracle.sptrsv_csc(work.indptr, work.indices, work.data,
                                  work.rhs, work.n)
@@ -1310,6 +1312,13 @@ def test_full_size_headline_defaults(oracle):
     plan = automatic.schedule_plan(work.indptr, work.indices, work.data,
                                    work.rhs, work.n)
     assert plan.schedule.execution_mode == "sync_free"
+    assert plan.schedule.dependence_protocol == "mailbox"
+    assert plan.grid_sweep is not None and plan.grid_sweep[:3] == (128, 128, 128)
+    assert automatic.hip_lowering.grid_sweep["workgroups"] == 128
+    automatic = sptrsv.compile_sptrsv_csc(grid_sweep=False)
+    solve_and_check(automatic, work, expected, exact=True)
+    plan = automatic.schedule_plan(work.indptr, work.indices, work.data,
+                                   work.rhs, work.n)
     assert plan.schedule.dependence_protocol == "mailbox"
     assert plan.tile_rows == 4096 and automatic.hip_lowering.tile_rows == 4096
     assert 0.6 < plan.dag.tile_locality(4096) < 0.7
@@ -1364,7 +1373,13 @@ def test_full_size_under_bench_settings(oracle, name):
             assert solver.hip_lowering.tile_rows is None
             assert solver.current_schedule.threads_per_block == 1024
             return
-        assert solver.hip_lowering.tile_rows == options["tile_rows"]
+        # the grid of configuration 2 runs on the grid sweep, whose workgroup
+        # is its bundles' and helpers' wavefronts
+        assert solver.hip_lowering.grid_sweep is not None
+        assert solver.hip_lowering.tile_rows is None
+        assert solver.current_schedule.threads_per_block == (
+            solver.hip_lowering.grid_sweep["threads"])
+        return
     else:
         solver = sptrsv.compile_sptrsv_csr(**options)
         expected = oracle.sptrsv_csr(work.indptr, work.indices, work.data,

@@ -1040,6 +1040,87 @@ def test_level_walker_lowering_and_records():
     assert level_walker_records(wider, 4096, 4, forced=True)[0] == 1
 
 
+def test_grid_sweep_lowering_and_geometry():
+    """The executor of axis stencils on a three-dimensional grid: a lane per
+    grid line, a wavefront per bundle of lines, the operands of a step in
+    records the staging kernels lay out in the wavefronts' order."""
+    from lcd_amd.hip_grid_sweep import (SWEEP_ARGUMENTS, sweep_applies,
+                                        sweep_geometry)
+    geometry = sweep_geometry((128, 128, 128), 8, 1, 2, 1)
+    assert (geometry["nby"], geometry["nbz"], geometry["bundles"]) == (16, 16, 256)
+    assert geometry["steps"] == 128 + 7 + 7 and geometry["sp"] == 144
+    assert geometry["spa"] == 160 and geometry["spa"] % 32 == 0
+    assert (geometry["workgroups"], geometry["threads"]) == (128, 5 * 64)
+    assert geometry["slots"] == 256 * 160 * 64 and geometry["tiles"] == 256 * 5
+    assert geometry["lds_bytes"] < 160 * 1024
+    ragged = sweep_geometry((33, 17, 9), 16, 1, 2, 2)
+    assert (ragged["nby"], ragged["nbz"], ragged["wgz"]) == (2, 3, 2)
+    assert ragged["steps"] == 33 + 15 + 3 * 2 and ragged["zlag"] == 6
+    assert sweep_applies((128, 128, 128), 8, 1, 2, 1)
+    assert not sweep_applies((64, 64), 8, 1, 2, 1)            # two axes
+    assert not sweep_applies((500, 64, 64), 8, 1, 2, 1)       # lines too long
+    assert not sweep_applies((256, 64, 64), 16, 2, 4, 2)      # faces beyond the LDS
+    with pytest.raises(ValueError):
+        sweep_geometry((8, 8, 8), 32, 1, 1, 1)
+
+    module = demo_source("sptrsv", "sptrsv_csc_loop")
+    shape = (40, 20, 28, 8, 1, 2, 1)
+    threads = sweep_geometry(shape[:3], *shape[3:])["threads"]
+    result = lower(module, execution_mode="sync_free",
+                   thread_loop_iterator="j", task_lanes=4,
+                   wavefront_threads_per_block=threads,
+                   dependence_protocol="mailbox", grid_sweep=shape)
+    assert result.grid_sweep["nx"] == 40 and result.grid_sweep["components"] == 6
+    assert not result.band_walker and not result.level_walker
+    assert result.kernel_arguments[6:11] == list(SWEEP_ARGUMENTS)
+    # the matrix array is staged when its contents change, the right-hand
+    # side in front of every solve
+    assert result.sweep_static_arrays == ("Ax",) and result.sweep_dynamic
+    assert result.sweep_kernels == (
+        "sptrsv_csc_loop_hip_sweep_static", "sptrsv_csc_loop_hip_sweep_dynamic",
+        "sptrsv_csc_loop_hip_sweep_unstage")
+    kernel = result.kernel_source
+    # the task: three products in the order of the sequential loop (sources
+    # ascending: z, y, x), then the loop's own text over the staged node loads
+    order = [kernel.index(f"_g_value = {value};")
+             for value in ("_s_vz", "_s_vy", "_s_prev")]
+    assert order == sorted(order)
+    assert "_lcd_own_0 = _lcd_own_0 + (_g_operand_0 * _g_value);" in kernel
+    assert "_lcd_own_0 = _lcd_wdiv((_nl_0 - _lcd_own_0), _nl_2, _lcd_wr);" in kernel
+    assert "return lcd_div_checked(a, d, r);" in kernel
+    # nothing of the solution is polled in memory by a sweeping wavefront and
+    # nothing is added atomically; a missing entry is the neutral product
+    assert "lcd_atomic" not in kernel
+    assert "_s_c[k] = -0.0;" in kernel
+    assert "if (k < 0) _lcd_status[0] = 3; else _s_c[k] = Ax[_g_pos];" in kernel
+    assert "_s_rec[257] = _s_tile[0][st][lane];" in kernel      # b: pair 2, second half
+    assert "if (active) x[i] = _s_tile[st][lane];" in kernel
+    launcher = result.launcher_source
+    assert launcher.count("_hip.launch(") == 4 and "_hip_reset" not in launcher
+    assert "def sptrsv_csc_loop_hip_sweep_restage(_hip, " in launcher
+    hip_runtime.compile_code(result.source)
+
+    # a workgroup of another size than the sweep's, or a task whose tail is
+    # more than arithmetic over its node loads, is refused
+    with pytest.raises(HIPLoweringError, match="grid sweep"):
+        lower(module, execution_mode="sync_free", thread_loop_iterator="j",
+              task_lanes=4, wavefront_threads_per_block=256,
+              dependence_protocol="mailbox", grid_sweep=shape)
+    rooted = ast.parse(textwrap.dedent("""
+        def solve(Ap, Ai, Ax, b, n):
+            x = np.zeros(n)
+            for i in range(n):
+                x[i] = np.sqrt(b[i] - x[i]) / Ax[Ap[i]]
+                for j in range(Ap[i] + 1, Ap[i + 1]):
+                    x[Ai[j]] += Ax[j] * x[i]
+            return x
+    """))
+    with pytest.raises(HIPLoweringError):
+        lower(rooted, execution_mode="sync_free", thread_loop_iterator="j",
+              task_lanes=4, wavefront_threads_per_block=threads,
+              dependence_protocol="mailbox", grid_sweep=shape)
+
+
 def test_tiles_addressed_by_queue_position():
     """Tiles that do not follow the ids (boxes of a grid): sources, LDS slots
     and the value-as-flag copy are addressed by the place in the queue."""
