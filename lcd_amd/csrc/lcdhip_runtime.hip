@@ -61,7 +61,17 @@ struct lcdhip_graph {
 
 extern "C" const char *lcdhip_last_error(void) { return lcdhip::g_error.c_str(); }
 
-extern "C" const char *lcdhip_version(void) { return "lcdhip 0.1 (gfx950)"; }
+extern "C" const char *lcdhip_version(void)
+{
+    // (with the version of the run-time compiler: what a code object that is
+    // kept between processes has to be keyed by)
+    static char text[96];
+    int major = 0, minor = 0;
+    if (hiprtcVersion(&major, &minor) != HIPRTC_SUCCESS) major = minor = 0;
+    snprintf(text, sizeof(text), "lcdhip 0.2 (gfx950; hiprtc %d.%d; HIP %d.%d.%d)", major, minor,
+             HIP_VERSION_MAJOR, HIP_VERSION_MINOR, HIP_VERSION_PATCH);
+    return text;
+}
 
 extern "C" int lcdhip_device_count(int *count)
 {

@@ -75,6 +75,8 @@ from lcd_amd.scheduler import (
     automatic_tile_box,
     band_walker_applies,
     level_walker_records,
+    sequential_advice,
+    SchedulerAdvice,
     automatic_tile_rows,
     structured_grid,
     automatic_tile_threads,
@@ -301,6 +303,7 @@ def parallel(**kwargs):
                     level_walker=level,
                     grid_sweep=sweep,
                     prepared_division=kwargs.get("prepared_division", True),
+                    watchdog_seconds=kwargs.get("watchdog_seconds"),
                     full_fences=kwargs.get("full_fences", False),
                     dynamic_fetch=kwargs.get("dynamic_fetch", False),
                 )
@@ -713,6 +716,16 @@ def parallel(**kwargs):
                 trip_counter["probe"], host_values, argument_names,
                 sample_limit=TRIP_PROBE_SAMPLE)
 
+        def advise(dag, band_walker):
+            """The scheduler's word on a plan that belongs on the host, as
+            one warning when the plan is made and as ``plan.advice``."""
+            advice = sequential_advice(dag, band_walker)
+            if advice is not None and kwargs.get("advice", True):
+                import warnings
+                warnings.warn(f"@parallel({function.__name__}): {advice}.",
+                              SchedulerAdvice, stacklevel=4)
+            return advice
+
         def create_schedule_plan(dag_values):
             device = get_device()
             # structure arrays go to HBM once per plan and stay there
@@ -748,12 +761,29 @@ def parallel(**kwargs):
                       and walker_option != True
                       else walker_for(dag, schedule))
             if walker is not None:
-                schedule, lowering = walker
+                walker_dag = dag
                 if not incoming_positions:
                     # (a pull-shaped loop: the walker reads the rows through
                     # the incoming listing, which this DAG was built without)
-                    dag = build_device_dag(dag_plan, device_values, device,
-                                           levels=True, incoming=True)
+                    walker_dag = build_device_dag(
+                        dag_plan, device_values, device, levels=True,
+                        incoming=True)
+                # the walker's table has one cell per (source, destination): a
+                # structure that stores two entries for the same pair keeps
+                # the executors that take every entry
+                listed = walker_dag.array("in_src").shape[0]
+                if listed != walker_dag.edges:
+                    if walker_option is True:
+                        raise ValueError(
+                            "band_walker=True: the structure stores "
+                            f"{listed - walker_dag.edges} entries beside "
+                            "another entry of the same pair of iterations, "
+                            "which the walker's table has no cell for.")
+                    walker = None
+                else:
+                    dag = walker_dag
+            if walker is not None:
+                schedule, lowering = walker
                 execution_data = execution_data_from_device_dag(
                     dag, schedule.execution_mode, lowering.warp_mapped,
                     band_width=band_width, mailbox=True, tile_rows=None,
@@ -764,7 +794,7 @@ def parallel(**kwargs):
                         execution_data, lookup_values),
                     features=features, dag=dag, tile_rows=None,
                     single_chunk=False, task_records=False,
-                    band_walker=True)
+                    band_walker=True, advice=advise(dag, True))
                 plan_state[id(plan)] = {"resident": resident, "workspace": {}}
                 return plan
             sweep = sweep_for(
@@ -864,7 +894,8 @@ def parallel(**kwargs):
                 single_chunk=bool(lowering.task_record_lanes)
                 and getattr(dag, "record_overflow", 1) == 0,
                 task_records=records, tile_boxes=tile_boxes,
-                segment_registers=segment_registers)
+                segment_registers=segment_registers,
+                advice=advise(dag, False))
             plan_state[id(plan)] = {"resident": resident, "workspace": {}}
             return plan
 

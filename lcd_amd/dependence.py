@@ -191,6 +191,10 @@ class DependenceAnalysis:
     reduction_dependences: list = field(default_factory=list)
     reductions: dict = field(default_factory=dict)
     raw_dependences: list = field(default_factory=list)
+    # reader-before-writer orderings kept beside the RAW ones (the reference
+    # enumerates RAW only, compiler/legality_check.py:226-258): a task that
+    # reads what a later task overwrites must come first here too
+    war_dependences: list = field(default_factory=list)
     statement_ids: dict = field(default_factory=dict)   # (line, col) -> "Sk"
     conservative: bool = False    # a NextRule stands in for a kept candidate
 
@@ -348,9 +352,63 @@ def number_statements(function):
     return {location: f"S{k}" for k, location in enumerate(found)}
 
 
+def unique_loop_iterators(function, block_iterator):
+    """A copy of ``function`` in which every ``for`` loop binds a name of its
+    own: a loop that binds a name an earlier loop has bound gets a fresh one
+    (``p`` -> ``p__2``), in its body and in everything that follows it in
+    program order until the name is bound again.  The analysis keeps what it
+    knows of a loop (its range, its break tests, the value its search
+    matches) under the iterator's name, and two accesses spelled alike are
+    the same element of the same iteration only when the same loop binds
+    their iterator; with one name per loop both hold by construction.  The
+    block iterator keeps its name, and so does the first loop over each other
+    name (the thread-mapped loop is found by its name later)."""
+    function = deepcopy(function)
+    bound, counter = set(), {}
+
+    class Rename(ast.NodeTransformer):
+        def __init__(self, mapping):
+            self.mapping = mapping
+
+        def visit_Name(self, node):
+            if node.id in self.mapping:
+                return ast.copy_location(
+                    ast.Name(id=self.mapping[node.id], ctx=node.ctx), node)
+            return node
+
+    def walk(statements, mapping):
+        for statement in statements:
+            if isinstance(statement, ast.For):
+                statement.iter = Rename(mapping).visit(statement.iter)
+                target = statement.target
+                if isinstance(target, ast.Name):
+                    name = target.id
+                    if name != block_iterator and name in bound:
+                        counter[name] = counter.get(name, 1) + 1
+                        mapping[name] = f"{name}__{counter[name]}"
+                    else:
+                        mapping.pop(name, None)
+                    bound.add(name)
+                    statement.target = Rename(mapping).visit(target)
+                else:
+                    statement.target = Rename(mapping).visit(target)
+                walk(statement.body, mapping)
+                walk(statement.orelse, mapping)
+            elif isinstance(statement, (ast.If, ast.While)):
+                statement.test = Rename(mapping).visit(statement.test)
+                walk(statement.body, mapping)
+                walk(statement.orelse, mapping)
+            else:
+                Rename(mapping).visit(statement)
+
+    walk(function.body, {})
+    return function
+
+
 class _Analyzer:
     def __init__(self, function, block_iterator, function_props,
                  strict=False):
+        function = unique_loop_iterators(function, block_iterator)
         self.function = function
         self.block = block_iterator
         self.strict = strict
@@ -714,6 +772,28 @@ class _Analyzer:
         return ("kept", f"write {write_kind[0]} / read {read_kind[0]} has no "
                 "enumerable rule", None, "RAW")
 
+    def _anti_rule(self, array, write_kind, read_kind):
+        """The rule that keeps a reader ahead of the later task that
+        overwrites what it reads, for the two shapes whose RAW direction is
+        refuted because the element lies BEHIND the reader: a read of the
+        segments of ``range(i + c, n)`` against a write of the own segment
+        (reader i before every task it visits), and a read of ``X[I[p]]``
+        over a triangular segment against a write of ``X[i]`` (reader i
+        before task ``I[p]``).  None for every other pair."""
+        own = ("self", "own_position")
+        if write_kind[0] in own and read_kind[0] == "later_position":
+            return self._later_rule(read_kind[1], array)
+        if write_kind == ("self",) and read_kind[0] == "indirect":
+            segment = self.segments[read_kind[2]]
+            if ((segment.pointer_array, read_kind[1]) in self.triangular
+                    and segment.lower_offset >= 1
+                    and not segment.lower_is_position):
+                try:
+                    return self._rule(True, read_kind[1], read_kind[2], array)
+                except DependenceAnalysisError:
+                    return None
+        return None
+
     def run(self):
         loop = find_block_loop(self.function, self.block)
         if (isinstance(loop.iter, ast.Call) and loop.iter.args
@@ -799,7 +879,7 @@ class _Analyzer:
                         f"({operator}=)")
 
         # stages 2 and 3
-        raw, rules, conservative = [], [], False
+        raw, war, rules, conservative = [], [], [], False
         for array, write_kind, statement, is_update, target in (
                 last_writes.values()):
             for read_array, read_kind, node, reader in selected:
@@ -826,6 +906,18 @@ class _Analyzer:
                     reason=reason, rule=rule))
                 if rule is not None and rule not in rules:
                     rules.append(rule)
+                if verdict == "refuted":
+                    anti = self._anti_rule(array, write_kind, read_kind)
+                    if anti is not None:
+                        war.append(RawDependence(
+                            array=array, from_statement_id=sid(reader),
+                            to_statement_id=sid(statement),
+                            write_index=text(target), read_index=text(node),
+                            kind="WAR", verdict="kept",
+                            reason="the reader comes before the task that "
+                                   "overwrites the element", rule=anti))
+                        if anti not in rules:
+                            rules.append(anti)
         if any(isinstance(rule, NextRule) for rule in rules):
             # the chain already orders everything
             rules = [rule for rule in rules if isinstance(rule, NextRule)][:1]
@@ -835,6 +927,7 @@ class _Analyzer:
             reduction_dependences=reduction_rules,
             reductions=reductions,
             raw_dependences=raw,
+            war_dependences=war,
             statement_ids=dict(self.statement_ids),
             conservative=conservative,
         )

@@ -325,6 +325,10 @@ class BandWalkerMixin:
         start = (f"_w_uni[(_w_m + 1) & 3][_w_lane][{uniform}]" if head_lines
                  else "0.0")
 
+        minus_zero = (
+            f" || __double_as_longlong({register}) == (long long)0x8000000000000000ull"
+            if head_lines else "")
+
         def put(name, kind, where):
             return (f"{where} = (double){name};" if kind == INT
                     else f"{where} = {name};")
@@ -414,9 +418,13 @@ class BandWalkerMixin:
             f"            if ({it} < _w_n) {{",
             *body(stage_lines, p4),
             *body(head_lines, p4),
+            # (a block with a divisor the prepared reciprocal does not serve,
+            # or -- pull-shaped loops -- with an element that starts as -0.0,
+            # which the product of an empty cell would turn into +0.0, runs
+            # again with the general division and the products of real edges)
             *([f"{p4}_lcd_wr = lcd_div_prepare({division});",
-               f"{p4}_w_odd[m & 3][l] = !lcd_div_plain_divisor({division});"]
-              if division else [f"{p4}_w_odd[m & 3][l] = 0;"]),
+               f"{p4}_w_odd[m & 3][l] = !lcd_div_plain_divisor({division}){minus_zero};"]
+              if division else [f"{p4}_w_odd[m & 3][l] = 0{minus_zero};"]),
             *[p4 + put(name, kind, f"_w_uni[m & 3][l][{k}]")
               for k, (name, kind) in enumerate(slots)],
             "            }",
@@ -472,7 +480,8 @@ class BandWalkerMixin:
              f"|| !lcd_div_plain_quotient("
              f"{'_lcd_wout' if own_is_quotient else '_lcd_wq'}) "
              "|| !lcd_finite(_lcd_wout)) != 0ull;" if division else
-             "            _w_again = _w_again || __ballot(!lcd_finite(_lcd_wout)) != 0ull;"),
+             "            _w_again = _w_again || __ballot(_w_odd[ub][_w_lane] != 0 "
+             "|| !lcd_finite(_lcd_wout)) != 0ull;"),
             "            if (_w_again) {",
             "                // the general division, and the products of real edges only",
             f"                {register} = _w_acc0;",

@@ -158,6 +158,10 @@ class HIPLoweringResult:
     # tiled persistent executor: block-iterator values per tile, or None
     tile_rows: int | None = None
     spin_limit: int = DEFAULT_SPIN_LIMIT   # watchdog limit the caller chose
+    # time budget of one launch of a persistent executor in seconds: None =
+    # from the depth and size of the DAG, 0 = none (the poll count still ends
+    # a wait that cannot end)
+    watchdog_seconds: float | None = None
 
     @property
     def module_source(self):

@@ -112,8 +112,10 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                  dynamic_fetch=False, tile_positions=None,
                  tile_by_position=False, segment_registers=False,
                  pair_tables=True, band_walker=False, level_walker=0,
-                 prepared_division=True, grid_sweep=None):
+                 prepared_division=True, grid_sweep=None,
+                 watchdog_seconds=None):
         self.tile_positions = tile_positions
+        self.watchdog_seconds = watchdog_seconds
         # (nx, ny, nz, WY, GY, GZ, SKZ): the grid sweep over this grid
         self.grid_sweep = tuple(grid_sweep) if grid_sweep else None
         self._sweep = None
@@ -600,6 +602,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                                    and self._segment.get("registers")),
             structure_tables=tuple(self._structure_tables),
             spin_limit=self.spin_limit,
+            watchdog_seconds=self.watchdog_seconds,
             queue_node_loads=tuple(self._queue_node_loads),
             published_array=(self._published["array"]
                              if self._published else None),
@@ -1689,7 +1692,8 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
                  pipeline_fetch=True, full_fences=False, dynamic_fetch=False,
                  tile_positions=None, tile_by_position=False,
                  segment_registers=False, pair_tables=True, band_walker=False,
-                 level_walker=0, prepared_division=True, grid_sweep=None):
+                 level_walker=0, prepared_division=True, grid_sweep=None,
+                 watchdog_seconds=None):
     """HIP counterpart of ``lower_to_numba_cuda``
     (compiler/cuda_lowering.py:2854-2884); same parameters plus
     ``task_lanes`` (lanes cooperating on one task, a power of two <= 64),
@@ -1720,5 +1724,6 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
         tile_by_position=tile_by_position,
         segment_registers=segment_registers, pair_tables=pair_tables,
         band_walker=band_walker, level_walker=level_walker,
-        prepared_division=prepared_division, grid_sweep=grid_sweep)
+        prepared_division=prepared_division, grid_sweep=grid_sweep,
+        watchdog_seconds=watchdog_seconds)
     return lowerer.lower(code)

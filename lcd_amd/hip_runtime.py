@@ -175,11 +175,104 @@ def _check(status):
         raise HIPRuntimeError(message, status)
 
 
+_hook_notices = set()
+
+
+def _warn_hook(variable, what):
+    """One warning per process and developer hook that takes effect: the
+    kernels that run are then not the ones this package generates."""
+    if variable in _hook_notices:
+        return
+    _hook_notices.add(variable)
+    import warnings
+    warnings.warn(f"lcd_amd: {variable} is set: {what}", RuntimeWarning,
+                  stacklevel=3)
+
+
+def code_cache_directory():
+    """Where compiled code objects are kept between processes, or None when
+    the cache is switched off (``LCD_HIP_CACHE=0``): ``LCD_HIP_CACHE_DIR``,
+    else ``$XDG_CACHE_HOME/lcd_amd/hiprtc`` (``~/.cache`` by default)."""
+    if os.environ.get("LCD_HIP_CACHE", "1").strip().lower() in (
+            "0", "off", "no", "false"):
+        return None
+    chosen = os.environ.get("LCD_HIP_CACHE_DIR")
+    if chosen:
+        return chosen
+    base = os.environ.get("XDG_CACHE_HOME") or os.path.join(
+        os.path.expanduser("~"), ".cache")
+    return os.path.join(base, "lcd_amd", "hiprtc")
+
+
+_CACHE_MAGIC = b"LCDHIPCO1\n"
+
+
+def _cache_path(lib, source, opts):
+    directory = code_cache_directory()
+    if directory is None:
+        return None
+    key = hashlib.sha256()
+    for part in (lib.lcdhip_version(), b"\0".join(opts), source.encode()):
+        key.update(len(part).to_bytes(8, "little"))
+        key.update(part)
+    return os.path.join(directory, key.hexdigest() + ".co")
+
+
+def _cache_read(path):
+    """The code object kept under ``path``, or None: no such entry, or one
+    that is not whole (the payload carries its own SHA-256)."""
+    try:
+        with open(path, "rb") as handle:
+            blob = handle.read()
+    except OSError:
+        return None
+    head = len(_CACHE_MAGIC)
+    if len(blob) < head + 32 or blob[:head] != _CACHE_MAGIC:
+        return None
+    digest, code = blob[head:head + 32], blob[head + 32:]
+    if hashlib.sha256(code).digest() != digest or not code:
+        return None
+    return code
+
+
+def _cache_write(path, code):
+    """Atomically (write beside, rename); a cache that cannot be written is
+    no error."""
+    try:
+        os.makedirs(os.path.dirname(path), exist_ok=True)
+        temporary = f"{path}.{os.getpid()}.tmp"
+        with open(temporary, "wb") as handle:
+            handle.write(_CACHE_MAGIC + hashlib.sha256(code).digest() + code)
+        os.replace(temporary, path)
+    except OSError:
+        pass
+
+
+code_cache_statistics = {"hits": 0, "misses": 0}
+
+
 def compile_code(source, name="lcd_generated.hip", options=()):
-    """hiprtc-compile HIP source for gfx950; works without a GPU."""
+    """hiprtc-compile HIP source for gfx950; works without a GPU.
+
+    The code object is kept on disk under a key of the source text, every
+    option, the target and the versions of this library and of hiprtc, and
+    loaded from there by the next process (the reference keeps its compiled
+    variants for the life of one process, compiler/decorator.py:201-245;
+    hiprtc takes 0.1-0.3 s per kernel).  ``code_cache_directory`` says where
+    and how to switch it off."""
     lib = load_library()
     extra = tuple(os.environ.get("LCD_HIP_EXTRA_OPTIONS", "").split())
+    if extra:
+        _warn_hook("LCD_HIP_EXTRA_OPTIONS",
+                   f"every kernel is compiled with the extra options {extra}.")
     opts = [o.encode() for o in (*DEVICE_COMPILE_OPTIONS, *options, *extra)]
+    cached = _cache_path(lib, source, opts)
+    if cached is not None:
+        data = _cache_read(cached)
+        if data is not None:
+            code_cache_statistics["hits"] += 1
+            return data, ""
+    code_cache_statistics["misses"] += 1
     array = (ctypes.c_char_p * len(opts))(*opts)
     code, size, log = ctypes.c_void_p(), ctypes.c_size_t(), ctypes.c_char_p()
     status = lib.lcdhip_module_compile_code(
@@ -194,6 +287,8 @@ def compile_code(source, name="lcd_generated.hip", options=()):
             f"Failed to compile the generated HIP module {name}:\n{message}")
     data = ctypes.string_at(code, size.value)
     lib.lcdhip_free_host(code)
+    if cached is not None:
+        _cache_write(cached, data)
     return data, log_text
 
 
@@ -838,6 +933,9 @@ class CompiledHIPModule:
             if override:
                 path = os.path.join(override, self.lowering.kernel_name + ".hip")
                 if os.path.exists(path):
+                    _warn_hook("LCD_HIP_OVERRIDE_DIR",
+                               f"the text of {path} replaces the generated "
+                               f"kernel {self.lowering.kernel_name}.")
                     with open(path) as handle:
                         source = handle.read()
             digest = hashlib.blake2b(
@@ -1058,13 +1156,21 @@ def watchdog_budget(lowering, execution_data):
     """Time budget of one launch of a persistent executor for this plan, in
     units of 2^20 ticks of the 100 MHz wall clock (about 10.5 ms): two
     seconds plus 8 us per level of the DAG (per node for chain tasks, which
-    run their members one after the other), at most five minutes.  A stuck
+    run their members one after the other) plus 0.1 us per task (a wide DAG
+    of few levels takes its time too), at most five minutes.  A stuck
     schedule on a DAG of a few hundred levels then gives up after two seconds
     instead of the twenty-odd the poll count alone took, and a chain of
     millions of levels, whose launch legitimately runs for seconds, keeps
-    the time it needs.  0 (= poll count only) when the caller chose
-    ``spin_limit`` or the depth is not known."""
+    the time it needs.  ``watchdog_seconds`` of the lowering replaces the
+    figure (a GPU shared with other work wants more); 0 there, a
+    ``spin_limit`` the caller chose, or an unknown depth give 0: no time
+    budget, the poll count alone ends a wait that cannot end."""
     from lcd_amd.hip_emitter import DEFAULT_SPIN_LIMIT
+    chosen = getattr(lowering, "watchdog_seconds", None)
+    if chosen is not None:
+        if chosen <= 0:
+            return 0
+        return int(min(float(chosen), 3600.0) * 1.0e8 / WATCHDOG_UNIT_TICKS) + 1
     if getattr(lowering, "spin_limit", DEFAULT_SPIN_LIMIT) != DEFAULT_SPIN_LIMIT:
         return 0
     bands = getattr(execution_data, "band_ptr", None)
@@ -1074,12 +1180,13 @@ def watchdog_budget(lowering, execution_data):
         depth = len(bands) - 1
         nodes = getattr(execution_data, "task_nodes", None)
         chains = getattr(execution_data, "task_ptr", None)
+        tasks = len(nodes) if nodes is not None else 0
         if (nodes is not None and chains is not None
                 and len(chains) - 1 != len(nodes)):
             depth = len(nodes)
     except TypeError:
         return 0
-    seconds = min(2.0 + 8.0e-6 * max(depth, 0), 300.0)
+    seconds = min(2.0 + 8.0e-6 * max(depth, 0) + 1.0e-7 * max(tasks, 0), 300.0)
     return int(seconds * 1.0e8 / WATCHDOG_UNIT_TICKS) + 1
 
 

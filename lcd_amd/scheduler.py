@@ -168,6 +168,9 @@ class SchedulePlan:
     level_walker: int = 0
     # the grid sweep: (nx, ny, nz, WY, GY, GZ, SKZ), or None
     grid_sweep: tuple | None = None
+    # what the scheduler has to say about the plan beyond the schedule (a
+    # DAG that belongs on the host), or None
+    advice: str | None = None
 
 
 # Grid sweep, automatic choice (WY, GY, GZ, SKZ): bundles of 8 x 8 grid lines
@@ -264,6 +267,49 @@ PUBLISHED_TILE_MIN_LOCALITY = 0.2
 BAND_WALKER_TASKS_PER_LEVEL = 6
 BAND_WALKER_SPAN = 64
 BAND_WALKER_THREADS_PER_BLOCK = 1024
+
+
+class SchedulerAdvice(UserWarning):
+    """The plan will run, but the scheduler expects another place to be
+    faster (see ``SchedulePlan.advice``)."""
+
+
+# A DAG that is close to a chain has nothing to run in parallel: the GPU pays
+# its per-task cost in sequence -- 0.06 us on the band walker (143 cycles: the
+# dependent arithmetic of a row and what one wavefront issues beside it),
+# 0.43 us per level in tiles when an edge is too long for the walker -- where
+# one host core runs the compiled loop at about 1.2 ns per stored entry (the
+# single-threaded C restatement: 30 ms for the 4 M-row band of width 8,
+# against 250 ms on the walker).  The estimates only have to tell 8 x apart.
+BAND_WALKER_SECONDS_PER_TASK = 6.0e-8
+TILED_SECONDS_PER_LEVEL = 4.3e-7
+HOST_LOOP_SECONDS_PER_ENTRY = 1.2e-9
+HOST_LOOP_SECONDS_PER_TASK = 2.0e-9
+SEQUENTIAL_ADVICE_MIN_TASKS = 10000
+
+
+def sequential_advice(dag, band_walker=False):
+    """Text for ``SchedulePlan.advice`` when the DAG is so close to a chain
+    (fewer than BAND_WALKER_TASKS_PER_LEVEL tasks per level) that a compiled
+    sequential loop on one host core is expected to beat the GPU, else None.
+    The plan still runs on the GPU: the caller may have its data there."""
+    levels = int(getattr(dag, "levels", 0) or 0)
+    if (dag.n < SEQUENTIAL_ADVICE_MIN_TASKS
+            or levels * BAND_WALKER_TASKS_PER_LEVEL <= dag.n):
+        return None
+    device = (dag.n * BAND_WALKER_SECONDS_PER_TASK if band_walker
+              else levels * TILED_SECONDS_PER_LEVEL)
+    host = (dag.n * HOST_LOOP_SECONDS_PER_TASK
+            + (dag.edges + dag.n) * HOST_LOOP_SECONDS_PER_ENTRY)
+    if device <= 2.0 * host:
+        return None
+    return (
+        f"the dependence DAG is close to a chain ({levels} levels for "
+        f"{dag.n} iterations): nothing runs in parallel, and the GPU is "
+        f"expected to take about {device * 1e3:.3g} ms per call "
+        f"({'one wavefront in program order' if band_walker else 'one hand-off per level'}"
+        f") where a compiled sequential loop on one host core takes about "
+        f"{host * 1e3:.3g} ms; the call runs on the GPU all the same")
 
 
 def band_walker_applies(dag, forced=False):

@@ -1692,3 +1692,154 @@ def test_unrecognised_dependence_is_kept_as_the_complete_order():
     assert chain.successors() == dag and chain.levels == 5
     assert lcd_oracle.literal_extract_dag(lcd_oracle.rule_next(2), 5)[0] == [
         [2], [3], [4], [], []]
+
+
+def test_a_reused_iterator_name_and_a_reader_before_its_writer():
+    """Two accesses spelled alike are the same element of the same iteration
+    only when the same loop binds their iterator: ILU0 with the diagonal
+    search and the update loop both written over ``j_ptr`` (legal Python)
+    keeps the rule of the loop as the reference spells it.  And a task that
+    reads what a later task overwrites stays ahead of it, although the
+    reference enumerates RAW dependences only
+    (compiler/legality_check.py:226-258)."""
+    import inspect
+    from lcd_amd.demo import spilu0, sptrsv
+    from lcd_amd.dependence import LaterRule, SegmentRule, unique_loop_iterators
+    source = textwrap.dedent(inspect.getsource(spilu0.ilu0_csr))
+    original = analyze_dependences(ast.parse(source), "i", spilu0.FUNCTION_PROPS)
+    reused = source.replace("diag_ptr", "j_ptr")
+    assert reused != source
+    analysis = analyze_dependences(ast.parse(reused), "i", spilu0.FUNCTION_PROPS)
+    assert not analysis.conservative
+    assert analysis.ordering_dependences == original.ordering_dependences
+    assert isinstance(analysis.ordering_dependences[0], SegmentRule)
+    kept = [d for d in analysis.raw_dependences if d.verdict == "kept"]
+    assert len(analysis.raw_dependences) == 6 and len(kept) == 2
+    renamed = unique_loop_iterators(ast.parse(reused).body[0], "i")
+    targets = [node.target.id for node in ast.walk(renamed)
+               if isinstance(node, ast.For)]
+    assert sorted(targets) == ["i", "j_ptr", "j_ptr__2", "k_ptr", "kj_ptr"]
+
+    probe = ast.parse(textwrap.dedent("""
+        def scale(Ap, Ax, n):
+            for i in range(n):
+                total = 0.0
+                for k in range(i + 1, n):
+                    for q in range(Ap[k], Ap[k + 1]):
+                        total = total + Ax[q]
+                for p in range(Ap[i], Ap[i + 1]):
+                    Ax[p] = Ax[p] * 2.0 + total
+    """))
+    analysis = analyze_dependences(probe, "i",
+                                   {"Ap": ["monotonically_increasing"]})
+    assert not analysis.conservative
+    assert [type(rule) for rule in analysis.ordering_dependences] == [LaterRule]
+    assert all(d.verdict == "refuted" for d in analysis.raw_dependences)
+    assert [d.kind for d in analysis.war_dependences] == ["WAR"]
+    # the demo loops keep the rules the reference's tests record: their
+    # reader-before-writer pairs are ordered by a RAW rule already
+    for function, props, iterator, count in (
+            (sptrsv.sptrsv_csc_loop, sptrsv.FUNCTION_PROPS_CSC, "i", 1),
+            (spilu0.ilu0_csc, spilu0.FUNCTION_PROPS, "k", 2)):
+        analysis = analyze_dependences(
+            ast.parse(textwrap.dedent(inspect.getsource(function))), iterator,
+            props)
+        assert len(analysis.ordering_dependences) == count
+        assert analysis.war_dependences
+        assert all(d.rule in analysis.ordering_dependences
+                   for d in analysis.war_dependences)
+
+
+def test_code_objects_are_kept_between_processes(tmp_path, monkeypatch):
+    """The on-disk cache of hiprtc output: a miss compiles and stores, the
+    next compile of the same text and options is a hit that returns the same
+    bytes, another option is another entry, a damaged entry is compiled
+    again and replaced, and LCD_HIP_CACHE=0 switches it all off."""
+    source = 'extern "C" __global__ void probe(int* out) { out[0] = 41; }\n'
+    monkeypatch.setenv("LCD_HIP_CACHE_DIR", str(tmp_path))
+    monkeypatch.delenv("LCD_HIP_CACHE", raising=False)
+    monkeypatch.delenv("LCD_HIP_EXTRA_OPTIONS", raising=False)
+    counts = hip_runtime.code_cache_statistics
+    before = dict(counts)
+    first, _ = hip_runtime.compile_code(source, "probe.hip")
+    assert counts["misses"] == before["misses"] + 1
+    entries = sorted(tmp_path.glob("*.co"))
+    assert len(entries) == 1 and first[:4] == b"\x7fELF"
+    second, _ = hip_runtime.compile_code(source, "probe.hip")
+    assert counts["hits"] == before["hits"] + 1 and second == first
+    hip_runtime.compile_code(source, "probe.hip", ("-DOTHER=1",))
+    assert len(list(tmp_path.glob("*.co"))) == 2
+    # a damaged entry (cut short, or its payload changed) is not trusted
+    blob = entries[0].read_bytes()
+    for damaged in (blob[:len(blob) // 2], blob[:-1] + bytes([blob[-1] ^ 1]),
+                    b"something else"):
+        entries[0].write_bytes(damaged)
+        misses = counts["misses"]
+        again, _ = hip_runtime.compile_code(source, "probe.hip")
+        assert counts["misses"] == misses + 1 and again == first
+        assert entries[0].read_bytes() == blob
+    # a compile error is not kept
+    with pytest.raises(hip_runtime.HIPModuleCompilationError):
+        hip_runtime.compile_code("not a kernel", "broken.hip")
+    assert len(list(tmp_path.glob("*.co"))) == 2
+    monkeypatch.setenv("LCD_HIP_CACHE", "0")
+    assert hip_runtime.code_cache_directory() is None
+    hits = counts["hits"]
+    hip_runtime.compile_code(source, "probe.hip")
+    assert counts["hits"] == hits
+    monkeypatch.delenv("LCD_HIP_CACHE_DIR")
+    monkeypatch.setenv("LCD_HIP_CACHE", "1")
+    monkeypatch.setenv("XDG_CACHE_HOME", str(tmp_path / "xdg"))
+    assert hip_runtime.code_cache_directory() == str(
+        tmp_path / "xdg" / "lcd_amd" / "hiprtc")
+
+
+def test_developer_hooks_and_watchdog_budget(tmp_path, monkeypatch):
+    """Compile hooks that change what runs say so once; the time budget of a
+    launch follows the depth and the size of the DAG unless the caller gives
+    one (0: none)."""
+    import warnings
+    from types import SimpleNamespace
+    monkeypatch.setenv("LCD_HIP_CACHE", "0")
+    monkeypatch.setenv("LCD_HIP_EXTRA_OPTIONS", "-DLCD_PROBE=1")
+    hip_runtime._hook_notices.discard("LCD_HIP_EXTRA_OPTIONS")
+    source = 'extern "C" __global__ void probe(int* out) { out[0] = LCD_PROBE; }\n'
+    with pytest.warns(RuntimeWarning, match="LCD_HIP_EXTRA_OPTIONS"):
+        hip_runtime.compile_code(source, "probe.hip")
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        hip_runtime.compile_code(source, "probe.hip")      # said once
+    monkeypatch.delenv("LCD_HIP_EXTRA_OPTIONS")
+
+    unit = 1.0e8 / hip_runtime.WATCHDOG_UNIT_TICKS
+    data = SimpleNamespace(band_ptr=np.zeros(383, np.int32),
+                           task_nodes=np.zeros(2_000_000, np.int32),
+                           task_ptr=np.zeros(2_000_001, np.int32))
+    plain = SimpleNamespace(spin_limit=1 << 22, watchdog_seconds=None)
+    seconds = hip_runtime.watchdog_budget(plain, data) / unit
+    assert 2.2 <= seconds <= 2.25          # 2 s + 382 x 8 us + 2 M x 0.1 us
+    assert hip_runtime.watchdog_budget(
+        SimpleNamespace(spin_limit=1000, watchdog_seconds=None), data) == 0
+    assert hip_runtime.watchdog_budget(
+        SimpleNamespace(spin_limit=1 << 22, watchdog_seconds=0), data) == 0
+    assert 30.0 <= hip_runtime.watchdog_budget(
+        SimpleNamespace(spin_limit=1000, watchdog_seconds=30.0), data) / unit <= 30.1
+
+
+def test_the_scheduler_says_when_the_host_would_win():
+    """A DAG close to a chain gets the advice (and, through the decorator,
+    one warning); a wide DAG, a small one, or a chain the estimates do not
+    tell apart get none."""
+    from types import SimpleNamespace
+    chain = SimpleNamespace(n=4_194_304, levels=4_194_304, edges=33_554_396)
+    advice = S.sequential_advice(chain, band_walker=True)
+    assert advice is not None and "close to a chain" in advice
+    assert "252 ms" in advice and "one wavefront in program order" in advice
+    tiled = S.sequential_advice(chain, band_walker=False)
+    assert tiled is not None and "one hand-off per level" in tiled
+    grid = SimpleNamespace(n=2_097_152, levels=382, edges=6_242_304)
+    assert S.sequential_advice(grid) is None
+    short = SimpleNamespace(n=5000, levels=5000, edges=4999)
+    assert S.sequential_advice(short, True) is None
+    assert issubclass(S.SchedulerAdvice, UserWarning)
+    assert S.SchedulePlan(schedule=None, execution_data=None).advice is None
