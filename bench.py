@@ -108,6 +108,11 @@ def elementwise_error(got, expected):
     return float(np.max(np.abs(got - expected) / (np.abs(expected) + floor)))
 
 
+def hip_runtime_module():
+    from lcd_amd import hip_runtime
+    return hip_runtime
+
+
 def build_solver(work, args, config):
     from lcd_amd.demo import spilu0, sptrsv
     options = {} if args.auto else dict(TUNED[config])
@@ -219,24 +224,95 @@ def cpu_baseline(work, seconds):
     }
 
 
-def python_loop_baseline(work, rows):
-    """The undecorated Python loop on the leading ``rows`` tasks."""
-    rows = min(rows, work.n)
-    ptr = work.indptr[:rows + 1].tolist()
-    if work.kind != "sptrsv_csc":
-        return None
-    idx, val, rhs = work.indices.tolist(), work.data.tolist(), work.rhs.tolist()
-    x = [0.0] * work.n
+PYTHON_LOOP_SECONDS = 1.5
+
+
+def python_loop_baseline(work, seconds=PYTHON_LOOP_SECONDS):
+    """The undecorated Python loop of the configuration (README.md:85-92,
+    compiler/demo/sptrsv.py:26-43, compiler/demo/spilu0.py:21-47, the loops
+    the reference's own end-to-end tests run on the host,
+    compiler/e2e_tests/test_spilu0_e2e.py:19-70) on the leading tasks, for
+    about ``seconds`` on one core, projected to the whole problem by the
+    entries visited (the cost per entry does not change along these
+    structures).  Lists instead of arrays: the loop a user would write over
+    NumPy arrays is several times slower still."""
+    n = work.n
+    ptr, idx = work.indptr.tolist(), work.indices.tolist()
+    val = work.data.tolist()
+    deadline = time.perf_counter() + seconds
     start = time.perf_counter()
-    for i in range(rows):
-        x[i] = (rhs[i] - x[i]) / val[ptr[i]]
-        for j in range(ptr[i] + 1, ptr[i + 1]):
-            x[idx[j]] += val[j] * x[i]
+    rows = 0
+    if work.kind == "sptrsv_csc":
+        rhs = work.rhs.tolist()
+        x = [0.0] * n
+        for i in range(n):
+            x[i] = (rhs[i] - x[i]) / val[ptr[i]]
+            for j in range(ptr[i] + 1, ptr[i + 1]):
+                x[idx[j]] += val[j] * x[i]
+            rows = i + 1
+            if (i & 1023) == 0 and time.perf_counter() > deadline:
+                break
+    elif work.kind == "sptrsv_csr":
+        rhs = work.rhs.tolist()
+        x = [0.0] * n
+        for i in range(n):
+            x[i] = rhs[i]
+            for j in range(ptr[i], ptr[i + 1] - 1):
+                x[i] -= val[j] * x[idx[j]]
+            x[i] /= val[ptr[i + 1] - 1]
+            rows = i + 1
+            if (i & 1023) == 0 and time.perf_counter() > deadline:
+                break
+    else:
+        for i in range(n):
+            row_start, row_end = ptr[i], ptr[i + 1]
+            for k_ptr in range(row_start, row_end):
+                k = idx[k_ptr]
+                if k >= i:
+                    break
+                diag_val = 0.0
+                for diag_ptr in range(ptr[k], ptr[k + 1]):
+                    if idx[diag_ptr] == k:
+                        diag_val = val[diag_ptr]
+                        break
+                if diag_val != 0.0:
+                    val[k_ptr] = val[k_ptr] / diag_val
+                    l_ik = val[k_ptr]
+                    for j_ptr in range(k_ptr + 1, row_end):
+                        j = idx[j_ptr]
+                        for kj_ptr in range(ptr[k], ptr[k + 1]):
+                            if idx[kj_ptr] == j:
+                                val[j_ptr] = val[j_ptr] - l_ik * val[kj_ptr]
+                                break
+            rows = i + 1
+            if (i & 255) == 0 and time.perf_counter() > deadline:
+                break
     elapsed = time.perf_counter() - start
-    return {"rows": rows, "seconds": round(elapsed, 4),
-            "projected_full_solve_ms": round(elapsed / rows * work.n * 1e3, 1),
-            "note": "CPython list-based restatement of the README loop, "
-                    "one core; numba is not installed on this image"}
+    entries = max(ptr[rows], 1)
+    return {"rows": rows, "entries": entries, "seconds": round(elapsed, 4),
+            "cores": 1,
+            "projected_full_ms": round(elapsed / entries * ptr[n] * 1e3, 1),
+            "note": "the undecorated loop in CPython over lists, one core, "
+                    f"leading {rows} of {n} iterations, projected by entries; "
+                    "numba is not installed on this image"}
+
+
+def latency_bounds(levels, arch):
+    """What the dependences alone cost, in ms: ``levels`` dependent tasks one
+    after the other with the hand-off free (``registers``: the chain of
+    fp64 steps measured in one lane -- a bound under every executor, the
+    walkers and the grid sweep included), with the hop between wavefronts of
+    one workgroup through LDS (``lds``: tiles), and with the hop between
+    workgroups through memory (``memory``: the flat queue, level launches).
+    ``bound`` is the smallest."""
+    chain = float(arch.get("chain_step_s", 0.0) or 0.0)
+    lds = float(arch.get("lds_handoff_s", 0.0) or 0.0)
+    memory = float(arch.get("handoff_s", 0.0) or 0.0)
+    bounds = {"registers": levels * chain * 1e3,
+              "lds": levels * (chain + lds) * 1e3,
+              "memory": levels * (chain + memory) * 1e3}
+    bounds["bound"] = min(bounds.values())
+    return {key: round(value, 5) for key, value in bounds.items()}
 
 
 def oracle_result(work):
@@ -250,8 +326,8 @@ def oracle_result(work):
     return lcd_oracle.ilu0_csr(work.data, work.indices, work.indptr)
 
 
-def run_configuration(config, args, device, steps, warmup, handoff_s,
-                      cpu_seconds, python_loop=False):
+def run_configuration(config, args, device, steps, warmup, arch,
+                      cpu_seconds, python_loop=True):
     """Time one configuration; returns its record (see the module text)."""
     from lcd_amd import workloads
     from lcd_amd.dag_codegen import build_device_dag
@@ -350,6 +426,9 @@ def run_configuration(config, args, device, steps, warmup, handoff_s,
             "generate_s": round(generate_s, 3), "upload_s": round(upload_s, 3),
             "inspect_compile_bind_s": round(inspect_s, 3),
             "first_call_s": round(first_call_s, 4),
+            # code objects found on disk / compiled by hiprtc so far in this
+            # process (a second process finds them all)
+            "code_cache": dict(hip_runtime_module().code_cache_statistics),
         },
     }
     # the on-device inspector alone (edges, counts, level sets and, for the
@@ -417,11 +496,18 @@ def run_configuration(config, args, device, steps, warmup, handoff_s,
         "launches_per_step": launches_per_step,
         "avg_launch_ms": round(kernel_ms, 6),
         "dependency_levels": plan.dag.levels,
-        # what the dependences alone allow: every level waits for one
-        # release->acquire hand-off between workgroups (idle-machine figure)
-        "handoff_us": round(handoff_s * 1e6, 4),
-        "latency_bound_ms": round(plan.dag.levels * handoff_s * 1e3, 5),
+        # what the dependences alone cost (see latency_bounds): the floor is
+        # the chain of dependent fp64 tasks with every hand-off free; the
+        # figures with a hop per level say what each kind of executor pays
+        "handoff_us": {"memory": round(arch["handoff_s"] * 1e6, 4),
+                       "lds": round(arch["lds_handoff_s"] * 1e6, 4),
+                       "registers": round(arch["chain_step_s"] * 1e6, 4)},
     }
+    bounds = latency_bounds(plan.dag.levels, arch)
+    record["roofline"]["latency_bound_ms"] = bounds.pop("bound")
+    record["roofline"]["latency_by_handoff_ms"] = bounds
+    record["roofline"]["latency_bound_holds"] = bool(
+        record["roofline"]["latency_bound_ms"] <= ms_per_step)
 
     if not args.no_check:
         expected = oracle_result(work)
@@ -437,11 +523,10 @@ def run_configuration(config, args, device, steps, warmup, handoff_s,
         record["parity_ok"] = bool(error <= RTOL)
         del got, expected
     if not args.no_cpu:
-        record["cpu_baseline"] = cpu_baseline(work, cpu_seconds)
+        if cpu_seconds > 0:
+            record["cpu_baseline"] = cpu_baseline(work, cpu_seconds)
         if python_loop:
-            loop = python_loop_baseline(work, 200_000)
-            if loop is not None:
-                record["cpu_python_loop"] = loop
+            record["cpu_python_loop"] = python_loop_baseline(work)
     # release the device memory of this configuration before the next one
     del call, plan, solver, operands, pristine, values, work
     gc.collect()
@@ -546,12 +631,11 @@ def main():
     from lcd_amd import hip_runtime
     device = hip_runtime.default_device()
     arch = device.measure_arch()
-    handoff_s = float(arch["handoff_s"])
 
     headline = args.config or "c2"
     everything = args.config is None
     head = run_configuration(headline, args, device, args.steps, args.warmup,
-                             handoff_s, args.cpu_seconds, python_loop=True)
+                             arch, args.cpu_seconds)
     result = {
         "metric": METRIC,
         "value": head["value"],
@@ -589,21 +673,26 @@ def main():
         records = {}
         for config in ("c1", "c2", "c3", "c4", "c5"):
             if config == headline and vars(sub_args) == vars(args):
-                records[config] = {k: v for k, v in head.items()
-                                   if k != "cpu_python_loop"}
+                records[config] = dict(head)
                 continue
             print(f"bench: {config}", file=sys.stderr, flush=True)
             steps, warmup = SUB_STEPS[config]
             records[config] = run_configuration(
-                config, sub_args, device, steps, warmup, handoff_s,
+                config, sub_args, device, steps, warmup, arch,
                 CPU_SECONDS_SUB)
         # configuration 2 under the level-launched executor, the mode
         # BASELINE.json names for it (one captured graph of `levels` launches)
         print("bench: c2 wavefront", file=sys.stderr, flush=True)
         sub_args.mode = "wavefront"
         records["c2_wavefront"] = run_configuration(
-            "c2", sub_args, device, 20, 3, handoff_s, 0.0)
-        records["c2_wavefront"].pop("cpu_baseline", None)
+            "c2", sub_args, device, 20, 3, arch, 0.0, python_loop=False)
+        # ILU0 under level launches with 128 threads per block, the mode and
+        # block size the reference's demo fixes
+        # (compiler/demo/spilu0.py:85-98)
+        print("bench: c4 wavefront", file=sys.stderr, flush=True)
+        sub_args.tpb, sub_args.lanes = 128, 4
+        records["c4_wavefront"] = run_configuration(
+            "c4", sub_args, device, 5, 1, arch, 0.0, python_loop=False)
         result["configs"] = records
         failed += [name for name, record in records.items()
                    if not record.get("parity_ok", True)]

@@ -89,6 +89,12 @@ typedef struct {
     double handoff_s;
     double barrier_s;
     double graph_node_s;
+    /* the same hop between two wavefronts of ONE workgroup through LDS, and
+     * one step of a chain of dependent fp64 tasks x = (b - c * x) / d in one
+     * lane: what a dependence costs when its hand-off is free, the floor of
+     * levels x step under every executor (no counterpart in the reference) */
+    double lds_handoff_s;
+    double chain_step_s;
 } lcdhip_arch;
 int lcdhip_measure_arch(lcdhip_arch *out);
 

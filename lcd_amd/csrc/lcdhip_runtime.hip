@@ -1048,6 +1048,44 @@ __global__ void lcdhip_handoff_probe_kernel(int32_t *flag, int32_t hops,
     }
 }
 
+// Two wavefronts of ONE workgroup hand a word back and forth through LDS: the
+// hop a dependent task pays when its producer runs in the same workgroup
+// (tiles, faces between the bundles of a grid sweep).  Every wait is bounded.
+__global__ void lcdhip_lds_handoff_probe_kernel(int32_t hops, int32_t *timed_out)
+{
+    __shared__ int32_t flag;
+    if (threadIdx.x == 0)
+        flag = 0;
+    __syncthreads();
+    const int32_t me = static_cast<int32_t>(threadIdx.x >> 6);
+    if ((threadIdx.x & 63) != 0 || me > 1)
+        return;
+    for (int32_t hop = me; hop < hops; hop += 2) {
+        int64_t spins = 0;
+        while (__hip_atomic_load(&flag, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_WORKGROUP) != hop) {
+            if (++spins > (1ll << 22)) {
+                *timed_out = 1;
+                return;
+            }
+        }
+        __hip_atomic_store(&flag, hop + 1, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+}
+
+// One wavefront runs `steps` dependent steps x = (b - c * x) / d in fp64: what
+// a chain of tasks of a triangular solve costs when every hand-off is free (a
+// register of the same lane): no executor of such a chain can be faster.
+__global__ void lcdhip_chain_probe_kernel(double *out, int32_t steps, double b,
+                                          double c, double d)
+{
+    double x = out[threadIdx.x];
+    for (int32_t step = 0; step < steps; ++step)
+        x = (b - c * x) / d;
+    out[threadIdx.x] = x;
+}
+
 // `rounds` barriers over a grid that the host sized to be fully resident.
 __global__ void lcdhip_barrier_probe_kernel(int32_t *arrive, int32_t rounds,
                                             int32_t *timed_out)
@@ -1172,6 +1210,48 @@ extern "C" int lcdhip_measure_arch(lcdhip_arch *out)
             samples.push_back(ms * 1.0e-3 / hops);
     }
     out->handoff_s = median(samples);
+
+    // the same ping-pong between two wavefronts of one workgroup, through LDS
+    samples.clear();
+    for (int repeat = 0; repeat < 4; ++repeat) {
+        LCDHIP_CHECK(hipEventRecord(start_event, stream));
+        hipLaunchKernelGGL(lcdhip_lds_handoff_probe_kernel, dim3(1), dim3(128),
+                           0, stream, hops, d_timed_out);
+        LCDHIP_CHECK(hipEventRecord(stop_event, stream));
+        LCDHIP_CHECK(hipEventSynchronize(stop_event));
+        LCDHIP_CHECK(hipEventElapsedTime(&ms, start_event, stop_event));
+        if (repeat)
+            samples.push_back(ms * 1.0e-3 / hops);
+    }
+    out->lds_handoff_s = median(samples);
+
+    // a chain of dependent fp64 steps (multiply, subtract, divide) in one lane;
+    // the launch itself is taken out with a second, shorter run
+    samples.clear();
+    {
+        double *d_chain = reinterpret_cast<double *>(d_flags);
+        const int32_t long_steps = 20000, short_steps = 2000;
+        float ms_long = 0.0f, ms_short = 0.0f;
+        for (int repeat = 0; repeat < 4; ++repeat) {
+            LCDHIP_CHECK(hipMemsetAsync(d_flags, 0, 64 * 8, stream));
+            LCDHIP_CHECK(hipEventRecord(start_event, stream));
+            hipLaunchKernelGGL(lcdhip_chain_probe_kernel, dim3(1), dim3(64), 0,
+                               stream, d_chain, long_steps, 1.0, -0.25, 6.0);
+            LCDHIP_CHECK(hipEventRecord(stop_event, stream));
+            LCDHIP_CHECK(hipEventSynchronize(stop_event));
+            LCDHIP_CHECK(hipEventElapsedTime(&ms_long, start_event, stop_event));
+            LCDHIP_CHECK(hipEventRecord(start_event, stream));
+            hipLaunchKernelGGL(lcdhip_chain_probe_kernel, dim3(1), dim3(64), 0,
+                               stream, d_chain, short_steps, 1.0, -0.25, 6.0);
+            LCDHIP_CHECK(hipEventRecord(stop_event, stream));
+            LCDHIP_CHECK(hipEventSynchronize(stop_event));
+            LCDHIP_CHECK(hipEventElapsedTime(&ms_short, start_event, stop_event));
+            if (repeat && ms_long > ms_short)
+                samples.push_back((ms_long - ms_short) * 1.0e-3 /
+                                  (long_steps - short_steps));
+        }
+    }
+    out->chain_step_s = samples.empty() ? 0.0 : median(samples);
 
     // grid barrier over one workgroup per CU
     samples.clear();

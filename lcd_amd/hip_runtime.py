@@ -90,7 +90,8 @@ class _Props(ctypes.Structure):
 class _Arch(ctypes.Structure):
     _fields_ = [(name, ctypes.c_double) for name in (
         "launch_latency_s", "atomic_cost_s", "memory_bandwidth_bytes_per_s",
-        "lane_flops_per_s", "handoff_s", "barrier_s", "graph_node_s")]
+        "lane_flops_per_s", "handoff_s", "barrier_s", "graph_node_s",
+        "lds_handoff_s", "chain_step_s")]
 
 
 RULE_SEGMENT, RULE_LATER, RULE_NEXT = 0, 1, 2

@@ -65,6 +65,8 @@ class ArchConstants:
     handoff_s: float = 0.0        # release -> acquire between workgroups
     barrier_s: float = 0.0        # one grid barrier of a resident grid
     graph_node_s: float = 0.0     # one dependent kernel node of a hipGraph
+    lds_handoff_s: float = 0.0    # the hop between wavefronts of one workgroup
+    chain_step_s: float = 0.0     # one dependent fp64 task, hand-off free
 
 
 # The mailbox protocol's level time on a busy MI355X: 3.3 x the idle-GPU

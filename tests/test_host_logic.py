@@ -1843,3 +1843,31 @@ def test_the_scheduler_says_when_the_host_would_win():
     assert S.sequential_advice(short, True) is None
     assert issubclass(S.SchedulerAdvice, UserWarning)
     assert S.SchedulePlan(schedule=None, execution_data=None).advice is None
+
+
+def test_bench_latency_bounds_are_bounds():
+    """The dependency-latency figures of the bench line: the floor is the
+    chain of dependent tasks with the hand-off free, and a hop per level can
+    only add to it."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location(
+        "lcd_bench_host", os.path.join(ROOT, "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    arch = dict(handoff_s=5.2e-7, lds_handoff_s=1.1e-7, chain_step_s=4.0e-8)
+    bounds = bench.latency_bounds(382, arch)
+    assert bounds["bound"] == bounds["registers"] == round(382 * 4.0e-5, 5)
+    assert bounds["registers"] < bounds["lds"] < bounds["memory"]
+    assert bounds["memory"] == round(382 * (4.0e-8 + 5.2e-7) * 1e3, 5)
+    # the undecorated loops of the three kinds run on the host
+    for name, size in (("c1", dict(nx=12, ny=12)), ("c3", dict(n=300)),
+                       ("c4", dict(nx=10, ny=10))):
+        work = bench_workload(name, size)
+        loop = bench.python_loop_baseline(work, seconds=5.0)
+        assert loop["rows"] == work.n and loop["entries"] == work.nnz
+        assert loop["projected_full_ms"] > 0
+
+
+def bench_workload(name, size):
+    from lcd_amd import workloads
+    return workloads.configuration(name, **size)
