@@ -412,6 +412,11 @@ class _Emitter:
                 if place == "uniform":
                     return (f"lcd_rseg_uni(_lcd_rseg, {node.slice.id} - "
                             "_lcd_seg_base)")
+                if segment.get("foreign"):
+                    # (never a position of the task's own segment)
+                    return (f"lcd_pub_ldp(_lcd_pub, {self.expr(node.slice)}, "
+                            f"{STATUS_ARGUMENT}, _task_aborted, _lcd_t0, "
+                            "_lcd_ptile, _lcd_tpos0, _lcd_tlen)")
                 return ("lcd_rseg_ldp(_lcd_pub, _lcd_seg, _lcd_seg_base, "
                         f"_lcd_seg_own, {self.expr(node.slice)}, "
                         f"{STATUS_ARGUMENT}, _task_aborted, _lcd_t0, "
@@ -511,6 +516,9 @@ class _Emitter:
             if (name == "_lcd_raw" and self.published is not None
                     and self.segment.get("registers")):
                 target = node.args[0]
+                if self.segment.get("foreign"):
+                    return ("lcd_pub_ld(_lcd_pub, _lcd_ptile, _lcd_tpos0, "
+                            f"_lcd_tlen, {self.expr(target.slice)})")
                 return ("lcd_rseg_ldr(_lcd_pub, _lcd_seg, _lcd_seg_base, "
                         f"_lcd_seg_own, {self.expr(target.slice)}, _lcd_ptile, "
                         "_lcd_tpos0, _lcd_tlen)")
@@ -524,6 +532,11 @@ class _Emitter:
                 return f"lcd_pdiv({args[0]}, {args[1]}, _lcd_rcp)"
             if name == "_lcd_settle" and self.published is not None:
                 target = node.args[0]
+                if self.segment is not None and self.segment.get("foreign"):
+                    return (f"lcd_pull_settle(_lcd_pub, "
+                            f"{self.expr(target.slice)}, {args[1]}, "
+                            f"{STATUS_ARGUMENT}, _task_aborted, _lcd_t0, "
+                            "_lcd_ptile, _lcd_tpos0, _lcd_tlen)")
                 return ("lcd_seg_settle(_lcd_pub, _lcd_seg_base, _lcd_seg_own, "
                         f"{self.expr(target.slice)}, {args[1]}, "
                         f"{STATUS_ARGUMENT}, _task_aborted, _lcd_t0, "
@@ -570,9 +583,14 @@ class _Emitter:
             place = self._register_position(target.slice)
             offset = f"{self.expr(target.slice)} - _lcd_seg_base"
             if place == "lane":
+                if segment.get("foreign"):
+                    return f"_lcd_rseg = {value_text};"
                 return (f"{{ _lcd_rseg = {value_text}; "
                         f"_lcd_seg[{offset}] = _lcd_rseg; }}")
             if place == "uniform":
+                if segment.get("foreign"):
+                    return (f"if ((lcd_index_t)(threadIdx.x & 63u) == {offset}) "
+                            f"_lcd_rseg = {value_text};")
                 return (f"lcd_rseg_put(_lcd_rseg, _lcd_seg, {offset}, "
                         f"{value_text});")
             raise HIPLoweringError(

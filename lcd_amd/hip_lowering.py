@@ -1080,10 +1080,13 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
         if self._segment is not None:
             array = self._segment["array"]
             lines += [
-                f"    __shared__ LCD_T_{array} _lcd_seg_store["
-                "LCD_GROUPS_PER_BLOCK * LCD_SEG_CAP];",
-                f"    LCD_T_{array}* const _lcd_seg = &_lcd_seg_store["
-                "(threadIdx.x / LCD_TASK_LANES) * LCD_SEG_CAP];",
+                # (no copy in LDS of a segment that lives in registers and
+                # is read at run-time positions by nobody)
+                *([] if self._segment.get("foreign") else [
+                    f"    __shared__ LCD_T_{array} _lcd_seg_store["
+                    "LCD_GROUPS_PER_BLOCK * LCD_SEG_CAP];",
+                    f"    LCD_T_{array}* const _lcd_seg = &_lcd_seg_store["
+                    "(threadIdx.x / LCD_TASK_LANES) * LCD_SEG_CAP];"]),
                 "    lcd_index_t _lcd_seg_base = 0, _lcd_seg_limit = 0;",
                 *(["    lcd_index_t _lcd_seg_own = 0;"] if self._published else []),
                 *([f"    LCD_T_{array} _lcd_rseg = 0.0;",

@@ -129,6 +129,50 @@ class SequentialPullMixin:
                 isinstance(target, ast.Name) for target in statement.targets)
                    for statement in before + after):
             return None
+        # With the own segment in registers and the searches in tables the
+        # loop runs to a bound the wavefront counts when it takes the task
+        # (`_counted_producer_plan`): no load of the producer's id and no
+        # test on it per iteration.
+        counted = None
+        segment = self._segment or {}
+        if (leave is not None and leave == 1 and len(before) == 1
+                and segment.get("registers") and segment.get("counted")
+                and self._structure_tables
+                and name == self._sequential_pull["iterator"]
+                and segment["counted"]["producer"] == before[0].targets[0].id):
+            counted = segment["counted"]
+            bound = ast.Name(id="_lcd_low_end", ctx=ast.Load())
+            self._kinds.locals["_lcd_low_end"] = INT
+            self._kinds.locals["_lcd_low_at"] = INT
+            self._own_registers += ["_lcd_low_end", "_lcd_low_at"]
+
+            class AtLane(ast.NodeTransformer):
+                def visit_Name(self, sub):
+                    if sub.id == counted["producer"]:
+                        return ast.copy_location(ast.Subscript(
+                            value=ast.Name(id=counted["index"], ctx=ast.Load()),
+                            slice=ast.Name(id="_lcd_low_at", ctx=ast.Load()),
+                            ctx=ast.Load()), sub)
+                    return sub
+
+            leaves = emitter.expr(ast.fix_missing_locations(
+                AtLane().visit(deepcopy(leading[leave].test))))
+            count_lines = [
+                "{",
+                "    _lcd_low_at = _lcd_seg_base + _lane;",
+                f"    const bool _lcd_low_stop = _lane < _lcd_seg_own && "
+                f"_lcd_low_at >= {lower} && _lcd_low_at < "
+                f"{emitter.expr(upper)} && {leaves};",
+                "    const unsigned long long _lcd_low_mask = "
+                "__ballot(_lcd_low_stop);",
+                "    _lcd_low_end = _lcd_low_mask ? _lcd_seg_base + "
+                "(lcd_index_t)__ffsll((long long)_lcd_low_mask) - 1 : "
+                f"{emitter.expr(upper)};",
+                "}",
+            ]
+            if not counted["used"]:
+                before = []
+            upper, leave = bound, None
         # everything an iteration sets up before it reads its producer is
         # located one iteration ahead, `diag_ptr = table[k]` included
         structure = after + list(structure)
@@ -192,7 +236,7 @@ class SequentialPullMixin:
             targets=[ast.Name(id=local, ctx=ast.Store())],
             value=ast.Name(id=f"_nx_{local}", ctx=ast.Load())))
             for local in names]
-        lines = [f"{name} = {lower};"]
+        lines = [f"{name} = {lower};", *(count_lines if counted else [])]
         lines += self._emit_guarded(ahead(0), emitter, 0, hooks)
         lines += [VALUE_WAIT_BEGIN, "_lcd_blocked = false;",
                   f"for (; {name} < {emitter.expr(upper)}; ++{name}) {{"]

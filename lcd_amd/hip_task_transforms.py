@@ -419,7 +419,103 @@ class TaskTransformMixin:
         if any(entry[0] == "pair" for entry in tables):
             self._kinds.arrays["_lcd_pair_base"] = INT
             plan["pair_row"] = True
+        if tables:
+            self._counted_producer_plan(body, outer, tables)
         return tuple(tables)
+
+    def _counted_producer_plan(self, task_body, outer, tables):
+        """A producer loop that opens with ``k = IDX[p]; if k >= i: break``
+        runs over the leading positions of the task's own segment whose entry
+        of IDX is below the task: with the segment in registers (lane l at
+        position l) the wavefront finds their number with one load of IDX
+        and a ballot when it takes the task, and the loop runs to that bound
+        without a load and a test per producer (``plan["counted"]``).
+
+        Every producer then is another task (``k < i``), so a position that
+        comes out of a table over the producer's segment (the gathered
+        lookup, the pair table) never lies in the task's own segment.  When
+        every read of the array goes through the loop variables that walk
+        the own segment or through such a position, the reads need not ask
+        whose segment they hit and nobody reads the copy of the own segment
+        in LDS (``plan["foreign"]``)."""
+        plan = self._segment
+        body = outer.body
+        if len(body) < 2 or len(outer.iter.args) != 2:
+            return
+        first, leave = body[0], body[1]
+        if not (isinstance(first, ast.Assign) and len(first.targets) == 1
+                and isinstance(first.targets[0], ast.Name)
+                and isinstance(first.value, ast.Subscript)
+                and isinstance(first.value.value, ast.Name)
+                and first.value.value.id not in self._all_written
+                and isinstance(first.value.slice, ast.Name)
+                and first.value.slice.id == outer.target.id):
+            return
+        producer, index_array = first.targets[0].id, first.value.value.id
+        if not (isinstance(leave, ast.If) and not leave.orelse
+                and len(leave.body) == 1
+                and isinstance(leave.body[0], ast.Break)
+                and isinstance(leave.test, ast.Compare)
+                and len(leave.test.ops) == 1
+                and isinstance(leave.test.ops[0], ast.GtE)
+                and isinstance(leave.test.left, ast.Name)
+                and leave.test.left.id == producer
+                and isinstance(leave.test.comparators[0], ast.Name)
+                and leave.test.comparators[0].id == self.loop_iterator):
+            return
+        rest = ast.Module(body=list(body[2:]), type_ignores=[])
+        stores = [node.id for node in ast.walk(rest)
+                  if isinstance(node, ast.Name)
+                  and isinstance(node.ctx, ast.Store)]
+        if producer in stores or self.loop_iterator in stores:
+            return
+        plan["counted"] = {
+            "producer": producer, "index": index_array,
+            "used": any(isinstance(node, ast.Name) and node.id == producer
+                        and isinstance(node.ctx, ast.Load)
+                        for node in ast.walk(rest))}
+        # positions of another task's segment: the gathered lookups and the
+        # pair table, both over the same index array as the loop's producers
+        foreign_tables = {entry[1] for entry in tables
+                          if entry[0] == "at" and entry[3] == index_array}
+        pairs = any(entry[0] == "pair" and entry[3] == index_array
+                    for entry in tables)
+        foreign_names = {}
+        for node in ast.walk(rest):
+            if not isinstance(node, (ast.Assign, ast.AugAssign, ast.For)):
+                continue
+            targets = (node.targets if isinstance(node, ast.Assign)
+                       else [node.target])
+            for target in targets:
+                if not isinstance(target, ast.Name):
+                    continue
+                value = node.value if isinstance(node, ast.Assign) else None
+                good = value is not None and (
+                    (isinstance(value, ast.Subscript)
+                     and isinstance(value.value, ast.Name)
+                     and value.value.id in foreign_tables
+                     and isinstance(value.slice, ast.Name)
+                     and value.slice.id == outer.target.id)
+                    or (pairs and isinstance(value, ast.Call)
+                        and isinstance(value.func, ast.Name)
+                        and value.func.id == "_lcd_pair_at"))
+                foreign_names[target.id] = (foreign_names.get(target.id, True)
+                                            and good)
+        others = ast.Module(body=[statement for statement in task_body
+                                  if statement is not outer], type_ignores=[])
+        for node in list(ast.walk(rest)) + list(ast.walk(others)):
+            if (isinstance(node, ast.Subscript)
+                    and isinstance(node.value, ast.Name)
+                    and node.value.id == plan["array"]):
+                position = node.slice
+                if not isinstance(position, ast.Name):
+                    return
+                if position.id in plan["owned"]:
+                    continue
+                if not (isinstance(node.ctx, ast.Load)
+                        and foreign_names.get(position.id)):
+                    return
+        plan["foreign"] = True
 
     def _segment_lines(self):
         """(prologue, epilogue) of a task that stages its own segment."""
@@ -451,7 +547,8 @@ class TaskTransformMixin:
                 "_task_aborted = true; _lcd_seg_own = 0; }",
                 f"_lcd_rseg = _lane < _lcd_seg_own ? {array}[_lcd_seg_base + "
                 "_lane] : 0.0;",
-                "if (_lane < _lcd_seg_own) _lcd_seg[_lane] = _lcd_rseg;",
+                *([] if plan.get("foreign") else
+                  ["if (_lane < _lcd_seg_own) _lcd_seg[_lane] = _lcd_rseg;"]),
                 *([f"_lcd_pair_row = _lcd_pair_base[{it}];"]
                   if plan.get("pair_row") else []),
             ]
