@@ -74,6 +74,14 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 OVERRIDE_VARIABLES = ("LCD_HIP_OVERRIDE_DIR", "LCD_HIP_EXTRA_OPTIONS")
 # Steps of the sub-records (the headline uses --steps / --warmup): the chain
 # of configuration 5 takes long per solve.
+# Under level launches (--mode wavefront): a task per lane whose record of
+# four incoming entries comes in with vector loads, read from operands laid
+# out in level order (128^3 grid: 1.00 ms with 128 threads per block, 0.98 with
+# 64; four lanes per task 1.11 ms).
+TUNED_LEVEL_LAUNCHES = {
+    "c2": dict(task_lanes=1, threads_per_block=64),
+}
+
 SUB_STEPS = {"c1": (50, 10), "c2": (50, 10), "c3": (50, 10), "c4": (20, 3),
              "c5": (3, 1)}
 CPU_SECONDS_SUB = 3.0
@@ -123,6 +131,8 @@ def build_solver(work, args, config):
             options.pop("spin_sleep", None)
             options.pop("resident_waves_per_cu", None)
             options.pop("dependence_protocol", None)
+            if args.mode == "wavefront":
+                options.update(TUNED_LEVEL_LAUNCHES.get(config, {}))
     if args.tpb:
         options["threads_per_block"] = args.tpb
     if args.lanes:

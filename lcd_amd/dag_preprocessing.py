@@ -254,7 +254,7 @@ def band_chains(nodes, level_ptr, dag_ptr, dag_index, band_width):
 def execution_data_from_device_dag(dag, execution_mode, warp_mapped,
                                    pushed=False, band_width=1, mailbox=False,
                                    tile_rows=None, record_lanes=None,
-                                   tile_boxes=None):
+                                   tile_boxes=None, level_positions=False):
     """Executor arrays straight from the on-device inspector (no host copy
     except the level offsets the launcher iterates over)."""
     if not isinstance(band_width, int) or band_width <= 0:
@@ -279,6 +279,11 @@ def execution_data_from_device_dag(dag, execution_mode, warp_mapped,
             initial_dep_count=counts, dag_ptr=dag.array("dag_ptr"),
             dag_index=dag.array("dag_index"))
     task_nodes = dag.array("wavefronts")
+    if level_positions and not tile_rows:
+        # level launches over operands in level order: one tile that holds
+        # every node is the level order itself, with its inverse beside it,
+        # so the records can name a source by its place in that order
+        task_nodes = dag.tile_order(max(int(dag.n), 1))
     if tile_rows:
         # tiled executor: tasks grouped by id // tile_rows, level order inside
         if not dag.topological_ids:
@@ -309,7 +314,8 @@ def execution_data_from_device_dag(dag, execution_mode, warp_mapped,
             # order the executor visits the tasks
             records = dag.task_records(
                 int(record_lanes),
-                tiled=(2 if tile_boxes is not None else bool(tile_rows)))
+                tiled=(2 if tile_boxes is not None or (
+                    level_positions and not tile_rows) else bool(tile_rows)))
             auxiliary.update(zip(
                 ("_lcd_rec_in", "_lcd_rec_src", "_lcd_rec_pos"), records))
         return WarpTaskExecutionData(

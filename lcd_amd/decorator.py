@@ -879,7 +879,8 @@ def parallel(**kwargs):
                     band_width=band_width,
                     mailbox=lowering.dependence_protocol == MAILBOX_DEPENDENCE,
                     tile_rows=lowering.tile_rows,
-                    record_lanes=lowering.task_record_lanes)
+                    record_lanes=lowering.task_record_lanes,
+                    level_positions=lowering.level_records)
             segment_registers, structure_tables = (
                 registers_for(schedule, tile_rows, device_values, lookup_values,
                               dag.n)
@@ -1027,11 +1028,12 @@ class BoundCall:
     def update_values(self):
         """Tell the call that the contents of the matrix arrays have changed
         in place since it was bound (executors that keep a copy of them in
-        their own layout -- the grid sweep -- lay it out again; the arrays
-        named in ``lowering.sweep_static_arrays``).  Everything else, the
+        their own layout -- the grid sweep, the level launches over operands
+        in level order -- lay it out again; the arrays named in
+        ``lowering.stage_static_arrays``).  Everything else, the
         right-hand side included, is read at every launch."""
-        if getattr(self.lowering, "grid_sweep", None):
-            hip_runtime.stage_sweep_values(
+        if getattr(self.lowering, "restage_launcher_name", None):
+            hip_runtime.stage_static_values(
                 self.compiled, self.lowering, self.prepared.values,
                 self.prepared.module, self.prepared.device)
 

@@ -132,10 +132,13 @@ class HIPLoweringResult:
     # whether anything is staged per launch, the arrays the matrix part reads
     # and the launcher function that stages the matrix part
     grid_sweep: dict | None = None
-    sweep_kernels: tuple = ()
+    stage_kernels: tuple = ()
     sweep_dynamic: bool = False
-    sweep_static_arrays: tuple = ()
-    sweep_launcher_name: str | None = None
+    stage_static_arrays: tuple = ()
+    restage_launcher_name: str | None = None
+    # level launches read operands laid out in level order (staging kernels
+    # ``stage_kernels``; sources named by their place in the level order)
+    level_records: bool = False
     # the pointer array of the task's own segment (ILU0's row), and whether
     # that segment is kept in registers (segments of at most 64 entries)
     segment_pointer: str | None = None
@@ -573,6 +576,13 @@ class _Emitter:
                     f"write their own element of {target.value.id} only.")
             return ("{ lcd_tile_st(_lcd_xq, _lcd_tile, _lcd_tile_row0, "
                     f"_lcd_tile_rows, (lcd_index_t)_task, {value_text}); "
+                    f"{element} = {value_text}; }}")
+        level = getattr(self.lowerer, "_level_records", None)
+        if (level is not None and self.mailbox is not None
+                and target.value.id == self.mailbox["array"]):
+            # level launches over operands in level order: the consumers
+            # read the copy of the array in that order
+            return (f"{{ _lcd_xq[_task] = {value_text}; "
                     f"{element} = {value_text}; }}")
         if self.tile is not None and target.value.id == self.tile["array"]:
             return (f"lcd_tile_st({target.value.id}, _lcd_tile, _lcd_tile_row0, "

@@ -487,7 +487,7 @@ class GridSweepMixin:
             text = text.replace(f"@{key}@", str(value))
         return text.strip("\n").split("\n")
 
-    def _grid_sweep_kernels(self, function_name, signature, declarations):
+    def _grid_stage_kernels(self, function_name, signature, declarations):
         """The three kernels around the sweep: what a step's record holds of
         the matrix arrays (``..._sweep_static``), what it holds of the other
         arrays (``..._sweep_dynamic``), and the solution back to its array

@@ -113,8 +113,14 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                  tile_by_position=False, segment_registers=False,
                  pair_tables=True, band_walker=False, level_walker=0,
                  prepared_division=True, grid_sweep=None,
-                 watchdog_seconds=None):
+                 watchdog_seconds=None, level_records=True):
         self.tile_positions = tile_positions
+        # level launches that gather: operands laid out in level order
+        self.level_records_enabled = bool(level_records)
+        self._level_records = None
+        # entries per task record (the lanes of a task; four for the level
+        # launches that give a task to one lane, see `_level_wide_lines`)
+        self.record_lanes = 1
         self.watchdog_seconds = watchdog_seconds
         # (nx, ny, nz, WY, GY, GZ, SKZ): the grid sweep over this grid
         self.grid_sweep = tuple(grid_sweep) if grid_sweep else None
@@ -230,6 +236,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                     "task_lanes must be a power of two <= 64 that divides "
                     f"threads_per_block; got {lanes} with {tpb}.")
             self.task_lanes = lanes
+        self.record_lanes = self.task_lanes
         if self.execution_mode != "plain" and not self.block_task and (
                 tpb % WAVEFRONT_SIZE and tpb > WAVEFRONT_SIZE):
             raise HIPLoweringError(
@@ -288,6 +295,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                 "HIP lowering expects exactly one synchronous function.")
         function = functions[0]
         function.decorator_list = []
+        self._sweep_function_name = function.name
         top_index, target_loop, enclosing = self._target_loop(function)
         self._target_loop_cache = target_loop
         self.host_loops = enclosing
@@ -435,6 +443,8 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                 gather["records"] = bool(self.task_records)
                 # (a plain load: nothing here is still being written)
                 self.poll_load = "lcd_ld_once"
+                if gather["records"] and self.level_records_enabled:
+                    self._level_records = self._level_records_plan(body)
         self._segment_registers_plan(body)
         self._structure_tables = self._pair_table_plan(body)
         if self.tile_rows:
@@ -506,6 +516,11 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
         for name, _, _ in self._queue_node_loads:
             executor_arguments.append(name)
             kernel_arguments.append(name)
+        if self._level_records is not None:
+            # (the node values in level order were found with the node loads)
+            for _, staged, _, _ in self._level_records["values"]:
+                executor_arguments.append(staged)
+                kernel_arguments.append(staged)
         missing = ({sid for sid, _ in self.reductions.values()} - lowered_ids)
         if missing:
             raise HIPLoweringError(
@@ -589,13 +604,19 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
             level_walker=(self.level_walker if self._walker
                           and self._walker["kind"] == "level" else 0),
             grid_sweep=(dict(self._sweep["geometry"]) if self._sweep else None),
-            sweep_kernels=(tuple(self._sweep["kernels"]) if self._sweep
-                           else ()),
+            stage_kernels=(tuple(self._sweep["kernels"]) if self._sweep
+                           else tuple(self._level_records["kernels"])
+                           if self._level_records else ()),
             sweep_dynamic=bool(self._sweep and self._sweep["dynamic_kernel"]),
-            sweep_static_arrays=(tuple(self._sweep["static_arrays"])
-                                 if self._sweep else ()),
-            sweep_launcher_name=(function_name + "_hip_sweep_restage"
-                                 if self._sweep else None),
+            stage_static_arrays=(tuple(self._sweep["static_arrays"])
+                                 if self._sweep
+                                 else tuple(self._level_records["static_arrays"])
+                                 if self._level_records else ()),
+            restage_launcher_name=(function_name + "_hip_sweep_restage"
+                                   if self._sweep
+                                   else function_name + "_hip_level_restage"
+                                   if self._level_records else None),
+            level_records=self._level_records is not None,
             segment_pointer=(self._segment["pointer"]
                              if self._segment else None),
             segment_registers=bool(self._segment
@@ -607,7 +628,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
             published_array=(self._published["array"]
                              if self._published else None),
             task_record_lanes=(
-                self.task_lanes if self._mailbox
+                self.record_lanes if self._mailbox
                 and self._mailbox["gather"]
                 and self._mailbox["gather"].get("records") else None),
             value_flag_array=(
@@ -752,7 +773,9 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
             return list(WAVEFRONT_ARGUMENTS) + (
                 ["_lcd_in_ptr", "_lcd_in_pos", "_lcd_in_src",
                  *(RECORD_ARGUMENTS if self._mailbox["gather"].get("records")
-                   else ())]
+                   else ()),
+                 *([*self._level_records["operands"].values(), "_lcd_xq"]
+                   if self._level_records is not None else ())]
                 if self.level_gather else [])
         return []
 
@@ -944,6 +967,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
             "#ifndef LCD_INDEX_TYPE", "#define LCD_INDEX_TYPE int", "#endif",
             f"#define LCD_TPB {self.threads_per_block}",
             f"#define LCD_TASK_LANES {self.task_lanes}",
+            f"#define LCD_RECORD_LANES {self.record_lanes}",
             f"#define LCD_GROUPS_PER_BLOCK (LCD_TPB / LCD_TASK_LANES)",
             "#ifndef LCD_SPIN_LIMIT",
             # a poll of LDS takes a tenth of a poll of memory: keep the
@@ -1003,6 +1027,11 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
         mutable_executor = {"dep_count", "task_counter", "done",
                             STATUS_ARGUMENT, "_lcd_mailbox", "_lcd_pub",
                             "_lcd_xq", *SWEEP_ARGUMENTS}
+        if self._level_records is not None:
+            # (written by the staging kernels, which share the signature)
+            mutable_executor |= set(self._level_records["operands"].values())
+            mutable_executor |= {staged for _, staged, _, _
+                                 in self._level_records["values"]}
         for name in kernel_arguments:
             if name in array_arguments:
                 const = (name not in written_arrays
@@ -1107,9 +1136,18 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
         def task(indent, body_lines=None):
             pad = "    " * indent
             out = [f"{pad}if ({guard}) {{"]
+            if self._level_records is not None:
+                # every node of the level order lies in the loop's range (the
+                # DAG was built over it), and a test on the loaded id would
+                # hold the record's loads back until the id has arrived
+                out = [f"{pad}{{"]
             if self.execution_mode != "sync_free":
                 out += [pad + "    " + line for line in prefetch]
-            if self.level_gather:
+            wide = (self._level_records is not None
+                    and self._level_records.get("wide"))
+            if wide:
+                out += self._level_wide_sum_lines(indent + 1)
+            elif self.level_gather:
                 # the producers ran in earlier launches: their values are
                 # there, the products are added in (source, position) order
                 records = self._mailbox["gather"].get("records", False)
@@ -1155,7 +1193,10 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                          f"{pad}    {self.group_sync}",
                          f"{pad}}}"])
             fetch = []
-            if self.level_gather and self._mailbox["gather"].get("records"):
+            if (self._level_records is not None
+                    and self._level_records.get("wide")):
+                fetch = self._level_wide_fetch_lines(indent)
+            elif self.level_gather and self._mailbox["gather"].get("records"):
                 # the record of the task is addressed by its place in the
                 # level order: its loads leave with the load of the task id
                 fetch = [f"{pad}const bool _pending = true;",
@@ -1180,6 +1221,12 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                          "/ LCD_TASK_LANES;")
             lines.append("    if (_task >= band_end) return;")
             lines += node_loop(1, task)
+            if self._level_records is not None:
+                lines.append("}")
+                return (self._level_stage_kernels(
+                    self._sweep_function_name, signature,
+                    self._declarations(local_names, 1), guard)
+                        + "\n".join(lines) + "\n")
         elif self._walker is not None:
             walker = (self._level_walker_text(task_body)
                       if self._walker["kind"] == "level"
@@ -1200,7 +1247,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
             if self._walker["kind"] == "sweep":
                 # the staging kernels share the signature and the locals
                 lines.append("}")
-                return (self._grid_sweep_kernels(
+                return (self._grid_stage_kernels(
                     self._sweep_function_name, signature,
                     self._declarations(local_names, 1))
                         + "\n".join(lines) + "\n")
@@ -1563,10 +1610,35 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
         elif self.execution_mode == "wavefront":
             start = kernel_arguments.index("band_start")
             end = kernel_arguments.index("band_end")
+            records = self._level_records
+            if records is not None:
+                # the right-hand side's share of the node values goes into
+                # level order in front of the level launches; the matrix's
+                # share and the edge operands only when they have changed
+                stage_args = "(" + ", ".join(
+                    "_count" if name == "band_end" else text
+                    for name, text in zip(kernel_arguments, args)) + ",)"
+                static, dynamic = records["kernels"]
+                body.append("_count = _hip.length(task_nodes)")
+                if records["dynamic"]:
+                    body.append(f"_hip.launch({dynamic!r}, (_count + 255) // 256 "
+                                f"or 1, 256, {stage_args})")
             body.append(
                 f"_hip.launch_levels({kernel_name!r}, band_ptr, "
                 f"{max(1, self.threads_per_block // self.task_lanes)}, "
                 f"{self.threads_per_block}, {call_args}, {start}, {end})")
+            if records is not None:
+                restage = [
+                    "_count = _hip.length(task_nodes)",
+                    f"_hip.launch({static!r}, (_count * {self.record_lanes} + 255) "
+                    f"// 256 or 1, 256, {stage_args})"]
+                text = (f"def {launcher_name}(_hip, "
+                        + ", ".join(launcher_arguments) + "):\n"
+                        + "\n".join("    " + line for line in body) + "\n"
+                        f"\n\ndef {self._sweep_function_name}_hip_level_restage"
+                        "(_hip, " + ", ".join(launcher_arguments) + "):\n"
+                        + "\n".join("    " + line for line in restage) + "\n")
+                return text, launcher_arguments
         else:
             count_array = {PULL_DEPENDENCE: "done",
                            MAILBOX_DEPENDENCE: "task_nodes"}.get(
@@ -1696,7 +1768,7 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
                  tile_positions=None, tile_by_position=False,
                  segment_registers=False, pair_tables=True, band_walker=False,
                  level_walker=0, prepared_division=True, grid_sweep=None,
-                 watchdog_seconds=None):
+                 watchdog_seconds=None, level_records=True):
     """HIP counterpart of ``lower_to_numba_cuda``
     (compiler/cuda_lowering.py:2854-2884); same parameters plus
     ``task_lanes`` (lanes cooperating on one task, a power of two <= 64),
@@ -1728,5 +1800,5 @@ def lower_to_hip(code, loop_iterator, reductions=None, kernel_name=None,
         segment_registers=segment_registers, pair_tables=pair_tables,
         band_walker=band_walker, level_walker=level_walker,
         prepared_division=prepared_division, grid_sweep=grid_sweep,
-        watchdog_seconds=watchdog_seconds)
+        watchdog_seconds=watchdog_seconds, level_records=level_records)
     return lowerer.lower(code)

@@ -2,6 +2,7 @@
 its gathered form): their plans and the readiness code a task polls."""
 
 import ast
+import re
 from copy import deepcopy
 
 from lcd_amd.structural_lookups import structure_aliases
@@ -13,6 +14,9 @@ from lcd_amd.hip_emitter import (
     _names_in,
 )
 
+
+# entries of a task record when level launches give a task to one lane
+LEVEL_WIDE_ENTRIES = 4
 
 class ProtocolMixin:
     """Methods of ``HIPLowerer`` (lcd_amd/hip_lowering.py)."""
@@ -336,6 +340,18 @@ class ProtocolMixin:
             f"{name} = {staged[name]}[_mb_next + _lane];" if name in staged
             else f"{name} = {emitter.expr(node)};"
             for name, node, _ in gather["operands"])
+        level = self._level_records
+        if level is not None and records:
+            # level order: the operands of the record's edges sit beside it
+            loads = " ".join(
+                f"{name} = {level['operands'][name]}"
+                "[_task * LCD_TASK_LANES + _lane];"
+                for name, _, _ in gather["operands"])
+            if declare:
+                lines.append(f"{pad}bool _g_queue = true; (void)_g_queue;")
+        elif level is not None:
+            # (further chunks name their sources by id)
+            loads += " _g_queue = false;"
         head = "if (_pending && _mb_next + _lane < _mb_end)" if declare else (
             "if (_mb_next + _lane < _mb_end)")
         decode = ("_g_off = (unsigned)(_g_src - _lcd_tile_row0); "
@@ -351,8 +367,9 @@ class ProtocolMixin:
                 "(lcd_index_t)task_nodes[_task]; "
                 "_mb_next = _lcd_rec_in[2 * _task]; "
                 "_mb_end = _lcd_rec_in[2 * _task + 1]; "
-                f"_g_pos = _lcd_rec_pos[{slot}]; "
-                f"_g_src = _lcd_rec_src[{slot}]; {decode}"
+                + ("" if level is not None and "_g_pos" not in _names_in(
+                    gather["value"]) else f"_g_pos = _lcd_rec_pos[{slot}]; ")
+                + f"_g_src = _lcd_rec_src[{slot}]; {decode}"
                 + " ".join(self._queue_load_lines) + " }")
             lines.append(f"{pad}{head} {{ {loads} }}")
             if self.single_chunk:
@@ -612,6 +629,12 @@ class ProtocolMixin:
                 "__ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) : "
                 f"{self.poll_load}(&{array}[_g_src]))" if tiled
                 else f"{self.poll_load}(&{array}[_g_src])")
+        if self._level_records is not None:
+            # the record names a source by its place in the level order: the
+            # value is read from the copy of the array in that order, which
+            # the launch of the source's level wrote contiguously
+            load = (f"(_g_queue ? _lcd_xq[_g_src] : {load})"
+                    if not self.single_chunk else "_lcd_xq[_g_src]")
         missing = "(_lane < _mb_have && lcd_is_empty(_mb_value))"
         complete = (f"lcd_group_none({missing})" if self.task_lanes > 1
                     else f"!{missing}")
@@ -644,7 +667,9 @@ class ProtocolMixin:
             # set when the task is fetched and cleared by its poll
             memory_poll = (
                 "{ const double _g_raw = lcd_is_empty(_g_early) ? "
-                f"{self.poll_load}(&{array}[_g_src]) : _g_early; "
+                + ("_lcd_xq[_g_src]" if self._level_records is not None
+                   else f"{self.poll_load}(&{array}[_g_src])")
+                + " : _g_early; "
                 "if (!lcd_is_empty(_g_raw)) { _mb_value = _g_raw; "
                 "_need = false; } }")
             return [
@@ -751,6 +776,216 @@ class ProtocolMixin:
             "{ _missing = 1; break; }",
             f"{pad}bool _ready = !({total});",
         ]
+
+    def _level_records_plan(self, body):
+        """Level launches over operands in level order.  A launch then reads
+        contiguous memory only: the record of a task (its first incoming
+        edges), the operands of those edges, the task's node values, and the
+        values of its sources from a copy of the array in level order that
+        the tasks write beside the array itself.  The copies are filled by
+        two staging kernels that share the kernel's signature: one for what
+        comes from the arrays the edge operands read (the matrix; run again
+        when their contents change), one for the rest of the node values
+        (the right-hand side; run in front of every call).  Returns the plan,
+        or None when the task does not fit: a host loop around the launches,
+        an operand or a product that names its source by id, a store to the
+        array at another place than the task's own."""
+        gather, kinds = self._mailbox["gather"], self._kinds
+        array = self._mailbox["array"]
+        if self.host_loops or self.chain_tasks:
+            return None
+        if "_g_src" in _names_in(gather["value"]):
+            return None
+        operands = {}
+        static_arrays = []
+        for index, (name, node, kind) in enumerate(gather["operands"]):
+            if "_g_src" in _names_in(node.slice):
+                return None
+            operands[name] = f"_lcd_lr_{index}"
+            kinds.arrays[operands[name]] = kind
+            for sub in ast.walk(node):
+                if (isinstance(sub, ast.Subscript)
+                        and isinstance(sub.value, ast.Name)
+                        and kinds.arrays.get(sub.value.id) == FLOAT
+                        and sub.value.id not in static_arrays):
+                    static_arrays.append(sub.value.id)
+        for statement in body:
+            for node in ast.walk(statement):
+                targets = (node.targets if isinstance(node, ast.Assign) else
+                           [node.target] if isinstance(node, ast.AugAssign)
+                           else [])
+                for target in targets:
+                    if (isinstance(target, ast.Subscript)
+                            and isinstance(target.value, ast.Name)
+                            and target.value.id == array
+                            and not (isinstance(target.slice, ast.Name)
+                                     and target.slice.id == self.loop_iterator)):
+                        if node is not self._mailbox["sites"][0]:
+                            return None
+        kinds.arrays["_lcd_xq"] = FLOAT
+        function_name = self._sweep_function_name
+        wide = self.task_lanes == 1
+        if wide:
+            # a task per lane: its record has LEVEL_WIDE_ENTRIES entries,
+            # fetched with vector loads (`_level_wide_fetch_lines`)
+            self.record_lanes = LEVEL_WIDE_ENTRIES
+        return {"operands": operands, "values": [], "order": [], "wide": wide,
+                "static_arrays": static_arrays, "dynamic": False,
+                "kernels": (function_name + "_hip_level_static",
+                            function_name + "_hip_level_dynamic")}
+
+    def _level_wide_fetch_lines(self, indent):
+        """Level records with a task per lane: the record's sources and the
+        operands of its edges come in with one vector load per array (the
+        addresses depend on the task's place in the level order alone), the
+        node values beside them."""
+        pad = "    " * indent
+        level, gather = self._level_records, self._mailbox["gather"]
+        lines = [
+            f"{pad}const int _mb_begin = _lcd_rec_in[2 * _task], "
+            "_mb_end = _lcd_rec_in[2 * _task + 1];",
+            f"{pad}const int _mb_have = (_mb_end - _mb_begin) < "
+            "LCD_RECORD_LANES ? (_mb_end - _mb_begin) : LCD_RECORD_LANES;",
+            f"{pad}const int4 _g_s = ((const int4*)_lcd_rec_src)[_task];",
+            f"{pad}const lcd_index_t _g_srcs[4] = {{_g_s.x, _g_s.y, _g_s.z, "
+            "_g_s.w};"]
+        for name, _, kind in gather["operands"]:
+            vector = "int4" if kind == INT else "double4"
+            scalar = "lcd_index_t" if kind == INT else "double"
+            staged = level["operands"][name]
+            lines += [
+                f"{pad}const {vector} {name}_v = "
+                f"((const {vector}*){staged})[_task];",
+                f"{pad}const {scalar} {name}_w[4] = {{{name}_v.x, {name}_v.y, "
+                f"{name}_v.z, {name}_v.w}};"]
+        return lines
+
+    def _level_wide_sum_lines(self, indent):
+        """... and the task's sum: the sources' values from the copy of the
+        array in level order, all loads in flight together, the products
+        added in the order of the record (the order of the sequential loop);
+        entries beyond the record are read by id, one by one."""
+        pad = "    " * indent
+        gather, emitter = self._mailbox["gather"], self._emitter
+        own = self._mailbox["register"]
+        array = self._mailbox["array"]
+
+        sign = "-" if gather["negate"] else ""
+        lines = [f"{pad}double _g_values[4] = {{0.0, 0.0, 0.0, 0.0}};",
+                 f"{pad}#pragma unroll",
+                 f"{pad}for (int _e = 0; _e < LCD_RECORD_LANES; ++_e) "
+                 "if (_e < _mb_have) _g_values[_e] = _lcd_xq[_g_srcs[_e]];"]
+        for entry in range(LEVEL_WIDE_ENTRIES):
+            lines.append(
+                f"{pad}if ({entry} < _mb_have) {own} = {own} + "
+                f"{sign}({self._wide_product_text(entry)});")
+        if not self.single_chunk:
+            operands = " ".join(
+                f"const {'lcd_index_t' if kind == INT else 'double'} {name} = "
+                f"{emitter.expr(node)};" for name, node, kind in gather["operands"])
+            lines += [
+                f"{pad}for (int _e = _mb_begin + LCD_RECORD_LANES; _e < _mb_end; "
+                "++_e) {",
+                f"{pad}    const lcd_index_t _g_pos = _lcd_in_pos[_e]; (void)_g_pos;",
+                f"{pad}    const lcd_index_t _g_src = _lcd_in_src[_e];",
+                f"{pad}    {operands}",
+                f"{pad}    const double _g_value = {array}[_g_src];",
+                f"{pad}    {own} = {own} + {sign}({emitter.expr(gather['value'])});",
+                f"{pad}}}"]
+        return lines
+
+    def _wide_product_text(self, entry):
+        """The product of one record entry, over the registers the wide
+        fetch filled."""
+        gather, emitter = self._mailbox["gather"], self._emitter
+        text = emitter.expr(gather["value"])
+        for name, _, _ in gather["operands"]:
+            text = re.sub(rf"\b{re.escape(name)}\b", f"{name}_w[{entry}]", text)
+        return re.sub(r"\b_g_value\b", f"_g_values[{entry}]", text)
+
+    def _level_value_load(self, name, node, text):
+        """A node value ``R[e]`` of a read-only float array in level order:
+        ``_lcd_lv_k[_task]``, or None when it stays a load by id."""
+        level = self._level_records
+        if level is None or self._kinds.arrays.get(node.value.id) != FLOAT:
+            return None
+        if any(isinstance(sub, ast.Name) and sub.id.startswith("_nl_")
+               and self._kinds.locals.get(sub.id) == FLOAT
+               for sub in ast.walk(node.slice)):
+            return None
+        staged = f"_lcd_lv_{len(level['values'])}"
+        static = node.value.id in level["static_arrays"]
+        level["values"].append((name, staged, text, static))
+        level["dynamic"] = level["dynamic"] or not static
+        self._kinds.arrays[staged] = FLOAT
+        return staged
+
+    def _level_stage_kernels(self, function_name, signature, declarations,
+                             guard):
+        """The two staging kernels of the level records (same signature as
+        the level kernel; ``band_start`` = 0 and ``band_end`` = the number of
+        tasks).  Static: a thread per slot of the records; dynamic: a thread
+        per task."""
+        level, gather = self._level_records, self._mailbox["gather"]
+        emitter, it = self._emitter, self.loop_iterator
+        static_name, dynamic_name = level["kernels"]
+
+        def head(name, per_task):
+            lines = ["", 'extern "C" __global__ void __launch_bounds__(256)',
+                     f"{name}(", f"        {signature})", "{",
+                     *declarations,
+                     f"    lcd_index_t {it} = 0;",
+                     "    const long long _slot = (long long)blockIdx.x * "
+                     "blockDim.x + threadIdx.x;"]
+            if per_task:
+                lines += ["    const long long _task = (long long)band_start "
+                          "+ _slot;",
+                          "    const int _lane = 0; (void)_lane;"]
+            else:
+                lines += ["    const long long _task = (long long)band_start "
+                          "+ _slot / LCD_RECORD_LANES;",
+                          "    const int _lane = (int)(_slot % LCD_RECORD_LANES);"]
+            lines += ["    if (_task >= band_end) return;",
+                      f"    {it} = task_nodes[_task];"]
+            return lines
+
+        def values(static):
+            lines = []
+            for kind, line, is_static in level["order"]:
+                if kind == "value":
+                    if is_static == static:
+                        lines.append(f"        {line}")
+                else:
+                    lines.append(f"        {line}")
+            return lines
+
+        loads = [f"            {level['operands'][name]}[_slot] = "
+                 f"{emitter.expr(node)};"
+                 for name, node, _ in gather["operands"]]
+        clears = [f"            {level['operands'][name]}[_slot] = 0;"
+                  for name, _, _ in gather["operands"]]
+        static = head(static_name, False) + [
+            f"    if ({guard}) {{",
+            "        if (_lane == 0) {",
+            *["    " + line for line in values(True)],
+            "        }",
+            "        const int _mb_next = _lcd_rec_in[2 * _task], "
+            "_mb_end = _lcd_rec_in[2 * _task + 1];",
+            "        if (_mb_next + _lane < _mb_end) {",
+            "            const lcd_index_t _g_pos = _lcd_rec_pos[_slot]; "
+            "(void)_g_pos;",
+            *loads,
+            "        } else {",
+            *clears,
+            "        }",
+            "    }",
+            "}", ""]
+        dynamic = head(dynamic_name, True) + [
+            f"    if ({guard}) {{",
+            *values(False),
+            "    }",
+            "}", ""]
+        return "\n".join(static + dynamic)
 
     def _stage_kernel_text(self, stage_name):
         """``_lcd_staged_k[s] = R[f(in_pos[s])]`` for every message ``s``."""

@@ -1315,6 +1315,25 @@ def prepare_hip_arguments(lowering, argument_values, execution_data,
                 workspace[("state", name)] = cached
             host_values[name] = cached
 
+    if getattr(lowering, "level_records", False):
+        # operands of the records' edges, node values and the copy of the
+        # array the tasks write, all in level order
+        lanes = int(lowering.task_record_lanes or 1)
+        for name in lowering.launcher_arguments:
+            if not (name.startswith(("_lcd_lr_", "_lcd_lv_"))
+                    or name == "_lcd_xq"):
+                continue
+            dtype = (np.int32 if lowering.array_arguments.get(name) == "int"
+                     else np.float64)
+            slots = max(n_tasks, 1) * (lanes if name.startswith("_lcd_lr_")
+                                       else 1)
+            cached = workspace.get(("state", name))
+            if cached is None or len(cached) != slots or (
+                    cached.dtype != dtype):
+                cached = device.empty((slots,), dtype)
+                workspace[("state", name)] = cached
+            host_values[name] = cached
+
     missing = [name for name in lowering.launcher_arguments
                if name not in host_values]
     if missing:
@@ -1336,14 +1355,15 @@ def prepare_hip_arguments(lowering, argument_values, execution_data,
     module = None
     if compiled_module is not None:
         module = _load_for_values(compiled_module, lowering, prepared, device)
-    if (getattr(lowering, "grid_sweep", None) and module is not None
+    if (getattr(lowering, "restage_launcher_name", None) and module is not None
             and isinstance(device, HIPDevice)):
-        # the matrix's share of the sweep's records: staged again when the
-        # contents of its arrays have changed since the last time
+        # the matrix's share of the staged records (grid sweep, level
+        # records): staged again when the contents of its arrays have
+        # changed since the last time
         digests = tuple(device.digest(prepared[name])
-                        for name in lowering.sweep_static_arrays)
+                        for name in lowering.stage_static_arrays)
         if workspace.get(("sweep", "digests")) != digests:
-            stage_sweep_values(compiled_module, lowering, prepared, module,
+            stage_static_values(compiled_module, lowering, prepared, module,
                                device)
             workspace[("sweep", "digests")] = digests
     # a captured graph stays valid while every pointer and scalar is unchanged
@@ -1455,7 +1475,7 @@ def _load_for_values(compiled, lowering, prepared, device):
                     stage.append(ctypes.c_void_p)
             argument_ctypes[lowering.stage_kernel_name] = stage + [
                 ctypes.c_int64]
-        for name in getattr(lowering, "sweep_kernels", ()):
+        for name in getattr(lowering, "stage_kernels", ()):
             # the staging kernels of the grid sweep share the signature
             argument_ctypes[name] = list(ctypes_of)
         compiled.loaded[cache_key] = device.load_module(code, argument_ctypes)
@@ -1503,13 +1523,13 @@ def _sweep_reset(buffers, device):
     device.fill_zero(buffers["_lcd_sw_claim"])
 
 
-def stage_sweep_values(compiled_module, lowering, prepared_values, module,
+def stage_static_values(compiled_module, lowering, prepared_values, module,
                        device):
     """Lay the matrix's share of the grid sweep's records out again (the
     coefficients by direction, the node loads that come from the matrix
     arrays, the prepared reciprocals): to be called whenever the contents of
-    ``lowering.sweep_static_arrays`` have changed."""
-    launcher = compiled_module.namespace[lowering.sweep_launcher_name]
+    ``lowering.stage_static_arrays`` have changed."""
+    launcher = compiled_module.namespace[lowering.restage_launcher_name]
     context = LaunchContext(device, module, None)
     launcher(context, *[prepared_values[name]
                         for name in lowering.launcher_arguments])

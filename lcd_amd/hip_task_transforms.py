@@ -941,11 +941,26 @@ class TaskTransformMixin:
         for text in order[:node_count]:
             name, node = temps[text]
             queued = self._queue_node_load(node)
+            level = self._level_records
             if queued is not None:
                 # addressed by the queue position: issued with the task id
                 self._queue_load_lines.append(f"{name} = {queued}[_task];")
+                if level is not None:
+                    level["order"].append(
+                        ("queue", f"{name} = {queued}[_task];", None))
+                continue
+            text = f"{name} = {emitter.expr(node)};"
+            staged = self._level_value_load(name, node, text)
+            if staged is not None:
+                # in level order, filled by the staging kernels
+                self._queue_load_lines.append(f"{name} = {staged}[_task];")
+                level["order"].append(
+                    ("value", f"{text} {staged}[_task] = {name};",
+                     node.value.id in level["static_arrays"]))
             else:
-                prefetch.append(f"{name} = {emitter.expr(node)};")
+                prefetch.append(text)
+                if level is not None:
+                    level["order"].append(("load", text, None))
         self._own_registers.extend(temps[text][0] for text in order)
         reload_lines = []
         if first_iteration:

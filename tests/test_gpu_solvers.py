@@ -146,6 +146,20 @@ def test_level_launches_gather_their_products(oracle, lanes):
         for _ in range(2):
             solve_and_check(gathered, work, expected, exact=True)
         solve_and_check(pushed, work, expected)
+    # the operands of a launch lie in level order (staged copies): other
+    # matrix values and another right-hand side through the same plan
+    assert gathered.hip_lowering.level_records
+    assert gathered.hip_lowering.task_record_lanes == max(lanes, 4 if lanes == 1
+                                                          else lanes)
+    work = workloads.configuration("c2", nx=20, ny=18, nz=16)
+    rng = np.random.default_rng(lanes)
+    for _ in range(2):
+        values = work.data * rng.uniform(0.5, 1.5, len(work.data))
+        rhs = rng.standard_normal(work.n)
+        expected = oracle.sptrsv_csc(work.indptr, work.indices, values, rhs,
+                                     work.n)
+        np.testing.assert_array_equal(
+            gathered(work.indptr, work.indices, values, rhs, work.n), expected)
     # a power-law factor: hundreds of incoming entries for some rows
     lower, diagonal, rhs = random_lower_factor(3000, 7)
     import scipy.sparse as sp

@@ -807,6 +807,53 @@ def test_level_launches_gather_incoming_products():
                    wavefront_threads_per_block=128,
                    dependence_protocol="mailbox")
     assert result.dependence_protocol == "mailbox"
+    # the operands a launch reads lie in level order: the edge operand of the
+    # records, the copy of x the tasks write, the node values
+    assert result.level_records
+    assert result.kernel_arguments[-10:] == [
+        "_lcd_in_ptr", "_lcd_in_pos", "_lcd_in_src", "_lcd_rec_in",
+        "_lcd_rec_src", "_lcd_rec_pos", "_lcd_lr_0", "_lcd_xq",
+        "_lcd_lv_0", "_lcd_lv_1"]
+    assert result.stage_kernels == ("sptrsv_csc_loop_hip_level_static",
+                                    "sptrsv_csc_loop_hip_level_dynamic")
+    assert result.stage_static_arrays == ("Ax",)
+    assert result.restage_launcher_name == "sptrsv_csc_loop_hip_level_restage"
+    source = result.source
+    # the matrix's share is staged by one kernel, the right-hand side's by
+    # the other, which runs in front of the level launches of every call
+    static = source[source.index("sptrsv_csc_loop_hip_level_static("):
+                    source.index("sptrsv_csc_loop_hip_level_dynamic(")]
+    dynamic = source[source.index("sptrsv_csc_loop_hip_level_dynamic("):
+                     source.index("sptrsv_csc_loop_hip_kernel(")]
+    assert "_lcd_lv_1[_task] = _nl_2;" in static and "b[i]" not in static
+    assert "_lcd_lr_0[_slot] = Ax[_g_pos];" in static
+    assert "_lcd_lv_0[_task] = _nl_0;" in dynamic and "Ax[" not in dynamic
+    launcher = result.launcher_source
+    assert launcher.index("sptrsv_csc_loop_hip_level_dynamic") < launcher.index(
+        "launch_levels") < launcher.index("def sptrsv_csc_loop_hip_level_restage")
+    kernel = result.kernel_source
+    kernel = kernel[kernel.index("sptrsv_csc_loop_hip_kernel("):]
+    assert "_g_operand_0 = _lcd_lr_0[_task * LCD_TASK_LANES + _lane];" in kernel
+    assert "_nl_0 = _lcd_lv_0[_task];" in kernel and "b[i]" not in kernel
+    assert ("const double _g_value = (_g_queue ? _lcd_xq[_g_src] : "
+            "lcd_ld_once(&x[_g_src]));") in kernel
+    assert "{ _lcd_xq[_task] = _lcd_own_0; x[i] = _lcd_own_0; }" in kernel
+    hip_runtime.compile_code(result.source)
+    # (the variant for DAGs whose records hold every incoming edge)
+    single = lower(module, execution_mode="wavefront",
+                   thread_loop_iterator="j", task_lanes=4,
+                   wavefront_threads_per_block=128,
+                   dependence_protocol="mailbox", single_chunk=True)
+    assert "lcd_is_empty(_g_early) ? _lcd_xq[_g_src] : _g_early" in (
+        single.kernel_source)
+    assert "&x[_g_src]" not in single.kernel_source
+    hip_runtime.compile_code(single.source)
+    # without them: operands and sources by id, as the incoming listing has them
+    result = lower(module, execution_mode="wavefront",
+                   thread_loop_iterator="j", task_lanes=4,
+                   wavefront_threads_per_block=128,
+                   dependence_protocol="mailbox", level_records=False)
+    assert not result.level_records and result.stage_kernels == ()
     assert result.kernel_arguments[-6:] == [
         "_lcd_in_ptr", "_lcd_in_pos", "_lcd_in_src", "_lcd_rec_in",
         "_lcd_rec_src", "_lcd_rec_pos"]
@@ -1075,8 +1122,8 @@ def test_grid_sweep_lowering_and_geometry():
     assert result.kernel_arguments[6:11] == list(SWEEP_ARGUMENTS)
     # the matrix array is staged when its contents change, the right-hand
     # side in front of every solve
-    assert result.sweep_static_arrays == ("Ax",) and result.sweep_dynamic
-    assert result.sweep_kernels == (
+    assert result.stage_static_arrays == ("Ax",) and result.sweep_dynamic
+    assert result.stage_kernels == (
         "sptrsv_csc_loop_hip_sweep_static", "sptrsv_csc_loop_hip_sweep_dynamic",
         "sptrsv_csc_loop_hip_sweep_unstage")
     kernel = result.kernel_source
