@@ -78,8 +78,13 @@ OVERRIDE_VARIABLES = ("LCD_HIP_OVERRIDE_DIR", "LCD_HIP_EXTRA_OPTIONS")
 # four incoming entries comes in with vector loads, read from operands laid
 # out in level order (128^3 grid: 1.00 ms with 128 threads per block, 0.98 with
 # 64; four lanes per task 1.11 ms).
+# ILU0: a row per wavefront, the row in registers and the pivot loop's
+# searches in tables as in the persistent executor, plain loads (9-point
+# 1024^2: 16.6 ms; four lanes per row with searches 27.8 ms).
 TUNED_LEVEL_LAUNCHES = {
     "c2": dict(task_lanes=1, threads_per_block=64),
+    "c4": dict(task_lanes=64, threads_per_block=128,
+               dependence_protocol="pull"),
 }
 
 SUB_STEPS = {"c1": (50, 10), "c2": (50, 10), "c3": (50, 10), "c4": (20, 3),
@@ -700,7 +705,6 @@ def main():
         # block size the reference's demo fixes
         # (compiler/demo/spilu0.py:85-98)
         print("bench: c4 wavefront", file=sys.stderr, flush=True)
-        sub_args.tpb, sub_args.lanes = 128, 4
         records["c4_wavefront"] = run_configuration(
             "c4", sub_args, device, 5, 1, arch, 0.0, python_loop=False)
         result["configs"] = records

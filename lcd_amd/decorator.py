@@ -61,6 +61,7 @@ from lcd_amd.hip_runtime import (
 from lcd_amd.scheduler import (
     AUTO,
     SYNC_FREE,
+    WAVEFRONT,
     AnalyticScheduler,
     CalibratedScheduler,
     SchedulePlan,
@@ -393,9 +394,12 @@ def parallel(**kwargs):
             Level 0: neither."""
             if registers_option is False:
                 return 0, {}
+            # (level launches take the registers with the tables or not at
+            # all: their task reads other segments through the tables only)
+            level_launches = schedule.execution_mode == WAVEFRONT
             try:
                 variant = lower_variant(schedule.lowering_key, rows,
-                                        registers=1)
+                                        registers=2 if level_launches else 1)
             except HIPLoweringError:
                 return 0, {}
             if not variant.segment_registers:
@@ -411,10 +415,10 @@ def parallel(**kwargs):
                         f"entries; the longest has {longest}.")
                 return 0, {}
             if not kwargs.get("pair_tables", True):
-                return 1, {}
+                return 0 if level_launches else 1, {}
             variant = lower_variant(schedule.lowering_key, rows, registers=2)
             if not variant.structure_tables:
-                return 1, {}
+                return 0 if level_launches else 1, {}
             device = get_device()
             tables = {}
             try:
@@ -433,13 +437,13 @@ def parallel(**kwargs):
                         entries = device.pair_lookup_entries(
                             values[pointer_array], values[index_array])
                         if entries > PAIR_TABLE_ENTRIES_PER_POSITION * positions:
-                            return 1, {}
+                            return 0 if level_launches else 1, {}
                         tables["_lcd_pair_base"], tables[name] = (
                             device.pair_lookup_build(values[pointer_array],
                                                      values[index_array],
                                                      offsets=True))
             except (hip_runtime.HIPRuntimeError, KeyError):
-                return 1, {}
+                return 0 if level_launches else 1, {}
             return 2, tables
 
         def walker_for(dag, schedule):

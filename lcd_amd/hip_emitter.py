@@ -415,6 +415,8 @@ class _Emitter:
                 if place == "uniform":
                     return (f"lcd_rseg_uni(_lcd_rseg, {node.slice.id} - "
                             "_lcd_seg_base)")
+                if segment.get("foreign") and self.published.get("plain"):
+                    return element
                 if segment.get("foreign"):
                     # (never a position of the task's own segment)
                     return (f"lcd_pub_ldp(_lcd_pub, {self.expr(node.slice)}, "
@@ -519,6 +521,8 @@ class _Emitter:
             if (name == "_lcd_raw" and self.published is not None
                     and self.segment.get("registers")):
                 target = node.args[0]
+                if self.segment.get("foreign") and self.published.get("plain"):
+                    return self.element(target)
                 if self.segment.get("foreign"):
                     return ("lcd_pub_ld(_lcd_pub, _lcd_ptile, _lcd_tpos0, "
                             f"_lcd_tlen, {self.expr(target.slice)})")
@@ -535,6 +539,9 @@ class _Emitter:
                 return f"lcd_pdiv({args[0]}, {args[1]}, _lcd_rcp)"
             if name == "_lcd_settle" and self.published is not None:
                 target = node.args[0]
+                if (self.segment is not None and self.segment.get("foreign")
+                        and self.published.get("plain")):
+                    return args[1]
                 if self.segment is not None and self.segment.get("foreign"):
                     return (f"lcd_pull_settle(_lcd_pub, "
                             f"{self.expr(target.slice)}, {args[1]}, "

@@ -258,6 +258,19 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
             and direct_dependence.kind == PUSH_DEPENDENCE
             and self.warp_mapped and self.execution_mode == "wavefront"
             and not chain_tasks)
+        # level launches of a task with a sequential producer loop (ILU0's
+        # pivot loop): the task of the persistent pull executor -- own
+        # segment in registers, searches in tables, structure located one
+        # producer ahead -- with plain loads where that one polls (every
+        # producer ran in an earlier launch)
+        self.level_pull = (
+            dependence_protocol == PULL_DEPENDENCE
+            and direct_dependence is not None
+            and direct_dependence.kind == PULL_DEPENDENCE
+            and getattr(direct_dependence, "sequential", False)
+            and self.warp_mapped and self.execution_mode == "wavefront"
+            and not chain_tasks and self.task_lanes == 64
+            and bool(segment_registers) and bool(pair_tables))
         self.dependence_protocol = (
             dependence_protocol
             if (direct_dependence is not None
@@ -266,7 +279,7 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                 and sync_free_ready_count == 0
                 # the members of a chain task wait on their counters one by
                 # one (compiler/cuda_lowering.py:1360-1410)
-                and not chain_tasks) or self.level_gather
+                and not chain_tasks) or self.level_gather or self.level_pull
             else COUNTER_DEPENDENCE)
         if chain_tasks:
             self.tile_rows = None
@@ -424,8 +437,12 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
             # release fence ahead of it and the acquire behind the wait all
             # disappear from the chain between two levels.
             self._published = {"array": self._segment["array"],
-                               "buffer": "_lcd_pub"}
-            kinds.arrays["_lcd_pub"] = FLOAT
+                               "buffer": "_lcd_pub",
+                               # level launches: the array itself holds the
+                               # producers' final values, no buffer beside it
+                               "plain": self.level_pull}
+            if not self.level_pull:
+                kinds.arrays["_lcd_pub"] = FLOAT
         if self.level_gather:
             if self._mailbox["gather"] is None:
                 # the loop does not fit the gathered form: atomics as before
@@ -447,6 +464,15 @@ class HIPLowerer(ProtocolMixin, SequentialPullMixin, TaskTransformMixin,
                     self._level_records = self._level_records_plan(body)
         self._segment_registers_plan(body)
         self._structure_tables = self._pair_table_plan(body)
+        if self.level_pull and not (
+                self._published is not None and self._segment is not None
+                and self._segment.get("registers")
+                and self._segment.get("foreign")):
+            raise HIPLoweringError(
+                "Level launches of a sequential producer loop with the pull "
+                "protocol need a task whose own segment fits the registers "
+                "of a wavefront and whose reads of other segments all go "
+                "through the inspector's tables.")
         if self.tile_rows:
             self._tile = self._tile_plan(target_loop)
         if (self.task_records and self._mailbox is not None

@@ -253,7 +253,8 @@ class SequentialPullMixin:
         # diagonal) come first in the rest; behind the last of them the
         # lanes' own first loads get their second attempt
         again = (self._second_attempts(fetched, emitter)
-                 if leading_loads else [])
+                 if leading_loads and not self._published.get("plain")
+                 else [])
         for position, child in enumerate(rest):
             lines += self._emit_guarded(child, emitter, 1, hooks)
             if position == len(leading_loads) - 1:

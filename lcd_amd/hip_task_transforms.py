@@ -540,11 +540,15 @@ class TaskTransformMixin:
         if plan.get("registers"):
             # (segments longer than 64 entries are excluded by the caller; one
             # that is longer anyway stops the launch through the status word)
+            plain = bool(self._published and self._published.get("plain"))
             prologue = [
                 f"_lcd_seg_base = {bound(0)};",
                 f"_lcd_seg_own = {bound(1)} - _lcd_seg_base;",
-                f"if (_lcd_seg_own > 64) {{ {STATUS_ARGUMENT}[0] = 1; "
-                "_task_aborted = true; _lcd_seg_own = 0; }",
+                # (level launches have no status word: the caller has checked
+                # the segment lengths of the structure this plan is for)
+                *([] if plain else
+                  [f"if (_lcd_seg_own > 64) {{ {STATUS_ARGUMENT}[0] = 1; "
+                   "_task_aborted = true; _lcd_seg_own = 0; }"]),
                 f"_lcd_rseg = _lane < _lcd_seg_own ? {array}[_lcd_seg_base + "
                 "_lane] : 0.0;",
                 *([] if plan.get("foreign") else
@@ -557,6 +561,9 @@ class TaskTransformMixin:
                 "_lcd_tpos0, _lcd_tlen, _lcd_seg_base + _lane, _lcd_rseg); "
                 f"{array}[_lcd_seg_base + _lane] = _lcd_rseg; }}",
             ]
+            if plain:
+                epilogue = [f"if (_lane < _lcd_seg_own) "
+                            f"{array}[_lcd_seg_base + _lane] = _lcd_rseg;"]
             return prologue, epilogue
         prologue = [
             f"_lcd_seg_base = {bound(0)};",

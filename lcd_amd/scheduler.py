@@ -587,6 +587,15 @@ class ScheduleSpace:
                 else (MAILBOX_DEPENDENCE,)
                 if (self.level_gather and self.thread_mapped
                     and _wave_task(block, n_warp))
+                # level launches of a sequential producer loop, a wavefront
+                # per task: the pull executor's task with plain loads (the
+                # lowering keeps the counters where it does not apply)
+                else (PULL_DEPENDENCE,)
+                if (mode == WAVEFRONT and self.sequential_pull
+                    and self.thread_mapped
+                    and PULL_DEPENDENCE in self.dependence_protocols
+                    and lanes in (0, WAVE_SIZE) and block >= WAVE_SIZE
+                    and _wave_task(block, n_warp))
                 else (COUNTER_DEPENDENCE,))
             for protocol in protocols:
                 if (protocol == PULL_DEPENDENCE and self.sequential_pull

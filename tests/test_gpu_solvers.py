@@ -610,6 +610,56 @@ def test_ilu0_csr_variants(oracle, options):
                 forced(matrix.data.copy(), indices, indptr)
 
 
+def test_ilu0_level_launches_with_the_row_in_registers(oracle):
+    """ILU0 under level launches, a row per wavefront: the task of the
+    persistent pull executor (row in registers, pivot searches in the
+    inspector's tables, the next pivot located ahead) with plain loads --
+    every pivot row was finished by an earlier launch.  Bit-identical on the
+    stencil and on rows of uneven length; a structure with rows beyond 64
+    entries keeps the counters and the searches."""
+    print("ilu0 level pull", flush=True)
+    factor = spilu0.compile_ilu0_csr(
+        execution_mode="wavefront", threads_per_block=128, task_lanes=64,
+        thread_unroll=1, dependence_protocol="pull")
+    work = workloads.configuration("c4", nx=72, ny=56)
+    expected = oracle.ilu0_csr(work.data, work.indices, work.indptr)
+    for _ in range(2):
+        np.testing.assert_array_equal(
+            factor(work.data.copy(), work.indices, work.indptr), expected)
+    lowering = factor.hip_lowering
+    assert lowering.execution_mode == "wavefront"
+    assert lowering.dependence_protocol == "pull" and lowering.segment_registers
+    source = factor.hip_kernel_source
+    assert "_lcd_pair[" in source and "lcd_sorted_find" not in source
+    assert "_lcd_pub" not in source and "lcd_pull_settle(" not in source
+    import scipy.sparse as sp
+    rng = np.random.default_rng(5)
+    n = 3000
+    pattern = sp.random(n, n, density=6.0 / n, random_state=3, format="csr")
+    pattern = pattern + pattern.T + sp.identity(n)
+    matrix = sp.csr_matrix(pattern)
+    matrix.data = rng.uniform(-1.0, 1.0, len(matrix.data))
+    matrix = sp.csr_matrix(matrix + sp.diags(np.full(n, 40.0)))
+    matrix.sort_indices()
+    assert np.diff(matrix.indptr).max() <= 64
+    indptr = matrix.indptr.astype(np.int32)
+    indices = matrix.indices.astype(np.int32)
+    np.testing.assert_array_equal(
+        factor(matrix.data.copy(), indices, indptr),
+        oracle.ilu0_csr(matrix.data, indices, indptr))
+    assert factor.hip_lowering.segment_registers
+    lower, diagonal, _ = random_lower_factor(2500, 11)
+    long_rows = sp.csr_matrix(lower + lower.T * 0.5 + sp.diags(4 * diagonal))
+    long_rows.sort_indices()
+    indptr = long_rows.indptr.astype(np.int32)
+    indices = long_rows.indices.astype(np.int32)
+    np.testing.assert_array_equal(
+        factor(long_rows.data.copy(), indices, indptr),
+        oracle.ilu0_csr(long_rows.data, indices, indptr))
+    assert not factor.hip_lowering.segment_registers
+    assert factor.hip_lowering.dependence_protocol == "counter"
+
+
 @pytest.mark.parametrize("mode", ["wavefront", "sync_free", None])
 def test_ilu0_csc_matches_the_sequential_loop(oracle, mode):
     """compiler/e2e_tests/test_spilu0_e2e.py:107-121: the column form, every
