@@ -406,12 +406,40 @@ __global__ void kahn_expand_kernel(const int32_t *__restrict__ dag_ptr,
 
 // ---- level sets, algorithm 2: ordered sweep ------------------------------
 // Valid when every edge goes from a lower to a higher id.  Wavefronts take
-// 64 consecutive ids in order; level(v) = 1 + max level(pred).  Predecessors
-// inside the same 64-id chunk are read from LDS, so a dependency chain inside
-// a chunk advances at LDS latency; predecessors in earlier chunks are polled
-// in global memory.  Chunks are handed out in id order, so the lowest
-// unfinished chunk can always finish: no deadlock.  state[0] chunk counter,
-// state[1] watchdog flag, state[2] max level + 1.
+// 64 consecutive ids in order, a lane per node; level(v) = 1 + max
+// level(pred).  Predecessor lists are sorted, so a node's predecessors in
+// earlier chunks come first and those inside its own chunk last.  The former
+// are read from memory: once with a plain load (a level is written once over
+// the -1 the array starts with, so any other value is final whichever cache
+// served it), then, where that came back -1, with device-coherent polls and a
+// nap between them.  The latter go through LDS alone: between two rounds of
+// polls the chunk settles every chain among its own nodes that has become
+// free, at LDS latency and with no load from memory in the way.  Chunks are
+// handed out in id order, so the lowest unfinished chunk can always finish:
+// no deadlock.  state[0] chunk counter, state[1] watchdog flag, state[2] max
+// level + 1.
+// Sum of (destination - source) over every kSpanSample-th edge of the
+// (dst << 32 | src) keys: how far back a node's predecessors lie on average.
+constexpr int kSpanSample = 16;
+
+__global__ void edge_span_kernel(const unsigned long long *__restrict__ keys,
+                                 int64_t edges, unsigned long long *sum)
+{
+    const int64_t e = (blockIdx.x * static_cast<int64_t>(blockDim.x) +
+                       threadIdx.x) * kSpanSample;
+    unsigned long long span = 0;
+    if (e < edges) {
+        const unsigned long long key = keys[e];
+        span = (key >> 32) - (key & 0xffffffffull);
+    }
+    for (int offset = 32; offset > 0; offset >>= 1)
+        span += __shfl_xor(span, offset);
+    if ((threadIdx.x & 63) == 0 && span)
+        atomicAdd(sum, span);
+}
+
+constexpr int32_t kHeavyNode = 96;   // predecessors beyond which the wavefront helps
+
 __global__ void __launch_bounds__(256)
 sweep_levels_kernel(const int32_t *__restrict__ pred_ptr,
                     const int32_t *__restrict__ pred_index, int64_t n,
@@ -434,32 +462,106 @@ sweep_levels_kernel(const int32_t *__restrict__ pred_ptr,
         int32_t p = pending ? pred_ptr[v] : 0;
         const int32_t p_end = pending ? pred_ptr[v + 1] : 0;
         int32_t best = -1;
+        // A node with many predecessors (a dense row of a power-law matrix)
+        // is first read by the whole wavefront, 64 predecessors at a time:
+        // the levels that are there already go into its maximum at once, and
+        // its lane takes over at the first one that is still missing (they
+        // are sorted, and what is missing is what was handed out last, so
+        // that is near the end of the list).  Nobody waits here.
+        unsigned long long heavy = __ballot(pending && p_end - p > kHeavyNode);
+        while (heavy) {
+            const int owner = __ffsll(static_cast<long long>(heavy)) - 1;
+            heavy &= heavy - 1;
+            const int32_t q0 = __shfl(p, owner), q1 = __shfl(p_end, owner);
+            int32_t stop = q1, high = -1;
+            for (int32_t q = q0 + lane; q < q1; q += 64) {
+                const int64_t u = pred_index[q];
+                int32_t l = -1;
+                if (u < base) {
+                    l = level_of[u];
+                    if (l < 0)
+                        l = __hip_atomic_load(&level_of[u], __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+                }
+                if (l < 0) {
+                    stop = q;        // inside the chunk, or not there yet
+                    break;
+                }
+                high = l > high ? l : high;
+            }
+            for (int offset = 32; offset > 0; offset >>= 1) {
+                const int32_t other_high = __shfl_xor(high, offset);
+                const int32_t other_stop = __shfl_xor(stop, offset);
+                high = other_high > high ? other_high : high;
+                stop = other_stop < stop ? other_stop : stop;
+            }
+            if (lane == owner) {
+                best = high > best ? high : best;
+                p = stop;
+            }
+        }
+        // first pass over the predecessors in earlier chunks: plain loads.
+        // `u` is the predecessor at p (read once, when p gets there).
+        int64_t u = pending && p < p_end ? pred_index[p] : -1;
+        bool outside = pending && p < p_end && u < base;
+        while (outside) {
+            const int32_t l = level_of[u];
+            if (l < 0)
+                break;
+            best = l > best ? l : best;
+            ++p;
+            u = p < p_end ? pred_index[p] : -1;
+            outside = p < p_end && u < base;
+        }
         int64_t spins = 0;
         while (__ballot(pending)) {
-            if (pending) {
-                while (p < p_end) {
-                    const int64_t u = pred_index[p];
-                    const int32_t l =
-                        u >= base ? chunk_level[wave][u - base]
-                                  : __hip_atomic_load(&level_of[u],
-                                                      __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT);
-                    if (l < 0)
-                        break;
-                    best = l > best ? l : best;
-                    ++p;
-                }
-                if (p == p_end) {
-                    const int32_t mine = best + 1;
-                    chunk_level[wave][lane] = mine;
-                    __hip_atomic_store(&level_of[v], mine, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-                    highest = mine + 1 > highest ? mine + 1 : highest;
-                    pending = false;
-                }
+            while (outside) {
+                const int32_t l = __hip_atomic_load(
+                    &level_of[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (l < 0)
+                    break;
+                best = l > best ? l : best;
+                ++p;
+                u = p < p_end ? pred_index[p] : -1;
+                outside = p < p_end && u < base;
             }
-            if (++spins > (1ll << 24) ||
-                ((spins & 1023) == 0 &&
+            // the chains inside the chunk, as far as they are free
+            bool moved = true;
+            while (moved) {
+                bool finished = false;
+                if (pending && !outside) {
+                    while (p < p_end) {
+                        const int32_t l = chunk_level[wave][u - base];
+                        if (l < 0)
+                            break;
+                        best = l > best ? l : best;
+                        ++p;
+                        u = p < p_end ? pred_index[p] : -1;
+                    }
+                    if (p == p_end) {
+                        const int32_t mine = best + 1;
+                        chunk_level[wave][lane] = mine;
+                        __hip_atomic_store(&level_of[v], mine, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                        highest = mine + 1 > highest ? mine + 1 : highest;
+                        pending = false;
+                        finished = true;
+                    }
+                }
+                moved = __ballot(finished) != 0;
+            }
+            // (a short nap while the wait is young -- a neighbour's level
+            // is a hop away --, a longer one for the chunks far behind)
+            if (__ballot(outside)) {
+                if (spins < 16)
+                    __builtin_amdgcn_s_sleep(1);
+                else
+                    __builtin_amdgcn_s_sleep(16);
+            }
+            // (every wait ends: a bound on the rounds of one chunk, and a
+            // look at the flag another wavefront may have raised)
+            if (++spins > (1ll << 22) ||
+                ((spins & 255) == 0 &&
                  __hip_atomic_load(&state[1], __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT))) {
                 state[1] = 1;
@@ -508,12 +610,34 @@ __global__ void chain_fill_kernel(int64_t n, int32_t *__restrict__ level_of,
         level_of[v] = static_cast<int32_t>(v);
 }
 
-__global__ void level_histogram_kernel(const int32_t *__restrict__ level_of,
-                                       int64_t n, int32_t *__restrict__ hist)
+// Nodes per level.  With few levels every bin is hot: a workgroup counts its
+// share in LDS first (levels below kHistogramBins) and adds what it found to
+// memory once per bin.
+constexpr int kHistogramBins = 4096;
+
+__global__ void __launch_bounds__(256)
+level_histogram_kernel(const int32_t *__restrict__ level_of, int64_t n,
+                       int32_t *__restrict__ hist)
 {
-    int64_t v = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
-    if (v < n && level_of[v] >= 0)
-        atomicAdd(&hist[level_of[v]], 1);
+    __shared__ int32_t bins[kHistogramBins];
+    for (int b = threadIdx.x; b < kHistogramBins; b += blockDim.x)
+        bins[b] = 0;
+    __syncthreads();
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t v = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+         v < n; v += stride) {
+        const int32_t level = level_of[v];
+        if (level < 0)
+            continue;
+        if (level < kHistogramBins)
+            atomicAdd(&bins[level], 1);
+        else
+            atomicAdd(&hist[level], 1);
+    }
+    __syncthreads();
+    for (int b = threadIdx.x; b < kHistogramBins; b += blockDim.x)
+        if (bins[b])
+            atomicAdd(&hist[b], bins[b]);
 }
 
 inline unsigned blocks_for(int64_t count)
@@ -529,19 +653,21 @@ inline int bits_for(uint64_t max_value)
     return bits;
 }
 
+// Temporaries of one inspector call, from the library's block pool.  They go
+// back when the call returns, behind one wait for the device: work that
+// still reads them may be in flight (hipFree used to wait the same way).
 struct Scratch {
     std::vector<void *> owned;
     ~Scratch()
     {
-        for (void *p : owned)
-            if (p)
-                (void)hipFree(p);
+        lcdhip::pool_retire(owned.data(), owned.size());
     }
     template <class T>
     hipError_t alloc(T **out, size_t count)
     {
         void *p = nullptr;
-        hipError_t status = hipMalloc(&p, std::max<size_t>(count, 1) * sizeof(T));
+        hipError_t status =
+            lcdhip::pool_alloc(&p, std::max<size_t>(count, 1) * sizeof(T));
         if (status == hipSuccess)
             owned.push_back(p);
         *out = static_cast<T *>(p);
@@ -555,19 +681,23 @@ extern "C" int lcdhip_dag_destroy(lcdhip_dag *dag)
 {
     if (!dag)
         return LCDHIP_OK;
-    for (int32_t *&array : dag->arrays)
-        if (array) {
-            (void)hipFree(array);
-            array = nullptr;
-        }
+    // (the arrays may still be read by work in flight)
+    void *blocks[LCDHIP_DAG_ARRAYS];
+    for (int which = 0; which < LCDHIP_DAG_ARRAYS; ++which) {
+        blocks[which] = dag->arrays[which];
+        dag->arrays[which] = nullptr;
+    }
+    lcdhip::pool_retire(blocks, LCDHIP_DAG_ARRAYS);
     delete dag;
     return LCDHIP_OK;
 }
 
 static int dag_alloc(lcdhip_dag *dag, int which, int64_t count)
 {
-    LCDHIP_CHECK(hipMalloc(&dag->arrays[which],
-                           std::max<int64_t>(count, 1) * sizeof(int32_t)));
+    void *block = nullptr;
+    LCDHIP_CHECK(lcdhip::pool_alloc(
+        &block, std::max<int64_t>(count, 1) * sizeof(int32_t)));
+    dag->arrays[which] = static_cast<int32_t *>(block);
     dag->counts[which] = count;
     return LCDHIP_OK;
 }
@@ -875,6 +1005,7 @@ static int build_levels(lcdhip_dag *dag, const unsigned long long *d_transposed,
         LCDHIP_CHECK(scratch.alloc(&pred_index, edges));
         LCDHIP_CHECK(scratch.alloc(&state, 4));
         LCDHIP_CHECK(hipMemsetAsync(state, 0, 16, stream));
+        unsigned long long *span_sum = nullptr, host_span = 0;
         {
             size_t temp_bytes = 0;
             char *temp = nullptr;
@@ -889,6 +1020,16 @@ static int build_levels(lcdhip_dag *dag, const unsigned long long *d_transposed,
             int32_t total = static_cast<int32_t>(edges);
             LCDHIP_CHECK(hipMemcpyAsync(pred_ptr + n, &total, 4,
                                         hipMemcpyHostToDevice, stream));
+            if (edges > 0) {
+                LCDHIP_CHECK(scratch.alloc(&span_sum, 1));
+                LCDHIP_CHECK(hipMemsetAsync(span_sum, 0, 8, stream));
+                hipLaunchKernelGGL(
+                    edge_span_kernel,
+                    dim3(blocks_for((edges + kSpanSample - 1) / kSpanSample)),
+                    dim3(kBlock), 0, stream, d_transposed, edges, span_sum);
+                LCDHIP_CHECK(hipMemcpyAsync(&host_span, span_sum, 8,
+                                            hipMemcpyDeviceToHost, stream));
+            }
             LCDHIP_CHECK(hipStreamSynchronize(stream));
         }
         if (edges > 0) {
@@ -896,13 +1037,15 @@ static int build_levels(lcdhip_dag *dag, const unsigned long long *d_transposed,
             LCDHIP_CHECK(scratch.alloc(&sorted, edges));
             size_t temp_bytes = 0;
             char *temp = nullptr;
+            const int end_bit =
+                std::min(64, 32 + bits_for(static_cast<uint64_t>(n)));
             LCDHIP_CHECK(rocprim::radix_sort_keys(
                 nullptr, temp_bytes, d_transposed, sorted,
-                static_cast<size_t>(edges), 0, 64, stream));
+                static_cast<size_t>(edges), 0, end_bit, stream));
             LCDHIP_CHECK(scratch.alloc(&temp, temp_bytes));
             LCDHIP_CHECK(rocprim::radix_sort_keys(
                 temp, temp_bytes, d_transposed, sorted,
-                static_cast<size_t>(edges), 0, 64, stream));
+                static_cast<size_t>(edges), 0, end_bit, stream));
             hipLaunchKernelGGL(low_words_kernel, dim3(blocks_for(edges)),
                                dim3(kBlock), 0, stream, sorted, edges,
                                pred_index);
@@ -919,9 +1062,27 @@ static int build_levels(lcdhip_dag *dag, const unsigned long long *d_transposed,
         hipLaunchKernelGGL(chain_fill_kernel, dim3(blocks_for(n)), dim3(kBlock),
                            0, stream, n, level_of, state);
         const int64_t chunks = (n + 63) / 64;
+        // How many chunks are in flight at once.  The chunks wait for one
+        // another through memory polls, and polls that cannot succeed yet
+        // slow down the ones that can.  Predecessors that lie close (grids,
+        // bands) are always among the chunks in flight: a wide window (four
+        // workgroups per CU) gives the diagonal front of such a DAG its
+        // parallelism (whole inspection of the 128^3 grid: 8.4 / 6.0 / 4.7 /
+        // 4.7 ms at 1 / 2 / 4 / 8 per CU; of the 9-point 1024^2 ILU0 DAG,
+        // 3070 levels deep: 8.4 / 6.9 / 6.9 / 7.7 ms).  Predecessors spread
+        // over all earlier ids (a random or power-law matrix) are mostly
+        // finished already under a narrow window (one workgroup per CU) and
+        // mostly polled in vain under a wide one (1 M rows, 16 M edges, mean
+        // span 0.25 n: the sweep alone 2.3 ms against 8.4 ms).
+        const double mean_span =
+            edges > 0 ? static_cast<double>(host_span) * kSpanSample /
+                            static_cast<double>(edges)
+                      : 0.0;
+        const int per_cu = mean_span * 8.0 > static_cast<double>(n) ? 1 : 4;
         const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(
             (chunks + 3) / 4,
-            static_cast<int64_t>(lcdhip::context().props.multiProcessorCount) * 8));
+            static_cast<int64_t>(lcdhip::context().props.multiProcessorCount) *
+                per_cu));
         hipLaunchKernelGGL(sweep_levels_kernel, dim3(blocks), dim3(256), 0,
                            stream, pred_ptr, pred_index, n, level_of, state);
         LCDHIP_CHECK(hipGetLastError());
@@ -985,8 +1146,13 @@ static int build_levels(lcdhip_dag *dag, const unsigned long long *d_transposed,
         int32_t *hist = nullptr;
         LCDHIP_CHECK(scratch.alloc(&hist, levels + 1));
         LCDHIP_CHECK(hipMemsetAsync(hist, 0, (levels + 1) * 4, stream));
-        hipLaunchKernelGGL(level_histogram_kernel, dim3(blocks_for(n)),
-                           dim3(kBlock), 0, stream, level_of, n, hist);
+        hipLaunchKernelGGL(
+            level_histogram_kernel,
+            dim3(std::min<unsigned>(
+                blocks_for(n),
+                static_cast<unsigned>(
+                    lcdhip::context().props.multiProcessorCount) * 4)),
+            dim3(256), 0, stream, level_of, n, hist);
         size_t temp_bytes = 0;
         char *temp = nullptr;
         LCDHIP_CHECK(rocprim::exclusive_scan(
@@ -1054,7 +1220,8 @@ extern "C" int lcdhip_dag_band_chains(lcdhip_dag *dag, int64_t band_width,
     for (int which : {LCDHIP_DAG_TASK_NODES, LCDHIP_DAG_TASK_PTR,
                       LCDHIP_DAG_BAND_PTR})
         if (dag->arrays[which]) {
-            (void)hipFree(dag->arrays[which]);
+            void *block = dag->arrays[which];
+            lcdhip::pool_retire(&block, 1);
             dag->arrays[which] = nullptr;
             dag->counts[which] = 0;
         }
@@ -1202,7 +1369,8 @@ namespace {
 void dag_release(lcdhip_dag *dag, int which)
 {
     if (dag->arrays[which]) {
-        (void)hipFree(dag->arrays[which]);
+        void *block = dag->arrays[which];
+        lcdhip::pool_retire(&block, 1);
         dag->arrays[which] = nullptr;
         dag->counts[which] = 0;
     }

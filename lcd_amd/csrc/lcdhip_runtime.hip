@@ -7,10 +7,14 @@
 #include <hip/hiprtc.h>
 
 #include <algorithm>
+#include <atomic>
 #include <chrono>
 #include <cstdlib>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "lcdhip_common.h"
@@ -100,6 +104,138 @@ static __device__ __align__(256) unsigned long long
 #define LCDHIP_MAX_DEVICES 64
 static unsigned long long *g_digest_scratch[LCDHIP_MAX_DEVICES] = {};
 
+// ---------------------------------------------------- block pool ----
+namespace lcdhip {
+namespace {
+struct Pool {
+    std::mutex lock;
+    std::unordered_map<void *, std::pair<size_t, int>> blocks;   // capacity, device
+    std::multimap<std::pair<int, size_t>, void *> idle;          // (device, capacity)
+    size_t idle_bytes = 0;
+};
+Pool &pool()
+{
+    static Pool instance;
+    return instance;
+}
+size_t pool_capacity(size_t bytes)
+{
+    // powers of two up to 1 MiB, multiples of 1 MiB beyond
+    if (bytes <= 256)
+        return 256;
+    if (bytes > (size_t(1) << 20))
+        return (bytes + (size_t(1) << 20) - 1) & ~((size_t(1) << 20) - 1);
+    size_t capacity = 256;
+    while (capacity < bytes)
+        capacity <<= 1;
+    return capacity;
+}
+}  // namespace
+
+hipError_t pool_alloc(void **out, size_t bytes)
+{
+    *out = nullptr;
+    int device = 0;
+    hipError_t status = hipGetDevice(&device);
+    if (status != hipSuccess)
+        return status;
+    const size_t capacity = pool_capacity(bytes);
+    Pool &p = pool();
+    {
+        std::lock_guard<std::mutex> guard(p.lock);
+        auto found = p.idle.find({device, capacity});
+        if (found != p.idle.end()) {
+            *out = found->second;
+            p.idle.erase(found);
+            p.idle_bytes -= capacity;
+            return hipSuccess;
+        }
+    }
+    void *pointer = nullptr;
+    status = hipMalloc(&pointer, capacity);
+    if (status != hipSuccess) {
+        // what is idle may be what is missing
+        pool_trim();
+        status = hipMalloc(&pointer, capacity);
+        if (status != hipSuccess)
+            return status;
+    }
+    std::lock_guard<std::mutex> guard(p.lock);
+    p.blocks[pointer] = {capacity, device};
+    *out = pointer;
+    return hipSuccess;
+}
+
+void pool_release(void *pointer)
+{
+    if (!pointer)
+        return;
+    Pool &p = pool();
+    std::unique_lock<std::mutex> guard(p.lock);
+    auto found = p.blocks.find(pointer);
+    if (found == p.blocks.end()) {
+        guard.unlock();
+        (void)hipFree(pointer);
+        return;
+    }
+    const size_t capacity = found->second.first;
+    if (p.idle_bytes + capacity > kPoolIdleBytes) {
+        p.blocks.erase(found);
+        guard.unlock();
+        (void)hipFree(pointer);
+        return;
+    }
+    p.idle.insert({{found->second.second, capacity}, pointer});
+    p.idle_bytes += capacity;
+}
+
+namespace {
+std::atomic<int> g_open_captures{0};
+}
+
+void pool_retire(void *const *pointers, size_t count)
+{
+    bool any = false;
+    for (size_t k = 0; k < count; ++k)
+        any = any || pointers[k] != nullptr;
+    if (!any)
+        return;
+    if (g_open_captures.load() > 0) {
+        Pool &p = pool();
+        for (size_t k = 0; k < count; ++k) {
+            if (!pointers[k])
+                continue;
+            {
+                std::lock_guard<std::mutex> guard(p.lock);
+                p.blocks.erase(pointers[k]);
+            }
+            (void)hipFree(pointers[k]);
+        }
+        return;
+    }
+    (void)hipDeviceSynchronize();
+    for (size_t k = 0; k < count; ++k)
+        pool_release(pointers[k]);
+}
+
+void pool_trim()
+{
+    Pool &p = pool();
+    std::vector<void *> doomed;
+    {
+        std::lock_guard<std::mutex> guard(p.lock);
+        for (auto &entry : p.idle) {
+            doomed.push_back(entry.second);
+            p.blocks.erase(entry.second);
+        }
+        p.idle.clear();
+        p.idle_bytes = 0;
+    }
+    for (void *pointer : doomed)
+        (void)hipFree(pointer);
+}
+}  // namespace lcdhip
+
 extern "C" int lcdhip_init(int device)
 {
     auto &ctx = context();
@@ -135,6 +271,7 @@ extern "C" int lcdhip_shutdown(void)
     if (!ctx.ready)
         return LCDHIP_OK;
     LCDHIP_CHECK(hipStreamSynchronize(ctx.stream));
+    lcdhip::pool_trim();
     LCDHIP_CHECK(hipStreamDestroy(ctx.stream));
     ctx.stream = nullptr;
     ctx.ready = false;
@@ -499,6 +636,7 @@ extern "C" int lcdhip_graph_begin_capture(lcdhip_stream stream)
     LCDHIP_REQUIRE_INIT();
     LCDHIP_CHECK(hipStreamBeginCapture(resolve_stream(stream),
                                        hipStreamCaptureModeRelaxed));
+    lcdhip::g_open_captures.fetch_add(1);
     return LCDHIP_OK;
 }
 
@@ -507,6 +645,8 @@ extern "C" int lcdhip_graph_end_capture(lcdhip_stream stream, lcdhip_graph **out
     LCDHIP_REQUIRE_INIT();
     auto *graph = new lcdhip_graph();
     hipError_t status = hipStreamEndCapture(resolve_stream(stream), &graph->graph);
+    if (lcdhip::g_open_captures.load() > 0)
+        lcdhip::g_open_captures.fetch_sub(1);
     if (status != hipSuccess) {
         set_error("hipStreamEndCapture: %s", hipGetErrorString(status));
         delete graph;

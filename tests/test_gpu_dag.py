@@ -571,3 +571,32 @@ def test_digest_is_content_sensitive(device):
     c = device.to_device(c_host)
     assert device.digest(a) == device.digest(b)
     assert device.digest(a) != device.digest(c)
+
+
+def test_inspections_reuse_device_memory_safely(device, oracle):
+    """The inspector keeps its device blocks for reuse (temporaries and the
+    arrays of destroyed DAGs): inspections of different structures and sizes
+    one after another, with DAGs alive and destroyed in between, each match
+    the oracle -- nothing depends on what an earlier one left in a block.
+    Power-law rows with hundreds of predecessors (read by the whole
+    wavefront) and long-range edges (the narrow sweep window) are among
+    them."""
+    kept = []
+    for round_ in range(2):
+        for name, overrides in (("c3", dict(n=40000)), ("c1", {}),
+                                ("c4", dict(nx=64, ny=48)),
+                                ("c3", dict(n=9000)),
+                                ("c2", dict(nx=16, ny=12, nz=10))):
+            work = workloads.configuration(name, **overrides)
+            print("dag reuse", round_, name, overrides, flush=True)
+            dag, _ = _check_dag(device, oracle, _rule_for(oracle, work),
+                                work.n)
+            if name == "c1":
+                kept.append(dag)        # stays alive across the others
+            else:
+                dag.destroy()
+    for dag in kept:
+        work = workloads.configuration("c1")
+        expected = oracle.dag_build([_rule_for(oracle, work)], work.n)
+        np.testing.assert_array_equal(dag.host("level_of"), expected.level_of)
+        dag.destroy()
