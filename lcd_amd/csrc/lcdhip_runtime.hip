@@ -179,14 +179,30 @@ void pool_release(void *pointer)
         return;
     }
     const size_t capacity = found->second.first;
-    if (p.idle_bytes + capacity > kPoolIdleBytes) {
+    if (capacity > kPoolIdleBytes) {
         p.blocks.erase(found);
         guard.unlock();
         (void)hipFree(pointer);
         return;
     }
+    // what comes back is what the next call will ask for: make room for it
+    // by freeing blocks that have been idle (of other sizes: an earlier
+    // structure's) rather than the one just used
+    std::vector<void *> evicted;
+    while (p.idle_bytes + capacity > kPoolIdleBytes && !p.idle.empty()) {
+        auto victim = p.idle.begin();
+        if (victim->first.second == capacity && p.idle.size() > 1)
+            victim = std::prev(p.idle.end());
+        p.idle_bytes -= victim->first.second;
+        evicted.push_back(victim->second);
+        p.blocks.erase(victim->second);
+        p.idle.erase(victim);
+    }
     p.idle.insert({{found->second.second, capacity}, pointer});
     p.idle_bytes += capacity;
+    guard.unlock();
+    for (void *old : evicted)
+        (void)hipFree(old);
 }
 
 namespace {
