@@ -305,6 +305,7 @@ def parallel(**kwargs):
                     grid_sweep=sweep,
                     prepared_division=kwargs.get("prepared_division", True),
                     watchdog_seconds=kwargs.get("watchdog_seconds"),
+                    level_records=kwargs.get("level_records", True),
                     full_fences=kwargs.get("full_fences", False),
                     dynamic_fetch=kwargs.get("dynamic_fetch", False),
                 )
