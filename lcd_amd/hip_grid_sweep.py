@@ -123,7 +123,7 @@ _SWEEP_KERNEL = r"""
     lcd_index_t _g_pos = 0, _g_src = 0; double _g_value = 0.0;
     double @operand@ = 0.0; double _lcd_wout = 0.0;
     (void)_g_pos; (void)_g_src; (void)_lane;
-    auto _lcd_wdiv = [&](double a, double d, double r) { return lcd_div_checked(a, d, r); };
+    auto _lcd_wdiv = [&](double a, double d, double r) { return lcd_div_checked_any(a, d, r); };
     (void)_lcd_wdiv;
     // the workgroups take their places in launch order: a place depends on
     // lower places only, and a place that is taken belongs to a workgroup
@@ -471,8 +471,7 @@ class GridSweepMixin:
         if geometry["wy"] == 16:
             vy = [f"{pad}const double _s_vy = lcd_row_shr1_or(fy_now, _s_prev);"]
         else:
-            vy = [f"{pad}double _s_vy = lcd_row_give<1>(_s_prev);",
-                  f"{pad}if (ly == 0) _s_vy = fy_now;"]
+            vy = [f"{pad}const double _s_vy = lcd_row_shr1_sel(fy_now, _s_prev, ly == 0);"]
         task = []
         for k, value in enumerate(("_s_vz", "_s_vy", "_s_prev")):
             task += [f"{pad}_g_value = {value}; {operand} = "

@@ -1134,7 +1134,10 @@ def test_grid_sweep_lowering_and_geometry():
     assert order == sorted(order)
     assert "_lcd_own_0 = _lcd_own_0 + (_g_operand_0 * _g_value);" in kernel
     assert "_lcd_own_0 = _lcd_wdiv((_nl_0 - _lcd_own_0), _nl_2, _lcd_wr);" in kernel
-    assert "return lcd_div_checked(a, d, r);" in kernel
+    # (one branch for the whole wavefront around the second division, and the
+    # y neighbour's value by a shift whose result feeds the select directly)
+    assert "return lcd_div_checked_any(a, d, r);" in kernel
+    assert "const double _s_vy = lcd_row_shr1_sel(fy_now, _s_prev, ly == 0);" in kernel
     # nothing of the solution is polled in memory by a sweeping wavefront and
     # nothing is added atomically; a missing entry is the neutral product
     assert "lcd_atomic" not in kernel
