@@ -243,9 +243,16 @@ _SWEEP_KERNEL = r"""
         double* yw = yw_real ? &_s_sh.yin[(_s_wave + 1) % SW_NW][0][lz] : &_s_sh.trash[_s_lane];
         double* zw = zw_real ? &_s_sh.zin[(_s_wave + SW_GY) % SW_NW][0][ly] : &_s_sh.trash[_s_lane];
         const int yw_inc = yw_real ? SW_D * SW_WZ : 0, zw_inc = zw_real ? SW_D * SW_WY : 0;
-        char* yout_g = (char*)(_lcd_sw_yface + (size_t)(beta + 1) * SW_YROWS * SW_WZ + lz);
-        char* zout_g = (char*)(_lcd_sw_zface + (size_t)(beta + SW_NBY) * SW_ZROWS * SW_WY + ly);
-        const bool y_face_lane = ly == SW_WY - 1, z_face_lane = lz == SW_WZ - 1;
+        // faces for other workgroups: one store of the whole wavefront through a
+        // buffer descriptor of the consumer's array; the lanes that are not on the
+        // face carry an offset beyond the array, which the hardware drops (no
+        // change of the execution mask around the store)
+        const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(_lcd_sw_yface + (size_t)(YG ? beta + 1 : beta) * SW_YROWS * SW_WZ), 0, SW_YROWS * SW_WZ * 8, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(_lcd_sw_zface + (size_t)(ZG ? beta + SW_NBY : beta) * SW_ZROWS * SW_WY), 0, SW_ZROWS * SW_WY * 8, 0x00020000);
+        const unsigned yvo = ly == SW_WY - 1 ? lz * 8u : 0x80000000u;
+        const unsigned zvo = lz == SW_WZ - 1 ? ly * 8u : 0x80000000u;
         // reads: the y face (first lanes of the rows; the others read zeros), the z
         // value from the face (first z row) or the ring (the row below)
         const double* yr = ly == 0 ? &_s_sh.yin[_s_wave][SW_YLAG][lz] : &_s_sh.zeros[_s_lane];
@@ -256,10 +263,12 @@ _SWEEP_KERNEL = r"""
         double _s_prev = 0.0;
         double fy = lcd_lds_ld(yr), vzf = lcd_lds_ld(zf), vzr = 0.0;
         unsigned spins = 0; bool dead = false;
+        int soff = SW_D * SW_STEP_BYTES, ysoff = 0, zsoff = 0;     // (running offsets: no multiply per step)
         for (int s0 = 0; s0 < SW_SP; s0 += SW_D) {
-            const int soff = (s0 + SW_D) * SW_STEP_BYTES;
 #pragma unroll
             for (int j = 0; j < SW_D; ++j) {
+                // (one wait for the step's records: the last of them is asked for first)
+                asm volatile("" :: "v"(_s_o[j][SW_P - 1]));
 @take@
                 if (__builtin_expect(__ballot(!(fy == fy) || !(vzf == vzf)) != 0ull, 0)) {
                     // a value that is no number: the empty marker is waited for
@@ -281,10 +290,10 @@ _SWEEP_KERNEL = r"""
 @task@
                 _s_prev = _lcd_wout;
                 lcd_lds_st(rw + (j & 7) * 64, _s_prev);
-                lcd_lds_st(yw + j * SW_WZ, _s_prev);
-                lcd_lds_st(zw + j * SW_WY, _s_prev);
-                if (YG) { if (y_face_lane) lcd_st((double*)(yout_g + j * (SW_WZ * 8)), _s_prev); }
-                if (ZG) { if (z_face_lane) lcd_st((double*)(zout_g + j * (SW_WY * 8)), _s_prev); }
+                if (SW_GY > 1) lcd_lds_st(yw + j * SW_WZ, _s_prev);
+                if (SW_GZ > 1) lcd_lds_st(zw + j * SW_WY, _s_prev);
+                if (YG) lcd_buffer_st(ry, yvo + j * (SW_WZ * 8), ysoff, _s_prev);
+                if (ZG) lcd_buffer_st(rz, zvo + j * (SW_WY * 8), zsoff, _s_prev);
                 *(double*)(outp + j * 512) = _s_prev;
 #pragma unroll
                 for (int k = 0; k < SW_P; ++k)
@@ -292,7 +301,8 @@ _SWEEP_KERNEL = r"""
                 if (SW_SKZ < 2) vzr = lcd_lds_ld(zr + ((j + 1 - SW_SKZ) & 7) * 64);
             }
             yr += yr_inc; zf += zf_inc; yw += yw_inc; zw += zw_inc;
-            yout_g += SW_D * SW_WZ * 8; zout_g += SW_D * SW_WY * 8; outp += SW_D * 512;
+            outp += SW_D * 512;
+            soff += SW_D * SW_STEP_BYTES; ysoff += SW_D * SW_WZ * 8; zsoff += SW_D * SW_WY * 8;
         }
         if (dead) _lcd_status[0] = 1;
     };
