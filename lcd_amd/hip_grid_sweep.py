@@ -51,7 +51,7 @@ SWEEP_FLOAT_ARGUMENTS = SWEEP_ARGUMENTS[:4]
 LDS_BYTES = 160 * 1024
 
 
-def sweep_geometry(grid, wy=16, gy=1, gz=2, skz=2, components=6):
+def sweep_geometry(grid, wy=16, gy=1, gz=2, skz=2, components=6, dynamic=1):
     """Everything the kernels, the launcher and the runtime derive from the
     grid and the shape of the sweep (see the module text), as a dict."""
     nx, ny, nz = (int(extent) for extent in grid)
@@ -63,7 +63,12 @@ def sweep_geometry(grid, wy=16, gy=1, gz=2, skz=2, components=6):
     steps = nx + (wy - 1) + (wz - 1) * skz
     sp = -(-steps // SWEEP_DEPTH) * SWEEP_DEPTH
     ylag, zlag = wy - 1, (wz - 1) * skz
-    pairs = -(-int(components) // 2)
+    # A step's record: the components the matrix gives, two to a plane of 64
+    # lanes x 16 bytes (the last alone in a plane of 64 x 8 bytes when their
+    # number is odd), then a plane of 64 x 8 bytes for every component that is
+    # staged in front of each solve -- those are written as whole lines.
+    static = int(components) - int(dynamic)
+    pairs, halves = static // 2, static % 2 + int(dynamic)
     # (records per bundle: the loop's steps, the steps the prefetch runs
     # ahead, rounded up to the tiles of the staging kernels)
     spa = -(-(sp + SWEEP_DEPTH) // SWEEP_TILE_STEPS) * SWEEP_TILE_STEPS
@@ -73,6 +78,7 @@ def sweep_geometry(grid, wy=16, gy=1, gz=2, skz=2, components=6):
         spa=spa, wgy=-(-nby // gy), wgz=-(-nbz // gz),
         waves=gy * gz, helpers=gy + gz, ylag=ylag, zlag=zlag,
         yrows=ylag + sp + 1, zrows=zlag + sp + 1, pairs=pairs,
+        halves=halves, record=pairs * 128 + halves * 64,
         components=int(components))
     geometry["workgroups"] = geometry["wgy"] * geometry["wgz"]
     geometry["threads"] = (geometry["waves"] + geometry["helpers"]) * 64
@@ -100,13 +106,13 @@ _SWEEP_KERNEL = r"""
     // ---- grid sweep: a lane per grid line, a wavefront per bundle of lines
     constexpr int SW_NX = @nx@, SW_NY = @ny@, SW_NZ = @nz@, SW_WY = @wy@, SW_WZ = @wz@;
     constexpr int SW_GY = @gy@, SW_GZ = @gz@, SW_SKZ = @skz@, SW_D = @depth@;
-    constexpr int SW_S = @steps@, SW_SP = @sp@, SW_SPA = @spa@, SW_P = @pairs@;
+    constexpr int SW_S = @steps@, SW_SP = @sp@, SW_SPA = @spa@, SW_P = @pairs@, SW_H8 = @halves@;
     constexpr int SW_NBY = @nby@, SW_NBZ = @nbz@, SW_WGY = @wgy@;
     constexpr int SW_NW = SW_GY * SW_GZ, SW_H = SW_GY + SW_GZ;
     constexpr int SW_YLAG = @ylag@, SW_ZLAG = @zlag@;
     constexpr int SW_YROWS = @yrows@, SW_ZROWS = @zrows@;
     constexpr int SW_YV = SW_S - SW_YLAG, SW_ZV = SW_S - SW_ZLAG;   // rows of a face that get written
-    constexpr int SW_STEP_BYTES = SW_P * 1024;
+    constexpr int SW_STEP_BYTES = SW_P * 1024 + SW_H8 * 512;
     static_assert(LCD_TPB == (SW_NW + SW_H) * 64, "workgroup size of the sweep");
     struct _s_shared_t {
         double yin[SW_NW][SW_YROWS][SW_WZ];     // incoming faces by the consumer's step (+ lag rows in front)
@@ -226,15 +232,20 @@ _SWEEP_KERNEL = r"""
         const int beta = _s_by + SW_NBY * _s_bz;
         const int ly = _s_lane % SW_WY, lz = _s_lane / SW_WY;
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(_lcd_sw_ops + (size_t)beta * SW_SPA * (SW_P * 128)), 0, SW_SPA * SW_STEP_BYTES, 0x00020000);
-        const unsigned loff = _s_lane * 16u;
+            (void*)(_lcd_sw_ops + (size_t)beta * SW_SPA * (SW_STEP_BYTES / 8)), 0, SW_SPA * SW_STEP_BYTES, 0x00020000);
+        const unsigned loff = _s_lane * 16u, hoff = SW_P * 1024u + _s_lane * 8u;
         char* outp = (char*)(_lcd_sw_out + (size_t)beta * SW_SPA * 64) + _s_lane * 8u;
-        lcd_v4u _s_o[SW_D][SW_P];
+        lcd_v4u _s_o[SW_D][SW_P > 0 ? SW_P : 1];
+        lcd_v2u _s_h[SW_D][SW_H8 > 0 ? SW_H8 : 1];
 #pragma unroll
-        for (int j = 0; j < SW_D; ++j)
+        for (int j = 0; j < SW_D; ++j) {
 #pragma unroll
             for (int k = 0; k < SW_P; ++k)
                 _s_o[j][k] = __builtin_amdgcn_raw_buffer_load_b128(rs, loff + k * 1024, j * SW_STEP_BYTES, 0);
+#pragma unroll
+            for (int k = 0; k < SW_H8; ++k)
+                _s_h[j][k] = __builtin_amdgcn_raw_buffer_load_b64(rs, hoff + k * 512, j * SW_STEP_BYTES, 0);
+        }
         const bool y_in_group = _s_gy + 1 < SW_GY, z_in_group = _s_gz + 1 < SW_GZ;
         // face writes inside the workgroup go to the consumer's array at
         // (own step - lag); every other lane writes the trash
@@ -268,7 +279,8 @@ _SWEEP_KERNEL = r"""
 #pragma unroll
             for (int j = 0; j < SW_D; ++j) {
                 // (one wait for the step's records: the last of them is asked for first)
-                asm volatile("" :: "v"(_s_o[j][SW_P - 1]));
+                if (SW_H8 > 0) asm volatile("" :: "v"(_s_h[j][SW_H8 > 0 ? SW_H8 - 1 : 0]));
+                else asm volatile("" :: "v"(_s_o[j][SW_P > 0 ? SW_P - 1 : 0]));
 @take@
                 if (__builtin_expect(__ballot(!(fy == fy) || !(vzf == vzf)) != 0ull, 0)) {
                     // a value that is no number: the empty marker is waited for
@@ -298,6 +310,9 @@ _SWEEP_KERNEL = r"""
 #pragma unroll
                 for (int k = 0; k < SW_P; ++k)
                     _s_o[j][k] = __builtin_amdgcn_raw_buffer_load_b128(rs, loff + k * 1024, soff + j * SW_STEP_BYTES, 0);
+#pragma unroll
+                for (int k = 0; k < SW_H8; ++k)
+                    _s_h[j][k] = __builtin_amdgcn_raw_buffer_load_b64(rs, hoff + k * 512, soff + j * SW_STEP_BYTES, 0);
                 if (SW_SKZ < 2) vzr = lcd_lds_ld(zr + ((j + 1 - SW_SKZ) & 7) * 64);
             }
             yr += yr_inc; zf += zf_inc; yw += yw_inc; zw += zw_inc;
@@ -319,7 +334,7 @@ _SWEEP_KERNEL = r"""
 
 _SWEEP_SLOT = r"""
     constexpr int SW_NX = @nx@, SW_NY = @ny@, SW_NZ = @nz@, SW_WY = @wy@, SW_WZ = @wz@;
-    constexpr int SW_SKZ = @skz@, SW_SPA = @spa@, SW_P = @pairs@, SW_NBY = @nby@;
+    constexpr int SW_SKZ = @skz@, SW_SPA = @spa@, SW_P = @pairs@, SW_REC = @record@, SW_NBY = @nby@;
     const long long _s_t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (_s_t >= (long long)@slots@) return;
     const int _s_lane = (int)(_s_t & 63);
@@ -330,7 +345,7 @@ _SWEEP_SLOT = r"""
     const int _s_x = _s_step - _s_lane % SW_WY - SW_SKZ * (_s_lane / SW_WY);
     const bool _s_active = _s_x >= 0 && _s_x < SW_NX && _s_y < SW_NY && _s_z < SW_NZ;
     @it@ = _s_active ? (lcd_index_t)(_s_x + SW_NX * (_s_y + (long long)SW_NY * _s_z)) : 0;
-    double* const _s_rec = _lcd_sw_ops + _s_row * (SW_P * 128) + _s_lane * 2;
+    double* const _s_rec = _lcd_sw_ops + _s_row * SW_REC;      // the step's record
     (void)_s_rec; (void)_lane;
 """
 
@@ -340,7 +355,7 @@ _SWEEP_TILE = r"""
     // memory is touched in runs along the grid lines on one side and along the
     // lanes of a record on the other, the tile turns in LDS between the two
     constexpr int SW_NX = @nx@, SW_NY = @ny@, SW_NZ = @nz@, SW_WY = @wy@, SW_WZ = @wz@;
-    constexpr int SW_SKZ = @skz@, SW_SPA = @spa@, SW_P = @pairs@, SW_NBY = @nby@;
+    constexpr int SW_SKZ = @skz@, SW_SPA = @spa@, SW_P = @pairs@, SW_REC = @record@, SW_NBY = @nby@;
     constexpr int SW_TS = @tile_steps@;
     const int _s_beta = (int)(blockIdx.x / (SW_SPA / SW_TS));
     const int _s_s0 = (int)(blockIdx.x % (SW_SPA / SW_TS)) * SW_TS;
@@ -439,8 +454,21 @@ class GridSweepMixin:
         }
 
     def _sweep_component(self, c):
+        """Component ``c`` of step ``j``'s record in the sweeping wavefront's
+        registers."""
+        pairs = self._sweep["geometry"]["pairs"]
+        if c >= 2 * pairs:
+            return f"lcd_whole(_s_h[j][{c - 2 * pairs}])"
         return (f"lcd_lo(_s_o[j][{c // 2}])" if c % 2 == 0
                 else f"lcd_hi(_s_o[j][{c // 2}])")
+
+    def _sweep_record_slot(self, c, lane):
+        """Where component ``c`` of lane ``lane`` lies in a step's record
+        (``_s_rec``): in a plane of pairs, or in a plane of its own."""
+        pairs = self._sweep["geometry"]["pairs"]
+        if c >= 2 * pairs:
+            return f"_s_rec[{pairs * 128 + (c - 2 * pairs) * 64} + {lane}]"
+        return f"_s_rec[{(c // 2) * 128 + c % 2} + {lane} * 2]"
 
     def _grid_sweep_text(self, task_lines):
         """Kernel body of the sweep (everything after the declarations)."""
@@ -450,7 +478,9 @@ class GridSweepMixin:
         self._sweep = parts
         geometry = sweep_geometry(
             self.grid_sweep[:3], *self.grid_sweep[3:],
-            components=parts["components"])
+            components=parts["components"],
+            dynamic=sum(1 for slot in parts["slots"]
+                        if slot[0] in parts["dynamic"]))
         if geometry["lds_bytes"] > LDS_BYTES or (
                 self.threads_per_block != geometry["threads"]):
             return None
@@ -514,8 +544,8 @@ class GridSweepMixin:
         names = tuple(f"{function_name}_hip_sweep_{kind}"
                       for kind in ("static", "dynamic", "unstage"))
 
-        def component(c):
-            return f"_s_rec[{(c // 2) * 128 + c % 2}]"
+        def component(c, lane="_s_lane"):
+            return self._sweep_record_slot(c, lane)
 
         def put(name, kind):
             return f"(double){name}" if kind == INT else name
@@ -564,8 +594,8 @@ class GridSweepMixin:
             # (a lane without a task computes on ones)
             *[f"    {component(entries + k)} = _s_active ? {put(name, kind)} : 1.0;"
               for k, (name, kind) in static_slots],
-            *([f"    {component(parts['components'])} = 0.0;"]
-              if parts["components"] % 2 else []),
+            # (the unused half of an odd last plane of pairs does not exist:
+            # an odd component has a plane of 8-byte slots)
         ]
         tile_head = _SWEEP_TILE
         for key, value in dict(geometry, tile_steps=SWEEP_TILE_STEPS).items():
@@ -583,24 +613,30 @@ class GridSweepMixin:
         count = max(len(dynamic_slots), 1)
         dynamic_body = [
             f"    __shared__ double _s_tile[{count}][SW_TS][65];",
-            "    for (int p = 0; p < 8; ++p) {",
+            f"    double _s_v[{count}][8];",
+            # (a slot without a task reads task 0's operands, so that the
+            # eight passes' loads are all under way together, and computes
+            # on ones)
+            "    _Pragma(\"unroll\") for (int p = 0; p < 8; ++p) {",
             "        const int lane = p * 8 + (int)(threadIdx.x >> 5), st = (int)(threadIdx.x & 31);",
             "        bool active;",
             f"        {it} = _s_task(lane, st, active);",
-            "        if (active) {",
-            *["            " + line for line in all_lines],
-            *(["            " + line for line in reciprocal]
+            *["        " + line for line in all_lines],
+            *(["        " + line for line in reciprocal]
               if division and "_lcd_wr" in parts["dynamic"] else []),
-            "        }",
-            # (a lane without a task computes on ones)
-            *[f"        _s_tile[{q}][st][lane] = active ? {put(name, kind)} : 1.0;"
+            *[f"        _s_v[{q}][p] = active ? {put(name, kind)} : 1.0;"
               for q, (k, (name, kind)) in enumerate(dynamic_slots)],
+            "    }",
+            "    _Pragma(\"unroll\") for (int p = 0; p < 8; ++p) {",
+            "        const int lane = p * 8 + (int)(threadIdx.x >> 5), st = (int)(threadIdx.x & 31);",
+            *[f"        _s_tile[{q}][st][lane] = _s_v[{q}][p];"
+              for q in range(len(dynamic_slots))],
             "    }",
             "    __syncthreads();",
             "    for (int u = 0; u < 8; ++u) {",
             "        const int at = u * 256 + (int)threadIdx.x, st = at >> 6, lane = at & 63;",
-            "        double* const _s_rec = _lcd_sw_ops + (_s_row0 + st) * (SW_P * 128) + lane * 2;",
-            *[f"        {component(entries + k)} = _s_tile[{q}][st][lane];"
+            "        double* const _s_rec = _lcd_sw_ops + (_s_row0 + st) * SW_REC;",
+            *[f"        {component(entries + k, 'lane')} = _s_tile[{q}][st][lane];"
               for q, (k, _) in enumerate(dynamic_slots)],
             "    }",
         ]

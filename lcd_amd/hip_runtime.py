@@ -1496,7 +1496,7 @@ def _sweep_buffers(lowering, device, workspace):
         slots = geometry["slots"]
         faces = geometry["bundles"] + geometry["nby"] + 1
         cached = {
-            "_lcd_sw_ops": device.empty((slots * geometry["pairs"] * 2,),
+            "_lcd_sw_ops": device.empty((slots // 64 * geometry["record"],),
                                         np.float64),
             "_lcd_sw_out": device.empty((slots,), np.float64),
             "_lcd_sw_yface": device.empty(

@@ -1143,7 +1143,16 @@ def test_grid_sweep_lowering_and_geometry():
     assert "lcd_atomic" not in kernel
     assert "_s_c[k] = -0.0;" in kernel
     assert "if (k < 0) _lcd_status[0] = 3; else _s_c[k] = Ax[_g_pos];" in kernel
-    assert "_s_rec[257] = _s_tile[0][st][lane];" in kernel      # b: pair 2, second half
+    # a step's record: two planes of pairs (the three operands and the
+    # diagonal), a plane of 8-byte slots for the reciprocal, and one for the
+    # right-hand side, which the staging in front of a solve writes as whole
+    # lines; the sweeping wavefront asks for the last plane's value first
+    assert (result.grid_sweep["pairs"], result.grid_sweep["halves"],
+            result.grid_sweep["record"]) == (2, 2, 384)
+    assert "_s_rec[320 + lane] = _s_tile[0][st][lane];" in kernel
+    assert "_s_rec[256 + _s_lane] = _s_active ? _lcd_wr : 1.0;" in kernel
+    assert "_nl_0 = lcd_whole(_s_h[j][1]);" in kernel
+    assert 'asm volatile("" :: "v"(_s_h[j][SW_H8 > 0 ? SW_H8 - 1 : 0]));' in kernel
     assert "if (active) x[i] = _s_tile[st][lane];" in kernel
     launcher = result.launcher_source
     assert launcher.count("_hip.launch(") == 4 and "_hip_reset" not in launcher
