@@ -14,6 +14,12 @@ from lcd_amd.hip_emitter import (
 )
 
 
+# Level launches: how many producers of a task are read "flat" -- every table
+# entry of all of them asked for at once, then every value, then the
+# arithmetic producer by producer -- before the producer loop takes the rest.
+LEVEL_FLAT_PRODUCERS = 4
+
+
 class SequentialPullMixin:
     """Methods of ``HIPLowerer`` (lcd_amd/hip_lowering.py)."""
 
@@ -236,7 +242,17 @@ class SequentialPullMixin:
             targets=[ast.Name(id=local, ctx=ast.Store())],
             value=ast.Name(id=f"_nx_{local}", ctx=ast.Load())))
             for local in names]
-        lines = [f"{name} = {lower};", *(count_lines if counted else [])]
+        lines = [f"{name} = {lower};"]
+        flat = None
+        if (counted is not None and speculative and leave is None
+                and self._published.get("plain")):
+            flat = self._flat_producers(
+                name, node.iter.args[1], before + structure, names,
+                first_loads, take_over, rest, emitter, hooks)
+        if flat is not None:
+            lines += flat[0] + count_lines + flat[1]
+        else:
+            lines += count_lines if counted else []
         lines += self._emit_guarded(ahead(0), emitter, 0, hooks)
         lines += [VALUE_WAIT_BEGIN, "_lcd_blocked = false;",
                   f"for (; {name} < {emitter.expr(upper)}; ++{name}) {{"]
@@ -263,6 +279,155 @@ class SequentialPullMixin:
                                  f"{register} = {load};")
         lines += ["}", VALUE_WAIT_END]
         return lines
+
+    def _flat_producers(self, name, row_end, located, names, first_loads,
+                        take_over, rest, emitter, hooks):
+        """Level launches (every producer ran in an earlier launch, nothing
+        is polled): the first ``LEVEL_FLAT_PRODUCERS`` producers of a task
+        without the chain of dependent trips the producer loop makes of
+        them.  What the located statements read from the inspector's tables
+        is asked for at once for all of them, through loads that no guard
+        encloses (an entry that is not there -- the producer beyond the
+        loop's end, the lane without an entry -- reads entry 0 instead: a
+        guarded load keeps its wait inside the guard, and the trips come
+        back); then the values they point at, the same way; then the
+        iterations themselves, which find everything in registers.  Returns
+        (lines in front of the count of the loop's bound, lines behind it),
+        or None where a statement has a shape this does not know (the
+        producer loop then does all the work, as it does for the producers
+        after these)."""
+        flat = LEVEL_FLAT_PRODUCERS
+        kinds = self._kinds
+        tables = ({entry[1] for entry in self._structure_tables}
+                  | {entry[3] for entry in self._structure_tables})
+        loaded = []
+        for statement in first_loads:
+            for sub in ast.walk(statement):
+                if (isinstance(sub, ast.Name) and isinstance(sub.ctx, ast.Store)
+                        and sub.id not in loaded):
+                    loaded.append(sub.id)
+
+        def pure(node):
+            for sub in ast.walk(node):
+                if isinstance(sub, ast.Subscript):
+                    return False
+                if isinstance(sub, ast.Call) and not (
+                        isinstance(sub.func, ast.Name)
+                        and sub.func.id == "_lcd_rseg_first"):
+                    return False
+            return True
+
+        def renamed(node, q):
+            prefix = f"_f{q}_"
+
+            class Rename(ast.NodeTransformer):
+                def visit_Name(self, sub):
+                    if sub.id in names or sub.id in loaded:
+                        return ast.copy_location(
+                            ast.Name(id=prefix + sub.id, ctx=sub.ctx), sub)
+                    if sub.id == name and q:
+                        return ast.copy_location(ast.BinOp(
+                            left=ast.Name(id=name, ctx=ast.Load()),
+                            op=ast.Add(), right=ast.Constant(value=q)), sub)
+                    return sub
+
+            return ast.fix_missing_locations(Rename().visit(deepcopy(node)))
+
+        def both(guard, test):
+            return test if guard is None else f"({guard}) && ({test})"
+
+        ask, settle, values, work = [], [], [], []
+        for q in range(flat):
+            here = (f"({name} + {q}) < {emitter.expr(row_end)}" if q
+                    else f"{name} < {emitter.expr(row_end)}")
+            on = (f"({name} + {q}) < _lcd_low_end" if q
+                  else f"{name} < _lcd_low_end")
+
+            def locate(statement, guard):
+                if isinstance(statement, ast.If) and not statement.orelse:
+                    if not pure(statement.test):
+                        return False
+                    test = emitter.expr(renamed(statement.test, q))
+                    return all(locate(child, both(guard, test))
+                               for child in statement.body)
+                if not (isinstance(statement, ast.Assign)
+                        and len(statement.targets) == 1
+                        and isinstance(statement.targets[0], ast.Name)):
+                    return False
+                target = f"_f{q}_{statement.targets[0].id}"
+                value = statement.value
+                if pure(value):
+                    text = f"{target} = {emitter.expr(renamed(value, q))};"
+                    ask.append(text if guard is None
+                               else f"if ({guard}) {text}")
+                    return True
+                if (isinstance(value, ast.Subscript)
+                        and isinstance(value.value, ast.Name)
+                        and value.value.id in tables and pure(value.slice)):
+                    index = emitter.expr(renamed(value.slice, q))
+                    ask.append(f"{target} = {value.value.id}"
+                               f"[({both(guard, here)}) ? {index} : 0];")
+                    return True
+                if (isinstance(value, ast.Call)
+                        and isinstance(value.func, ast.Name)
+                        and value.func.id == "_lcd_pair_at"
+                        and len(value.args) == 2
+                        and all(pure(arg) for arg in value.args)):
+                    row, at = (emitter.expr(renamed(arg, q))
+                               for arg in value.args)
+                    where = both(guard, here)
+                    for part in ("_o", "_s"):
+                        kinds.locals[target + part] = INT
+                        self._own_registers.append(target + part)
+                    ask.append(
+                        f"{target}_o = _lcd_pair[({where}) ? _lcd_pair_row + "
+                        f"(({row}) - _lcd_seg_base) * _lcd_seg_own + "
+                        f"(({at}) - _lcd_seg_base) : 0];")
+                    ask.append(f"{target}_s = _lcd_pair_start"
+                               f"[({where}) ? {row} : 0];")
+                    settle.append(
+                        f"{target} = ({both(guard, on)}) ? "
+                        f"lcd_pair_pos({target}_o, {target}_s) : -1;")
+                    return True
+                return False
+
+            if not all(locate(statement, None) for statement in located):
+                return None
+            for statement in first_loads:
+                test, body = None, [statement]
+                if isinstance(statement, ast.If) and not statement.orelse:
+                    if not pure(statement.test):
+                        return None
+                    test = emitter.expr(renamed(statement.test, q))
+                    body = statement.body
+                for child in body:
+                    if not (isinstance(child, ast.Assign)
+                            and len(child.targets) == 1
+                            and isinstance(child.targets[0], ast.Name)
+                            and isinstance(child.value, ast.Call)
+                            and isinstance(child.value.func, ast.Name)
+                            and child.value.func.id == "_lcd_raw"
+                            and len(child.value.args) == 1
+                            and isinstance(child.value.args[0], ast.Subscript)
+                            and isinstance(child.value.args[0].value, ast.Name)
+                            and pure(child.value.args[0].slice)):
+                        return None
+                    source = child.value.args[0]
+                    index = emitter.expr(renamed(source.slice, q))
+                    values.append(
+                        f"_f{q}_{child.targets[0].id} = {source.value.id}"
+                        f"[({both(test, on)}) ? {index} : 0];")
+            work.append(f"if ({name} < _lcd_low_end) {{")
+            for local in names + loaded:
+                work.append(f"    {local} = _f{q}_{local};")
+            for child in rest:
+                work += self._emit_guarded(child, emitter, 1, hooks)
+            work += [f"    ++{name};", "}"]
+        for q in range(flat):
+            for local in names + loaded:
+                kinds.locals[f"_f{q}_{local}"] = kinds.locals.get(local, INT)
+                self._own_registers.append(f"_f{q}_{local}")
+        return ask, settle + values + work
 
     def _second_attempts(self, first_loads, emitter):
         """Second attempt of an iteration's first loads, once, behind the

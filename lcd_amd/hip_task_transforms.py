@@ -992,7 +992,10 @@ class TaskTransformMixin:
         # only: measured 1-2 % there; level launches lose 4 % and the flagged
         # pull 1 % (ILU0, 9-point grid) because rows of consecutive levels
         # are neighbours, so `Ap[i]` is warm in L2 from the level before
-        # while a queue-ordered copy is cold at every level
+        # while a queue-ordered copy is cold at every level (the same with
+        # the task's producers taken flat, where the copies -- the row's
+        # bounds and its place in the pair table -- save a whole dependent
+        # trip: 14.4 against 13.5 ms)
         value_flags = self._value_pull is not None or (
             self._mailbox is not None and self._mailbox["gather"] is not None)
         if (not self.queue_node_loads_enabled or self.chain_tasks

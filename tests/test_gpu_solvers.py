@@ -632,6 +632,10 @@ def test_ilu0_level_launches_with_the_row_in_registers(oracle):
     source = factor.hip_kernel_source
     assert "_lcd_pair[" in source and "lcd_sorted_find" not in source
     assert "_lcd_pub" not in source and "lcd_pull_settle(" not in source
+    # (the first four pivots of a row are taken flat, the pivot loop has the
+    # rest: the random rows below have up to a dozen)
+    assert "_f3__sp_kj_ptr_o = _lcd_pair[" in source
+    assert "for (; k_ptr < _lcd_low_end; ++k_ptr) {" in source
     import scipy.sparse as sp
     rng = np.random.default_rng(5)
     n = 3000

@@ -1302,6 +1302,32 @@ def test_own_segment_in_registers():
             "((_nx__sp_first) - _lcd_seg_base)], "
             "_lcd_pair_start[(k_ptr + 1)]);") in text
     hip_runtime.compile_code(tabled.source)
+    # Under level launches the same task reads plainly (every pivot row was
+    # finished by an earlier launch), and its first four pivots are taken
+    # flat: the table entries of all four are asked for with the row itself,
+    # through loads that no guard encloses (an entry that is not there reads
+    # entry 0), their values likewise, and the iterations follow with
+    # everything in registers; the pivot loop takes what is left.
+    level = lower_to_hip(module, segment_registers=2,
+                         **{**options, "execution_mode": "wavefront"})
+    text = level.kernel_source
+    assert "_lcd_pub" not in text and "lcd_pull_settle(" not in text
+    ask = text.index("_f3__sp_kj_ptr_o = _lcd_pair[(((_f3__sp_first < row_end)) && "
+                     "((k_ptr + 3) < row_end)) ? _lcd_pair_row + ")
+    count = text.index("const unsigned long long _lcd_low_mask = __ballot(")
+    settle = text.index(
+        "_f3__sp_kj_ptr = (((_f3__sp_first < row_end)) && ((k_ptr + 3) < "
+        "_lcd_low_end)) ? lcd_pair_pos(_f3__sp_kj_ptr_o, _f3__sp_kj_ptr_s) : -1;")
+    values = text.index(
+        "_f0__sp_ld_h0 = A_data[(((_f0_diag_ptr >= 0)) && (k_ptr < _lcd_low_end)) "
+        "? _f0_diag_ptr : 0];")
+    work = text.index("diag_ptr = _f0_diag_ptr;")
+    loop = text.index("for (; k_ptr < _lcd_low_end; ++k_ptr) {")
+    assert ask < count < settle < values < work < loop
+    assert text.count("++k_ptr;") == 4
+    hip_runtime.compile_code(level.source)
+    # (the persistent executor's pivots are polled for: nothing flat there)
+    assert "_f0_" not in tabled.kernel_source
     # (without registers the tables are not used: segments may be long)
     assert lower_to_hip(module, **options).structure_tables == ()
     # eight lanes per row: rows share a wavefront, registers do not apply
